@@ -1,0 +1,372 @@
+"""Pins for the CPU oracle (runs without a GPU).
+
+Each oracle function is checked against something that does not retype its
+formula: the reference tests' known answers and special-value matrices,
+closed forms, invariants and brute-force loops on tiny inputs.  A plausible
+mistake (a swapped nibble, a dropped zero-point, a transposed operand, a
+wrong NaN rule) fails at least one test here.
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+from oracle import bf16, eltwise, gemm, quant, rowops
+
+
+# --------------------------------------------------------------------- bf16
+
+def test_bf16_exact_values_and_rne_ties():
+    vals = np.array([1.0, -2.0, 0.0, -0.0, 0.5, 65280.0], np.float32)
+    assert list(bf16.f32_to_bf16_bits(vals)) == [0x3F80, 0xC000, 0x0000, 0x8000, 0x3F00, 0x477F]
+    # 1 + 2^-8 is halfway between 1.0 (even) and 1 + 2^-7: ties go to even.
+    assert bf16.f32_to_bf16_bits(np.float32(1 + 2 ** -8)) == 0x3F80
+    # 1 + 3*2^-8 is halfway between 0x3F81 (odd) and 0x3F82 (even).
+    assert bf16.f32_to_bf16_bits(np.float32(1 + 3 * 2 ** -8)) == 0x3F82
+    # just above halfway rounds up
+    assert bf16.f32_to_bf16_bits(np.float32(1 + 2 ** -8 + 2 ** -20)) == 0x3F81
+
+
+def test_bf16_specials():
+    b = bf16.f32_to_bf16_bits(np.array([np.inf, -np.inf, np.nan, 3.4028235e38], np.float32))
+    assert b[0] == 0x7F80 and b[1] == 0xFF80
+    assert (b[2] & 0x7F80) == 0x7F80 and (b[2] & 0x7F) != 0
+    assert b[3] == 0x7F80  # rounds past the largest finite bf16
+    x = np.array([1.5, -3.25, 1e-3], np.float32)
+    assert np.array_equal(bf16.round_bf16(bf16.round_bf16(x)), bf16.round_bf16(x))
+
+
+# --------------------------------------------------------------- int4 / int8
+
+def test_int4_pack_literal_bytes():
+    q = np.array([[1, 15], [2, 0], [3, 7], [4, 8]], np.uint8)  # K=4, N=2
+    p = quant.pack_int4_k(q)
+    assert p.tolist() == [[0x21, 0x0F], [0x43, 0x87]]
+    assert np.array_equal(quant.unpack_int4_k(p), q)
+
+
+def test_int4_pack_roundtrip_random():
+    rng = np.random.default_rng(0)
+    q = rng.integers(0, 16, size=(128, 33), dtype=np.uint8)
+    assert np.array_equal(quant.unpack_int4_k(quant.pack_int4_k(q)), q)
+    with pytest.raises(ValueError):
+        quant.pack_int4_k(np.full((2, 2), 16, np.uint8))
+
+
+def _brute_int4(x_bits, packed, s_bits, z, round_w):
+    # Independent restatement: reads nibbles straight from the bytes.
+    M, K = x_bits.shape
+    N = packed.shape[1]
+    xs = bf16.bf16_bits_to_f32(x_bits)
+    ss = bf16.bf16_bits_to_f32(s_bits)
+    y = np.zeros((M, N))
+    for n in range(N):
+        for k in range(K):
+            byte = int(packed[k // 2, n])
+            qv = (byte >> 4) if (k % 2) else (byte & 0xF)
+            w = float(np.float32(qv - int(z[k // 64, n])) * ss[k // 64, n])
+            if round_w:
+                w = float(bf16.round_bf16(np.float32(w)))
+            for m in range(M):
+                y[m, n] += float(xs[m, k]) * w
+    return y
+
+
+@pytest.mark.parametrize("round_w", [True, False])
+def test_int4_matmul_brute_force(round_w):
+    rng = np.random.default_rng(1)
+    x, p, s, z = quant.make_int4_case(rng, 3, 128, 5)
+    y, yb = quant.int4_g64_matmul(x, p, s, z, round_w=round_w)
+    ref = _brute_int4(x, p, s, z, round_w)
+    np.testing.assert_allclose(y, ref, rtol=1e-12, atol=1e-12)
+    np.testing.assert_array_equal(yb, bf16.f32_to_bf16_bits(ref.astype(np.float32)))
+
+
+def test_int4_matmul_all_ones_closed_form():
+    rng = np.random.default_rng(2)
+    K, N = 256, 7
+    q = np.ones((K, N), np.uint8)
+    z = np.zeros((K // 64, N), np.uint8)
+    s = bf16.f32_to_bf16_bits(rng.uniform(1e-3, 1e-2, size=(K // 64, N)).astype(np.float32))
+    x = bf16.f32_to_bf16_bits(np.ones((2, K), np.float32))
+    y, _ = quant.int4_g64_matmul(x, quant.pack_int4_k(q), s, z)
+    expect = 64.0 * bf16.bf16_bits_to_f32(s).astype(np.float64).sum(axis=0)
+    np.testing.assert_allclose(y, np.broadcast_to(expect, y.shape), rtol=1e-12)
+
+
+def test_int4_zero_point_sign():
+    # q = z everywhere -> the dequantized weight is exactly zero.
+    q = np.full((128, 4), 9, np.uint8)
+    z = np.full((2, 4), 9, np.uint8)
+    s = bf16.f32_to_bf16_bits(np.full((2, 4), 0.5, np.float32))
+    x = bf16.f32_to_bf16_bits(np.arange(256, dtype=np.float32).reshape(2, 128))
+    y, _ = quant.int4_g64_matmul(x, quant.pack_int4_k(q), s, z)
+    assert np.all(y == 0)
+    # q = z + 1 -> weight = s: Y = 0.5 * row sums
+    y, _ = quant.int4_g64_matmul(x, quant.pack_int4_k(q + 1), s, z)
+    np.testing.assert_allclose(y[:, 0], 0.5 * bf16.bf16_bits_to_f32(x).sum(axis=1))
+
+
+def test_int8_brute_force_and_identity():
+    rng = np.random.default_rng(3)
+    x, w, s = quant.make_int8_case(rng, 2, 64, 3)
+    y, _ = quant.int8_pc_matmul(x, w, s)
+    xs = bf16.bf16_bits_to_f32(x)
+    ref = np.zeros((2, 3))
+    for m in range(2):
+        for n in range(3):
+            acc = 0.0
+            for k in range(64):
+                acc += float(xs[m, k]) * int(w[k, n])
+            ref[m, n] = acc * float(s[n])
+    np.testing.assert_allclose(y, ref, rtol=1e-12)
+    eye = np.eye(8, dtype=np.int8)
+    x8 = bf16.randn_bf16(rng, (4, 8))
+    y8, _ = quant.int8_pc_matmul(x8, eye, np.ones(8, np.float32))
+    np.testing.assert_array_equal(y8, bf16.bf16_bits_to_f32(x8))
+
+
+# ------------------------------------------ the reference's affine quantizer
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_affine_roundtrip_reference_tolerance(bits):
+    # tests/test_quantized.py:418-431
+    rng = np.random.default_rng(42)
+    w = rng.standard_normal((8, 128)).astype(np.float32) * 0.1
+    packed, sc, bi = quant.affine_quantize(w, bits=bits, group_size=64)
+    back = quant.affine_dequantize(packed, sc, bi, bits=bits, group_size=64, shape=w.shape)
+    atol = 0.02 if bits == 8 else 0.05
+    np.testing.assert_allclose(back, w, atol=atol, rtol=0.3)
+    # and the max error is at most half a step per group
+    step = np.repeat(sc, 64, axis=1)
+    assert np.all(np.abs(back - w) <= 0.5 * step + 1e-6)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_affine_shapes(bits):
+    # tests/test_quantized.py:433-447
+    packed, sc, bi = quant.affine_quantize(np.ones((16, 128), np.float32), bits=bits, group_size=64)
+    if bits == 4:
+        assert packed.shape == (16, 16) and packed.dtype == np.uint32
+    else:
+        assert packed.shape == (16, 128) and packed.dtype == np.uint8
+    assert sc.shape == (16, 2) and bi.shape == (16, 2)
+
+
+def test_affine_zeros():
+    # tests/test_quantized.py:449-455
+    w = np.zeros((2, 64), np.float32)
+    packed, sc, bi = quant.affine_quantize(w, bits=4, group_size=32)
+    back = quant.affine_dequantize(packed, sc, bi, bits=4, group_size=32, shape=w.shape)
+    np.testing.assert_allclose(back, 0.0, atol=1e-6)
+
+
+def test_affine_matmul_reference_tolerance():
+    # tests/test_quantized.py:461-485 (4-bit, f32 activations)
+    rng = np.random.default_rng(42)
+    x = rng.standard_normal((8, 128)).astype(np.float32) * 0.1
+    w = rng.standard_normal((16, 128)).astype(np.float32) * 0.1
+    ref = x @ w.T
+    packed, sc, bi = quant.affine_quantize(w, bits=4, group_size=64)
+    wd = quant.affine_dequantize(packed, sc, bi, bits=4, group_size=64, shape=w.shape)
+    np.testing.assert_allclose(x @ wd.T, ref, atol=0.05, rtol=0.3)
+
+
+def test_affine_ones_known_answer_through_hot_path_format():
+    # tests/test_quantized.py:528-541: ones(1,64) @ ones(2,64).T == [[64, 64]]
+    w = np.ones((2, 64), np.float32)
+    packed, sc, bi = quant.affine_quantize(w, bits=4, group_size=64)
+    p, s, z = quant.affine_to_int4_g64(packed, sc, bi, K=64)
+    x = bf16.f32_to_bf16_bits(np.ones((1, 64), np.float32))
+    y, yb = quant.int4_g64_matmul(x, p, s, z)
+    np.testing.assert_array_equal(y, [[64.0, 64.0]])
+    np.testing.assert_array_equal(bf16.bf16_bits_to_f32(yb), [[64.0, 64.0]])
+
+
+def test_affine_converter_matches_reference_dequant():
+    # A weight whose affine code is representable: w = 0.25 * (q - 3)
+    rng = np.random.default_rng(5)
+    q = rng.integers(0, 16, size=(4, 128))
+    q[:, ::64] = 0
+    q[:, 1::64] = 15
+    w = (0.25 * (q - 3)).astype(np.float32)
+    packed, sc, bi = quant.affine_quantize(w, bits=4, group_size=64)
+    ref = quant.affine_dequantize(packed, sc, bi, bits=4, group_size=64, shape=w.shape)
+    p, s, z = quant.affine_to_int4_g64(packed, sc, bi, K=128)
+    mine = quant.int4_g64_dequant(p, s, z)
+    np.testing.assert_array_equal(mine.T, ref)
+
+
+# -------------------------------------------------------------------- GEMM
+
+def test_gemm_identity_ones_and_overflow_case():
+    rng = np.random.default_rng(6)
+    a = rng.standard_normal((16, 16)).astype(np.float32)
+    np.testing.assert_array_equal(gemm.dot_general(a, np.eye(16)), a)
+    ones = gemm.dot_general(np.ones((3, 37)), np.ones((37, 5)))
+    assert np.all(ones == 37)
+    # tests/test_f32_gemm_precision.py:55-60: every product 7e4 * 1/1024.
+    c, c32 = gemm.matmul_f32(np.full((8, 1024), 7e4, np.float32), np.full((1024, 8), 1 / 1024, np.float32))
+    np.testing.assert_allclose(c32, 7e4, rtol=1e-6)
+
+
+def test_gemm_k1_signed_zero():
+    # ops/binary_ops.mm:904-1004: K == 1 is a multiply and keeps -0.
+    c = gemm.dot_general(np.array([[-0.0, 2.0]]).T, np.array([[1.0, -0.0]]))
+    assert np.signbit(c[0, 0]) and c[0, 0] == 0
+    assert np.signbit(c[1, 1]) and c[1, 1] == 0
+
+
+def test_dot_general_batch_contract_brute_force():
+    rng = np.random.default_rng(7)
+    a = rng.standard_normal((2, 3, 4))   # [b, k, m]
+    b = rng.standard_normal((4, 2, 3))   # [n, b, k]
+    c = gemm.dot_general(a, b, lhs_batch=(0,), rhs_batch=(1,), lhs_contract=(1,), rhs_contract=(2,))
+    assert c.shape == (2, 4, 4)
+    for bi in range(2):
+        for m in range(4):
+            for n in range(4):
+                s = sum(a[bi, k, m] * b[n, bi, k] for k in range(3))
+                assert abs(c[bi, m, n] - s) < 1e-12
+
+
+def test_rel_err_measure():
+    assert gemm.rel_err([1.0, 2.0], [1.0, 2.0]) == 0
+    assert gemm.rel_err([1.0, 2.5], [1.0, 2.0]) == 0.25
+
+
+# ----------------------------------------------------------------- rowops
+
+def _softmax_special():
+    # restates tests/test_native_softmax.py:_special
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((8, 40)) * 4).astype(np.float32)
+    x[0, 3] = np.nan
+    x[1, :] = -np.inf
+    x[2, 5] = np.inf
+    x[3, 0] = np.nan
+    x[3, 1:] = -np.inf
+    x[4, :] = 80.0
+    x[5, 7] = -np.inf
+    return x
+
+
+def test_softmax_special_rows():
+    x = _softmax_special()
+    y = rowops.softmax(x)
+    for r in range(4):
+        assert np.all(np.isnan(y[r])), r
+    np.testing.assert_allclose(y[4], 1 / 40)
+    assert y[5, 7] == 0
+    for r in (5, 6, 7):
+        assert abs(y[r].sum() - 1) < 1e-12
+        row = x[r].astype(np.float64)
+        e = [math.exp(v - max(row)) for v in row]
+        np.testing.assert_allclose(y[r], np.array(e) / sum(e), rtol=1e-12)
+
+
+def test_softmax_bf16_rounding_points():
+    x = bf16.f32_to_bf16_bits(np.array([[0.0, 0.0, 0.0, 0.0], [1.0, 1.0, 1.0, 80.0]], np.float32))
+    y = bf16.bf16_bits_to_f32(rowops.softmax_bf16(x))
+    np.testing.assert_array_equal(y[0], [0.25] * 4)
+    assert y[1, 3] == 1.0
+    np.testing.assert_allclose(y[1, :3], math.exp(-79.0), rtol=2 ** -7)
+
+
+def test_rmsnorm_closed_form_and_loop():
+    g = np.array([0.5, 1.0, 1.5, 2.0])
+    x = np.full((1, 4), -3.0)
+    y = rowops.rmsnorm(x, g, eps=0.0)
+    np.testing.assert_allclose(y[0], -g)
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((3, 9))
+    g = rng.uniform(0.5, 1.5, 9)
+    y = rowops.rmsnorm(x, g)
+    for r in range(3):
+        ms = sum(v * v for v in x[r]) / 9
+        for c in range(9):
+            assert abs(y[r, c] - x[r, c] / math.sqrt(ms + 1e-6) * g[c]) < 1e-12
+
+
+def _edge(shape, seed):
+    # restates tests/test_argreduce_nan.py:_edge
+    special_vals = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 1.0, -1.0, 3.5], np.float32)
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal(shape).astype(np.float32)
+    special = rng.random(shape) < 0.7
+    x[special] = rng.choice(special_vals, size=int(special.sum()))
+    return x
+
+
+@pytest.mark.parametrize("shape,seed", [((512, 37), 0), ((300, 1), 0), ((8, 2049), 3), ((64, 300), 5)])
+def test_argmax_special_values_vs_brute(shape, seed):
+    x = _edge(shape, seed)
+    got = rowops.argmax(x)
+    ref = [rowops.brute_argmax_row(list(row)) for row in x]
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_argmax_known_rows():
+    # tests/test_argreduce_nan.py:57-66 with the answers XLA's rule fixes.
+    x = np.random.default_rng(1).standard_normal((6, 16)).astype(np.float32)
+    x[0] = np.nan
+    x[1, 5] = np.nan
+    x[1, 9] = np.nan
+    x[2] = 2.0
+    x[3, :4] = [np.inf, np.nan, -np.inf, np.nan]
+    x[4, -1] = np.nan
+    got = rowops.argmax(x)
+    assert got[:5].tolist() == [0, 5, 0, 1, 15]
+    assert got[5] == int(np.argmax(x[5]))
+    z = np.array([[-0.0, 0.0], [0.0, -0.0], [-1.0, -0.0]], np.float32)
+    assert rowops.argmax(z).tolist() == [0, 0, 1]
+
+
+def test_argmax_int_ties_lowest_index():
+    x = np.array([[5, 9, 9, 1], [-3, -3, -3, -3]], np.int32)
+    assert rowops.argmax(x).tolist() == [1, 0]
+
+
+def test_reduce_sum_max():
+    x = np.array([[1.0, np.nan, 2.0], [-0.0, 0.0, -1.0], [-0.0, -0.0, -2.0], [1.0, 2.0, 3.0]])
+    m = rowops.reduce_max(x)
+    assert np.isnan(m[0])
+    assert m[1] == 0 and not np.signbit(m[1])
+    assert m[2] == 0 and np.signbit(m[2])
+    assert m[3] == 3
+    assert rowops.reduce_sum(x[3:]).tolist() == [6.0]
+
+
+# ----------------------------------------------------------------- eltwise
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_chain6_spot_values(dtype):
+    x = np.array([0.0, -1.0, 2.0, -0.0], np.float32)
+    y = eltwise.evaluate(eltwise.CHAIN6, [x], dtype)
+    assert y[0] == 0.5 and y[1] == -1.0 and y[3] == 0.5
+    if dtype == "f32":
+        assert abs(y[2] - math.log1p(math.exp(3.5))) < 1e-6
+    else:
+        # exp(3.5) = 33.115 rounds to 33.0 in bf16, log1p(33) = 3.5264 -> 3.53125
+        assert y[2] == 3.53125
+
+
+def test_chain6_brute_force_per_element():
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal(200) * math.sqrt(2)).astype(np.float32)
+    y = eltwise.evaluate(eltwise.CHAIN6, [x], "f32")
+    for v, out in zip(x.tolist(), y.tolist()):
+        b = float(np.float32(float(np.float32(v * 1.5)) + 0.5))
+        d = float(np.float32(math.log1p(float(np.float32(math.exp(b))))))
+        ref = max(d, v) if v > 0 else b
+        assert abs(out - ref) <= 1e-6 * max(1.0, abs(ref))
+
+
+def test_eltwise_nan_and_signed_zero_max():
+    prog = [("maximum", (0, 1))]
+    a = np.array([np.nan, 1.0, -0.0, 0.0], np.float32)
+    b = np.array([1.0, np.nan, 0.0, -0.0], np.float32)
+    y = eltwise.evaluate(prog, [a, b])
+    assert np.isnan(y[0]) and np.isnan(y[1])
+    assert y[2] == 0 and not np.signbit(y[2]) and not np.signbit(y[3])
