@@ -1,0 +1,103 @@
+/*
+ * mk_kernels.h -- C-ABI of the MI355X (gfx950) hot-path kernels.
+ *
+ * This is the internal operator boundary of the plugin: the executor calls
+ * these entry points where the reference calls a NativeOpHandler
+ * (src/pjrt_plugin/ops/registry.h:87-88, a function taking the device, the
+ * command buffer, the op and its input buffers) or encodes an MPSGraph
+ * segment (src/pjrt_plugin/core/mps_executable.mm:7328-7388).
+ *
+ * Conventions (all entry points):
+ *   - pointers are device pointers (hipMalloc'd), row-major, densely packed;
+ *   - bf16 tensors are 16-bit bit patterns (uint16_t storage);
+ *   - `stream` is a hipStream_t (0 = the null stream); every call is
+ *     asynchronous on it and allocates nothing;
+ *   - shapes are validated on the host before any launch; the return value is
+ *     MK_OK or an MK_E* code, and mk_last_error() describes the failure.
+ *     Nothing is launched when a call fails validation.
+ */
+#ifndef MK_KERNELS_H_
+#define MK_KERNELS_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  MK_OK = 0,
+  MK_EINVAL = 1,        /* bad pointer, shape or size */
+  MK_EUNSUPPORTED = 2,  /* valid request this build does not implement */
+  MK_EWORKSPACE = 3,    /* workspace missing or too small */
+  MK_ELAUNCH = 4        /* the HIP launch itself failed */
+};
+
+/* Message for the last failing call on this thread ("" when none). */
+const char* mk_last_error(void);
+
+/* Library version string. */
+const char* mk_version(void);
+
+/* ------------------------------------------------------------------------
+ * Quantized matmul (decode-shaped: weight-stationary, HBM bound).
+ *
+ * Replaces the reference's affine quantized GEMM
+ * (src/jax_plugins/silicon/quantized.py:1077-1152, kernels :760-958), which
+ * reads W [N, K] as uint32 words of eight nibbles and runs outside jax.jit,
+ * with the workload's jit-level format:
+ *
+ *   int4 g64:  x bf16 [M, K]; w_packed uint8 [K/2, N], two nibbles per byte
+ *              along K, low nibble = even k (reference nibble order,
+ *              quantized.py:189-190); scale bf16 [K/64, N]; zero uint8
+ *              [K/64, N] holding 0..15.  y = x @ ((w - zero) * scale), bf16
+ *              [M, N], f32 accumulation.
+ *   int8 pc:   x bf16 [M, K]; w int8 [K, N]; scale f32 [N].
+ *              y = x @ (w * scale), bf16 [M, N], f32 accumulation.
+ *
+ * Both need K % 64 == 0 and N % 8 == 0.  `workspace` receives split-K
+ * partial sums when a call splits K across workgroups (small N, or x too
+ * large for LDS); mk_qmatmul_workspace_bytes gives the size, 0 when none is
+ * needed (then workspace may be NULL).  Its contents need no initialisation.
+ * Calls that share a workspace must be ordered (same stream).
+ * ---------------------------------------------------------------------- */
+enum { MK_QFMT_INT4_G64 = 0, MK_QFMT_INT8_PC = 1 };
+
+int64_t mk_qmatmul_workspace_bytes(int fmt, int64_t M, int64_t K, int64_t N);
+
+int mk_int4g64_matmul_bf16(const void* x, const void* w_packed, const void* scale,
+                           const void* zero, void* y, int64_t M, int64_t K, int64_t N,
+                           void* workspace, int64_t workspace_bytes, void* stream);
+
+int mk_int8pc_matmul_bf16(const void* x, const void* w, const void* scale, void* y,
+                          int64_t M, int64_t K, int64_t N, void* workspace,
+                          int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * dot_general GEMM (canonical batched NN form).
+ *
+ * Replaces the reference's dot_general lowering (HandleDotGeneral,
+ * src/pjrt_plugin/ops/binary_ops.mm:644-1100; rank-2 NN path :1011-1019;
+ * native tiled kernels runtime/metal_kernels.mm:2477-2761 selected by
+ * ClassifyDotGeneralNN, core/mps_executable.mm:2706-2891).  The executor
+ * reduces dot_general (batch dims, contracting dims, transposes) to
+ *   C[b] = A[b] @ B[b],  A [batch, M, K], B [batch, K, N], C [batch, M, N],
+ * all row-major and densely packed.
+ *
+ * mk_gemm_bf16: bf16 inputs, f32 accumulation; C is bf16 (out_f32 = 0) or
+ *   f32 (out_f32 = 1, dot_general with preferred_element_type = f32,
+ *   binary_ops.mm:775-782).
+ * mk_gemm_f32:  f32 inputs and output, f32 products and accumulation.
+ * Both need K % 8 == 0 and N % 8 == 0 (else MK_EUNSUPPORTED).
+ * ---------------------------------------------------------------------- */
+int mk_gemm_bf16(const void* a, const void* b, void* c, int64_t batch, int64_t M, int64_t N,
+                 int64_t K, int out_f32, void* stream);
+
+int mk_gemm_f32(const void* a, const void* b, void* c, int64_t batch, int64_t M, int64_t N,
+                int64_t K, void* stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* MK_KERNELS_H_ */

@@ -1,0 +1,441 @@
+// dot_general GEMM for gfx950: C[b] = A[b] @ B[b], row-major A [M,K] and
+// B [K,N] (the canonical form the executor reduces dot_general to; reference
+// HandleDotGeneral, ops/binary_ops.mm:644-1100, rank-2 NN path :1011-1019,
+// and the generated tiled kernels runtime/metal_kernels.mm:2477-2761).
+//
+// bf16 x bf16 -> f32 accumulation -> bf16 or f32 output
+//   (preferred_element_type = f32 returns f32, binary_ops.mm:775-782)
+// f32  x f32  -> f32 (v_mfma_f32_16x16x4_f32, full f32 products)
+//
+// Design:
+//   * Block tile BM x BN x 64 (bf16) with WM x WN waves; every wave owns a
+//     (BM/WM) x (BN/WN) sub-tile of 16x16 MFMA tiles held in accumulators.
+//   * Global -> registers -> LDS double buffering, one barrier per k-tile:
+//     the next k-tile's global loads are in flight while the MFMAs consume
+//     the current one.
+//   * A is staged as-is ([m][k], k contiguous).  B arrives n-contiguous, but
+//     the MFMA wants k runs per lane, so each thread transposes an 8x8 block
+//     of B in registers (v_perm_b32 on 16-bit halves) while staging; LDS then
+//     holds B as [n][k].  Rows are padded to 144 B so the 16-byte fragment
+//     reads of 16 consecutive rows hit distinct LDS banks.
+//   * The MFMA is issued as B-fragment x A-fragment, which yields C^T tiles:
+//     each lane then owns 4 consecutive columns of one row, stored as one
+//     8-byte (bf16) or 16-byte (f32) write.
+//   * Workgroup -> tile mapping is XCD-aware: runs of consecutive logical
+//     ids stay on one XCD and cover a 4-row band of tiles, so the A panels and
+//     B panels they share stay in that XCD's L2.
+#include "common.h"
+
+namespace mk {
+
+struct GemmArgs {
+  const void* a;
+  const void* b;
+  void* c;
+  int M, N, K;
+  int64_t sa, sb, sc;  // batch strides in elements
+  int out_f32;         // bf16 kernel: 1 -> f32 output, 0 -> bf16 output
+};
+
+// Map a logical workgroup id to a (tile row, tile col) with bands of GM tile
+// rows, so consecutive ids sweep a GM-tall column block.
+__device__ __forceinline__ void tile_coords(uint32_t L, int tiles_m, int tiles_n, int& tm, int& tn) {
+  constexpr int GM = 4;
+  if (tiles_m % GM == 0) {
+    const int band = (int)L / (GM * tiles_n);
+    const int r = (int)L - band * GM * tiles_n;
+    tm = band * GM + r % GM;
+    tn = r / GM;
+  } else {
+    tm = (int)L / tiles_n;
+    tn = (int)L - tm * tiles_n;
+  }
+}
+
+template <int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmArgs p) {
+  constexpr int BK = 64;
+  constexpr int LDK = BK + 8;  // padded row length (bf16 elements)
+  constexpr int NT = WM * WN * 64;
+  constexpr int TM = BM / WM / 16;
+  constexpr int TN = BN / WN / 16;
+  constexpr int ACH = BM * BK / 8 / NT;             // A 16-byte chunks per thread
+  constexpr int BTOT = (BK / 8) * (BN / 8);         // B 8x8 blocks per tile
+  constexpr int BBL = (BTOT + NT - 1) / NT;         // B blocks per thread
+  static_assert(ACH * NT * 8 == BM * BK, "A staging must divide evenly");
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint16_t* As = reinterpret_cast<uint16_t*>(smem);  // [2][BM][LDK]
+  uint16_t* Bs = As + 2 * BM * LDK;                   // [2][BN][LDK]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int tiles_m = (p.M + BM - 1) / BM, tiles_n = (p.N + BN - 1) / BN;
+  int tm, tn;
+  tile_coords(xcd_logical_id(blockIdx.x, gridDim.x), tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const uint16_t* A = static_cast<const uint16_t*>(p.a) + (size_t)blockIdx.z * p.sa;
+  const uint16_t* B = static_cast<const uint16_t*>(p.b) + (size_t)blockIdx.z * p.sb;
+  const int M = p.M, N = p.N, K = p.K;
+
+  u32x4 ra[ACH];
+  u32x4 rb[BBL][8];
+
+  auto load_tile = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int q = tid + i * NT;
+      const int row = q / (BK / 8), kc = q % (BK / 8);
+      const int gm = m0 + row, gk = k0 + 8 * kc;
+      ra[i] = (gm < M && gk < K) ? *reinterpret_cast<const u32x4*>(A + (size_t)gm * K + gk)
+                                 : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int i = 0; i < BBL; ++i) {
+      const int q = tid + i * NT;
+      const int kb = q / (BN / 8), nb = q % (BN / 8);
+      const int gn = n0 + 8 * nb;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const int gk = k0 + 8 * kb + r;
+        rb[i][r] = (q < BTOT && gn < N && gk < K) ? *reinterpret_cast<const u32x4*>(B + (size_t)gk * N + gn)
+                                      : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  };
+
+  auto store_tile = [&](int buf) {
+    uint16_t* as = As + buf * BM * LDK;
+    uint16_t* bs = Bs + buf * BN * LDK;
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int q = tid + i * NT;
+      const int row = q / (BK / 8), kc = q % (BK / 8);
+      *reinterpret_cast<u32x4*>(as + row * LDK + 8 * kc) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < BBL; ++i) {
+      const int q = tid + i * NT;
+      if (q >= BTOT) break;
+      const int kb = q / (BN / 8), nb = q % (BN / 8);
+      // Transpose the 8 (k) x 8 (n) block: column c gets halfword c of rows 0..7.
+      const uint32_t* w = reinterpret_cast<const uint32_t*>(&rb[i][0]);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+        const int d = c >> 1;
+        u32x4 o;
+        o.x = perm(w[1 * 4 + d], w[0 * 4 + d], sel);
+        o.y = perm(w[3 * 4 + d], w[2 * 4 + d], sel);
+        o.z = perm(w[5 * 4 + d], w[4 * 4 + d], sel);
+        o.w = perm(w[7 * 4 + d], w[6 * 4 + d], sel);
+        *reinterpret_cast<u32x4*>(bs + (8 * nb + c) * LDK + 8 * kb) = o;
+      }
+    }
+  };
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int KT = (K + BK - 1) / BK;
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+
+  const int arow = wm * TM * 16 + (lane & 15);
+  const int brow = wn * TN * 16 + (lane & 15);
+  const int kofs = 8 * (lane >> 4);
+
+  for (int kt = 0; kt < KT; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < KT) load_tile((kt + 1) * BK);
+    const uint16_t* as = As + buf * BM * LDK;
+    const uint16_t* bs = Bs + buf * BN * LDK;
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      u32x4 af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        af[i] = *reinterpret_cast<const u32x4*>(as + (arow + 16 * i) * LDK + 32 * ks + kofs);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        bf[j] = *reinterpret_cast<const u32x4*>(bs + (brow + 16 * j) * LDK + 32 * ks + kofs);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(bf[j], af[i], acc[i][j]);
+    }
+    if (kt + 1 < KT) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue: lane owns row m, columns n..n+3 of each 16x16 tile.
+  const int mrow = m0 + wm * TM * 16 + (lane & 15);
+  const int ncol = n0 + wn * TN * 16 + 4 * (lane >> 4);
+  if (p.out_f32) {
+    float* C = static_cast<float*>(p.c) + (size_t)blockIdx.z * p.sc;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = mrow + 16 * i;
+      if (m >= M) continue;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = ncol + 16 * j;
+        if (n < N) *reinterpret_cast<f32x4*>(C + (size_t)m * N + n) = acc[i][j];
+      }
+    }
+  } else {
+    uint16_t* C = static_cast<uint16_t*>(p.c) + (size_t)blockIdx.z * p.sc;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = mrow + 16 * i;
+      if (m >= M) continue;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = ncol + 16 * j;
+        if (n < N) {
+          u32x2 o;
+          o.x = pack_bf16x2(acc[i][j].x, acc[i][j].y);
+          o.y = pack_bf16x2(acc[i][j].z, acc[i][j].w);
+          *reinterpret_cast<u32x2*>(C + (size_t)m * N + n) = o;
+        }
+      }
+    }
+  }
+}
+
+// f32 GEMM: v_mfma_f32_16x16x4_f32.  Within each 32-k chunk a lane of k
+// block j (= lane / 16) feeds k = 8j + s to the s-th MFMA, for both operands,
+// so a fragment is 8 consecutive floats of one row (two 16-byte LDS reads).
+template <int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_f32_kernel(GemmArgs p) {
+  constexpr int BK = 32;
+  constexpr int LDK = BK + 4;  // padded row length (floats): 144 B
+  constexpr int NT = WM * WN * 64;
+  constexpr int TM = BM / WM / 16;
+  constexpr int TN = BN / WN / 16;
+  constexpr int ACH = BM * BK / 4 / NT;          // A 16-byte chunks per thread
+  constexpr int BTOT = (BK / 4) * (BN / 4);      // B 4x4 blocks per tile
+  constexpr int BBL = (BTOT + NT - 1) / NT;      // B blocks per thread
+  static_assert(ACH * NT * 4 == BM * BK, "A staging must divide evenly");
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* As = reinterpret_cast<float*>(smem);  // [2][BM][LDK]
+  float* Bs = As + 2 * BM * LDK;               // [2][BN][LDK]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int tiles_m = (p.M + BM - 1) / BM, tiles_n = (p.N + BN - 1) / BN;
+  int tm, tn;
+  tile_coords(xcd_logical_id(blockIdx.x, gridDim.x), tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const float* A = static_cast<const float*>(p.a) + (size_t)blockIdx.z * p.sa;
+  const float* B = static_cast<const float*>(p.b) + (size_t)blockIdx.z * p.sb;
+  const int M = p.M, N = p.N, K = p.K;
+
+  f32x4 ra[ACH];
+  f32x4 rb[BBL][4];
+
+  auto load_tile = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int q = tid + i * NT;
+      const int row = q / (BK / 4), kc = q % (BK / 4);
+      const int gm = m0 + row, gk = k0 + 4 * kc;
+      ra[i] = (gm < M && gk < K) ? *reinterpret_cast<const f32x4*>(A + (size_t)gm * K + gk)
+                                 : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int i = 0; i < BBL; ++i) {
+      const int q = tid + i * NT;
+      const int kb = q / (BN / 4), nb = q % (BN / 4);
+      const int gn = n0 + 4 * nb;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int gk = k0 + 4 * kb + r;
+        rb[i][r] = (q < BTOT && gn < N && gk < K) ? *reinterpret_cast<const f32x4*>(B + (size_t)gk * N + gn)
+                                      : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  };
+
+  auto store_tile = [&](int buf) {
+    float* as = As + buf * BM * LDK;
+    float* bs = Bs + buf * BN * LDK;
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int q = tid + i * NT;
+      const int row = q / (BK / 4), kc = q % (BK / 4);
+      *reinterpret_cast<f32x4*>(as + row * LDK + 4 * kc) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < BBL; ++i) {
+      const int q = tid + i * NT;
+      if (q >= BTOT) break;
+      const int kb = q / (BN / 4), nb = q % (BN / 4);
+      *reinterpret_cast<f32x4*>(bs + (4 * nb + 0) * LDK + 4 * kb) =
+          f32x4{rb[i][0].x, rb[i][1].x, rb[i][2].x, rb[i][3].x};
+      *reinterpret_cast<f32x4*>(bs + (4 * nb + 1) * LDK + 4 * kb) =
+          f32x4{rb[i][0].y, rb[i][1].y, rb[i][2].y, rb[i][3].y};
+      *reinterpret_cast<f32x4*>(bs + (4 * nb + 2) * LDK + 4 * kb) =
+          f32x4{rb[i][0].z, rb[i][1].z, rb[i][2].z, rb[i][3].z};
+      *reinterpret_cast<f32x4*>(bs + (4 * nb + 3) * LDK + 4 * kb) =
+          f32x4{rb[i][0].w, rb[i][1].w, rb[i][2].w, rb[i][3].w};
+    }
+  };
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int KT = (K + BK - 1) / BK;
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+
+  const int arow = wm * TM * 16 + (lane & 15);
+  const int brow = wn * TN * 16 + (lane & 15);
+  const int kofs = 8 * (lane >> 4);
+
+  for (int kt = 0; kt < KT; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < KT) load_tile((kt + 1) * BK);
+    const float* as = As + buf * BM * LDK;
+    const float* bs = Bs + buf * BN * LDK;
+    f32x4 af[TM][2], bf[TN][2];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      af[i][0] = *reinterpret_cast<const f32x4*>(as + (arow + 16 * i) * LDK + kofs);
+      af[i][1] = *reinterpret_cast<const f32x4*>(as + (arow + 16 * i) * LDK + kofs + 4);
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      bf[j][0] = *reinterpret_cast<const f32x4*>(bs + (brow + 16 * j) * LDK + kofs);
+      bf[j][1] = *reinterpret_cast<const f32x4*>(bs + (brow + 16 * j) * LDK + kofs + 4);
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(bf[j][s >> 2][s & 3], af[i][s >> 2][s & 3],
+                                                          acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < KT) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  float* C = static_cast<float*>(p.c) + (size_t)blockIdx.z * p.sc;
+  const int mrow = m0 + wm * TM * 16 + (lane & 15);
+  const int ncol = n0 + wn * TN * 16 + 4 * (lane >> 4);
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int m = mrow + 16 * i;
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = ncol + 16 * j;
+      if (n < N) *reinterpret_cast<f32x4*>(C + (size_t)m * N + n) = acc[i][j];
+    }
+  }
+}
+
+}  // namespace mk
+
+// ---------------------------------------------------------------------------
+// Host launchers
+// ---------------------------------------------------------------------------
+#include "../capi_internal.h"
+
+namespace {
+
+hipError_t lds_opt_in(const void* fn, size_t bytes) {
+  if (bytes <= 64 * 1024) return hipSuccess;
+  return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
+template <int BM, int BN, int WM, int WN>
+hipError_t launch_bf16(const mk::GemmArgs& a, int batch, hipStream_t st) {
+  constexpr size_t lds = (size_t)2 * (BM + BN) * (64 + 8) * 2;
+  const void* fn = (const void*)mk::gemm_bf16_kernel<BM, BN, WM, WN>;
+  hipError_t e = lds_opt_in(fn, lds);
+  if (e != hipSuccess) return e;
+  const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+  hipLaunchKernelGGL((mk::gemm_bf16_kernel<BM, BN, WM, WN>), dim3(tiles, 1, batch),
+                     dim3(WM * WN * 64), lds, st, a);
+  return hipGetLastError();
+}
+
+template <int BM, int BN, int WM, int WN>
+hipError_t launch_f32(const mk::GemmArgs& a, int batch, hipStream_t st) {
+  constexpr size_t lds = (size_t)2 * (BM + BN) * (32 + 4) * 4;
+  const void* fn = (const void*)mk::gemm_f32_kernel<BM, BN, WM, WN>;
+  hipError_t e = lds_opt_in(fn, lds);
+  if (e != hipSuccess) return e;
+  const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+  hipLaunchKernelGGL((mk::gemm_f32_kernel<BM, BN, WM, WN>), dim3(tiles, 1, batch),
+                     dim3(WM * WN * 64), lds, st, a);
+  return hipGetLastError();
+}
+
+int check_gemm(const char* fn, const void* a, const void* b, void* c, int64_t batch, int64_t M,
+               int64_t N, int64_t K) {
+  if (!a || !b || !c) return mkc::fail(MK_EINVAL, "%s: null pointer argument", fn);
+  if (batch <= 0 || M <= 0 || N <= 0 || K <= 0)
+    return mkc::fail(MK_EINVAL, "%s: batch, M, N, K must be positive (got %lld, %lld, %lld, %lld)",
+                     fn, (long long)batch, (long long)M, (long long)N, (long long)K);
+  if (K % 8 != 0 || N % 8 != 0)
+    return mkc::fail(MK_EUNSUPPORTED, "%s: needs K %% 8 == 0 and N %% 8 == 0 (got K=%lld, N=%lld)",
+                     fn, (long long)K, (long long)N);
+  if (M > (1 << 24) || N > (1 << 24) || K > (1 << 24) || batch > 65535 || M * K > ((int64_t)1 << 40))
+    return mkc::fail(MK_EINVAL, "%s: shape too large", fn);
+  return MK_OK;
+}
+
+int env_tile() {
+  const char* v = getenv("MK_GEMM_TILE");
+  return v ? atoi(v) : 0;
+}
+
+}  // namespace
+
+extern "C" int mk_gemm_bf16(const void* a, const void* b, void* c, int64_t batch, int64_t M,
+                            int64_t N, int64_t K, int out_f32, void* stream) {
+  mkc::clear_error();
+  int rc = check_gemm("mk_gemm_bf16", a, b, c, batch, M, N, K);
+  if (rc != MK_OK) return rc;
+  mk::GemmArgs p;
+  p.a = a; p.b = b; p.c = c;
+  p.M = (int)M; p.N = (int)N; p.K = (int)K;
+  p.sa = M * K; p.sb = K * N; p.sc = M * N;
+  p.out_f32 = out_f32 ? 1 : 0;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256) * batch;
+  int tile = env_tile();
+  if (tile == 0) tile = big_tiles >= 192 ? 256 : 128;
+  hipError_t e = tile == 256 ? launch_bf16<256, 256, 2, 2>(p, (int)batch, st)
+                             : launch_bf16<128, 128, 2, 2>(p, (int)batch, st);
+  if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "mk_gemm_bf16: launch failed: %s", hipGetErrorString(e));
+  return MK_OK;
+}
+
+extern "C" int mk_gemm_f32(const void* a, const void* b, void* c, int64_t batch, int64_t M,
+                           int64_t N, int64_t K, void* stream) {
+  mkc::clear_error();
+  int rc = check_gemm("mk_gemm_f32", a, b, c, batch, M, N, K);
+  if (rc != MK_OK) return rc;
+  mk::GemmArgs p;
+  p.a = a; p.b = b; p.c = c;
+  p.M = (int)M; p.N = (int)N; p.K = (int)K;
+  p.sa = M * K; p.sb = K * N; p.sc = M * N;
+  p.out_f32 = 1;
+  hipError_t e = launch_f32<128, 128, 2, 2>(p, (int)batch, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "mk_gemm_f32: launch failed: %s", hipGetErrorString(e));
+  return MK_OK;
+}

@@ -1,0 +1,65 @@
+"""ctypes binding of the kernel C-ABI (include/mk_kernels.h).
+
+The library is built in-tree by ``jax-metallib_amd/build.py`` (or
+``__graft_entry__.build()``).  Loading fails loudly when it is missing: the
+plugin has no CPU fallback.
+"""
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(os.path.dirname(HERE), "lib")
+KERNELS_SO = os.path.join(LIB_DIR, "libmk_kernels.so")
+
+MK_OK, MK_EINVAL, MK_EUNSUPPORTED, MK_EWORKSPACE, MK_ELAUNCH = 0, 1, 2, 3, 4
+MK_QFMT_INT4_G64, MK_QFMT_INT8_PC = 0, 1
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+
+# name -> (restype, argtypes); mirrors include/mk_kernels.h
+SIGNATURES = {
+    "mk_last_error": (ctypes.c_char_p, []),
+    "mk_version": (ctypes.c_char_p, []),
+    "mk_qmatmul_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64]),
+    "mk_int4g64_matmul_bf16": (_i32, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p]),
+    "mk_int8pc_matmul_bf16": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p]),
+    "mk_gemm_bf16": (_i32, [_p, _p, _p, _i64, _i64, _i64, _i64, _i32, _p]),
+    "mk_gemm_f32": (_i32, [_p, _p, _p, _i64, _i64, _i64, _i64, _p]),
+}
+
+_LIB = None
+
+
+class MKError(RuntimeError):
+    """A kernel entry point returned a non-zero MK_E* status."""
+
+    def __init__(self, code, msg):
+        super().__init__(f"[MK error {code}] {msg}")
+        self.code = code
+
+
+def lib():
+    """The loaded kernel library (raises if it has not been built)."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(KERNELS_SO):
+            raise RuntimeError(
+                f"{KERNELS_SO} is missing: build it with `python jax-metallib_amd/build.py` "
+                "(the plugin has no CPU fallback)")
+        L = ctypes.CDLL(KERNELS_SO)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = L
+    return _LIB
+
+
+def check(status):
+    """Raise MKError for a non-zero status, with mk_last_error()'s message."""
+    if status != MK_OK:
+        raise MKError(status, lib().mk_last_error().decode())
+    return status

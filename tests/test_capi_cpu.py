@@ -1,0 +1,68 @@
+"""Host-only checks of the kernel C-ABI (no GPU needed): the built library
+loads, exports every entry point include/mk_kernels.h declares, and rejects
+bad arguments on the host before any launch."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from mi355x import _lib
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared(header):
+    text = open(os.path.join(REPO, "include", header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mk_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    L = _lib.lib()
+    names = _declared("mk_kernels.h")
+    assert names, "no declarations parsed"
+    for n in names:
+        assert hasattr(L, n), f"{n} declared but not exported"
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature in mi355x/_lib.py"
+
+
+def test_workspace_query_is_host_only():
+    L = _lib.lib()
+    assert L.mk_qmatmul_workspace_bytes(_lib.MK_QFMT_INT4_G64, 16, 4096, 14336) >= 0
+    assert L.mk_qmatmul_workspace_bytes(_lib.MK_QFMT_INT4_G64, 16, 4096, 1024) > 0
+    assert L.mk_qmatmul_workspace_bytes(_lib.MK_QFMT_INT4_G64, 16, 4000, 14336) == -1
+    assert L.mk_qmatmul_workspace_bytes(7, 16, 4096, 14336) == -1
+
+
+@pytest.mark.parametrize("M,K,N,code", [
+    (0, 64, 8, _lib.MK_EINVAL),
+    (16, 100, 8, _lib.MK_EINVAL),   # K not a multiple of 64
+    (16, 64, 12, _lib.MK_EINVAL),   # N not a multiple of 8
+])
+def test_bad_shapes_rejected_before_launch(M, K, N, code):
+    L = _lib.lib()
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    rc = L.mk_int4g64_matmul_bf16(fake, fake, fake, fake, fake, M, K, N, fake, 1 << 30, None)
+    assert rc == code
+    assert L.mk_last_error()
+    rc = L.mk_int8pc_matmul_bf16(fake, fake, fake, fake, M, K, N, fake, 1 << 30, None)
+    assert rc == code
+
+
+def test_null_pointer_rejected():
+    L = _lib.lib()
+    rc = L.mk_int4g64_matmul_bf16(None, None, None, None, None, 16, 64, 8, None, 0, None)
+    assert rc == _lib.MK_EINVAL
+    assert b"null" in L.mk_last_error()
+
+
+def test_missing_workspace_rejected():
+    L = _lib.lib()
+    fake = ctypes.c_void_p(0x1000)
+    # N = 1024 gives 16 column tiles, so K is split across workgroups and a
+    # workspace is required; validation fails before any launch.
+    assert L.mk_qmatmul_workspace_bytes(_lib.MK_QFMT_INT4_G64, 16, 4096, 1024) > 0
+    rc = L.mk_int4g64_matmul_bf16(fake, fake, fake, fake, fake, 16, 4096, 1024, None, 0, None)
+    assert rc == _lib.MK_EWORKSPACE

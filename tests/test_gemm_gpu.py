@@ -1,0 +1,113 @@
+"""GPU parity of the dot_general GEMM kernels (mk_gemm_bf16 / mk_gemm_f32)
+against the oracle (float64 matmul, oracle/gemm.py) and closed forms.
+
+Tolerances are the workload's: bf16 output rel 2e-2, f32 rel 1e-5 (the
+reference's measure max|out - ref| / max|ref|,
+tests/test_f32_gemm_precision.py:25-27 under /root/reference)."""
+
+import numpy as np
+import pytest
+
+from _gpu import (BF16_RTOL, F32_RTOL, assert_rel_close, dev, dev_bf16, host_bf16, need_gpu,
+                  torch)
+from oracle import bf16 as obf
+from oracle import gemm
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    need_gpu()
+    from mi355x import ops
+    return ops
+
+
+def _case(rng, shape, scale):
+    return obf.f32_to_bf16_bits((rng.standard_normal(shape) * scale).astype(np.float32))
+
+
+BF16_SHAPES = [
+    (1, 16, 16, 64), (1, 128, 128, 128), (1, 200, 264, 72), (1, 1024, 1024, 1024),
+    (3, 64, 96, 40), (2, 300, 520, 136), (1, 4096, 4096, 4096), (16, 2048, 2048, 128),
+]
+
+
+@pytest.mark.parametrize("batch,M,N,K", BF16_SHAPES)
+@pytest.mark.parametrize("out_f32", [False, True])
+def test_gemm_bf16_matches_oracle(batch, M, N, K, out_f32):
+    ops = _ops()
+    if (M, N, K) == (4096, 4096, 4096) and not out_f32:
+        pytest.skip("covered by the f32-output run of the same shape")
+    rng = np.random.default_rng(batch * 131 + M + N + K)
+    a = _case(rng, (batch, M, K), 1.0 / np.sqrt(np.sqrt(K)))
+    b = _case(rng, (batch, K, N), 1.0 / np.sqrt(np.sqrt(K)))
+    print(f"gemm bf16 case b={batch} M={M} N={N} K={K} out_f32={out_f32}", flush=True)
+    c = ops.gemm_bf16(dev_bf16(a), dev_bf16(b), out_f32=out_f32)
+    torch.cuda.synchronize()
+    if M * N * K * batch > 2 ** 31:
+        # float64 reference on a row sample keeps the CPU cost bounded.
+        rows = np.random.default_rng(1).choice(M, size=min(M, 64), replace=False)
+        ref = np.matmul(obf.bf16_bits_to_f32(a[:, rows]).astype(np.float64),
+                        obf.bf16_bits_to_f32(b).astype(np.float64))
+        out = (c if out_f32 else c.float()).cpu().numpy()[:, rows]
+    else:
+        ref, _ = gemm.matmul_bf16(a, b)
+        out = (c.float() if not out_f32 else c).cpu().numpy()
+        out = out.reshape(ref.shape)
+    # f32 output is exact bf16 products accumulated in f32; bf16 output adds
+    # one rounding.
+    assert_rel_close(out, ref, 1e-5 * 8 if out_f32 else BF16_RTOL, f"bf16 gemm {batch}x{M}x{N}x{K}")
+
+
+def test_gemm_bf16_closed_forms():
+    ops = _ops()
+    K = 512
+    eye = np.eye(K, dtype=np.float32)
+    rng = np.random.default_rng(3)
+    a = obf.f32_to_bf16_bits(rng.standard_normal((64, K)).astype(np.float32))
+    c = ops.gemm_bf16(dev_bf16(a), dev_bf16(obf.f32_to_bf16_bits(eye)), out_f32=True)
+    assert np.array_equal(c.cpu().numpy(), obf.bf16_bits_to_f32(a))  # A @ I == A exactly
+    ones = obf.f32_to_bf16_bits(np.ones((32, K), np.float32))
+    ones_b = obf.f32_to_bf16_bits(np.ones((K, 24), np.float32))
+    c = ops.gemm_bf16(dev_bf16(ones), dev_bf16(ones_b), out_f32=True)
+    assert np.all(c.cpu().numpy() == K)
+
+
+F32_SHAPES = [(1, 16, 16, 32), (1, 2048, 2048, 2048), (1, 100, 136, 48), (4, 256, 128, 512),
+              (1, 1024, 1024, 1024)]
+
+
+@pytest.mark.parametrize("batch,M,N,K", F32_SHAPES)
+def test_gemm_f32_matches_oracle(batch, M, N, K):
+    ops = _ops()
+    rng = np.random.default_rng(batch + M + 7 * N + K)
+    a = (rng.standard_normal((batch, M, K)) / np.sqrt(np.sqrt(K))).astype(np.float32)
+    b = (rng.standard_normal((batch, K, N)) / np.sqrt(np.sqrt(K))).astype(np.float32)
+    print(f"gemm f32 case b={batch} M={M} N={N} K={K}", flush=True)
+    c = ops.gemm_f32(dev(a), dev(b))
+    torch.cuda.synchronize()
+    ref, _ = gemm.matmul_f32(a, b)
+    assert_rel_close(c.cpu().numpy().reshape(ref.shape), ref, F32_RTOL, f"f32 gemm {batch}x{M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("scale", [1.0, 1e3, 1e5])
+def test_gemm_f32_precision_scales(scale):
+    """The reference's f32 GEMM precision test: rel <= 2e-5 at scales 1, 1e3,
+    1e5 (tests/test_f32_gemm_precision.py:40-52); here at the workload's 1e-5."""
+    ops = _ops()
+    rng = np.random.default_rng(0)
+    a = (rng.standard_normal((256, 256)) * scale).astype(np.float32)
+    b = rng.standard_normal((256, 256)).astype(np.float32)
+    c = ops.gemm_f32(dev(a), dev(b))
+    ref, _ = gemm.matmul_f32(a, b)
+    assert_rel_close(c.cpu().numpy(), ref, F32_RTOL, f"scale {scale}")
+
+
+def test_gemm_f32_overflow_case():
+    """7e4-magnitude case of tests/test_f32_gemm_precision.py:55-60: the f32
+    path must not narrow to f16 (65504 max)."""
+    ops = _ops()
+    a = np.full((32, 32), 7e4, np.float32)
+    b = np.eye(32, dtype=np.float32)
+    c = ops.gemm_f32(dev(a), dev(b)).cpu().numpy()
+    assert np.all(c == 7e4)

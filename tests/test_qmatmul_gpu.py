@@ -1,0 +1,132 @@
+"""GPU parity of the int4 group-64 and int8 per-channel dequant-matmul
+kernels (mk_int4g64_matmul_bf16 / mk_int8pc_matmul_bf16) against the oracle.
+
+The oracle restates Y = X @ ((W - z) * s) in float64 (oracle/quant.py) and
+in C (oracle/c/oracle.c); the workload's bf16 tolerance is rel 2e-2.
+"""
+
+import numpy as np
+import pytest
+
+from _gpu import (BF16_RTOL, assert_rel_close, dev, dev_bf16, host_bf16, host_bf16_bits, need_gpu,
+                  torch)
+from oracle import cport, quant
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    need_gpu()
+    from mi355x import ops
+    return ops
+
+
+INT4_SHAPES = [
+    (1, 64, 8), (16, 128, 128), (5, 256, 264), (16, 1024, 1024), (3, 512, 136),
+    (17, 256, 384), (33, 192, 512), (16, 4096, 1024), (64, 2048, 896),
+]
+
+
+@pytest.mark.parametrize("M,K,N", INT4_SHAPES)
+def test_int4_g64_matches_oracle(M, K, N):
+    ops = _ops()
+    rng = np.random.default_rng(1000 + M * 7 + K + N)
+    x, packed, s, z = quant.make_int4_case(rng, M, K, N)
+    print(f"int4 case M={M} K={K} N={N}", flush=True)
+    y = ops.int4_g64_matmul(dev_bf16(x), dev(packed), dev_bf16(s), dev(z))
+    torch.cuda.synchronize()
+    ref, _ = quant.int4_g64_matmul(x, packed, s, z)
+    assert_rel_close(host_bf16(y), ref, BF16_RTOL, f"int4 {M}x{K}x{N}")
+
+
+def test_int4_g64_headline_shape():
+    """M=16, K=4096, N=14336 (the workload's headline case) vs the C oracle."""
+    ops = _ops()
+    rng = np.random.default_rng(0)
+    M, K, N = 16, 4096, 14336
+    x, packed, s, z = quant.make_int4_case(rng, M, K, N)
+    y = ops.int4_g64_matmul(dev_bf16(x), dev(packed), dev_bf16(s), dev(z))
+    torch.cuda.synchronize()
+    ref = cport.int4_g64_matmul(x, packed, s, z)
+    assert_rel_close(host_bf16(y), ref, BF16_RTOL, "int4 headline")
+
+
+def test_int4_g64_deterministic_and_reusable_workspace():
+    ops = _ops()
+    rng = np.random.default_rng(5)
+    x, packed, s, z = quant.make_int4_case(rng, 16, 4096, 2048)
+    args = (dev_bf16(x), dev(packed), dev_bf16(s), dev(z))
+    y1 = host_bf16_bits(ops.int4_g64_matmul(*args))
+    y2 = host_bf16_bits(ops.int4_g64_matmul(*args))
+    torch.cuda.synchronize()
+    assert np.array_equal(y1, y2)
+
+
+def test_int4_g64_shapes_in_sequence_share_workspace():
+    """Calls of different shapes back to back through one cached workspace
+    (a split-K shape between whole-K shapes) all match the oracle."""
+    ops = _ops()
+    rng = np.random.default_rng(11)
+    for (M, K, N) in [(16, 1024, 1024), (3, 512, 136), (16, 4096, 14336), (5, 4096, 512)]:
+        x, packed, s, z = quant.make_int4_case(rng, M, K, N)
+        y = ops.int4_g64_matmul(dev_bf16(x), dev(packed), dev_bf16(s), dev(z))
+        torch.cuda.synchronize()
+        ref = cport.int4_g64_matmul(x, packed, s, z)
+        assert_rel_close(host_bf16(y), ref, BF16_RTOL, f"int4 seq {M}x{K}x{N}")
+
+
+def test_int4_g64_known_answer_all_ones():
+    """x = 1, q = 15, z = 14, s = 0.5: every output is K * 0.5."""
+    ops = _ops()
+    M, K, N = 4, 256, 128
+    x = np.full((M, K), 0x3F80, np.uint16)
+    packed = np.full((K // 2, N), 0xFF, np.uint8)
+    s = np.full((K // 64, N), 0x3F00, np.uint16)
+    z = np.full((K // 64, N), 14, np.uint8)
+    y = host_bf16(ops.int4_g64_matmul(dev_bf16(x), dev(packed), dev_bf16(s), dev(z)))
+    assert np.all(y == K * 0.5)
+
+
+INT8_SHAPES = [(1, 64, 8), (16, 256, 128), (7, 512, 264), (16, 4096, 1024), (20, 320, 256)]
+
+
+@pytest.mark.parametrize("M,K,N", INT8_SHAPES)
+def test_int8_pc_matches_oracle(M, K, N):
+    ops = _ops()
+    rng = np.random.default_rng(2000 + M + K + N)
+    x, w, s = quant.make_int8_case(rng, M, K, N)
+    print(f"int8 case M={M} K={K} N={N}", flush=True)
+    y = ops.int8_pc_matmul(dev_bf16(x), dev(w), dev(s))
+    torch.cuda.synchronize()
+    ref, _ = quant.int8_pc_matmul(x, w, s)
+    assert_rel_close(host_bf16(y), ref, BF16_RTOL, f"int8 {M}x{K}x{N}")
+
+
+def test_int8_pc_headline_shape():
+    ops = _ops()
+    rng = np.random.default_rng(0)
+    M, K, N = 16, 4096, 14336
+    x, w, s = quant.make_int8_case(rng, M, K, N)
+    y = ops.int8_pc_matmul(dev_bf16(x), dev(w), dev(s))
+    torch.cuda.synchronize()
+    ref = cport.int8_pc_matmul(x, w, s)
+    assert_rel_close(host_bf16(y), ref, BF16_RTOL, "int8 headline")
+
+
+def test_workspace_too_small_is_rejected_before_launch():
+    ops = _ops()
+    from mi355x import _lib
+    L = _lib.lib()
+    M, K, N = 16, 4096, 1024  # 16 column tiles: K is split, a workspace is needed
+    need = L.mk_qmatmul_workspace_bytes(_lib.MK_QFMT_INT4_G64, M, K, N)
+    assert need > 0
+    x = torch.zeros((M, K), dtype=torch.bfloat16, device="cuda:0")
+    w = torch.zeros((K // 2, N), dtype=torch.uint8, device="cuda:0")
+    s = torch.zeros((K // 64, N), dtype=torch.bfloat16, device="cuda:0")
+    z = torch.zeros((K // 64, N), dtype=torch.uint8, device="cuda:0")
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda:0")
+    ws = torch.zeros(16, dtype=torch.uint8, device="cuda:0")
+    rc = L.mk_int4g64_matmul_bf16(x.data_ptr(), w.data_ptr(), s.data_ptr(), z.data_ptr(),
+                                  y.data_ptr(), M, K, N, ws.data_ptr(), 16, None)
+    assert rc == _lib.MK_EWORKSPACE
+    assert b"workspace" in L.mk_last_error()
