@@ -30,7 +30,9 @@
 //     with its scale, y += s * (acc - (128 + z) * xsum) -- the scale is
 //     applied per group on the 16x16 MFMA tile instead of per weight.
 //   * x is staged once per wave in LDS, pre-permuted into the MFMA A-operand
-//     order, with its 64-k group sums.
+//     order.  The x row sums come from one extra MFMA per step against a B
+//     operand of bf16 ones, which lands them directly in the accumulator
+//     layout (lane (c, j) holds rows 4j..4j+3).
 //
 // Numerics: products bf16 x bf16 are exact in the MFMA and accumulate in
 // f32.  The dequantised weight (q - z) * s is used exactly; XLA:CPU rounds
@@ -87,18 +89,6 @@ __device__ __forceinline__ void stage_x(const QArgs& a, u32x4* xl, int lane, int
   }
 }
 
-// Sum of the 8 bf16 values of one staged fragment, in slot order.
-__device__ __forceinline__ float frag_sum(const u32x4& v) {
-  float s = 0.f;
-  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    s += bf16_to_f32(w[i] & 0xFFFFu);
-    s += bf16_to_f32(w[i] >> 16);
-  }
-  return s;
-}
-
 // 4x4 byte transpose: rows r0..r3 (4 bytes each) -> columns c0..c3, where
 // column b holds byte b of r0, r1, r2, r3 in bytes 0..3.
 __device__ __forceinline__ void transpose4x4(uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3,
@@ -144,10 +134,6 @@ __device__ __forceinline__ u32x4 unpack_int8(uint32_t t0, uint32_t t1) {
   b.z = pack_bf16x2(ubyte_f32<0>(t1), ubyte_f32<1>(t1));
   b.w = pack_bf16x2(ubyte_f32<2>(t1), ubyte_f32<3>(t1));
   return b;
-}
-
-__device__ __forceinline__ uint32_t load_w4(const uint8_t* p, bool ok) {
-  return ok ? *reinterpret_cast<const uint32_t*>(p) : 0u;
 }
 
 // Write this wave's y fragments ([4 tiles][4 rows]) into its LDS region as
@@ -198,50 +184,45 @@ __global__ __launch_bounds__(NW * kWave) void int4g64_gemv_kernel(QArgs a) {
   const int n0 = tile * kQCols;
   const int c = lane & 15, j = lane >> 4;
   const int kbeg = ksi * (a.K / a.ks) + wv * a.kwave;
-  const int ncol = n0 + 4 * c;
-  const bool colok = ncol < a.N;
+  // Columns past N (last tile) read column N-4 instead: their results are
+  // never stored, and every load stays in bounds without a branch.
+  const int ncol = min(n0 + 4 * c, a.N - 4);
   const int ngroups = a.kwave >> 6;
-  const size_t N = (size_t)a.N;
+  const uint32_t N = (uint32_t)a.N;
 
   unsigned char* wsm = smem + wv * a.wave_lds;
   u32x4* xl = reinterpret_cast<u32x4*>(wsm);
-  float* xs = reinterpret_cast<float*>(smem + NW * a.wave_lds) + wv * ngroups * kQRows;
 
-  // W rows of this lane: kp = kbeg/2 + 32*g + 16*h + 4*j + r (group g, step h).
-  const uint8_t* wbase = a.w + (size_t)(kbeg / 2 + 4 * j) * N + ncol;
-  const size_t sbase = (size_t)(kbeg >> 6) * N + ncol;
-  const uint16_t* sptr = reinterpret_cast<const uint16_t*>(a.s);
+  // Per-wave (uniform) base pointers plus 32-bit per-lane offsets, so the
+  // loads use the scalar-base addressing mode.  Lane rows: kp = kbeg/2 +
+  // 32*g + 16*h + 4*j + r for group g, step h.
+  const uint8_t* wwave = a.w + (size_t)(kbeg / 2) * N;
+  const uint16_t* swave = reinterpret_cast<const uint16_t*>(a.s) + (size_t)(kbeg >> 6) * N;
+  const uint8_t* zwave = a.z + (size_t)(kbeg >> 6) * N;
+  uint32_t woff[8];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) woff[4 * h + q] = (uint32_t)(16 * h + 4 * j + q) * N + (uint32_t)ncol;
 
   uint32_t rn[kQPF][8];
   u32x2 sn[kQPF];
   uint32_t zn[kQPF];
   auto load_group = [&](int g, uint32_t (&r)[8], u32x2& sv, uint32_t& zv) {
-    const uint8_t* p = wbase + (size_t)(32 * g) * N;
+    const uint8_t* wg = wwave + (size_t)(32 * g) * N;
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) r[4 * h + q] = load_w4(p + (size_t)(16 * h + q) * N, colok);
-    const size_t so = sbase + (size_t)g * N;
-    sv = colok ? *reinterpret_cast<const u32x2*>(sptr + so) : u32x2{0u, 0u};
-    zv = colok ? *reinterpret_cast<const uint32_t*>(a.z + so) : 0u;
+    for (int q = 0; q < 8; ++q) r[q] = *reinterpret_cast<const uint32_t*>(wg + woff[q]);
+    sv = *reinterpret_cast<const u32x2*>(swave + (size_t)g * N + ncol);
+    zv = *reinterpret_cast<const uint32_t*>(zwave + (size_t)g * N + ncol);
   };
 #pragma unroll
   for (int p = 0; p < kQPF; ++p)
     if (p < ngroups) load_group(p, rn[p], sn[p], zn[p]);
 
   stage_x<true>(a, xl, lane, m0, mrows, kbeg);
-  for (int t = lane; t < ngroups * kQRows; t += kWave) {
-    const int g = t >> 4, m = t & 15;
-    float s = 0.f;
-#pragma unroll
-    for (int cc = 0; cc < 8; ++cc) {
-      const int kc = 8 * g + cc;
-      s += frag_sum(xl[((kc >> 2) * 4 + (kc & 3)) * 16 + m]);
-    }
-    xs[g * kQRows + m] = s;
-  }
   __syncthreads();
 
+  const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0
   f32x4 y[4];
 #pragma unroll
   for (int w = 0; w < 4; ++w) y[w] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -258,26 +239,27 @@ __global__ __launch_bounds__(NW * kWave) void int4g64_gemv_kernel(QArgs a) {
       const uint32_t zv = zn[p];
       if (g + kQPF < ngroups) load_group(g + kQPF, rn[p], sn[p], zn[p]);
 
-      f32x4 acc[4];
+      f32x4 acc[4], xsum;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const u32x4 A = xl[((2 * g + h) * 4 + j) * 16 + c];
         uint32_t t[4];
         transpose4x4(rc[4 * h + 0], rc[4 * h + 1], rc[4 * h + 2], rc[4 * h + 3], t[0], t[1], t[2],
                      t[3]);
+        const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int w = 0; w < 4; ++w)
-          acc[w] = mfma16x16x32(A, unpack_int4(t[w]), h == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[w]);
+        for (int w = 0; w < 4; ++w) acc[w] = mfma16x16x32(A, unpack_int4(t[w]), h == 0 ? zero4 : acc[w]);
+        // Row sums of x over the group (every column of this tile equal):
+        // lane (c, j) gets sum_k x[4j + i][k] in element i.
+        xsum = mfma16x16x32(A, ones, h == 0 ? zero4 : xsum);
       }
-      const f32x4 xv = *reinterpret_cast<const f32x4*>(xs + g * kQRows + 4 * j);
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         const uint32_t sw = (w < 2) ? sv.x : sv.y;
         const float sf = bf16_to_f32((w & 1) ? (sw >> 16) : (sw & 0xFFFFu));
         const float zf = (float)((zv >> (8 * w)) & 0xFFu);
-        const float sz = sf * (128.f + zf);
-        y[w] = sf * acc[w] + y[w];
-        y[w] = y[w] - sz * xv;
+        const float cz = 128.f + zf;
+        y[w] = sf * (acc[w] - cz * xsum) + y[w];
       }
     }
   }
@@ -300,37 +282,34 @@ __global__ __launch_bounds__(NW * kWave) void int8pc_gemv_kernel(QArgs a) {
   const int n0 = tile * kQCols;
   const int c = lane & 15, j = lane >> 4;
   const int kbeg = ksi * (a.K / a.ks) + wv * a.kwave;
-  const int ncol = n0 + 4 * c;
-  const bool colok = ncol < a.N;
+  const int ncol = min(n0 + 4 * c, a.N - 4);  // see int4g64_gemv_kernel
   const int nsteps = a.kwave >> 5;
-  const size_t N = (size_t)a.N;
+  const uint32_t N = (uint32_t)a.N;
 
   unsigned char* wsm = smem + wv * a.wave_lds;
   u32x4* xl = reinterpret_cast<u32x4*>(wsm);
-  float* xs = reinterpret_cast<float*>(smem + NW * a.wave_lds) + wv * kQRows;
 
-  // W rows of this lane: k = kbeg + 32*step + 8*j + r.
-  const uint8_t* wbase = a.w + (size_t)(kbeg + 8 * j) * N + ncol;
+  // Lane rows: k = kbeg + 32*step + 8*j + r.
+  const uint8_t* wwave = a.w + (size_t)kbeg * N;
+  uint32_t woff[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) woff[q] = (uint32_t)(8 * j + q) * N + (uint32_t)ncol;
 
   uint32_t rn[kQPF][8];
   auto load_step = [&](int st, uint32_t (&r)[8]) {
-    const uint8_t* p = wbase + (size_t)(32 * st) * N;
+    const uint8_t* ws = wwave + (size_t)(32 * st) * N;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) r[q] = load_w4(p + (size_t)q * N, colok);
+    for (int q = 0; q < 8; ++q) r[q] = *reinterpret_cast<const uint32_t*>(ws + woff[q]);
   };
 #pragma unroll
   for (int p = 0; p < kQPF; ++p)
     if (p < nsteps) load_step(p, rn[p]);
 
   stage_x<false>(a, xl, lane, m0, mrows, kbeg);
-  if (lane < kQRows) {
-    float s = 0.f;
-    for (int kc = 0; kc < (a.kwave >> 3); ++kc) s += frag_sum(xl[((kc >> 2) * 4 + (kc & 3)) * 16 + lane]);
-    xs[lane] = s;
-  }
   __syncthreads();
 
-  f32x4 y[4];
+  const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0
+  f32x4 y[4], xsum = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int w = 0; w < 4; ++w) y[w] = f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -349,14 +328,314 @@ __global__ __launch_bounds__(NW * kWave) void int8pc_gemv_kernel(QArgs a) {
       transpose4x4(rc[4], rc[5], rc[6], rc[7], hi[0], hi[1], hi[2], hi[3]);
 #pragma unroll
       for (int w = 0; w < 4; ++w) y[w] = mfma16x16x32(A, unpack_int8(lo[w], hi[w]), y[w]);
+      xsum = mfma16x16x32(A, ones, xsum);
     }
   }
   // Remove the +128 offset: y -= 128 * sum_k x over this wave's K range.
-  const f32x4 xv = *reinterpret_cast<const f32x4*>(xs + 4 * j);
 #pragma unroll
-  for (int w = 0; w < 4; ++w) y[w] = y[w] - 128.f * xv;
+  for (int w = 0; w < 4; ++w) y[w] = y[w] - 128.f * xsum;
   spill_y(wsm, y, c, j);
   reduce_and_store<NW, true>(a, smem, ksi, rb, m0, mrows, n0);
+}
+
+// ---------------------------------------------------------------------------
+// Streaming kernels (N % 16 == 0, the workload shapes).
+//
+// Every operand goes global -> LDS by DMA (global_load_lds_dwordx4: 16 B per
+// lane, written at M0 + 16 * lane, no VGPRs): per 32-k step one 1 KB block of
+// x fragments and one (int4) or two (int8) 1 KB blocks of weights, through a
+// ring of R steps per wave, plus the group scales / zero-points once.  A wave
+// thus keeps R steps of weight bytes in flight from its first instructions,
+// and since nothing is loaded into registers, every wait is explicit:
+// s_waitcnt vmcnt(n) lets exactly the step about to be consumed complete.
+// LDS reads are inline asm (ending in lgkmcnt(0)) because the compiler's
+// wait-count pass cannot tell which DMA an LDS read depends on and would
+// otherwise wait for the whole stream.  Their outputs are early-clobber
+// ("=&v"): a load's destination must never share a register with an address
+// that a later instruction of the same block still reads.
+//
+// Weight block = 16 W rows x 64 B.  DMA lane L = 16 r + 4 jj + kk loads row
+// (4 jj + r), bytes [16 kk, 16 kk + 16) of the tile, so MFMA lane (c, j),
+// which needs rows 4 j + r, bytes 4c..4c+3, reads dwords 64 r + 16 j + c:
+// the 64 lanes of each read hit 64 distinct banks.  x block: DMA lane L
+// loads MFMA lane L's own A fragment, read back as one contiguous 16 B.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void* lds_vptr;
+typedef __attribute__((address_space(1))) const void* glb_cptr;
+
+__device__ __forceinline__ void dma16(const void* g, void* lds_uniform) {
+  __builtin_amdgcn_global_load_lds((glb_cptr)g, (lds_vptr)lds_uniform, 16, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_vptr)p;
+}
+
+// s_waitcnt vmcnt(n) for a value the unrolled loops fold to a constant.
+__device__ __forceinline__ void vm_wait(int n) {
+  switch (n) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(1)" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+    case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
+    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+    case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
+    case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+    case 7: asm volatile("s_waitcnt vmcnt(7)" ::: "memory"); break;
+    case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    case 9: asm volatile("s_waitcnt vmcnt(9)" ::: "memory"); break;
+    case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
+    case 11: asm volatile("s_waitcnt vmcnt(11)" ::: "memory"); break;
+    case 12: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
+    case 13: asm volatile("s_waitcnt vmcnt(13)" ::: "memory"); break;
+    case 14: asm volatile("s_waitcnt vmcnt(14)" ::: "memory"); break;
+    case 15: asm volatile("s_waitcnt vmcnt(15)" ::: "memory"); break;
+    case 16: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
+    case 17: asm volatile("s_waitcnt vmcnt(17)" ::: "memory"); break;
+    case 18: asm volatile("s_waitcnt vmcnt(18)" ::: "memory"); break;
+    case 19: asm volatile("s_waitcnt vmcnt(19)" ::: "memory"); break;
+    case 20: asm volatile("s_waitcnt vmcnt(20)" ::: "memory"); break;
+    case 21: asm volatile("s_waitcnt vmcnt(21)" ::: "memory"); break;
+    case 22: asm volatile("s_waitcnt vmcnt(22)" ::: "memory"); break;
+    case 23: asm volatile("s_waitcnt vmcnt(23)" ::: "memory"); break;
+    case 24: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
+    case 25: asm volatile("s_waitcnt vmcnt(25)" ::: "memory"); break;
+    case 26: asm volatile("s_waitcnt vmcnt(26)" ::: "memory"); break;
+    case 27: asm volatile("s_waitcnt vmcnt(27)" ::: "memory"); break;
+    case 28: asm volatile("s_waitcnt vmcnt(28)" ::: "memory"); break;
+    case 29: asm volatile("s_waitcnt vmcnt(29)" ::: "memory"); break;
+    case 30: asm volatile("s_waitcnt vmcnt(30)" ::: "memory"); break;
+    case 31: asm volatile("s_waitcnt vmcnt(31)" ::: "memory"); break;
+    case 32: asm volatile("s_waitcnt vmcnt(32)" ::: "memory"); break;
+    case 33: asm volatile("s_waitcnt vmcnt(33)" ::: "memory"); break;
+    case 34: asm volatile("s_waitcnt vmcnt(34)" ::: "memory"); break;
+    case 35: asm volatile("s_waitcnt vmcnt(35)" ::: "memory"); break;
+    case 36: asm volatile("s_waitcnt vmcnt(36)" ::: "memory"); break;
+    case 37: asm volatile("s_waitcnt vmcnt(37)" ::: "memory"); break;
+    case 38: asm volatile("s_waitcnt vmcnt(38)" ::: "memory"); break;
+    case 39: asm volatile("s_waitcnt vmcnt(39)" ::: "memory"); break;
+    case 40: asm volatile("s_waitcnt vmcnt(40)" ::: "memory"); break;
+    case 41: asm volatile("s_waitcnt vmcnt(41)" ::: "memory"); break;
+    case 42: asm volatile("s_waitcnt vmcnt(42)" ::: "memory"); break;
+    case 43: asm volatile("s_waitcnt vmcnt(43)" ::: "memory"); break;
+    case 44: asm volatile("s_waitcnt vmcnt(44)" ::: "memory"); break;
+    case 45: asm volatile("s_waitcnt vmcnt(45)" ::: "memory"); break;
+    case 46: asm volatile("s_waitcnt vmcnt(46)" ::: "memory"); break;
+    case 47: asm volatile("s_waitcnt vmcnt(47)" ::: "memory"); break;
+    case 48: asm volatile("s_waitcnt vmcnt(48)" ::: "memory"); break;
+    case 49: asm volatile("s_waitcnt vmcnt(49)" ::: "memory"); break;
+    case 50: asm volatile("s_waitcnt vmcnt(50)" ::: "memory"); break;
+    case 51: asm volatile("s_waitcnt vmcnt(51)" ::: "memory"); break;
+    case 52: asm volatile("s_waitcnt vmcnt(52)" ::: "memory"); break;
+    case 53: asm volatile("s_waitcnt vmcnt(53)" ::: "memory"); break;
+    case 54: asm volatile("s_waitcnt vmcnt(54)" ::: "memory"); break;
+    case 55: asm volatile("s_waitcnt vmcnt(55)" ::: "memory"); break;
+    case 56: asm volatile("s_waitcnt vmcnt(56)" ::: "memory"); break;
+    case 57: asm volatile("s_waitcnt vmcnt(57)" ::: "memory"); break;
+    case 58: asm volatile("s_waitcnt vmcnt(58)" ::: "memory"); break;
+    case 59: asm volatile("s_waitcnt vmcnt(59)" ::: "memory"); break;
+    case 60: asm volatile("s_waitcnt vmcnt(60)" ::: "memory"); break;
+    case 61: asm volatile("s_waitcnt vmcnt(61)" ::: "memory"); break;
+    case 62: asm volatile("s_waitcnt vmcnt(62)" ::: "memory"); break;
+    case 63: asm volatile("s_waitcnt vmcnt(63)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+  }
+}
+
+// One step's LDS reads for MFMA lane (c, j): the 16 B A fragment at xaddr and
+// the 4 weight row dwords of a block at waddr (dwords 0, 64, 128, 192).
+__device__ __forceinline__ void read_step(uint32_t xaddr, uint32_t waddr, u32x4& A, uint32_t& r0,
+                                          uint32_t& r1, uint32_t& r2, uint32_t& r3) {
+  u32x2 p, q;
+  asm volatile(
+      "ds_read_b128 %0, %3\n\t"
+      "ds_read2st64_b32 %1, %4 offset1:1\n\t"
+      "ds_read2st64_b32 %2, %4 offset0:2 offset1:3\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(A), "=&v"(p), "=&v"(q)
+      : "v"(xaddr), "v"(waddr)
+      : "memory");
+  r0 = p.x;
+  r1 = p.y;
+  r2 = q.x;
+  r3 = q.y;
+}
+
+__device__ __forceinline__ void read_rows(uint32_t waddr, uint32_t& r0, uint32_t& r1, uint32_t& r2,
+                                          uint32_t& r3) {
+  u32x2 p, q;
+  asm volatile(
+      "ds_read2st64_b32 %0, %2 offset1:1\n\t"
+      "ds_read2st64_b32 %1, %2 offset0:2 offset1:3\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(p), "=&v"(q)
+      : "v"(waddr)
+      : "memory");
+  r0 = p.x;
+  r1 = p.y;
+  r2 = q.x;
+  r3 = q.y;
+}
+
+__device__ __forceinline__ void read_scale_zero(uint32_t saddr, uint32_t zaddr, u32x2& sv, uint32_t& zv) {
+  asm volatile(
+      "ds_read_b64 %0, %2\n\t"
+      "ds_read_b32 %1, %3\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(sv), "=&v"(zv)
+      : "v"(saddr), "v"(zaddr)
+      : "memory");
+}
+
+template <int S, int R>  // 32-k steps per wave; ring of R steps
+__global__ __launch_bounds__(8 * kWave) void int4g64_stream_kernel(QArgs a) {
+  constexpr int G = S / 2;
+  static_assert(G <= 8 && R <= S, "scale / zero block holds 8 groups");
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const uint32_t L = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int tile = (int)(L / (uint32_t)a.ks);
+  const int ksi = (int)(L - (uint32_t)tile * a.ks);
+  const int rb = blockIdx.y;
+  const int m0 = rb * kQRows;
+  const int mrows = min(kQRows, a.M - m0);
+  const int n0 = tile * kQCols;
+  const int c = lane & 15, j = lane >> 4;
+  const int kbeg = ksi * (a.K / a.ks) + wv * 32 * S;
+  const size_t N = (size_t)a.N;
+  // Wave LDS: [R] weight blocks | [R] x blocks | scales (1 KB) | zeros (1 KB).
+  unsigned char* wl = smem + wv * a.wave_lds;
+  unsigned char* wring = wl;
+  unsigned char* xring = wl + R * 1024;
+  unsigned char* sblk = wl + 2 * R * 1024;
+  unsigned char* zblk = sblk + 1024;
+
+  // Scales: group g row = 64 columns x 2 B = lanes 8g..8g+7; zero-points:
+  // 64 B = lanes 4g..4g+3 (lanes 32..63 repeat 0..31).  Groups past G and
+  // columns past N repeat valid ones (never consumed / never stored).
+  {
+    const int gs = min(lane >> 3, G - 1), gz = min((lane >> 2) & 7, G - 1);
+    const uint16_t* sp = reinterpret_cast<const uint16_t*>(a.s) + (size_t)((kbeg >> 6) + gs) * N +
+                         min(n0 + 8 * (lane & 7), a.N - 8);
+    const uint8_t* zp = a.z + (size_t)((kbeg >> 6) + gz) * N + min(n0 + 16 * (lane & 3), a.N - 16);
+    dma16(sp, sblk);
+    dma16(zp, zblk);
+  }
+  // Step t: x fragment of MFMA lane (c, j) = lane; weight rows kp =
+  // kbeg/2 + 16 t + 4 jj + r for DMA lane 16 r + 4 jj + kk.
+  const uint16_t* xsrc = a.x + (size_t)min(m0 + c, a.M - 1) * a.K + kbeg + 8 * j;
+  const int r = lane >> 4, jj = (lane >> 2) & 3, kk = lane & 3;
+  const uint8_t* wsrc = a.w + (size_t)(kbeg / 2 + 4 * jj + r) * N + min(n0 + 16 * kk, a.N - 16);
+  auto issue = [&](int t) {
+    dma16(xsrc + 32 * t, xring + (t % R) * 1024);
+    dma16(wsrc + (size_t)(16 * t) * N, wring + (t % R) * 1024);
+  };
+#pragma unroll
+  for (int t = 0; t < R; ++t) issue(t);
+
+  const uint32_t xaddr0 = lds_addr(xring) + 16 * lane;
+  const uint32_t waddr0 = lds_addr(wring) + 4 * (16 * j + c);
+  const uint32_t saddr0 = lds_addr(sblk) + 8 * c;
+  const uint32_t zaddr0 = lds_addr(zblk) + 4 * c;
+  const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0
+  const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+  f32x4 y[4] = {zero4, zero4, zero4, zero4};
+  f32x4 acc[4], xsum;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int issued = (s + R < S) ? s + R : S;
+    vm_wait(2 * (issued - 1 - s));
+    u32x4 v;
+    uint32_t r0, r1, r2, r3, t[4];
+    read_step(xaddr0 + (s % R) * 1024, waddr0 + (s % R) * 1024, v, r0, r1, r2, r3);
+    if (s + R < S) issue(s + R);  // this slot's reads have completed
+    transpose4x4(r0, r1, r2, r3, t[0], t[1], t[2], t[3]);
+    // x slot order k0 k2 k4 k6 k1 k3 k5 k7 (matches unpack_int4).
+    const u32x4 A = {perm(v.y, v.x, 0x05040100u), perm(v.w, v.z, 0x05040100u),
+                     perm(v.y, v.x, 0x07060302u), perm(v.w, v.z, 0x07060302u)};
+    const bool first = (s & 1) == 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) acc[w] = mfma16x16x32(A, unpack_int4(t[w]), first ? zero4 : acc[w]);
+    xsum = mfma16x16x32(A, ones, first ? zero4 : xsum);
+    if (!first) {
+      const int g = s >> 1;
+      u32x2 sv;
+      uint32_t zv;
+      read_scale_zero(saddr0 + 128 * g, zaddr0 + 64 * g, sv, zv);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t sw = (w < 2) ? sv.x : sv.y;
+        const float sf = bf16_to_f32((w & 1) ? (sw >> 16) : (sw & 0xFFFFu));
+        const float cz = 128.f + (float)((zv >> (8 * w)) & 0xFFu);
+        y[w] = sf * (acc[w] - cz * xsum) + y[w];
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  spill_y(wl, y, c, j);
+  reduce_and_store<8, false>(a, smem, ksi, rb, m0, mrows, n0);
+}
+
+template <int S, int R>  // 32-k steps per wave, ring of R steps (3 KB each)
+__global__ __launch_bounds__(8 * kWave) void int8pc_stream_kernel(QArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const uint32_t L = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int tile = (int)(L / (uint32_t)a.ks);
+  const int ksi = (int)(L - (uint32_t)tile * a.ks);
+  const int rb = blockIdx.y;
+  const int m0 = rb * kQRows;
+  const int mrows = min(kQRows, a.M - m0);
+  const int n0 = tile * kQCols;
+  const int c = lane & 15, j = lane >> 4;
+  const int kbeg = ksi * (a.K / a.ks) + wv * 32 * S;
+  const size_t N = (size_t)a.N;
+  // Wave LDS: [R] x (weight block h = 0, weight block h = 1, x block).
+  unsigned char* wl = smem + wv * a.wave_lds;
+
+  // Step t: weight rows kbeg + 32 t + 8 jj + 4 h + r in block h (DMA lane
+  // 16 r + 4 jj + kk), x fragment of MFMA lane (c, j) = lane.
+  const uint16_t* xsrc = a.x + (size_t)min(m0 + c, a.M - 1) * a.K + kbeg + 8 * j;
+  const int r = lane >> 4, jj = (lane >> 2) & 3, kk = lane & 3;
+  const uint8_t* wsrc = a.w + (size_t)(kbeg + 8 * jj + r) * N + min(n0 + 16 * kk, a.N - 16);
+  auto issue = [&](int t) {
+    unsigned char* dst = wl + (t % R) * 3072;
+    dma16(wsrc + (size_t)(32 * t) * N, dst);
+    dma16(wsrc + (size_t)(32 * t + 4) * N, dst + 1024);
+    dma16(xsrc + 32 * t, dst + 2048);
+  };
+#pragma unroll
+  for (int t = 0; t < R; ++t) issue(t);
+
+  const uint32_t base = lds_addr(wl);
+  const uint32_t waddr0 = base + 4 * (16 * j + c);
+  const uint32_t xaddr0 = base + 2048 + 16 * lane;
+  const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0
+  const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+  f32x4 y[4] = {zero4, zero4, zero4, zero4};
+  f32x4 xsum = zero4;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int issued = (s + R < S) ? s + R : S;
+    vm_wait(3 * (issued - 1 - s));
+    u32x4 A;
+    uint32_t q[8], lo[4], hi[4];
+    read_step(xaddr0 + (s % R) * 3072, waddr0 + (s % R) * 3072, A, q[0], q[1], q[2], q[3]);
+    read_rows(waddr0 + (s % R) * 3072 + 1024, q[4], q[5], q[6], q[7]);
+    if (s + R < S) issue(s + R);  // this slot's reads have completed
+    transpose4x4(q[0], q[1], q[2], q[3], lo[0], lo[1], lo[2], lo[3]);
+    transpose4x4(q[4], q[5], q[6], q[7], hi[0], hi[1], hi[2], hi[3]);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) y[w] = mfma16x16x32(A, unpack_int8(lo[w], hi[w]), y[w]);
+    xsum = mfma16x16x32(A, ones, xsum);
+  }
+#pragma unroll
+  for (int w = 0; w < 4; ++w) y[w] = y[w] - 128.f * xsum;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  spill_y(wl, y, c, j);
+  reduce_and_store<8, true>(a, smem, ksi, rb, m0, mrows, n0);
 }
 
 // Second pass when K was split across workgroups: y = sum_ks part (in ks
@@ -390,6 +669,8 @@ constexpr size_t kMaxLds = 160 * 1024;
 
 struct QPlan {
   int ks, nw, kwave, ntiles, rowblocks, wave_lds;
+  int stream_steps;  // > 0: streaming kernel with this many 32-k steps per wave
+  int ring;          // int8 streaming kernel: ring slots
   size_t lds_bytes;
   int64_t part_bytes;
 };
@@ -408,8 +689,7 @@ bool fill_plan(int fmt, int64_t K, int ks, int nw, QPlan* p) {
   const int xbytes = p->kwave * 32;          // 16 rows x kwave bf16
   const int ybytes = mk::kQRows * mk::kQCols * 4;
   p->wave_lds = xbytes > ybytes ? xbytes : ybytes;
-  const int xs_floats = (fmt == MK_QFMT_INT4_G64 ? (p->kwave / 64) : 1) * mk::kQRows;
-  p->lds_bytes = (size_t)nw * p->wave_lds + (size_t)nw * xs_floats * 4;
+  p->lds_bytes = (size_t)nw * p->wave_lds;
   return p->lds_bytes <= kMaxLds;
 }
 
@@ -417,9 +697,43 @@ bool fill_plan(int fmt, int64_t K, int ks, int nw, QPlan* p) {
 // workgroup whenever x fits in LDS and the grid already covers ~192+ CUs;
 // otherwise the smallest split that does.  Every wave gets a whole number of
 // 64-k groups.  MK_QMM_KS / MK_QMM_NW force a choice (tuning sweeps).
+// Streaming kernels: 8 waves, K = ks * 8 * 32 * S with S in {16, 8, 4}
+// (int4 needs S even), N % 16 == 0.  Prefer the fewest splits that still
+// give >= 192 workgroups.
+bool plan_stream(int fmt, int64_t K, int64_t N, QPlan* p) {
+  if (N % 16 != 0 || N < 16 || getenv("MK_QMM_GENERIC")) return false;
+  const int ks_env = env_int("MK_QMM_KS", 0);
+  const int steps[3] = {16, 8, 4};
+  for (int ks = 1; ks <= 64; ks *= 2) {
+    if (ks_env > 0 && ks != ks_env) continue;
+    for (int i = 0; i < 3; ++i) {
+      const int S = steps[i];
+      if (K != (int64_t)ks * 8 * 32 * S) continue;
+      if ((int64_t)p->ntiles * p->rowblocks * ks < 192 && ks_env <= 0 && 2 * ks <= 64 &&
+          K % ((int64_t)2 * ks * 8 * 32 * 4) == 0)
+        break;  // a larger split would still divide K: try it for more workgroups
+      p->ks = ks;
+      p->nw = 8;
+      p->kwave = 32 * S;
+      p->stream_steps = S;
+      p->ring = fmt == MK_QFMT_INT4_G64 ? (S < 8 ? S : 8) : (S < 4 ? S : 4);
+      p->wave_lds = fmt == MK_QFMT_INT4_G64 ? (2 * p->ring + 2) * 1024 : p->ring * 3072;
+      p->lds_bytes = (size_t)8 * p->wave_lds;
+      return true;
+    }
+  }
+  return false;
+}
+
 bool plan_q(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p) {
   p->ntiles = (int)((N + mk::kQCols - 1) / mk::kQCols);
   p->rowblocks = (int)((M + mk::kQRows - 1) / mk::kQRows);
+  p->stream_steps = 0;
+  p->ring = 0;
+  if (plan_stream(fmt, K, N, p)) {
+    p->part_bytes = p->ks > 1 ? (int64_t)p->rowblocks * p->ks * mk::kQRows * N * 4 : 0;
+    return true;
+  }
   const int ks_env = env_int("MK_QMM_KS", 0), nw_env = env_int("MK_QMM_NW", 0);
   const int nws[4] = {8, 4, 2, 1};
   QPlan best;
@@ -456,6 +770,24 @@ hipError_t lds_opt_in(const void* fn, size_t bytes) {
   return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
 }
 
+hipError_t launch_reduce(int fmt, const mk::QArgs& a, hipStream_t st);
+
+template <int S>
+hipError_t launch_stream(int fmt, const mk::QArgs& a, const QPlan& p, hipStream_t st) {
+  dim3 grid(p.ntiles * p.ks, p.rowblocks), block(8 * mk::kWave);
+  const void* fn = fmt == MK_QFMT_INT4_G64 ? (const void*)mk::int4g64_stream_kernel<S, (S < 8 ? S : 8)>
+                                           : (const void*)mk::int8pc_stream_kernel<S, (S < 4 ? S : 4)>;
+  hipError_t e = lds_opt_in(fn, p.lds_bytes);
+  if (e != hipSuccess) return e;
+  if (fmt == MK_QFMT_INT4_G64)
+    hipLaunchKernelGGL((mk::int4g64_stream_kernel<S, (S < 8 ? S : 8)>), grid, block, p.lds_bytes, st, a);
+  else
+    hipLaunchKernelGGL((mk::int8pc_stream_kernel<S, (S < 4 ? S : 4)>), grid, block, p.lds_bytes, st, a);
+  e = hipGetLastError();
+  if (e != hipSuccess || p.ks == 1) return e;
+  return launch_reduce(fmt, a, st);
+}
+
 template <int NW>
 hipError_t launch_q(int fmt, const mk::QArgs& a, const QPlan& p, hipStream_t st) {
   dim3 grid(p.ntiles * p.ks, p.rowblocks), block(NW * mk::kWave);
@@ -470,6 +802,10 @@ hipError_t launch_q(int fmt, const mk::QArgs& a, const QPlan& p, hipStream_t st)
   }
   e = hipGetLastError();
   if (e != hipSuccess || p.ks == 1) return e;
+  return launch_reduce(fmt, a, st);
+}
+
+hipError_t launch_reduce(int fmt, const mk::QArgs& a, hipStream_t st) {
   const int64_t chunks = (int64_t)a.M * (a.N / 4);
   const int blocks = (int)std::min<int64_t>((chunks + 255) / 256, 4096);
   if (fmt == MK_QFMT_INT4_G64)
@@ -513,7 +849,13 @@ int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, v
   a.wave_lds = p.wave_lds;
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e;
-  switch (p.nw) {
+  if (p.stream_steps > 0) {
+    switch (p.stream_steps) {
+      case 16: e = launch_stream<16>(fmt, a, p, st); break;
+      case 8: e = launch_stream<8>(fmt, a, p, st); break;
+      default: e = launch_stream<4>(fmt, a, p, st); break;
+    }
+  } else switch (p.nw) {
     case 1: e = launch_q<1>(fmt, a, p, st); break;
     case 2: e = launch_q<2>(fmt, a, p, st); break;
     case 4: e = launch_q<4>(fmt, a, p, st); break;
