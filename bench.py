@@ -137,6 +137,96 @@ def bench_int8(torch, ops, steps, warmup, M=16, K=4096, N=14336):
     return {"bytes": per_set, "sec_per_call": t, "gbs": per_set / t / 1e9, "nsets": nsets}
 
 
+def _rot_sets(total_bytes_per_set, floor_sets=2):
+    """How many distinct input sets to rotate so their total exceeds the
+    256 MB Infinity Cache."""
+    return max(floor_sets, -(-300 * 2 ** 20 // total_bytes_per_set))
+
+
+def bench_gemm_bf16(torch, ops, steps, warmup, batch=1, M=4096, N=4096, K=4096, out_f32=False):
+    per = 2 * batch * (M * K + K * N)
+    nsets = _rot_sets(per)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    sc = 1.0 / np.sqrt(np.sqrt(K))
+    sets = []
+    for _ in range(nsets):
+        a = (torch.randn((batch, M, K), device="cuda", generator=g) * sc).to(torch.bfloat16)
+        b = (torch.randn((batch, K, N), device="cuda", generator=g) * sc).to(torch.bfloat16)
+        c = torch.empty((batch, M, N), dtype=torch.float32 if out_f32 else torch.bfloat16, device="cuda")
+        sets.append((a, b, c))
+
+    def fn(i):
+        a, b, c = sets[i]
+        ops.gemm_bf16(a, b, out_f32=out_f32, out=c)
+
+    secs, n = time_graph_launches(torch, fn, nsets, steps, warmup)
+    t = secs / n
+    flops = 2.0 * batch * M * N * K
+    out_bytes = batch * M * N * (4 if out_f32 else 2)
+    return {"sec_per_call": t, "tflops": flops / t / 1e12, "bytes": per + out_bytes, "nsets": nsets}
+
+
+def bench_gemm_f32(torch, ops, steps, warmup, M=2048, N=2048, K=2048):
+    per = 4 * (M * K + K * N)
+    nsets = _rot_sets(per)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    sets = [((torch.randn((M, K), device="cuda", generator=g)), torch.randn((K, N), device="cuda", generator=g),
+             torch.empty((M, N), device="cuda")) for _ in range(nsets)]
+
+    def fn(i):
+        a, b, c = sets[i]
+        ops.gemm_f32(a, b, out=c)
+
+    secs, n = time_graph_launches(torch, fn, nsets, steps, warmup)
+    t = secs / n
+    return {"sec_per_call": t, "tflops": 2.0 * M * N * K / t / 1e12}
+
+
+def bench_rowop(torch, ops, kind, dtype, steps, warmup, rows=8192, cols=8192):
+    """softmax / rmsnorm / argmax / chain6 on X [rows, cols] ~ N(0, 2)."""
+    tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+    esz = 4 if dtype == "f32" else 2
+    per = rows * cols * esz
+    nsets = _rot_sets(per)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    xs = [(torch.randn((rows, cols), device="cuda", generator=g) * np.sqrt(2.0)).to(tdt) for _ in range(nsets)]
+    gam = (torch.rand((cols,), device="cuda", generator=g) + 0.5).to(tdt)
+    if kind == "argmax":
+        out = torch.empty((rows,), dtype=torch.int32, device="cuda")
+        moved = per + rows * 4
+    else:
+        out = torch.empty((rows, cols), dtype=tdt, device="cuda")
+        moved = 2 * per + (cols * esz if kind == "rmsnorm" else 0)
+    prog = [("LOAD", 0, 0, 0, 0, 0.0), ("CONST", 1, 0, 0, 0, 1.5), ("MUL", 2, 0, 1, 0, 0.0),
+            ("CONST", 1, 0, 0, 0, 0.5), ("ADD", 3, 2, 1, 0, 0.0), ("EXP", 4, 3, 0, 0, 0.0),
+            ("LOG1P", 5, 4, 0, 0, 0.0), ("MAX", 6, 5, 0, 0, 0.0), ("CONST", 1, 0, 0, 0, 0.0),
+            ("CMP_GT", 7, 0, 1, 0, 0.0), ("SELECT", 8, 7, 6, 3, 0.0)]
+
+    def fn(i):
+        x = xs[i]
+        if kind == "softmax":
+            ops.softmax(x, out=out)
+        elif kind == "rmsnorm":
+            ops.rmsnorm(x, gam, out=out)
+        elif kind == "argmax":
+            ops.argmax(x, out=out)
+        else:
+            ops.elementwise(prog, [x], out_slot=8, out=out)
+
+    secs, n = time_graph_launches(torch, fn, nsets, steps, warmup)
+    t = secs / n
+    return {"sec_per_call": t, "gbs": moved / t / 1e9, "bytes": moved}
+
+
+def _hbm_entry(gbs, us, extra=None):
+    e = {"value": round(gbs, 2), "unit": "GB/s", "us_per_call": round(us, 3),
+         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
+    if extra:
+        e.update(extra)
+    return e
+
+
 def cpu_baseline_int4(target_s, M=16, K=4096, N=14336):
     """Time the oracle's C port (OpenMP) on a column slice of the headline
     case, sized to roughly target_s seconds; report GB/s of the same
@@ -181,7 +271,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of workloads (int4,int8)")
+    ap.add_argument("--only", default="",
+                    help="comma list of secondary workloads (int8,gemm,softmax,rmsnorm,argmax,chain6)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one MI355X only (asked for --gpus {args.gpus}); "
@@ -207,6 +298,36 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(r8["gbs"], 2), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(r8["gbs"] / HBM_PEAK_GBS, 4), "traffic": None},
         }
+
+    def want(name):
+        return not only or name in only
+
+    if want("gemm"):
+        log("[bench] bf16 GEMM 4096^3 ...")
+        rg = bench_gemm_bf16(torch, ops, max(50, args.steps // 20), 5)
+        log(f"[bench] bf16 gemm: {rg['sec_per_call'] * 1e6:.1f} us, {rg['tflops']:.1f} TFLOP/s")
+        secondary["bf16_gemm_4096"] = {
+            "value": round(rg["tflops"], 2), "unit": "TFLOP/s", "us_per_call": round(rg["sec_per_call"] * 1e6, 3),
+            "roofline": {"bound": "mfma", "achieved": round(rg["tflops"], 2), "peak": BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(rg["tflops"] / BF16_PEAK_TFLOPS, 4), "traffic": None}}
+        rb = bench_gemm_bf16(torch, ops, max(50, args.steps // 20), 5, batch=16, M=2048, N=2048, K=128)
+        gbs = rb["bytes"] / rb["sec_per_call"] / 1e9
+        log(f"[bench] batched bf16 gemm: {rb['sec_per_call'] * 1e6:.1f} us, {rb['tflops']:.1f} TFLOP/s, {gbs:.0f} GB/s")
+        secondary["bf16_bmm_16x2048x128x2048"] = _hbm_entry(gbs, rb["sec_per_call"] * 1e6,
+                                                           {"tflops": round(rb["tflops"], 2)})
+        rf = bench_gemm_f32(torch, ops, max(50, args.steps // 20), 5)
+        log(f"[bench] f32 gemm 2048^3: {rf['sec_per_call'] * 1e6:.1f} us, {rf['tflops']:.1f} TFLOP/s")
+        secondary["f32_gemm_2048"] = {
+            "value": round(rf["tflops"], 2), "unit": "TFLOP/s", "us_per_call": round(rf["sec_per_call"] * 1e6, 3),
+            "roofline": {"bound": "mfma", "achieved": round(rf["tflops"], 2), "peak": 157.3,
+                         "unit": "TFLOP/s", "frac": round(rf["tflops"] / 157.3, 4), "traffic": None}}
+    for kind in ("softmax", "rmsnorm", "argmax", "chain6"):
+        if not want(kind):
+            continue
+        for dt in ("f32", "bf16"):
+            r = bench_rowop(torch, ops, kind, dt, max(50, args.steps // 10), 5)
+            log(f"[bench] {kind} {dt} 8192x8192: {r['sec_per_call'] * 1e6:.1f} us, {r['gbs']:.0f} GB/s")
+            secondary[f"{kind}_{dt}_8192x8192"] = _hbm_entry(r["gbs"], r["sec_per_call"] * 1e6)
 
     cpu = None
     if not args.no_cpu:

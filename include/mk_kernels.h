@@ -96,6 +96,77 @@ int mk_gemm_bf16(const void* a, const void* b, void* c, int64_t batch, int64_t M
 int mk_gemm_f32(const void* a, const void* b, void* c, int64_t batch, int64_t M, int64_t N,
                 int64_t K, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Last-axis row operations on X [rows, cols] (row-major).
+ *
+ * Replace the reference's native row kernels and the MPSGraph reductions
+ * around them: softmax (pattern FuseSoftmaxPatterns,
+ * src/pjrt_plugin/core/mps_executable.mm:2091-2372; kernels
+ * runtime/metal_kernels.mm:1579-1740 and the XLA rounding emulation
+ * :1742-1819), last-axis sum/max (NativeIntrinsicReduceHandler,
+ * mps_executable.mm:4911-5070; kernels metal_kernels.mm:769-1065), argmax
+ * (HandleMultiResultReduce, ops/reduction_ops.mm:1407-1668) and RMSNorm
+ * (the workload's x * rsqrt(mean(x^2) + eps) * g; the reference's closest
+ * path is its LayerNorm fusion, mps_executable.mm:1457-1820).
+ *
+ * dtype: MK_DT_F32 or MK_DT_BF16 (x, g and y share it; argmax writes int32).
+ * softmax: a row whose max is NaN or +-inf becomes all NaN.  argmax: index
+ * of the first NaN, else of the first maximum, -0 == +0.  max: NaN
+ * propagates, -0 < +0.  sum: f32 accumulation, result in dtype.
+ * ---------------------------------------------------------------------- */
+enum { MK_DT_F32 = 0, MK_DT_BF16 = 1 };
+enum { MK_REDUCE_SUM = 0, MK_REDUCE_MAX = 1 };
+
+int mk_softmax_lastdim(int dtype, const void* x, void* y, int64_t rows, int64_t cols, void* stream);
+
+int mk_rmsnorm_lastdim(int dtype, const void* x, const void* g, void* y, int64_t rows, int64_t cols,
+                       float eps, void* stream);
+
+int mk_argmax_lastdim(int dtype, const void* x, void* out_i32, int64_t rows, int64_t cols,
+                      void* stream);
+
+int mk_reduce_lastdim(int dtype, int op, const void* x, void* y, int64_t rows, int64_t cols,
+                      void* stream);
+
+/* ------------------------------------------------------------------------
+ * Fused elementwise program (one pass over memory).
+ *
+ * Replaces the reference's elementwise MPSGraph segments
+ * (core/mps_executable.mm:7393-7508) and its opt-in generated fusion kernels
+ * (FusionSnippet :4303-4351, GenerateFusedKernelSource :4445-4586).  The
+ * executor lowers a chain of StableHLO elementwise ops to instructions over
+ * 12 register slots; MK_EW_LOAD reads input `a` (n elements, or 1 element
+ * broadcast), MK_EW_CONST writes `imm`, every other op reads slots a (b, c)
+ * and writes slot dst.  bf16 programs round each float result to bf16
+ * (XLA:CPU's per-op rounding, reference ops/registry.h:273-287).
+ * Comparisons give 1.0 / 0.0; SELECT yields b where a != 0, else c.
+ * At most 32 instructions and 4 inputs; every source slot must be written
+ * before it is read (checked on the host).
+ * ---------------------------------------------------------------------- */
+enum {
+  MK_EW_LOAD = 0, MK_EW_CONST = 1,
+  MK_EW_ADD = 2, MK_EW_SUB = 3, MK_EW_MUL = 4, MK_EW_DIV = 5, MK_EW_MAX = 6, MK_EW_MIN = 7,
+  MK_EW_POW = 8,
+  MK_EW_NEG = 9, MK_EW_ABS = 10, MK_EW_EXP = 11, MK_EW_LOG = 12, MK_EW_LOG1P = 13,
+  MK_EW_EXPM1 = 14, MK_EW_TANH = 15, MK_EW_RSQRT = 16, MK_EW_SQRT = 17, MK_EW_LOGISTIC = 18,
+  MK_EW_FLOOR = 19, MK_EW_CEIL = 20,
+  MK_EW_CMP_EQ = 21, MK_EW_CMP_NE = 22, MK_EW_CMP_LT = 23, MK_EW_CMP_LE = 24,
+  MK_EW_CMP_GT = 25, MK_EW_CMP_GE = 26,
+  MK_EW_SELECT = 27, MK_EW_ROUND_BF16 = 28,
+  MK_EW_NUM_OPS = 29
+};
+
+typedef struct mk_ew_instr {
+  int32_t op;
+  int32_t dst;
+  int32_t a, b, c;
+  float imm;
+} mk_ew_instr;
+
+int mk_elementwise(int dtype, const mk_ew_instr* prog, int n_instr, const void* const* inputs,
+                   const int64_t* input_numel, int n_inputs, int out_slot, void* out, int64_t n,
+                   void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

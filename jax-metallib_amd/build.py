@@ -36,6 +36,8 @@ KERNEL_SOURCES = [
     "capi.cpp",
     "kernels/qmatmul.hip",
     "kernels/gemm.hip",
+    "kernels/rowops.hip",
+    "kernels/eltwise.hip",
 ]
 
 

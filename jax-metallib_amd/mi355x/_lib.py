@@ -14,6 +14,18 @@ KERNELS_SO = os.path.join(LIB_DIR, "libmk_kernels.so")
 
 MK_OK, MK_EINVAL, MK_EUNSUPPORTED, MK_EWORKSPACE, MK_ELAUNCH = 0, 1, 2, 3, 4
 MK_QFMT_INT4_G64, MK_QFMT_INT8_PC = 0, 1
+MK_DT_F32, MK_DT_BF16 = 0, 1
+MK_REDUCE_SUM, MK_REDUCE_MAX = 0, 1
+EW_OPS = ["LOAD", "CONST", "ADD", "SUB", "MUL", "DIV", "MAX", "MIN", "POW", "NEG", "ABS", "EXP", "LOG",
+          "LOG1P", "EXPM1", "TANH", "RSQRT", "SQRT", "LOGISTIC", "FLOOR", "CEIL", "CMP_EQ", "CMP_NE",
+          "CMP_LT", "CMP_LE", "CMP_GT", "CMP_GE", "SELECT", "ROUND_BF16"]
+EW = {name: i for i, name in enumerate(EW_OPS)}
+
+
+class EwInstr(ctypes.Structure):
+    """mk_ew_instr (include/mk_kernels.h)."""
+    _fields_ = [("op", ctypes.c_int32), ("dst", ctypes.c_int32), ("a", ctypes.c_int32),
+                ("b", ctypes.c_int32), ("c", ctypes.c_int32), ("imm", ctypes.c_float)]
 
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -28,6 +40,11 @@ SIGNATURES = {
     "mk_int8pc_matmul_bf16": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p]),
     "mk_gemm_bf16": (_i32, [_p, _p, _p, _i64, _i64, _i64, _i64, _i32, _p]),
     "mk_gemm_f32": (_i32, [_p, _p, _p, _i64, _i64, _i64, _i64, _p]),
+    "mk_softmax_lastdim": (_i32, [_i32, _p, _p, _i64, _i64, _p]),
+    "mk_rmsnorm_lastdim": (_i32, [_i32, _p, _p, _p, _i64, _i64, ctypes.c_float, _p]),
+    "mk_argmax_lastdim": (_i32, [_i32, _p, _p, _i64, _i64, _p]),
+    "mk_reduce_lastdim": (_i32, [_i32, _i32, _p, _p, _i64, _i64, _p]),
+    "mk_elementwise": (_i32, [_i32, _p, _i32, _p, _p, _i32, _i32, _p, _i64, _p]),
 }
 
 _LIB = None

@@ -112,3 +112,79 @@ def gemm_f32(a, b, out=None):
     c = out if out is not None else torch.empty(shape, dtype=torch.float32, device=a.device)
     check(lib().mk_gemm_f32(_ptr(a), _ptr(b), _ptr(c), batch, M, N, K, _stream(a.device)))
     return c
+
+
+def _dt(t):
+    if t.dtype == torch.float32:
+        return _lib.MK_DT_F32
+    if t.dtype in _BF16:
+        return _lib.MK_DT_BF16
+    raise ValueError(f"unsupported dtype {t.dtype}")
+
+
+def _rows_cols(x):
+    cols = x.shape[-1]
+    return x.numel() // cols, cols
+
+
+def softmax(x, out=None):
+    """Softmax over the last axis (f32 or bf16)."""
+    _require(x, (torch.float32,) + _BF16, "x")
+    rows, cols = _rows_cols(x)
+    y = out if out is not None else torch.empty_like(x)
+    check(lib().mk_softmax_lastdim(_dt(x), _ptr(x), _ptr(y), rows, cols, _stream(x.device)))
+    return y
+
+
+def rmsnorm(x, g, eps=1e-6, out=None):
+    """x * rsqrt(mean(x^2, -1) + eps) * g."""
+    _require(x, (torch.float32,) + _BF16, "x")
+    _require(g, (x.dtype,), "g")
+    rows, cols = _rows_cols(x)
+    if g.numel() != cols:
+        raise ValueError("rmsnorm: g must have cols elements")
+    y = out if out is not None else torch.empty_like(x)
+    check(lib().mk_rmsnorm_lastdim(_dt(x), _ptr(x), _ptr(g), _ptr(y), rows, cols, eps, _stream(x.device)))
+    return y
+
+
+def argmax(x, out=None):
+    """Index (int32) of the first NaN, else of the first maximum, per row."""
+    _require(x, (torch.float32,) + _BF16, "x")
+    rows, cols = _rows_cols(x)
+    y = out if out is not None else torch.empty(x.shape[:-1], dtype=torch.int32, device=x.device)
+    check(lib().mk_argmax_lastdim(_dt(x), _ptr(x), _ptr(y), rows, cols, _stream(x.device)))
+    return y
+
+
+def reduce_lastdim(x, op="sum", out=None):
+    """Row sum (f32 accumulation) or NaN-propagating row max, in x's dtype."""
+    _require(x, (torch.float32,) + _BF16, "x")
+    rows, cols = _rows_cols(x)
+    y = out if out is not None else torch.empty(x.shape[:-1], dtype=x.dtype, device=x.device)
+    code = {"sum": _lib.MK_REDUCE_SUM, "max": _lib.MK_REDUCE_MAX}[op]
+    check(lib().mk_reduce_lastdim(_dt(x), code, _ptr(x), _ptr(y), rows, cols, _stream(x.device)))
+    return y
+
+
+def elementwise(program, inputs, out_slot, out=None, dtype=None):
+    """Evaluate an elementwise register program (list of (op, dst, a, b, c,
+    imm) tuples, op a name from mi355x._lib.EW_OPS) over same-shaped inputs
+    (or 1-element scalars)."""
+    import ctypes as _ct
+
+    big = [t for t in inputs if t.numel() != 1]
+    ref = big[0] if big else inputs[0]
+    for t in inputs:
+        _require(t, (torch.float32,) + _BF16, "input")
+    n = ref.numel()
+    dt = _dt(ref)
+    arr = (_lib.EwInstr * len(program))()
+    for i, (op, dst, a, b, c, imm) in enumerate(program):
+        arr[i] = _lib.EwInstr(_lib.EW[op], dst, a, b, c, imm)
+    ptrs = (_ct.c_void_p * max(1, len(inputs)))(*[t.data_ptr() for t in inputs])
+    numel = (_ct.c_int64 * max(1, len(inputs)))(*[t.numel() for t in inputs])
+    y = out if out is not None else torch.empty(ref.shape, dtype=ref.dtype, device=ref.device)
+    check(lib().mk_elementwise(dt, arr, len(program), ptrs, numel, len(inputs), out_slot, _ptr(y), n,
+                               _stream(ref.device)))
+    return y

@@ -66,3 +66,27 @@ def test_missing_workspace_rejected():
     assert L.mk_qmatmul_workspace_bytes(_lib.MK_QFMT_INT4_G64, 16, 4096, 1024) > 0
     rc = L.mk_int4g64_matmul_bf16(fake, fake, fake, fake, fake, 16, 4096, 1024, None, 0, None)
     assert rc == _lib.MK_EWORKSPACE
+
+
+def test_elementwise_program_validated_on_host():
+    L = _lib.lib()
+    fake = ctypes.c_void_p(0x1000)
+    ins = (_lib.EwInstr * 1)(_lib.EwInstr(_lib.EW["ADD"], 0, 1, 2, 0, 0.0))
+    ptrs = (ctypes.c_void_p * 1)(fake.value)
+    numel = (ctypes.c_int64 * 1)(16)
+    rc = L.mk_elementwise(_lib.MK_DT_F32, ins, 1, ptrs, numel, 1, 0, fake, 16, None)
+    assert rc == _lib.MK_EINVAL and b"undefined slot" in L.mk_last_error()
+    ins = (_lib.EwInstr * 1)(_lib.EwInstr(_lib.EW["LOAD"], 0, 0, 0, 0, 0.0))
+    numel = (ctypes.c_int64 * 1)(7)  # neither 1 nor n
+    rc = L.mk_elementwise(_lib.MK_DT_F32, ins, 1, ptrs, numel, 1, 0, fake, 16, None)
+    assert rc == _lib.MK_EINVAL
+
+
+def test_rowops_reject_bad_args_on_host():
+    L = _lib.lib()
+    fake = ctypes.c_void_p(0x1000)
+    assert L.mk_softmax_lastdim(_lib.MK_DT_F32, fake, fake, 0, 8, None) == _lib.MK_EINVAL
+    assert L.mk_softmax_lastdim(7, fake, fake, 1, 8, None) == _lib.MK_EUNSUPPORTED
+    assert L.mk_rmsnorm_lastdim(_lib.MK_DT_F32, fake, None, fake, 1, 8, 1e-6, None) == _lib.MK_EINVAL
+    assert L.mk_reduce_lastdim(_lib.MK_DT_F32, 9, fake, fake, 1, 8, None) == _lib.MK_EUNSUPPORTED
+    assert L.mk_gemm_bf16(fake, fake, fake, 1, 16, 12, 16, 0, None) == _lib.MK_EUNSUPPORTED

@@ -1,0 +1,99 @@
+"""GPU parity of the fused elementwise kernel (mk_elementwise) against the
+oracle's op-by-op evaluation (oracle/eltwise.py), for the workload's 6-op
+chain (mul, add, exp, log1p, max, select) in f32 and bf16 (per-op bf16
+rounding) and for single ops with special values."""
+
+import numpy as np
+import pytest
+
+from _gpu import BF16_RTOL, dev, dev_bf16, host_bf16, host_bf16_bits, need_gpu, torch
+from oracle import bf16 as obf
+from oracle import eltwise
+
+pytestmark = pytest.mark.gpu
+
+# CHAIN6 as a register program: slots 0 = x; then one slot per step.
+CHAIN6_PROGRAM = [
+    ("LOAD", 0, 0, 0, 0, 0.0),
+    ("CONST", 1, 0, 0, 0, 1.5), ("MUL", 2, 0, 1, 0, 0.0),
+    ("CONST", 1, 0, 0, 0, 0.5), ("ADD", 3, 2, 1, 0, 0.0),
+    ("EXP", 4, 3, 0, 0, 0.0),
+    ("LOG1P", 5, 4, 0, 0, 0.0),
+    ("MAX", 6, 5, 0, 0, 0.0),
+    ("CONST", 1, 0, 0, 0, 0.0), ("CMP_GT", 7, 0, 1, 0, 0.0),
+    ("SELECT", 8, 7, 6, 3, 0.0),
+]
+
+
+def _ops():
+    need_gpu()
+    from mi355x import ops
+    return ops
+
+
+def _close_f32(out, ref, rtol=1e-5):
+    out = np.asarray(out, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert np.array_equal(np.isnan(out), np.isnan(ref))
+    f = ~np.isnan(ref)
+    err = np.abs(out[f] - ref[f])
+    tol = rtol * np.abs(ref[f]) + 1e-30
+    assert np.all(err <= tol), f"max rel {np.max(err / np.maximum(np.abs(ref[f]), 1e-30)):.3e}"
+
+
+@pytest.mark.parametrize("n", [1, 7, 8, 1000, 4096 * 3 + 5, 1 << 20])
+def test_chain6_f32(n):
+    ops = _ops()
+    x = (np.random.default_rng(n).standard_normal(n) * np.sqrt(2.0)).astype(np.float32)
+    y = ops.elementwise(CHAIN6_PROGRAM, [dev(x)], out_slot=8).cpu().numpy()
+    ref = eltwise.evaluate(eltwise.CHAIN6, [x], "f32")
+    _close_f32(y, ref)
+
+
+@pytest.mark.parametrize("n", [8, 1000, 1 << 20])
+def test_chain6_bf16(n):
+    ops = _ops()
+    xb = obf.f32_to_bf16_bits((np.random.default_rng(n + 1).standard_normal(n) * np.sqrt(2.0)).astype(np.float32))
+    y = host_bf16(ops.elementwise(CHAIN6_PROGRAM, [dev_bf16(xb)], out_slot=8))
+    ref = eltwise.evaluate(eltwise.CHAIN6, [obf.bf16_bits_to_f32(xb)], "bf16")
+    rel = np.abs(y - ref) / np.maximum(np.abs(ref), 1e-30)
+    assert np.max(rel) <= BF16_RTOL, np.max(rel)
+    # With the same per-op rounding points, almost every element is bit-equal.
+    assert np.mean(y == ref) > 0.98
+
+
+def test_binary_ops_and_special_values():
+    ops = _ops()
+    vals = np.array([0.0, -0.0, 1.0, -1.0, 2.5, np.inf, -np.inf, np.nan], np.float32)
+    a = np.repeat(vals, len(vals))
+    b = np.tile(vals, len(vals))
+    for name, ref_fn in [("ADD", np.add), ("SUB", np.subtract), ("MUL", np.multiply),
+                         ("MAX", eltwise._max), ("MIN", eltwise._min)]:
+        prog = [("LOAD", 0, 0, 0, 0, 0.0), ("LOAD", 1, 1, 0, 0, 0.0), (name, 2, 0, 1, 0, 0.0)]
+        y = ops.elementwise(prog, [dev(a), dev(b)], out_slot=2).cpu().numpy()
+        with np.errstate(invalid="ignore"):
+            ref = ref_fn(a.astype(np.float64), b.astype(np.float64)).astype(np.float32)
+        assert np.array_equal(np.isnan(y), np.isnan(ref)), name
+        f = ~np.isnan(ref)
+        assert np.array_equal(y[f], ref[f]), name
+        assert np.array_equal(np.signbit(y[f]), np.signbit(ref[f])), name
+
+
+def test_scalar_broadcast_input_and_compare_select():
+    ops = _ops()
+    x = np.linspace(-3, 3, 4097).astype(np.float32)
+    thr = np.array([0.25], np.float32)
+    prog = [("LOAD", 0, 0, 0, 0, 0.0), ("LOAD", 1, 1, 0, 0, 0.0), ("CMP_GE", 2, 0, 1, 0, 0.0),
+            ("NEG", 3, 0, 0, 0, 0.0), ("SELECT", 4, 2, 0, 3, 0.0)]
+    y = ops.elementwise(prog, [dev(x), dev(thr)], out_slot=4).cpu().numpy()
+    np.testing.assert_array_equal(y, np.where(x >= 0.25, x, -x))
+
+
+def test_invalid_program_rejected_on_host():
+    ops = _ops()
+    from mi355x._lib import MKError
+    x = dev(np.ones(16, np.float32))
+    with pytest.raises(MKError):
+        ops.elementwise([("ADD", 0, 1, 2, 0, 0.0)], [x], out_slot=0)  # reads undefined slots
+    with pytest.raises(MKError):
+        ops.elementwise([("LOAD", 0, 3, 0, 0, 0.0)], [x], out_slot=0)  # no input 3
