@@ -167,6 +167,14 @@ int mk_elementwise(int dtype, const mk_ew_instr* prog, int n_instr, const void* 
                    const int64_t* input_numel, int n_inputs, int out_slot, void* out, int64_t n,
                    void* stream);
 
+/* The first mk_elementwise call of a program on a device compiles a
+ * specialised straight-line kernel for it (hiprtc, gfx950) and caches it;
+ * mk_elementwise_prepare does that ahead of time (at plan-build time, and
+ * always before capturing a HIP graph).  Setting MK_EW_JIT=0 uses the
+ * precompiled register-program interpreter instead (same results). */
+int mk_elementwise_prepare(int dtype, const mk_ew_instr* prog, int n_instr, int n_inputs,
+                           int out_slot);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

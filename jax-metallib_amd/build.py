@@ -34,6 +34,7 @@ COMMON = [
 # Kernel library sources (order = link order).
 KERNEL_SOURCES = [
     "capi.cpp",
+    "ew_jit.cpp",
     "kernels/qmatmul.hip",
     "kernels/gemm.hip",
     "kernels/rowops.hip",
@@ -68,7 +69,7 @@ def build(jobs=None, verbose=True):
     with concurrent.futures.ThreadPoolExecutor(jobs) as ex:
         objs = list(ex.map(_compile, KERNEL_SOURCES))
     target = os.path.join(LIB, "libmk_kernels.so")
-    _link(objs, target)
+    _link(objs, target, ["-L/opt/rocm/lib", "-lhiprtc", "-Wl,-rpath,/opt/rocm/lib"])
     if verbose:
         print(f"built {os.path.relpath(target, REPO)}")
     return target

@@ -226,38 +226,19 @@ __global__ __launch_bounds__(256) void eltwise_kernel(EwArgs a) {
 // Host launcher
 // ---------------------------------------------------------------------------
 #include "../capi_internal.h"
+#include "../ew_jit.h"
 
-extern "C" int mk_elementwise(int dtype, const mk_ew_instr* prog, int n_instr, const void* const* inputs,
-                              const int64_t* input_numel, int n_inputs, int out_slot, void* out, int64_t n,
-                              void* stream) {
-  mkc::clear_error();
-  const char* fn = "mk_elementwise";
-  if (!prog || !out || (n_inputs > 0 && (!inputs || !input_numel)))
-    return mkc::fail(MK_EINVAL, "%s: null pointer argument", fn);
-  if (dtype != MK_DT_F32 && dtype != MK_DT_BF16) return mkc::fail(MK_EUNSUPPORTED, "%s: dtype %d", fn, dtype);
+namespace {
+
+// Host-side validation shared by mk_elementwise and mk_elementwise_prepare:
+// slots in range, loads of real inputs, sources written before use.
+int validate_program(const char* fn, const mk_ew_instr* prog, int n_instr, int n_inputs, int out_slot) {
+  if (!prog) return mkc::fail(MK_EINVAL, "%s: null program", fn);
   if (n_instr <= 0 || n_instr > mk::kEwMaxInstr)
     return mkc::fail(MK_EINVAL, "%s: program length %d outside 1..%d", fn, n_instr, mk::kEwMaxInstr);
   if (n_inputs < 0 || n_inputs > mk::kEwMaxInputs)
     return mkc::fail(MK_EINVAL, "%s: %d inputs (max %d)", fn, n_inputs, mk::kEwMaxInputs);
-  if (n <= 0) return mkc::fail(MK_EINVAL, "%s: element count must be positive", fn);
   if (out_slot < 0 || out_slot >= mk::kEwSlots) return mkc::fail(MK_EINVAL, "%s: bad output slot", fn);
-  mk::EwArgs a;
-  bool aligned = ((uintptr_t)out % 16 == 0) && (n % mk::kEwVec == 0);
-  for (int i = 0; i < n_inputs; ++i) {
-    if (!inputs[i]) return mkc::fail(MK_EINVAL, "%s: input %d is null", fn, i);
-    if (input_numel[i] != 1 && input_numel[i] != n)
-      return mkc::fail(MK_EINVAL, "%s: input %d has %lld elements (need 1 or %lld)", fn, i,
-                       (long long)input_numel[i], (long long)n);
-    a.in[i] = inputs[i];
-    a.in_numel[i] = input_numel[i];
-    if (input_numel[i] == n && (uintptr_t)inputs[i] % 16 != 0) aligned = false;
-  }
-  for (int i = n_inputs; i < mk::kEwMaxInputs; ++i) {
-    a.in[i] = nullptr;
-    a.in_numel[i] = 1;
-  }
-  // Validate every instruction on the host: slots in range, loads of real
-  // inputs, sources defined before use.
   bool defined[mk::kEwSlots] = {false};
   for (int i = 0; i < n_instr; ++i) {
     const mk_ew_instr& in = prog[i];
@@ -275,9 +256,58 @@ extern "C" int mk_elementwise(int dtype, const mk_ew_instr* prog, int n_instr, c
       if (src[k] < 0 || src[k] >= mk::kEwSlots || !defined[src[k]])
         return mkc::fail(MK_EINVAL, "%s: instr %d reads undefined slot %d", fn, i, src[k]);
     defined[in.dst] = true;
-    a.ins[i] = in;
   }
   if (!defined[out_slot]) return mkc::fail(MK_EINVAL, "%s: output slot %d never written", fn, out_slot);
+  return MK_OK;
+}
+
+bool jit_enabled() {
+  const char* v = getenv("MK_EW_JIT");
+  return !(v && v[0] == '0');
+}
+
+}  // namespace
+
+extern "C" int mk_elementwise_prepare(int dtype, const mk_ew_instr* prog, int n_instr, int n_inputs,
+                                      int out_slot) {
+  mkc::clear_error();
+  const char* fn = "mk_elementwise_prepare";
+  if (dtype != MK_DT_F32 && dtype != MK_DT_BF16) return mkc::fail(MK_EUNSUPPORTED, "%s: dtype %d", fn, dtype);
+  int rc = validate_program(fn, prog, n_instr, n_inputs, out_slot);
+  if (rc != MK_OK || !jit_enabled()) return rc;
+  void* k = nullptr;
+  return mkc::ew_jit_get(dtype, prog, n_instr, n_inputs, out_slot, &k);
+}
+
+extern "C" int mk_elementwise(int dtype, const mk_ew_instr* prog, int n_instr, const void* const* inputs,
+                              const int64_t* input_numel, int n_inputs, int out_slot, void* out, int64_t n,
+                              void* stream) {
+  mkc::clear_error();
+  const char* fn = "mk_elementwise";
+  if (!prog || !out || (n_inputs > 0 && (!inputs || !input_numel)))
+    return mkc::fail(MK_EINVAL, "%s: null pointer argument", fn);
+  if (dtype != MK_DT_F32 && dtype != MK_DT_BF16) return mkc::fail(MK_EUNSUPPORTED, "%s: dtype %d", fn, dtype);
+  {
+    const int rc = validate_program(fn, prog, n_instr, n_inputs, out_slot);
+    if (rc != MK_OK) return rc;
+  }
+  if (n <= 0) return mkc::fail(MK_EINVAL, "%s: element count must be positive", fn);
+  mk::EwArgs a;
+  bool aligned = ((uintptr_t)out % 16 == 0) && (n % mk::kEwVec == 0);
+  for (int i = 0; i < n_inputs; ++i) {
+    if (!inputs[i]) return mkc::fail(MK_EINVAL, "%s: input %d is null", fn, i);
+    if (input_numel[i] != 1 && input_numel[i] != n)
+      return mkc::fail(MK_EINVAL, "%s: input %d has %lld elements (need 1 or %lld)", fn, i,
+                       (long long)input_numel[i], (long long)n);
+    a.in[i] = inputs[i];
+    a.in_numel[i] = input_numel[i];
+    if (input_numel[i] == n && (uintptr_t)inputs[i] % 16 != 0) aligned = false;
+  }
+  for (int i = n_inputs; i < mk::kEwMaxInputs; ++i) {
+    a.in[i] = nullptr;
+    a.in_numel[i] = 1;
+  }
+  for (int i = 0; i < n_instr; ++i) a.ins[i] = prog[i];
   a.out = out;
   a.n = n;
   a.n_instr = n_instr;
@@ -285,6 +315,22 @@ extern "C" int mk_elementwise(int dtype, const mk_ew_instr* prog, int n_instr, c
   const int64_t chunks = (n + mk::kEwVec - 1) / mk::kEwVec;
   const int blocks = (int)std::min<int64_t>((chunks + 255) / 256, 256 * 16);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (jit_enabled()) {
+    // Generated straight-line kernel (compiled on the first call of this
+    // program on this device; see mk_elementwise_prepare).
+    void* k = nullptr;
+    const int rc = mkc::ew_jit_get(dtype, prog, n_instr, n_inputs, out_slot, &k);
+    if (rc != MK_OK) return rc;
+    int vec_ok = aligned ? 1 : 0;
+    long long nn[4] = {1, 1, 1, 1};
+    for (int i = 0; i < n_inputs; ++i) nn[i] = (long long)a.in_numel[i];
+    long long nl = (long long)n;
+    void* args[] = {&a.in[0], &a.in[1], &a.in[2], &a.in[3], &nn[0], &nn[1], &nn[2], &nn[3], &a.out, &nl, &vec_ok};
+    const int jblocks = (int)std::min<int64_t>((chunks + 255) / 256, 256 * 32);
+    hipError_t e = hipModuleLaunchKernel((hipFunction_t)k, jblocks, 1, 1, 256, 1, 1, 0, st, args, nullptr);
+    if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
+    return MK_OK;
+  }
   if (dtype == MK_DT_BF16) {
     if (aligned) hipLaunchKernelGGL((mk::eltwise_kernel<true, true>), dim3(blocks), dim3(256), 0, st, a);
     else hipLaunchKernelGGL((mk::eltwise_kernel<true, false>), dim3(blocks), dim3(256), 0, st, a);

@@ -45,6 +45,7 @@ SIGNATURES = {
     "mk_argmax_lastdim": (_i32, [_i32, _p, _p, _i64, _i64, _p]),
     "mk_reduce_lastdim": (_i32, [_i32, _i32, _p, _p, _i64, _i64, _p]),
     "mk_elementwise": (_i32, [_i32, _p, _i32, _p, _p, _i32, _i32, _p, _i64, _p]),
+    "mk_elementwise_prepare": (_i32, [_i32, _p, _i32, _i32, _i32]),
 }
 
 _LIB = None

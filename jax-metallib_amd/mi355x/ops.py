@@ -185,6 +185,7 @@ def elementwise(program, inputs, out_slot, out=None, dtype=None):
     ptrs = (_ct.c_void_p * max(1, len(inputs)))(*[t.data_ptr() for t in inputs])
     numel = (_ct.c_int64 * max(1, len(inputs)))(*[t.numel() for t in inputs])
     y = out if out is not None else torch.empty(ref.shape, dtype=ref.dtype, device=ref.device)
+    check(lib().mk_elementwise_prepare(dt, arr, len(program), len(inputs), out_slot))
     check(lib().mk_elementwise(dt, arr, len(program), ptrs, numel, len(inputs), out_slot, _ptr(y), n,
                                _stream(ref.device)))
     return y

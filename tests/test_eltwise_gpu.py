@@ -31,6 +31,17 @@ def _ops():
     return ops
 
 
+@pytest.fixture(params=["jit", "interpreter"], autouse=True)
+def ew_path(request, monkeypatch):
+    """Run every test on both paths: the generated kernel (default) and the
+    precompiled interpreter (MK_EW_JIT=0)."""
+    if request.param == "interpreter":
+        monkeypatch.setenv("MK_EW_JIT", "0")
+    else:
+        monkeypatch.delenv("MK_EW_JIT", raising=False)
+    return request.param
+
+
 def _close_f32(out, ref, rtol=1e-5):
     out = np.asarray(out, np.float64)
     ref = np.asarray(ref, np.float64)
