@@ -346,6 +346,147 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f32_kernel(GemmArgs p) {
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Large-tile bf16 GEMM (M % 256 == 0, N % 256 == 0, K % 64 == 0).
+//
+// 256 x 256 x 64 workgroup tile, 8 waves as 2 (m) x 4 (n), each wave a
+// 128 x 64 tile of 8 x 4 16x16x32 MFMA accumulators.  Both operands are
+// staged in LDS in their natural layouts (A [m][k], B [k][n]) through
+// registers with one barrier per k-tile (double buffer, 128 KB).  The B
+// fragments come straight out of the [k][n] layout with gfx950's transposing
+// LDS read, ds_read_b64_tr_b16: within each 16-lane group, lanes 4r + q name
+// the 8 bytes of row r, columns 4q..4q+3, and lane j receives column j of
+// the 4 x 16 block -- four consecutive k of one n, i.e. half of an MFMA
+// fragment.  No register transposes remain.
+//
+// LDS swizzles (16-byte chunks): A row r, chunk c lives at chunk
+// c ^ ((r >> 1) & 7), so the 16 rows of one fragment read cover all 64
+// banks; B row k, chunk c lives at c ^ (k & 3 | ((k >> 3) & 3) << 2), so the
+// 16 rows one transposing read touches land in 16 different 16-byte slots.
+// ---------------------------------------------------------------------------
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4* lds_s16x4_ptr;
+
+__device__ __forceinline__ int swz_a(int row, int c) { return c ^ ((row >> 1) & 7); }
+__device__ __forceinline__ int swz_b(int k, int c) { return c ^ ((k & 3) | (((k >> 3) & 3) << 2)); }
+
+__device__ __forceinline__ u32x2 lds_tr16(const uint16_t* p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+__global__ __launch_bounds__(512) void gemm_bf16_256_kernel(GemmArgs p) {
+  constexpr int BM = 256, BN = 256, BK = 64, NT = 512;
+  constexpr int TM = 8, TN = 4;  // per-wave MFMA tiles (128 x 64)
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint16_t* As = reinterpret_cast<uint16_t*>(smem);  // [2][BM * BK]
+  uint16_t* Bs = As + 2 * BM * BK;                    // [2][BK * BN]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
+  const int tiles_m = p.M / BM, tiles_n = p.N / BN;
+  int tm, tn;
+  tile_coords(xcd_logical_id(blockIdx.x, gridDim.x), tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const uint16_t* A = static_cast<const uint16_t*>(p.a) + (size_t)blockIdx.z * p.sa + (size_t)m0 * p.K;
+  const uint16_t* B = static_cast<const uint16_t*>(p.b) + (size_t)blockIdx.z * p.sb + n0;
+  const int K = p.K, N = p.N;
+
+  // Staging: 4 A chunks (row q/8, chunk q%8) and 4 B chunks (row q/32,
+  // chunk q%32) per thread, q = tid + 512 i.
+  u32x4 ra[4], rb[4];
+  auto load_tile = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int q = tid + NT * i;
+      ra[i] = *reinterpret_cast<const u32x4*>(A + (size_t)(q >> 3) * K + k0 + 8 * (q & 7));
+      rb[i] = *reinterpret_cast<const u32x4*>(B + (size_t)(k0 + (q >> 5)) * N + 8 * (q & 31));
+    }
+  };
+  auto store_tile = [&](int buf) {
+    uint16_t* as = As + buf * BM * BK;
+    uint16_t* bs = Bs + buf * BK * BN;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int q = tid + NT * i;
+      const int ar = q >> 3, ac = q & 7, br = q >> 5, bc = q & 31;
+      *reinterpret_cast<u32x4*>(as + ar * BK + 8 * swz_a(ar, ac)) = ra[i];
+      *reinterpret_cast<u32x4*>(bs + br * BN + 8 * swz_b(br, bc)) = rb[i];
+    }
+  };
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int KT = K / BK;
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+
+  // Per-lane fragment coordinates.
+  const int arow0 = wm * 128 + (lane & 15);          // + 16 * i
+  const int akb = lane >> 4;                          // k block (8 k) in a 32-k step
+  const int g = lane >> 4, r = (lane & 15) >> 2, q = lane & 3;
+  const int bcol0 = wn * 64 + 4 * q;                  // + 16 * j
+
+  for (int kt = 0; kt < KT; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < KT) load_tile((kt + 1) * BK);
+    const uint16_t* as = As + buf * BM * BK;
+    const uint16_t* bs = Bs + buf * BK * BN;
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      u32x4 af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int row = arow0 + 16 * i;
+        af[i] = *reinterpret_cast<const u32x4*>(as + row * BK + 8 * swz_a(row, 4 * ks + akb));
+      }
+      const int k1 = 32 * ks + 8 * g + r;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int col = bcol0 + 16 * j;
+        const u32x2 lo = lds_tr16(bs + k1 * BN + 8 * swz_b(k1, col >> 3) + (col & 7));
+        const u32x2 hi = lds_tr16(bs + (k1 + 4) * BN + 8 * swz_b(k1 + 4, col >> 3) + (col & 7));
+        bf[j] = u32x4{lo.x, lo.y, hi.x, hi.y};
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(bf[j], af[i], acc[i][j]);
+    }
+    if (kt + 1 < KT) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue (C^T tiles): lane owns row m, columns n..n+3 of each tile.
+  const int mrow = m0 + wm * 128 + (lane & 15);
+  const int ncol = n0 + wn * 64 + 4 * (lane >> 4);
+  if (p.out_f32) {
+    float* C = static_cast<float*>(p.c) + (size_t)blockIdx.z * p.sc;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        *reinterpret_cast<f32x4*>(C + (size_t)(mrow + 16 * i) * N + ncol + 16 * j) = acc[i][j];
+  } else {
+    uint16_t* C = static_cast<uint16_t*>(p.c) + (size_t)blockIdx.z * p.sc;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        u32x2 o;
+        o.x = pack_bf16x2(acc[i][j].x, acc[i][j].y);
+        o.y = pack_bf16x2(acc[i][j].z, acc[i][j].w);
+        *reinterpret_cast<u32x2*>(C + (size_t)(mrow + 16 * i) * N + ncol + 16 * j) = o;
+      }
+  }
+}
+
 }  // namespace mk
 
 // ---------------------------------------------------------------------------
@@ -418,9 +559,21 @@ extern "C" int mk_gemm_bf16(const void* a, const void* b, void* c, int64_t batch
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256) * batch;
   int tile = env_tile();
-  if (tile == 0) tile = big_tiles >= 192 ? 256 : 128;
-  hipError_t e = tile == 256 ? launch_bf16<256, 256, 2, 2>(p, (int)batch, st)
-                             : launch_bf16<128, 128, 2, 2>(p, (int)batch, st);
+  if (tile == 0) tile = big_tiles >= 128 ? 256 : 128;
+  hipError_t e;
+  if (tile == 256 && M % 256 == 0 && N % 256 == 0 && K % 64 == 0) {
+    constexpr size_t lds = (size_t)2 * (256 * 64 + 64 * 256) * 2;
+    e = lds_opt_in((const void*)mk::gemm_bf16_256_kernel, lds);
+    if (e == hipSuccess) {
+      hipLaunchKernelGGL(mk::gemm_bf16_256_kernel, dim3((unsigned)((M / 256) * (N / 256)), 1, (unsigned)batch),
+                         dim3(512), lds, st, p);
+      e = hipGetLastError();
+    }
+  } else if (tile == 256) {
+    e = launch_bf16<256, 256, 2, 2>(p, (int)batch, st);
+  } else {
+    e = launch_bf16<128, 128, 2, 2>(p, (int)batch, st);
+  }
   if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "mk_gemm_bf16: launch failed: %s", hipGetErrorString(e));
   return MK_OK;
 }

@@ -111,3 +111,19 @@ def test_gemm_f32_overflow_case():
     b = np.eye(32, dtype=np.float32)
     c = ops.gemm_f32(dev(a), dev(b)).cpu().numpy()
     assert np.all(c == 7e4)
+
+
+@pytest.mark.parametrize("batch,M,N,K", [(1, 256, 256, 64), (3, 512, 768, 320), (2, 1024, 256, 1024)])
+def test_gemm_bf16_large_tile_path(batch, M, N, K, monkeypatch):
+    """The 256x256 kernel (transposing LDS reads for B) on shapes small enough
+    for a full float64 check, forced with MK_GEMM_TILE=256."""
+    ops = _ops()
+    monkeypatch.setenv("MK_GEMM_TILE", "256")
+    rng = np.random.default_rng(batch + M + N + K)
+    a = _case(rng, (batch, M, K), 1.0 / np.sqrt(np.sqrt(K)))
+    b = _case(rng, (batch, K, N), 1.0 / np.sqrt(np.sqrt(K)))
+    c = ops.gemm_bf16(dev_bf16(a), dev_bf16(b), out_f32=True)
+    ref, _ = gemm.matmul_bf16(a, b)
+    assert_rel_close(c.cpu().numpy().reshape(ref.shape), ref, 8e-5, f"256 tile {batch}x{M}x{N}x{K}")
+    cb = ops.gemm_bf16(dev_bf16(a), dev_bf16(b), out_f32=False)
+    assert_rel_close(cb.float().cpu().numpy().reshape(ref.shape), ref, BF16_RTOL, "256 tile bf16 out")
