@@ -350,8 +350,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f32_kernel(GemmArgs p) {
 // ---------------------------------------------------------------------------
 // Large-tile bf16 GEMM (M % 256 == 0, N % 256 == 0, K % 64 == 0).
 //
-// 256 x 256 x 64 workgroup tile, 8 waves as 2 (m) x 4 (n), each wave a
-// 128 x 64 tile of 8 x 4 16x16x32 MFMA accumulators.  Both operands are
+// 256 x 256 x 64 workgroup tile; WM x WN waves (2 x 4: each wave a 128 x 64
+// tile of 8 x 4 16x16x32 MFMA accumulators; 2 x 2: 128 x 128, 8 x 8).  Both operands are
 // staged in LDS in their natural layouts (A [m][k], B [k][n]) through
 // registers with one barrier per k-tile (double buffer, 128 KB).  The B
 // fragments come straight out of the [k][n] layout with gfx950's transposing
@@ -376,15 +376,17 @@ __device__ __forceinline__ u32x2 lds_tr16(const uint16_t* p) {
   return __builtin_bit_cast(u32x2, v);
 }
 
-__global__ __launch_bounds__(512) void gemm_bf16_256_kernel(GemmArgs p) {
-  constexpr int BM = 256, BN = 256, BK = 64, NT = 512;
-  constexpr int TM = 8, TN = 4;  // per-wave MFMA tiles (128 x 64)
+template <int WM_, int WN_>
+__global__ __launch_bounds__(WM_ * WN_ * 64) void gemm_bf16_256_kernel(GemmArgs p) {
+  constexpr int BM = 256, BN = 256, BK = 64, NT = WM_ * WN_ * 64;
+  constexpr int TM = BM / WM_ / 16, TN = BN / WN_ / 16;  // per-wave MFMA tiles
+  constexpr int CH = BM * BK / 8 / NT;                   // 16-byte chunks per thread (A and B each)
   extern __shared__ __align__(16) unsigned char smem[];
   uint16_t* As = reinterpret_cast<uint16_t*>(smem);  // [2][BM * BK]
   uint16_t* Bs = As + 2 * BM * BK;                    // [2][BK * BN]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 2, wn = wave & 3;
+  const int wm = wave / WN_, wn = wave % WN_;
   const int tiles_m = p.M / BM, tiles_n = p.N / BN;
   int tm, tn;
   tile_coords(xcd_logical_id(blockIdx.x, gridDim.x), tiles_m, tiles_n, tm, tn);
@@ -393,23 +395,27 @@ __global__ __launch_bounds__(512) void gemm_bf16_256_kernel(GemmArgs p) {
   const uint16_t* B = static_cast<const uint16_t*>(p.b) + (size_t)blockIdx.z * p.sb + n0;
   const int K = p.K, N = p.N;
 
-  // Staging: 4 A chunks (row q/8, chunk q%8) and 4 B chunks (row q/32,
-  // chunk q%32) per thread, q = tid + 512 i.
-  u32x4 ra[4], rb[4];
-  auto load_tile = [&](int k0) {
+  // Staging: CH A chunks (row q/8, chunk q%8) and CH B chunks (row q/32,
+  // chunk q%32) per thread, q = tid + NT * i, moved in two halves so only
+  // CH/2 + CH/2 chunks sit in registers at a time: half h of the next tile is
+  // loaded before 32-k step h and stored to the free buffer after it.
+  constexpr int HC = CH / 2;
+  static_assert(HC * 2 == CH, "staging splits in halves");
+  u32x4 ra[HC], rb[HC];
+  auto load_half = [&](int k0, int h) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int q = tid + NT * i;
+    for (int i = 0; i < HC; ++i) {
+      const int q = tid + NT * (h * HC + i);
       ra[i] = *reinterpret_cast<const u32x4*>(A + (size_t)(q >> 3) * K + k0 + 8 * (q & 7));
       rb[i] = *reinterpret_cast<const u32x4*>(B + (size_t)(k0 + (q >> 5)) * N + 8 * (q & 31));
     }
   };
-  auto store_tile = [&](int buf) {
+  auto store_half = [&](int buf, int h) {
     uint16_t* as = As + buf * BM * BK;
     uint16_t* bs = Bs + buf * BK * BN;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int q = tid + NT * i;
+    for (int i = 0; i < HC; ++i) {
+      const int q = tid + NT * (h * HC + i);
       const int ar = q >> 3, ac = q & 7, br = q >> 5, bc = q & 31;
       *reinterpret_cast<u32x4*>(as + ar * BK + 8 * swz_a(ar, ac)) = ra[i];
       *reinterpret_cast<u32x4*>(bs + br * BN + 8 * swz_b(br, bc)) = rb[i];
@@ -423,29 +429,29 @@ __global__ __launch_bounds__(512) void gemm_bf16_256_kernel(GemmArgs p) {
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int KT = K / BK;
-  load_tile(0);
-  store_tile(0);
+  load_half(0, 0);
+  store_half(0, 0);
+  load_half(0, 1);
+  store_half(0, 1);
   __syncthreads();
 
   // Per-lane fragment coordinates.
-  const int arow0 = wm * 128 + (lane & 15);          // + 16 * i
+  const int arow0 = wm * (16 * TM) + (lane & 15);   // + 16 * i
   const int akb = lane >> 4;                          // k block (8 k) in a 32-k step
   const int g = lane >> 4, r = (lane & 15) >> 2, q = lane & 3;
-  const int bcol0 = wn * 64 + 4 * q;                  // + 16 * j
+  const int bcol0 = wn * (16 * TN) + 4 * q;          // + 16 * j
 
   for (int kt = 0; kt < KT; ++kt) {
     const int buf = kt & 1;
-    if (kt + 1 < KT) load_tile((kt + 1) * BK);
+    const bool more = kt + 1 < KT;
     const uint16_t* as = As + buf * BM * BK;
     const uint16_t* bs = Bs + buf * BK * BN;
 #pragma unroll
     for (int ks = 0; ks < BK / 32; ++ks) {
-      u32x4 af[TM], bf[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int row = arow0 + 16 * i;
-        af[i] = *reinterpret_cast<const u32x4*>(as + row * BK + 8 * swz_a(row, 4 * ks + akb));
-      }
+      if (more) load_half((kt + 1) * BK, ks);
+      // All B fragments of the step, then one A fragment per row of tiles
+      // (keeps only TN + 1 fragments live).
+      u32x4 bf[TN];
       const int k1 = 32 * ks + 8 * g + r;
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
@@ -455,17 +461,20 @@ __global__ __launch_bounds__(512) void gemm_bf16_256_kernel(GemmArgs p) {
         bf[j] = u32x4{lo.x, lo.y, hi.x, hi.y};
       }
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+      for (int i = 0; i < TM; ++i) {
+        const int row = arow0 + 16 * i;
+        const u32x4 af = *reinterpret_cast<const u32x4*>(as + row * BK + 8 * swz_a(row, 4 * ks + akb));
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(bf[j], af[i], acc[i][j]);
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(bf[j], af, acc[i][j]);
+      }
+      if (more) store_half(buf ^ 1, ks);
     }
-    if (kt + 1 < KT) store_tile(buf ^ 1);
     __syncthreads();
   }
 
   // Epilogue (C^T tiles): lane owns row m, columns n..n+3 of each tile.
-  const int mrow = m0 + wm * 128 + (lane & 15);
-  const int ncol = n0 + wn * 64 + 4 * (lane >> 4);
+  const int mrow = m0 + wm * (16 * TM) + (lane & 15);
+  const int ncol = n0 + wn * (16 * TN) + 4 * (lane >> 4);
   if (p.out_f32) {
     float* C = static_cast<float*>(p.c) + (size_t)blockIdx.z * p.sc;
 #pragma unroll
@@ -563,12 +572,16 @@ extern "C" int mk_gemm_bf16(const void* a, const void* b, void* c, int64_t batch
   hipError_t e;
   if (tile == 256 && M % 256 == 0 && N % 256 == 0 && K % 64 == 0) {
     constexpr size_t lds = (size_t)2 * (256 * 64 + 64 * 256) * 2;
-    e = lds_opt_in((const void*)mk::gemm_bf16_256_kernel, lds);
-    if (e == hipSuccess) {
-      hipLaunchKernelGGL(mk::gemm_bf16_256_kernel, dim3((unsigned)((M / 256) * (N / 256)), 1, (unsigned)batch),
-                         dim3(512), lds, st, p);
-      e = hipGetLastError();
+    const dim3 grid((unsigned)((M / 256) * (N / 256)), 1, (unsigned)batch);
+    const char* w = getenv("MK_GEMM_WAVES");
+    if (w && atoi(w) == 4) {
+      e = lds_opt_in((const void*)mk::gemm_bf16_256_kernel<2, 2>, lds);
+      if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256_kernel<2, 2>), grid, dim3(256), lds, st, p);
+    } else {
+      e = lds_opt_in((const void*)mk::gemm_bf16_256_kernel<2, 4>, lds);
+      if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256_kernel<2, 4>), grid, dim3(512), lds, st, p);
     }
+    if (e == hipSuccess) e = hipGetLastError();
   } else if (tile == 256) {
     e = launch_bf16<256, 256, 2, 2>(p, (int)batch, st);
   } else {
