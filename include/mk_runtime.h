@@ -1,0 +1,159 @@
+/*
+ * mk_runtime.h -- the plugin's runtime API: client, device buffers,
+ * executables compiled from StableHLO text, completion events and owned
+ * errors, on one MI355X.
+ *
+ * This is the object model and call contract of the reference's PJRT C-API
+ * layer, restated as plain C: every entry point mirrors one PJRT callback
+ * (cited below) with the same argument meaning, ownership and error
+ * behaviour.  The PJRT function table itself (GetPjrtApi,
+ * src/pjrt_plugin/api/pjrt_api.cc:324-329) is a thin adapter over these
+ * calls; it needs the exact pjrt_c_api.h of the jaxlib it is loaded into,
+ * which this build does not have (see the integration notes).
+ *
+ * Conventions (from the reference, src/pjrt_plugin/api/):
+ *   - calls return NULL on success or an owned mkrt_error (free it with
+ *     mkrt_error_destroy), as PJRT callbacks return PJRT_Error*
+ *     (pjrt_handles.h:75, pjrt_memory.cc:22-57);
+ *   - error codes are PJRT_Error_Code values (absl status numbering);
+ *   - element types are PJRT_Buffer_Type values;
+ *   - objects are created by the runtime and destroyed by the caller;
+ *     execute borrows its inputs and returns new output buffers, each
+ *     owning its device memory, plus one completion event
+ *     (pjrt_executable.cc:245-301);
+ *   - destroying a buffer waits for the work producing it
+ *     (core/mps_buffer.mm:656-662).
+ */
+#ifndef MK_RUNTIME_H_
+#define MK_RUNTIME_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* PJRT_Error_Code (absl::StatusCode numbering). */
+enum {
+  MKRT_OK = 0,
+  MKRT_CANCELLED = 1,
+  MKRT_UNKNOWN = 2,
+  MKRT_INVALID_ARGUMENT = 3,
+  MKRT_DEADLINE_EXCEEDED = 4,
+  MKRT_NOT_FOUND = 5,
+  MKRT_ALREADY_EXISTS = 6,
+  MKRT_PERMISSION_DENIED = 7,
+  MKRT_RESOURCE_EXHAUSTED = 8,
+  MKRT_FAILED_PRECONDITION = 9,
+  MKRT_ABORTED = 10,
+  MKRT_OUT_OF_RANGE = 11,
+  MKRT_UNIMPLEMENTED = 12,
+  MKRT_INTERNAL = 13,
+  MKRT_UNAVAILABLE = 14
+};
+
+/* PJRT_Buffer_Type values for the types this plugin handles. */
+enum {
+  MKRT_PRED = 1,
+  MKRT_S8 = 2,
+  MKRT_S16 = 3,
+  MKRT_S32 = 4,
+  MKRT_S64 = 5,
+  MKRT_U8 = 6,
+  MKRT_U16 = 7,
+  MKRT_U32 = 8,
+  MKRT_U64 = 9,
+  MKRT_F16 = 10,
+  MKRT_F32 = 11,
+  MKRT_F64 = 12,
+  MKRT_BF16 = 13
+};
+
+typedef struct mkrt_error mkrt_error;
+typedef struct mkrt_client mkrt_client;
+typedef struct mkrt_buffer mkrt_buffer;
+typedef struct mkrt_executable mkrt_executable;
+typedef struct mkrt_event mkrt_event;
+
+/* Errors (PJRT_Error_Destroy / _Message / _GetCode, pjrt_memory.cc:59-104). */
+void mkrt_error_destroy(mkrt_error* err);
+const char* mkrt_error_message(const mkrt_error* err);
+int mkrt_error_code(const mkrt_error* err);
+
+/* Client (PJRT_Client_Create / _Destroy / _PlatformName,
+ * pjrt_client.cc:34-82; platform name pjrt_api.cc:18).  One HIP device
+ * (ordinal 0), one stream, a caching device allocator. */
+mkrt_error* mkrt_client_create(mkrt_client** out);
+void mkrt_client_destroy(mkrt_client* client);
+const char* mkrt_client_platform_name(const mkrt_client* client);
+/* PJRT_Device_MemoryStats (pjrt_device.cc:110-140). */
+mkrt_error* mkrt_client_memory_stats(mkrt_client* client, int64_t* bytes_in_use, int64_t* bytes_limit);
+
+/* Buffers (PJRT_Client_BufferFromHostBuffer pjrt_client.cc:254-293: a
+ * synchronous copy whose done-with-host event is already ready;
+ * PJRT_Buffer_ToHostBuffer pjrt_buffer.cc:217-234: waits for the producer). */
+mkrt_error* mkrt_buffer_from_host(mkrt_client* client, const void* data, int type, const int64_t* dims,
+                                  int ndims, mkrt_buffer** out, mkrt_event** done_with_host);
+mkrt_error* mkrt_buffer_to_host(mkrt_buffer* buf, void* dst, int64_t dst_bytes, mkrt_event** done);
+int mkrt_buffer_type(const mkrt_buffer* buf);
+int mkrt_buffer_ndims(const mkrt_buffer* buf);
+const int64_t* mkrt_buffer_dims(const mkrt_buffer* buf);
+int64_t mkrt_buffer_bytes(const mkrt_buffer* buf);
+/* PJRT_Buffer_ReadyEvent (pjrt_buffer.cc:241-247). */
+mkrt_error* mkrt_buffer_ready_event(mkrt_buffer* buf, mkrt_event** out);
+/* PJRT_Client_CreateErrorBuffer (pjrt_client.cc:362-386): a buffer whose
+ * ready event carries the error; reading it returns that error. */
+mkrt_error* mkrt_buffer_create_error(mkrt_client* client, int code, const char* message, int type,
+                                     const int64_t* dims, int ndims, mkrt_buffer** out);
+/* PJRT_Buffer_Destroy: waits for the producer, then returns the memory to
+ * the client's allocator. */
+void mkrt_buffer_destroy(mkrt_buffer* buf);
+
+/* Compile (PJRT_Client_Compile, pjrt_client.cc:178-244).  `format` "mlir"
+ * takes StableHLO in MLIR text form (as jax's lowered.as_text() prints it);
+ * unsupported ops fail here with a message listing them
+ * (pjrt_client.cc:211-220).  The execution plan is built on the first
+ * execute (core/mps_executable.mm:9152, BuildExecutionPlan :7627). */
+mkrt_error* mkrt_compile(mkrt_client* client, const char* code, int64_t code_bytes, const char* format,
+                         mkrt_executable** out);
+/* Parse and plan only, without a device: the same compile-time support
+ * check (unsupported ops fail with UNIMPLEMENTED listing them,
+ * pjrt_client.cc:211-220), plus the plan trace written into plan_text
+ * (truncated to plan_text_bytes, NUL-terminated) and the step count. */
+mkrt_error* mkrt_compile_check(const char* code, int64_t code_bytes, const char* format, char* plan_text,
+                               int64_t plan_text_bytes, int* num_steps);
+int mkrt_executable_num_inputs(const mkrt_executable* exe);
+int mkrt_executable_num_outputs(const mkrt_executable* exe);
+/* Number of kernel launches per execute and a one-line-per-step plan
+ * description ("" before the first execute) -- the plan trace. */
+int mkrt_executable_num_steps(const mkrt_executable* exe);
+const char* mkrt_executable_plan(const mkrt_executable* exe);
+/* PJRT_LoadedExecutable_Execute (pjrt_executable.cc:245-301): inputs are
+ * borrowed; `outputs` receives num_outputs new buffers; `done` (optional)
+ * receives the completion event of the whole execution. */
+mkrt_error* mkrt_execute(mkrt_executable* exe, mkrt_buffer* const* inputs, int num_inputs,
+                         mkrt_buffer** outputs, mkrt_event** done);
+void mkrt_executable_destroy(mkrt_executable* exe);
+
+/* Events (pjrt_event.cc, core/completion_event.h).  await waits at most
+ * timeout_ms (< 0: the MK_COMPLETION_TIMEOUT_MS environment value, default
+ * 30000) and returns DEADLINE_EXCEEDED when it elapses (the work is left
+ * pending); a ready event with an error returns a copy of that error.
+ * event_error before the event is ready returns FAILED_PRECONDITION
+ * (pjrt_event.cc:32-44).  on_ready runs the callback once, on the
+ * completing thread or inline when already ready (pjrt_event.cc:81-98); the
+ * callback receives an owned error or NULL. */
+typedef void (*mkrt_event_callback)(mkrt_error* err, void* user);
+mkrt_error* mkrt_event_create(mkrt_event** out);
+mkrt_error* mkrt_event_set(mkrt_event* ev, int code, const char* message);
+int mkrt_event_is_ready(const mkrt_event* ev);
+mkrt_error* mkrt_event_error(const mkrt_event* ev);
+mkrt_error* mkrt_event_await(mkrt_event* ev, int64_t timeout_ms);
+mkrt_error* mkrt_event_on_ready(mkrt_event* ev, mkrt_event_callback cb, void* user);
+void mkrt_event_destroy(mkrt_event* ev);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* MK_RUNTIME_H_ */

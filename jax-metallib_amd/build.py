@@ -4,7 +4,8 @@
     python jax-metallib_amd/build.py --jobs 8
 
 Outputs (git-ignored, shipped with the tree):
-    jax-metallib_amd/lib/libmk_kernels.so   kernel C-ABI (include/mk_kernels.h)
+    jax-metallib_amd/lib/libmk_kernels.so   kernel C-ABI (include/mk_kernels.h) and
+                                            the plugin runtime (include/mk_runtime.h)
 
 Every HIP translation unit is compiled with hipcc for gfx950 only, with the
 packed-FP32 feature disabled (-Xclang -target-feature -Xclang -packed-fp32-ops);
@@ -39,6 +40,9 @@ KERNEL_SOURCES = [
     "kernels/gemm.hip",
     "kernels/rowops.hip",
     "kernels/eltwise.hip",
+    "runtime/shlo_parser.cpp",
+    "runtime/planner.cpp",
+    "runtime/runtime.cpp",
 ]
 
 

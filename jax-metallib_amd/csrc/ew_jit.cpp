@@ -133,7 +133,9 @@ std::string generate(int dtype, const mk_ew_instr* prog, int n_instr, int n_inpu
   std::string slot[16];
   for (int i = 0; i < n_instr; ++i) {
     const mk_ew_instr& in = prog[i];
-    const std::string A = slot[in.a], B = slot[in.b], C = slot[in.c];
+    // Operand fields an op does not use may hold anything (-1 included).
+    auto src = [&](int k) { return k >= 0 && k < 16 ? slot[k] : std::string(); };
+    const std::string A = src(in.a), B = src(in.b), C = src(in.c);
     std::string ex;
     bool rnd = bf;
     switch (in.op) {

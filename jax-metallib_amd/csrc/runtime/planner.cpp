@@ -1,0 +1,1076 @@
+// Planner: StableHLO graph -> kernel steps.
+//
+// Walks back from the returned values.  Each value is produced by one of:
+//   - a fused pattern rooted at it (softmax, RMSNorm, argmax, last-axis
+//     reduce, dot_general as GEMM, dot_general over a dequantized int4/int8
+//     weight as one dequant-matmul), matched structurally the way the
+//     reference's fusion passes match MLIR (IsSoftmaxPattern,
+//     core/mps_executable.mm:1922-2089; LayerNorm :1457-1820; argmax
+//     detectArgReduceKind, ops/reduction_ops.mm:74-115; HandleDotGeneral,
+//     ops/binary_ops.mm:644-1100);
+//   - an elementwise program: the maximal elementwise DAG under the value,
+//     scalars folded in as immediates, lowered to mk_elementwise
+//     instructions (the reference's fused elementwise segments,
+//     core/mps_executable.mm:7393-7508 and :4303-4586);
+//   - a view (reshape, same-type convert, size-1 broadcast) of another value,
+//     which shares its buffer;
+//   - an argument or a constant.
+// Pattern internals that something else also needs are simply computed
+// again by that consumer, so matches never depend on use counts.
+#include "planner.h"
+
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <functional>
+#include <map>
+#include <set>
+#include <sstream>
+
+#include "mk_runtime.h"
+
+namespace mkrt {
+
+namespace {
+
+bool is_float(int dt) { return dt == DT_F32 || dt == DT_BF16 || dt == DT_F16 || dt == DT_F64; }
+
+int mk_dt(int dt) { return dt == DT_F32 ? MK_DT_F32 : dt == DT_BF16 ? MK_DT_BF16 : -1; }
+
+float to_bf16_value(double v) {
+  float f = (float)v;
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7f800000u) != 0x7f800000u) u += 0x7fffu + ((u >> 16) & 1u);
+  else if (u & 0x007fffffu) u |= 0x00400000u;
+  u &= 0xffff0000u;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+double round_to(double v, int dt) {
+  if (dt == DT_F32) return (float)v;
+  if (dt == DT_BF16) return to_bf16_value(v);
+  return v;
+}
+
+const std::set<std::string>& unary_ops() {
+  static const std::set<std::string> s = {"negate", "abs", "exponential", "log", "log_plus_one",
+                                          "exponential_minus_one", "tanh", "rsqrt", "sqrt",
+                                          "logistic", "floor", "ceil", "not", "convert"};
+  return s;
+}
+const std::set<std::string>& binary_ops() {
+  static const std::set<std::string> s = {"add", "subtract", "multiply", "divide", "maximum",
+                                          "minimum", "power", "compare", "and", "or"};
+  return s;
+}
+
+class Planner {
+ public:
+  explicit Planner(const Function& f) : f_(f), slot_of_(f.values.size(), -1), state_(f.values.size(), 0) {}
+
+  Plan run() {
+    for (size_t i = 0; i < f_.args.size(); ++i) {
+      const int a = f_.args[i];
+      Slot s;
+      s.kind = SLOT_ARG;
+      s.arg_index = (int)i;
+      s.bytes = type(a).bytes();
+      plan_.in_slot.push_back(new_slot(s));
+      slot_of_[a] = plan_.in_slot.back();
+      plan_.in_type.push_back(type(a));
+    }
+    std::set<int> used_out;
+    for (int r : f_.rets) {
+      int s = need(r);
+      if (!unsupported_.empty()) continue;
+      // Results own their memory: a result that is an argument, a constant
+      // or a buffer already handed to another result gets its own copy.
+      if (plan_.slots[s].kind != SLOT_TEMP || used_out.count(s)) {
+        Step st;
+        st.kind = ST_COPY;
+        st.in = {s};
+        st.bytes = type(r).bytes();
+        Slot t;
+        t.bytes = st.bytes;
+        st.out = new_slot(t);
+        st.desc = "copy " + type(r).str();
+        plan_.steps.push_back(st);
+        s = st.out;
+      }
+      used_out.insert(s);
+      plan_.out_slot.push_back(s);
+      plan_.out_type.push_back(type(r));
+    }
+    if (!unsupported_.empty()) {
+      std::string m = "unsupported operations for the MI355X plugin: ";
+      bool first = true;
+      for (const std::string& u : unsupported_) {
+        m += (first ? "" : "; ") + u;
+        first = false;
+      }
+      throw PlanError(MKRT_UNIMPLEMENTED, m);
+    }
+    return plan_;
+  }
+
+ private:
+  const Function& f_;
+  Plan plan_;
+  std::vector<int> slot_of_;
+  std::vector<char> state_;  // 1 = in progress (cycle guard)
+  std::set<std::string> unsupported_;
+
+  // ---- graph helpers -------------------------------------------------------
+  const TensorType& type(int v) const { return f_.values[v].type; }
+  const Op* def(int v) const { return f_.values[v].def_op < 0 ? nullptr : &f_.ops[f_.values[v].def_op]; }
+  bool is(int v, const char* name) const {
+    const Op* o = def(v);
+    return o && o->name == name;
+  }
+  int64_t numel(int v) const { return type(v).numel(); }
+  int64_t last_dim(int v) const { return type(v).dims.empty() ? 1 : type(v).dims.back(); }
+
+  int new_slot(const Slot& s) {
+    plan_.slots.push_back(s);
+    return (int)plan_.slots.size() - 1;
+  }
+
+  void reject(const Op* op, const std::string& why) {
+    unsupported_.insert((op ? "stablehlo." + op->name : std::string("value")) + (why.empty() ? "" : " (" + why + ")"));
+  }
+
+  static bool monotonic(const std::vector<int64_t>& d) {
+    for (size_t i = 1; i < d.size(); ++i)
+      if (d[i] <= d[i - 1]) return false;
+    return true;
+  }
+
+  // A broadcast_in_dim that only inserts size-1 dimensions (same element
+  // order), i.e. a reshape.
+  bool is_expand(const Op& op, int v) const {
+    if (op.name != "broadcast_in_dim" || op.operands.empty()) return false;
+    return numel(op.operands[0]) == numel(v) && monotonic(op.dims);
+  }
+
+  // Same buffer contents: reshape, same-type convert, size-1 expansion.
+  int view_src(int v) const {
+    const Op* op = def(v);
+    if (!op || op->operands.empty()) return -1;
+    const int s = op->operands[0];
+    if (op->name == "reshape" && numel(s) == numel(v) && type(s).dtype == type(v).dtype) return s;
+    if (op->name == "convert" && type(s).dtype == type(v).dtype) return s;
+    if (is_expand(*op, v) && type(s).dtype == type(v).dtype) return s;
+    return -1;
+  }
+  int peel_view(int v) const {
+    for (int s; (s = view_src(v)) >= 0;) v = s;
+    return v;
+  }
+  // Views and converts (for dtype-changing converts the caller checks the
+  // source type it ends at).
+  int peel_cvt(int v) const {
+    while (true) {
+      int s = view_src(v);
+      if (s < 0 && is(v, "convert")) s = def(v)->operands[0];
+      if (s < 0) return v;
+      v = s;
+    }
+  }
+
+  // v is a splat constant (through broadcasts, reshapes, converts).
+  bool splat(int v, double* out) const {
+    const int dt = type(v).dtype;
+    int u = v;
+    while (true) {
+      const Op* op = def(u);
+      if (!op) return false;
+      if (op->name == "constant") {
+        if (op->const_values.empty()) return false;
+        const double c = op->const_values[0];
+        for (double x : op->const_values)
+          if (!(x == c || (x != x && c != c))) return false;
+        *out = round_to(c, is_float(dt) ? dt : DT_F64);
+        return true;
+      }
+      if ((op->name == "broadcast_in_dim" || op->name == "reshape" || op->name == "convert") && !op->operands.empty()) {
+        u = op->operands[0];
+        continue;
+      }
+      return false;
+    }
+  }
+  bool splat_is(int v, double c) const {
+    double x;
+    return splat(v, &x) && (x == c || (x != x && c != c));
+  }
+
+  // v[i*C + j] == s[i] (broadcast along the last axis); returns s or -1.
+  int row_src(int v, int64_t C) const {
+    while (true) {
+      const Op* op = def(v);
+      if (!op || op->operands.empty()) return -1;
+      const int s = op->operands[0];
+      if ((op->name == "reshape" || (op->name == "convert" && type(s).dtype == type(v).dtype)) &&
+          numel(s) == numel(v) && last_dim(s) == C && last_dim(v) == C) {
+        v = s;
+        continue;
+      }
+      if (op->name != "broadcast_in_dim" || !monotonic(op->dims) || C <= 0 || numel(s) * C != numel(v))
+        return -1;
+      const int last = (int)type(v).dims.size() - 1;
+      for (size_t i = 0; i < op->dims.size(); ++i)
+        if (op->dims[i] == last && type(s).dims[i] != 1) return -1;
+      return s;
+    }
+  }
+  // v[i*C + j] == s[j]; returns s or -1.
+  int col_src(int v, int64_t C) const {
+    while (true) {
+      const Op* op = def(v);
+      if (!op || op->operands.empty()) return -1;
+      const int s = op->operands[0];
+      if (op->name == "reshape" && numel(s) == numel(v) && last_dim(s) == C && last_dim(v) == C &&
+          numel(s) == C) {
+        return s;
+      }
+      if (op->name != "broadcast_in_dim" || !monotonic(op->dims) || numel(s) != C) return -1;
+      const int last = (int)type(v).dims.size() - 1;
+      bool ok = false;
+      for (size_t i = 0; i < op->dims.size(); ++i) {
+        if (op->dims[i] == last && type(s).dims[i] == C) ok = true;
+      }
+      return ok || C == 1 ? s : -1;
+    }
+  }
+
+  // Last-axis reduce: returns the reduced input of `v`'s defining op (with
+  // body `body` and the neutral init) or -1.
+  int reduce_last_input(int v, const char* body) const {
+    const Op* op = def(v);
+    if (!op || op->name != "reduce" || op->operands.size() != 2 || op->reduce_body != body) return -1;
+    const int x = op->operands[0];
+    const int rank = (int)type(x).dims.size();
+    if (rank == 0 || op->dims.size() != 1 || op->dims[0] != rank - 1) return -1;
+    double init;
+    if (!splat(op->operands[1], &init)) return -1;
+    if (strcmp(body, "add") == 0 && init != 0.0) return -1;
+    if (strcmp(body, "maximum") == 0 && !(init == -INFINITY)) return -1;
+    return x;
+  }
+
+  // ---- materialisation -----------------------------------------------------
+  int need(int v) {
+    if (slot_of_[v] >= 0) return slot_of_[v];
+    if (state_[v]) throw PlanError(MKRT_INVALID_ARGUMENT, "cyclic value graph");
+    state_[v] = 1;
+    const int s = produce(v);
+    state_[v] = 0;
+    slot_of_[v] = s;
+    return s;
+  }
+
+  int temp_for(int v) {
+    Slot s;
+    s.bytes = type(v).bytes();
+    return new_slot(s);
+  }
+
+  int produce(int v) {
+    const Op* op = def(v);
+    if (!op) return 0;  // arguments are pre-assigned
+    const int src = view_src(v);
+    if (src >= 0) return need(src);
+    if (numel(v) == 0) return temp_for(v);  // nothing to compute
+    const std::string& n = op->name;
+    if (n == "constant") {
+      double c;
+      if (numel(v) > 4096 && splat(v, &c) && mk_dt(type(v).dtype) >= 0) return ew_root(v);
+      return const_slot(v, *op);
+    }
+    if (n == "dot_general" || n == "dot") {
+      int s;
+      if (try_qmm(v, &s)) return s;
+      if (try_gemm(v, *op, &s)) return s;
+      return dummy(v);
+    }
+    if (n == "reduce") {
+      int s;
+      if (try_argmax(v, *op, &s)) return s;
+      if (try_reduce(v, &s)) return s;
+      reject(op, "reduce over " + type(op->operands[0]).str() + " with body " + op->reduce_body);
+      return dummy(v);
+    }
+    if (n == "divide") {
+      int s;
+      if (try_softmax(v, &s)) return s;
+    }
+    if (n == "multiply") {
+      int s;
+      if (try_rmsnorm(v, &s)) return s;
+    }
+    if (n == "convert") {
+      int s;
+      if (try_qmm(v, &s)) return s;
+      if (try_reduce(v, &s)) return s;
+    }
+    if (is_elementwise(v)) return ew_root(v);
+    reject(op, op->name == "broadcast_in_dim" ? "broadcast of a non-scalar outside a fused pattern" : "");
+    return dummy(v);
+  }
+
+  int dummy(int v) { return temp_for(v); }
+
+  int const_slot(int v, const Op& op) {
+    Slot s;
+    s.kind = SLOT_CONST;
+    const TensorType& t = type(v);
+    s.bytes = t.bytes();
+    const int64_t n = t.numel();
+    const int eb = dtype_bytes(t.dtype);
+    if (eb == 0) {
+      reject(&op, "constant of type " + t.str());
+      return new_slot(s);
+    }
+    s.data.resize((size_t)s.bytes);
+    for (int64_t i = 0; i < n; ++i) {
+      const double x = op.const_values.size() == 1 ? op.const_values[0]
+                       : (size_t)i < op.const_values.size() ? op.const_values[i] : 0.0;
+      uint8_t* p = s.data.data() + i * eb;
+      switch (t.dtype) {
+        case DT_F32: { float f = (float)x; memcpy(p, &f, 4); break; }
+        case DT_F64: memcpy(p, &x, 8); break;
+        case DT_BF16: { float f = to_bf16_value(x); uint32_t u; memcpy(&u, &f, 4); uint16_t h = (uint16_t)(u >> 16); memcpy(p, &h, 2); break; }
+        case DT_PRED: case DT_S8: case DT_U8: { int8_t b = (int8_t)(int64_t)x; memcpy(p, &b, 1); break; }
+        case DT_S16: case DT_U16: { int16_t b = (int16_t)(int64_t)x; memcpy(p, &b, 2); break; }
+        case DT_S32: case DT_U32: { int32_t b = (int32_t)(int64_t)x; memcpy(p, &b, 4); break; }
+        case DT_S64: case DT_U64: { int64_t b = (int64_t)x; memcpy(p, &b, 8); break; }
+        default: reject(&op, "constant of type " + t.str());
+      }
+    }
+    return new_slot(s);
+  }
+
+  // ---- GEMM ------------------------------------------------------------------
+  struct DotShape {
+    int64_t batch = 1, M = 0, N = 0, K = 0;
+  };
+  // Canonical [B..., M..., K] x [B..., K, N] (the reference's NN fast path,
+  // ops/binary_ops.mm:1011-1019).
+  bool dot_shape(const Op& op, DotShape* d) const {
+    if (op.operands.size() != 2) return false;
+    const TensorType& ta = type(op.operands[0]);
+    const TensorType& tb = type(op.operands[1]);
+    const int ra = (int)ta.dims.size(), rb = (int)tb.dims.size();
+    std::vector<int64_t> lb = op.lhs_batch, rbt = op.rhs_batch, lc = op.lhs_contract, rc = op.rhs_contract;
+    if (op.name == "dot") {
+      if (ra < 1 || rb < 1 || rb > 2) return false;
+      lc = {ra - 1};
+      rc = {0};
+    }
+    const int nb = (int)lb.size();
+    if (rbt.size() != lb.size()) return false;
+    for (int i = 0; i < nb; ++i)
+      if (lb[i] != i || rbt[i] != i || ta.dims[i] != tb.dims[i]) return false;
+    if (lc.size() != 1 || rc.size() != 1 || lc[0] != ra - 1 || rc[0] != nb) return false;
+    if (rb != nb + 2 && !(rb == nb + 1)) return false;
+    if (nb > 0 && ra != nb + 2) return false;
+    d->batch = 1;
+    for (int i = 0; i < nb; ++i) d->batch *= ta.dims[i];
+    d->K = ta.dims[ra - 1];
+    if (tb.dims[nb] != d->K) return false;
+    d->N = rb == nb + 2 ? tb.dims[nb + 1] : 1;
+    d->M = d->batch * d->K == 0 ? 0 : ta.numel() / (d->batch * d->K);
+    return true;
+  }
+
+  bool try_gemm(int v, const Op& op, int* out) {
+    DotShape d;
+    if (!dot_shape(op, &d)) {
+      reject(&op, "dimension numbers other than [batch..., M, K] x [batch..., K, N]");
+      return false;
+    }
+    const int ta = type(op.operands[0]).dtype, tb = type(op.operands[1]).dtype, tr = type(v).dtype;
+    Step st;
+    if (ta == DT_F32 && tb == DT_F32 && tr == DT_F32) {
+      st.kind = ST_GEMM_F32;
+      st.dt = MK_DT_F32;
+    } else if (ta == DT_BF16 && tb == DT_BF16 && (tr == DT_BF16 || tr == DT_F32)) {
+      st.kind = ST_GEMM_BF16;
+      st.dt = MK_DT_BF16;
+      st.out_f32 = tr == DT_F32;
+    } else {
+      reject(&op, std::string("operand types ") + dtype_name(ta) + " x " + dtype_name(tb) + " -> " + dtype_name(tr));
+      return false;
+    }
+    if (d.K == 0) {
+      st.kind = ST_ZERO;
+      st.bytes = type(v).bytes();
+      st.out = temp_for(v);
+      st.desc = "zero " + type(v).str() + " (empty contraction)";
+      plan_.steps.push_back(st);
+      *out = st.out;
+      return true;
+    }
+    if (numel(v) != d.batch * d.M * d.N) {
+      reject(&op, "result type " + type(v).str() + " does not match the operands");
+      return false;
+    }
+    if (d.K % 8 != 0 || d.N % 8 != 0) {
+      reject(&op, "K and N must be multiples of 8 (K=" + std::to_string(d.K) + ", N=" + std::to_string(d.N) + ")");
+      return false;
+    }
+    st.in = {need(op.operands[0]), need(op.operands[1])};
+    st.batch = d.batch;
+    st.M = d.M;
+    st.N = d.N;
+    st.K = d.K;
+    st.out = temp_for(v);
+    std::ostringstream ds;
+    ds << (st.kind == ST_GEMM_F32 ? "gemm_f32" : "gemm_bf16") << " batch=" << d.batch << " M=" << d.M << " N=" << d.N
+       << " K=" << d.K << " -> " << dtype_name(tr);
+    st.desc = ds.str();
+    plan_.steps.push_back(st);
+    *out = st.out;
+    return true;
+  }
+
+  // ---- dequant-matmul ----------------------------------------------------------
+  // Recognises X @ dequant(W) where the weight is built in jnp as
+  //   int4 g64: (interleave(P & 15, P >> 4).astype(f) - repeat(z, 64)) * repeat(s, 64)
+  //   int8 per-channel: W.astype(f) * s[None, :]
+  // (any order of the commutative operands, converts anywhere), followed by
+  // a bf16 result.  The packing and group layout are the quantized formats
+  // of mk_kernels.h.
+
+  static int64_t prod(const std::vector<int64_t>& d, size_t a, size_t b) {
+    int64_t p = 1;
+    for (size_t i = a; i < b; ++i) p *= d[i];
+    return p;
+  }
+
+  // v [K, N] == src[k / g, n] (jnp.repeat(src, g, axis=0), which lowers to
+  // expand_dims / tile / reshape chains); returns src or -1.
+  int rep_rows(int v, int64_t K, int64_t N, int64_t g) const {
+    if (numel(v) != K * N || K / g <= 1 || N <= 1 || g <= 1) return -1;
+    const int u = peel_cvt(v);
+    const Op* b = def(u);
+    if (!b || b->name != "broadcast_in_dim" || !monotonic(b->dims) || numel(u) != K * N) return -1;
+    const int s = b->operands[0];
+    const std::vector<int64_t>& R = type(u).dims;
+    const std::vector<int64_t>& S = type(s).dims;
+    if (numel(s) * g != K * N || S.size() != b->dims.size()) return -1;
+    std::vector<char> bc(R.size(), 1);
+    for (size_t i = 0; i < S.size(); ++i) {
+      if (S[i] == R[b->dims[i]]) bc[b->dims[i]] = 0;
+      else if (S[i] != 1) return -1;
+    }
+    int first = -1, last = -1;
+    for (size_t j = 0; j < R.size(); ++j)
+      if (bc[j] && R[j] > 1) {
+        if (first < 0) first = (int)j;
+        last = (int)j;
+      }
+    if (first < 0) return -1;
+    for (int j = first; j <= last; ++j)
+      if (!bc[j] && R[j] != 1) return -1;
+    if (prod(R, 0, first) != K / g || prod(R, first, last + 1) != g || prod(R, last + 1, R.size()) != N) return -1;
+    return peel_cvt(s);
+  }
+
+  // v [K, N] == nibble (k % 2) of P[k / 2, n], low nibble first
+  // (jnp.stack([P & 15, P >> 4], axis=1).reshape(K, N)); returns P or -1.
+  int interleave_src(int v, int64_t K, int64_t N) const {
+    if (numel(v) != K * N) return -1;
+    const int u = peel_cvt(v);
+    const Op* c = def(u);
+    if (!c || c->name != "concatenate" || c->operands.size() != 2 || numel(u) != K * N) return -1;
+    const std::vector<int64_t>& R = type(u).dims;
+    if (c->dim < 0 || c->dim >= (int64_t)R.size() || R[c->dim] != 2) return -1;
+    if (prod(R, 0, c->dim) != K / 2 || prod(R, c->dim + 1, R.size()) != N) return -1;
+    const int lo = peel_cvt(c->operands[0]), hi = peel_cvt(c->operands[1]);
+    const int p_lo = nibble_src(lo, false), p_hi = nibble_src(hi, true);
+    if (p_lo < 0 || p_lo != p_hi) return -1;
+    if (type(p_lo).dtype != DT_U8 || numel(p_lo) != (K / 2) * N) return -1;
+    return p_lo;
+  }
+  int nibble_src(int v, bool high) const {
+    v = peel_view(v);
+    const Op* op = def(v);
+    if (!op || op->operands.size() != 2) return -1;
+    int a = op->operands[0], b = op->operands[1];
+    if (op->name == "and") {
+      if (!splat_is(b, 15) && splat_is(a, 15)) std::swap(a, b);
+      if (!splat_is(b, 15)) return -1;
+      if (!high) return peel_view(a);
+      return shr4_src(a);
+    }
+    if (high) return shr4_src(v);
+    return -1;
+  }
+  int shr4_src(int v) const {
+    v = peel_view(v);
+    const Op* op = def(v);
+    if (!op || op->name != "shift_right_logical" || op->operands.size() != 2 || !splat_is(op->operands[1], 4))
+      return -1;
+    return peel_view(op->operands[0]);
+  }
+
+  bool try_qmm(int v, int* out) {
+    const Op* top = def(v);
+    int dv = v;
+    if (top->name == "convert") {
+      dv = top->operands[0];
+      if (type(v).dtype != DT_BF16 || !is(dv, "dot_general")) return false;
+    } else if (type(v).dtype != DT_BF16) {
+      return false;
+    }
+    const Op* dot = def(dv);
+    if (!dot || dot->name != "dot_general") return false;
+    DotShape d;
+    if (!dot_shape(*dot, &d) || d.batch != 1 || type(dot->operands[1]).dims.size() != 2) return false;
+    const int x = peel_cvt(dot->operands[0]);
+    if (type(x).dtype != DT_BF16 || numel(x) != d.M * d.K || numel(v) != d.M * d.N) return false;
+    const int w = peel_cvt(dot->operands[1]);
+    const Op* mul = def(w);
+    if (!mul || mul->name != "multiply") return false;
+    const int64_t K = d.K, N = d.N, M = d.M;
+    for (int order = 0; order < 2; ++order) {
+      const int f0 = mul->operands[order], f1 = mul->operands[1 - order];
+      // int4: f0 = (q - z), f1 = repeat(s)
+      const int sub = peel_cvt(f0);
+      if (K % 64 == 0 && is(sub, "subtract")) {
+        const int s = rep_rows(f1, K, N, 64);
+        const int z = rep_rows(def(sub)->operands[1], K, N, 64);
+        const int p = interleave_src(def(sub)->operands[0], K, N);
+        if (s >= 0 && z >= 0 && p >= 0 && type(s).dtype == DT_BF16 && type(z).dtype == DT_U8) {
+          const int64_t ws = mk_qmatmul_workspace_bytes(MK_QFMT_INT4_G64, M, K, N);
+          if (ws < 0) return false;
+          Step st;
+          st.kind = ST_QMM_INT4;
+          st.dt = MK_DT_BF16;
+          st.in = {need(x), need(p), need(s), need(z)};
+          st.M = M;
+          st.K = K;
+          st.N = N;
+          st.out = temp_for(v);
+          plan_.workspace_bytes = std::max(plan_.workspace_bytes, ws);
+          st.desc = "int4_g64_matmul M=" + std::to_string(M) + " K=" + std::to_string(K) + " N=" +
+                    std::to_string(N) + " -> bf16";
+          plan_.steps.push_back(st);
+          *out = st.out;
+          return true;
+        }
+      }
+      // int8: f0 = W, f1 = s[None, :]
+      const int wq = peel_cvt(f0);
+      if (type(wq).dtype == DT_S8 && type(wq).dims == std::vector<int64_t>{K, N}) {
+        const int sc = col_src(f1, N);
+        if (sc < 0) continue;
+        const int s = peel_cvt(sc);
+        if (type(s).dtype != DT_F32 || numel(s) != N) continue;
+        const int64_t ws = mk_qmatmul_workspace_bytes(MK_QFMT_INT8_PC, M, K, N);
+        if (ws < 0) return false;
+        Step st;
+        st.kind = ST_QMM_INT8;
+        st.dt = MK_DT_BF16;
+        st.in = {need(x), need(wq), need(s)};
+        st.M = M;
+        st.K = K;
+        st.N = N;
+        st.out = temp_for(v);
+        plan_.workspace_bytes = std::max(plan_.workspace_bytes, ws);
+        st.desc = "int8_pc_matmul M=" + std::to_string(M) + " K=" + std::to_string(K) + " N=" + std::to_string(N) +
+                  " -> bf16";
+        plan_.steps.push_back(st);
+        *out = st.out;
+        return true;
+      }
+    }
+    return false;
+  }
+
+  // ---- row patterns ----------------------------------------------------------------
+  // jax.nn.softmax: exp(x - max(x)) / sum(exp(x - max(x))) over the last axis;
+  // bf16 sums may be upcast to f32 and back (jnp.sum).
+  bool try_softmax(int v, int* out) {
+    const Op* div = def(v);
+    const int dt = type(v).dtype;
+    if (mk_dt(dt) < 0 || div->operands.size() != 2) return false;
+    const int64_t C = last_dim(v);
+    const int e = div->operands[0];
+    int s = row_src(div->operands[1], C);
+    if (s < 0) return false;
+    s = peel_cvt(s);
+    const int ein = reduce_last_input(s, "add");
+    if (ein < 0 || peel_cvt(ein) != peel_view(e)) return false;
+    const int ev = peel_view(e);
+    if (!is(ev, "exponential") || type(ev).dtype != dt) return false;
+    const int dsub = peel_view(def(ev)->operands[0]);
+    if (!is(dsub, "subtract")) return false;
+    const int x = peel_view(def(dsub)->operands[0]);
+    int m = row_src(def(dsub)->operands[1], C);
+    if (m < 0) return false;
+    m = peel_view(m);
+    if (is(m, "maximum")) {  // jnp.max(..., initial=-inf)
+      const Op* mx = def(m);
+      if (splat_is(mx->operands[1], -INFINITY)) m = peel_view(mx->operands[0]);
+      else if (splat_is(mx->operands[0], -INFINITY)) m = peel_view(mx->operands[1]);
+      else return false;
+    }
+    const int xm = reduce_last_input(m, "maximum");
+    if (xm < 0 || peel_view(xm) != x || type(x).dtype != dt || numel(x) != numel(v)) return false;
+    Step st;
+    st.kind = ST_SOFTMAX;
+    st.dt = mk_dt(dt);
+    st.in = {need(x)};
+    st.cols = C;
+    st.rows = numel(v) / C;
+    st.out = temp_for(v);
+    st.desc = "softmax rows=" + std::to_string(st.rows) + " cols=" + std::to_string(C) + " " + dtype_name(dt);
+    plan_.steps.push_back(st);
+    *out = st.out;
+    return true;
+  }
+
+  // x * rsqrt(mean(x*x, -1, keepdims) + eps) * g, any association of the
+  // three factors.
+  bool try_rmsnorm(int v, int* out) {
+    const int dt = type(v).dtype;
+    if (mk_dt(dt) < 0) return false;
+    const int64_t C = last_dim(v);
+    std::vector<int> fac;
+    std::function<void(int, int)> flat = [&](int u, int depth) {
+      u = peel_view(u);
+      if (depth < 2 && is(u, "multiply") && type(u).dtype == dt && numel(u) == numel(v)) {
+        flat(def(u)->operands[0], depth + 1);
+        flat(def(u)->operands[1], depth + 1);
+      } else {
+        fac.push_back(u);
+      }
+    };
+    flat(def(v)->operands[0], 1);
+    flat(def(v)->operands[1], 1);
+    if (fac.size() != 3) return false;
+    int x = -1, g = -1, r = -1;
+    for (int u : fac) {
+      int t;
+      if (g < 0 && (t = col_src(u, C)) >= 0 && numel(peel_view(t)) == C && numel(u) != C) {
+        g = peel_view(t);
+        continue;
+      }
+      if (r < 0 && (t = row_src(u, C)) >= 0 && numel(u) != numel(t)) {
+        r = t;
+        continue;
+      }
+      if (x < 0 && numel(u) == numel(v)) {
+        x = u;
+        continue;
+      }
+      return false;
+    }
+    if (x < 0 || g < 0 || r < 0 || type(x).dtype != dt || type(g).dtype != dt) return false;
+    // r = rsqrt(ms + eps)
+    int rs = peel_cvt(r);
+    if (!is(rs, "rsqrt")) return false;
+    int add = peel_cvt(def(rs)->operands[0]);
+    if (!is(add, "add")) return false;
+    double eps;
+    int ms;
+    if (splat(def(add)->operands[1], &eps)) ms = def(add)->operands[0];
+    else if (splat(def(add)->operands[0], &eps)) ms = def(add)->operands[1];
+    else return false;
+    ms = peel_cvt(ms);
+    // ms = sum / C or sum * (1/C)
+    int sum;
+    double c;
+    const Op* mo = def(ms);
+    if (!mo || mo->operands.size() != 2) return false;
+    if (mo->name == "divide" && splat(mo->operands[1], &c) && c == (double)C) sum = mo->operands[0];
+    else if (mo->name == "multiply" && splat(mo->operands[1], &c) && fabs(c * C - 1.0) < 1e-6) sum = mo->operands[0];
+    else if (mo->name == "multiply" && splat(mo->operands[0], &c) && fabs(c * C - 1.0) < 1e-6) sum = mo->operands[1];
+    else return false;
+    const int sq_in = reduce_last_input(peel_view(sum), "add");
+    if (sq_in < 0) return false;
+    const int sq = peel_cvt(sq_in);
+    if (!is(sq, "multiply")) return false;
+    const int xv = peel_cvt(x);
+    if (peel_cvt(def(sq)->operands[0]) != xv || peel_cvt(def(sq)->operands[1]) != xv) return false;
+    Step st;
+    st.kind = ST_RMSNORM;
+    st.dt = mk_dt(dt);
+    st.in = {need(x), need(g)};
+    st.cols = C;
+    st.rows = numel(v) / C;
+    st.eps = (float)eps;
+    st.out = temp_for(v);
+    std::ostringstream ds;
+    ds << "rmsnorm rows=" << st.rows << " cols=" << C << " eps=" << eps << " " << dtype_name(dt);
+    st.desc = ds.str();
+    plan_.steps.push_back(st);
+    *out = st.out;
+    return true;
+  }
+
+  // jnp.argmax: a two-operand reduce over (x, iota) along the last axis.
+  bool try_argmax(int v, const Op& op, int* out) {
+    if (op.operands.size() != 4 || op.reduce_body != "argmax" || op.results.size() != 2) return false;
+    if (v != op.results[1]) {
+      reject(&op, "value result of an argmax reduce");
+      return false;
+    }
+    const int x = op.operands[0], idx = op.operands[1];
+    const int rank = (int)type(x).dims.size();
+    const int dt = type(x).dtype;
+    const int id = peel_view(idx);
+    if (mk_dt(dt) < 0 || rank == 0 || op.dims.size() != 1 || op.dims[0] != rank - 1) return false;
+    if (!is(id, "iota") || def(id)->dim != rank - 1 || type(id).dims != type(x).dims) return false;
+    if (type(v).dtype != DT_S32 || numel(v) * last_dim(x) != numel(x)) return false;
+    double i0, x0;
+    if (!splat(op.operands[3], &i0) || i0 != 0.0) return false;
+    if (!splat(op.operands[2], &x0) || !(x0 == -INFINITY)) return false;
+    Step st;
+    st.kind = ST_ARGMAX;
+    st.dt = mk_dt(dt);
+    st.in = {need(x)};
+    st.cols = last_dim(x);
+    st.rows = numel(x) / st.cols;
+    st.out = temp_for(v);
+    st.desc = "argmax rows=" + std::to_string(st.rows) + " cols=" + std::to_string(st.cols) + " " + dtype_name(dt) +
+              " -> i32";
+    plan_.steps.push_back(st);
+    *out = st.out;
+    return true;
+  }
+
+  // Last-axis sum/max; bf16 sums written as convert(reduce_f32(convert(x)))
+  // map to the bf16 kernel (f32 accumulation, one rounding).
+  bool try_reduce(int v, int* out) {
+    int r = v, x;
+    int dt = type(v).dtype;
+    if (is(v, "convert")) {
+      r = def(v)->operands[0];
+      if (!is(r, "reduce") || dt != DT_BF16 || type(r).dtype != DT_F32) return false;
+    }
+    const char* body = nullptr;
+    int op = 0;
+    if ((x = reduce_last_input(r, "add")) >= 0) {
+      body = "sum";
+      op = MK_REDUCE_SUM;
+    } else if ((x = reduce_last_input(r, "maximum")) >= 0) {
+      body = "max";
+      op = MK_REDUCE_MAX;
+    } else {
+      return false;
+    }
+    if (r != v) {
+      x = peel_cvt(x);
+      if (type(x).dtype != DT_BF16 || op != MK_REDUCE_SUM) return false;
+    }
+    if (mk_dt(dt) < 0 || type(x).dtype != dt || numel(v) * last_dim(x) != numel(x)) return false;
+    Step st;
+    st.kind = ST_REDUCE;
+    st.dt = mk_dt(dt);
+    st.reduce_op = op;
+    st.in = {need(x)};
+    st.cols = last_dim(x);
+    st.rows = st.cols ? numel(x) / st.cols : 0;
+    st.out = temp_for(v);
+    st.desc = std::string("reduce_") + body + " rows=" + std::to_string(st.rows) + " cols=" +
+              std::to_string(st.cols) + " " + dtype_name(dt);
+    plan_.steps.push_back(st);
+    *out = st.out;
+    return true;
+  }
+
+  // ---- elementwise programs ------------------------------------------------------------
+  bool is_elementwise(int v) const {
+    const Op* op = def(v);
+    if (!op) return false;
+    if (op->name == "select" || op->name == "clamp") return true;
+    if (op->name == "broadcast_in_dim") return !op->operands.empty() && numel(op->operands[0]) == 1;
+    if (op->name == "constant") return op->const_splat;
+    return unary_ops().count(op->name) || binary_ops().count(op->name);
+  }
+
+  struct EwCtx {
+    int dt;        // DT_F32 or DT_BF16 (program dtype)
+    int64_t n;     // element count
+    std::vector<mk_ew_instr> prog;
+    std::map<int, int> reg;  // value -> virtual register (instruction index)
+    std::vector<int> loads;  // value ids of inputs
+    std::vector<int64_t> load_numel;
+    std::set<int> force;     // values to load instead of inlining
+    std::string fail;        // reason the value cannot be expressed
+    int split_hint = -1;     // largest inlined subexpression (split candidate)
+    int split_size = 0;
+  };
+
+  // Unused operand fields are 0 (the kernel ignores them).
+  int ew_emit(EwCtx& c, int op, int a = 0, int b = 0, int cc = 0, float imm = 0.f) {
+    mk_ew_instr in{};
+    in.op = op;
+    in.dst = (int)c.prog.size();
+    in.a = a;
+    in.b = b;
+    in.c = cc;
+    in.imm = imm;
+    c.prog.push_back(in);
+    return in.dst;
+  }
+
+  int ew_load(EwCtx& c, int u) {
+    const int64_t ne = numel(u);
+    if (ne != c.n && ne != 1) {
+      c.fail = "broadcast of a non-scalar " + type(u).str() + " into an elementwise op";
+      return -1;
+    }
+    if (type(u).dtype != c.dt) {
+      c.fail = std::string("elementwise input of type ") + dtype_name(type(u).dtype) + " in a " +
+               dtype_name(c.dt) + " program";
+      return -1;
+    }
+    for (size_t i = 0; i < c.loads.size(); ++i)
+      if (c.loads[i] == u) return ew_emit(c, MK_EW_LOAD, (int)i);
+    c.loads.push_back(u);
+    c.load_numel.push_back(ne);
+    return ew_emit(c, MK_EW_LOAD, (int)c.loads.size() - 1);
+  }
+
+  // Returns the virtual register holding u; `size` accumulates the number
+  // of instructions generated for u's subtree.
+  int ew_value(EwCtx& c, int u, bool root, int* size) {
+    auto it = c.reg.find(u);
+    if (it != c.reg.end()) return it->second;
+    const int before = (int)c.prog.size();
+    int r = ew_value_uncached(c, u, root);
+    if (r < 0) return -1;
+    const int sz = (int)c.prog.size() - before;
+    *size += sz;
+    if (!root && sz > c.split_size && is_elementwise(u) && numel(u) == c.n && type(u).dtype == c.dt &&
+        !c.force.count(u)) {
+      c.split_size = sz;
+      c.split_hint = u;
+    }
+    c.reg[u] = r;
+    return r;
+  }
+
+  int ew_value_uncached(EwCtx& c, int u, bool root) {
+    double k;
+    const TensorType& t = type(u);
+    if (splat(u, &k) && is_float(t.dtype)) return ew_emit(c, MK_EW_CONST, 0, 0, 0, (float)k);
+    if (splat(u, &k) && t.dtype == DT_PRED) return ew_emit(c, MK_EW_CONST, 0, 0, 0, k != 0 ? 1.f : 0.f);
+    const int vs = view_src(u);
+    if (vs >= 0 && !c.force.count(u)) {
+      int dummy = 0;
+      return ew_value(c, vs, false, &dummy);
+    }
+    const Op* op = def(u);
+    if (!op || (!root && c.force.count(u)) || !is_elementwise(u)) return ew_load(c, u);
+    if (op->name == "broadcast_in_dim") return ew_load(c, op->operands[0]);  // scalar broadcast
+    // Per-node type rules: bf16 programs hold only bf16 (and predicate)
+    // values; f32 programs round bf16-typed nodes explicitly.
+    const int dt = t.dtype;
+    if (dt != DT_PRED && dt != DT_F32 && dt != DT_BF16) {
+      c.fail = std::string("elementwise ") + op->name + " on " + dtype_name(dt);
+      return -1;
+    }
+    if (c.dt == DT_BF16 && dt == DT_F32) {
+      c.fail = std::string("f32 ") + op->name + " inside a bf16 elementwise chain";
+      return -1;
+    }
+    std::vector<int> r;
+    int sz = 0;
+    for (int o : op->operands) {
+      if (op->name == "compare" && type(o).dtype != DT_F32 && type(o).dtype != DT_BF16) {
+        c.fail = std::string("compare on ") + dtype_name(type(o).dtype);
+        return -1;
+      }
+      const int x = ew_value(c, o, false, &sz);
+      if (x < 0) return -1;
+      r.push_back(x);
+    }
+    int res = -1;
+    const std::string& n = op->name;
+    static const std::map<std::string, int> un = {
+        {"negate", MK_EW_NEG}, {"abs", MK_EW_ABS}, {"exponential", MK_EW_EXP}, {"log", MK_EW_LOG},
+        {"log_plus_one", MK_EW_LOG1P}, {"exponential_minus_one", MK_EW_EXPM1}, {"tanh", MK_EW_TANH},
+        {"rsqrt", MK_EW_RSQRT}, {"sqrt", MK_EW_SQRT}, {"logistic", MK_EW_LOGISTIC}, {"floor", MK_EW_FLOOR},
+        {"ceil", MK_EW_CEIL}};
+    static const std::map<std::string, int> bin = {
+        {"add", MK_EW_ADD}, {"subtract", MK_EW_SUB}, {"multiply", MK_EW_MUL}, {"divide", MK_EW_DIV},
+        {"maximum", MK_EW_MAX}, {"minimum", MK_EW_MIN}, {"power", MK_EW_POW}};
+    static const std::map<std::string, int> cmp = {{"EQ", MK_EW_CMP_EQ}, {"NE", MK_EW_CMP_NE},
+                                                    {"LT", MK_EW_CMP_LT}, {"LE", MK_EW_CMP_LE},
+                                                    {"GT", MK_EW_CMP_GT}, {"GE", MK_EW_CMP_GE}};
+    if (un.count(n)) {
+      if (dt == DT_PRED) {
+        c.fail = n + " on a predicate";
+        return -1;
+      }
+      res = ew_emit(c, un.at(n), r[0]);
+    } else if (bin.count(n)) {
+      if (dt == DT_PRED) {
+        c.fail = n + " on a predicate";
+        return -1;
+      }
+      res = ew_emit(c, bin.at(n), r[0], r[1]);
+    } else if (n == "compare") {
+      if (!cmp.count(op->compare_dir)) {
+        c.fail = "compare direction '" + op->compare_dir + "'";
+        return -1;
+      }
+      res = ew_emit(c, cmp.at(op->compare_dir), r[0], r[1]);
+    } else if (n == "select") {
+      res = ew_emit(c, MK_EW_SELECT, r[0], r[1], r[2]);
+    } else if (n == "clamp") {  // clamp(lo, x, hi)
+      const int m = ew_emit(c, MK_EW_MAX, r[1], r[0]);
+      res = ew_emit(c, MK_EW_MIN, m, r[2]);
+    } else if (n == "and" || n == "or") {
+      if (dt != DT_PRED) {
+        c.fail = n + " on " + dtype_name(dt);
+        return -1;
+      }
+      res = ew_emit(c, n == "and" ? MK_EW_MUL : MK_EW_MAX, r[0], r[1]);
+    } else if (n == "not") {
+      if (dt != DT_PRED) {
+        c.fail = "not on " + std::string(dtype_name(dt));
+        return -1;
+      }
+      const int one = ew_emit(c, MK_EW_CONST, 0, 0, 0, 1.f);
+      res = ew_emit(c, MK_EW_SUB, one, r[0]);
+    } else if (n == "convert") {
+      const int st = type(op->operands[0]).dtype;
+      if (dt == DT_PRED) {
+        if (!is_float(st)) {
+          c.fail = std::string("convert ") + dtype_name(st) + " -> i1";
+          return -1;
+        }
+        const int z = ew_emit(c, MK_EW_CONST, 0, 0, 0, 0.f);
+        res = ew_emit(c, MK_EW_CMP_NE, r[0], z);
+      } else if (st == DT_PRED || st == DT_F32 || st == DT_BF16) {
+        res = r[0];
+        if (dt == DT_BF16 && st == DT_F32 && c.dt == DT_F32) res = ew_emit(c, MK_EW_ROUND_BF16, r[0]);
+        return res;
+      } else {
+        c.fail = std::string("convert ") + dtype_name(st) + " -> " + dtype_name(dt);
+        return -1;
+      }
+    } else {
+      c.fail = "elementwise " + n;
+      return -1;
+    }
+    // bf16-typed results inside an f32 program round like XLA's bf16 ops.
+    if (c.dt == DT_F32 && dt == DT_BF16) res = ew_emit(c, MK_EW_ROUND_BF16, res);
+    return res;
+  }
+
+  // Number of register operands an instruction reads.
+  static int n_src(int op) {
+    if (op == MK_EW_LOAD || op == MK_EW_CONST) return 0;
+    if (op == MK_EW_SELECT) return 3;
+    if ((op >= MK_EW_ADD && op <= MK_EW_POW) || (op >= MK_EW_CMP_EQ && op <= MK_EW_CMP_GE)) return 2;
+    return 1;
+  }
+
+  // Virtual registers -> the kernel's 12 slots (linear scan; a register is
+  // freed after its last read).  Returns false when more than 12 are live.
+  static bool assign_slots(std::vector<mk_ew_instr>& prog, int root, int* out_slot) {
+    const int n = (int)prog.size();
+    std::vector<int> last(n, -1);
+    for (int i = 0; i < n; ++i) {
+      const mk_ew_instr& in = prog[i];
+      const int src[3] = {in.a, in.b, in.c};
+      for (int k = 0; k < n_src(in.op); ++k) last[src[k]] = i;
+    }
+    last[root] = n;
+    std::vector<int> phys(n, -1);
+    std::vector<int> owner(12, -1);
+    for (int i = 0; i < n; ++i) {
+      mk_ew_instr& in = prog[i];
+      const int ns = n_src(in.op);
+      int src[3] = {in.a, in.b, in.c};
+      int mapped[3] = {0, 0, 0};
+      for (int k = 0; k < ns; ++k) mapped[k] = phys[src[k]];
+      for (int k = 0; k < ns; ++k)
+        if (last[src[k]] == i) owner[phys[src[k]]] = -1;
+      int p = -1;
+      for (int k = 0; k < 12 && p < 0; ++k)
+        if (owner[k] < 0) p = k;
+      if (p < 0) return false;
+      owner[p] = i;
+      phys[i] = p;
+      if (last[i] < 0) owner[p] = -1;  // dead result
+      in.dst = p;
+      if (ns > 0) {
+        in.a = mapped[0];
+        in.b = mapped[1];
+        in.c = mapped[2];
+      }
+    }
+    *out_slot = phys[root];
+    return true;
+  }
+
+  int ew_root(int v) {
+    const int dt = type(v).dtype;
+    if (dt != DT_F32 && dt != DT_BF16) {
+      reject(def(v), std::string("elementwise result of type ") + dtype_name(dt));
+      return dummy(v);
+    }
+    std::set<int> force;
+    for (int attempt = 0; attempt < 24; ++attempt) {
+      EwCtx c;
+      c.dt = dt;
+      c.n = numel(v);
+      c.force = force;
+      int sz = 0;
+      const int r = ew_value(c, v, true, &sz);
+      if (r < 0) {
+        reject(def(v), c.fail);
+        return dummy(v);
+      }
+      std::vector<mk_ew_instr> prog = c.prog;
+      int out_slot = 0;
+      const bool fits = c.loads.size() <= 4 && prog.size() <= 32 && assign_slots(prog, r, &out_slot);
+      if (!fits) {
+        if (c.split_hint < 0) {
+          reject(def(v), "elementwise program does not fit the kernel's limits");
+          return dummy(v);
+        }
+        force.insert(c.split_hint);
+        continue;
+      }
+      Step st;
+      st.kind = ST_EW;
+      st.dt = mk_dt(dt);
+      for (int u : c.loads) st.in.push_back(need(u));
+      st.in_numel = c.load_numel;
+      st.prog = prog;
+      st.prog_out = out_slot;
+      st.n = c.n;
+      st.out = temp_for(v);
+      st.desc = "elementwise " + std::to_string(prog.size()) + " instr, " + std::to_string(c.loads.size()) +
+                " inputs, n=" + std::to_string(c.n) + " " + dtype_name(dt);
+      plan_.steps.push_back(st);
+      return st.out;
+    }
+    reject(def(v), "elementwise program does not fit the kernel's limits");
+    return dummy(v);
+  }
+};
+
+}  // namespace
+
+std::string Plan::describe() const {
+  std::string s;
+  for (const Step& st : steps) s += st.desc + "\n";
+  return s;
+}
+
+Plan build_plan(const Function& fn) { return Planner(fn).run(); }
+
+}  // namespace mkrt

@@ -1,0 +1,81 @@
+// Execution plan: the parsed StableHLO function mapped onto the hot-path
+// kernels (mk_kernels.h).  The reference keeps the same split between a
+// compile-time support check and a plan of native steps built once and then
+// replayed per call (ExecutionPlan / NativeStep,
+// src/pjrt_plugin/core/mps_executable.mm:97-287; BuildExecutionPlan :7627).
+#pragma once
+
+#include <stdint.h>
+
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "mk_kernels.h"
+#include "shlo.h"
+
+namespace mkrt {
+
+enum SlotKind { SLOT_ARG = 0, SLOT_TEMP = 1, SLOT_CONST = 2 };
+
+// A device buffer the plan reads or writes.  Arguments are the caller's
+// buffers; temporaries are allocated per execute; constants are uploaded once.
+struct Slot {
+  SlotKind kind = SLOT_TEMP;
+  int64_t bytes = 0;
+  int arg_index = -1;
+  std::vector<uint8_t> data;  // SLOT_CONST contents
+};
+
+enum StepKind {
+  ST_GEMM_BF16,
+  ST_GEMM_F32,
+  ST_QMM_INT4,
+  ST_QMM_INT8,
+  ST_SOFTMAX,
+  ST_RMSNORM,
+  ST_ARGMAX,
+  ST_REDUCE,
+  ST_EW,
+  ST_COPY,
+  ST_ZERO
+};
+
+struct Step {
+  StepKind kind = ST_COPY;
+  int dt = MK_DT_F32;     // MK_DT_* of the kernel
+  std::vector<int> in;    // slot ids
+  int out = -1;           // slot id
+  int64_t batch = 1, M = 0, N = 0, K = 0;
+  int out_f32 = 0;
+  int64_t rows = 0, cols = 0;
+  float eps = 0.f;
+  int reduce_op = MK_REDUCE_SUM;
+  std::vector<mk_ew_instr> prog;
+  std::vector<int64_t> in_numel;
+  int prog_out = 0;
+  int64_t n = 0;      // elementwise element count
+  int64_t bytes = 0;  // copy / zero size
+  std::string desc;
+};
+
+struct Plan {
+  std::vector<Slot> slots;
+  std::vector<Step> steps;
+  std::vector<int> in_slot;   // per argument
+  std::vector<int> out_slot;  // per result (a TEMP slot written by a step)
+  std::vector<TensorType> in_type, out_type;
+  int64_t workspace_bytes = 0;  // shared by the dequant-matmul steps
+  std::string describe() const;
+};
+
+struct PlanError : std::runtime_error {
+  int code;  // MKRT_* error code
+  PlanError(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+// Maps every value the function returns onto kernel steps.  Throws
+// PlanError(UNIMPLEMENTED) listing every op that has no kernel route.
+Plan build_plan(const Function& fn);
+
+}  // namespace mkrt

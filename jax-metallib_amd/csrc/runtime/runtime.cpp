@@ -1,0 +1,706 @@
+// Runtime behind include/mk_runtime.h: one HIP device, one stream, a caching
+// device allocator, completion events fired by a completion thread, and
+// executables that run a kernel plan (planner.h).
+//
+// Ordering model.  Every device operation of a client (host<->device copies,
+// kernel steps, copies between buffers) is issued on the client's single
+// stream, so stream order alone makes buffer reuse safe: memory returned to
+// the allocator can be handed out again at once, since any later user is
+// queued behind every earlier reader.  Host-visible completion is tracked
+// with events: each execute records a HIP event, and the completion thread
+// waits for those in order and marks the matching mkrt_event ready,
+// running its callbacks there (the reference's CompletionEvent fired from
+// Metal's completion handler, core/completion_event.h:32-229).
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <condition_variable>
+#include <deque>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "mk_kernels.h"
+#include "mk_runtime.h"
+#include "planner.h"
+#include "shlo.h"
+
+struct mkrt_error {
+  int code;
+  std::string message;
+};
+
+namespace {
+
+mkrt_error* make_error(int code, const char* fmt, ...) {
+  char buf[2048];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  return new mkrt_error{code, buf};
+}
+
+mkrt_error* copy_error(const mkrt_error* e) { return e ? new mkrt_error{e->code, e->message} : nullptr; }
+
+// Shared state of one completion: ready flag, optional error, callbacks.
+struct EventState {
+  std::mutex mu;
+  std::condition_variable cv;
+  bool ready = false;
+  int code = MKRT_OK;
+  std::string message;
+  std::vector<std::pair<mkrt_event_callback, void*>> callbacks;
+
+  void set(int c, const std::string& m) {
+    std::vector<std::pair<mkrt_event_callback, void*>> cbs;
+    {
+      std::lock_guard<std::mutex> g(mu);
+      if (ready) return;
+      ready = true;
+      code = c;
+      message = m;
+      cbs.swap(callbacks);
+    }
+    cv.notify_all();
+    for (auto& cb : cbs) cb.first(c == MKRT_OK ? nullptr : new mkrt_error{c, m}, cb.second);
+  }
+};
+
+std::shared_ptr<EventState> ready_state(int code = MKRT_OK, const std::string& msg = std::string()) {
+  auto s = std::make_shared<EventState>();
+  s->ready = true;
+  s->code = code;
+  s->message = msg;
+  return s;
+}
+
+int64_t default_timeout_ms() {
+  const char* v = getenv("MK_COMPLETION_TIMEOUT_MS");
+  if (v && *v) {
+    const long long t = atoll(v);
+    if (t > 0) return t;
+  }
+  return 30000;
+}
+
+// Caching allocator: freed blocks are kept per rounded size and handed out
+// again in stream order.  Sizes round to 512 B below 1 MiB and to 2 MiB above.
+class Allocator {
+ public:
+  ~Allocator() { release_cached(); }
+
+  static size_t round(size_t n) {
+    if (n == 0) return 0;
+    if (n < (1u << 20)) return (n + 511) & ~(size_t)511;
+    return (n + (2u << 20) - 1) & ~(((size_t)2 << 20) - 1);
+  }
+
+  hipError_t alloc(size_t bytes, void** out) {
+    *out = nullptr;
+    const size_t r = round(bytes);
+    if (r == 0) return hipSuccess;
+    {
+      std::lock_guard<std::mutex> g(mu_);
+      auto it = free_.find(r);
+      if (it != free_.end()) {
+        *out = it->second;
+        free_.erase(it);
+        cached_ -= r;
+        in_use_ += r;
+        sizes_[*out] = r;
+        return hipSuccess;
+      }
+    }
+    hipError_t e = hipMalloc(out, r);
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) {
+      (void)hipGetLastError();
+      release_cached();
+      e = hipMalloc(out, r);
+    }
+    if (e != hipSuccess) {
+      *out = nullptr;
+      return e;
+    }
+    std::lock_guard<std::mutex> g(mu_);
+    sizes_[*out] = r;
+    in_use_ += r;
+    return hipSuccess;
+  }
+
+  void free(void* p) {
+    if (!p) return;
+    std::lock_guard<std::mutex> g(mu_);
+    auto it = sizes_.find(p);
+    if (it == sizes_.end()) return;
+    const size_t r = it->second;
+    sizes_.erase(it);
+    in_use_ -= r;
+    cached_ += r;
+    free_.emplace(r, p);
+  }
+
+  void release_cached() {
+    std::multimap<size_t, void*> blocks;
+    {
+      std::lock_guard<std::mutex> g(mu_);
+      blocks.swap(free_);
+      cached_ = 0;
+    }
+    for (auto& b : blocks) (void)hipFree(b.second);
+  }
+
+  int64_t in_use() {
+    std::lock_guard<std::mutex> g(mu_);
+    return (int64_t)in_use_;
+  }
+
+ private:
+  std::mutex mu_;
+  std::multimap<size_t, void*> free_;
+  std::map<void*, size_t> sizes_;
+  size_t in_use_ = 0, cached_ = 0;
+};
+
+}  // namespace
+
+struct mkrt_client {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  Allocator alloc;
+  std::mutex stream_mu;  // serialises multi-call sequences on the stream
+
+  // Completion thread.
+  std::mutex q_mu;
+  std::condition_variable q_cv;
+  std::deque<std::pair<hipEvent_t, std::shared_ptr<EventState>>> queue;
+  bool stopping = false;
+  std::thread worker;
+  std::mutex ev_pool_mu;
+  std::vector<hipEvent_t> ev_pool;
+
+  hipEvent_t get_event() {
+    {
+      std::lock_guard<std::mutex> g(ev_pool_mu);
+      if (!ev_pool.empty()) {
+        hipEvent_t e = ev_pool.back();
+        ev_pool.pop_back();
+        return e;
+      }
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreateWithFlags(&e, hipEventDisableTiming | hipEventBlockingSync) != hipSuccess) return nullptr;
+    return e;
+  }
+
+  void completion_loop() {
+    (void)hipSetDevice(device);
+    while (true) {
+      std::pair<hipEvent_t, std::shared_ptr<EventState>> item;
+      {
+        std::unique_lock<std::mutex> l(q_mu);
+        q_cv.wait(l, [&] { return stopping || !queue.empty(); });
+        if (queue.empty()) return;
+        item = queue.front();
+        queue.pop_front();
+      }
+      const hipError_t e = hipEventSynchronize(item.first);
+      {
+        std::lock_guard<std::mutex> g(ev_pool_mu);
+        ev_pool.push_back(item.first);
+      }
+      if (e == hipSuccess) item.second->set(MKRT_OK, std::string());
+      else item.second->set(MKRT_INTERNAL, std::string("device execution failed: ") + hipGetErrorString(e));
+    }
+  }
+
+  // Marks `st` ready once everything issued so far on the stream has run.
+  hipError_t track(const std::shared_ptr<EventState>& st) {
+    hipEvent_t e = get_event();
+    if (!e) return hipErrorOutOfMemory;
+    hipError_t r = hipEventRecord(e, stream);
+    if (r != hipSuccess) {
+      std::lock_guard<std::mutex> g(ev_pool_mu);
+      ev_pool.push_back(e);
+      return r;
+    }
+    {
+      std::lock_guard<std::mutex> g(q_mu);
+      queue.emplace_back(e, st);
+    }
+    q_cv.notify_one();
+    return hipSuccess;
+  }
+};
+
+struct mkrt_buffer {
+  mkrt_client* client = nullptr;
+  int type = 0;
+  std::vector<int64_t> dims;
+  int64_t bytes = 0;
+  void* data = nullptr;
+  std::shared_ptr<EventState> ready;  // producer
+};
+
+struct mkrt_event {
+  std::shared_ptr<EventState> st;
+};
+
+struct mkrt_executable {
+  mkrt_client* client = nullptr;
+  mkrt::Function fn;
+  mkrt::Plan plan;
+  std::string plan_text;
+  std::mutex plan_mu;
+  std::atomic<bool> prepared{false};
+  std::vector<void*> const_mem;  // per slot, SLOT_CONST only
+  void* workspace = nullptr;
+};
+
+namespace {
+
+int64_t dims_numel(const int64_t* dims, int ndims) {
+  int64_t n = 1;
+  for (int i = 0; i < ndims; ++i) n *= dims[i];
+  return n;
+}
+
+mkrt_error* hip_error(const char* what, hipError_t e) {
+  return make_error(MKRT_INTERNAL, "%s: %s", what, hipGetErrorString(e));
+}
+
+mkrt_error* await_state(const std::shared_ptr<EventState>& st, int64_t timeout_ms) {
+  if (timeout_ms < 0) timeout_ms = default_timeout_ms();
+  std::unique_lock<std::mutex> l(st->mu);
+  if (!st->cv.wait_for(l, std::chrono::milliseconds(timeout_ms), [&] { return st->ready; }))
+    return make_error(MKRT_DEADLINE_EXCEEDED, "completion not signalled within %lld ms (MK_COMPLETION_TIMEOUT_MS)",
+                      (long long)timeout_ms);
+  if (st->code != MKRT_OK) return new mkrt_error{st->code, st->message};
+  return nullptr;
+}
+
+mkrt_buffer* new_buffer(mkrt_client* c, int type, const std::vector<int64_t>& dims, void* data, int64_t bytes,
+                        std::shared_ptr<EventState> ready) {
+  mkrt_buffer* b = new mkrt_buffer;
+  b->client = c;
+  b->type = type;
+  b->dims = dims;
+  b->bytes = bytes;
+  b->data = data;
+  b->ready = std::move(ready);
+  return b;
+}
+
+// First-execute preparation: constants uploaded, workspace allocated,
+// elementwise programs compiled (core/mps_executable.mm:9152 builds the
+// plan lazily under plan_mutex_, mps_executable.h:96-100).
+mkrt_error* prepare(mkrt_executable* x) {
+  if (x->prepared.load(std::memory_order_acquire)) return nullptr;
+  std::lock_guard<std::mutex> g(x->plan_mu);
+  if (x->prepared.load(std::memory_order_relaxed)) return nullptr;
+  mkrt_client* c = x->client;
+  x->const_mem.assign(x->plan.slots.size(), nullptr);
+  for (size_t i = 0; i < x->plan.slots.size(); ++i) {
+    const mkrt::Slot& s = x->plan.slots[i];
+    if (s.kind != mkrt::SLOT_CONST || s.bytes == 0) continue;
+    void* p = nullptr;
+    hipError_t e = c->alloc.alloc((size_t)s.bytes, &p);
+    if (e != hipSuccess) return hip_error("constant allocation", e);
+    x->const_mem[i] = p;
+    std::lock_guard<std::mutex> sg(c->stream_mu);
+    e = hipMemcpyAsync(p, s.data.data(), (size_t)s.bytes, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return hip_error("constant upload", e);
+  }
+  if (x->plan.workspace_bytes > 0) {
+    hipError_t e = c->alloc.alloc((size_t)x->plan.workspace_bytes, &x->workspace);
+    if (e != hipSuccess) return hip_error("workspace allocation", e);
+  }
+  for (const mkrt::Step& st : x->plan.steps) {
+    if (st.kind != mkrt::ST_EW) continue;
+    if (mk_elementwise_prepare(st.dt, st.prog.data(), (int)st.prog.size(), (int)st.in.size(), st.prog_out) != MK_OK)
+      return make_error(MKRT_INTERNAL, "elementwise program: %s", mk_last_error());
+  }
+  x->prepared.store(true, std::memory_order_release);
+  return nullptr;
+}
+
+int run_step(const mkrt::Step& st, const std::vector<void*>& mem, void* ws, int64_t ws_bytes, hipStream_t s) {
+  auto in = [&](int i) { return (const void*)mem[st.in[i]]; };
+  void* out = mem[st.out];
+  switch (st.kind) {
+    case mkrt::ST_GEMM_BF16:
+      return mk_gemm_bf16(in(0), in(1), out, st.batch, st.M, st.N, st.K, st.out_f32, s);
+    case mkrt::ST_GEMM_F32:
+      return mk_gemm_f32(in(0), in(1), out, st.batch, st.M, st.N, st.K, s);
+    case mkrt::ST_QMM_INT4:
+      return mk_int4g64_matmul_bf16(in(0), in(1), in(2), in(3), out, st.M, st.K, st.N, ws, ws_bytes, s);
+    case mkrt::ST_QMM_INT8:
+      return mk_int8pc_matmul_bf16(in(0), in(1), in(2), out, st.M, st.K, st.N, ws, ws_bytes, s);
+    case mkrt::ST_SOFTMAX:
+      return mk_softmax_lastdim(st.dt, in(0), out, st.rows, st.cols, s);
+    case mkrt::ST_RMSNORM:
+      return mk_rmsnorm_lastdim(st.dt, in(0), in(1), out, st.rows, st.cols, st.eps, s);
+    case mkrt::ST_ARGMAX:
+      return mk_argmax_lastdim(st.dt, in(0), out, st.rows, st.cols, s);
+    case mkrt::ST_REDUCE:
+      return mk_reduce_lastdim(st.dt, st.reduce_op, in(0), out, st.rows, st.cols, s);
+    case mkrt::ST_EW: {
+      std::vector<const void*> ins;
+      for (size_t i = 0; i < st.in.size(); ++i) ins.push_back(in((int)i));
+      return mk_elementwise(st.dt, st.prog.data(), (int)st.prog.size(), ins.data(), st.in_numel.data(),
+                            (int)ins.size(), st.prog_out, out, st.n, s);
+    }
+    case mkrt::ST_COPY:
+      if (st.bytes == 0) return MK_OK;
+      return hipMemcpyAsync(out, in(0), (size_t)st.bytes, hipMemcpyDeviceToDevice, s) == hipSuccess ? MK_OK
+                                                                                                     : MK_ELAUNCH;
+    case mkrt::ST_ZERO:
+      if (st.bytes == 0) return MK_OK;
+      return hipMemsetAsync(out, 0, (size_t)st.bytes, s) == hipSuccess ? MK_OK : MK_ELAUNCH;
+  }
+  return MK_EUNSUPPORTED;
+}
+
+}  // namespace
+
+extern "C" {
+
+void mkrt_error_destroy(mkrt_error* err) { delete err; }
+const char* mkrt_error_message(const mkrt_error* err) { return err ? err->message.c_str() : ""; }
+int mkrt_error_code(const mkrt_error* err) { return err ? err->code : MKRT_OK; }
+
+mkrt_error* mkrt_client_create(mkrt_client** out) {
+  if (!out) return make_error(MKRT_INVALID_ARGUMENT, "mkrt_client_create: null out");
+  *out = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n < 1) {
+    (void)hipGetLastError();
+    return make_error(MKRT_UNAVAILABLE, "no HIP device available (%s)", hipGetErrorString(e));
+  }
+  e = hipSetDevice(0);
+  if (e != hipSuccess) return hip_error("hipSetDevice", e);
+  mkrt_client* c = new mkrt_client;
+  e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete c;
+    return hip_error("hipStreamCreate", e);
+  }
+  c->worker = std::thread([c] { c->completion_loop(); });
+  *out = c;
+  return nullptr;
+}
+
+void mkrt_client_destroy(mkrt_client* c) {
+  if (!c) return;
+  (void)hipStreamSynchronize(c->stream);
+  {
+    std::lock_guard<std::mutex> g(c->q_mu);
+    c->stopping = true;
+  }
+  c->q_cv.notify_all();
+  if (c->worker.joinable()) c->worker.join();
+  for (hipEvent_t e : c->ev_pool) (void)hipEventDestroy(e);
+  (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+const char* mkrt_client_platform_name(const mkrt_client*) { return "mi355x"; }
+
+mkrt_error* mkrt_client_memory_stats(mkrt_client* c, int64_t* bytes_in_use, int64_t* bytes_limit) {
+  if (!c || !bytes_in_use || !bytes_limit) return make_error(MKRT_INVALID_ARGUMENT, "mkrt_client_memory_stats: null argument");
+  size_t fr = 0, total = 0;
+  hipError_t e = hipMemGetInfo(&fr, &total);
+  if (e != hipSuccess) return hip_error("hipMemGetInfo", e);
+  *bytes_in_use = c->alloc.in_use();
+  *bytes_limit = (int64_t)total;
+  return nullptr;
+}
+
+mkrt_error* mkrt_buffer_from_host(mkrt_client* c, const void* data, int type, const int64_t* dims, int ndims,
+                                  mkrt_buffer** out, mkrt_event** done_with_host) {
+  if (!c || !out || (ndims > 0 && !dims) || ndims < 0)
+    return make_error(MKRT_INVALID_ARGUMENT, "mkrt_buffer_from_host: null argument");
+  *out = nullptr;
+  const int eb = mkrt::dtype_bytes(type);
+  if (eb == 0) return make_error(MKRT_INVALID_ARGUMENT, "mkrt_buffer_from_host: unsupported element type %d", type);
+  for (int i = 0; i < ndims; ++i)
+    if (dims[i] < 0) return make_error(MKRT_INVALID_ARGUMENT, "mkrt_buffer_from_host: negative dimension");
+  const int64_t bytes = dims_numel(dims, ndims) * eb;
+  if (bytes > 0 && !data) return make_error(MKRT_INVALID_ARGUMENT, "mkrt_buffer_from_host: null data");
+  void* p = nullptr;
+  hipError_t e = c->alloc.alloc((size_t)bytes, &p);
+  if (e != hipSuccess) return make_error(MKRT_RESOURCE_EXHAUSTED, "device allocation of %lld bytes: %s",
+                                         (long long)bytes, hipGetErrorString(e));
+  if (bytes > 0) {
+    std::lock_guard<std::mutex> g(c->stream_mu);
+    e = hipMemcpyAsync(p, data, (size_t)bytes, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+      c->alloc.free(p);
+      return hip_error("host-to-device copy", e);
+    }
+  }
+  *out = new_buffer(c, type, std::vector<int64_t>(dims, dims + ndims), p, bytes, ready_state());
+  if (done_with_host) *done_with_host = new mkrt_event{ready_state()};
+  return nullptr;
+}
+
+mkrt_error* mkrt_buffer_to_host(mkrt_buffer* b, void* dst, int64_t dst_bytes, mkrt_event** done) {
+  if (!b) return make_error(MKRT_INVALID_ARGUMENT, "mkrt_buffer_to_host: null buffer");
+  if (done) *done = nullptr;
+  if (dst_bytes < b->bytes || (b->bytes > 0 && !dst))
+    return make_error(MKRT_INVALID_ARGUMENT, "mkrt_buffer_to_host: destination holds %lld bytes, buffer has %lld",
+                      (long long)dst_bytes, (long long)b->bytes);
+  if (mkrt_error* err = await_state(b->ready, -1)) return err;
+  if (b->bytes > 0) {
+    std::lock_guard<std::mutex> g(b->client->stream_mu);
+    hipError_t e = hipMemcpyAsync(dst, b->data, (size_t)b->bytes, hipMemcpyDeviceToHost, b->client->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(b->client->stream);
+    if (e != hipSuccess) return hip_error("device-to-host copy", e);
+  }
+  if (done) *done = new mkrt_event{ready_state()};
+  return nullptr;
+}
+
+int mkrt_buffer_type(const mkrt_buffer* b) { return b ? b->type : 0; }
+int mkrt_buffer_ndims(const mkrt_buffer* b) { return b ? (int)b->dims.size() : 0; }
+const int64_t* mkrt_buffer_dims(const mkrt_buffer* b) { return b ? b->dims.data() : nullptr; }
+int64_t mkrt_buffer_bytes(const mkrt_buffer* b) { return b ? b->bytes : 0; }
+
+mkrt_error* mkrt_buffer_ready_event(mkrt_buffer* b, mkrt_event** out) {
+  if (!b || !out) return make_error(MKRT_INVALID_ARGUMENT, "mkrt_buffer_ready_event: null argument");
+  *out = new mkrt_event{b->ready};
+  return nullptr;
+}
+
+mkrt_error* mkrt_buffer_create_error(mkrt_client* c, int code, const char* message, int type, const int64_t* dims,
+                                     int ndims, mkrt_buffer** out) {
+  if (!c || !out || (ndims > 0 && !dims) || ndims < 0)
+    return make_error(MKRT_INVALID_ARGUMENT, "mkrt_buffer_create_error: null argument");
+  if (code == MKRT_OK) return make_error(MKRT_INVALID_ARGUMENT, "mkrt_buffer_create_error: code must not be OK");
+  const int eb = mkrt::dtype_bytes(type);
+  *out = new_buffer(c, type, std::vector<int64_t>(dims, dims + ndims), nullptr,
+                    eb ? dims_numel(dims, ndims) * eb : 0, ready_state(code, message ? message : ""));
+  return nullptr;
+}
+
+void mkrt_buffer_destroy(mkrt_buffer* b) {
+  if (!b) return;
+  if (b->data) {
+    // Wait for the producer (core/mps_buffer.mm:656-662); later users of the
+    // memory are ordered behind every earlier reader on the stream.
+    std::unique_lock<std::mutex> l(b->ready->mu);
+    b->ready->cv.wait(l, [&] { return b->ready->ready; });
+    l.unlock();
+    b->client->alloc.free(b->data);
+  }
+  delete b;
+}
+
+}  // extern "C"
+
+namespace {
+
+// Parse + plan (no device work): the compile-time support check.
+mkrt_error* compile_text(const char* code, int64_t code_bytes, const char* format, mkrt::Function* fn,
+                         mkrt::Plan* plan) {
+  if (format && strcmp(format, "mlir") != 0)
+    return make_error(MKRT_UNIMPLEMENTED, "program format '%s' is not supported (StableHLO MLIR text only)", format);
+  std::string text(code, code_bytes >= 0 ? (size_t)code_bytes : strlen(code));
+  if (text.compare(0, 4, "ML\xefR") == 0)
+    return make_error(MKRT_UNIMPLEMENTED,
+                      "MLIR bytecode (VHLO portable artifact) is not read; pass the StableHLO text form");
+  try {
+    *fn = mkrt::parse_stablehlo_text(text);
+    *plan = mkrt::build_plan(*fn);
+  } catch (const mkrt::PlanError& e) {
+    return make_error(e.code, "%s", e.what());
+  } catch (const std::exception& e) {
+    return make_error(MKRT_INVALID_ARGUMENT, "StableHLO parse error: %s", e.what());
+  }
+  return nullptr;
+}
+
+}  // namespace
+
+extern "C" {
+
+mkrt_error* mkrt_compile(mkrt_client* c, const char* code, int64_t code_bytes, const char* format,
+                         mkrt_executable** out) {
+  if (!c || !code || !out) return make_error(MKRT_INVALID_ARGUMENT, "mkrt_compile: null argument");
+  *out = nullptr;
+  mkrt_executable* x = new mkrt_executable;
+  x->client = c;
+  if (mkrt_error* err = compile_text(code, code_bytes, format, &x->fn, &x->plan)) {
+    delete x;
+    return err;
+  }
+  x->plan_text = x->plan.describe();
+  *out = x;
+  return nullptr;
+}
+
+mkrt_error* mkrt_compile_check(const char* code, int64_t code_bytes, const char* format, char* plan_text,
+                               int64_t plan_text_bytes, int* num_steps) {
+  if (!code) return make_error(MKRT_INVALID_ARGUMENT, "mkrt_compile_check: null code");
+  mkrt::Function fn;
+  mkrt::Plan plan;
+  if (mkrt_error* err = compile_text(code, code_bytes, format, &fn, &plan)) return err;
+  if (num_steps) *num_steps = (int)plan.steps.size();
+  if (plan_text && plan_text_bytes > 0) {
+    const std::string t = plan.describe();
+    const size_t n = std::min((size_t)plan_text_bytes - 1, t.size());
+    memcpy(plan_text, t.data(), n);
+    plan_text[n] = 0;
+  }
+  return nullptr;
+}
+
+int mkrt_executable_num_inputs(const mkrt_executable* x) { return x ? (int)x->plan.in_slot.size() : 0; }
+int mkrt_executable_num_outputs(const mkrt_executable* x) { return x ? (int)x->plan.out_slot.size() : 0; }
+int mkrt_executable_num_steps(const mkrt_executable* x) { return x ? (int)x->plan.steps.size() : 0; }
+const char* mkrt_executable_plan(const mkrt_executable* x) { return x ? x->plan_text.c_str() : ""; }
+
+mkrt_error* mkrt_execute(mkrt_executable* x, mkrt_buffer* const* inputs, int num_inputs, mkrt_buffer** outputs,
+                         mkrt_event** done) {
+  if (!x) return make_error(MKRT_INVALID_ARGUMENT, "No executable to execute");
+  if (done) *done = nullptr;
+  const mkrt::Plan& p = x->plan;
+  if (num_inputs != (int)p.in_slot.size() || (num_inputs > 0 && !inputs) || (!outputs && !p.out_slot.empty()))
+    return make_error(MKRT_INVALID_ARGUMENT, "mkrt_execute: expected %d inputs, got %d", (int)p.in_slot.size(),
+                      num_inputs);
+  for (int i = 0; i < num_inputs; ++i) {
+    const mkrt_buffer* b = inputs[i];
+    if (!b) return make_error(MKRT_INVALID_ARGUMENT, "mkrt_execute: input %d is null", i);
+    if (b->client != x->client) return make_error(MKRT_INVALID_ARGUMENT, "mkrt_execute: input %d from another client", i);
+    if (b->type != p.in_type[i].dtype || b->dims != p.in_type[i].dims)
+      return make_error(MKRT_INVALID_ARGUMENT, "mkrt_execute: input %d is %s, the program takes %s", i,
+                        mkrt::TensorType{b->type, b->dims}.str().c_str(), p.in_type[i].str().c_str());
+    std::lock_guard<std::mutex> g(b->ready->mu);
+    if (b->ready->ready && b->ready->code != MKRT_OK)
+      return make_error(b->ready->code, "mkrt_execute: input %d carries an error: %s", i, b->ready->message.c_str());
+  }
+  if (mkrt_error* err = prepare(x)) return err;
+  mkrt_client* c = x->client;
+
+  // Device memory for every slot.
+  std::vector<void*> mem(p.slots.size(), nullptr);
+  std::vector<char> is_out(p.slots.size(), 0);
+  for (int s : p.out_slot) is_out[s] = 1;
+  std::vector<void*> temps;
+  mkrt_error* err = nullptr;
+  for (size_t i = 0; i < p.slots.size() && !err; ++i) {
+    const mkrt::Slot& s = p.slots[i];
+    if (s.kind == mkrt::SLOT_ARG) {
+      mem[i] = inputs[s.arg_index]->data;
+    } else if (s.kind == mkrt::SLOT_CONST) {
+      mem[i] = x->const_mem[i];
+    } else {
+      hipError_t e = c->alloc.alloc((size_t)s.bytes, &mem[i]);
+      if (e != hipSuccess)
+        err = make_error(MKRT_RESOURCE_EXHAUSTED, "device allocation of %lld bytes: %s", (long long)s.bytes,
+                         hipGetErrorString(e));
+      else
+        temps.push_back(mem[i]);
+    }
+  }
+  auto st = std::make_shared<EventState>();
+  if (!err) {
+    std::lock_guard<std::mutex> g(c->stream_mu);
+    for (size_t k = 0; k < p.steps.size() && !err; ++k) {
+      const int rc = run_step(p.steps[k], mem, x->workspace, p.workspace_bytes, c->stream);
+      if (rc != MK_OK)
+        err = make_error(MKRT_INTERNAL, "step %zu (%s) failed: %s", k, p.steps[k].desc.c_str(),
+                         rc == MK_ELAUNCH && mk_last_error()[0] == 0 ? "launch error" : mk_last_error());
+    }
+    if (!err) {
+      hipError_t e = c->track(st);
+      if (e != hipSuccess) err = hip_error("completion event", e);
+    }
+  }
+  if (err) {
+    // Memory is returned in stream order; anything already queued finishes
+    // before a later user of the same blocks.
+    for (void* t : temps) c->alloc.free(t);
+    return err;
+  }
+  for (size_t i = 0; i < p.slots.size(); ++i)
+    if (p.slots[i].kind == mkrt::SLOT_TEMP && !is_out[i]) c->alloc.free(mem[i]);
+  for (size_t r = 0; r < p.out_slot.size(); ++r) {
+    const mkrt::TensorType& t = p.out_type[r];
+    outputs[r] = new_buffer(c, t.dtype, t.dims, mem[p.out_slot[r]], t.bytes(), st);
+  }
+  if (done) *done = new mkrt_event{st};
+  return nullptr;
+}
+
+void mkrt_executable_destroy(mkrt_executable* x) {
+  if (!x) return;
+  mkrt_client* c = x->client;
+  for (void* p : x->const_mem) c->alloc.free(p);
+  c->alloc.free(x->workspace);
+  delete x;
+}
+
+mkrt_error* mkrt_event_create(mkrt_event** out) {
+  if (!out) return make_error(MKRT_INVALID_ARGUMENT, "mkrt_event_create: null out");
+  *out = new mkrt_event{std::make_shared<EventState>()};
+  return nullptr;
+}
+
+mkrt_error* mkrt_event_set(mkrt_event* ev, int code, const char* message) {
+  if (!ev) return make_error(MKRT_INVALID_ARGUMENT, "mkrt_event_set: null event");
+  ev->st->set(code, message ? message : "");
+  return nullptr;
+}
+
+int mkrt_event_is_ready(const mkrt_event* ev) {
+  if (!ev) return 0;
+  std::lock_guard<std::mutex> g(ev->st->mu);
+  return ev->st->ready ? 1 : 0;
+}
+
+mkrt_error* mkrt_event_error(const mkrt_event* ev) {
+  if (!ev) return make_error(MKRT_INVALID_ARGUMENT, "mkrt_event_error: null event");
+  std::lock_guard<std::mutex> g(ev->st->mu);
+  if (!ev->st->ready) return make_error(MKRT_FAILED_PRECONDITION, "event is not ready");
+  if (ev->st->code != MKRT_OK) return new mkrt_error{ev->st->code, ev->st->message};
+  return nullptr;
+}
+
+mkrt_error* mkrt_event_await(mkrt_event* ev, int64_t timeout_ms) {
+  if (!ev) return make_error(MKRT_INVALID_ARGUMENT, "mkrt_event_await: null event");
+  return await_state(ev->st, timeout_ms);
+}
+
+mkrt_error* mkrt_event_on_ready(mkrt_event* ev, mkrt_event_callback cb, void* user) {
+  if (!ev || !cb) return make_error(MKRT_INVALID_ARGUMENT, "mkrt_event_on_ready: null argument");
+  int code;
+  std::string msg;
+  {
+    std::lock_guard<std::mutex> g(ev->st->mu);
+    if (!ev->st->ready) {
+      ev->st->callbacks.emplace_back(cb, user);
+      return nullptr;
+    }
+    code = ev->st->code;
+    msg = ev->st->message;
+  }
+  cb(code == MKRT_OK ? nullptr : new mkrt_error{code, msg}, user);
+  return nullptr;
+}
+
+void mkrt_event_destroy(mkrt_event* ev) { delete ev; }
+
+}  // extern "C"

@@ -1,4 +1,4 @@
-"""ctypes binding of the kernel C-ABI (include/mk_kernels.h).
+"""ctypes binding of the plugin's C-ABI (include/mk_kernels.h, include/mk_runtime.h).
 
 The library is built in-tree by ``jax-metallib_amd/build.py`` (or
 ``__graft_entry__.build()``).  Loading fails loudly when it is missing: the
@@ -48,6 +48,46 @@ SIGNATURES = {
     "mk_elementwise_prepare": (_i32, [_i32, _p, _i32, _i32, _i32]),
 }
 
+_cb = ctypes.CFUNCTYPE(None, _p, _p)
+_pp = ctypes.POINTER(_p)
+
+# name -> (restype, argtypes); mirrors include/mk_runtime.h (opaque handles as void*)
+RUNTIME_SIGNATURES = {
+    "mkrt_error_destroy": (None, [_p]),
+    "mkrt_error_message": (ctypes.c_char_p, [_p]),
+    "mkrt_error_code": (_i32, [_p]),
+    "mkrt_client_create": (_p, [_pp]),
+    "mkrt_client_destroy": (None, [_p]),
+    "mkrt_client_platform_name": (ctypes.c_char_p, [_p]),
+    "mkrt_client_memory_stats": (_p, [_p, ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
+    "mkrt_buffer_from_host": (_p, [_p, _p, _i32, ctypes.POINTER(_i64), _i32, _pp, _pp]),
+    "mkrt_buffer_to_host": (_p, [_p, _p, _i64, _pp]),
+    "mkrt_buffer_type": (_i32, [_p]),
+    "mkrt_buffer_ndims": (_i32, [_p]),
+    "mkrt_buffer_dims": (ctypes.POINTER(_i64), [_p]),
+    "mkrt_buffer_bytes": (_i64, [_p]),
+    "mkrt_buffer_ready_event": (_p, [_p, _pp]),
+    "mkrt_buffer_create_error": (_p, [_p, _i32, ctypes.c_char_p, _i32, ctypes.POINTER(_i64), _i32, _pp]),
+    "mkrt_buffer_destroy": (None, [_p]),
+    "mkrt_compile": (_p, [_p, ctypes.c_char_p, _i64, ctypes.c_char_p, _pp]),
+    "mkrt_compile_check": (_p, [ctypes.c_char_p, _i64, ctypes.c_char_p, ctypes.c_char_p, _i64,
+                                ctypes.POINTER(_i32)]),
+    "mkrt_executable_num_inputs": (_i32, [_p]),
+    "mkrt_executable_num_outputs": (_i32, [_p]),
+    "mkrt_executable_num_steps": (_i32, [_p]),
+    "mkrt_executable_plan": (ctypes.c_char_p, [_p]),
+    "mkrt_execute": (_p, [_p, _pp, _i32, _pp, _pp]),
+    "mkrt_executable_destroy": (None, [_p]),
+    "mkrt_event_create": (_p, [_pp]),
+    "mkrt_event_set": (_p, [_p, _i32, ctypes.c_char_p]),
+    "mkrt_event_is_ready": (_i32, [_p]),
+    "mkrt_event_error": (_p, [_p]),
+    "mkrt_event_await": (_p, [_p, _i64]),
+    "mkrt_event_on_ready": (_p, [_p, _cb, _p]),
+    "mkrt_event_destroy": (None, [_p]),
+}
+EVENT_CALLBACK = _cb
+
 _LIB = None
 
 
@@ -68,7 +108,7 @@ def lib():
                 f"{KERNELS_SO} is missing: build it with `python jax-metallib_amd/build.py` "
                 "(the plugin has no CPU fallback)")
         L = ctypes.CDLL(KERNELS_SO)
-        for name, (res, args) in SIGNATURES.items():
+        for name, (res, args) in list(SIGNATURES.items()) + list(RUNTIME_SIGNATURES.items()):
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args

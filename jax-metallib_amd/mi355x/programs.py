@@ -1,0 +1,278 @@
+"""StableHLO text of the workload's jitted functions.
+
+Each function returns the module text that ``jax.jit(f).lower(*args).as_text()``
+prints for the jnp function in its docstring (pretty-printed StableHLO, the
+form jax's MLIR printer emits).  The plugin's compile path reads this text;
+these builders give the exact programs at any shape, for tests and the
+benchmark, without jax installed.
+
+The quantized formats are this plugin's (the reference's quantized matmul is
+not jittable, src/jax_metallib/quantized.py:1077-1152):
+  int4 g64: X bf16 [M, K]; P uint8 [K/2, N], element k of column n in byte
+            P[k // 2, n], low nibble for even k (the reference's nibble order,
+            quantized.py:189-190); scale bf16 [K/64, N]; zero uint8 [K/64, N]
+            (values 0..15); Y = X @ ((q - z) * s) as bf16.
+  int8 per-channel: W int8 [K, N], scale f32 [N]; Y = X @ (W * s) as bf16.
+"""
+
+_HEADER = ('module @{name} attributes {{mhlo.num_partitions = 1 : i32, mhlo.num_replicas = 1 : i32}} {{\n'
+           '  func.func public @main({args}) -> ({rets}) {{\n')
+_FOOTER = '  }\n}\n'
+
+
+def _t(shape, dt):
+    return "tensor<" + "".join(f"{d}x" for d in shape) + dt + ">"
+
+
+def _module(name, args, rets, body):
+    a = ", ".join(f"%arg{i}: {t}" for i, t in enumerate(args))
+    r = ", ".join(f'{t} {{jax.result_info = "{"" if len(rets) == 1 else f"[{i}]"}"}}'
+                  for i, t in enumerate(rets))
+    lines = "".join(f"    {l}\n" for l in body)
+    return _HEADER.format(name=name, args=a, rets=r) + lines + _FOOTER
+
+
+_NEG_INF = {"f32": "0xFF800000", "bf16": "0xFF80"}
+
+
+def matmul(M, K, N, dt="bf16", batch=None, preferred_f32=False):
+    """jnp.matmul(a, b) (a [batch.., M, K], b [batch.., K, N]);
+    preferred_f32: jnp.matmul(a, b, preferred_element_type=jnp.float32)."""
+    bd = [] if batch is None else [batch]
+    ta, tb = _t(bd + [M, K], dt), _t(bd + [K, N], dt)
+    odt = "f32" if preferred_f32 else dt
+    tc = _t(bd + [M, N], odt)
+    dims = ("batching_dims = [0] x [0], contracting_dims = [2] x [1]" if batch is not None
+            else "contracting_dims = [1] x [0]")
+    body = [f"%0 = stablehlo.dot_general %arg0, %arg1, {dims}, precision = [DEFAULT, DEFAULT] : "
+            f"({ta}, {tb}) -> {tc}", f"return %0 : {tc}"]
+    return _module("jit_matmul", [ta, tb], [tc], body)
+
+
+def softmax(R, C, dt="f32"):
+    """jax.nn.softmax(x, axis=-1) on x [R, C]."""
+    tx, tr, tr1 = _t([R, C], dt), _t([R], dt), _t([R, 1], dt)
+    s = _t([], dt)
+    body = [
+        f"%cst = stablehlo.constant dense<{_NEG_INF[dt]}> : {s}",
+        f"%0 = stablehlo.reduce(%arg0 init: %cst) applies stablehlo.maximum across dimensions = [1] : "
+        f"({tx}, {s}) -> {tr}",
+        f"%cst_0 = stablehlo.constant dense<{_NEG_INF[dt]}> : {s}",
+        f"%1 = stablehlo.broadcast_in_dim %cst_0, dims = [] : ({s}) -> {tr}",
+        f"%2 = stablehlo.maximum %1, %0 : {tr}",
+        f"%3 = stablehlo.broadcast_in_dim %2, dims = [0] : ({tr}) -> {tr1}",
+        f"%4 = stablehlo.broadcast_in_dim %3, dims = [0, 1] : ({tr1}) -> {tx}",
+        f"%5 = stablehlo.subtract %arg0, %4 : {tx}",
+        f"%6 = stablehlo.exponential %5 : {tx}",
+    ]
+    if dt == "bf16":
+        # jnp.sum upcasts bf16 to f32 for the reduction.
+        txf, trf = _t([R, C], "f32"), _t([R], "f32")
+        body += [
+            f"%7 = stablehlo.convert %6 : ({tx}) -> {txf}",
+            "%cst_1 = stablehlo.constant dense<0.000000e+00> : tensor<f32>",
+            f"%8 = stablehlo.reduce(%7 init: %cst_1) applies stablehlo.add across dimensions = [1] : "
+            f"({txf}, tensor<f32>) -> {trf}",
+            f"%9 = stablehlo.convert %8 : ({trf}) -> {tr}",
+        ]
+    else:
+        body += [
+            "%cst_1 = stablehlo.constant dense<0.000000e+00> : tensor<f32>",
+            f"%9 = stablehlo.reduce(%6 init: %cst_1) applies stablehlo.add across dimensions = [1] : "
+            f"({tx}, tensor<f32>) -> {tr}",
+        ]
+    body += [
+        f"%10 = stablehlo.broadcast_in_dim %9, dims = [0] : ({tr}) -> {tr1}",
+        f"%11 = stablehlo.broadcast_in_dim %10, dims = [0, 1] : ({tr1}) -> {tx}",
+        f"%12 = stablehlo.divide %6, %11 : {tx}",
+        f"return %12 : {tx}",
+    ]
+    return _module("jit_softmax", [tx], [tx], body)
+
+
+def rmsnorm(R, C, dt="f32", eps="9.99999997E-7"):
+    """x * jax.lax.rsqrt(jnp.mean(x * x, axis=-1, keepdims=True) + 1e-6) * g
+    on x [R, C], g [C]."""
+    tx, tg, tr, tr1 = _t([R, C], dt), _t([C], dt), _t([R], "f32"), _t([R, 1], "f32")
+    tr1d, t1c = _t([R, 1], dt), _t([1, C], dt)
+    body = [f"%0 = stablehlo.multiply %arg0, %arg0 : {tx}"]
+    src = "%0"
+    if dt == "bf16":
+        body.append(f"%c0 = stablehlo.convert %0 : ({tx}) -> {_t([R, C], 'f32')}")
+        src = "%c0"
+    body += [
+        "%cst = stablehlo.constant dense<0.000000e+00> : tensor<f32>",
+        f"%1 = stablehlo.reduce({src} init: %cst) applies stablehlo.add across dimensions = [1] : "
+        f"({_t([R, C], 'f32')}, tensor<f32>) -> {tr}",
+        f"%2 = stablehlo.broadcast_in_dim %1, dims = [0] : ({tr}) -> {tr1}",
+        f"%cst_0 = stablehlo.constant dense<{float(C):.6e}> : tensor<f32>",
+        f"%3 = stablehlo.broadcast_in_dim %cst_0, dims = [] : (tensor<f32>) -> {tr1}",
+        f"%4 = stablehlo.divide %2, %3 : {tr1}",
+    ]
+    m = "%4"
+    if dt == "bf16":
+        body.append(f"%c4 = stablehlo.convert %4 : ({tr1}) -> {tr1d}")
+        m = "%c4"
+    body += [
+        f"%cst_1 = stablehlo.constant dense<{eps}> : {_t([], dt)}",
+        f"%5 = stablehlo.broadcast_in_dim %cst_1, dims = [] : ({_t([], dt)}) -> {tr1d}",
+        f"%6 = stablehlo.add {m}, %5 : {tr1d}",
+        f"%7 = stablehlo.rsqrt %6 : {tr1d}",
+        f"%8 = stablehlo.broadcast_in_dim %7, dims = [0, 1] : ({tr1d}) -> {tx}",
+        f"%9 = stablehlo.multiply %arg0, %8 : {tx}",
+        f"%10 = stablehlo.broadcast_in_dim %arg1, dims = [1] : ({tg}) -> {t1c}",
+        f"%11 = stablehlo.broadcast_in_dim %10, dims = [0, 1] : ({t1c}) -> {tx}",
+        f"%12 = stablehlo.multiply %9, %11 : {tx}",
+        f"return %12 : {tx}",
+    ]
+    return _module("jit_rmsnorm", [tx, tg], [tx], body)
+
+
+def argmax(R, C, dt="f32"):
+    """jnp.argmax(x, axis=-1) on x [R, C] -> int32 [R]."""
+    tx, ti, tr, tri = _t([R, C], dt), _t([R, C], "i32"), _t([R], dt), _t([R], "i32")
+    s = _t([], dt)
+    body = [
+        f"%0 = stablehlo.iota dim = 1 : {ti}",
+        f"%cst = stablehlo.constant dense<{_NEG_INF[dt]}> : {s}",
+        "%c = stablehlo.constant dense<0> : tensor<i32>",
+        f"%1:2 = stablehlo.reduce(%arg0 init: %cst), (%0 init: %c) across dimensions = [1] : "
+        f"({tx}, {ti}, {s}, tensor<i32>) -> ({tr}, {tri})",
+        f" reducer(%arg1: {s}, %arg3: {s}) (%arg2: tensor<i32>, %arg4: tensor<i32>)  {{",
+        f"  %2 = stablehlo.compare  GT, %arg1, %arg3,  FLOAT : ({s}, {s}) -> tensor<i1>",
+        f"  %3 = stablehlo.compare  NE, %arg1, %arg1,  FLOAT : ({s}, {s}) -> tensor<i1>",
+        "  %4 = stablehlo.or %2, %3 : tensor<i1>",
+        f"  %5 = stablehlo.compare  EQ, %arg1, %arg3,  FLOAT : ({s}, {s}) -> tensor<i1>",
+        "  %6 = stablehlo.compare  LT, %arg2, %arg4,  SIGNED : (tensor<i32>, tensor<i32>) -> tensor<i1>",
+        "  %7 = stablehlo.and %5, %6 : tensor<i1>",
+        "  %8 = stablehlo.or %4, %7 : tensor<i1>",
+        f"  %9 = stablehlo.select %4, %arg1, %arg3 : tensor<i1>, {s}",
+        "  %10 = stablehlo.select %8, %arg2, %arg4 : tensor<i1>, tensor<i32>",
+        f"  stablehlo.return %9, %10 : {s}, tensor<i32>",
+        "}",
+        f"return %1#1 : {tri}",
+    ]
+    return _module("jit_argmax", [tx], [tri], body)
+
+
+def reduce(R, C, op="sum", dt="f32"):
+    """jnp.sum(x, axis=-1) / jnp.max(x, axis=-1) on x [R, C]."""
+    tx, tr = _t([R, C], dt), _t([R], dt)
+    if op == "max":
+        body = [f"%cst = stablehlo.constant dense<{_NEG_INF[dt]}> : {_t([], dt)}",
+                f"%0 = stablehlo.reduce(%arg0 init: %cst) applies stablehlo.maximum across dimensions = [1] : "
+                f"({tx}, {_t([], dt)}) -> {tr}",
+                f"return %0 : {tr}"]
+    elif dt == "bf16":
+        txf, trf = _t([R, C], "f32"), _t([R], "f32")
+        body = [f"%0 = stablehlo.convert %arg0 : ({tx}) -> {txf}",
+                "%cst = stablehlo.constant dense<0.000000e+00> : tensor<f32>",
+                f"%1 = stablehlo.reduce(%0 init: %cst) applies stablehlo.add across dimensions = [1] : "
+                f"({txf}, tensor<f32>) -> {trf}",
+                f"%2 = stablehlo.convert %1 : ({trf}) -> {tr}",
+                f"return %2 : {tr}"]
+    else:
+        body = ["%cst = stablehlo.constant dense<0.000000e+00> : tensor<f32>",
+                f"%0 = stablehlo.reduce(%arg0 init: %cst) applies stablehlo.add across dimensions = [1] : "
+                f"({tx}, tensor<f32>) -> {tr}",
+                f"return %0 : {tr}"]
+    return _module(f"jit_{op}", [tx], [tr], body)
+
+
+def chain6(R, C, dt="f32"):
+    """The workload's 6-op chain on x [R, C]:
+    a = x * 1.5; b = a + 0.5; y = jnp.where(x > 0, jnp.maximum(jnp.log1p(jnp.exp(b)), x), b)."""
+    tx, tp, s = _t([R, C], dt), _t([R, C], "i1"), _t([], dt)
+    body = [
+        f"%cst = stablehlo.constant dense<1.500000e+00> : {s}",
+        f"%0 = stablehlo.broadcast_in_dim %cst, dims = [] : ({s}) -> {tx}",
+        f"%1 = stablehlo.multiply %arg0, %0 : {tx}",
+        f"%cst_0 = stablehlo.constant dense<5.000000e-01> : {s}",
+        f"%2 = stablehlo.broadcast_in_dim %cst_0, dims = [] : ({s}) -> {tx}",
+        f"%3 = stablehlo.add %1, %2 : {tx}",
+        f"%4 = stablehlo.exponential %3 : {tx}",
+        f"%5 = stablehlo.log_plus_one %4 : {tx}",
+        f"%6 = stablehlo.maximum %5, %arg0 : {tx}",
+        f"%cst_1 = stablehlo.constant dense<0.000000e+00> : {s}",
+        f"%7 = stablehlo.broadcast_in_dim %cst_1, dims = [] : ({s}) -> {tx}",
+        f"%8 = stablehlo.compare  GT, %arg0, %7,  FLOAT : ({tx}, {tx}) -> {tp}",
+        f"%9 = stablehlo.select %8, %6, %3 : {tp}, {tx}",
+        f"return %9 : {tx}",
+    ]
+    return _module("jit_chain6", [tx], [tx], body)
+
+
+def int4_g64_matmul(M, K, N):
+    """def f(x, p, s, z):
+           q = jnp.stack([p & 15, p >> 4], axis=1).reshape(K, N)
+           w = (q.astype(f32) - jnp.repeat(z, 64, 0).astype(f32)) * jnp.repeat(s, 64, 0).astype(f32)
+           return jnp.dot(x.astype(f32), w).astype(bf16)"""
+    G = K // 64
+    tx, tp, ts, tz = _t([M, K], "bf16"), _t([K // 2, N], "ui8"), _t([G, N], "bf16"), _t([G, N], "ui8")
+    tp3, tc = _t([K // 2, 1, N], "ui8"), _t([K // 2, 2, N], "ui8")
+    tq, tqf = _t([K, N], "ui8"), _t([K, N], "f32")
+    tz3, tzb, ts3, tsb = _t([G, 1, N], "ui8"), _t([G, 64, N], "ui8"), _t([G, 1, N], "bf16"), _t([G, 64, N], "bf16")
+    tsk, txf, ty, tyf = _t([K, N], "bf16"), _t([M, K], "f32"), _t([M, N], "bf16"), _t([M, N], "f32")
+    body = [
+        "%c = stablehlo.constant dense<15> : tensor<ui8>",
+        f"%0 = stablehlo.broadcast_in_dim %c, dims = [] : (tensor<ui8>) -> {tp}",
+        f"%1 = stablehlo.and %arg1, %0 : {tp}",
+        "%c_0 = stablehlo.constant dense<4> : tensor<ui8>",
+        f"%2 = stablehlo.broadcast_in_dim %c_0, dims = [] : (tensor<ui8>) -> {tp}",
+        f"%3 = stablehlo.shift_right_logical %arg1, %2 : {tp}",
+        f"%4 = stablehlo.broadcast_in_dim %1, dims = [0, 2] : ({tp}) -> {tp3}",
+        f"%5 = stablehlo.broadcast_in_dim %3, dims = [0, 2] : ({tp}) -> {tp3}",
+        f"%6 = stablehlo.concatenate %4, %5, dim = 1 : ({tp3}, {tp3}) -> {tc}",
+        f"%7 = stablehlo.reshape %6 : ({tc}) -> {tq}",
+        f"%8 = stablehlo.reshape %arg3 : ({tz}) -> {tz3}",
+        f"%9 = stablehlo.broadcast_in_dim %8, dims = [0, 1, 2] : ({tz3}) -> {tzb}",
+        f"%10 = stablehlo.reshape %9 : ({tzb}) -> {tq}",
+        f"%11 = stablehlo.reshape %arg2 : ({ts}) -> {ts3}",
+        f"%12 = stablehlo.broadcast_in_dim %11, dims = [0, 1, 2] : ({ts3}) -> {tsb}",
+        f"%13 = stablehlo.reshape %12 : ({tsb}) -> {tsk}",
+        f"%14 = stablehlo.convert %7 : ({tq}) -> {tqf}",
+        f"%15 = stablehlo.convert %10 : ({tq}) -> {tqf}",
+        f"%16 = stablehlo.subtract %14, %15 : {tqf}",
+        f"%17 = stablehlo.convert %13 : ({tsk}) -> {tqf}",
+        f"%18 = stablehlo.multiply %16, %17 : {tqf}",
+        f"%19 = stablehlo.convert %arg0 : ({tx}) -> {txf}",
+        f"%20 = stablehlo.dot_general %19, %18, contracting_dims = [1] x [0], precision = [DEFAULT, DEFAULT] : "
+        f"({txf}, {tqf}) -> {tyf}",
+        f"%21 = stablehlo.convert %20 : ({tyf}) -> {ty}",
+        f"return %21 : {ty}",
+    ]
+    return _module("jit_int4_g64_matmul", [tx, tp, ts, tz], [ty], body)
+
+
+def int8_pc_matmul(M, K, N):
+    """def f(x, w, s):
+           return jnp.dot(x.astype(f32), w.astype(f32) * s[None, :]).astype(bf16)"""
+    tx, tw, ts = _t([M, K], "bf16"), _t([K, N], "i8"), _t([N], "f32")
+    twf, t1n, txf, ty, tyf = _t([K, N], "f32"), _t([1, N], "f32"), _t([M, K], "f32"), _t([M, N], "bf16"), _t([M, N], "f32")
+    body = [
+        f"%0 = stablehlo.convert %arg1 : ({tw}) -> {twf}",
+        f"%1 = stablehlo.broadcast_in_dim %arg2, dims = [1] : ({ts}) -> {t1n}",
+        f"%2 = stablehlo.broadcast_in_dim %1, dims = [0, 1] : ({t1n}) -> {twf}",
+        f"%3 = stablehlo.multiply %0, %2 : {twf}",
+        f"%4 = stablehlo.convert %arg0 : ({tx}) -> {txf}",
+        f"%5 = stablehlo.dot_general %4, %3, contracting_dims = [1] x [0], precision = [DEFAULT, DEFAULT] : "
+        f"({txf}, {twf}) -> {tyf}",
+        f"%6 = stablehlo.convert %5 : ({tyf}) -> {ty}",
+        f"return %6 : {ty}",
+    ]
+    return _module("jit_int8_pc_matmul", [tx, tw, ts], [ty], body)
+
+
+def plumbing(n=1024):
+    """jnp.tanh(a @ b).sum(axis=1) on f32 [n, n]."""
+    t, tr = _t([n, n], "f32"), _t([n], "f32")
+    body = [
+        f"%0 = stablehlo.dot_general %arg0, %arg1, contracting_dims = [1] x [0], precision = [DEFAULT, DEFAULT] : "
+        f"({t}, {t}) -> {t}",
+        f"%1 = stablehlo.tanh %0 : {t}",
+        "%cst = stablehlo.constant dense<0.000000e+00> : tensor<f32>",
+        f"%2 = stablehlo.reduce(%1 init: %cst) applies stablehlo.add across dimensions = [1] : "
+        f"({t}, tensor<f32>) -> {tr}",
+        f"return %2 : {tr}",
+    ]
+    return _module("jit_plumbing", [t, t], [tr], body)

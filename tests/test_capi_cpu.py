@@ -1,6 +1,6 @@
-"""Host-only checks of the kernel C-ABI (no GPU needed): the built library
-loads, exports every entry point include/mk_kernels.h declares, and rejects
-bad arguments on the host before any launch."""
+"""Host-only checks of the C-ABI (no GPU needed): the built library loads,
+exports every entry point include/mk_kernels.h and include/mk_runtime.h
+declare, and rejects bad arguments on the host before any launch."""
 
 import ctypes
 import os
@@ -13,10 +13,10 @@ from mi355x import _lib
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def _declared(header):
+def _declared(header, prefix="mk_"):
     text = open(os.path.join(REPO, "include", header)).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(mk_[a-z0-9_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(" + prefix + r"[a-z0-9_]+)\s*\(", text)))
 
 
 def test_every_declared_symbol_is_exported_and_bound():
@@ -26,6 +26,15 @@ def test_every_declared_symbol_is_exported_and_bound():
     for n in names:
         assert hasattr(L, n), f"{n} declared but not exported"
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature in mi355x/_lib.py"
+
+
+def test_every_runtime_symbol_is_exported_and_bound():
+    L = _lib.lib()
+    names = _declared("mk_runtime.h", "mkrt_")
+    assert len(names) >= 30, names
+    for n in names:
+        assert hasattr(L, n), f"{n} declared but not exported"
+        assert n in _lib.RUNTIME_SIGNATURES, f"{n} has no ctypes signature in mi355x/_lib.py"
 
 
 def test_workspace_query_is_host_only():

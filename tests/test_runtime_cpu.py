@@ -1,0 +1,302 @@
+"""Host-side tests of the plugin runtime (no GPU): the StableHLO reader, the
+planner's kernel routing, compile-time rejection of unsupported programs,
+and the event/error object model.
+
+The compile path mirrors the reference's PJRT_Client_Compile: unsupported
+ops fail at compile with a message listing them
+(src/pjrt_plugin/api/pjrt_client.cc:211-220); events follow
+src/pjrt_plugin/api/pjrt_event.cc (error before ready is
+FAILED_PRECONDITION, :32-44; on_ready runs inline when already ready,
+:81-98) and the await timeout of core/completion_event.h.
+"""
+
+import re
+
+import pytest
+
+from mi355x import programs as P
+from mi355x import runtime as rt
+
+
+def plan(text):
+    t, n = rt.compile_check(text)
+    steps = [l for l in t.strip().splitlines() if l]
+    assert len(steps) == n
+    return steps
+
+
+# Every workload function of the benchmark plans to exactly one kernel step
+# at its full size.
+@pytest.mark.parametrize("text,step", [
+    (P.int4_g64_matmul(16, 4096, 14336), "int4_g64_matmul M=16 K=4096 N=14336 -> bf16"),
+    (P.int4_g64_matmul(1, 4096, 14336), "int4_g64_matmul M=1 K=4096 N=14336 -> bf16"),
+    (P.int8_pc_matmul(16, 4096, 14336), "int8_pc_matmul M=16 K=4096 N=14336 -> bf16"),
+    (P.matmul(4096, 4096, 4096), "gemm_bf16 batch=1 M=4096 N=4096 K=4096 -> bf16"),
+    (P.matmul(4096, 4096, 4096, preferred_f32=True), "gemm_bf16 batch=1 M=4096 N=4096 K=4096 -> f32"),
+    (P.matmul(2048, 128, 2048, batch=16), "gemm_bf16 batch=16 M=2048 N=2048 K=128 -> bf16"),
+    (P.matmul(2048, 2048, 2048, dt="f32"), "gemm_f32 batch=1 M=2048 N=2048 K=2048 -> f32"),
+    (P.softmax(8192, 8192), "softmax rows=8192 cols=8192 f32"),
+    (P.softmax(8192, 8192, "bf16"), "softmax rows=8192 cols=8192 bf16"),
+    (P.rmsnorm(8192, 8192), "rmsnorm rows=8192 cols=8192 eps=1e-06 f32"),
+    (P.argmax(8192, 8192), "argmax rows=8192 cols=8192 f32 -> i32"),
+    (P.argmax(8192, 8192, "bf16"), "argmax rows=8192 cols=8192 bf16 -> i32"),
+    (P.reduce(8192, 8192, "sum"), "reduce_sum rows=8192 cols=8192 f32"),
+    (P.reduce(8192, 8192, "sum", "bf16"), "reduce_sum rows=8192 cols=8192 bf16"),
+    (P.reduce(8192, 8192, "max", "bf16"), "reduce_max rows=8192 cols=8192 bf16"),
+    (P.chain6(8192, 8192), "elementwise 11 instr, 1 inputs, n=67108864 f32"),
+    (P.chain6(8192, 8192, "bf16"), "elementwise 11 instr, 1 inputs, n=67108864 bf16"),
+])
+def test_workload_plans_to_one_kernel(text, step):
+    assert plan(text) == [step]
+
+
+def test_rmsnorm_bf16_keeps_the_bf16_epsilon():
+    # 1e-6 printed as a bf16 constant is the bf16 value nearest 1e-6.
+    (s,) = plan(P.rmsnorm(64, 128, "bf16"))
+    eps = float(re.search(r"eps=([0-9.e+-]+)", s).group(1))
+    assert s.startswith("rmsnorm rows=64 cols=128") and s.endswith("bf16")
+    assert abs(eps - 9.98377799987793e-07) < 1e-12
+
+
+def test_plumbing_chain_plans_three_steps():
+    assert plan(P.plumbing()) == [
+        "gemm_f32 batch=1 M=1024 N=1024 K=1024 -> f32",
+        "elementwise 2 instr, 1 inputs, n=1048576 f32",
+        "reduce_sum rows=1024 cols=1024 f32",
+    ]
+
+
+def _wrap(args, rets, body):
+    a = ", ".join(f"%arg{i}: {t}" for i, t in enumerate(args))
+    r = ", ".join(rets)
+    return ("module @jit_f {\n  func.func public @main(" + a + ") -> (" + r + ") {\n" +
+            "".join("    " + l + "\n" for l in body) + "  }\n}\n")
+
+
+def test_private_function_is_inlined():
+    inner = P.softmax(8, 16).replace("func.func public @main", "func.func private @_softmax")
+    inner = inner.split("\n", 1)[1].rsplit("}", 1)[0]  # the func.func only
+    text = ("module @jit_f {\n  func.func public @main(%arg0: tensor<8x16xf32>) -> (tensor<8x16xf32>) {\n"
+            "    %0 = call @_softmax(%arg0) : (tensor<8x16xf32>) -> tensor<8x16xf32>\n"
+            "    return %0 : tensor<8x16xf32>\n  }\n" + inner + "}\n")
+    assert plan(text) == ["softmax rows=8 cols=16 f32"]
+
+
+GENERIC_ARGMAX = """module @jit_argmax {
+  func.func public @main(%arg0: tensor<4x8xf32>) -> tensor<4xi32> {
+    %0 = "stablehlo.iota"() {iota_dimension = 1 : i64} : () -> tensor<4x8xi32>
+    %1 = "stablehlo.constant"() {value = dense<0xFF800000> : tensor<f32>} : () -> tensor<f32>
+    %2 = "stablehlo.constant"() {value = dense<0> : tensor<i32>} : () -> tensor<i32>
+    %3:2 = "stablehlo.reduce"(%arg0, %0, %1, %2) ({
+    ^bb0(%a: tensor<f32>, %b: tensor<i32>, %c: tensor<f32>, %d: tensor<i32>):
+      %4 = "stablehlo.compare"(%a, %c) {comparison_direction = #stablehlo<comparison_direction GT>} : (tensor<f32>, tensor<f32>) -> tensor<i1>
+      %5 = "stablehlo.compare"(%a, %a) {comparison_direction = #stablehlo<comparison_direction NE>} : (tensor<f32>, tensor<f32>) -> tensor<i1>
+      %6 = "stablehlo.or"(%4, %5) : (tensor<i1>, tensor<i1>) -> tensor<i1>
+      %7 = "stablehlo.select"(%6, %a, %c) : (tensor<i1>, tensor<f32>, tensor<f32>) -> tensor<f32>
+      %8 = "stablehlo.select"(%6, %b, %d) : (tensor<i1>, tensor<i32>, tensor<i32>) -> tensor<i32>
+      "stablehlo.return"(%7, %8) : (tensor<f32>, tensor<i32>) -> ()
+    }) {dimensions = array<i64: 1>} : (tensor<4x8xf32>, tensor<4x8xi32>, tensor<f32>, tensor<i32>) -> (tensor<4xf32>, tensor<4xi32>)
+    "func.return"(%3#1) : (tensor<4xi32>) -> ()
+  }
+}
+"""
+
+
+def test_generic_form_argmax():
+    assert plan(GENERIC_ARGMAX) == ["argmax rows=4 cols=8 f32 -> i32"]
+
+
+def test_generic_form_reduce_and_broadcast():
+    text = _wrap(["tensor<4x8xf32>"], ["tensor<4xf32>"], [
+        '%0 = "stablehlo.constant"() {value = dense<0.000000e+00> : tensor<f32>} : () -> tensor<f32>',
+        '%1 = "stablehlo.reduce"(%arg0, %0) ({',
+        '^bb0(%a: tensor<f32>, %b: tensor<f32>):',
+        '  %2 = "stablehlo.add"(%a, %b) : (tensor<f32>, tensor<f32>) -> tensor<f32>',
+        '  "stablehlo.return"(%2) : (tensor<f32>) -> ()',
+        '}) {dimensions = array<i64: 1>} : (tensor<4x8xf32>, tensor<f32>) -> tensor<4xf32>',
+        '"func.return"(%1) : (tensor<4xf32>) -> ()',
+    ])
+    assert plan(text) == ["reduce_sum rows=4 cols=8 f32"]
+
+
+def test_returning_an_argument_copies_it():
+    text = _wrap(["tensor<4x8xf32>"], ["tensor<4x8xf32>", "tensor<4x8xf32>"], [
+        "%0 = stablehlo.exponential %arg0 : tensor<4x8xf32>",
+        "return %arg0, %0 : tensor<4x8xf32>, tensor<4x8xf32>",
+    ])
+    assert plan(text) == ["copy tensor<4x8xf32>", "elementwise 2 instr, 1 inputs, n=32 f32"]
+
+
+def test_same_value_returned_twice_gets_two_buffers():
+    text = _wrap(["tensor<4x8xf32>"], ["tensor<4x8xf32>", "tensor<4x8xf32>"], [
+        "%0 = stablehlo.tanh %arg0 : tensor<4x8xf32>",
+        "return %0, %0 : tensor<4x8xf32>, tensor<4x8xf32>",
+    ])
+    assert plan(text) == ["elementwise 2 instr, 1 inputs, n=32 f32", "copy tensor<4x8xf32>"]
+
+
+def test_reshape_is_a_view():
+    text = _wrap(["tensor<4x8xf32>"], ["tensor<32xf32>"], [
+        "%0 = stablehlo.reshape %arg0 : (tensor<4x8xf32>) -> tensor<32xf32>",
+        "%1 = stablehlo.negate %0 : tensor<32xf32>",
+        "%2 = stablehlo.reshape %1 : (tensor<32xf32>) -> tensor<4x8xf32>",
+        "%3 = stablehlo.reshape %2 : (tensor<4x8xf32>) -> tensor<32xf32>",
+        "return %3 : tensor<32xf32>",
+    ])
+    assert plan(text) == ["elementwise 2 instr, 1 inputs, n=32 f32"]
+
+
+def test_long_elementwise_chain_is_split():
+    body = ["%0 = stablehlo.tanh %arg0 : tensor<64xf32>"]
+    for i in range(1, 50):
+        body.append(f"%{i} = stablehlo.add %{i - 1}, %arg{i % 3} : tensor<64xf32>")
+    body.append("return %49 : tensor<64xf32>")
+    steps = plan(_wrap(["tensor<64xf32>"] * 3, ["tensor<64xf32>"], body))
+    assert len(steps) >= 2
+    assert all(s.startswith("elementwise") for s in steps)
+    assert all(int(re.search(r"(\d+) instr", s).group(1)) <= 32 for s in steps)
+
+
+def test_five_inputs_are_split_to_four_per_program():
+    body = ["%0 = stablehlo.add %arg0, %arg1 : tensor<64xf32>"]
+    for i in range(2, 5):
+        body.append(f"%{i - 1} = stablehlo.multiply %{i - 2}, %arg{i} : tensor<64xf32>")
+    body.append("return %3 : tensor<64xf32>")
+    steps = plan(_wrap(["tensor<64xf32>"] * 5, ["tensor<64xf32>"], body))
+    assert len(steps) == 2
+    assert all(int(re.search(r"(\d+) inputs", s).group(1)) <= 4 for s in steps)
+
+
+def test_bf16_typed_node_in_f32_program_rounds():
+    # x.astype(bf16).astype(f32) * 2 rounds once to bf16 inside an f32
+    # program: load, round, constant, multiply (3 without the rounding).
+    text = _wrap(["tensor<64xf32>"], ["tensor<64xf32>"], [
+        "%0 = stablehlo.convert %arg0 : (tensor<64xf32>) -> tensor<64xbf16>",
+        "%1 = stablehlo.convert %0 : (tensor<64xbf16>) -> tensor<64xf32>",
+        "%cst = stablehlo.constant dense<2.000000e+00> : tensor<f32>",
+        "%2 = stablehlo.broadcast_in_dim %cst, dims = [] : (tensor<f32>) -> tensor<64xf32>",
+        "%3 = stablehlo.multiply %1, %2 : tensor<64xf32>",
+        "return %3 : tensor<64xf32>",
+    ])
+    assert plan(text) == ["elementwise 4 instr, 1 inputs, n=64 f32"]
+
+
+def _unsupported(text):
+    with pytest.raises(rt.PluginError) as ei:
+        rt.compile_check(text)
+    assert ei.value.code == rt.UNIMPLEMENTED, ei.value
+    return ei.value.message
+
+
+def test_unsupported_ops_fail_at_compile_with_a_list():
+    text = _wrap(["tensor<4x8xf32>", "tensor<8x4xf32>"], ["tensor<8x4xf32>", "tensor<4x8xf32>"], [
+        "%0 = stablehlo.transpose %arg0, dims = [1, 0] : (tensor<4x8xf32>) -> tensor<8x4xf32>",
+        "%1 = stablehlo.cosine %arg1 : tensor<8x4xf32>",
+        "%2 = stablehlo.add %0, %1 : tensor<8x4xf32>",
+        "%3 = stablehlo.sine %arg0 : tensor<4x8xf32>",
+        "return %2, %3 : tensor<8x4xf32>, tensor<4x8xf32>",
+    ])
+    msg = _unsupported(text)
+    for op in ("stablehlo.transpose", "stablehlo.cosine", "stablehlo.sine"):
+        assert op in msg, msg
+
+
+def test_non_canonical_dot_is_rejected():
+    # x @ w.T as a contraction over both last dims: not the [M,K] x [K,N] form.
+    text = _wrap(["tensor<16x64xbf16>", "tensor<32x64xbf16>"], ["tensor<16x32xbf16>"], [
+        "%0 = stablehlo.dot_general %arg0, %arg1, contracting_dims = [1] x [1] : "
+        "(tensor<16x64xbf16>, tensor<32x64xbf16>) -> tensor<16x32xbf16>",
+        "return %0 : tensor<16x32xbf16>",
+    ])
+    assert "stablehlo.dot_general" in _unsupported(text)
+
+
+def test_gemm_alignment_is_checked_at_compile():
+    assert "multiples of 8" in _unsupported(P.matmul(16, 60, 32))
+
+
+def test_broken_softmax_is_not_fused():
+    # The max is taken over another tensor: not a softmax, and the row
+    # broadcast it needs has no elementwise route.
+    text = P.softmax(8, 16).replace(
+        "%0 = stablehlo.reduce(%arg0 init: %cst)", "%0 = stablehlo.reduce(%arg1 init: %cst)").replace(
+        "@main(%arg0: tensor<8x16xf32>)", "@main(%arg0: tensor<8x16xf32>, %arg1: tensor<8x16xf32>)")
+    assert "broadcast" in _unsupported(text)
+
+
+def test_argmax_values_result_is_rejected():
+    text = P.argmax(4, 8).replace("return %1#1 : tensor<4xi32>", "return %1#0 : tensor<4xf32>").replace(
+        "-> (tensor<4xi32> {", "-> (tensor<4xf32> {")
+    assert "argmax" in _unsupported(text)
+
+
+@pytest.mark.parametrize("text", [
+    "this is not stablehlo",
+    "module @m {\n  func.func public @main(%arg0: tensor<4xf32>) -> tensor<4xf32> {\n"
+    "    %0 = stablehlo.add %arg0, %undefined : tensor<4xf32>\n    return %0 : tensor<4xf32>\n  }\n}\n",
+    "module @m {\n  func.func public @main(%arg0: tensor<4xq7>) -> tensor<4xf32> {\n"
+    "    return %arg0 : tensor<4xf32>\n  }\n}\n",
+])
+def test_malformed_text_is_invalid_argument(text):
+    with pytest.raises(rt.PluginError) as ei:
+        rt.compile_check(text)
+    assert ei.value.code == rt.INVALID_ARGUMENT
+
+
+def test_bytecode_is_unimplemented():
+    with pytest.raises(rt.PluginError) as ei:
+        rt.compile_check(b"ML\xefR\x00\x01\x02")
+    assert ei.value.code == rt.UNIMPLEMENTED
+    assert "bytecode" in ei.value.message
+
+
+def test_client_without_device_is_unavailable():
+    try:
+        c = rt.Client()
+    except rt.PluginError as e:
+        assert e.code == rt.UNAVAILABLE
+        return
+    c.close()
+    pytest.skip("a HIP device is visible")
+
+
+def test_event_lifecycle():
+    e = rt.Event.create()
+    assert not e.is_ready()
+    with pytest.raises(rt.PluginError) as ei:
+        e.error()
+    assert ei.value.code == rt.FAILED_PRECONDITION
+    with pytest.raises(rt.PluginError) as ei:
+        e.wait(20)
+    assert ei.value.code == rt.DEADLINE_EXCEEDED
+    seen = []
+    e.on_ready(seen.append)
+    assert seen == []
+    e.set()
+    assert seen == [None] and e.is_ready()
+    e.error()
+    e.wait(0)
+    late = []
+    e.on_ready(late.append)  # already ready: runs inline
+    assert late == [None]
+
+
+def test_event_error_reaches_waiters_and_callbacks():
+    e = rt.Event.create()
+    seen = []
+    e.on_ready(seen.append)
+    e.set(rt.INTERNAL, "device lost")
+    assert seen[0].code == rt.INTERNAL and seen[0].message == "device lost"
+    for call in (lambda: e.wait(10), e.error):
+        with pytest.raises(rt.PluginError) as ei:
+            call()
+        assert ei.value.code == rt.INTERNAL and ei.value.message == "device lost"
+
+
+def test_event_timeout_from_environment(monkeypatch):
+    monkeypatch.setenv("MK_COMPLETION_TIMEOUT_MS", "30")
+    e = rt.Event.create()
+    with pytest.raises(rt.PluginError) as ei:
+        e.wait()  # negative timeout: the environment value
+    assert ei.value.code == rt.DEADLINE_EXCEEDED
+    assert "30 ms" in ei.value.message
