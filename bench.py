@@ -227,6 +227,68 @@ def _hbm_entry(gbs, us, extra=None):
     return e
 
 
+def traffic_from_profiles(kernel):
+    """Measured HBM bytes per launch of `kernel`, from the committed rocprof
+    PMC summary profiles/<kernel>_traffic.md (FETCH_SIZE + WRITE_SIZE per
+    dispatch, scaled by the copy-kernel calibration it records), or None."""
+    path = os.path.join(REPO, "profiles", f"{kernel}_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
+def profile_run(torch, ops, kind, steps):
+    """Eager (no graph) launches of one kernel for PMC collection, followed by
+    a plain 256 MiB device copy (8 times) that calibrates FETCH_SIZE and
+    WRITE_SIZE.  Returns the kernel's mean time per launch (HIP events on the
+    launch stream)."""
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        if kind == "int4":
+            from oracle import quant
+            M, K, N = 16, 4096, 14336
+            rng = np.random.default_rng(0)
+            x, packed, s, z = quant.make_int4_case(rng, M, K, N)
+            xd = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).cuda()
+            wd, zd = torch.from_numpy(packed).cuda(), torch.from_numpy(z).cuda()
+            sd = torch.from_numpy(s.view(np.int16)).view(torch.bfloat16).cuda()
+            yd = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+
+            def fn():
+                ops.int4_g64_matmul(xd, wd, sd, zd, out=yd)
+        elif kind == "gemm":
+            g = torch.Generator(device="cuda").manual_seed(0)
+            a = (torch.randn((4096, 4096), device="cuda", generator=g) / 8).to(torch.bfloat16)
+            b = (torch.randn((4096, 4096), device="cuda", generator=g) / 8).to(torch.bfloat16)
+            c = torch.empty((4096, 4096), dtype=torch.bfloat16, device="cuda")
+
+            def fn():
+                ops.gemm_bf16(a, b, out=c)
+        else:
+            raise SystemExit(f"bench.py: unknown --profile kind {kind}")
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(steps):
+            fn()
+        end.record(stream)
+        torch.cuda.synchronize()
+        t = start.elapsed_time(end) / 1e3 / steps
+        src = torch.empty(256 * 2 ** 20, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(8):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+    return t
+
+
 def cpu_baseline_int4(target_s, M=16, K=4096, N=14336):
     """Time the oracle's C port (OpenMP) on a column slice of the headline
     case, sized to roughly target_s seconds; report GB/s of the same
@@ -272,7 +334,11 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list of secondary workloads (int8,gemm,softmax,rmsnorm,argmax,chain6)")
+                    help="comma list of secondary workloads (int8,gemm,softmax,rmsnorm,argmax,chain6), "
+                         "or 'none'")
+    ap.add_argument("--profile", default="",
+                    help="int4 | gemm: eager launches of one kernel plus a 256 MiB copy calibration, "
+                         "for rocprofv3 --pmc runs (prints the kernel's us/launch)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one MI355X only (asked for --gpus {args.gpus}); "
@@ -284,6 +350,11 @@ def main():
     from mi355x import ops
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.profile:
+        t = profile_run(torch, ops, args.profile, args.steps)
+        print(json.dumps({"profile": args.profile, "us_per_launch": round(t * 1e6, 3), "steps": args.steps}),
+              flush=True)
+        return
     only = set(filter(None, args.only.split(",")))
 
     log(f"[bench] int4 g64 M=16 K=4096 N=14336: steps={args.steps} warmup={args.warmup}")
@@ -309,7 +380,8 @@ def main():
         secondary["bf16_gemm_4096"] = {
             "value": round(rg["tflops"], 2), "unit": "TFLOP/s", "us_per_call": round(rg["sec_per_call"] * 1e6, 3),
             "roofline": {"bound": "mfma", "achieved": round(rg["tflops"], 2), "peak": BF16_PEAK_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(rg["tflops"] / BF16_PEAK_TFLOPS, 4), "traffic": None}}
+                         "unit": "TFLOP/s", "frac": round(rg["tflops"] / BF16_PEAK_TFLOPS, 4),
+                         "traffic": traffic_from_profiles("gemm_bf16_256_kernel_4096")}}
         rb = bench_gemm_bf16(torch, ops, max(50, args.steps // 20), 5, batch=16, M=2048, N=2048, K=128)
         gbs = rb["bytes"] / rb["sec_per_call"] / 1e9
         log(f"[bench] batched bf16 gemm: {rb['sec_per_call'] * 1e6:.1f} us, {rb['tflops']:.1f} TFLOP/s, {gbs:.0f} GB/s")
@@ -353,7 +425,8 @@ def main():
                                "(packed [2048,14336] u8, bf16 scale + u8 zero per 64 k), bf16 out",
                    "M": 16, "K": 4096, "N": 14336, "input_sets": r4["nsets"]},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_profiles("int4g64_stream_kernel_M16_K4096_N14336")},
         "cpu_baseline": cpu,
         "secondary": secondary,
     }
