@@ -56,10 +56,12 @@ const char* mk_version(void);
  *              y = x @ (w * scale), bf16 [M, N], f32 accumulation.
  *
  * Both need K % 64 == 0 and N % 8 == 0.  `workspace` receives split-K
- * partial sums when a call splits K across workgroups (small N, or x too
- * large for LDS); mk_qmatmul_workspace_bytes gives the size, 0 when none is
- * needed (then workspace may be NULL).  Its contents need no initialisation.
- * Calls that share a workspace must be ordered (same stream).
+ * partial sums when a call splits K across workgroups;
+ * mk_qmatmul_workspace_bytes gives the size, 0 when none is needed (then
+ * workspace may be NULL).  Its first 64 KB hold per-tile arrival counters:
+ * zero-fill a workspace once before its first use; every completed call
+ * leaves the counters at zero again.  Calls that share a workspace must be
+ * ordered (same stream).
  * ---------------------------------------------------------------------- */
 enum { MK_QFMT_INT4_G64 = 0, MK_QFMT_INT8_PC = 1 };
 

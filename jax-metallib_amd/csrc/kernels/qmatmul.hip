@@ -59,6 +59,7 @@ struct QArgs {
   int ks;            // workgroups per column tile (split-K)
   int kwave;         // k handled by one wave (multiple of 64)
   int wave_lds;      // bytes of LDS per wave (x staging, then partial y)
+  uint32_t* cnt;     // wide kernel, ks > 1: per-tile arrival counters (zero between calls)
 };
 
 // Stage this wave's x block [16 rows][kwave] into LDS as 16-byte MFMA A
@@ -577,6 +578,323 @@ __global__ __launch_bounds__(8 * kWave) void int4g64_stream_kernel(QArgs a) {
   reduce_and_store<8, false>(a, smem, ksi, rb, m0, mrows, n0);
 }
 
+// ---------------------------------------------------------------------------
+// Wide int4 kernel: 256 output columns per workgroup.
+//
+// The 64-column kernel above streams 64-byte strips of every weight row and
+// DMAs one 1 KB x slice per 1 KB of weights, so half of its L2->LDS traffic is
+// re-reads of x.  Here a workgroup owns 256 columns (256-byte row segments;
+// x is 1/5 of the traffic) and K is split over `ks` workgroups to fill the
+// chip.  Each of the 8 waves covers all 256 columns over its own G groups of
+// 64 k, with a private DMA ring of R 32-k steps (normally all of them, issued
+// at once): slot = 16 weight rows x 256 B, 16-column chunk c of row r at
+// position c ^ (r & 7) ^ 8 (c & 1), so the transposing reads below are
+// conflict-free.  x goes straight to registers as whole lines.
+// ds_read_b64_tr_b8 hands MFMA lane (c, j) the bytes of column c of two
+// column blocks in rows 4j..4j+3 of a step, i.e. its B fragments for two
+// MFMAs; the bytes become bf16 (128 + q) in registers as in the kernels above.  Scales
+// and zero points come from tr16 / tr8 reads of the wave's scale block.
+//
+// Split-K partials are combined in the kernel: every workgroup writes its
+// f32 partial with device-coherent (sc1) stores, waits for them, and bumps
+// the tile's arrival counter with a device-scope atomic; the last arriver
+// reads the other partials with device-coherent loads, sums all of them in
+// k order (so results do not depend on arrival order), writes bf16 y and
+// resets the counter.  No workgroup waits on another and no cache-wide
+// fence is needed.
+// ---------------------------------------------------------------------------
+constexpr int kWideTN = 256;
+constexpr int kWideSlot = 4 * 1024;   // one 32-k step: 16 weight rows x 256 B
+constexpr int kWideRedStride = kWideTN + 4;  // padded f32 row of the y spill
+constexpr int kWideCounters = 16384;  // counter slots at the start of the workspace
+constexpr size_t kWidePartOffset = 64 * 1024;
+
+// LDS position of weight chunk ch (16 columns) in slot row r:
+// ch ^ (r & 7) ^ 8 (ch & 1).  A transposing read of the chunk pair (b, b+1),
+// b even, then touches 16 distinct positions across rows 0..7 (conflict-free),
+// and wide_pos(hi, r) is the lane constant K with position = b ^ K for
+// chunk b + hi.
+__device__ __forceinline__ int wide_pos(int hi, int r) { return hi ^ (r & 7) ^ (8 * hi); }
+// Inverse: the chunk stored at position p of row r.
+__device__ __forceinline__ int wide_chunk(int p, int r) {
+  const int c0 = (p ^ r) & 1;
+  return p ^ (r & 7) ^ (8 * c0);
+}
+
+// Eight transposing byte reads.
+__device__ __forceinline__ void lds_tr8x8(const uint32_t (&ad)[8], u32x2 (&o)[8]) {
+  asm volatile(
+      "ds_read_b64_tr_b8 %0, %8\n\t"
+      "ds_read_b64_tr_b8 %1, %9\n\t"
+      "ds_read_b64_tr_b8 %2, %10\n\t"
+      "ds_read_b64_tr_b8 %3, %11\n\t"
+      "ds_read_b64_tr_b8 %4, %12\n\t"
+      "ds_read_b64_tr_b8 %5, %13\n\t"
+      "ds_read_b64_tr_b8 %6, %14\n\t"
+      "ds_read_b64_tr_b8 %7, %15\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&v"(o[4]), "=&v"(o[5]), "=&v"(o[6]),
+        "=&v"(o[7])
+      : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3]), "v"(ad[4]), "v"(ad[5]), "v"(ad[6]), "v"(ad[7])
+      : "memory");
+}
+
+// Scales of one group for all 16 column blocks (4 tr16 reads: 4 blocks
+// each) and its zero points (2 tr8 reads: 8 blocks each).
+__device__ __forceinline__ void lds_scale_zero(uint32_t sa, uint32_t za, u32x2 (&sv)[4], u32x2 (&zv)[2]) {
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %6\n\t"
+      "ds_read_b64_tr_b16 %1, %6 offset:128\n\t"
+      "ds_read_b64_tr_b16 %2, %6 offset:256\n\t"
+      "ds_read_b64_tr_b16 %3, %6 offset:384\n\t"
+      "ds_read_b64_tr_b8 %4, %7\n\t"
+      "ds_read_b64_tr_b8 %5, %7 offset:128\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(sv[0]), "=&v"(sv[1]), "=&v"(sv[2]), "=&v"(sv[3]), "=&v"(zv[0]), "=&v"(zv[1])
+      : "v"(sa), "v"(za)
+      : "memory");
+}
+
+// Four device-coherent 16-byte loads (sc1: they miss the local L2) in flight
+// together.
+__device__ __forceinline__ void ld4_sc1(const float* p0, const float* p1, const float* p2, const float* p3,
+                                        f32x4& v0, f32x4& v1, f32x4& v2, f32x4& v3) {
+  asm volatile(
+      "global_load_dwordx4 %0, %4, off sc1\n\t"
+      "global_load_dwordx4 %1, %5, off sc1\n\t"
+      "global_load_dwordx4 %2, %6, off sc1\n\t"
+      "global_load_dwordx4 %3, %7, off sc1\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3)
+      : "v"(p0), "v"(p1), "v"(p2), "v"(p3)
+      : "memory");
+}
+
+// y quads of this thread = the KS split-K partials (this workgroup's among
+// them, already acknowledged) summed in k order.
+template <int KS>
+__device__ __forceinline__ void wide_sum_partials(const float* tile_part, f32x4 (&own)[2]) {
+  f32x4 v[2][KS];
+  const float* src[2][KS];
+#pragma unroll
+  for (int it = 0; it < 2; ++it)
+#pragma unroll
+    for (int k2 = 0; k2 < KS; ++k2)
+      src[it][k2] = tile_part + (size_t)k2 * kQRows * kWideTN + 4 * (threadIdx.x + 8 * kWave * it);
+  if constexpr (KS == 2) {
+    ld4_sc1(src[0][0], src[0][1], src[1][0], src[1][1], v[0][0], v[0][1], v[1][0], v[1][1]);
+  } else {
+#pragma unroll
+    for (int it = 0; it < 2; ++it)
+#pragma unroll
+      for (int k2 = 0; k2 < KS; k2 += 4)
+        ld4_sc1(src[it][k2], src[it][k2 + 1], src[it][k2 + 2], src[it][k2 + 3], v[it][k2], v[it][k2 + 1],
+                v[it][k2 + 2], v[it][k2 + 3]);
+  }
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    f32x4 acc = v[it][0];
+#pragma unroll
+    for (int k2 = 1; k2 < KS; ++k2) acc += v[it][k2];
+    own[it] = acc;
+  }
+}
+
+template <int G, int R>  // G 64-k groups per wave; ring of R 32-k steps
+__global__ __launch_bounds__(8 * kWave) void int4g64_wide_kernel(QArgs a) {
+  constexpr int TN = kWideTN, NB = TN / 16, S = 2 * G;
+  constexpr int DPS = TN / 64;                             // weight DMAs per step
+  constexpr int SB = ((G * TN * 2 + 1023) / 1024) * 1024;  // scale block bytes
+  constexpr int ZB = ((G * TN + 1023) / 1024) * 1024;      // zero-point block bytes
+  static_assert(R >= 2 && R <= S && G <= 4, "ring holds both steps of a group");
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const uint32_t L = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int tile = (int)(L / (uint32_t)a.ks);
+  const int ksi = (int)(L - (uint32_t)tile * a.ks);
+  const int rb = blockIdx.y;
+  const int m0 = rb * kQRows;
+  const int mrows = min(kQRows, a.M - m0);
+  const int n0 = tile * TN;
+  const int c = lane & 15, j = lane >> 4;
+  const int kbeg = ksi * (a.K / a.ks) + wv * 64 * G;
+  const size_t N = (size_t)a.N;
+  unsigned char* wl = smem + wv * a.wave_lds;
+  unsigned char* ring = wl;
+  unsigned char* sblk = wl + R * kWideSlot;
+  unsigned char* zblk = sblk + SB;
+
+  // k order inside each 64-k group g: MFMA lane group j, half h (of the two
+  // MFMAs) covers k = kbeg + 64 g + 16 j + 8 h .. +7, so a lane's x for a
+  // group is 16 contiguous bf16 and a row of x is read as whole lines.  x
+  // goes straight to registers (all groups, issued first).
+  u32x4 xr[G][2];
+  {
+    const uint16_t* xp = a.x + (size_t)min(m0 + c, a.M - 1) * a.K + kbeg + 16 * j;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      xr[g][0] = *reinterpret_cast<const u32x4*>(xp + 64 * g);
+      xr[g][1] = *reinterpret_cast<const u32x4*>(xp + 64 * g + 8);
+    }
+  }
+  // Scale rows [G][TN] bf16 and zero rows [G][TN] u8 of this wave's groups
+  // (rows past G repeat the last one; never used).
+#pragma unroll
+  for (int q = 0; q < SB / 1024; ++q) {
+    const int b = q * 1024 + 16 * lane;
+    const int g = min(b / (2 * TN), G - 1), col = (b % (2 * TN)) / 2;
+    dma16(reinterpret_cast<const uint16_t*>(a.s) + (size_t)((kbeg >> 6) + g) * N + n0 + col, sblk + q * 1024);
+  }
+#pragma unroll
+  for (int q = 0; q < ZB / 1024; ++q) {
+    const int b = q * 1024 + 16 * lane;
+    const int g = min(b / TN, G - 1), col = b % TN;
+    dma16(a.z + (size_t)((kbeg >> 6) + g) * N + n0 + col, zblk + q * 1024);
+  }
+
+  // Step t = 2g + h: weight DMA q (= MFMA lane group j) lane L fills slot
+  // row rr = 4q + L/16 (W row kbeg/2 + 32 g + 8 q + 4 h + L/16), chunk
+  // position p = L%16 from global chunk wide_chunk(p, rr).
+  const uint8_t* wsrc[DPS];
+  int wch[DPS];
+#pragma unroll
+  for (int q = 0; q < DPS; ++q) {
+    const int rr = 4 * q + (lane >> 4);
+    wsrc[q] = a.w + (size_t)(kbeg / 2 + 8 * q + (lane >> 4)) * N + n0 + 16 * wide_chunk(lane & 15, rr);
+  }
+  auto issue = [&](int t) {
+    unsigned char* slot = ring + (t % R) * kWideSlot;
+    const int g = t >> 1, h = t & 1;
+#pragma unroll
+    for (int q = 0; q < DPS; ++q) dma16(wsrc[q] + (size_t)(32 * g + 4 * h) * N, slot + q * 1024);
+  };
+#pragma unroll
+  for (int t = 0; t < R; ++t) issue(t);
+
+  // Per-lane LDS offsets.  Transposing weight read of lane (c, j) for the
+  // column-block pair (b, b+1), b even: lane pair (2r, 2r+1) of each 16-lane
+  // group names the two 8-byte halves of row r; rows r < 4 are slot row
+  // 4j + r at chunk b, rows r >= 4 slot row 4j + r - 4 at chunk b + 1.  The
+  // chunk position is then b ^ (a lane constant), so the address of pair b
+  // is wbase ^ (16 b).
+  const int r8 = (lane & 15) >> 1, hi = r8 >> 2;
+  const int wrow = 4 * j + (r8 & 3);
+  const uint32_t woff = (uint32_t)(wrow * TN + 8 * (lane & 1) + 16 * wide_pos(hi, wrow));
+  const uint32_t ring0 = lds_addr(ring);
+  // Scale tr16 read: lane 4r + q of a group names row (block) r, columns 4q..4q+3.
+  const uint32_t soff = lds_addr(sblk) + (uint32_t)(((lane & 15) >> 2) * 32 + 8 * (lane & 3));
+  const uint32_t zoff = lds_addr(zblk) + (uint32_t)(r8 * 16 + 8 * (lane & 1));
+
+  const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0
+  const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+  f32x4 y[NB], acc[NB], xs;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) y[b] = zero4;
+
+#pragma unroll
+  for (int t = 0; t < S; ++t) {
+    const int g = t >> 1, h = t & 1;
+    const int issued = (R + t < S) ? R + t : S;  // steps issued before this wait
+    vm_wait(DPS * (issued - (t + 1)));
+    const uint32_t wb = ring0 + (uint32_t)((t % R) * kWideSlot) + woff;
+    u32x2 w2[NB / 2];
+    {
+      uint32_t ad[8];
+#pragma unroll
+      for (int p = 0; p < 8; ++p) ad[p] = wb ^ (uint32_t)(32 * p);
+      lds_tr8x8(ad, w2);
+    }
+    // This step's slot is read: refill it.
+    if (t + R < S) issue(t + R);
+
+    // x slot order k0 k2 k4 k6 k1 k3 k5 k7 (matches unpack_int4).
+    const u32x4 v = xr[g][h];
+    const u32x4 A = {perm(v.y, v.x, 0x05040100u), perm(v.w, v.z, 0x05040100u), perm(v.y, v.x, 0x07060302u),
+                     perm(v.w, v.z, 0x07060302u)};
+    xs = mfma16x16x32(A, ones, h ? xs : zero4);
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+      acc[b] = mfma16x16x32(A, unpack_int4((b & 1) ? w2[b >> 1].y : w2[b >> 1].x), h ? acc[b] : zero4);
+    if (h) {
+      u32x2 sv[4], zv[2];
+      lds_scale_zero(soff + (uint32_t)(g * 2 * TN), zoff + (uint32_t)(g * TN), sv, zv);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const uint32_t sw = (b & 2) ? sv[b >> 2].y : sv[b >> 2].x;
+        const float sf = __uint_as_float((b & 1) ? (sw & 0xFFFF0000u) : (sw << 16));
+        const uint32_t zw = (b & 4) ? zv[b >> 3].y : zv[b >> 3].x;
+        const float cz = 128.f + (float)((zw >> (8 * (b & 3))) & 0xFFu);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[b][i] = fmaf(sf, fmaf(-cz, xs[i], acc[b][i]), y[b][i]);
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // Sum the 8 waves: each spills y as [16 m][TN] f32 (padded rows) into its
+  // own region; lane (c, j) holds column 16b + c, rows 4j..4j+3.
+  float* red = reinterpret_cast<float*>(wl);
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[(4 * j + i) * kWideRedStride + 16 * b + c] = y[b][i];
+  __syncthreads();
+  f32x4 own[2];
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int q = threadIdx.x + 8 * kWave * it;  // quad index: 16 rows x 64 quads
+    const int m = q >> 6, n = 4 * (q & 63);
+    f32x4 acc = zero4;
+#pragma unroll
+    for (int w = 0; w < 8; ++w)
+      acc += *reinterpret_cast<const f32x4*>(smem + w * a.wave_lds + (m * kWideRedStride + n) * 4);
+    own[it] = acc;
+  }
+  const int ntiles = a.N / TN;
+  if (a.ks > 1) {
+    const size_t tbase = ((size_t)(rb * ntiles + tile) * a.ks) * kQRows * TN;
+    // Device-coherent 16-byte stores (sc1: written through past the per-XCD
+    // L2), then wait for their acknowledgement.
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int q = threadIdx.x + 8 * kWave * it;
+      float* dst = a.part + tbase + (size_t)ksi * kQRows * TN + 4 * q;
+      asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(dst), "v"(own[it]) : "memory");
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // partial stores acknowledged
+    __syncthreads();  // (also: every wave is done reading the spills)
+    // The flag lives in dynamic LDS: a static __shared__ would shift the
+    // dynamic base off the 256-byte alignment the swizzled addressing needs.
+    volatile uint32_t* flag = reinterpret_cast<volatile uint32_t*>(smem);
+    if (threadIdx.x == 0) {
+      uint32_t* ctr = a.cnt + rb * ntiles + tile;
+      asm volatile("" : "+v"(ctr));  // per-lane address: a vector atomic
+      const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t last = old == (uint32_t)(a.ks - 1);
+      if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *flag = last;
+    }
+    __syncthreads();
+    if (!*flag) return;
+    // Device-coherent 16-byte loads (sc1: miss the local L2) of every
+    // partial, then the sum in k order.
+    switch (a.ks) {
+      case 2: wide_sum_partials<2>(a.part + tbase, own); break;
+      case 4: wide_sum_partials<4>(a.part + tbase, own); break;
+      default: wide_sum_partials<8>(a.part + tbase, own); break;
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int q = threadIdx.x + 8 * kWave * it;
+    const int m = q >> 6, n = n0 + 4 * (q & 63);
+    if (m < mrows)
+      *reinterpret_cast<u32x2*>(a.y + (size_t)(m0 + m) * N + n) =
+          u32x2{pack_bf16x2(own[it].x, own[it].y), pack_bf16x2(own[it].z, own[it].w)};
+  }
+}
+
 template <int S, int R>  // 32-k steps per wave, ring of R steps (3 KB each)
 __global__ __launch_bounds__(8 * kWave) void int8pc_stream_kernel(QArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -671,6 +989,7 @@ struct QPlan {
   int ks, nw, kwave, ntiles, rowblocks, wave_lds;
   int stream_steps;  // > 0: streaming kernel with this many 32-k steps per wave
   int ring;          // int8 streaming kernel: ring slots
+  int wide_groups;   // > 0: wide int4 kernel with this many 64-k groups per wave
   size_t lds_bytes;
   int64_t part_bytes;
 };
@@ -725,13 +1044,57 @@ bool plan_stream(int fmt, int64_t K, int64_t N, QPlan* p) {
   return false;
 }
 
+// Wide int4 kernel: N % 256 == 0, K = ks * 8 * 64 * G with G in {1, 2, 4};
+// the fewest splits that give >= 192 workgroups (the most the 64 KB counter
+// region and G >= 1 allow).  Grids below 128 workgroups stay on the
+// 64-column kernels.  MK_QMM_WIDE=0 disables it.
+bool plan_wide(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p) {
+  const char* env = getenv("MK_QMM_WIDE");
+  if (fmt != MK_QFMT_INT4_G64 || N % mk::kWideTN != 0 || K % 512 != 0 || (env && env[0] == '0')) return false;
+  const int ntiles = (int)(N / mk::kWideTN);
+  const int rb = (int)((M + mk::kQRows - 1) / mk::kQRows);
+  const int ks_env = env_int("MK_QMM_KS", 0);
+  int best = 0;
+  for (int ks = 1; ks <= 8; ks *= 2) {
+    if (ks_env > 0 && ks != ks_env) continue;
+    if (K % ((int64_t)ks * 512) != 0) break;
+    const int64_t G = K / ((int64_t)ks * 512);
+    if (G > 4) continue;
+    if (G != 1 && G != 2 && G != 4) continue;
+    if (ks > 1 && (int64_t)rb * ntiles > mk::kWideCounters) break;
+    best = ks;
+    if ((int64_t)ntiles * rb * ks >= 192) break;
+  }
+  if (best == 0 || (int64_t)ntiles * rb * best < 128) return false;
+  const int G = (int)(K / ((int64_t)best * 512));
+  const int R = G == 4 ? 4 : 2 * G;
+  const int sb = ((G * mk::kWideTN * 2 + 1023) / 1024) * 1024, zb = ((G * mk::kWideTN + 1023) / 1024) * 1024;
+  int wl = R * mk::kWideSlot + sb + zb;
+  wl = std::max(wl, mk::kQRows * mk::kWideRedStride * 4);
+  wl = (wl + 255) & ~255;
+  p->ks = best;
+  p->nw = 8;
+  p->ntiles = ntiles;
+  p->rowblocks = rb;
+  p->wide_groups = G;
+  p->kwave = 64 * G;
+  p->wave_lds = wl;
+  p->lds_bytes = (size_t)8 * wl;
+  p->part_bytes = best > 1 ? (int64_t)mk::kWidePartOffset + (int64_t)rb * ntiles * best * mk::kQRows * mk::kWideTN * 4
+                           : 0;
+  return p->lds_bytes <= kMaxLds;
+}
+
 bool plan_q(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p) {
-  p->ntiles = (int)((N + mk::kQCols - 1) / mk::kQCols);
-  p->rowblocks = (int)((M + mk::kQRows - 1) / mk::kQRows);
   p->stream_steps = 0;
   p->ring = 0;
+  p->wide_groups = 0;
+  if (plan_wide(fmt, M, K, N, p)) return true;
+  p->wide_groups = 0;
+  p->ntiles = (int)((N + mk::kQCols - 1) / mk::kQCols);
+  p->rowblocks = (int)((M + mk::kQRows - 1) / mk::kQRows);
   if (plan_stream(fmt, K, N, p)) {
-    p->part_bytes = p->ks > 1 ? (int64_t)p->rowblocks * p->ks * mk::kQRows * N * 4 : 0;
+    p->part_bytes = p->ks > 1 ? (int64_t)mk::kWidePartOffset + (int64_t)p->rowblocks * p->ks * mk::kQRows * N * 4 : 0;
     return true;
   }
   const int ks_env = env_int("MK_QMM_KS", 0), nw_env = env_int("MK_QMM_NW", 0);
@@ -760,7 +1123,7 @@ bool plan_q(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p) {
   // Grid too small even at the largest split tried: keep the first plan that
   // fits (fewest partials) rather than fail.
 done:
-  p->part_bytes = p->ks > 1 ? (int64_t)p->rowblocks * p->ks * mk::kQRows * N * 4 : 0;
+  p->part_bytes = p->ks > 1 ? (int64_t)mk::kWidePartOffset + (int64_t)p->rowblocks * p->ks * mk::kQRows * N * 4 : 0;
   return true;
 }
 
@@ -771,6 +1134,16 @@ hipError_t lds_opt_in(const void* fn, size_t bytes) {
 }
 
 hipError_t launch_reduce(int fmt, const mk::QArgs& a, hipStream_t st);
+
+template <int G>
+hipError_t launch_wide(const mk::QArgs& a, const QPlan& p, hipStream_t st) {
+  constexpr int R = G == 4 ? 4 : 2 * G;
+  dim3 grid(p.ntiles * p.ks, p.rowblocks), block(8 * mk::kWave);
+  hipError_t e = lds_opt_in((const void*)mk::int4g64_wide_kernel<G, R>, p.lds_bytes);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((mk::int4g64_wide_kernel<G, R>), grid, block, p.lds_bytes, st, a);
+  return hipGetLastError();
+}
 
 template <int S>
 hipError_t launch_stream(int fmt, const mk::QArgs& a, const QPlan& p, hipStream_t st) {
@@ -840,16 +1213,27 @@ int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, v
   a.s = s;
   a.z = static_cast<const uint8_t*>(z);
   a.y = static_cast<uint16_t*>(y);
-  a.part = p.part_bytes > 0 ? static_cast<float*>(ws) : nullptr;
+  // Workspace: [0, 64 KB) arrival counters of the wide kernel (zero between
+  // calls), then split-K partials for whichever kernel runs.
+  a.part = p.part_bytes > 0 ? reinterpret_cast<float*>(static_cast<unsigned char*>(ws) + mk::kWidePartOffset)
+                            : nullptr;
   a.M = (int)M;
   a.K = (int)K;
   a.N = (int)N;
   a.ks = p.ks;
   a.kwave = p.kwave;
   a.wave_lds = p.wave_lds;
+  a.cnt = nullptr;
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e;
-  if (p.stream_steps > 0) {
+  if (p.wide_groups > 0) {
+    if (p.part_bytes > 0) a.cnt = static_cast<uint32_t*>(ws);
+    switch (p.wide_groups) {
+      case 1: e = launch_wide<1>(a, p, st); break;
+      case 2: e = launch_wide<2>(a, p, st); break;
+      default: e = launch_wide<4>(a, p, st); break;
+    }
+  } else if (p.stream_steps > 0) {
     switch (p.stream_steps) {
       case 16: e = launch_stream<16>(fmt, a, p, st); break;
       case 8: e = launch_stream<8>(fmt, a, p, st); break;

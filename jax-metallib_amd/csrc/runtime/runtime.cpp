@@ -322,8 +322,13 @@ mkrt_error* prepare(mkrt_executable* x) {
     if (e != hipSuccess) return hip_error("constant upload", e);
   }
   if (x->plan.workspace_bytes > 0) {
+    // The dequant-matmul workspace starts zero-filled (its arrival counters).
     hipError_t e = c->alloc.alloc((size_t)x->plan.workspace_bytes, &x->workspace);
     if (e != hipSuccess) return hip_error("workspace allocation", e);
+    std::lock_guard<std::mutex> sg(c->stream_mu);
+    e = hipMemsetAsync(x->workspace, 0, (size_t)x->plan.workspace_bytes, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return hip_error("workspace clear", e);
   }
   for (const mkrt::Step& st : x->plan.steps) {
     if (st.kind != mkrt::ST_EW) continue;

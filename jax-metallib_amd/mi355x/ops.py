@@ -34,8 +34,9 @@ _BF16 = (torch.bfloat16, torch.int16, torch.uint16)
 
 
 def workspace(nbytes, device):
-    """A device workspace of at least nbytes, cached per device (the kernels
-    need no particular initial contents)."""
+    """A device workspace of at least nbytes, cached per device.  It starts
+    zero-filled (its first 64 KB are arrival counters that every completed
+    call leaves at zero)."""
     key = torch.device(device).index or 0
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:

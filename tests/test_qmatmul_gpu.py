@@ -130,3 +130,54 @@ def test_workspace_too_small_is_rejected_before_launch():
                                   y.data_ptr(), M, K, N, ws.data_ptr(), 16, None)
     assert rc == _lib.MK_EWORKSPACE
     assert b"workspace" in L.mk_last_error()
+
+
+# Shapes that take the 256-column kernel (mk_qmatmul plan "wide"): every
+# group count per wave (G = 1, 2, 4), split-K factors 1..8 with the in-kernel
+# last-arriver reduction, and two row blocks with a partial second block.
+WIDE_SHAPES = [
+    (16, 4096, 14336),   # ks = 4, G = 2 (the headline plan)
+    (16, 2048, 14336),   # ks = 4, G = 1
+    (1, 8192, 8192),     # ks = 8, G = 2
+    (20, 4096, 8192),    # two row blocks, ks = 4
+    (1, 2048, 65536),    # ks = 1, G = 4: no split
+]
+
+
+@pytest.mark.parametrize("M,K,N", WIDE_SHAPES)
+def test_int4_wide_kernel_matches_oracle(M, K, N):
+    ops = _ops()
+    rng = np.random.default_rng(7 * M + K + N)
+    x, packed, s, z = quant.make_int4_case(rng, M, K, N)
+    print(f"int4 wide case M={M} K={K} N={N}", flush=True)
+    y = ops.int4_g64_matmul(dev_bf16(x), dev(packed), dev_bf16(s), dev(z))
+    torch.cuda.synchronize()
+    ref = cport.int4_g64_matmul(x, packed, s, z)
+    assert_rel_close(host_bf16(y), ref, BF16_RTOL, f"int4 wide {M}x{K}x{N}")
+
+
+def test_int4_wide_kernel_deterministic_across_calls():
+    """The split-K sum runs in k order whichever workgroup arrives last, and
+    every call returns the arrival counters to zero: repeated calls give the
+    same bits."""
+    ops = _ops()
+    rng = np.random.default_rng(21)
+    x, packed, s, z = quant.make_int4_case(rng, 16, 4096, 14336)
+    args = (dev_bf16(x), dev(packed), dev_bf16(s), dev(z))
+    first = host_bf16_bits(ops.int4_g64_matmul(*args))
+    for _ in range(5):
+        assert np.array_equal(host_bf16_bits(ops.int4_g64_matmul(*args)), first)
+
+
+def test_int4_wide_and_split_k_paths_share_a_workspace():
+    """Wide-kernel calls (counters in the workspace's first 64 KB) interleaved
+    with 64-column split-K calls (partials after it) through one workspace."""
+    ops = _ops()
+    rng = np.random.default_rng(23)
+    for (M, K, N) in [(16, 4096, 14336), (16, 4096, 1024), (1, 8192, 8192), (5, 4096, 512),
+                      (16, 4096, 14336)]:
+        x, packed, s, z = quant.make_int4_case(rng, M, K, N)
+        y = ops.int4_g64_matmul(dev_bf16(x), dev(packed), dev_bf16(s), dev(z))
+        torch.cuda.synchronize()
+        ref = cport.int4_g64_matmul(x, packed, s, z)
+        assert_rel_close(host_bf16(y), ref, BF16_RTOL, f"int4 mixed {M}x{K}x{N}")
