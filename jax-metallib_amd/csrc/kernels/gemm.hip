@@ -496,6 +496,159 @@ __global__ __launch_bounds__(WM_ * WN_ * 64) void gemm_bf16_256_kernel(GemmArgs 
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// 256 x 256 tile fed by LDS DMA.
+//
+// A 4-stage ring of 32-k stages (A 256 x 32 | B 32 x 256 bf16, 32 KB each,
+// 128 KB of LDS) is filled by global_load_lds three stages ahead, so the
+// MFMAs of stage k overlap the HBM latency of stages k+1..k+3 and no staging
+// registers are needed.  Each stage takes 4 DMA instructions per wave and
+// one barrier (raw s_barrier: every thread first waits for its own DMAs of
+// the stage, so no fence drains the ring).  The DMAs are issued from inline
+// asm with explicit waits, so the compiler -- which then sees no pending
+// LDS writes -- schedules the fragment reads against the MFMAs itself.
+// LDS layouts (swizzles applied by choosing each DMA lane's source chunk):
+//   A row r (64 B): 16-byte chunk c at position c ^ (r / 4 % 4);
+//   B k row (512 B): chunk c at c ^ (2 (k % 4) + 8 (k / 8 % 2)),
+// which make the A ds_read_b128 and the B ds_read_b64_tr_b16 fragment reads
+// bank-conflict-free.  Waves 2 x 4, each 128 x 64 (8 x 4 MFMA 16x16x32
+// tiles per 32 k).
+// ---------------------------------------------------------------------------
+#ifndef MK_GEMM_STAGES
+#define MK_GEMM_STAGES 4
+#endif
+constexpr int kGemmStages = MK_GEMM_STAGES;
+constexpr int kGemmStageBytes = 32 * 1024;
+
+__device__ __forceinline__ int swz_b2(int k, int c) { return c ^ ((2 * (k & 3)) | (((k >> 3) & 1) << 3)); }
+
+// 16-byte LDS DMA of every lane (source per lane) to LDS byte address
+// lds_base + 16 * lane (lds_base wave-uniform).
+__device__ __forceinline__ void dma16_asm(const void* src, uint32_t lds_base) {
+  const uint32_t base = __builtin_amdgcn_readfirstlane(lds_base);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base) : "memory");
+}
+
+template <int WN_>  // waves 2 x WN_; each 128 x (256 / WN_)
+__global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs p) {
+  constexpr int BM = 256, BN = 256, BK = 32, TM = 8, TN = 256 / WN_ / 16;
+  constexpr int NW = 2 * WN_, DI = 16 / NW;  // waves; DMA instructions per wave for A (and B)
+  constexpr int ABYTES = BM * BK * 2;  // 16 KB
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN_, wn = wave % WN_;
+  const int tiles_m = p.M / BM, tiles_n = p.N / BN;
+  int tm, tn;
+  tile_coords(xcd_logical_id(blockIdx.x, gridDim.x), tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const uint16_t* A = static_cast<const uint16_t*>(p.a) + (size_t)blockIdx.z * p.sa + (size_t)m0 * p.K;
+  const uint16_t* B = static_cast<const uint16_t*>(p.b) + (size_t)blockIdx.z * p.sb + n0;
+  const int K = p.K, N = p.N;
+
+  // DMA sources.  A instruction i (rows 16i..16i+15): lane L fills row
+  // 16i + L/4, position L%4.  B instruction i (k rows 2i, 2i+1): lane L
+  // fills k row 2i + L/32, position L%32.  Wave w issues i = DI w .. DI w + DI - 1
+  // of each.
+  const uint16_t* asrc[DI];
+  const uint16_t* bsrc[DI];
+#pragma unroll
+  for (int u = 0; u < DI; ++u) {
+    const int i = DI * wave + u;
+    const int row = 16 * i + (lane >> 2), pa = lane & 3;
+    asrc[u] = A + (size_t)row * K + 8 * (pa ^ ((row >> 2) & 3));
+    const int kr = 2 * i + (lane >> 5), pb = lane & 31;
+    bsrc[u] = B + (size_t)kr * N + 8 * swz_b2(kr, pb);
+  }
+  const uint32_t sbase = lds_addr(smem);
+  auto issue = [&](int kt) {
+    const uint32_t st = sbase + (uint32_t)((kt % kGemmStages) * kGemmStageBytes);
+#pragma unroll
+    for (int u = 0; u < DI; ++u) dma16_asm(asrc[u] + kt * BK, st + (uint32_t)((DI * wave + u) * 1024));
+#pragma unroll
+    for (int u = 0; u < DI; ++u)
+      dma16_asm(bsrc[u] + (size_t)kt * BK * N, st + (uint32_t)(ABYTES + (DI * wave + u) * 1024));
+  };
+
+  // Fragment offsets within a stage.  A tile i of this wave: row
+  // wm*128 + 16i + (lane & 15), 16-byte chunk lane >> 4.  B tile j, low/high
+  // 4 k: tr16 lane 4r + q of 16-lane group g reads k row 8g + r (+4), columns
+  // wn*64 + 16j + 4q .. +3.
+  const int arow = wm * 128 + (lane & 15);
+  const int aoff = arow * 64 + 16 * ((lane >> 4) ^ ((arow >> 2) & 3));
+  int boff[2 * TN];
+  {
+    const int g = lane >> 4, r = (lane & 15) >> 2, q = lane & 3;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = wn * (16 * TN) + 16 * j + 4 * q;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int k1 = 8 * g + r + 4 * h;
+        boff[2 * j + h] = ABYTES + k1 * (BN * 2) + 16 * swz_b2(k1, col >> 3) + 2 * (col & 7);
+      }
+    }
+  }
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int KT = K / BK;
+  const int pre = KT < kGemmStages - 1 ? KT : kGemmStages - 1;
+  for (int kt = 0; kt < pre; ++kt) issue(kt);
+  for (int kt = 0; kt < KT; ++kt) {
+    // This thread's DMAs of stage kt have landed (later stages may not).
+    {
+      const int ahead = KT - 1 - kt < kGemmStages - 2 ? KT - 1 - kt : kGemmStages - 2;  // later stages in flight
+      vm_wait(2 * DI * ahead);
+    }
+    // Everyone's have; everyone is done reading stage kt-1's slot.
+    asm volatile("s_barrier" ::: "memory");
+    if (kt + kGemmStages - 1 < KT) issue(kt + kGemmStages - 1);
+    const unsigned char* st = smem + (kt % kGemmStages) * kGemmStageBytes;
+    u32x4 bf[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(st + boff[2 * j]));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(st + boff[2 * j + 1]));
+      const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+      bf[j] = u32x4{l2.x, l2.y, h2.x, h2.y};
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const u32x4 af = *reinterpret_cast<const u32x4*>(st + aoff + 1024 * i);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(bf[j], af, acc[i][j]);
+    }
+  }
+
+  // Epilogue (C^T tiles): lane owns row m, columns n..n+3 of each tile.
+  const int mrow = m0 + wm * (16 * TM) + (lane & 15);
+  const int ncol = n0 + wn * (16 * TN) + 4 * (lane >> 4);
+  if (p.out_f32) {
+    float* C = static_cast<float*>(p.c) + (size_t)blockIdx.z * p.sc;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        *reinterpret_cast<f32x4*>(C + (size_t)(mrow + 16 * i) * N + ncol + 16 * j) = acc[i][j];
+  } else {
+    uint16_t* C = static_cast<uint16_t*>(p.c) + (size_t)blockIdx.z * p.sc;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        u32x2 o;
+        o.x = pack_bf16x2(acc[i][j].x, acc[i][j].y);
+        o.y = pack_bf16x2(acc[i][j].z, acc[i][j].w);
+        *reinterpret_cast<u32x2*>(C + (size_t)(mrow + 16 * i) * N + ncol + 16 * j) = o;
+      }
+  }
+}
+
 }  // namespace mk
 
 // ---------------------------------------------------------------------------
@@ -570,7 +723,21 @@ extern "C" int mk_gemm_bf16(const void* a, const void* b, void* c, int64_t batch
   int tile = env_tile();
   if (tile == 0) tile = big_tiles >= 128 ? 256 : 128;
   hipError_t e;
-  if (tile == 256 && M % 256 == 0 && N % 256 == 0 && K % 64 == 0) {
+  const char* dma_env = getenv("MK_GEMM_DMA");
+  const bool dma = !(dma_env && dma_env[0] == '0');
+  if (tile == 256 && dma && M % 256 == 0 && N % 256 == 0 && K % 32 == 0) {
+    constexpr size_t lds = (size_t)mk::kGemmStages * mk::kGemmStageBytes;
+    const dim3 grid((unsigned)((M / 256) * (N / 256)), 1, (unsigned)batch);
+    const char* w = getenv("MK_GEMM_WAVES");
+    if (w && atoi(w) == 4) {
+      e = lds_opt_in((const void*)mk::gemm_bf16_256dma_kernel<2>, lds);
+      if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256dma_kernel<2>), grid, dim3(256), lds, st, p);
+    } else {
+      e = lds_opt_in((const void*)mk::gemm_bf16_256dma_kernel<4>, lds);
+      if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256dma_kernel<4>), grid, dim3(512), lds, st, p);
+    }
+    if (e == hipSuccess) e = hipGetLastError();
+  } else if (tile == 256 && M % 256 == 0 && N % 256 == 0 && K % 64 == 0) {
     constexpr size_t lds = (size_t)2 * (256 * 64 + 64 * 256) * 2;
     const dim3 grid((unsigned)((M / 256) * (N / 256)), 1, (unsigned)batch);
     const char* w = getenv("MK_GEMM_WAVES");
