@@ -26,6 +26,7 @@
 #include "../../include/mk_kernels.h"
 #include "capi_internal.h"
 #include "ew_jit.h"
+#include "kernels/ew_math.h"
 
 namespace mkc {
 namespace {
@@ -66,24 +67,14 @@ std::string generate(int dtype, const mk_ew_instr* prog, int n_instr, int n_inpu
        "typedef float f4 __attribute__((ext_vector_type(4)));\n"
        "typedef u32 u4 __attribute__((ext_vector_type(4)));\n"
        "__device__ __forceinline__ float bf2f(u32 b) { return __uint_as_float(b << 16); }\n"
-       "__device__ __forceinline__ u32 f2bf(float f) {\n"
-       "  u32 u = __float_as_uint(f);\n"
-       "  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x7fffffu)) return ((u >> 16) | 0x40u) & 0xffffu;\n"
-       "  u += 0x7fffu + ((u >> 16) & 1u);\n"
-       "  return u >> 16;\n"
-       "}\n"
        "__device__ __forceinline__ float R(float f) { return (float)(__bf16)f; }\n"
-       "__device__ __forceinline__ float lg1p_fast(float x) {\n"
-       "  const float u = 1.0f + x;\n"
-       "  return (u == 1.0f) ? x : __logf(u) * (x / (u - 1.0f)); }\n"
-       "__device__ __forceinline__ float mx(float a, float b) {\n"
-       "  if (a != a) return a; if (b != b) return b;\n"
-       "  if (a == b) return (__float_as_uint(a) & 0x80000000u) ? b : a;\n"
-       "  return a > b ? a : b; }\n"
-       "__device__ __forceinline__ float mn(float a, float b) {\n"
-       "  if (a != a) return a; if (b != b) return b;\n"
-       "  if (a == b) return (__float_as_uint(a) & 0x80000000u) ? a : b;\n"
-       "  return a < b ? a : b; }\n";
+       "typedef float f2 __attribute__((ext_vector_type(2)));\n"
+       "typedef __bf16 b2 __attribute__((ext_vector_type(2)));\n"
+       "__device__ __forceinline__ u32 P2(float a, float b) {\n"
+       "  return __builtin_bit_cast(u32, __builtin_convertvector((f2){a, b}, b2)); }\n"
+       "__device__ __forceinline__ void R2(float& a, float& b) {\n"
+       "  const u32 w = P2(a, b); a = __uint_as_float(w << 16); b = __uint_as_float(w & 0xffff0000u); }\n"
+       MK_EW_MATH_SRC "\n";
   // Element loader: vector or scalar path, or a 1-element broadcast.
   if (bf) {
     s += "__device__ __forceinline__ void ld(const void* p, long long numel, long long idx, bool vec, long long n, float* o) {\n"
@@ -96,9 +87,9 @@ std::string generate(int dtype, const mk_ew_instr* prog, int n_instr, int n_inpu
          "}\n"
          "__device__ __forceinline__ void st(void* p, long long idx, bool vec, long long n, const float* v) {\n"
          "  u16* q = (u16*)p;\n"
-         "  if (vec) { u4 w; w.x = f2bf(v[0]) | (f2bf(v[1]) << 16); w.y = f2bf(v[2]) | (f2bf(v[3]) << 16);\n"
-         "    w.z = f2bf(v[4]) | (f2bf(v[5]) << 16); w.w = f2bf(v[6]) | (f2bf(v[7]) << 16); *(u4*)(q + idx) = w; return; }\n"
-         "  for (int e = 0; e < 8; ++e) if (idx + e < n) q[idx + e] = (u16)f2bf(v[e]);\n"
+         "  if (vec) { u4 w; w.x = P2(v[0], v[1]); w.y = P2(v[2], v[3]); w.z = P2(v[4], v[5]); w.w = P2(v[6], v[7]);\n"
+         "    *(u4*)(q + idx) = w; return; }\n"
+         "  for (int e = 0; e < 8; ++e) if (idx + e < n) q[idx + e] = (u16)P2(v[e], 0.f);\n"
          "}\n";
   } else {
     s += "__device__ __forceinline__ void ld(const void* p, long long numel, long long idx, bool vec, long long n, float* o) {\n"
@@ -129,54 +120,66 @@ std::string generate(int dtype, const mk_ew_instr* prog, int n_instr, int n_inpu
     snprintf(b, sizeof(b), "    float X%d[8]; ld(i%d, n%d, idx, vec, n, X%d);\n", k, k, k, k);
     s += b;
   }
-  s += "    float res[8];\n#pragma unroll\n    for (int e = 0; e < 8; ++e) {\n";
+  // bf16 programs evaluate two elements per iteration so that each op's
+  // rounding is one packed conversion for both (R2); f32 programs go one by one.
+  const int lanes = bf ? 2 : 1;
+  s += bf ? "    float res[8];\n#pragma unroll\n    for (int e = 0; e < 8; e += 2) {\n"
+          : "    float res[8];\n#pragma unroll\n    for (int e = 0; e < 8; ++e) {\n";
   std::string slot[16];
   for (int i = 0; i < n_instr; ++i) {
     const mk_ew_instr& in = prog[i];
-    // Operand fields an op does not use may hold anything (-1 included).
-    auto src = [&](int k) { return k >= 0 && k < 16 ? slot[k] : std::string(); };
-    const std::string A = src(in.a), B = src(in.b), C = src(in.c);
-    std::string ex;
-    bool rnd = bf;
-    switch (in.op) {
-      case MK_EW_LOAD: ex = "X" + std::to_string(in.a) + "[e]"; rnd = false; break;
-      case MK_EW_CONST: ex = fmt_const(in.imm); rnd = false; break;
-      case MK_EW_ADD: ex = A + " + " + B; break;
-      case MK_EW_SUB: ex = A + " - " + B; break;
-      case MK_EW_MUL: ex = A + " * " + B; break;
-      case MK_EW_DIV: ex = A + " / " + B; break;
-      case MK_EW_MAX: ex = "mx(" + A + ", " + B + ")"; break;
-      case MK_EW_MIN: ex = "mn(" + A + ", " + B + ")"; break;
-      case MK_EW_POW: ex = "powf(" + A + ", " + B + ")"; break;
-      case MK_EW_NEG: ex = "-" + A; break;
-      case MK_EW_ABS: ex = "fabsf(" + A + ")"; break;
-      // bf16 programs round every result to 8 significant bits, so the
-      // hardware-approximation forms (relative error ~1e-6) suffice there.
-      case MK_EW_EXP: ex = (bf ? "__expf(" : "expf(") + A + ")"; break;
-      case MK_EW_LOG: ex = (bf ? "__logf(" : "logf(") + A + ")"; break;
-      case MK_EW_LOG1P: ex = (bf ? "lg1p_fast(" : "log1pf(") + A + ")"; break;
-      case MK_EW_EXPM1: ex = "expm1f(" + A + ")"; break;
-      case MK_EW_TANH: ex = "tanhf(" + A + ")"; break;
-      case MK_EW_RSQRT: ex = "1.0f / sqrtf(" + A + ")"; break;
-      case MK_EW_SQRT: ex = "sqrtf(" + A + ")"; break;
-      case MK_EW_LOGISTIC: ex = std::string("1.0f / (1.0f + ") + (bf ? "__expf(-" : "expf(-") + A + "))"; break;
-      case MK_EW_FLOOR: ex = "floorf(" + A + ")"; break;
-      case MK_EW_CEIL: ex = "ceilf(" + A + ")"; break;
-      case MK_EW_CMP_EQ: ex = "(" + A + " == " + B + ") ? 1.f : 0.f"; rnd = false; break;
-      case MK_EW_CMP_NE: ex = "(" + A + " != " + B + ") ? 1.f : 0.f"; rnd = false; break;
-      case MK_EW_CMP_LT: ex = "(" + A + " < " + B + ") ? 1.f : 0.f"; rnd = false; break;
-      case MK_EW_CMP_LE: ex = "(" + A + " <= " + B + ") ? 1.f : 0.f"; rnd = false; break;
-      case MK_EW_CMP_GT: ex = "(" + A + " > " + B + ") ? 1.f : 0.f"; rnd = false; break;
-      case MK_EW_CMP_GE: ex = "(" + A + " >= " + B + ") ? 1.f : 0.f"; rnd = false; break;
-      case MK_EW_SELECT: ex = "(" + A + " != 0.f) ? " + B + " : " + C; rnd = false; break;
-      case MK_EW_ROUND_BF16: ex = "R(" + A + ")"; rnd = false; break;
-      default: ex = A; rnd = false; break;
-    }
     const std::string v = "v" + std::to_string(i);
-    s += "      const float " + v + " = " + (rnd ? "R(" + ex + ")" : "(" + ex + ")") + ";\n";
+    bool rnd = bf;
+    std::string decl;
+    for (int l = 0; l < lanes; ++l) {
+      const std::string sfx = bf ? "_" + std::to_string(l) : std::string();
+      // Operand fields an op does not use may hold anything (-1 included).
+      auto src = [&](int k) { return k >= 0 && k < 16 && !slot[k].empty() ? slot[k] + sfx : std::string(); };
+      const std::string A = src(in.a), B = src(in.b), C = src(in.c);
+      std::string ex;
+      switch (in.op) {
+        case MK_EW_LOAD: ex = "X" + std::to_string(in.a) + (l ? "[e + 1]" : "[e]"); rnd = false; break;
+        case MK_EW_CONST: ex = fmt_const(in.imm); rnd = false; break;
+        case MK_EW_ADD: ex = A + " + " + B; break;
+        case MK_EW_SUB: ex = A + " - " + B; break;
+        case MK_EW_MUL: ex = A + " * " + B; break;
+        case MK_EW_DIV: ex = A + " / " + B; break;
+        case MK_EW_MAX: ex = "mk_max(" + A + ", " + B + ")"; break;
+        case MK_EW_MIN: ex = "mk_min(" + A + ", " + B + ")"; break;
+        case MK_EW_POW: ex = "powf(" + A + ", " + B + ")"; break;
+        case MK_EW_NEG: ex = "-" + A; break;
+        case MK_EW_ABS: ex = "fabsf(" + A + ")"; break;
+        // bf16 programs round every result to 8 significant bits, so the
+        // short exp form (relative error < 2^-16) suffices there.
+        case MK_EW_EXP: ex = (bf ? "mk_exp_bf(" : "mk_exp(") + A + ")"; break;
+        case MK_EW_LOG: ex = (bf ? "__logf(" : "logf(") + A + ")"; break;
+        case MK_EW_LOG1P: ex = "mk_log1p(" + A + ")"; break;
+        case MK_EW_EXPM1: ex = "expm1f(" + A + ")"; break;
+        case MK_EW_TANH: ex = "tanhf(" + A + ")"; break;
+        case MK_EW_RSQRT: ex = "1.0f / sqrtf(" + A + ")"; break;
+        case MK_EW_SQRT: ex = "sqrtf(" + A + ")"; break;
+        case MK_EW_LOGISTIC: ex = "1.0f / (1.0f + mk_exp(-" + A + "))"; break;
+        case MK_EW_FLOOR: ex = "floorf(" + A + ")"; break;
+        case MK_EW_CEIL: ex = "ceilf(" + A + ")"; break;
+        case MK_EW_CMP_EQ: ex = "(" + A + " == " + B + ") ? 1.f : 0.f"; rnd = false; break;
+        case MK_EW_CMP_NE: ex = "(" + A + " != " + B + ") ? 1.f : 0.f"; rnd = false; break;
+        case MK_EW_CMP_LT: ex = "(" + A + " < " + B + ") ? 1.f : 0.f"; rnd = false; break;
+        case MK_EW_CMP_LE: ex = "(" + A + " <= " + B + ") ? 1.f : 0.f"; rnd = false; break;
+        case MK_EW_CMP_GT: ex = "(" + A + " > " + B + ") ? 1.f : 0.f"; rnd = false; break;
+        case MK_EW_CMP_GE: ex = "(" + A + " >= " + B + ") ? 1.f : 0.f"; rnd = false; break;
+        case MK_EW_SELECT: ex = "(" + A + " != 0.f) ? " + B + " : " + C; rnd = false; break;
+        case MK_EW_ROUND_BF16: ex = "R(" + A + ")"; rnd = false; break;
+        default: ex = A; rnd = false; break;
+      }
+      decl += (l ? ", " : "      float ") + v + sfx + " = (" + ex + ")";
+    }
+    s += decl + ";\n";
+    if (rnd) s += "      R2(" + v + "_0, " + v + "_1);\n";
     slot[in.dst] = v;
   }
-  s += "      res[e] = " + slot[out_slot] + ";\n    }\n    st(out, idx, vec, n, res);\n  }\n}\n";
+  s += bf ? "      res[e] = " + slot[out_slot] + "_0; res[e + 1] = " + slot[out_slot] + "_1;\n"
+          : "      res[e] = " + slot[out_slot] + ";\n";
+  s += "    }\n    st(out, idx, vec, n, res);\n  }\n}\n";
   return s;
 }
 

@@ -17,6 +17,7 @@
 // ops/registry.h:273-287).  maximum/minimum propagate NaN and order -0 < +0.
 // Comparisons yield 1.0 / 0.0 (never rounded); select picks b where a != 0.
 #include "common.h"
+#include "ew_math.h"
 
 #include <math.h>
 
@@ -39,19 +40,7 @@ struct EwArgs {
 
 __device__ __forceinline__ float ew_bf16r(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
-__device__ __forceinline__ float ew_max(float a, float b) {
-  if (a != a) return a;
-  if (b != b) return b;
-  if (a == b) return (__float_as_uint(a) & 0x80000000u) ? b : a;
-  return a > b ? a : b;
-}
-
-__device__ __forceinline__ float ew_min(float a, float b) {
-  if (a != a) return a;
-  if (b != b) return b;
-  if (a == b) return (__float_as_uint(a) & 0x80000000u) ? a : b;
-  return a < b ? a : b;
-}
+MK_EW_MATH_DEFS
 
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 
@@ -178,19 +167,19 @@ __global__ __launch_bounds__(256) void eltwise_kernel(EwArgs a) {
         MK_EW_CASE(MK_EW_SUB, u - v)
         MK_EW_CASE(MK_EW_MUL, u * v)
         MK_EW_CASE(MK_EW_DIV, u / v)
-        MK_EW_CASE(MK_EW_MAX, ew_max(u, v))
-        MK_EW_CASE(MK_EW_MIN, ew_min(u, v))
+        MK_EW_CASE(MK_EW_MAX, mk_max(u, v))
+        MK_EW_CASE(MK_EW_MIN, mk_min(u, v))
         MK_EW_CASE(MK_EW_POW, powf(u, v))
         MK_EW_CASE(MK_EW_NEG, -u)
         MK_EW_CASE(MK_EW_ABS, fabsf(u))
-        MK_EW_CASE(MK_EW_EXP, expf(u))
+        MK_EW_CASE(MK_EW_EXP, BF16 ? mk_exp_bf(u) : mk_exp(u))
         MK_EW_CASE(MK_EW_LOG, logf(u))
-        MK_EW_CASE(MK_EW_LOG1P, log1pf(u))
+        MK_EW_CASE(MK_EW_LOG1P, mk_log1p(u))
         MK_EW_CASE(MK_EW_EXPM1, expm1f(u))
         MK_EW_CASE(MK_EW_TANH, tanhf(u))
         MK_EW_CASE(MK_EW_RSQRT, 1.0f / sqrtf(u))
         MK_EW_CASE(MK_EW_SQRT, sqrtf(u))
-        MK_EW_CASE(MK_EW_LOGISTIC, 1.0f / (1.0f + expf(-u)))
+        MK_EW_CASE(MK_EW_LOGISTIC, 1.0f / (1.0f + mk_exp(-u)))
         MK_EW_CASE(MK_EW_FLOOR, floorf(u))
         MK_EW_CASE(MK_EW_CEIL, ceilf(u))
         MK_EW_CASE(MK_EW_CMP_EQ, u == v ? 1.f : 0.f)

@@ -90,6 +90,80 @@ def test_binary_ops_and_special_values():
         assert np.array_equal(np.signbit(y[f]), np.signbit(ref[f])), name
 
 
+def _exp_inputs():
+    f = np.finfo(np.float32)
+    dense = np.linspace(-104.0, 89.0, 1 << 21).astype(np.float32)
+    # Around the overflow threshold ln(FLT_MAX) = 88.7228391 and the
+    # denormal range, one ulp at a time.
+    hi = np.nextafter(np.float32(88.72283), np.float32(np.inf)) + np.arange(-64, 64, dtype=np.float32) * np.float32(7.62939453125e-06)
+    special = np.array([0.0, -0.0, 1e-30, -1e-30, f.tiny, -87.33655, -103.2789, -103.9721,
+                        np.inf, -np.inf, np.nan], np.float32)
+    return np.concatenate([dense, hi.astype(np.float32), special])
+
+
+def _log1p_inputs():
+    r = np.random.default_rng(7)
+    near_m1 = (-1.0 + np.logspace(-7.2, -0.05, 1 << 18)).astype(np.float32)
+    mid = np.linspace(-0.99, 2.0, 1 << 20).astype(np.float32)
+    tiny = np.logspace(-44, -1, 1 << 18).astype(np.float32)
+    big = np.logspace(-1, 38.5, 1 << 18).astype(np.float32)
+    rnd = (r.standard_normal(1 << 18) * 0.05).astype(np.float32)
+    special = np.array([0.0, -0.0, -1.0, -1.5, 0.0625, -0.0625, np.nextafter(np.float32(0.0625), np.float32(0)),
+                        3.4e38, np.inf, -np.inf, np.nan, 1e-45], np.float32)
+    return np.concatenate([near_m1, mid, tiny, -tiny[tiny < 0.9], big, rnd, special])
+
+
+def _ulp_check_f32(y, x, ref64, max_rel):
+    """Every result within max_rel of the float64 value rounded to f32
+    (denormal results within 2 ulp of the smallest subnormal); infinities,
+    NaNs and signed zeros exactly."""
+    ref = ref64.astype(np.float32)
+    assert np.array_equal(np.isnan(y), np.isnan(ref)), x[np.isnan(y) != np.isnan(ref)][:8]
+    f = ~np.isnan(ref)
+    y, ref, xs = y[f], ref[f], x[f]
+    inf = np.isinf(ref)
+    assert np.array_equal(y[inf], ref[inf]), xs[inf][y[inf] != ref[inf]][:8]
+    zero = ref == 0
+    assert np.array_equal(np.signbit(y[zero & (xs == 0)]), np.signbit(ref[zero & (xs == 0)]))
+    fin = ~inf
+    err = np.abs(y[fin].astype(np.float64) - ref64[f][fin])
+    tol = np.maximum(max_rel * np.abs(ref64[f][fin]), 2.0 * 1.401298464324817e-45)
+    bad = err > tol
+    assert not bad.any(), (xs[fin][bad][:8], y[fin][bad][:8], ref[fin][bad][:8])
+
+
+def test_exp_log1p_accuracy_sweep_f32():
+    """mk_exp and mk_log1p against float64 over dense sweeps: within 1e-6
+    relative (8 f32 ulp; the workload's f32 tolerance is 1e-5)."""
+    ops = _ops()
+    for name, xs, fn in [("EXP", _exp_inputs(), np.exp), ("LOG1P", _log1p_inputs(), np.log1p)]:
+        prog = [("LOAD", 0, 0, 0, 0, 0.0), (name, 1, 0, 0, 0, 0.0)]
+        y = ops.elementwise(prog, [dev(xs)], out_slot=1).cpu().numpy()
+        with np.errstate(all="ignore"):
+            ref64 = fn(xs.astype(np.float64))
+        _ulp_check_f32(y, xs, ref64, 1e-6)
+
+
+def test_exp_log1p_accuracy_sweep_bf16():
+    """bf16 programs: each result is the float64 value rounded to bf16, or a
+    neighbour of it when the exact value lies within 2^-14 of a rounding
+    midpoint."""
+    ops = _ops()
+    for name, xs, fn in [("EXP", _exp_inputs(), np.exp), ("LOG1P", _log1p_inputs(), np.log1p)]:
+        xb = obf.f32_to_bf16_bits(xs)
+        xf = obf.bf16_bits_to_f32(xb)
+        prog = [("LOAD", 0, 0, 0, 0, 0.0), (name, 1, 0, 0, 0, 0.0)]
+        y = host_bf16(ops.elementwise(prog, [dev_bf16(xb)], out_slot=1))
+        with np.errstate(all="ignore"):
+            ref = obf.bf16_bits_to_f32(obf.f32_to_bf16_bits(fn(xf.astype(np.float64)).astype(np.float32)))
+        assert np.array_equal(np.isnan(y), np.isnan(ref))
+        f = ~np.isnan(ref) & ~np.isinf(ref)
+        assert np.array_equal(y[np.isinf(ref)], ref[np.isinf(ref)])
+        rel = np.abs(y[f] - ref[f]) / np.maximum(np.abs(ref[f]), 1e-38)
+        assert np.max(rel) <= 2.0 ** -7, np.max(rel)
+        assert np.mean(y[f] == ref[f]) > 0.995
+
+
 def test_scalar_broadcast_input_and_compare_select():
     ops = _ops()
     x = np.linspace(-3, 3, 4097).astype(np.float32)
