@@ -40,7 +40,8 @@ const char* mk_last_error(void);
 const char* mk_version(void);
 
 /* ------------------------------------------------------------------------
- * Quantized matmul (decode-shaped: weight-stationary, HBM bound).
+ * Quantized matmul, any M: HBM bound at decode shapes (M <= 16), MFMA bound
+ * from a few hundred rows.
  *
  * Replaces the reference's affine quantized GEMM
  * (src/jax_plugins/silicon/quantized.py:1077-1152, kernels :760-958), which
@@ -56,9 +57,10 @@ const char* mk_version(void);
  *              y = x @ (w * scale), bf16 [M, N], f32 accumulation.
  *
  * Both need K % 64 == 0 and N % 8 == 0.  `workspace` receives split-K
- * partial sums when a call splits K across workgroups;
- * mk_qmatmul_workspace_bytes gives the size, 0 when none is needed (then
- * workspace may be NULL).  Its first 64 KB hold per-tile arrival counters:
+ * partial sums when a call splits K across workgroups, and for many rows
+ * (M >= 768, or M >= 256 when N % 64 != 0) the bf16-dequantised W [K, N]
+ * that the bf16 GEMM then multiplies; mk_qmatmul_workspace_bytes gives the
+ * size, 0 when none is needed (then workspace may be NULL).  Its first 64 KB hold per-tile arrival counters:
  * zero-fill a workspace once before its first use; every completed call
  * leaves the counters at zero again.  Calls that share a workspace must be
  * ordered (same stream).

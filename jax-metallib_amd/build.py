@@ -37,6 +37,7 @@ KERNEL_SOURCES = [
     "capi.cpp",
     "ew_jit.cpp",
     "kernels/qmatmul.hip",
+    "kernels/qgemm.hip",
     "kernels/gemm.hip",
     "kernels/rowops.hip",
     "kernels/eltwise.hip",

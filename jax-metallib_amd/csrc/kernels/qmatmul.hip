@@ -892,12 +892,67 @@ __global__ __launch_bounds__(256) void qmm_splitk_reduce_kernel(QArgs a) {
   }
 }
 
+// Large-M path, first pass: the dequantised weight as bf16 [K, N] (into the
+// workspace), which the bf16 GEMM then multiplies.  int4: (q - z) * s is
+// exact in f32 (at most 12 significant bits) and rounded once to bf16 (RNE);
+// int8: w * s is rounded to f32, then to bf16.  One thread: 8
+// columns of one packed row (int4: k = 2r and 2r + 1) or of one k row (int8);
+// every load and store is a whole 8- or 16-byte vector.
+template <bool INT4>
+__global__ __launch_bounds__(256) void qmm_dequant_kernel(QArgs a, uint16_t* wd) {
+  const int N8 = a.N / 8;
+  const int64_t rows = INT4 ? a.K / 2 : a.K;
+  const int64_t total = rows * N8;
+  for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += (int64_t)gridDim.x * 256) {
+    const int64_t r = t / N8;
+    const int c0 = (int)(t - r * N8) * 8;
+    const u32x2 wb = *reinterpret_cast<const u32x2*>(a.w + r * a.N + c0);
+    if (INT4) {
+      const int64_t g = r / 32;  // 64-k group of rows 2r, 2r + 1
+      const u32x4 sb = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.s) + g * a.N + c0);
+      const u32x2 zb = *reinterpret_cast<const u32x2*>(a.z + g * a.N + c0);
+      uint32_t lo[4], hi[4];
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        float e[2], o[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int c = j + h;
+          const uint32_t byte = ((c < 4 ? wb.x : wb.y) >> (8 * (c & 3))) & 0xffu;
+          const int zz = (int)(((c < 4 ? zb.x : zb.y) >> (8 * (c & 3))) & 0xffu);
+          const uint32_t sw = (c < 2 ? sb.x : c < 4 ? sb.y : c < 6 ? sb.z : sb.w) >> (16 * (c & 1));
+          const float s = bf16_to_f32(sw & 0xffffu);
+          e[h] = (float)((int)(byte & 15u) - zz) * s;
+          o[h] = (float)((int)(byte >> 4) - zz) * s;
+        }
+        lo[j / 2] = pack_bf16x2(e[0], e[1]);
+        hi[j / 2] = pack_bf16x2(o[0], o[1]);
+      }
+      *reinterpret_cast<u32x4*>(wd + (2 * r) * a.N + c0) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+      *reinterpret_cast<u32x4*>(wd + (2 * r + 1) * a.N + c0) = u32x4{hi[0], hi[1], hi[2], hi[3]};
+    } else {
+      const float* sp = static_cast<const float*>(a.s) + c0;
+      const f32x4 s0 = *reinterpret_cast<const f32x4*>(sp), s1 = *reinterpret_cast<const f32x4*>(sp + 4);
+      const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+      uint32_t out[4];
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        const int8_t b0 = (int8_t)(((j < 4 ? wb.x : wb.y) >> (8 * (j & 3))) & 0xffu);
+        const int8_t b1 = (int8_t)(((j < 4 ? wb.x : wb.y) >> (8 * ((j + 1) & 3))) & 0xffu);
+        out[j / 2] = pack_bf16x2((float)b0 * sv[j], (float)b1 * sv[j + 1]);
+      }
+      *reinterpret_cast<u32x4*>(wd + r * a.N + c0) = u32x4{out[0], out[1], out[2], out[3]};
+    }
+  }
+}
+
 }  // namespace mk
 
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
 #include "../capi_internal.h"
+#include "qgemm.h"
 
 namespace {
 
@@ -908,6 +963,8 @@ struct QPlan {
   int stream_steps;  // > 0: streaming kernel with this many 32-k steps per wave
   int ring;          // int8 streaming kernel: ring slots
   int wide_groups;   // > 0: wide int4 kernel with this many 64-k groups per wave
+  int deq;           // 1: dequantise W to bf16 in the workspace, then the bf16 GEMM
+  int qg;            // 1: the many-row kernel of qgemm.hip (no workspace)
   size_t lds_bytes;
   int64_t part_bytes;
 };
@@ -1003,10 +1060,32 @@ bool plan_wide(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p) {
   return p->lds_bytes <= kMaxLds;
 }
 
+// Many rows.  The streaming kernels re-read the weights once per 16 rows;
+// from kQgMinRows rows the qgemm.hip kernel (weights read once per 256 rows,
+// dequantised in LDS) takes over, and from kDeqMinRows rows W is dequantised
+// to bf16 in the workspace once and multiplied by the bf16 GEMM, whose wider
+// tiles win there (measured crossover between 512 and 768 rows at K = 4096,
+// N = 14336).  Shapes qgemm does not take use the GEMM path from
+// kDeqFallbackRows.  MK_QMM_QG_M / MK_QMM_DEQ_M override the thresholds; 0
+// disables that path.
+constexpr int kQgMinRows = 128;
+constexpr int kDeqMinRows = 768;
+constexpr int kDeqFallbackRows = 256;
+
 bool plan_q(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p) {
-  p->stream_steps = 0;
-  p->ring = 0;
-  p->wide_groups = 0;
+  *p = QPlan{};
+  const int qg_m = env_int("MK_QMM_QG_M", kQgMinRows);
+  const int deq_m = env_int("MK_QMM_DEQ_M", kDeqMinRows);
+  const bool deq = deq_m > 0 && (M >= deq_m || M >= std::min(deq_m, kDeqFallbackRows));
+  if (qg_m > 0 && M >= qg_m && !(deq_m > 0 && M >= deq_m) && mkq::qgemm_supported(M, K, N)) {
+    p->qg = 1;
+    return true;
+  }
+  if (deq) {
+    p->deq = 1;
+    p->part_bytes = (int64_t)mk::kWidePartOffset + K * N * 2;
+    return true;
+  }
   if (plan_wide(fmt, M, K, N, p)) return true;
   p->wide_groups = 0;
   p->ntiles = (int)((N + mk::kQCols - 1) / mk::kQCols);
@@ -1144,6 +1223,25 @@ int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, v
   a.cnt = nullptr;
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e;
+  if (p.qg) {
+    e = mkq::qgemm_launch(fmt == MK_QFMT_INT4_G64, x, w, s, z, y, M, K, N, st);
+    if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
+    return MK_OK;
+  }
+  if (p.deq) {
+    uint16_t* wd = reinterpret_cast<uint16_t*>(a.part);
+    const int64_t total = (fmt == MK_QFMT_INT4_G64 ? K / 2 : K) * (N / 8);
+    const int blocks = (int)std::min<int64_t>((total + 255) / 256, 16384);
+    if (fmt == MK_QFMT_INT4_G64)
+      hipLaunchKernelGGL(mk::qmm_dequant_kernel<true>, dim3(blocks), dim3(256), 0, st, a, wd);
+    else
+      hipLaunchKernelGGL(mk::qmm_dequant_kernel<false>, dim3(blocks), dim3(256), 0, st, a, wd);
+    e = hipGetLastError();
+    if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: dequantise launch failed: %s", fn, hipGetErrorString(e));
+    const int rc = mk_gemm_bf16(x, wd, y, 1, M, N, K, 0, stream);
+    if (rc != MK_OK) return rc;
+    return MK_OK;
+  }
   if (p.wide_groups > 0) {
     if (p.part_bytes > 0) a.cnt = static_cast<uint32_t*>(ws);
     switch (p.wide_groups) {

@@ -113,6 +113,101 @@ def test_int8_pc_headline_shape():
     assert_rel_close(host_bf16(y), ref, BF16_RTOL, "int8 headline")
 
 
+# Many rows (M >= 128): the qgemm kernel (N % 64 == 0) or, for other N, W
+# dequantised to bf16 in the workspace and the bf16 GEMM.  The workload's
+# M = 256 and 4096 rows at reduced K, N; ragged M; K of 1, 2, 3 and 5 steps of
+# 64 (the kernel's loop tail); N = 776 takes the dequantise-then-GEMM path.
+LARGE_M_SHAPES = [(256, 4096, 2048), (4096, 512, 512), (300, 1024, 776), (512, 256, 14336),
+                  (130, 192, 128), (256, 64, 64), (1000, 320, 192), (128, 128, 640)]
+
+
+@pytest.mark.parametrize("M,K,N", LARGE_M_SHAPES)
+def test_int4_g64_large_m_matches_oracle(M, K, N):
+    ops = _ops()
+    rng = np.random.default_rng(3000 + M + K + N)
+    x, packed, s, z = quant.make_int4_case(rng, M, K, N)
+    print(f"int4 large-M case M={M} K={K} N={N}", flush=True)
+    y = ops.int4_g64_matmul(dev_bf16(x), dev(packed), dev_bf16(s), dev(z))
+    torch.cuda.synchronize()
+    ref = cport.int4_g64_matmul(x, packed, s, z)
+    assert_rel_close(host_bf16(y), ref, BF16_RTOL, f"int4 {M}x{K}x{N}")
+
+
+@pytest.mark.parametrize("M,K,N", LARGE_M_SHAPES)
+def test_int8_pc_large_m_matches_oracle(M, K, N):
+    ops = _ops()
+    rng = np.random.default_rng(4000 + M + K + N)
+    x, w, s = quant.make_int8_case(rng, M, K, N)
+    print(f"int8 large-M case M={M} K={K} N={N}", flush=True)
+    y = ops.int8_pc_matmul(dev_bf16(x), dev(w), dev(s))
+    torch.cuda.synchronize()
+    ref = cport.int8_pc_matmul(x, w, s)
+    assert_rel_close(host_bf16(y), ref, BF16_RTOL, f"int8 {M}x{K}x{N}")
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+def test_many_row_paths_agree(monkeypatch, fmt):
+    """M = 256 through the three paths: qgemm (default), dequantise-then-GEMM
+    (MK_QMM_QG_M=0) and the streaming kernels (MK_QMM_DEQ_M=0 as well).  They
+    differ in the bf16 rounding of the dequantised int4 weights and in
+    summation order; all meet the oracle and each other at the workload's
+    bf16 tolerance."""
+    ops = _ops()
+    rng = np.random.default_rng(77)
+    M, K, N = 256, 2048, 1024
+    if fmt == "int4":
+        x, packed, s, z = quant.make_int4_case(rng, M, K, N)
+        args = (dev_bf16(x), dev(packed), dev_bf16(s), dev(z))
+        run, ref = ops.int4_g64_matmul, cport.int4_g64_matmul(x, packed, s, z)
+    else:
+        x, w, s = quant.make_int8_case(rng, M, K, N)
+        args = (dev_bf16(x), dev(w), dev(s))
+        run, ref = ops.int8_pc_matmul, cport.int8_pc_matmul(x, w, s)
+    y_qg = host_bf16(run(*args))
+    monkeypatch.setenv("MK_QMM_QG_M", "0")
+    y_deq = host_bf16(run(*args))
+    monkeypatch.setenv("MK_QMM_DEQ_M", "0")
+    y_str = host_bf16(run(*args))
+    torch.cuda.synchronize()
+    for name, y in [("qgemm", y_qg), ("dequantise+GEMM", y_deq), ("streaming", y_str)]:
+        assert_rel_close(y, ref, BF16_RTOL, f"{fmt} {name} path")
+    assert_rel_close(y_qg, y_str, BF16_RTOL, f"{fmt} qgemm vs streaming")
+    assert_rel_close(y_deq, y_str, BF16_RTOL, f"{fmt} dequantise+GEMM vs streaming")
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+def test_qgemm_kernel_many_row_tiles(monkeypatch, fmt):
+    """The qgemm kernel itself over several 256-row tiles with a ragged last
+    one (MK_QMM_DEQ_M=0 keeps larger M off the dequantise-then-GEMM path)."""
+    ops = _ops()
+    monkeypatch.setenv("MK_QMM_DEQ_M", "0")
+    rng = np.random.default_rng(91)
+    M, K, N = 1000, 320, 192
+    if fmt == "int4":
+        x, packed, s, z = quant.make_int4_case(rng, M, K, N)
+        y = ops.int4_g64_matmul(dev_bf16(x), dev(packed), dev_bf16(s), dev(z))
+        ref = cport.int4_g64_matmul(x, packed, s, z)
+    else:
+        x, w, s = quant.make_int8_case(rng, M, K, N)
+        y = ops.int8_pc_matmul(dev_bf16(x), dev(w), dev(s))
+        ref = cport.int8_pc_matmul(x, w, s)
+    torch.cuda.synchronize()
+    assert_rel_close(host_bf16(y), ref, BF16_RTOL, f"{fmt} qgemm {M}x{K}x{N}")
+
+
+def test_int4_g64_large_m_known_answer():
+    """x = 1, q = 15, z = 14, s = 0.5 at M = 512: every output is K * 0.5."""
+    ops = _ops()
+    M, K, N = 512, 1024, 512
+    x = torch.ones((M, K), dtype=torch.bfloat16, device="cuda:0")
+    w = torch.full((K // 2, N), 0xFF, dtype=torch.uint8, device="cuda:0")
+    s = torch.full((K // 64, N), 0.5, dtype=torch.bfloat16, device="cuda:0")
+    z = torch.full((K // 64, N), 14, dtype=torch.uint8, device="cuda:0")
+    y = ops.int4_g64_matmul(x, w, s, z)
+    torch.cuda.synchronize()
+    assert torch.all(y.float() == K * 0.5)
+
+
 def test_workspace_too_small_is_rejected_before_launch():
     ops = _ops()
     from mi355x import _lib
