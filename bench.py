@@ -353,7 +353,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list of secondary workloads (int8,gemm,softmax,rmsnorm,argmax,chain6), "
+                    help="comma list of secondary workloads (int8,qmm_m,gemm,softmax,rmsnorm,argmax,chain6), "
                          "or 'none'")
     ap.add_argument("--profile", default="",
                     help="int4 | gemm: eager launches of one kernel plus a 256 MiB copy calibration, "
@@ -391,6 +391,24 @@ def main():
 
     def want(name):
         return not only or name in only
+
+    if want("qmm_m"):
+        # The rest of the workload's quantized sweep (M in {1, 16, 256, 4096}).
+        for M in (1, 256, 4096):
+            steps_m = args.steps if M == 1 else max(20, args.steps // (20 if M == 256 else 100))
+            for fmt, fn in (("int4", bench_int4), ("int8", bench_int8)):
+                r = fn(torch, ops, steps_m, 5, M=M)
+                tf = 2 * M * 4096 * 14336 / r["sec_per_call"] / 1e12
+                log(f"[bench] {fmt} M={M}: {r['sec_per_call'] * 1e6:.1f} us, {r['gbs']:.0f} GB/s, {tf:.1f} TFLOP/s")
+                if M == 1:
+                    entry = _hbm_entry(r["gbs"], r["sec_per_call"] * 1e6, {"tflops": round(tf, 2)})
+                else:
+                    entry = {"value": round(tf, 2), "unit": "TFLOP/s", "us_per_call": round(r["sec_per_call"] * 1e6, 3),
+                             "gbs": round(r["gbs"], 2),
+                             "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS,
+                                          "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                                          "traffic": None}}
+                secondary[f"{fmt}_dequant_matmul_M{M}"] = entry
 
     if want("gemm"):
         log("[bench] bf16 GEMM 4096^3 ...")

@@ -64,7 +64,10 @@ def test_int4_headline_shape(client):
     assert_rel_close(bf16_bits_to_f32(y), ref, BF16_RTOL, "int4 runtime")
 
 
-@pytest.mark.parametrize("M,K,N", [(1, 1024, 512), (16, 2048, 1024), (5, 512, 136)])
+# 256 rows take the fused many-row kernel, 800 rows dequantise W into the
+# executable's workspace and run the bf16 GEMM.
+@pytest.mark.parametrize("M,K,N", [(1, 1024, 512), (16, 2048, 1024), (5, 512, 136), (256, 1024, 512),
+                                   (800, 512, 384)])
 def test_int4_shapes(client, M, K, N):
     rng = np.random.default_rng(M * 7 + N)
     x, p, s, z = quant.make_int4_case(rng, M, K, N)
@@ -73,7 +76,7 @@ def test_int4_shapes(client, M, K, N):
     assert_rel_close(bf16_bits_to_f32(y), ref, BF16_RTOL, f"int4 {M}x{K}x{N}")
 
 
-@pytest.mark.parametrize("M,K,N", [(16, 4096, 14336), (3, 1024, 520)])
+@pytest.mark.parametrize("M,K,N", [(16, 4096, 14336), (3, 1024, 520), (256, 1024, 512), (800, 512, 384)])
 def test_int8(client, M, K, N):
     rng = np.random.default_rng(1)
     x, w, s = quant.make_int8_case(rng, M, K, N)
