@@ -133,6 +133,32 @@ int mk_reduce_lastdim(int dtype, int op, const void* x, void* y, int64_t rows, i
                       void* stream);
 
 /* ------------------------------------------------------------------------
+ * Decoder-layer data movement and masking (the workload's Llama-style
+ * decoder config).  No single reference function corresponds: jax.jit
+ * lowers these steps to generic StableHLO (the reference's own transformer
+ * layer benchmark, benchmarks/vs_cpu.py:603-626: qkv reshape (B, T, 3, H,
+ * Dh), q @ swapaxes(k) * scale, softmax, @ v, transpose back), which the
+ * reference runs op by op on MPSGraph.  All bf16, head dim D = 128.
+ *
+ * mk_rope_qkv_split_bf16: qkv [B*S, 3*H*D] (blocks q | k | v) ->
+ *   q [B*H, S, D], kT [B*H, D, S], v [B*H, S, D]; q and k rotated:
+ *   out[i] = x[i] c - x[i+D/2] s, out[i+D/2] = x[i+D/2] c + x[i] s with
+ *   c, s = cos_table / sin_table [S, D/2] (f32).  Needs S % 64 == 0.
+ * mk_softmax_causal_bf16: scores [batches, S, S] -> probs: row i keeps
+ *   columns j <= i, p = exp(scale s - m) / sum in f32, zeros for j > i.
+ *   Needs S % 8 == 0, S <= 8192.
+ * mk_merge_heads_bf16: o [B*H, S, D] -> out [B*S, H*D].
+ * ---------------------------------------------------------------------- */
+int mk_rope_qkv_split_bf16(const void* qkv, const float* cos_table, const float* sin_table, void* q,
+                           void* kT, void* v, int64_t B, int64_t S, int64_t H, int64_t D, void* stream);
+
+int mk_softmax_causal_bf16(const void* scores, void* probs, int64_t batches, int64_t S, float scale,
+                           void* stream);
+
+int mk_merge_heads_bf16(const void* o, void* out, int64_t B, int64_t H, int64_t S, int64_t D,
+                        void* stream);
+
+/* ------------------------------------------------------------------------
  * Fused elementwise program (one pass over memory).
  *
  * Replaces the reference's elementwise MPSGraph segments

@@ -38,6 +38,7 @@ KERNEL_SOURCES = [
     "ew_jit.cpp",
     "kernels/qmatmul.hip",
     "kernels/qgemm.hip",
+    "kernels/decoder.hip",
     "kernels/gemm.hip",
     "kernels/rowops.hip",
     "kernels/eltwise.hip",

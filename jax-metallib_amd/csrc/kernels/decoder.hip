@@ -1,0 +1,323 @@
+// The pieces of the workload's Llama-style decoder layer that are not
+// GEMMs, row reductions or plain elementwise chains, for gfx950:
+//
+//   * mk_rope_qkv_split_bf16: the fused QKV projection output [B*S, 3*H*D]
+//     (column blocks q | k | v, each H heads of D, the reference layer's
+//     reshape (B, T, 3, H, Dh), benchmarks/vs_cpu.py:603-610) split into
+//     per-head q [B*H, S, D], k transposed kT [B*H, D, S] and v [B*H, S, D],
+//     with rotary position embedding applied to q and k on the way
+//     (rotate-half form: x[i] * cos - x[i + D/2] * sin, x[i + D/2] * cos +
+//     x[i] * sin; cos/sin tables [S, D/2] in f32 from the caller).  kT is
+//     what the batched NN GEMM needs for the scores q @ k^T.
+//   * mk_softmax_causal_bf16: scores [B*H, S, S] -> probabilities, row i of
+//     each S x S block keeping columns j <= i: p = exp(scale*s - m) / sum
+//     (m, sum over j <= i) in f32, zeros above the diagonal.  Columns past
+//     the diagonal are never read.
+//   * mk_merge_heads_bf16: attention output [B*H, S, D] -> [B*S, H*D] (the
+//     reference layer's transpose (0, 2, 1, 3) + reshape, vs_cpu.py:615).
+//
+// jax.jit lowers these parts to generic StableHLO (slices, concatenates,
+// multiplies for the rotation; iota / compare / select for the mask;
+// transposes), which the reference runs as MPSGraph ops; here each is one
+// pass over memory with 16-byte accesses.
+#include "common.h"
+
+#include <math.h>
+
+namespace mk {
+
+constexpr int kRopeTok = 64;  // tokens per workgroup of the split kernel
+constexpr int kHeadDim = 128;
+
+struct RopeArgs {
+  const uint16_t* qkv;
+  const float* cosb;
+  const float* sinb;
+  uint16_t* q;
+  uint16_t* kT;
+  uint16_t* v;
+  int B, S, H;
+};
+
+__device__ __forceinline__ void unpack8(const u32x4& w, float (&f)[8]) {
+  const uint32_t a[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = bf16_to_f32(a[i] & 0xffffu);
+    f[2 * i + 1] = bf16_to_f32(a[i] >> 16);
+  }
+}
+
+__device__ __forceinline__ u32x4 pack8(const float (&f)[8]) {
+  return u32x4{pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7])};
+}
+
+// Workgroup: one (batch b, head h) and 64 consecutive tokens.  Thread t
+// handles token s0 + t/4 and the 16-dimension slices 16 c .. +15 and
+// 64 + 16 c .. +15 (c = t % 4), which are rotation partners.
+__global__ __launch_bounds__(256) void rope_qkv_split_kernel(RopeArgs a) {
+  constexpr int D = kHeadDim, HALF = D / 2;
+  __shared__ __attribute__((aligned(16))) uint16_t kt[D][kRopeTok + 8];  // k of the tile, transposed (row pad 16 B)
+  const int tid = threadIdx.x;
+  const int tiles = a.S / kRopeTok;
+  const int bh = blockIdx.x / tiles, s0 = (blockIdx.x - bh * tiles) * kRopeTok;
+  const int b = bh / a.H, h = bh - b * a.H;
+  const int tok = tid >> 2, c = tid & 3;
+  const int s = s0 + tok;
+  const int64_t row = (int64_t)(b * a.S + s) * (3 * a.H * D);
+  const float* cs = a.cosb + (int64_t)s * HALF + 16 * c;
+  const float* sn = a.sinb + (int64_t)s * HALF + 16 * c;
+  float cv[16], sv[16];
+#pragma unroll
+  for (int i = 0; i < 16; i += 4) {
+    const f32x4 c4 = *reinterpret_cast<const f32x4*>(cs + i);
+    const f32x4 s4 = *reinterpret_cast<const f32x4*>(sn + i);
+    cv[i] = c4.x; cv[i + 1] = c4.y; cv[i + 2] = c4.z; cv[i + 3] = c4.w;
+    sv[i] = s4.x; sv[i + 1] = s4.y; sv[i + 2] = s4.z; sv[i + 3] = s4.w;
+  }
+  const int64_t out_row = ((int64_t)bh * a.S + s) * D;
+#pragma unroll
+  for (int part = 0; part < 3; ++part) {  // q, k, v
+    const uint16_t* src = a.qkv + row + (int64_t)part * a.H * D + h * D;
+    float lo[16], hi[16];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      float f[8];
+      unpack8(*reinterpret_cast<const u32x4*>(src + 16 * c + 8 * u), f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) lo[8 * u + e] = f[e];
+      unpack8(*reinterpret_cast<const u32x4*>(src + HALF + 16 * c + 8 * u), f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) hi[8 * u + e] = f[e];
+    }
+    if (part < 2) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float x0 = lo[i], x1 = hi[i];
+        lo[i] = x0 * cv[i] - x1 * sv[i];
+        hi[i] = x1 * cv[i] + x0 * sv[i];
+      }
+    }
+    if (part == 1) {
+      // k: through LDS so kT rows (one dimension, 64 tokens) store whole.
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        kt[16 * c + i][tok] = (uint16_t)f32_to_bf16(lo[i]);
+        kt[HALF + 16 * c + i][tok] = (uint16_t)f32_to_bf16(hi[i]);
+      }
+    } else {
+      uint16_t* dst = (part == 0 ? a.q : a.v) + out_row;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        float f[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = lo[8 * u + e];
+        *reinterpret_cast<u32x4*>(dst + 16 * c + 8 * u) = pack8(f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = hi[8 * u + e];
+        *reinterpret_cast<u32x4*>(dst + HALF + 16 * c + 8 * u) = pack8(f);
+      }
+    }
+  }
+  __syncthreads();
+  // kT [bh][d][s0 .. s0 + 63]: 128 rows of 128 B; thread t writes row t/2,
+  // half t%2 (32 tokens = 4 x 16 B).
+  {
+    const int d = tid >> 1, half = tid & 1;
+    uint16_t* dst = a.kT + ((int64_t)bh * D + d) * a.S + s0 + 32 * half;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      *reinterpret_cast<u32x4*>(dst + 8 * u) = *reinterpret_cast<const u32x4*>(&kt[d][32 * half + 8 * u]);
+  }
+}
+
+struct CausalArgs {
+  const uint16_t* s;
+  uint16_t* p;
+  int64_t rows;
+  int S;
+  float scale;
+};
+
+__device__ __forceinline__ float c_wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float c_wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// One workgroup (256 threads) per row; VPT vectors of 8 columns per thread.
+// Vectors entirely above the diagonal are neither read nor exponentiated,
+// only zero-filled.
+template <int VPT>
+__global__ __launch_bounds__(256) void softmax_causal_kernel(CausalArgs a) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const int i = (int)(row % a.S);  // position in the sequence: columns 0..i kept
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint16_t* src = a.s + row * a.S;
+  uint16_t* dst = a.p + row * a.S;
+  float v[VPT][8];
+  float m = -INFINITY;
+#pragma unroll
+  for (int q = 0; q < VPT; ++q) {
+    const int c0 = (q * 256 + tid) * 8;
+    if (c0 < a.S && c0 <= i) {
+      unpack8(*reinterpret_cast<const u32x4*>(src + c0), v[q]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v[q][e] = c0 + e <= i ? v[q][e] * a.scale : -INFINITY;
+        m = fmaxf(m, v[q][e]);
+      }
+    }
+  }
+  m = c_wave_max(m);
+  if (lane == 0) red[wv] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  float sum = 0.f;
+#pragma unroll
+  for (int q = 0; q < VPT; ++q) {
+    const int c0 = (q * 256 + tid) * 8;
+    if (c0 < a.S && c0 <= i) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float ex = c0 + e <= i ? __expf(v[q][e] - m) : 0.f;
+        v[q][e] = ex;
+        sum += ex;
+      }
+    }
+  }
+  sum = c_wave_sum(sum);
+  if (lane == 0) red[wv] = sum;
+  __syncthreads();
+  sum = red[0] + red[1] + red[2] + red[3];
+  const float r = 1.0f / sum;
+#pragma unroll
+  for (int q = 0; q < VPT; ++q) {
+    const int c0 = (q * 256 + tid) * 8;
+    if (c0 >= a.S) continue;
+    if (c0 <= i) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[q][e] *= r;
+      *reinterpret_cast<u32x4*>(dst + c0) = pack8(v[q]);
+    } else {
+      *reinterpret_cast<u32x4*>(dst + c0) = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+}
+
+struct MergeArgs {
+  const uint16_t* o;
+  uint16_t* out;
+  int B, H, S;
+};
+
+// out[b*S + s][h*D + d] = o[(b*H + h)*S + s][d]; one 16-byte chunk per thread.
+__global__ __launch_bounds__(256) void merge_heads_kernel(MergeArgs a) {
+  constexpr int D = kHeadDim, CH = D / 8;
+  const int64_t total = (int64_t)a.B * a.H * a.S * CH;
+  for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += (int64_t)gridDim.x * 256) {
+    const int ch = (int)(t % CH);
+    const int64_t r = t / CH;  // (b*H + h)*S + s
+    const int s = (int)(r % a.S);
+    const int64_t bh = r / a.S;
+    const int h = (int)(bh % a.H), b = (int)(bh / a.H);
+    const u32x4 w = *reinterpret_cast<const u32x4*>(a.o + r * D + 8 * ch);
+    *reinterpret_cast<u32x4*>(a.out + ((int64_t)b * a.S + s) * a.H * D + h * D + 8 * ch) = w;
+  }
+}
+
+}  // namespace mk
+
+// ---------------------------------------------------------------------------
+// Host launchers
+// ---------------------------------------------------------------------------
+#include "../capi_internal.h"
+
+#include <algorithm>
+
+extern "C" int mk_rope_qkv_split_bf16(const void* qkv, const float* cos_table, const float* sin_table, void* q,
+                                      void* kT, void* v, int64_t B, int64_t S, int64_t H, int64_t D,
+                                      void* stream) {
+  mkc::clear_error();
+  const char* fn = "mk_rope_qkv_split_bf16";
+  if (!qkv || !cos_table || !sin_table || !q || !kT || !v) return mkc::fail(MK_EINVAL, "%s: null pointer", fn);
+  if (B <= 0 || S <= 0 || H <= 0 || D <= 0) return mkc::fail(MK_EINVAL, "%s: sizes must be positive", fn);
+  if (D != mk::kHeadDim) return mkc::fail(MK_EUNSUPPORTED, "%s: head dim %lld (only 128)", fn, (long long)D);
+  if (S % mk::kRopeTok != 0)
+    return mkc::fail(MK_EUNSUPPORTED, "%s: sequence length %lld not a multiple of 64", fn, (long long)S);
+  if (B * H * (S / mk::kRopeTok) > (1 << 30) || B * S * 3 * H * D > ((int64_t)1 << 40))
+    return mkc::fail(MK_EINVAL, "%s: shape too large", fn);
+  mk::RopeArgs a;
+  a.qkv = static_cast<const uint16_t*>(qkv);
+  a.cosb = cos_table;
+  a.sinb = sin_table;
+  a.q = static_cast<uint16_t*>(q);
+  a.kT = static_cast<uint16_t*>(kT);
+  a.v = static_cast<uint16_t*>(v);
+  a.B = (int)B;
+  a.S = (int)S;
+  a.H = (int)H;
+  hipLaunchKernelGGL(mk::rope_qkv_split_kernel, dim3((unsigned)(B * H * (S / mk::kRopeTok))), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  return MK_OK;
+}
+
+extern "C" int mk_softmax_causal_bf16(const void* scores, void* probs, int64_t batches, int64_t S, float scale,
+                                      void* stream) {
+  mkc::clear_error();
+  const char* fn = "mk_softmax_causal_bf16";
+  if (!scores || !probs) return mkc::fail(MK_EINVAL, "%s: null pointer", fn);
+  if (batches <= 0 || S <= 0) return mkc::fail(MK_EINVAL, "%s: sizes must be positive", fn);
+  if (S % 8 != 0 || S > 8192)
+    return mkc::fail(MK_EUNSUPPORTED, "%s: sequence length %lld (need S %% 8 == 0, S <= 8192)", fn,
+                     (long long)S);
+  if (batches * S > (int64_t)1 << 31) return mkc::fail(MK_EINVAL, "%s: shape too large", fn);
+  mk::CausalArgs a;
+  a.s = static_cast<const uint16_t*>(scores);
+  a.p = static_cast<uint16_t*>(probs);
+  a.rows = batches * S;
+  a.S = (int)S;
+  a.scale = scale;
+  const dim3 grid((unsigned)(batches * S));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int vpt = (int)((S + 2047) / 2048);
+  switch (vpt) {
+    case 1: hipLaunchKernelGGL(mk::softmax_causal_kernel<1>, grid, dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL(mk::softmax_causal_kernel<2>, grid, dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL(mk::softmax_causal_kernel<4>, grid, dim3(256), 0, st, a); break;
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  return MK_OK;
+}
+
+extern "C" int mk_merge_heads_bf16(const void* o, void* out, int64_t B, int64_t H, int64_t S, int64_t D,
+                                   void* stream) {
+  mkc::clear_error();
+  const char* fn = "mk_merge_heads_bf16";
+  if (!o || !out) return mkc::fail(MK_EINVAL, "%s: null pointer", fn);
+  if (B <= 0 || S <= 0 || H <= 0 || D <= 0) return mkc::fail(MK_EINVAL, "%s: sizes must be positive", fn);
+  if (D != mk::kHeadDim) return mkc::fail(MK_EUNSUPPORTED, "%s: head dim %lld (only 128)", fn, (long long)D);
+  if (B * H * S > (int64_t)1 << 31) return mkc::fail(MK_EINVAL, "%s: shape too large", fn);
+  mk::MergeArgs a;
+  a.o = static_cast<const uint16_t*>(o);
+  a.out = static_cast<uint16_t*>(out);
+  a.B = (int)B;
+  a.H = (int)H;
+  a.S = (int)S;
+  const int64_t chunks = B * H * S * (D / 8);
+  const int blocks = (int)std::min<int64_t>((chunks + 255) / 256, 16384);
+  hipLaunchKernelGGL(mk::merge_heads_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  return MK_OK;
+}

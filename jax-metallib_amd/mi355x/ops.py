@@ -190,3 +190,44 @@ def elementwise(program, inputs, out_slot, out=None, dtype=None):
     check(lib().mk_elementwise(dt, arr, len(program), ptrs, numel, len(inputs), out_slot, _ptr(y), n,
                                _stream(ref.device)))
     return y
+
+
+def rope_qkv_split(qkv, cos_table, sin_table, B, S, H, D=128, q=None, kT=None, v=None):
+    """qkv bf16 [B*S, 3*H*D] (blocks q | k | v) -> q [B*H, S, D], kT
+    [B*H, D, S], v [B*H, S, D], with rotary embedding (rotate-half) applied
+    to q and k from the f32 tables cos_table / sin_table [S, D/2]."""
+    _require(qkv, _BF16, "qkv")
+    _require(cos_table, (torch.float32,), "cos_table")
+    _require(sin_table, (torch.float32,), "sin_table")
+    if qkv.shape != (B * S, 3 * H * D) or cos_table.shape != (S, D // 2) or sin_table.shape != (S, D // 2):
+        raise ValueError("rope_qkv_split: inconsistent shapes")
+    dev = qkv.device
+    q = q if q is not None else torch.empty((B * H, S, D), dtype=torch.bfloat16, device=dev)
+    kT = kT if kT is not None else torch.empty((B * H, D, S), dtype=torch.bfloat16, device=dev)
+    v = v if v is not None else torch.empty((B * H, S, D), dtype=torch.bfloat16, device=dev)
+    check(lib().mk_rope_qkv_split_bf16(_ptr(qkv), _ptr(cos_table), _ptr(sin_table), _ptr(q), _ptr(kT), _ptr(v),
+                                       B, S, H, D, _stream(dev)))
+    return q, kT, v
+
+
+def softmax_causal(scores, scale, out=None):
+    """Causal softmax of bf16 scores [batches, S, S]: row i keeps columns
+    j <= i, p = exp(scale*s - m) / sum in f32, zeros above the diagonal."""
+    _require(scores, _BF16, "scores")
+    if scores.dim() != 3 or scores.shape[1] != scores.shape[2]:
+        raise ValueError("softmax_causal: scores must be [batches, S, S]")
+    p = out if out is not None else torch.empty_like(scores)
+    check(lib().mk_softmax_causal_bf16(_ptr(scores), _ptr(p), scores.shape[0], scores.shape[1], float(scale),
+                                       _stream(scores.device)))
+    return p
+
+
+def merge_heads(o, B, H, out=None):
+    """Attention output o bf16 [B*H, S, D] -> [B*S, H*D]."""
+    _require(o, _BF16, "o")
+    if o.dim() != 3 or o.shape[0] != B * H:
+        raise ValueError("merge_heads: o must be [B*H, S, D]")
+    S, D = o.shape[1], o.shape[2]
+    y = out if out is not None else torch.empty((B * S, H * D), dtype=torch.bfloat16, device=o.device)
+    check(lib().mk_merge_heads_bf16(_ptr(o), _ptr(y), B, H, S, D, _stream(o.device)))
+    return y
