@@ -141,16 +141,26 @@ int mk_reduce_lastdim(int dtype, int op, const void* x, void* y, int64_t rows, i
  * reference runs op by op on MPSGraph.  All bf16, head dim D = 128.
  *
  * mk_rope_qkv_split_bf16: qkv [B*S, 3*H*D] (blocks q | k | v) ->
- *   q [B*H, S, D], kT [B*H, D, S], v [B*H, S, D]; q and k rotated:
+ *   q [B*H, S, D], k, v [B*H, S, D]; q and k rotated:
  *   out[i] = x[i] c - x[i+D/2] s, out[i+D/2] = x[i+D/2] c + x[i] s with
- *   c, s = cos_table / sin_table [S, D/2] (f32).  Needs S % 64 == 0.
+ *   c, s = cos_table / sin_table [S, D/2] (f32).  k_rows = 0 writes k
+ *   transposed, kT [B*H, D, S] (the B operand of q @ k^T for mk_gemm_bf16).
+ *   Needs S % 64 == 0.
  * mk_softmax_causal_bf16: scores [batches, S, S] -> probs: row i keeps
  *   columns j <= i, p = exp(scale s - m) / sum in f32, zeros for j > i.
  *   Needs S % 8 == 0, S <= 8192.
  * mk_merge_heads_bf16: o [B*H, S, D] -> out [B*S, H*D].
+ * mk_attention_causal_bf16: the three steps above in one pass (scores,
+ *   causal softmax in f32 with the online max/sum rescaling, P rounded to
+ *   bf16 for P @ V, f32 accumulation) from q, k, v [B*H, S, D] (k_rows = 1)
+ *   straight to out [B*S, H*D].  Needs S % 128 == 0.
  * ---------------------------------------------------------------------- */
 int mk_rope_qkv_split_bf16(const void* qkv, const float* cos_table, const float* sin_table, void* q,
-                           void* kT, void* v, int64_t B, int64_t S, int64_t H, int64_t D, void* stream);
+                           void* k, void* v, int64_t B, int64_t S, int64_t H, int64_t D, int k_rows,
+                           void* stream);
+
+int mk_attention_causal_bf16(const void* q, const void* k, const void* v, void* out, int64_t B, int64_t H,
+                             int64_t S, int64_t D, float scale, void* stream);
 
 int mk_softmax_causal_bf16(const void* scores, void* probs, int64_t batches, int64_t S, float scale,
                            void* stream);

@@ -26,6 +26,9 @@
 
 namespace mk {
 
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4_t* lds_s16x4_t;
+
 constexpr int kRopeTok = 64;  // tokens per workgroup of the split kernel
 constexpr int kHeadDim = 128;
 
@@ -37,6 +40,7 @@ struct RopeArgs {
   uint16_t* kT;
   uint16_t* v;
   int B, S, H;
+  int k_rows;  // 1: k as [B*H, S, D] (for the attention kernel); 0: kT [B*H, D, S]
 };
 
 __device__ __forceinline__ void unpack8(const u32x4& w, float (&f)[8]) {
@@ -98,7 +102,7 @@ __global__ __launch_bounds__(256) void rope_qkv_split_kernel(RopeArgs a) {
         hi[i] = x1 * cv[i] + x0 * sv[i];
       }
     }
-    if (part == 1) {
+    if (part == 1 && !a.k_rows) {
       // k: through LDS so kT rows (one dimension, 64 tokens) store whole.
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
@@ -106,7 +110,7 @@ __global__ __launch_bounds__(256) void rope_qkv_split_kernel(RopeArgs a) {
         kt[HALF + 16 * c + i][tok] = (uint16_t)f32_to_bf16(hi[i]);
       }
     } else {
-      uint16_t* dst = (part == 0 ? a.q : a.v) + out_row;
+      uint16_t* dst = (part == 0 ? a.q : part == 1 ? a.kT : a.v) + out_row;
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         float f[8];
@@ -119,6 +123,7 @@ __global__ __launch_bounds__(256) void rope_qkv_split_kernel(RopeArgs a) {
       }
     }
   }
+  if (a.k_rows) return;  // uniform across the workgroup
   __syncthreads();
   // kT [bh][d][s0 .. s0 + 63]: 128 rows of 128 B; thread t writes row t/2,
   // half t%2 (32 tokens = 4 x 16 B).
@@ -212,6 +217,173 @@ __global__ __launch_bounds__(256) void softmax_causal_kernel(CausalArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Causal attention in one pass (flash-attention style): per (b, h) and 128
+// query rows, loop over 64-key tiles up to the diagonal; scores, the online
+// softmax and P @ V stay on chip, and the output goes straight to the merged
+// [B*S, H*D] layout.  8 waves, 16 query rows each; v_mfma_f32_16x16x32_bf16
+// throughout.
+//   S = Q K^T: first operand K rows (lane: key 16t + l%16, 8 consecutive d
+//     from an XOR-swizzled LDS tile), second Q rows (registers) -> lane holds
+//     row i = l%16 and keys 4(l/16) .. +3 of each 16-key block.
+//   P @ V: second operand P straight from those registers (bf16); its 8
+//     k-slots per lane are keys {4g .. 4g+3} and {16 + 4g .. 16 + 4g + 3} of
+//     a 32-key block (g = l/16), and the V fragment is read with
+//     ds_read_b64_tr_b16 from exactly those rows, so no shuffle is needed.
+// Scores are scaled into log2 units; exp2 is the hardware v_exp_f32.
+// ---------------------------------------------------------------------------
+constexpr int kFaQ = 128;  // query rows per workgroup
+constexpr int kFaKV = 64;  // keys per tile
+
+struct AttnArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* out;
+  int B, H, S;
+  float scale_log2;  // softmax scale times log2(e)
+};
+
+// V tile row swizzle (16-byte chunk position = chunk ^ fa_vswz(row)): the 64
+// lanes of one transposing read touch every bank exactly twice.
+__device__ __forceinline__ int fa_vswz(int r) { return (2 * (r & 3)) | (8 * ((r >> 2) & 1)); }
+
+__device__ __forceinline__ float fa_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__global__ __launch_bounds__(512) void attention_causal_kernel(AttnArgs a) {
+  constexpr int D = kHeadDim, ROWB = D * 2;  // 256-byte rows
+  __shared__ __attribute__((aligned(16))) unsigned char kv[2][2][kFaKV * ROWB];  // [buffer][K | V]
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane >> 4, l16 = lane & 15;
+  const int BH = a.B * a.H;
+  const int bh = (int)(blockIdx.x % BH);
+  const int qt = a.S / kFaQ - 1 - (int)(blockIdx.x / BH);  // longest rows first
+  const int q0 = qt * kFaQ, i0 = q0 + 16 * w;
+  const uint16_t* Qg = a.q + (int64_t)bh * a.S * D;
+  const uint16_t* Kg = a.k + (int64_t)bh * a.S * D;
+  const uint16_t* Vg = a.v + (int64_t)bh * a.S * D;
+
+  u32x4 qf[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) qf[s] = *reinterpret_cast<const u32x4*>(Qg + (int64_t)(i0 + l16) * D + 32 * s + 8 * g);
+
+  f32x4 o[8];
+#pragma unroll
+  for (int n = 0; n < 8; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, lsum = 0.f;
+
+  // Tile loads: thread -> 16-byte chunks tid and tid + 512 of the K and V
+  // tiles (row = id / 16, chunk = id % 16).
+  u32x4 kr[2], vr[2];
+  auto gload = [&](int t) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int id = tid + 512 * u, j = id >> 4, c = id & 15;
+      const int64_t off = (int64_t)(t * kFaKV + j) * D + 8 * c;
+      kr[u] = *reinterpret_cast<const u32x4*>(Kg + off);
+      vr[u] = *reinterpret_cast<const u32x4*>(Vg + off);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int id = tid + 512 * u, j = id >> 4, c = id & 15;
+      *reinterpret_cast<u32x4*>(&kv[buf][0][j * ROWB + 16 * (c ^ (j & 15))]) = kr[u];
+      *reinterpret_cast<u32x4*>(&kv[buf][1][j * ROWB + 16 * (c ^ fa_vswz(j))]) = vr[u];
+    }
+  };
+
+  // V fragment byte offsets (tile-relative): d tile n, 32-key block u, low /
+  // high 4 keys.  Lane (g, r = (l%16)/4, q = l%4) reads row 32u + 4g + r
+  // (+16), columns 16n + 4q .. +3.
+  const int vr_r = (lane & 15) >> 2, vr_q = lane & 3;
+
+  const int ntiles = (q0 + kFaQ) / kFaKV;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < ntiles) gload(t + 1);
+    const int kv0 = t * kFaKV;
+    if (kv0 <= i0 + 15) {  // some key of the tile is visible to this wave's rows
+      const unsigned char* Ks = kv[buf][0];
+      const unsigned char* Vs = kv[buf][1];
+      f32x4 sacc[4];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) sacc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+          const int j = 16 * tt + l16;
+          const u32x4 kf = *reinterpret_cast<const u32x4*>(Ks + j * ROWB + 16 * ((4 * s + g) ^ (j & 15)));
+          sacc[tt] = mfma16x16x32(kf, qf[s], sacc[tt]);
+        }
+      const int i = i0 + l16;
+      const bool diag = kv0 + kFaKV - 1 > i0;
+      float mt = -INFINITY;
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float x = sacc[tt][e] * a.scale_log2;
+          if (diag && kv0 + 16 * tt + 4 * g + e > i) x = -INFINITY;
+          sacc[tt][e] = x;
+          mt = fmaxf(mt, x);
+        }
+      mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+      const float mn = fmaxf(m, mt);
+      const float alpha = fa_exp2(m - mn);
+      m = mn;
+      float ps = 0.f;
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float p = fa_exp2(sacc[tt][e] - mn);
+          sacc[tt][e] = p;
+          ps += p;
+        }
+      lsum = lsum * alpha + ps;
+#pragma unroll
+      for (int n = 0; n < 8; ++n) o[n] *= alpha;
+      u32x4 pf[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        pf[u] = u32x4{pack_bf16x2(sacc[2 * u][0], sacc[2 * u][1]), pack_bf16x2(sacc[2 * u][2], sacc[2 * u][3]),
+                      pack_bf16x2(sacc[2 * u + 1][0], sacc[2 * u + 1][1]),
+                      pack_bf16x2(sacc[2 * u + 1][2], sacc[2 * u + 1][3])};
+#pragma unroll
+      for (int n = 0; n < 8; ++n)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int c = 2 * n + (vr_q >> 1), hb = 8 * (vr_q & 1);
+          const int r0 = 32 * u + 4 * g + vr_r, r1 = r0 + 16;
+          const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4_t)(Vs + r0 * ROWB + 16 * (c ^ fa_vswz(r0)) + hb));
+          const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4_t)(Vs + r1 * ROWB + 16 * (c ^ fa_vswz(r1)) + hb));
+          const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+          o[n] = mfma16x16x32(u32x4{l2.x, l2.y, h2.x, h2.y}, pf[u], o[n]);
+        }
+    }
+    if (t + 1 < ntiles) lstore(buf ^ 1);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  }
+
+  lsum += __shfl_xor(lsum, 16, 64);
+  lsum += __shfl_xor(lsum, 32, 64);
+  const float inv = 1.0f / lsum;
+  const int b = bh / a.H, h = bh - b * a.H;
+  uint16_t* out = a.out + ((int64_t)b * a.S + i0 + l16) * (a.H * D) + h * D + 4 * g;
+#pragma unroll
+  for (int n = 0; n < 8; ++n)
+    *reinterpret_cast<u32x2*>(out + 16 * n) =
+        u32x2{pack_bf16x2(o[n].x * inv, o[n].y * inv), pack_bf16x2(o[n].z * inv, o[n].w * inv)};
+}
+
 struct MergeArgs {
   const uint16_t* o;
   uint16_t* out;
@@ -243,11 +415,11 @@ __global__ __launch_bounds__(256) void merge_heads_kernel(MergeArgs a) {
 #include <algorithm>
 
 extern "C" int mk_rope_qkv_split_bf16(const void* qkv, const float* cos_table, const float* sin_table, void* q,
-                                      void* kT, void* v, int64_t B, int64_t S, int64_t H, int64_t D,
+                                      void* k, void* v, int64_t B, int64_t S, int64_t H, int64_t D, int k_rows,
                                       void* stream) {
   mkc::clear_error();
   const char* fn = "mk_rope_qkv_split_bf16";
-  if (!qkv || !cos_table || !sin_table || !q || !kT || !v) return mkc::fail(MK_EINVAL, "%s: null pointer", fn);
+  if (!qkv || !cos_table || !sin_table || !q || !k || !v) return mkc::fail(MK_EINVAL, "%s: null pointer", fn);
   if (B <= 0 || S <= 0 || H <= 0 || D <= 0) return mkc::fail(MK_EINVAL, "%s: sizes must be positive", fn);
   if (D != mk::kHeadDim) return mkc::fail(MK_EUNSUPPORTED, "%s: head dim %lld (only 128)", fn, (long long)D);
   if (S % mk::kRopeTok != 0)
@@ -259,7 +431,8 @@ extern "C" int mk_rope_qkv_split_bf16(const void* qkv, const float* cos_table, c
   a.cosb = cos_table;
   a.sinb = sin_table;
   a.q = static_cast<uint16_t*>(q);
-  a.kT = static_cast<uint16_t*>(kT);
+  a.kT = static_cast<uint16_t*>(k);
+  a.k_rows = k_rows ? 1 : 0;
   a.v = static_cast<uint16_t*>(v);
   a.B = (int)B;
   a.S = (int)S;
@@ -317,6 +490,33 @@ extern "C" int mk_merge_heads_bf16(const void* o, void* out, int64_t B, int64_t 
   const int64_t chunks = B * H * S * (D / 8);
   const int blocks = (int)std::min<int64_t>((chunks + 255) / 256, 16384);
   hipLaunchKernelGGL(mk::merge_heads_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
+  return MK_OK;
+}
+
+extern "C" int mk_attention_causal_bf16(const void* q, const void* k, const void* v, void* out, int64_t B,
+                                        int64_t H, int64_t S, int64_t D, float scale, void* stream) {
+  mkc::clear_error();
+  const char* fn = "mk_attention_causal_bf16";
+  if (!q || !k || !v || !out) return mkc::fail(MK_EINVAL, "%s: null pointer", fn);
+  if (B <= 0 || S <= 0 || H <= 0 || D <= 0) return mkc::fail(MK_EINVAL, "%s: sizes must be positive", fn);
+  if (D != mk::kHeadDim) return mkc::fail(MK_EUNSUPPORTED, "%s: head dim %lld (only 128)", fn, (long long)D);
+  if (S % mk::kFaQ != 0)
+    return mkc::fail(MK_EUNSUPPORTED, "%s: sequence length %lld not a multiple of 128", fn, (long long)S);
+  if (B * H * (S / mk::kFaQ) > (1 << 30) || B * H * S * D > ((int64_t)1 << 40))
+    return mkc::fail(MK_EINVAL, "%s: shape too large", fn);
+  mk::AttnArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.out = static_cast<uint16_t*>(out);
+  a.B = (int)B;
+  a.H = (int)H;
+  a.S = (int)S;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  hipLaunchKernelGGL(mk::attention_causal_kernel, dim3((unsigned)(B * H * (S / mk::kFaQ))), dim3(512), 0,
+                     static_cast<hipStream_t>(stream), a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
   return MK_OK;

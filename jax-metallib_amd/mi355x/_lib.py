@@ -41,7 +41,8 @@ SIGNATURES = {
     "mk_gemm_bf16": (_i32, [_p, _p, _p, _i64, _i64, _i64, _i64, _i32, _p]),
     "mk_gemm_f32": (_i32, [_p, _p, _p, _i64, _i64, _i64, _i64, _p]),
     "mk_softmax_lastdim": (_i32, [_i32, _p, _p, _i64, _i64, _p]),
-    "mk_rope_qkv_split_bf16": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p]),
+    "mk_rope_qkv_split_bf16": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _p]),
+    "mk_attention_causal_bf16": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, ctypes.c_float, _p]),
     "mk_softmax_causal_bf16": (_i32, [_p, _p, _i64, _i64, ctypes.c_float, _p]),
     "mk_merge_heads_bf16": (_i32, [_p, _p, _i64, _i64, _i64, _i64, _p]),
     "mk_rmsnorm_lastdim": (_i32, [_i32, _p, _p, _p, _i64, _i64, ctypes.c_float, _p]),

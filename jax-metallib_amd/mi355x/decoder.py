@@ -17,13 +17,16 @@ in one HIP graph:
 
     h    = rmsnorm(x, g_attn)                      mk_rmsnorm_lastdim
     qkv  = h @ Wqkv                                mk_int4g64_matmul_bf16
-    q, kT, v = split + rope(qkv)                   mk_rope_qkv_split_bf16
-    s    = q @ kT   (batched over B*H)             mk_gemm_bf16
-    p    = causal_softmax(s * Dh**-0.5)  (in place) mk_softmax_causal_bf16
-    o    = p @ v    (batched)                      mk_gemm_bf16
-    x   += merge_heads(o) @ Wo                     mk_merge_heads_bf16, int4, mk_elementwise
+    q, k, v = split + rope(qkv)                    mk_rope_qkv_split_bf16
+    a    = causal_attention(q, k, v), heads merged mk_attention_causal_bf16
+    x   += a @ Wo                                  int4, mk_elementwise
     h    = rmsnorm(x, g_mlp)
     x   += (silu(h @ Wg) * (h @ Wu)) @ Wd          int4 x 3, mk_elementwise
+
+attention="composed" runs the attention as the reference's layer writes it,
+one op at a time: s = q @ k^T (mk_gemm_bf16 on kT), p = causal softmax of
+s * Dh**-0.5 in place (mk_softmax_causal_bf16), o = p @ v (mk_gemm_bf16),
+merge heads (mk_merge_heads_bf16).  It materialises the [B*H, S, S] scores.
 """
 
 import math
@@ -133,19 +136,23 @@ RESIDUAL_PROGRAM = [("LOAD", 0, 0, 0, 0, 0.0), ("LOAD", 1, 1, 0, 0, 0.0), ("ADD"
 
 
 class Buffers:
-    """Every activation of one forward, allocated once."""
+    """Every activation of one forward, allocated once (the score matrix only
+    for the composed attention)."""
 
-    def __init__(self, cfg: DecoderConfig, device="cuda"):
+    def __init__(self, cfg: DecoderConfig, device="cuda", attention="fused"):
         T, A, BH = cfg.tokens, cfg.heads * cfg.head_dim, cfg.batch * cfg.heads
         bf = dict(dtype=torch.bfloat16, device=device)
         self.x = torch.empty((T, cfg.hidden), **bf)
         self.h = torch.empty((T, cfg.hidden), **bf)
         self.qkv = torch.empty((T, 3 * A), **bf)
+        self.attention = attention
         self.q = torch.empty((BH, cfg.seq, cfg.head_dim), **bf)
-        self.kT = torch.empty((BH, cfg.head_dim, cfg.seq), **bf)
+        kshape = (BH, cfg.head_dim, cfg.seq) if attention == "composed" else (BH, cfg.seq, cfg.head_dim)
+        self.k = torch.empty(kshape, **bf)
         self.v = torch.empty((BH, cfg.seq, cfg.head_dim), **bf)
-        self.s = torch.empty((BH, cfg.seq, cfg.seq), **bf)
-        self.o = torch.empty((BH, cfg.seq, cfg.head_dim), **bf)
+        if attention == "composed":
+            self.s = torch.empty((BH, cfg.seq, cfg.seq), **bf)
+            self.o = torch.empty((BH, cfg.seq, cfg.head_dim), **bf)
         self.attn = torch.empty((T, A), **bf)
         self.proj = torch.empty((T, cfg.hidden), **bf)
         self.gate = torch.empty((T, cfg.ffn), **bf)
@@ -162,11 +169,15 @@ def layer_forward(cfg: DecoderConfig, lw: LayerWeights, buf: Buffers, cos, sin):
     B, S, H, D = cfg.batch, cfg.seq, cfg.heads, cfg.head_dim
     ops.rmsnorm(buf.x, lw.g_attn, eps=cfg.eps, out=buf.h)
     _qmm(buf.h, lw.w_qkv, buf.qkv)
-    ops.rope_qkv_split(buf.qkv, cos, sin, B, S, H, D, q=buf.q, kT=buf.kT, v=buf.v)
-    ops.gemm_bf16(buf.q, buf.kT, out=buf.s)
-    ops.softmax_causal(buf.s, 1.0 / math.sqrt(D), out=buf.s)
-    ops.gemm_bf16(buf.s, buf.v, out=buf.o)
-    ops.merge_heads(buf.o, B, H, out=buf.attn)
+    composed = buf.attention == "composed"
+    ops.rope_qkv_split(buf.qkv, cos, sin, B, S, H, D, q=buf.q, k=buf.k, v=buf.v, k_transposed=composed)
+    if composed:
+        ops.gemm_bf16(buf.q, buf.k, out=buf.s)
+        ops.softmax_causal(buf.s, 1.0 / math.sqrt(D), out=buf.s)
+        ops.gemm_bf16(buf.s, buf.v, out=buf.o)
+        ops.merge_heads(buf.o, B, H, out=buf.attn)
+    else:
+        ops.attention_causal(buf.q, buf.k, buf.v, B, H, 1.0 / math.sqrt(D), out=buf.attn)
     _qmm(buf.attn, lw.w_o, buf.proj)
     ops.elementwise(RESIDUAL_PROGRAM, [buf.x, buf.proj], out_slot=2, out=buf.x)
     ops.rmsnorm(buf.x, lw.g_mlp, eps=cfg.eps, out=buf.h)

@@ -192,10 +192,11 @@ def elementwise(program, inputs, out_slot, out=None, dtype=None):
     return y
 
 
-def rope_qkv_split(qkv, cos_table, sin_table, B, S, H, D=128, q=None, kT=None, v=None):
-    """qkv bf16 [B*S, 3*H*D] (blocks q | k | v) -> q [B*H, S, D], kT
-    [B*H, D, S], v [B*H, S, D], with rotary embedding (rotate-half) applied
-    to q and k from the f32 tables cos_table / sin_table [S, D/2]."""
+def rope_qkv_split(qkv, cos_table, sin_table, B, S, H, D=128, q=None, k=None, v=None, k_transposed=True):
+    """qkv bf16 [B*S, 3*H*D] (blocks q | k | v) -> q [B*H, S, D], k, v
+    [B*H, S, D], with rotary embedding (rotate-half) applied to q and k from
+    the f32 tables cos_table / sin_table [S, D/2].  With k_transposed, k is
+    written as kT [B*H, D, S] (the B operand of q @ k^T)."""
     _require(qkv, _BF16, "qkv")
     _require(cos_table, (torch.float32,), "cos_table")
     _require(sin_table, (torch.float32,), "sin_table")
@@ -203,11 +204,26 @@ def rope_qkv_split(qkv, cos_table, sin_table, B, S, H, D=128, q=None, kT=None, v
         raise ValueError("rope_qkv_split: inconsistent shapes")
     dev = qkv.device
     q = q if q is not None else torch.empty((B * H, S, D), dtype=torch.bfloat16, device=dev)
-    kT = kT if kT is not None else torch.empty((B * H, D, S), dtype=torch.bfloat16, device=dev)
+    kshape = (B * H, D, S) if k_transposed else (B * H, S, D)
+    k = k if k is not None else torch.empty(kshape, dtype=torch.bfloat16, device=dev)
     v = v if v is not None else torch.empty((B * H, S, D), dtype=torch.bfloat16, device=dev)
-    check(lib().mk_rope_qkv_split_bf16(_ptr(qkv), _ptr(cos_table), _ptr(sin_table), _ptr(q), _ptr(kT), _ptr(v),
-                                       B, S, H, D, _stream(dev)))
-    return q, kT, v
+    check(lib().mk_rope_qkv_split_bf16(_ptr(qkv), _ptr(cos_table), _ptr(sin_table), _ptr(q), _ptr(k), _ptr(v),
+                                       B, S, H, D, 0 if k_transposed else 1, _stream(dev)))
+    return q, k, v
+
+
+def attention_causal(q, k, v, B, H, scale, out=None):
+    """Causal attention of q, k, v bf16 [B*H, S, D] in one pass -> out bf16
+    [B*S, H*D] (heads merged)."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _require(t, _BF16, n)
+    if q.dim() != 3 or q.shape[0] != B * H or k.shape != q.shape or v.shape != q.shape:
+        raise ValueError("attention_causal: q, k, v must all be [B*H, S, D]")
+    S, D = q.shape[1], q.shape[2]
+    y = out if out is not None else torch.empty((B * S, H * D), dtype=torch.bfloat16, device=q.device)
+    check(lib().mk_attention_causal_bf16(_ptr(q), _ptr(k), _ptr(v), _ptr(y), B, H, S, D, float(scale),
+                                         _stream(q.device)))
+    return y
 
 
 def softmax_causal(scores, scale, out=None):

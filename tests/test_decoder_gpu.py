@@ -48,7 +48,9 @@ def test_rope_qkv_split(B, S, H):
     qkv = torch.randn((B * S, 3 * H * D), generator=g).to(torch.bfloat16)
     cos, sin = _tables(S, D)
     q, kT, v = ops.rope_qkv_split(qkv.cuda(), cos.cuda(), sin.cuda(), B, S, H, D)
+    q2, k2, v2 = ops.rope_qkv_split(qkv.cuda(), cos.cuda(), sin.cuda(), B, S, H, D, k_transposed=False)
     torch.cuda.synchronize()
+    assert torch.equal(q2, q) and torch.equal(v2, v) and torch.equal(k2.transpose(1, 2), kT)
     x = qkv.float().reshape(B, S, 3, H, D).permute(2, 0, 3, 1, 4)  # [3, B, H, S, D]
     q_ref = _bf(_rope_ref(x[0], cos, sin)).reshape(B * H, S, D)
     k_ref = _bf(_rope_ref(x[1], cos, sin)).reshape(B * H, S, D)
@@ -95,6 +97,52 @@ def test_merge_heads(B, H, S):
     assert torch.equal(y, ref)
 
 
+def _attention_ref(q, k, v, scale):
+    """float64 causal attention on bf16 inputs [BH, S, D]; P rounded to bf16
+    as the kernel feeds it to P @ V (normalised at the end)."""
+    S = q.shape[1]
+    s = (q.double() @ k.double().transpose(1, 2)) * scale
+    s = s.masked_fill(~torch.ones((S, S), dtype=torch.bool).tril(), float("-inf"))
+    return torch.softmax(s, dim=-1) @ v.double()
+
+
+@pytest.mark.parametrize("B,H,S", [(1, 1, 128), (2, 3, 256), (1, 2, 1024)])
+def test_attention_causal_fused(B, H, S):
+    ops = _ops()
+    g = torch.Generator().manual_seed(B * 7 + H * 3 + S)
+    q = torch.randn((B * H, S, 128), generator=g).to(torch.bfloat16)
+    k = torch.randn((B * H, S, 128), generator=g).to(torch.bfloat16)
+    v = torch.randn((B * H, S, 128), generator=g).to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(128)
+    y = ops.attention_causal(q.cuda(), k.cuda(), v.cuda(), B, H, scale).float().cpu()
+    ref = _attention_ref(q, k, v, scale).reshape(B, H, S, 128).permute(0, 2, 1, 3).reshape(B * S, H * 128)
+    assert_rel_close(y.numpy(), ref.numpy(), BF16_RTOL, f"attention {B}x{H}x{S}")
+    # Row 0 of every head attends to key 0 only: exactly v[0] (bf16).
+    y0 = y.reshape(B, S, H, 128)[:, 0]
+    assert torch.equal(y0, v.reshape(B, H, S, 128)[:, :, 0].float())
+
+
+def test_attention_fused_vs_composed_accuracy():
+    """The composed path (bf16 scores, GEMM / causal softmax / GEMM) and the
+    one-pass kernel (f32 scores on chip) against float64: the composed path
+    meets the tolerance norm-wise, and the one-pass kernel is at least as
+    accurate (its only bf16 roundings are of P and of the output)."""
+    ops = _ops()
+    B, H, S = 2, 2, 256
+    g = torch.Generator().manual_seed(11)
+    q, k, v = (torch.randn((B * H, S, 128), generator=g).to(torch.bfloat16) for _ in range(3))
+    scale = 1.0 / math.sqrt(128)
+    fused = ops.attention_causal(q.cuda(), k.cuda(), v.cuda(), B, H, scale).double().cpu()
+    s = ops.gemm_bf16(q.cuda(), k.transpose(1, 2).contiguous().cuda())
+    p = ops.softmax_causal(s, scale)
+    comp = ops.merge_heads(ops.gemm_bf16(p, v.cuda()), B, H).double().cpu()
+    ref = _attention_ref(q, k, v, scale).reshape(B, H, S, 128).permute(0, 2, 1, 3).reshape(B * S, H * 128)
+    err_c = float((comp - ref).abs().max() / ref.abs().max())
+    err_f = float((fused - ref).abs().max() / ref.abs().max())
+    assert err_c <= BF16_RTOL, err_c
+    assert err_f <= err_c, (err_f, err_c)
+
+
 def test_decoder_kernels_reject_bad_shapes():
     ops = _ops()
     from mi355x._lib import MKError
@@ -104,6 +152,9 @@ def test_decoder_kernels_reject_bad_shapes():
         ops.rope_qkv_split(qkv, cos, cos, 2, 96, 1, 128)  # S % 64 != 0
     with pytest.raises(MKError):
         ops.softmax_causal(torch.zeros((1, 12, 12), dtype=torch.bfloat16, device="cuda"), 1.0)  # S % 8
+    z = torch.zeros((1, 192, 128), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(MKError):
+        ops.attention_causal(z, z, z, 1, 1, 1.0)  # S % 128 != 0
 
 
 # ---------------------------------------------------------------------------
@@ -148,13 +199,14 @@ def reference_forward(cfg, weights, x0, cos, sin):
     return x
 
 
-def test_decoder_forward_matches_reference():
+@pytest.mark.parametrize("attention", ["fused", "composed"])
+def test_decoder_forward_matches_reference(attention):
     need_gpu()
     from mi355x import decoder
     cfg = decoder.DecoderConfig(layers=2, hidden=256, heads=2, head_dim=128, ffn=512, batch=2, seq=128)
     weights = decoder.init_weights(cfg, seed=3)
     cos, sin = decoder.rope_tables(cfg)
-    buf = decoder.Buffers(cfg)
+    buf = decoder.Buffers(cfg, attention=attention)
     x0 = torch.randn((cfg.tokens, cfg.hidden), generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
     buf.x.copy_(x0.cuda())
     y = decoder.forward(cfg, weights, buf, cos, sin).float().cpu()
