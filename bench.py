@@ -137,6 +137,42 @@ def bench_int8(torch, ops, steps, warmup, M=16, K=4096, N=14336):
     return {"bytes": per_set, "sec_per_call": t, "gbs": per_set / t / 1e9, "nsets": nsets}
 
 
+def bench_decoder(torch, reps=10):
+    """The workload's Llama-style decoder (4 layers, hidden 2048, 16 x 128
+    heads, SwiGLU 8192, batch 4 x seq 2048, int4 g64 weights, random init):
+    one forward captured in a HIP graph, replayed `reps` times."""
+    from mi355x import decoder
+
+    cfg = decoder.DecoderConfig()
+    weights = decoder.init_weights(cfg, seed=0)
+    cos, sin = decoder.rope_tables(cfg)
+    buf = decoder.Buffers(cfg)
+    x0 = (torch.randn((cfg.tokens, cfg.hidden), device="cuda", generator=torch.Generator("cuda").manual_seed(0))
+          .to(torch.bfloat16))
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        buf.x.copy_(x0)
+        decoder.forward(cfg, weights, buf, cos, sin)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        decoder.forward(cfg, weights, buf, cos, sin)
+    g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(reps):
+            g.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / reps
+    return {"ms": ms, "tokens_per_s": cfg.tokens / ms * 1e3, "tflops": cfg.matmul_flops() / ms / 1e9,
+            "config": {"layers": cfg.layers, "hidden": cfg.hidden, "heads": cfg.heads, "head_dim": cfg.head_dim,
+                       "ffn": cfg.ffn, "batch": cfg.batch, "seq": cfg.seq, "weights": "int4 g64, random init",
+                       "data": "synthetic", "flops_counted": "projections + causal attention products"}}
+
+
 def _rot_sets(total_bytes_per_set, floor_sets=2):
     """How many distinct input sets to rotate so their total exceeds the
     256 MB Infinity Cache."""
@@ -353,7 +389,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list of secondary workloads (int8,qmm_m,gemm,softmax,rmsnorm,argmax,chain6), "
+                    help="comma list of secondary workloads (int8,qmm_m,gemm,decoder,softmax,rmsnorm,argmax,chain6), "
                          "or 'none'")
     ap.add_argument("--profile", default="",
                     help="int4 | gemm: eager launches of one kernel plus a 256 MiB copy calibration, "
@@ -437,6 +473,14 @@ def main():
             "value": round(rf["tflops"], 2), "unit": "TFLOP/s", "us_per_call": round(rf["sec_per_call"] * 1e6, 3),
             "roofline": {"bound": "mfma", "achieved": round(rf["tflops"], 2), "peak": 157.3,
                          "unit": "TFLOP/s", "frac": round(rf["tflops"] / 157.3, 4), "traffic": None}}
+    if want("decoder"):
+        rd = bench_decoder(torch)
+        log(f"[bench] decoder forward: {rd['ms']:.3f} ms, {rd['tokens_per_s']:.0f} tokens/s, {rd['tflops']:.1f} TFLOP/s")
+        secondary["llama_decoder_forward_4x2048_b4s2048_int4"] = {
+            "value": round(rd["tokens_per_s"], 1), "unit": "tokens/s", "ms_per_forward": round(rd["ms"], 4),
+            "roofline": {"bound": "mfma", "achieved": round(rd["tflops"], 2), "peak": BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(rd["tflops"] / BF16_PEAK_TFLOPS, 4), "traffic": None},
+            "config": rd["config"]}
     for kind in ("softmax", "rmsnorm", "argmax", "chain6"):
         if not want(kind):
             continue

@@ -56,12 +56,14 @@ class DecoderConfig:
     def tokens(self):
         return self.batch * self.seq
 
-    def matmul_flops(self):
-        """FLOPs of one forward: projections plus the two attention GEMMs
-        (computed in full; the causal half is not skipped)."""
+    def matmul_flops(self, causal=True):
+        """FLOPs of one forward: the projections plus the two attention
+        products (q @ k^T, p @ v), the latter over the causal half
+        (S (S + 1) / 2 score entries per head) unless causal=False."""
         T, Hd, A = self.tokens, self.hidden, self.heads * self.head_dim
         proj = 2 * T * (Hd * 3 * A + A * Hd + 2 * Hd * self.ffn + self.ffn * Hd)
-        attn = 2 * 2 * self.batch * self.heads * self.seq * self.seq * self.head_dim
+        pairs = self.seq * (self.seq + 1) // 2 if causal else self.seq * self.seq
+        attn = 2 * 2 * self.batch * self.heads * pairs * self.head_dim
         return self.layers * (proj + attn)
 
 
