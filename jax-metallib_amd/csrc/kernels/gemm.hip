@@ -509,7 +509,10 @@ __global__ __launch_bounds__(WM_ * WN_ * 64) void gemm_bf16_256_kernel(GemmArgs 
 // asm with explicit waits, so the compiler -- which then sees no pending
 // LDS writes -- schedules the fragment reads against the MFMAs itself.
 // LDS layouts (swizzles applied by choosing each DMA lane's source chunk):
-//   A row r (64 B): 16-byte chunk c at position c ^ (r / 4 % 4);
+//   A row r (64 B): 16-byte chunk c at position c ^ (r / 2 % 4) (ten chunk
+//     swizzles were measured with SQ_LDS_BANK_CONFLICT on this fragment read,
+//     row = lane % 16 and chunk = lane / 16; only this one had no conflicts,
+//     the former c ^ (r / 4 % 4) doubled the cycles of every A read);
 //   B k row (512 B): chunk c at c ^ (2 (k % 4) + 8 (k / 8 % 2)),
 // which make the A ds_read_b128 and the B ds_read_b64_tr_b16 fragment reads
 // bank-conflict-free.  Waves 2 x 4, each 128 x 64 (8 x 4 MFMA 16x16x32
@@ -556,7 +559,7 @@ __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs
   for (int u = 0; u < DI; ++u) {
     const int i = DI * wave + u;
     const int row = 16 * i + (lane >> 2), pa = lane & 3;
-    asrc[u] = A + (size_t)row * K + 8 * (pa ^ ((row >> 2) & 3));
+    asrc[u] = A + (size_t)row * K + 8 * (pa ^ ((row >> 1) & 3));
     const int kr = 2 * i + (lane >> 5), pb = lane & 31;
     bsrc[u] = B + (size_t)kr * N + 8 * swz_b2(kr, pb);
   }
@@ -575,7 +578,7 @@ __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs
   // 4 k: tr16 lane 4r + q of 16-lane group g reads k row 8g + r (+4), columns
   // wn*64 + 16j + 4q .. +3.
   const int arow = wm * 128 + (lane & 15);
-  const int aoff = arow * 64 + 16 * ((lane >> 4) ^ ((arow >> 2) & 3));
+  const int aoff = arow * 64 + 16 * ((lane >> 4) ^ ((arow >> 1) & 3));
   int boff[2 * TN];
   {
     const int g = lane >> 4, r = (lane & 15) >> 2, q = lane & 3;
