@@ -77,6 +77,19 @@ int mk_int8pc_matmul_bf16(const void* x, const void* w, const void* scale, void*
                           int64_t M, int64_t K, int64_t N, void* workspace,
                           int64_t workspace_bytes, void* stream);
 
+/* The same with an epilogue against aux (bf16 [M, N]), as for
+ * mk_gemm_bf16_epilogue (MK_EPI_ADD / MK_EPI_SWIGLU, declared below), fused
+ * into the final bf16 store of whichever kernel runs; aux may equal y.
+ * Bit-identical to the plain call followed by the elementwise program. */
+int mk_int4g64_matmul_epilogue_bf16(const void* x, const void* w_packed, const void* scale,
+                                    const void* zero, void* y, const void* aux, int epilogue, int64_t M,
+                                    int64_t K, int64_t N, void* workspace, int64_t workspace_bytes,
+                                    void* stream);
+
+int mk_int8pc_matmul_epilogue_bf16(const void* x, const void* w, const void* scale, void* y,
+                                   const void* aux, int epilogue, int64_t M, int64_t K, int64_t N,
+                                   void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------
  * dot_general GEMM (canonical batched NN form).
  *
@@ -99,6 +112,19 @@ int mk_gemm_bf16(const void* a, const void* b, void* c, int64_t batch, int64_t M
 
 int mk_gemm_f32(const void* a, const void* b, void* c, int64_t batch, int64_t M, int64_t N,
                 int64_t K, void* stream);
+
+/* mk_gemm_bf16_epilogue: mk_gemm_bf16 with bf16 output and an elementwise
+ * epilogue against aux (bf16, the layout of C), fused into the GEMM's store:
+ *   MK_EPI_ADD:    c = r(r(acc) + aux)                       (residual add)
+ *   MK_EPI_SWIGLU: c = r(r(aux * r(logistic(aux))) * r(acc)) (silu(aux) * acc)
+ * r() is bf16 rounding; the results equal, bit for bit, mk_gemm_bf16
+ * followed by the bf16 elementwise program (MK_EW_ADD, or MK_EW_LOGISTIC +
+ * MK_EW_MUL + MK_EW_MUL) -- the reference runs these as separate MPSGraph
+ * ops (ops/binary_ops.mm).  aux may equal c (in-place residual). */
+enum { MK_EPI_NONE = 0, MK_EPI_ADD = 1, MK_EPI_SWIGLU = 2 };
+
+int mk_gemm_bf16_epilogue(const void* a, const void* b, void* c, const void* aux, int epilogue,
+                          int64_t batch, int64_t M, int64_t N, int64_t K, void* stream);
 
 /* ------------------------------------------------------------------------
  * Last-axis row operations on X [rows, cols] (row-major).

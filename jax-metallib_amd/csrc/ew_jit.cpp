@@ -158,7 +158,7 @@ std::string generate(int dtype, const mk_ew_instr* prog, int n_instr, int n_inpu
         case MK_EW_TANH: ex = "tanhf(" + A + ")"; break;
         case MK_EW_RSQRT: ex = "1.0f / sqrtf(" + A + ")"; break;
         case MK_EW_SQRT: ex = "sqrtf(" + A + ")"; break;
-        case MK_EW_LOGISTIC: ex = "1.0f / (1.0f + mk_exp(-" + A + "))"; break;
+        case MK_EW_LOGISTIC: ex = (bf ? "mk_logistic_bf(" : "mk_logistic(") + A + ")"; break;
         case MK_EW_FLOOR: ex = "floorf(" + A + ")"; break;
         case MK_EW_CEIL: ex = "ceilf(" + A + ")"; break;
         case MK_EW_CMP_EQ: ex = "(" + A + " == " + B + ") ? 1.f : 0.f"; rnd = false; break;

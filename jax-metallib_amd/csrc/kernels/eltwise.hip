@@ -179,7 +179,7 @@ __global__ __launch_bounds__(256) void eltwise_kernel(EwArgs a) {
         MK_EW_CASE(MK_EW_TANH, tanhf(u))
         MK_EW_CASE(MK_EW_RSQRT, 1.0f / sqrtf(u))
         MK_EW_CASE(MK_EW_SQRT, sqrtf(u))
-        MK_EW_CASE(MK_EW_LOGISTIC, 1.0f / (1.0f + mk_exp(-u)))
+        MK_EW_CASE(MK_EW_LOGISTIC, BF16 ? mk_logistic_bf(u) : mk_logistic(u))
         MK_EW_CASE(MK_EW_FLOOR, floorf(u))
         MK_EW_CASE(MK_EW_CEIL, ceilf(u))
         MK_EW_CASE(MK_EW_CMP_EQ, u == v ? 1.f : 0.f)

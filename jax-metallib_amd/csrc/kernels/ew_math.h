@@ -12,8 +12,13 @@
 //             result is x itself.  The hardware log2 (v_log_f32) is within
 //             1 ulp of log2 over [0.5, 2), 1 + 2^-23 included, so no series
 //             is needed near 0; <= 1.9 ulp over every tested input.
-// bf16 programs round every op's result to 8 significant bits, so exp uses
-// the short form mk_exp_bf (2^(x*log2e), relative error < 2^-16).
+//   mk_logistic 1 / (1 + mk_exp(-x)) with the hardware reciprocal (1 ulp),
+//             within 4 ulp; below x = -80 the result is exp(x) itself
+//             (relative difference < 1e-34), which keeps the denormal results
+//             the reciprocal would flush.
+// bf16 programs round every op's result to 8 significant bits, so exp and
+// logistic use the short forms mk_exp_bf (2^(x*log2e), relative error
+// < 2^-16) and mk_logistic_bf.
 // maximum/minimum are the IEEE 754-2019 operations (v_maximum3/v_minimum3 on
 // gfx950): NaN propagates and -0 < +0, the StableHLO semantics.
 #pragma once
@@ -37,6 +42,14 @@
   }                                                                                     \
   __device__ __forceinline__ float mk_exp_bf(float x) {                                 \
     return __builtin_exp2f(x * 1.44269502f);                                            \
+  }                                                                                     \
+  __device__ __forceinline__ float mk_logistic(float x) {                               \
+    const float r = __builtin_amdgcn_rcpf(1.0f + mk_exp(-x));                           \
+    return x < -80.0f ? mk_exp(x) : r;                                                  \
+  }                                                                                     \
+  __device__ __forceinline__ float mk_logistic_bf(float x) {                            \
+    const float r = __builtin_amdgcn_rcpf(1.0f + mk_exp_bf(-x));                        \
+    return x < -80.0f ? mk_exp_bf(x) : r;                                               \
   }                                                                                     \
   __device__ __forceinline__ float mk_max(float a, float b) {                           \
     return __builtin_elementwise_maximum(a, b);                                         \

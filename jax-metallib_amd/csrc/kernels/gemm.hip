@@ -25,6 +25,7 @@
 //     ids stay on one XCD and cover a 4-row band of tiles, so the A panels and
 //     B panels they share stay in that XCD's L2.
 #include "common.h"
+#include "epilogue.h"
 
 namespace mk {
 
@@ -35,7 +36,15 @@ struct GemmArgs {
   int M, N, K;
   int64_t sa, sb, sc;  // batch strides in elements
   int out_f32;         // bf16 kernel: 1 -> f32 output, 0 -> bf16 output
+  int epi;             // bf16 output: MK_EPI_NONE / MK_EPI_ADD / MK_EPI_SWIGLU with aux
+  const uint16_t* aux; // bf16, same layout and batch stride as C
 };
+
+// Four bf16 outputs of C row-major at offset off, with the GEMM's epilogue.
+__device__ __forceinline__ void store_bf16x4(const GemmArgs& p, uint16_t* C, const uint16_t* X, size_t off,
+                                             const f32x4& acc) {
+  epi_store_bf16x4(C, X, p.epi, off, acc);
+}
 
 // Map a logical workgroup id to a (tile row, tile col) with bands of GM tile
 // rows, so consecutive ids sweep a GM-tall column block.
@@ -189,6 +198,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmArgs p) {
     }
   } else {
     uint16_t* C = static_cast<uint16_t*>(p.c) + (size_t)blockIdx.z * p.sc;
+    const uint16_t* X = p.aux + (p.epi != MK_EPI_NONE ? (size_t)blockIdx.z * p.sc : 0);
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       const int m = mrow + 16 * i;
@@ -196,12 +206,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_bf16_kernel(GemmArgs p) {
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int n = ncol + 16 * j;
-        if (n < N) {
-          u32x2 o;
-          o.x = pack_bf16x2(acc[i][j].x, acc[i][j].y);
-          o.y = pack_bf16x2(acc[i][j].z, acc[i][j].w);
-          *reinterpret_cast<u32x2*>(C + (size_t)m * N + n) = o;
-        }
+        if (n < N) store_bf16x4(p, C, X, (size_t)m * N + n, acc[i][j]);
       }
     }
   }
@@ -484,15 +489,11 @@ __global__ __launch_bounds__(WM_ * WN_ * 64) void gemm_bf16_256_kernel(GemmArgs 
         *reinterpret_cast<f32x4*>(C + (size_t)(mrow + 16 * i) * N + ncol + 16 * j) = acc[i][j];
   } else {
     uint16_t* C = static_cast<uint16_t*>(p.c) + (size_t)blockIdx.z * p.sc;
+    const uint16_t* X = p.aux + (p.epi != MK_EPI_NONE ? (size_t)blockIdx.z * p.sc : 0);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        u32x2 o;
-        o.x = pack_bf16x2(acc[i][j].x, acc[i][j].y);
-        o.y = pack_bf16x2(acc[i][j].z, acc[i][j].w);
-        *reinterpret_cast<u32x2*>(C + (size_t)(mrow + 16 * i) * N + ncol + 16 * j) = o;
-      }
+      for (int j = 0; j < TN; ++j) store_bf16x4(p, C, X, (size_t)(mrow + 16 * i) * N + ncol + 16 * j, acc[i][j]);
   }
 }
 
@@ -599,6 +600,23 @@ __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // Epilogue operand: loaded before the K loop so its latency hides behind
+  // the whole loop (64 VGPRs; the epilogue itself then only computes).  The
+  // 4-wave variant, with twice the tiles per wave, reads it at the end.
+  const int mrow = m0 + wm * (16 * TM) + (lane & 15);
+  const int ncol = n0 + wn * (16 * TN) + 4 * (lane >> 4);
+  constexpr bool kPreAux = WN_ == 4;
+  u32x2 auxv[kPreAux ? TM : 1][kPreAux ? TN : 1];
+  if (kPreAux && p.epi != MK_EPI_NONE) {
+    const uint16_t* X = p.aux + (size_t)blockIdx.z * p.sc;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        auxv[kPreAux ? i : 0][kPreAux ? j : 0] =
+            *reinterpret_cast<const u32x2*>(X + (size_t)(mrow + 16 * i) * N + ncol + 16 * j);
+  }
+
   const int KT = K / BK;
   const int pre = KT < kGemmStages - 1 ? KT : kGemmStages - 1;
   for (int kt = 0; kt < pre; ++kt) issue(kt);
@@ -629,8 +647,6 @@ __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs
   }
 
   // Epilogue (C^T tiles): lane owns row m, columns n..n+3 of each tile.
-  const int mrow = m0 + wm * (16 * TM) + (lane & 15);
-  const int ncol = n0 + wn * (16 * TN) + 4 * (lane >> 4);
   if (p.out_f32) {
     float* C = static_cast<float*>(p.c) + (size_t)blockIdx.z * p.sc;
 #pragma unroll
@@ -644,10 +660,11 @@ __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
-        u32x2 o;
-        o.x = pack_bf16x2(acc[i][j].x, acc[i][j].y);
-        o.y = pack_bf16x2(acc[i][j].z, acc[i][j].w);
-        *reinterpret_cast<u32x2*>(C + (size_t)(mrow + 16 * i) * N + ncol + 16 * j) = o;
+        const size_t off = (size_t)(mrow + 16 * i) * N + ncol + 16 * j;
+        if constexpr (kPreAux)
+          epi_store_bf16x4_v(C, auxv[i][j], p.epi, off, acc[i][j]);
+        else
+          epi_store_bf16x4(C, p.aux + (size_t)blockIdx.z * p.sc, p.epi, off, acc[i][j]);
       }
   }
 }
@@ -658,6 +675,8 @@ __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs
 // Host launchers
 // ---------------------------------------------------------------------------
 #include "../capi_internal.h"
+
+#include <algorithm>
 
 namespace {
 
@@ -711,16 +730,24 @@ int env_tile() {
 
 }  // namespace
 
-extern "C" int mk_gemm_bf16(const void* a, const void* b, void* c, int64_t batch, int64_t M,
-                            int64_t N, int64_t K, int out_f32, void* stream) {
+namespace {
+
+int run_gemm_bf16(const char* fn, const void* a, const void* b, void* c, const void* aux, int epi, int64_t batch,
+                  int64_t M, int64_t N, int64_t K, int out_f32, void* stream) {
   mkc::clear_error();
-  int rc = check_gemm("mk_gemm_bf16", a, b, c, batch, M, N, K);
+  int rc = check_gemm(fn, a, b, c, batch, M, N, K);
   if (rc != MK_OK) return rc;
+  if (epi != MK_EPI_NONE && epi != MK_EPI_ADD && epi != MK_EPI_SWIGLU)
+    return mkc::fail(MK_EINVAL, "%s: unknown epilogue %d", fn, epi);
+  if (epi != MK_EPI_NONE && (out_f32 || !aux))
+    return mkc::fail(MK_EINVAL, "%s: an epilogue needs a bf16 output and an aux operand", fn);
   mk::GemmArgs p;
   p.a = a; p.b = b; p.c = c;
   p.M = (int)M; p.N = (int)N; p.K = (int)K;
   p.sa = M * K; p.sb = K * N; p.sc = M * N;
   p.out_f32 = out_f32 ? 1 : 0;
+  p.epi = epi;
+  p.aux = static_cast<const uint16_t*>(aux);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256) * batch;
   int tile = env_tile();
@@ -757,9 +784,22 @@ extern "C" int mk_gemm_bf16(const void* a, const void* b, void* c, int64_t batch
   } else {
     e = launch_bf16<128, 128, 2, 2>(p, (int)batch, st);
   }
-  if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "mk_gemm_bf16: launch failed: %s", hipGetErrorString(e));
+  if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
   return MK_OK;
 }
+
+}  // namespace
+
+extern "C" int mk_gemm_bf16(const void* a, const void* b, void* c, int64_t batch, int64_t M,
+                            int64_t N, int64_t K, int out_f32, void* stream) {
+  return run_gemm_bf16("mk_gemm_bf16", a, b, c, nullptr, MK_EPI_NONE, batch, M, N, K, out_f32, stream);
+}
+
+extern "C" int mk_gemm_bf16_epilogue(const void* a, const void* b, void* c, const void* aux, int epilogue,
+                                     int64_t batch, int64_t M, int64_t N, int64_t K, void* stream) {
+  return run_gemm_bf16("mk_gemm_bf16_epilogue", a, b, c, aux, epilogue, batch, M, N, K, 0, stream);
+}
+
 
 extern "C" int mk_gemm_f32(const void* a, const void* b, void* c, int64_t batch, int64_t M,
                            int64_t N, int64_t K, void* stream) {
@@ -771,6 +811,8 @@ extern "C" int mk_gemm_f32(const void* a, const void* b, void* c, int64_t batch,
   p.M = (int)M; p.N = (int)N; p.K = (int)K;
   p.sa = M * K; p.sb = K * N; p.sc = M * N;
   p.out_f32 = 1;
+  p.epi = MK_EPI_NONE;
+  p.aux = nullptr;
   hipError_t e = launch_f32<128, 128, 2, 2>(p, (int)batch, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "mk_gemm_f32: launch failed: %s", hipGetErrorString(e));
   return MK_OK;

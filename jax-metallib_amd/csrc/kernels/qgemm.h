@@ -12,7 +12,8 @@ bool qgemm_supported(int64_t M, int64_t K, int64_t N);
 
 // int4: w uint8 [K/2, N], s bf16 [K/64, N], z uint8 [K/64, N];
 // int8: w int8 [K, N], s f32 [N], z unused.  x bf16 [M, K], y bf16 [M, N].
+// aux / epi: the bf16 store epilogue (epilogue.h), MK_EPI_NONE for none.
 hipError_t qgemm_launch(bool int4, const void* x, const void* w, const void* s, const void* z, void* y, int64_t M,
-                        int64_t K, int64_t N, hipStream_t stream);
+                        int64_t K, int64_t N, const void* aux, int epi, hipStream_t stream);
 
 }  // namespace mkq

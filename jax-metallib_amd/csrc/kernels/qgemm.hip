@@ -32,6 +32,7 @@
 // rounds each dequantised weight to bf16 once (relative 2^-9), well inside
 // the workload's bf16 tolerance.
 #include "common.h"
+#include "epilogue.h"
 #include "qgemm.h"
 
 #include <algorithm>
@@ -47,6 +48,8 @@ struct QgArgs {
   const void* s;
   const uint8_t* z;
   uint16_t* y;
+  const uint16_t* aux;  // epilogue operand or null
+  int epi;
   int M, K, N;
 };
 
@@ -268,7 +271,7 @@ __global__ __launch_bounds__(256) void qgemm_kernel(QgArgs a) {
         const f32x4 sc = *reinterpret_cast<const f32x4*>(static_cast<const float*>(a.s) + n);
         v = f32x4{v.x * sc.x, v.y * sc.y, v.z * sc.z, v.w * sc.w};
       }
-      *reinterpret_cast<u32x2*>(a.y + (int64_t)m * N + n) = u32x2{qg_pack(v.x, v.y), qg_pack(v.z, v.w)};
+      epi_store_bf16x4(a.y, a.aux, a.epi, (size_t)m * N + n, v);
     }
   }
 }
@@ -284,13 +287,15 @@ bool qgemm_supported(int64_t M, int64_t K, int64_t N) {
 }
 
 hipError_t qgemm_launch(bool int4, const void* x, const void* w, const void* s, const void* z, void* y, int64_t M,
-                        int64_t K, int64_t N, hipStream_t stream) {
+                        int64_t K, int64_t N, const void* aux, int epi, hipStream_t stream) {
   mk::QgArgs a;
   a.x = static_cast<const uint16_t*>(x);
   a.w = static_cast<const uint8_t*>(w);
   a.s = s;
   a.z = static_cast<const uint8_t*>(z);
   a.y = static_cast<uint16_t*>(y);
+  a.aux = static_cast<const uint16_t*>(aux);
+  a.epi = epi;
   a.M = (int)M;
   a.K = (int)K;
   a.N = (int)N;

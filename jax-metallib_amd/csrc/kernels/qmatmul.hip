@@ -39,6 +39,7 @@
 // that product to bf16 first (reference ops/registry.h:273-287), which is
 // within the workload's bf16 tolerance.
 #include "common.h"
+#include "epilogue.h"
 
 #include <algorithm>
 
@@ -60,6 +61,8 @@ struct QArgs {
   int kwave;         // k handled by one wave (multiple of 64)
   int wave_lds;      // bytes of LDS per wave (x staging, then partial y)
   uint32_t* cnt;     // wide kernel, ks > 1: per-tile arrival counters (zero between calls)
+  const uint16_t* aux;  // epilogue operand (bf16 [M, N]) or null
+  int epi;              // MK_EPI_* applied by every kernel's bf16 store
 };
 
 // Stage this wave's x block [16 rows][kwave] into LDS as 16-byte MFMA A
@@ -165,8 +168,7 @@ __device__ __forceinline__ void reduce_and_store(const QArgs& a, const unsigned 
       *reinterpret_cast<f32x4*>(a.part + ((size_t)(rb * a.ks + ksi) * kQRows + m) * a.N + n) = acc;
     } else {
       if (FMT8) acc *= *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(a.s) + n);
-      *reinterpret_cast<u32x2*>(a.y + (size_t)(m0 + m) * a.N + n) =
-          u32x2{pack_bf16x2(acc.x, acc.y), pack_bf16x2(acc.z, acc.w)};
+      epi_store_bf16x4(a.y, a.aux, a.epi, (size_t)(m0 + m) * a.N + n, acc);
     }
   }
 }
@@ -807,9 +809,7 @@ __global__ __launch_bounds__(8 * kWave) void int4g64_wide_kernel(QArgs a) {
   for (int it = 0; it < 2; ++it) {
     const int q = threadIdx.x + 8 * kWave * it;
     const int m = q >> 6, n = n0 + 4 * (q & 63);
-    if (m < mrows)
-      *reinterpret_cast<u32x2*>(a.y + (size_t)(m0 + m) * N + n) =
-          u32x2{pack_bf16x2(own[it].x, own[it].y), pack_bf16x2(own[it].z, own[it].w)};
+    if (m < mrows) epi_store_bf16x4(a.y, a.aux, a.epi, (size_t)(m0 + m) * N + n, own[it]);
   }
 }
 
@@ -887,8 +887,7 @@ __global__ __launch_bounds__(256) void qmm_splitk_reduce_kernel(QArgs a) {
     for (int k = 0; k < a.ks; ++k)
       acc += *reinterpret_cast<const f32x4*>(a.part + ((size_t)(rb * a.ks + k) * kQRows + mr) * a.N + n);
     if (FMT8) acc *= *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(a.s) + n);
-    *reinterpret_cast<u32x2*>(a.y + (size_t)m * a.N + n) =
-        u32x2{pack_bf16x2(acc.x, acc.y), pack_bf16x2(acc.z, acc.w)};
+    epi_store_bf16x4(a.y, a.aux, a.epi, (size_t)m * a.N + n, acc);
   }
 }
 
@@ -1186,8 +1185,12 @@ hipError_t launch_reduce(int fmt, const mk::QArgs& a, hipStream_t st) {
 }
 
 int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, void* y, int64_t M,
-          int64_t K, int64_t N, void* ws, int64_t ws_bytes, void* stream) {
+          int64_t K, int64_t N, void* ws, int64_t ws_bytes, void* stream, const void* aux = nullptr,
+          int epi = MK_EPI_NONE) {
   const char* fn = fmt == MK_QFMT_INT4_G64 ? "mk_int4g64_matmul_bf16" : "mk_int8pc_matmul_bf16";
+  if (epi != MK_EPI_NONE && epi != MK_EPI_ADD && epi != MK_EPI_SWIGLU)
+    return mkc::fail(MK_EINVAL, "%s: unknown epilogue %d", fn, epi);
+  if (epi != MK_EPI_NONE && !aux) return mkc::fail(MK_EINVAL, "%s: the epilogue needs aux", fn);
   if (!x || !w || !s || !y || (fmt == MK_QFMT_INT4_G64 && !z))
     return mkc::fail(MK_EINVAL, "%s: null pointer argument", fn);
   if (M <= 0 || K <= 0 || N <= 0)
@@ -1221,10 +1224,12 @@ int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, v
   a.kwave = p.kwave;
   a.wave_lds = p.wave_lds;
   a.cnt = nullptr;
+  a.aux = static_cast<const uint16_t*>(aux);
+  a.epi = epi;
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e;
   if (p.qg) {
-    e = mkq::qgemm_launch(fmt == MK_QFMT_INT4_G64, x, w, s, z, y, M, K, N, st);
+    e = mkq::qgemm_launch(fmt == MK_QFMT_INT4_G64, x, w, s, z, y, M, K, N, aux, epi, st);
     if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
     return MK_OK;
   }
@@ -1238,7 +1243,8 @@ int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, v
       hipLaunchKernelGGL(mk::qmm_dequant_kernel<false>, dim3(blocks), dim3(256), 0, st, a, wd);
     e = hipGetLastError();
     if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: dequantise launch failed: %s", fn, hipGetErrorString(e));
-    const int rc = mk_gemm_bf16(x, wd, y, 1, M, N, K, 0, stream);
+    const int rc = epi == MK_EPI_NONE ? mk_gemm_bf16(x, wd, y, 1, M, N, K, 0, stream)
+                                      : mk_gemm_bf16_epilogue(x, wd, y, aux, epi, 1, M, N, K, stream);
     if (rc != MK_OK) return rc;
     return MK_OK;
   }
@@ -1290,4 +1296,21 @@ extern "C" int mk_int8pc_matmul_bf16(const void* x, const void* w, const void* s
   mkc::clear_error();
   return run_q(MK_QFMT_INT8_PC, x, w, scale, nullptr, y, M, K, N, workspace, workspace_bytes,
                stream);
+}
+
+extern "C" int mk_int4g64_matmul_epilogue_bf16(const void* x, const void* w_packed, const void* scale,
+                                               const void* zero, void* y, const void* aux, int epilogue,
+                                               int64_t M, int64_t K, int64_t N, void* workspace,
+                                               int64_t workspace_bytes, void* stream) {
+  mkc::clear_error();
+  return run_q(MK_QFMT_INT4_G64, x, w_packed, scale, zero, y, M, K, N, workspace, workspace_bytes, stream, aux,
+               epilogue);
+}
+
+extern "C" int mk_int8pc_matmul_epilogue_bf16(const void* x, const void* w, const void* scale, void* y,
+                                              const void* aux, int epilogue, int64_t M, int64_t K, int64_t N,
+                                              void* workspace, int64_t workspace_bytes, void* stream) {
+  mkc::clear_error();
+  return run_q(MK_QFMT_INT8_PC, x, w, scale, nullptr, y, M, K, N, workspace, workspace_bytes, stream, aux,
+               epilogue);
 }

@@ -19,9 +19,14 @@ in one HIP graph:
     qkv  = h @ Wqkv                                mk_int4g64_matmul_bf16
     q, k, v = split + rope(qkv)                    mk_rope_qkv_split_bf16
     a    = causal_attention(q, k, v), heads merged mk_attention_causal_bf16
-    x   += a @ Wo                                  int4, mk_elementwise
+    x    = x + a @ Wo     (add in the GEMM store)  mk_int4g64_matmul_epilogue_bf16
     h    = rmsnorm(x, g_mlp)
-    x   += (silu(h @ Wg) * (h @ Wu)) @ Wd          int4 x 3, mk_elementwise
+    g    = h @ Wg                                  mk_int4g64_matmul_bf16
+    act  = silu(g) * (h @ Wu)  (in the GEMM store) mk_int4g64_matmul_epilogue_bf16
+    x    = x + act @ Wd   (add in the GEMM store)  mk_int4g64_matmul_epilogue_bf16
+
+fuse_epilogues=False runs the residual adds and silu(g) * u as separate
+elementwise programs (mk_elementwise); the results are bit-identical.
 
 attention="composed" runs the attention as the reference's layer writes it,
 one op at a time: s = q @ k^T (mk_gemm_bf16 on kT), p = causal softmax of
@@ -141,13 +146,14 @@ class Buffers:
     """Every activation of one forward, allocated once (the score matrix only
     for the composed attention)."""
 
-    def __init__(self, cfg: DecoderConfig, device="cuda", attention="fused"):
+    def __init__(self, cfg: DecoderConfig, device="cuda", attention="fused", fuse_epilogues=True):
         T, A, BH = cfg.tokens, cfg.heads * cfg.head_dim, cfg.batch * cfg.heads
         bf = dict(dtype=torch.bfloat16, device=device)
         self.x = torch.empty((T, cfg.hidden), **bf)
         self.h = torch.empty((T, cfg.hidden), **bf)
         self.qkv = torch.empty((T, 3 * A), **bf)
         self.attention = attention
+        self.fuse = fuse_epilogues
         self.q = torch.empty((BH, cfg.seq, cfg.head_dim), **bf)
         kshape = (BH, cfg.head_dim, cfg.seq) if attention == "composed" else (BH, cfg.seq, cfg.head_dim)
         self.k = torch.empty(kshape, **bf)
@@ -162,8 +168,8 @@ class Buffers:
         self.act = torch.empty((T, cfg.ffn), **bf)
 
 
-def _qmm(x, w: Int4Weight, out):
-    return ops.int4_g64_matmul(x, w.packed, w.scale, w.zero, out=out)
+def _qmm(x, w: Int4Weight, out, epilogue=None, aux=None):
+    return ops.int4_g64_matmul(x, w.packed, w.scale, w.zero, out=out, epilogue=epilogue, aux=aux)
 
 
 def layer_forward(cfg: DecoderConfig, lw: LayerWeights, buf: Buffers, cos, sin):
@@ -180,6 +186,15 @@ def layer_forward(cfg: DecoderConfig, lw: LayerWeights, buf: Buffers, cos, sin):
         ops.merge_heads(buf.o, B, H, out=buf.attn)
     else:
         ops.attention_causal(buf.q, buf.k, buf.v, B, H, 1.0 / math.sqrt(D), out=buf.attn)
+    if buf.fuse:
+        # Residual adds and silu(g) * u ride on the projections' stores
+        # (bit-identical to the separate elementwise programs below).
+        _qmm(buf.attn, lw.w_o, buf.x, epilogue="add", aux=buf.x)
+        ops.rmsnorm(buf.x, lw.g_mlp, eps=cfg.eps, out=buf.h)
+        _qmm(buf.h, lw.w_gate, buf.gate)
+        _qmm(buf.h, lw.w_up, buf.act, epilogue="swiglu", aux=buf.gate)
+        _qmm(buf.act, lw.w_down, buf.x, epilogue="add", aux=buf.x)
+        return
     _qmm(buf.attn, lw.w_o, buf.proj)
     ops.elementwise(RESIDUAL_PROGRAM, [buf.x, buf.proj], out_slot=2, out=buf.x)
     ops.rmsnorm(buf.x, lw.g_mlp, eps=cfg.eps, out=buf.h)

@@ -45,9 +45,22 @@ def workspace(nbytes, device):
     return ws
 
 
-def int4_g64_matmul(x, w_packed, scale, zero, out=None):
+_EPI = {None: _lib.MK_EPI_NONE, "add": _lib.MK_EPI_ADD, "swiglu": _lib.MK_EPI_SWIGLU}
+
+
+def _epilogue(epilogue, aux, shape, name):
+    code = _EPI[epilogue]
+    if code != _lib.MK_EPI_NONE:
+        _require(aux, _BF16, "aux")
+        if tuple(aux.shape) != tuple(shape):
+            raise ValueError(f"{name}: aux must have the output's shape {tuple(shape)}")
+    return code
+
+
+def int4_g64_matmul(x, w_packed, scale, zero, out=None, epilogue=None, aux=None):
     """y = x @ ((w - zero) * scale): x bf16 [M,K], w uint8 [K/2,N], scale bf16
-    [K/64,N], zero uint8 [K/64,N] -> bf16 [M,N]."""
+    [K/64,N], zero uint8 [K/64,N] -> bf16 [M,N].  epilogue "add" gives
+    y = r(r(xW) + aux), "swiglu" y = r(r(aux * r(logistic(aux))) * r(xW))."""
     _require(x, _BF16, "x")
     _require(w_packed, (torch.uint8,), "w_packed")
     _require(scale, _BF16, "scale")
@@ -57,10 +70,16 @@ def int4_g64_matmul(x, w_packed, scale, zero, out=None):
     if w_packed.shape[0] * 2 != K or scale.shape != (K // 64, N) or zero.shape != (K // 64, N):
         raise ValueError("int4_g64_matmul: inconsistent shapes")
     y = out if out is not None else torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    epi = _epilogue(epilogue, aux, (M, N), "int4_g64_matmul")
     nb = lib().mk_qmatmul_workspace_bytes(_lib.MK_QFMT_INT4_G64, M, K, N)
     ws = workspace(nb, x.device) if nb > 0 else None
-    check(lib().mk_int4g64_matmul_bf16(_ptr(x), _ptr(w_packed), _ptr(scale), _ptr(zero), _ptr(y),
-                                       M, K, N, _ptr(ws), max(nb, 0), _stream(x.device)))
+    if epi == _lib.MK_EPI_NONE:
+        check(lib().mk_int4g64_matmul_bf16(_ptr(x), _ptr(w_packed), _ptr(scale), _ptr(zero), _ptr(y),
+                                           M, K, N, _ptr(ws), max(nb, 0), _stream(x.device)))
+    else:
+        check(lib().mk_int4g64_matmul_epilogue_bf16(_ptr(x), _ptr(w_packed), _ptr(scale), _ptr(zero), _ptr(y),
+                                                    _ptr(aux), epi, M, K, N, _ptr(ws), max(nb, 0),
+                                                    _stream(x.device)))
     return y
 
 
@@ -91,16 +110,25 @@ def _bmk(a, b):
     return a2.shape[0], a2.shape[1], b2.shape[2], a2.shape[2]
 
 
-def gemm_bf16(a, b, out_f32=False, out=None):
-    """[batch,] M x K @ K x N in bf16 with f32 accumulation -> bf16 (or f32)."""
+def gemm_bf16(a, b, out_f32=False, out=None, epilogue=None, aux=None):
+    """[batch,] M x K @ K x N in bf16 with f32 accumulation -> bf16 (or f32).
+    epilogue "add" / "swiglu" with aux (bf16, the output's shape) as in
+    int4_g64_matmul (bf16 output only)."""
     _require(a, _BF16, "a")
     _require(b, _BF16, "b")
     batch, M, N, K = _bmk(a, b)
     shape = (M, N) if a.dim() == 2 else (batch, M, N)
     c = out if out is not None else torch.empty(
         shape, dtype=torch.float32 if out_f32 else torch.bfloat16, device=a.device)
-    check(lib().mk_gemm_bf16(_ptr(a), _ptr(b), _ptr(c), batch, M, N, K, 1 if out_f32 else 0,
-                             _stream(a.device)))
+    epi = _epilogue(epilogue, aux, shape, "gemm_bf16")
+    if epi == _lib.MK_EPI_NONE:
+        check(lib().mk_gemm_bf16(_ptr(a), _ptr(b), _ptr(c), batch, M, N, K, 1 if out_f32 else 0,
+                                 _stream(a.device)))
+    else:
+        if out_f32:
+            raise ValueError("gemm_bf16: epilogues write bf16")
+        check(lib().mk_gemm_bf16_epilogue(_ptr(a), _ptr(b), _ptr(c), _ptr(aux), epi, batch, M, N, K,
+                                          _stream(a.device)))
     return c
 
 

@@ -215,6 +215,24 @@ def test_decoder_forward_matches_reference(attention):
     assert_rel_close(y.numpy(), ref.numpy(), BF16_RTOL, "decoder forward")
 
 
+def test_decoder_fused_epilogues_bit_identical():
+    """Residual adds and SwiGLU fused into the projections' stores give the
+    same bits as the separate elementwise programs."""
+    need_gpu()
+    from mi355x import decoder
+    cfg = decoder.DecoderConfig(layers=2, hidden=256, heads=2, head_dim=128, ffn=512, batch=2, seq=128)
+    weights = decoder.init_weights(cfg, seed=6)
+    cos, sin = decoder.rope_tables(cfg)
+    x0 = torch.randn((cfg.tokens, cfg.hidden)).to(torch.bfloat16).cuda()
+    outs = []
+    for fuse in (True, False):
+        buf = decoder.Buffers(cfg, fuse_epilogues=fuse)
+        buf.x.copy_(x0)
+        outs.append(decoder.forward(cfg, weights, buf, cos, sin).clone())
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+
+
 def test_decoder_forward_graph_replays_match_eager():
     """A captured forward replays to the eager result (fresh input each time)."""
     need_gpu()

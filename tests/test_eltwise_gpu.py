@@ -132,11 +132,22 @@ def _ulp_check_f32(y, x, ref64, max_rel):
     assert not bad.any(), (xs[fin][bad][:8], y[fin][bad][:8], ref[fin][bad][:8])
 
 
+def _logistic64(x):
+    return np.where(x >= 0, 1.0 / (1.0 + np.exp(-np.abs(x))), np.exp(-np.abs(x)) / (1.0 + np.exp(-np.abs(x))))
+
+
+def _logistic_inputs():
+    return np.concatenate([np.linspace(-110.0, 110.0, 1 << 20).astype(np.float32),
+                           np.array([0.0, -0.0, -80.0, -80.00001, -87.5, -103.0, 17.0, np.inf, -np.inf, np.nan],
+                                    np.float32)])
+
+
 def test_exp_log1p_accuracy_sweep_f32():
-    """mk_exp and mk_log1p against float64 over dense sweeps: within 1e-6
-    relative (8 f32 ulp; the workload's f32 tolerance is 1e-5)."""
+    """mk_exp, mk_log1p and mk_logistic against float64 over dense sweeps:
+    within 1e-6 relative (8 f32 ulp; the workload's f32 tolerance is 1e-5)."""
     ops = _ops()
-    for name, xs, fn in [("EXP", _exp_inputs(), np.exp), ("LOG1P", _log1p_inputs(), np.log1p)]:
+    for name, xs, fn in [("EXP", _exp_inputs(), np.exp), ("LOG1P", _log1p_inputs(), np.log1p),
+                         ("LOGISTIC", _logistic_inputs(), _logistic64)]:
         prog = [("LOAD", 0, 0, 0, 0, 0.0), (name, 1, 0, 0, 0, 0.0)]
         y = ops.elementwise(prog, [dev(xs)], out_slot=1).cpu().numpy()
         with np.errstate(all="ignore"):
@@ -149,7 +160,8 @@ def test_exp_log1p_accuracy_sweep_bf16():
     neighbour of it when the exact value lies within 2^-14 of a rounding
     midpoint."""
     ops = _ops()
-    for name, xs, fn in [("EXP", _exp_inputs(), np.exp), ("LOG1P", _log1p_inputs(), np.log1p)]:
+    for name, xs, fn in [("EXP", _exp_inputs(), np.exp), ("LOG1P", _log1p_inputs(), np.log1p),
+                         ("LOGISTIC", _logistic_inputs(), _logistic64)]:
         xb = obf.f32_to_bf16_bits(xs)
         xf = obf.bf16_bits_to_f32(xb)
         prog = [("LOAD", 0, 0, 0, 0, 0.0), (name, 1, 0, 0, 0, 0.0)]

@@ -1,0 +1,104 @@
+"""GPU checks of the fused store epilogues (mk_gemm_bf16_epilogue and
+mk_int4g64 / mk_int8pc _matmul_epilogue_bf16): each must equal, bit for bit,
+the plain product followed by the bf16 elementwise program it replaces
+(residual add; silu(g) * u), on every kernel path (DMA / 256 / 128-tile
+GEMMs; streaming, wide, many-row and dequantise-then-GEMM quantized paths),
+in place (aux == out) and out of place."""
+
+import numpy as np
+import pytest
+
+from _gpu import dev, dev_bf16, need_gpu, torch
+from oracle import quant
+
+pytestmark = pytest.mark.gpu
+
+ADD = [("LOAD", 0, 0, 0, 0, 0.0), ("LOAD", 1, 1, 0, 0, 0.0), ("ADD", 2, 0, 1, 0, 0.0)]
+SWIGLU = [("LOAD", 0, 0, 0, 0, 0.0), ("LOAD", 1, 1, 0, 0, 0.0),
+          ("LOGISTIC", 2, 0, 0, 0, 0.0), ("MUL", 3, 0, 2, 0, 0.0), ("MUL", 4, 3, 1, 0, 0.0)]
+
+
+def _ops():
+    need_gpu()
+    from mi355x import ops
+    return ops
+
+
+def _unfused(ops, y, aux, epilogue):
+    if epilogue == "add":
+        return ops.elementwise(ADD, [aux, y], out_slot=2)
+    return ops.elementwise(SWIGLU, [aux, y], out_slot=4)
+
+
+@pytest.mark.parametrize("epilogue", ["add", "swiglu"])
+@pytest.mark.parametrize("batch,M,N,K", [(1, 512, 512, 256), (1, 256, 768, 64), (2, 256, 256, 96),
+                                         (1, 200, 136, 64), (3, 64, 128, 32)])
+def test_gemm_epilogue_matches_unfused(epilogue, batch, M, N, K):
+    ops = _ops()
+    g = torch.Generator().manual_seed(M + N + K + batch)
+    shape_a = (M, K) if batch == 1 else (batch, M, K)
+    shape_b = (K, N) if batch == 1 else (batch, K, N)
+    shape_c = (M, N) if batch == 1 else (batch, M, N)
+    a = (torch.randn(shape_a, generator=g) / 8).to(torch.bfloat16).cuda()
+    b = (torch.randn(shape_b, generator=g) / 8).to(torch.bfloat16).cuda()
+    aux = (torch.randn(shape_c, generator=g) * 2).to(torch.bfloat16).cuda()
+    ref = _unfused(ops, ops.gemm_bf16(a, b), aux, epilogue)
+    y = ops.gemm_bf16(a, b, epilogue=epilogue, aux=aux)
+    z = aux.clone()
+    ops.gemm_bf16(a, b, out=z, epilogue=epilogue, aux=z)  # in place
+    torch.cuda.synchronize()
+    assert torch.equal(y, ref)
+    assert torch.equal(z, ref)
+
+
+# M = 1 / 16: streaming and wide kernels; 130 / 256: many-row kernel; 800:
+# dequantise-then-GEMM; (16, 1024, 1024): split-K with the reduce pass.
+@pytest.mark.parametrize("epilogue", ["add", "swiglu"])
+@pytest.mark.parametrize("M,K,N", [(1, 512, 256), (16, 4096, 1024), (16, 1024, 14336), (130, 256, 192),
+                                   (256, 512, 512), (800, 256, 256), (5, 512, 136)])
+def test_quantized_epilogue_matches_unfused(epilogue, M, K, N):
+    ops = _ops()
+    rng = np.random.default_rng(M * 3 + K + N)
+    x, packed, s, z = quant.make_int4_case(rng, M, K, N)
+    args4 = (dev_bf16(x), dev(packed), dev_bf16(s), dev(z))
+    aux = (torch.randn((M, N), generator=torch.Generator().manual_seed(M + N)) * 2).to(torch.bfloat16).cuda()
+    ref = _unfused(ops, ops.int4_g64_matmul(*args4), aux, epilogue)
+    y = ops.int4_g64_matmul(*args4, epilogue=epilogue, aux=aux)
+    zz = aux.clone()
+    ops.int4_g64_matmul(*args4, out=zz, epilogue=epilogue, aux=zz)
+    torch.cuda.synchronize()
+    assert torch.equal(y, ref), f"int4 {M}x{K}x{N} {epilogue}"
+    assert torch.equal(zz, ref), f"int4 {M}x{K}x{N} {epilogue} in place"
+    x8, w8, s8 = quant.make_int8_case(rng, M, K, N)
+    args8 = (dev_bf16(x8), dev(w8), dev(s8))
+    from mi355x import _lib
+    L = _lib.lib()
+    y8 = ops.int8_pc_matmul(*args8)
+    ref8 = _unfused(ops, y8, aux, epilogue)
+    out8 = torch.empty_like(y8)
+    nb = L.mk_qmatmul_workspace_bytes(_lib.MK_QFMT_INT8_PC, M, K, N)
+    ws = ops.workspace(nb, "cuda:0") if nb > 0 else None
+    code = {"add": _lib.MK_EPI_ADD, "swiglu": _lib.MK_EPI_SWIGLU}[epilogue]
+    rc = L.mk_int8pc_matmul_epilogue_bf16(args8[0].data_ptr(), args8[1].data_ptr(), args8[2].data_ptr(),
+                                         out8.data_ptr(), aux.data_ptr(), code, M, K, N,
+                                         ws.data_ptr() if ws is not None else None, max(nb, 0),
+                                         torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 0, L.mk_last_error().decode()
+    assert torch.equal(out8, ref8), f"int8 {M}x{K}x{N} {epilogue}"
+
+
+def test_epilogue_rejects_bad_arguments():
+    ops = _ops()
+    from mi355x import _lib
+    L = _lib.lib()
+    a = torch.zeros((256, 64), dtype=torch.bfloat16, device="cuda")
+    b = torch.zeros((64, 256), dtype=torch.bfloat16, device="cuda")
+    c = torch.empty((256, 256), dtype=torch.bfloat16, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    assert L.mk_gemm_bf16_epilogue(a.data_ptr(), b.data_ptr(), c.data_ptr(), None, _lib.MK_EPI_ADD, 1, 256,
+                                   256, 64, st) == _lib.MK_EINVAL
+    assert L.mk_gemm_bf16_epilogue(a.data_ptr(), b.data_ptr(), c.data_ptr(), c.data_ptr(), 7, 1, 256, 256, 64,
+                                   st) == _lib.MK_EINVAL
+    with pytest.raises(ValueError):
+        ops.gemm_bf16(a, b, epilogue="add", aux=torch.zeros((8, 8), dtype=torch.bfloat16, device="cuda"))
