@@ -523,6 +523,7 @@ __global__ __launch_bounds__(WM_ * WN_ * 64) void gemm_bf16_256_kernel(GemmArgs 
 #define MK_GEMM_STAGES 4
 #endif
 constexpr int kGemmStages = MK_GEMM_STAGES;
+constexpr int kPipeStages = 5;  // 5 x 32 KB: all of the 160 KB LDS
 constexpr int kGemmStageBytes = 32 * 1024;
 
 __device__ __forceinline__ int swz_b2(int k, int c) { return c ^ ((2 * (k & 3)) | (((k >> 3) & 1) << 3)); }
@@ -534,7 +535,7 @@ __device__ __forceinline__ void dma16_asm(const void* src, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base) : "memory");
 }
 
-template <int WN_>  // waves 2 x WN_; each 128 x (256 / WN_)
+template <int WN_, bool PIPE>  // waves 2 x WN_; each 128 x (256 / WN_)
 __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs p) {
   constexpr int BM = 256, BN = 256, BK = 32, TM = 8, TN = 256 / WN_ / 16;
   constexpr int NW = 2 * WN_, DI = 16 / NW;  // waves; DMA instructions per wave for A (and B)
@@ -605,7 +606,7 @@ __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs
   // 4-wave variant, with twice the tiles per wave, reads it at the end.
   const int mrow = m0 + wm * (16 * TM) + (lane & 15);
   const int ncol = n0 + wn * (16 * TN) + 4 * (lane >> 4);
-  constexpr bool kPreAux = WN_ == 4;
+  constexpr bool kPreAux = WN_ == 4 && !PIPE;
   u32x2 auxv[kPreAux ? TM : 1][kPreAux ? TN : 1];
   if (kPreAux && p.epi != MK_EPI_NONE) {
     const uint16_t* X = p.aux + (size_t)blockIdx.z * p.sc;
@@ -618,6 +619,107 @@ __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs
   }
 
   const int KT = K / BK;
+  if constexpr (PIPE) {
+    // Fragment pipelining: the fragments of stage kt+1 are read from LDS
+    // while the MFMAs of stage kt (fragments already in registers) run, so
+    // LDS latency overlaps the matrix pipe instead of following it.  A
+    // stage's slot is free once its fragments are in registers, so a ring
+    // of kPipeStages slots keeps kPipeStages - 1 stages of DMA in flight.
+    // Measured on 4096^3 (skip-work variants of this loop): the L2 -> LDS
+    // feed alone takes ~70 us and the MFMA + fragment loop alone ~94 us, so
+    // the kernel is bound by how well the two overlap (~126 us).
+    auto read_b = [&](const unsigned char* st, u32x4* bf) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(st + boff[2 * j]));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(st + boff[2 * j + 1]));
+        const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+        bf[j] = u32x4{l2.x, l2.y, h2.x, h2.y};
+      }
+    };
+    // Ring of S stages; stage s lives in slot s % S.  Iteration kt issues
+    // stage kt + S (if it exists) into the slot stage kt has just left.
+    constexpr int S = kPipeStages;
+    auto issue_a = [&](int ks, int slot, int u) {
+      dma16_asm(asrc[u] + ks * BK, sbase + (uint32_t)(slot * kGemmStageBytes + (DI * wave + u) * 1024));
+    };
+    auto issue_b = [&](int ks, int slot, int u) {
+      dma16_asm(bsrc[u] + (size_t)ks * BK * N,
+                sbase + (uint32_t)(slot * kGemmStageBytes + ABYTES + (DI * wave + u) * 1024));
+    };
+    // The host only picks this kernel when KT >= 2 S (K >= 4096).
+    for (int s = 0; s < S; ++s) {
+#pragma unroll
+      for (int u = 0; u < DI; ++u) issue_a(s, s, u);
+#pragma unroll
+      for (int u = 0; u < DI; ++u) issue_b(s, s, u);
+    }
+    vm_wait(2 * DI * (S - 1));
+    asm volatile("s_barrier" ::: "memory");
+    // Fragments: A in one set (fragment i of stage kt+1 is read into the
+    // registers of fragment i of stage kt right after its last MFMA), B in
+    // two sets alternated by a 2x unrolled loop.
+    u32x4 bf0[TN], bf1[TN], af[TM];
+    read_b(smem, bf0);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const u32x4*>(smem + aoff + 1024 * i);
+    int slot_cur = 0;  // kt % S
+    auto step = [&](auto with_dma, int kt, u32x4* bfc, u32x4* bfn) {
+      constexpr bool kDma = decltype(with_dma)::value;
+      __builtin_amdgcn_sched_barrier(0);
+      // Own DMAs of stage kt+1 landed and own fragment reads of stage kt
+      // complete; after the barrier every wave's are, so stage kt+1 is
+      // visible and stage kt's slot is free.  lgkmcnt(0) and the barrier
+      // are builtins so the compiler knows the reads have completed and
+      // adds no wait of its own later.  DMA stages in flight after stage
+      // kt+1: kt+2 .. min(kt+S-1, KT-1), i.e. S-2 while iteration kt still
+      // issues one; in the last iterations the wait is for all of them.
+      if constexpr (kDma) vm_wait(2 * DI * (S - 2));
+      else vm_wait(0);
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      const int ks = kt + S;
+      const int slot_nx = slot_cur + 1 == S ? 0 : slot_cur + 1;
+      // On the last stage this reads a stale slot; the values are unused.
+      const unsigned char* nx = smem + slot_nx * kGemmStageBytes;
+      read_b(nx, bfn);
+      // The DMAs of the new stage are spread over the MFMA groups.
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(bfc[j], af[i], acc[i][j]);
+        af[i] = *reinterpret_cast<const u32x4*>(nx + aoff + 1024 * i);
+        if constexpr (kDma) {
+          if (i < DI) issue_a(ks, slot_cur, i);
+          else if (i < 2 * DI) issue_b(ks, slot_cur, i - DI);
+        }
+        // Keep this order: the compiler would otherwise cluster the reads
+        // and DMAs and move MFMAs across the barrier.
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      slot_cur = slot_nx;
+    };
+    using DmaOn = std::integral_constant<bool, true>;
+    using DmaOff = std::integral_constant<bool, false>;
+    // Pairs of iterations that both issue a stage; kt stays even, so the
+    // B fragment sets alternate at compile time.
+    int kt = 0;
+    for (; kt + 1 + S < KT; kt += 2) {
+      step(DmaOn{}, kt, bf0, bf1);
+      step(DmaOn{}, kt + 1, bf1, bf0);
+    }
+    // S or S+1 iterations remain; the first of S+1 still issues a stage.
+    if (kt + S < KT) {
+      step(DmaOn{}, kt, bf0, bf1);
+      ++kt;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bf0[j] = bf1[j];
+    }
+#pragma unroll
+    for (int t = 0; t < S; ++t) step(DmaOff{}, kt + t, (t & 1) ? bf1 : bf0, (t & 1) ? bf0 : bf1);
+  } else {
   const int pre = KT < kGemmStages - 1 ? KT : kGemmStages - 1;
   for (int kt = 0; kt < pre; ++kt) issue(kt);
   for (int kt = 0; kt < KT; ++kt) {
@@ -644,6 +746,7 @@ __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs
 #pragma unroll
       for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(bf[j], af, acc[i][j]);
     }
+  }
   }
 
   // Epilogue (C^T tiles): lane owns row m, columns n..n+3 of each tile.
@@ -759,12 +862,25 @@ int run_gemm_bf16(const char* fn, const void* a, const void* b, void* c, const v
     constexpr size_t lds = (size_t)mk::kGemmStages * mk::kGemmStageBytes;
     const dim3 grid((unsigned)((M / 256) * (N / 256)), 1, (unsigned)batch);
     const char* w = getenv("MK_GEMM_WAVES");
+    const char* pv = getenv("MK_GEMM_PIPE");
+    // The pipelined kernel (fragment prefetch + 5-stage ring) for long K
+    // loops without an epilogue.  It has no registers left to preload an
+    // epilogue operand, so epilogue calls keep the kernel that does.  At
+    // K = 2048 it is 3-5 % faster alone but ran the decoder's sequence of
+    // K = 2048 projections 1 % slower end to end (5.51 vs 5.45 ms): the
+    // clock under it (GRBM_GUI_ACTIVE per ns) is ~2.1 GHz against ~2.35 GHz,
+    // which slows the kernels around it.  From K = 4096 it gains 7-9 %.
+    const bool pipe = !(pv && atoi(pv) == 0) && p.epi == MK_EPI_NONE && K >= 4096;
     if (w && atoi(w) == 4) {
-      e = lds_opt_in((const void*)mk::gemm_bf16_256dma_kernel<2>, lds);
-      if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256dma_kernel<2>), grid, dim3(256), lds, st, p);
+      e = lds_opt_in((const void*)mk::gemm_bf16_256dma_kernel<2, false>, lds);
+      if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256dma_kernel<2, false>), grid, dim3(256), lds, st, p);
+    } else if (pipe) {
+      constexpr size_t lds_p = (size_t)mk::kPipeStages * mk::kGemmStageBytes;
+      e = lds_opt_in((const void*)mk::gemm_bf16_256dma_kernel<4, true>, lds_p);
+      if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256dma_kernel<4, true>), grid, dim3(512), lds_p, st, p);
     } else {
-      e = lds_opt_in((const void*)mk::gemm_bf16_256dma_kernel<4>, lds);
-      if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256dma_kernel<4>), grid, dim3(512), lds, st, p);
+      e = lds_opt_in((const void*)mk::gemm_bf16_256dma_kernel<4, false>, lds);
+      if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256dma_kernel<4, false>), grid, dim3(512), lds, st, p);
     }
     if (e == hipSuccess) e = hipGetLastError();
   } else if (tile == 256 && M % 256 == 0 && N % 256 == 0 && K % 64 == 0) {
