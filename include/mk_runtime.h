@@ -135,6 +135,52 @@ mkrt_error* mkrt_execute(mkrt_executable* exe, mkrt_buffer* const* inputs, int n
                          mkrt_buffer** outputs, mkrt_event** done);
 void mkrt_executable_destroy(mkrt_executable* exe);
 
+/* ------------------------------------------------------------------------
+ * Serialization and the compile cache.
+ *
+ * mkrt_executable_serialize replaces PJRT_Executable_Serialize
+ * (api/pjrt_executable.cc:169-187) and mkrt_deserialize replaces
+ * PJRT_Executable_DeserializeAndLoad (:303-340).  The reference serializes
+ * the program (a VHLO portable artifact, core/mps_executable.mm:7127-7143)
+ * and recompiles it on load.  Here the serialized form carries the
+ * StableHLO text plus the gfx950 code objects of the executable's fused
+ * elementwise programs, so a deserialized executable compiles nothing on
+ * its first execute.  Layout (little-endian):
+ *   "MKEX" | u32 version (1) | u32 flags (0) | u64 program bytes | program |
+ *   u32 code objects | per object: u64 source bytes | source |
+ *   u64 code bytes | code
+ * Errors as the reference's: empty or malformed data -> INVALID_ARGUMENT;
+ * a program that does not compile -> its compile error.
+ *
+ * The elementwise code objects are also cached on disk, one file per
+ * object under MK_CACHE_DIR (default $HOME/.cache/mi355x-mk), keyed by
+ * source, compile options and hiprtc version; MK_DISABLE_CACHE_PERSIST=1
+ * turns that off.  This is the counterpart of the reference's persisted
+ * autotune cache (core/mps_executable.mm:3270-3420,
+ * JAX_METALLIB_AUTOTUNE_CACHE_DIR / JAX_METALLIB_DISABLE_AUTOTUNE_CACHE_PERSIST).
+ * ---------------------------------------------------------------------- */
+typedef struct mkrt_serialized mkrt_serialized;
+mkrt_error* mkrt_executable_serialize(const mkrt_executable* exe, mkrt_serialized** out);
+/* The same from program text, without a client or device (parse, plan and
+ * compile the elementwise programs). */
+mkrt_error* mkrt_serialize_program(const char* code, int64_t code_bytes, const char* format,
+                                   mkrt_serialized** out);
+const void* mkrt_serialized_data(const mkrt_serialized* s);
+int64_t mkrt_serialized_size(const mkrt_serialized* s);
+void mkrt_serialized_destroy(mkrt_serialized* s);
+mkrt_error* mkrt_deserialize(mkrt_client* client, const void* bytes, int64_t size, mkrt_executable** out);
+/* Header and table check without a device: program size and code-object
+ * count, or INVALID_ARGUMENT for malformed data. */
+mkrt_error* mkrt_serialized_inspect(const void* bytes, int64_t size, int64_t* program_bytes,
+                                    int* num_code_objects);
+/* PJRT_Executable_Fingerprint (pjrt_executable.cc:189-196 returns one
+ * constant string for every executable): here 16 hex digits of FNV-1a 64
+ * over the program text, equal for equal programs. */
+const char* mkrt_executable_fingerprint(const mkrt_executable* exe);
+/* Process totals of the elementwise JIT: hiprtc compiles, disk-cache hits,
+ * memory-cache hits. */
+void mkrt_jit_cache_stats(int64_t* compiles, int64_t* disk_hits, int64_t* memory_hits);
+
 /* Events (pjrt_event.cc, core/completion_event.h).  await waits at most
  * timeout_ms (< 0: the MK_COMPLETION_TIMEOUT_MS environment value, default
  * 30000) and returns DEADLINE_EXCEEDED when it elapses (the work is left

@@ -2,6 +2,19 @@
 // HIP source, compiles it for gfx950 with hiprtc on first use and caches the
 // loaded kernel per (device, dtype, program).
 //
+// Compiled code objects are cached at two more levels, keyed by the exact
+// source text, the compile options and the hiprtc version:
+//   * in memory for the process (shared by every device), and seedable from
+//     a serialized executable (mkrt_deserialize), so a deserialized program
+//     launches without compiling;
+//   * on disk, one file per code object under MK_CACHE_DIR (default
+//     $HOME/.cache/mi355x-mk), written atomically (temporary file + rename)
+//     and verified against the full key on read.  MK_DISABLE_CACHE_PERSIST=1
+//     turns the disk level off.  This is the counterpart of the reference's
+//     persisted autotune cache (core/mps_executable.mm:3270-3420,
+//     JAX_METALLIB_AUTOTUNE_CACHE_DIR / _DISABLE_AUTOTUNE_CACHE_PERSIST):
+//     here the first-call cost is the hiprtc compile, not autotuning.
+//
 // This is the MI355X counterpart of the reference's generated fusion kernels
 // (GenerateFusedKernelSource, core/mps_executable.mm:4445-4586, with a
 // pipeline cache keyed by the chain, :4588-4629).  The generated kernel
@@ -18,6 +31,11 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <stdlib.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -37,7 +55,99 @@ struct JitKernel {
 };
 
 std::mutex g_mu;
-std::unordered_map<std::string, JitKernel> g_cache;
+std::unordered_map<std::string, JitKernel> g_cache;                 // loaded kernels per device
+std::unordered_map<std::string, std::vector<char>> g_code;          // code objects by source
+std::atomic<int64_t> g_compiles{0}, g_disk_hits{0}, g_mem_hits{0};
+
+// No FMA contraction: every StableHLO op rounds its own result, exactly as
+// the interpreter kernel and the op-by-op oracle evaluate it.
+const char* const kOpts[] = {"--offload-arch=gfx950", "-O3", "-ffp-contract=off", "-Xclang", "-target-feature",
+                             "-Xclang", "-packed-fp32-ops"};
+constexpr int kNumOpts = 7;
+
+// Everything the code object depends on besides the source.
+const std::string& compile_tag() {
+  static const std::string tag = [] {
+    int maj = 0, mn = 0;
+    hiprtcVersion(&maj, &mn);
+    std::string t = "hiprtc " + std::to_string(maj) + "." + std::to_string(mn) + "|";
+    for (int i = 0; i < kNumOpts; ++i) (t += kOpts[i]) += ' ';
+    return t;
+  }();
+  return tag;
+}
+
+uint64_t fnv1a64(const std::string& a, const std::string& b) {
+  uint64_t h = 1469598103934665603ull;
+  for (const std::string* s : {&a, &b})
+    for (unsigned char c : *s) h = (h ^ c) * 1099511628211ull;
+  return h;
+}
+
+// Disk cache directory ("" when disabled or unusable).
+std::string cache_dir() {
+  const char* off = getenv("MK_DISABLE_CACHE_PERSIST");
+  if (off && off[0] && strcmp(off, "0") != 0) return "";
+  std::string dir;
+  const char* env = getenv("MK_CACHE_DIR");
+  if (env && env[0]) {
+    dir = env;
+  } else {
+    const char* home = getenv("HOME");
+    if (!home || !home[0]) return "";
+    dir = std::string(home) + "/.cache";
+    mkdir(dir.c_str(), 0755);
+    dir += "/mi355x-mk";
+  }
+  mkdir(dir.c_str(), 0755);
+  struct stat st;
+  if (stat(dir.c_str(), &st) != 0 || !S_ISDIR(st.st_mode)) return "";
+  return dir;
+}
+
+// File layout: "MKCO", u32 version 1, u64 key bytes, key (tag + source),
+// u64 code bytes, code.
+constexpr uint32_t kCodeFileVersion = 1;
+
+std::string cache_path(const std::string& dir, const std::string& src) {
+  char name[64];
+  snprintf(name, sizeof(name), "/ew-%016llx.hsaco", (unsigned long long)fnv1a64(compile_tag(), src));
+  return dir + name;
+}
+
+bool read_cached(const std::string& path, const std::string& src, std::vector<char>* code) {
+  FILE* f = fopen(path.c_str(), "rb");
+  if (!f) return false;
+  bool ok = false;
+  char magic[4];
+  uint32_t ver = 0;
+  uint64_t klen = 0, clen = 0;
+  const std::string key = compile_tag() + src;
+  if (fread(magic, 1, 4, f) == 4 && memcmp(magic, "MKCO", 4) == 0 && fread(&ver, 4, 1, f) == 1 &&
+      ver == kCodeFileVersion && fread(&klen, 8, 1, f) == 1 && klen == key.size()) {
+    std::string k(klen, '\0');
+    if (fread(&k[0], 1, klen, f) == klen && k == key && fread(&clen, 8, 1, f) == 1 && clen > 0 &&
+        clen < (1ull << 30)) {
+      code->resize(clen);
+      ok = fread(code->data(), 1, clen, f) == clen;
+    }
+  }
+  fclose(f);
+  return ok;
+}
+
+void write_cached(const std::string& path, const std::string& src, const std::vector<char>& code) {
+  const std::string key = compile_tag() + src;
+  const std::string tmp = path + ".tmp." + std::to_string((long long)getpid());
+  FILE* f = fopen(tmp.c_str(), "wb");
+  if (!f) return;
+  const uint64_t klen = key.size(), clen = code.size();
+  bool ok = fwrite("MKCO", 1, 4, f) == 4 && fwrite(&kCodeFileVersion, 4, 1, f) == 1 && fwrite(&klen, 8, 1, f) == 1 &&
+            fwrite(key.data(), 1, klen, f) == klen && fwrite(&clen, 8, 1, f) == 1 &&
+            fwrite(code.data(), 1, clen, f) == clen;
+  ok = (fclose(f) == 0) && ok;
+  if (!ok || rename(tmp.c_str(), path.c_str()) != 0) unlink(tmp.c_str());
+}
 
 std::string key_of(int device, int dtype, const mk_ew_instr* prog, int n_instr, int n_inputs, int out_slot) {
   std::string k;
@@ -183,17 +293,13 @@ std::string generate(int dtype, const mk_ew_instr* prog, int n_instr, int n_inpu
   return s;
 }
 
-hipError_t compile_and_load(const std::string& src, JitKernel* k, std::string* err) {
+bool hiprtc_compile(const std::string& src, std::vector<char>* code, std::string* err) {
   hiprtcProgram p;
   if (hiprtcCreateProgram(&p, src.c_str(), "mk_ew_jit.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS) {
     *err = "hiprtcCreateProgram failed";
-    return hipErrorUnknown;
+    return false;
   }
-  // No FMA contraction: every StableHLO op rounds its own result, exactly as
-  // the interpreter kernel and the op-by-op oracle evaluate it.
-  const char* opts[] = {"--offload-arch=gfx950", "-O3", "-ffp-contract=off", "-Xclang", "-target-feature",
-                        "-Xclang", "-packed-fp32-ops"};
-  const hiprtcResult r = hiprtcCompileProgram(p, 7, opts);
+  const hiprtcResult r = hiprtcCompileProgram(p, kNumOpts, kOpts);
   if (r != HIPRTC_SUCCESS) {
     size_t ls = 0;
     hiprtcGetProgramLogSize(p, &ls);
@@ -201,13 +307,37 @@ hipError_t compile_and_load(const std::string& src, JitKernel* k, std::string* e
     if (ls) hiprtcGetProgramLog(p, &log[0]);
     *err = "hiprtc compile failed: " + log;
     hiprtcDestroyProgram(&p);
-    return hipErrorUnknown;
+    return false;
   }
   size_t cs = 0;
   hiprtcGetCodeSize(p, &cs);
-  std::vector<char> code(cs);
-  hiprtcGetCode(p, code.data());
+  code->resize(cs);
+  hiprtcGetCode(p, code->data());
   hiprtcDestroyProgram(&p);
+  g_compiles.fetch_add(1);
+  return true;
+}
+
+// Code object of a source: memory, then disk, then hiprtc.  g_mu held.
+const std::vector<char>* code_for(const std::string& src, std::string* err) {
+  auto it = g_code.find(src);
+  if (it != g_code.end()) {
+    g_mem_hits.fetch_add(1);
+    return &it->second;
+  }
+  std::vector<char> code;
+  const std::string dir = cache_dir();
+  const std::string path = dir.empty() ? "" : cache_path(dir, src);
+  if (!path.empty() && read_cached(path, src, &code)) {
+    g_disk_hits.fetch_add(1);
+  } else {
+    if (!hiprtc_compile(src, &code, err)) return nullptr;
+    if (!path.empty()) write_cached(path, src, code);
+  }
+  return &g_code.emplace(src, std::move(code)).first->second;
+}
+
+hipError_t load_module(const std::vector<char>& code, JitKernel* k, std::string* err) {
   hipError_t e = hipModuleLoadData(&k->mod, code.data());
   if (e != hipSuccess) {
     *err = std::string("hipModuleLoadData: ") + hipGetErrorString(e);
@@ -232,14 +362,38 @@ int ew_jit_get(int dtype, const mk_ew_instr* prog, int n_instr, int n_inputs, in
   std::lock_guard<std::mutex> lock(g_mu);
   auto it = g_cache.find(key);
   if (it == g_cache.end()) {
-    JitKernel k;
     std::string err;
-    e = compile_and_load(generate(dtype, prog, n_instr, n_inputs, out_slot), &k, &err);
+    const std::vector<char>* code = code_for(generate(dtype, prog, n_instr, n_inputs, out_slot), &err);
+    if (!code) return fail(MK_ELAUNCH, "mk_elementwise: %s", err.c_str());
+    JitKernel k;
+    e = load_module(*code, &k, &err);
     if (e != hipSuccess) return fail(MK_ELAUNCH, "mk_elementwise: %s", err.c_str());
     it = g_cache.emplace(key, k).first;
   }
   *fn_out = (void*)it->second.fn;
   return MK_OK;
+}
+
+int ew_jit_code(int dtype, const mk_ew_instr* prog, int n_instr, int n_inputs, int out_slot, std::string* source,
+                std::vector<char>* code) {
+  *source = generate(dtype, prog, n_instr, n_inputs, out_slot);
+  std::lock_guard<std::mutex> lock(g_mu);
+  std::string err;
+  const std::vector<char>* c = code_for(*source, &err);
+  if (!c) return fail(MK_ELAUNCH, "mk_elementwise: %s", err.c_str());
+  *code = *c;
+  return MK_OK;
+}
+
+void ew_jit_seed(const std::string& source, const std::vector<char>& code) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  g_code.emplace(source, code);
+}
+
+void ew_jit_stats(int64_t* compiles, int64_t* disk_hits, int64_t* mem_hits) {
+  *compiles = g_compiles.load();
+  *disk_hits = g_disk_hits.load();
+  *mem_hits = g_mem_hits.load();
 }
 
 }  // namespace mkc

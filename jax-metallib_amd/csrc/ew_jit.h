@@ -2,7 +2,10 @@
 // kernels for mk_ew_instr programs, cached per device and program.
 #pragma once
 
+#include <stdint.h>
+
 #include <string>
+#include <vector>
 
 #include "../../include/mk_kernels.h"
 
@@ -15,5 +18,17 @@ std::string ew_jit_source(int dtype, const mk_ew_instr* prog, int n_instr, int n
 // device, compiling and loading it on first use.  Returns MK_OK or an MK_E*
 // code with the message recorded for mk_last_error().
 int ew_jit_get(int dtype, const mk_ew_instr* prog, int n_instr, int n_inputs, int out_slot, void** fn_out);
+
+// Source and code object of a validated program (compiled, or taken from the
+// memory or disk cache); needs no device.
+int ew_jit_code(int dtype, const mk_ew_instr* prog, int n_instr, int n_inputs, int out_slot, std::string* source,
+                std::vector<char>* code);
+
+// Adds a code object for a source to the in-memory cache (a deserialized
+// executable's), so its first launch loads it instead of compiling.
+void ew_jit_seed(const std::string& source, const std::vector<char>& code);
+
+// Process totals: hiprtc compiles, disk-cache hits, memory-cache hits.
+void ew_jit_stats(int64_t* compiles, int64_t* disk_hits, int64_t* mem_hits);
 
 }  // namespace mkc

@@ -29,6 +29,7 @@
 #include <thread>
 #include <vector>
 
+#include "../ew_jit.h"
 #include "mk_kernels.h"
 #include "mk_runtime.h"
 #include "planner.h"
@@ -257,6 +258,8 @@ struct mkrt_event {
 
 struct mkrt_executable {
   mkrt_client* client = nullptr;
+  std::string program;      // the StableHLO text it was compiled from
+  std::string fingerprint;  // 16 hex digits of FNV-1a 64 over program
   mkrt::Function fn;
   mkrt::Plan plan;
   std::string plan_text;
@@ -537,7 +540,107 @@ mkrt_error* compile_text(const char* code, int64_t code_bytes, const char* forma
   return nullptr;
 }
 
+std::string fingerprint_of(const std::string& program) {
+  uint64_t h = 1469598103934665603ull;
+  for (unsigned char ch : program) h = (h ^ ch) * 1099511628211ull;
+  char b[20];
+  snprintf(b, sizeof(b), "%016llx", (unsigned long long)h);
+  return b;
+}
+
+// Serialized executable: "MKEX" | u32 version | u32 flags (0) | u64 program
+// bytes | program | u32 code objects | per object: u64 source bytes |
+// source | u64 code bytes | code.  Little-endian.
+constexpr uint32_t kSerialVersion = 1;
+
+void put_u32(std::string& b, uint32_t v) { b.append(reinterpret_cast<const char*>(&v), 4); }
+void put_u64(std::string& b, uint64_t v) { b.append(reinterpret_cast<const char*>(&v), 8); }
+
+mkrt_error* serialize_plan(const std::string& program, const mkrt::Plan& plan, std::string* out) {
+  std::vector<std::pair<std::string, std::vector<char>>> objs;
+  for (const mkrt::Step& st : plan.steps) {
+    if (st.kind != mkrt::ST_EW) continue;
+    std::string src;
+    std::vector<char> code;
+    if (mkc::ew_jit_code(st.dt, st.prog.data(), (int)st.prog.size(), (int)st.in.size(), st.prog_out, &src, &code) !=
+        MK_OK)
+      return make_error(MKRT_INTERNAL, "serialize: elementwise program: %s", mk_last_error());
+    bool dup = false;
+    for (const auto& o : objs) dup = dup || o.first == src;
+    if (!dup) objs.emplace_back(std::move(src), std::move(code));
+  }
+  std::string& b = *out;
+  b.clear();
+  b.append("MKEX", 4);
+  put_u32(b, kSerialVersion);
+  put_u32(b, 0);
+  put_u64(b, program.size());
+  b += program;
+  put_u32(b, (uint32_t)objs.size());
+  for (const auto& o : objs) {
+    put_u64(b, o.first.size());
+    b += o.first;
+    put_u64(b, o.second.size());
+    b.append(o.second.data(), o.second.size());
+  }
+  return nullptr;
+}
+
+// Parsed view of a serialized executable (pointers into the caller's bytes).
+struct SerialView {
+  const char* program = nullptr;
+  uint64_t program_bytes = 0;
+  std::vector<std::pair<std::string, std::vector<char>>> objs;
+};
+
+mkrt_error* parse_serialized(const void* bytes, int64_t size, SerialView* v, bool copy_objects) {
+  if (!bytes || size <= 0)
+    return make_error(MKRT_INVALID_ARGUMENT, "DeserializeAndLoad: empty serialized data");
+  const char* p = static_cast<const char*>(bytes);
+  const char* end = p + size;
+  auto take = [&](void* dst, size_t n) {
+    if ((size_t)(end - p) < n) return false;
+    memcpy(dst, p, n);
+    p += n;
+    return true;
+  };
+  char magic[4];
+  uint32_t ver = 0, flags = 0, nobj = 0;
+  if (!take(magic, 4) || memcmp(magic, "MKEX", 4) != 0)
+    return make_error(MKRT_INVALID_ARGUMENT, "DeserializeAndLoad: not a serialized mi355x executable (bad magic)");
+  if (!take(&ver, 4) || !take(&flags, 4))
+    return make_error(MKRT_INVALID_ARGUMENT, "DeserializeAndLoad: truncated header");
+  if (ver != kSerialVersion)
+    return make_error(MKRT_INVALID_ARGUMENT, "DeserializeAndLoad: serialized format version %u, this build reads %u",
+                      ver, kSerialVersion);
+  if (!take(&v->program_bytes, 8) || (uint64_t)(end - p) < v->program_bytes)
+    return make_error(MKRT_INVALID_ARGUMENT, "DeserializeAndLoad: truncated program");
+  v->program = p;
+  p += v->program_bytes;
+  if (!take(&nobj, 4)) return make_error(MKRT_INVALID_ARGUMENT, "DeserializeAndLoad: truncated code-object table");
+  for (uint32_t i = 0; i < nobj; ++i) {
+    uint64_t sl = 0, cl = 0;
+    if (!take(&sl, 8) || (uint64_t)(end - p) < sl)
+      return make_error(MKRT_INVALID_ARGUMENT, "DeserializeAndLoad: truncated code object %u", i);
+    const char* src = p;
+    p += sl;
+    if (!take(&cl, 8) || (uint64_t)(end - p) < cl || cl == 0)
+      return make_error(MKRT_INVALID_ARGUMENT, "DeserializeAndLoad: truncated code object %u", i);
+    const char* code = p;
+    p += cl;
+    if (copy_objects) v->objs.emplace_back(std::string(src, sl), std::vector<char>(code, code + cl));
+    else v->objs.emplace_back(std::string(), std::vector<char>());
+  }
+  if (p != end) return make_error(MKRT_INVALID_ARGUMENT, "DeserializeAndLoad: %lld trailing bytes",
+                                  (long long)(end - p));
+  return nullptr;
+}
+
 }  // namespace
+
+struct mkrt_serialized {
+  std::string bytes;
+};
 
 extern "C" {
 
@@ -551,6 +654,8 @@ mkrt_error* mkrt_compile(mkrt_client* c, const char* code, int64_t code_bytes, c
     delete x;
     return err;
   }
+  x->program.assign(code, code_bytes >= 0 ? (size_t)code_bytes : strlen(code));
+  x->fingerprint = fingerprint_of(x->program);
   x->plan_text = x->plan.describe();
   *out = x;
   return nullptr;
@@ -648,6 +753,71 @@ mkrt_error* mkrt_execute(mkrt_executable* x, mkrt_buffer* const* inputs, int num
   }
   if (done) *done = new mkrt_event{st};
   return nullptr;
+}
+
+mkrt_error* mkrt_executable_serialize(const mkrt_executable* x, mkrt_serialized** out) {
+  if (!x || !out) return make_error(MKRT_INVALID_ARGUMENT, "Serialize: null executable");
+  *out = nullptr;
+  mkrt_serialized* s = new mkrt_serialized;
+  if (mkrt_error* e = serialize_plan(x->program, x->plan, &s->bytes)) {
+    delete s;
+    return e;
+  }
+  *out = s;
+  return nullptr;
+}
+
+mkrt_error* mkrt_serialize_program(const char* code, int64_t code_bytes, const char* format, mkrt_serialized** out) {
+  if (!code || !out) return make_error(MKRT_INVALID_ARGUMENT, "mkrt_serialize_program: null argument");
+  *out = nullptr;
+  mkrt::Function fn;
+  mkrt::Plan plan;
+  if (mkrt_error* e = compile_text(code, code_bytes, format, &fn, &plan)) return e;
+  mkrt_serialized* s = new mkrt_serialized;
+  const std::string program(code, code_bytes >= 0 ? (size_t)code_bytes : strlen(code));
+  if (mkrt_error* e = serialize_plan(program, plan, &s->bytes)) {
+    delete s;
+    return e;
+  }
+  *out = s;
+  return nullptr;
+}
+
+const void* mkrt_serialized_data(const mkrt_serialized* s) { return s ? s->bytes.data() : nullptr; }
+int64_t mkrt_serialized_size(const mkrt_serialized* s) { return s ? (int64_t)s->bytes.size() : 0; }
+void mkrt_serialized_destroy(mkrt_serialized* s) { delete s; }
+
+mkrt_error* mkrt_serialized_inspect(const void* bytes, int64_t size, int64_t* program_bytes, int* num_code_objects) {
+  SerialView v;
+  if (mkrt_error* e = parse_serialized(bytes, size, &v, false)) return e;
+  if (program_bytes) *program_bytes = (int64_t)v.program_bytes;
+  if (num_code_objects) *num_code_objects = (int)v.objs.size();
+  return nullptr;
+}
+
+mkrt_error* mkrt_deserialize(mkrt_client* c, const void* bytes, int64_t size, mkrt_executable** out) {
+  if (!c || !out) return make_error(MKRT_INVALID_ARGUMENT, "DeserializeAndLoad: null argument");
+  *out = nullptr;
+  SerialView v;
+  if (mkrt_error* e = parse_serialized(bytes, size, &v, true)) return e;
+  for (const auto& o : v.objs) mkc::ew_jit_seed(o.first, o.second);
+  mkrt_error* e = mkrt_compile(c, v.program, (int64_t)v.program_bytes, "mlir", out);
+  if (e) {
+    mkrt_error* w = make_error(e->code, "DeserializeAndLoad: %s", e->message.c_str());
+    mkrt_error_destroy(e);
+    return w;
+  }
+  return nullptr;
+}
+
+const char* mkrt_executable_fingerprint(const mkrt_executable* x) { return x ? x->fingerprint.c_str() : ""; }
+
+void mkrt_jit_cache_stats(int64_t* compiles, int64_t* disk_hits, int64_t* memory_hits) {
+  int64_t c = 0, d = 0, m = 0;
+  mkc::ew_jit_stats(&c, &d, &m);
+  if (compiles) *compiles = c;
+  if (disk_hits) *disk_hits = d;
+  if (memory_hits) *memory_hits = m;
 }
 
 void mkrt_executable_destroy(mkrt_executable* x) {

@@ -86,6 +86,15 @@ RUNTIME_SIGNATURES = {
     "mkrt_executable_plan": (ctypes.c_char_p, [_p]),
     "mkrt_execute": (_p, [_p, _pp, _i32, _pp, _pp]),
     "mkrt_executable_destroy": (None, [_p]),
+    "mkrt_executable_serialize": (_p, [_p, _pp]),
+    "mkrt_serialize_program": (_p, [ctypes.c_char_p, _i64, ctypes.c_char_p, _pp]),
+    "mkrt_serialized_data": (_p, [_p]),
+    "mkrt_serialized_size": (_i64, [_p]),
+    "mkrt_serialized_destroy": (None, [_p]),
+    "mkrt_deserialize": (_p, [_p, ctypes.c_char_p, _i64, _pp]),
+    "mkrt_serialized_inspect": (_p, [ctypes.c_char_p, _i64, ctypes.POINTER(_i64), ctypes.POINTER(_i32)]),
+    "mkrt_executable_fingerprint": (ctypes.c_char_p, [_p]),
+    "mkrt_jit_cache_stats": (None, [ctypes.POINTER(_i64), ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
     "mkrt_event_create": (_p, [_pp]),
     "mkrt_event_set": (_p, [_p, _i32, ctypes.c_char_p]),
     "mkrt_event_is_ready": (_i32, [_p]),

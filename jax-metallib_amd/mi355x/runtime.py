@@ -61,6 +61,40 @@ def compile_check(text):
     return buf.value.decode(), n.value
 
 
+def _take_serialized(handle):
+    """bytes of an owned mkrt_serialized (freeing it)."""
+    L = _lib.lib()
+    try:
+        n = L.mkrt_serialized_size(handle)
+        return ctypes.string_at(L.mkrt_serialized_data(handle), n)
+    finally:
+        L.mkrt_serialized_destroy(handle)
+
+
+def serialize_program(text):
+    """Serialized executable of StableHLO text, without a device: the program
+    plus the compiled code objects of its fused elementwise programs."""
+    data = text.encode() if isinstance(text, str) else bytes(text)
+    h = _p()
+    _raise(_lib.lib().mkrt_serialize_program(data, len(data), b"mlir", ctypes.byref(h)))
+    return _take_serialized(h.value)
+
+
+def inspect_serialized(blob):
+    """(program bytes, code objects) of a serialized executable; raises
+    PluginError(INVALID_ARGUMENT) for malformed data."""
+    n, k = ctypes.c_int64(0), ctypes.c_int(0)
+    _raise(_lib.lib().mkrt_serialized_inspect(bytes(blob), len(blob), ctypes.byref(n), ctypes.byref(k)))
+    return n.value, k.value
+
+
+def jit_cache_stats():
+    """Process totals of the elementwise JIT: (compiles, disk hits, memory hits)."""
+    c, d, m = ctypes.c_int64(0), ctypes.c_int64(0), ctypes.c_int64(0)
+    _lib.lib().mkrt_jit_cache_stats(ctypes.byref(c), ctypes.byref(d), ctypes.byref(m))
+    return c.value, d.value, m.value
+
+
 class Event:
     """A completion event (PJRT_Event)."""
 
@@ -182,6 +216,17 @@ class Executable:
     def plan(self):
         return _lib.lib().mkrt_executable_plan(self._h).decode()
 
+    @property
+    def fingerprint(self):
+        """16 hex digits identifying the program (PJRT_Executable_Fingerprint)."""
+        return _lib.lib().mkrt_executable_fingerprint(self._h).decode()
+
+    def serialize(self):
+        """Serialized form (PJRT_Executable_Serialize): bytes for Client.deserialize."""
+        h = _p()
+        _raise(_lib.lib().mkrt_executable_serialize(self._h, ctypes.byref(h)))
+        return _take_serialized(h.value)
+
     def execute(self, inputs):
         """Run on borrowed input Buffers -> (list of new Buffers, completion Event)."""
         n_in = len(inputs)
@@ -243,6 +288,13 @@ class Client:
         data = text.encode() if isinstance(text, str) else bytes(text)
         h = _p()
         _raise(_lib.lib().mkrt_compile(self._h, data, len(data), b"mlir", ctypes.byref(h)))
+        return Executable(h.value, self)
+
+    def deserialize(self, blob):
+        """Executable from Executable.serialize bytes (PJRT_Executable_DeserializeAndLoad)."""
+        data = bytes(blob)
+        h = _p()
+        _raise(_lib.lib().mkrt_deserialize(self._h, data, len(data), ctypes.byref(h)))
         return Executable(h.value, self)
 
     def close(self):
