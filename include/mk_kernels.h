@@ -69,6 +69,13 @@ enum { MK_QFMT_INT4_G64 = 0, MK_QFMT_INT8_PC = 1 };
 
 int64_t mk_qmatmul_workspace_bytes(int fmt, int64_t M, int64_t K, int64_t N);
 
+/* 1 when a *_matmul_epilogue_bf16 call of this shape with this epilogue
+ * runs, 0 when it would return an error: MK_EPI_SWIGLU_PAIRS takes the
+ * dequantise-then-GEMM route only (many rows, M % 256 == 0, N % 256 == 0).
+ * Host-only; no reference counterpart (callers use it to choose between
+ * the paired and the two-product form). */
+int mk_qmatmul_epilogue_supported(int fmt, int64_t M, int64_t K, int64_t N, int epilogue);
+
 int mk_int4g64_matmul_bf16(const void* x, const void* w_packed, const void* scale,
                            const void* zero, void* y, int64_t M, int64_t K, int64_t N,
                            void* workspace, int64_t workspace_bytes, void* stream);
@@ -121,7 +128,16 @@ int mk_gemm_f32(const void* a, const void* b, void* c, int64_t batch, int64_t M,
  * followed by the bf16 elementwise program (MK_EW_ADD, or MK_EW_LOGISTIC +
  * MK_EW_MUL + MK_EW_MUL) -- the reference runs these as separate MPSGraph
  * ops (ops/binary_ops.mm).  aux may equal c (in-place residual). */
-enum { MK_EPI_NONE = 0, MK_EPI_ADD = 1, MK_EPI_SWIGLU = 2 };
+enum { MK_EPI_NONE = 0, MK_EPI_ADD = 1, MK_EPI_SWIGLU = 2, MK_EPI_SWIGLU_PAIRS = 3 };
+/* MK_EPI_SWIGLU_PAIRS: the gate and up projections as one product.  B's N
+ * columns interleave 16-column blocks of the gate and up weights (gate
+ * block q at columns 32q..32q+15, up block q at 32q+16..32q+31); C is
+ * bf16 [batch, M, N/2] with
+ *   C[m, 16q + c] = r(r(g * r(logistic(g))) * r(u)),
+ *   g = r(acc[m, 32q + c]),  u = r(acc[m, 32q + 16 + c]),
+ * bit-identical to two plain GEMMs and the MK_EPI_SWIGLU formula.  aux is
+ * unused (may be null).  Needs the 256x256 kernel's shapes: M % 256 == 0,
+ * N % 256 == 0, K % 32 == 0 (else MK_EUNSUPPORTED). */
 
 int mk_gemm_bf16_epilogue(const void* a, const void* b, void* c, const void* aux, int epilogue,
                           int64_t batch, int64_t M, int64_t N, int64_t K, void* stream);

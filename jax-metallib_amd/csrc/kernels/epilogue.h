@@ -5,6 +5,8 @@
 //   MK_EPI_ADD:    y = r(r(acc) + aux)                        (residual add)
 //   MK_EPI_SWIGLU: u = r(acc), g = aux,
 //                  y = r(r(g * r(logistic(g))) * u)           (silu(g) * u)
+//   MK_EPI_SWIGLU_PAIRS: the same with g = r(acc) of the interleaved gate
+//                  column and u = r(acc) of its up column (one GEMM).
 // with the bf16 programs' own logistic (ew_math.h, mk_logistic_bf).
 #pragma once
 
@@ -35,6 +37,20 @@ __device__ __forceinline__ void epi_store_bf16x4_v(uint16_t* y, const u32x2& w, 
         v[e] = epi_r(x[e] * sig) * u;
       }
     }
+  }
+  *reinterpret_cast<u32x2*>(y + off) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+}
+
+// MK_EPI_SWIGLU_PAIRS: four bf16 outputs from the gate accumulators g and
+// the up accumulators u of the same four positions, rounded as the two
+// plain GEMMs would have stored them and then combined as MK_EPI_SWIGLU.
+__device__ __forceinline__ void epi_store_swiglu_pair(uint16_t* y, size_t off, const f32x4& g, const f32x4& u) {
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float x = epi_r(g[e]);
+    const float sig = epi_r(mk_logistic_bf(x));
+    v[e] = epi_r(x * sig) * epi_r(u[e]);
   }
   *reinterpret_cast<u32x2*>(y + off) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
 }

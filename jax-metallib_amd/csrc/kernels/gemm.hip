@@ -608,7 +608,7 @@ __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs
   const int ncol = n0 + wn * (16 * TN) + 4 * (lane >> 4);
   constexpr bool kPreAux = WN_ == 4 && !PIPE;
   u32x2 auxv[kPreAux ? TM : 1][kPreAux ? TN : 1];
-  if (kPreAux && p.epi != MK_EPI_NONE) {
+  if (kPreAux && (p.epi == MK_EPI_ADD || p.epi == MK_EPI_SWIGLU)) {
     const uint16_t* X = p.aux + (size_t)blockIdx.z * p.sc;
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -750,7 +750,16 @@ __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs
   }
 
   // Epilogue (C^T tiles): lane owns row m, columns n..n+3 of each tile.
-  if (p.out_f32) {
+  if (p.epi == MK_EPI_SWIGLU_PAIRS) {
+    // Blocks j (gate) and j+1 (up), j even, hold the same output columns.
+    uint16_t* C = static_cast<uint16_t*>(p.c) + (size_t)blockIdx.z * p.sc;
+    const int N2 = N / 2, ncol2 = ncol / 2 + 2 * (lane >> 4);  // = n0/2 + wn*8*TN + 4*(lane>>4)
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int q = 0; q < TN / 2; ++q)
+        epi_store_swiglu_pair(C, (size_t)(mrow + 16 * i) * N2 + ncol2 + 16 * q, acc[i][2 * q], acc[i][2 * q + 1]);
+  } else if (p.out_f32) {
     float* C = static_cast<float*>(p.c) + (size_t)blockIdx.z * p.sc;
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -840,14 +849,19 @@ int run_gemm_bf16(const char* fn, const void* a, const void* b, void* c, const v
   mkc::clear_error();
   int rc = check_gemm(fn, a, b, c, batch, M, N, K);
   if (rc != MK_OK) return rc;
-  if (epi != MK_EPI_NONE && epi != MK_EPI_ADD && epi != MK_EPI_SWIGLU)
+  if (epi != MK_EPI_NONE && epi != MK_EPI_ADD && epi != MK_EPI_SWIGLU && epi != MK_EPI_SWIGLU_PAIRS)
     return mkc::fail(MK_EINVAL, "%s: unknown epilogue %d", fn, epi);
-  if (epi != MK_EPI_NONE && (out_f32 || !aux))
+  if (epi != MK_EPI_NONE && (out_f32 || (!aux && epi != MK_EPI_SWIGLU_PAIRS)))
     return mkc::fail(MK_EINVAL, "%s: an epilogue needs a bf16 output and an aux operand", fn);
+  const char* dma_env = getenv("MK_GEMM_DMA");
+  const bool dma = !(dma_env && dma_env[0] == '0');
+  if (epi == MK_EPI_SWIGLU_PAIRS && !(dma && M % 256 == 0 && N % 256 == 0 && K % 32 == 0))
+    return mkc::fail(MK_EUNSUPPORTED, "%s: paired SwiGLU needs M %% 256 == 0, N %% 256 == 0, K %% 32 == 0 "
+                     "(got M=%lld, N=%lld, K=%lld)", fn, (long long)M, (long long)N, (long long)K);
   mk::GemmArgs p;
   p.a = a; p.b = b; p.c = c;
   p.M = (int)M; p.N = (int)N; p.K = (int)K;
-  p.sa = M * K; p.sb = K * N; p.sc = M * N;
+  p.sa = M * K; p.sb = K * N; p.sc = epi == MK_EPI_SWIGLU_PAIRS ? M * (N / 2) : M * N;
   p.out_f32 = out_f32 ? 1 : 0;
   p.epi = epi;
   p.aux = static_cast<const uint16_t*>(aux);
@@ -855,22 +869,21 @@ int run_gemm_bf16(const char* fn, const void* a, const void* b, void* c, const v
   const int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256) * batch;
   int tile = env_tile();
   if (tile == 0) tile = big_tiles >= 128 ? 256 : 128;
+  if (epi == MK_EPI_SWIGLU_PAIRS) tile = 256;
   hipError_t e;
-  const char* dma_env = getenv("MK_GEMM_DMA");
-  const bool dma = !(dma_env && dma_env[0] == '0');
   if (tile == 256 && dma && M % 256 == 0 && N % 256 == 0 && K % 32 == 0) {
     constexpr size_t lds = (size_t)mk::kGemmStages * mk::kGemmStageBytes;
     const dim3 grid((unsigned)((M / 256) * (N / 256)), 1, (unsigned)batch);
     const char* w = getenv("MK_GEMM_WAVES");
     const char* pv = getenv("MK_GEMM_PIPE");
     // The pipelined kernel (fragment prefetch + 5-stage ring) for long K
-    // loops without an epilogue.  It has no registers left to preload an
-    // epilogue operand, so epilogue calls keep the kernel that does.  At
+    // loops without an epilogue operand.  It has no registers left to
+    // preload one, so ADD / SWIGLU calls keep the kernel that does.  At
     // K = 2048 it is 3-5 % faster alone but ran the decoder's sequence of
     // K = 2048 projections 1 % slower end to end (5.51 vs 5.45 ms): the
     // clock under it (GRBM_GUI_ACTIVE per ns) is ~2.1 GHz against ~2.35 GHz,
     // which slows the kernels around it.  From K = 4096 it gains 7-9 %.
-    const bool pipe = !(pv && atoi(pv) == 0) && p.epi == MK_EPI_NONE && K >= 4096;
+    const bool pipe = !(pv && atoi(pv) == 0) && (p.epi == MK_EPI_NONE || p.epi == MK_EPI_SWIGLU_PAIRS) && K >= 4096;
     if (w && atoi(w) == 4) {
       e = lds_opt_in((const void*)mk::gemm_bf16_256dma_kernel<2, false>, lds);
       if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256dma_kernel<2, false>), grid, dim3(256), lds, st, p);

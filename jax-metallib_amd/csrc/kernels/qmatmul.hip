@@ -1188,9 +1188,10 @@ int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, v
           int64_t K, int64_t N, void* ws, int64_t ws_bytes, void* stream, const void* aux = nullptr,
           int epi = MK_EPI_NONE) {
   const char* fn = fmt == MK_QFMT_INT4_G64 ? "mk_int4g64_matmul_bf16" : "mk_int8pc_matmul_bf16";
-  if (epi != MK_EPI_NONE && epi != MK_EPI_ADD && epi != MK_EPI_SWIGLU)
+  if (epi != MK_EPI_NONE && epi != MK_EPI_ADD && epi != MK_EPI_SWIGLU && epi != MK_EPI_SWIGLU_PAIRS)
     return mkc::fail(MK_EINVAL, "%s: unknown epilogue %d", fn, epi);
-  if (epi != MK_EPI_NONE && !aux) return mkc::fail(MK_EINVAL, "%s: the epilogue needs aux", fn);
+  if (epi != MK_EPI_NONE && epi != MK_EPI_SWIGLU_PAIRS && !aux)
+    return mkc::fail(MK_EINVAL, "%s: the epilogue needs aux", fn);
   if (!x || !w || !s || !y || (fmt == MK_QFMT_INT4_G64 && !z))
     return mkc::fail(MK_EINVAL, "%s: null pointer argument", fn);
   if (M <= 0 || K <= 0 || N <= 0)
@@ -1204,6 +1205,11 @@ int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, v
   QPlan p;
   if (!plan_q(fmt, M, K, N, &p))
     return mkc::fail(MK_EUNSUPPORTED, "%s: no launch configuration for K=%lld", fn, (long long)K);
+  // The paired SwiGLU (interleaved gate / up columns, y [M, N/2]) is an
+  // epilogue of the bf16 GEMM only: it needs the dequantise-then-GEMM route.
+  if (epi == MK_EPI_SWIGLU_PAIRS && !p.deq)
+    return mkc::fail(MK_EUNSUPPORTED, "%s: paired SwiGLU needs the dequantise-then-GEMM route (M >= %d)", fn,
+                     kDeqMinRows);
   if (p.part_bytes > 0 && (!ws || ws_bytes < p.part_bytes))
     return mkc::fail(MK_EWORKSPACE, "%s: workspace of %lld bytes needed, %lld given", fn,
                      (long long)p.part_bytes, (long long)ws_bytes);
@@ -1280,6 +1286,14 @@ extern "C" int64_t mk_qmatmul_workspace_bytes(int fmt, int64_t M, int64_t K, int
   QPlan p;
   if (!plan_q(fmt, M, K, N, &p)) return -1;
   return p.part_bytes;
+}
+
+extern "C" int mk_qmatmul_epilogue_supported(int fmt, int64_t M, int64_t K, int64_t N, int epilogue) {
+  if (mk_qmatmul_workspace_bytes(fmt, M, K, N) < 0) return 0;
+  if (epilogue == MK_EPI_NONE || epilogue == MK_EPI_ADD || epilogue == MK_EPI_SWIGLU) return 1;
+  if (epilogue != MK_EPI_SWIGLU_PAIRS) return 0;
+  QPlan p;
+  return plan_q(fmt, M, K, N, &p) && p.deq && M % 256 == 0 && N % 256 == 0 ? 1 : 0;
 }
 
 extern "C" int mk_int4g64_matmul_bf16(const void* x, const void* w_packed, const void* scale,

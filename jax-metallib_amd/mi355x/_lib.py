@@ -15,7 +15,7 @@ KERNELS_SO = os.path.join(LIB_DIR, "libmk_kernels.so")
 MK_OK, MK_EINVAL, MK_EUNSUPPORTED, MK_EWORKSPACE, MK_ELAUNCH = 0, 1, 2, 3, 4
 MK_QFMT_INT4_G64, MK_QFMT_INT8_PC = 0, 1
 MK_DT_F32, MK_DT_BF16 = 0, 1
-MK_EPI_NONE, MK_EPI_ADD, MK_EPI_SWIGLU = 0, 1, 2
+MK_EPI_NONE, MK_EPI_ADD, MK_EPI_SWIGLU, MK_EPI_SWIGLU_PAIRS = 0, 1, 2, 3
 MK_REDUCE_SUM, MK_REDUCE_MAX = 0, 1
 EW_OPS = ["LOAD", "CONST", "ADD", "SUB", "MUL", "DIV", "MAX", "MIN", "POW", "NEG", "ABS", "EXP", "LOG",
           "LOG1P", "EXPM1", "TANH", "RSQRT", "SQRT", "LOGISTIC", "FLOOR", "CEIL", "CMP_EQ", "CMP_NE",
@@ -37,6 +37,7 @@ SIGNATURES = {
     "mk_last_error": (ctypes.c_char_p, []),
     "mk_version": (ctypes.c_char_p, []),
     "mk_qmatmul_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64]),
+    "mk_qmatmul_epilogue_supported": (_i32, [_i32, _i64, _i64, _i64, _i32]),
     "mk_int4g64_matmul_bf16": (_i32, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p]),
     "mk_int8pc_matmul_bf16": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p]),
     "mk_gemm_bf16": (_i32, [_p, _p, _p, _i64, _i64, _i64, _i64, _i32, _p]),

@@ -21,12 +21,16 @@ in one HIP graph:
     a    = causal_attention(q, k, v), heads merged mk_attention_causal_bf16
     x    = x + a @ Wo     (add in the GEMM store)  mk_int4g64_matmul_epilogue_bf16
     h    = rmsnorm(x, g_mlp)
-    g    = h @ Wg                                  mk_int4g64_matmul_bf16
-    act  = silu(g) * (h @ Wu)  (in the GEMM store) mk_int4g64_matmul_epilogue_bf16
+    act  = silu(h @ Wg) * (h @ Wu)                 mk_int4g64_matmul_epilogue_bf16,
+           one product against [Wg | Wu] with        MK_EPI_SWIGLU_PAIRS (with
+           16-column blocks interleaved              fewer tokens than the
+                                                     many-row route takes: g,
+                                                     then MK_EPI_SWIGLU)
     x    = x + act @ Wd   (add in the GEMM store)  mk_int4g64_matmul_epilogue_bf16
 
-fuse_epilogues=False runs the residual adds and silu(g) * u as separate
-elementwise programs (mk_elementwise); the results are bit-identical.
+fuse_epilogues=False runs the gate and up projections as two products and
+the residual adds and silu(g) * u as separate elementwise programs
+(mk_elementwise); the results are bit-identical.
 
 attention="composed" runs the attention as the reference's layer writes it,
 one op at a time: s = q @ k^T (mk_gemm_bf16 on kT), p = causal softmax of
@@ -105,6 +109,14 @@ class LayerWeights:
     w_gate: Int4Weight
     w_up: Int4Weight
     w_down: Int4Weight
+    w_gateup: Int4Weight = None  # w_gate and w_up, 16-column blocks interleaved
+
+
+def interleave_int4(a: Int4Weight, b: Int4Weight) -> Int4Weight:
+    """[Wa | Wb] with 16-column blocks alternating (int4 g64 packs along K,
+    so every array of the weight is interleaved by column alike)."""
+    return Int4Weight(ops.interleave_gate_up(a.packed, b.packed), ops.interleave_gate_up(a.scale, b.scale),
+                      ops.interleave_gate_up(a.zero, b.zero))
 
 
 def init_weights(cfg: DecoderConfig, seed=0, device="cuda"):
@@ -121,6 +133,7 @@ def init_weights(cfg: DecoderConfig, seed=0, device="cuda"):
             w_gate=random_int4(rng, cfg.hidden, cfg.ffn, device),
             w_up=random_int4(rng, cfg.hidden, cfg.ffn, device),
             w_down=random_int4(rng, cfg.ffn, cfg.hidden, device)))
+        layers[-1].w_gateup = interleave_int4(layers[-1].w_gate, layers[-1].w_up)
     return layers
 
 
@@ -187,12 +200,16 @@ def layer_forward(cfg: DecoderConfig, lw: LayerWeights, buf: Buffers, cos, sin):
     else:
         ops.attention_causal(buf.q, buf.k, buf.v, B, H, 1.0 / math.sqrt(D), out=buf.attn)
     if buf.fuse:
-        # Residual adds and silu(g) * u ride on the projections' stores
-        # (bit-identical to the separate elementwise programs below).
+        # Residual adds and silu(g) * u ride on the projections' stores, and
+        # the gate and up projections are one product (bit-identical to the
+        # separate products and elementwise programs below).
         _qmm(buf.attn, lw.w_o, buf.x, epilogue="add", aux=buf.x)
         ops.rmsnorm(buf.x, lw.g_mlp, eps=cfg.eps, out=buf.h)
-        _qmm(buf.h, lw.w_gate, buf.gate)
-        _qmm(buf.h, lw.w_up, buf.act, epilogue="swiglu", aux=buf.gate)
+        if ops.int4_swiglu_pairs_supported(cfg.tokens, cfg.hidden, 2 * cfg.ffn):
+            _qmm(buf.h, lw.w_gateup, buf.act, epilogue="swiglu_pairs")
+        else:  # too few tokens for the many-row route: two products
+            _qmm(buf.h, lw.w_gate, buf.gate)
+            _qmm(buf.h, lw.w_up, buf.act, epilogue="swiglu", aux=buf.gate)
         _qmm(buf.act, lw.w_down, buf.x, epilogue="add", aux=buf.x)
         return
     _qmm(buf.attn, lw.w_o, buf.proj)

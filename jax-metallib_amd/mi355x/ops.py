@@ -45,22 +45,56 @@ def workspace(nbytes, device):
     return ws
 
 
-_EPI = {None: _lib.MK_EPI_NONE, "add": _lib.MK_EPI_ADD, "swiglu": _lib.MK_EPI_SWIGLU}
+_EPI = {None: _lib.MK_EPI_NONE, "add": _lib.MK_EPI_ADD, "swiglu": _lib.MK_EPI_SWIGLU,
+        "swiglu_pairs": _lib.MK_EPI_SWIGLU_PAIRS}
 
 
 def _epilogue(epilogue, aux, shape, name):
     code = _EPI[epilogue]
-    if code != _lib.MK_EPI_NONE:
+    if code == _lib.MK_EPI_SWIGLU_PAIRS:
+        if aux is not None:
+            raise ValueError(f"{name}: the paired SwiGLU takes no aux")
+    elif code != _lib.MK_EPI_NONE:
         _require(aux, _BF16, "aux")
         if tuple(aux.shape) != tuple(shape):
             raise ValueError(f"{name}: aux must have the output's shape {tuple(shape)}")
     return code
 
 
+def _out_cols(N, epilogue, name):
+    """Output columns: N, or N/2 for the paired SwiGLU (gate and up 16-column
+    blocks interleaved in the N weight columns)."""
+    if epilogue != "swiglu_pairs":
+        return N
+    if N % 32:
+        raise ValueError(f"{name}: the paired SwiGLU needs N % 32 == 0")
+    return N // 2
+
+
+def int4_swiglu_pairs_supported(M, K, N):
+    """Whether int4_g64_matmul(..., epilogue="swiglu_pairs") runs at this
+    shape (N = the interleaved width): only the many-row route has it."""
+    return bool(lib().mk_qmatmul_epilogue_supported(_lib.MK_QFMT_INT4_G64, M, K, N, _lib.MK_EPI_SWIGLU_PAIRS))
+
+
+def interleave_gate_up(gate, up, block=16):
+    """[..., F] gate and up weights (any per-column layout: packed int4,
+    scales, zero points, bf16) -> [..., 2F] with 16-column blocks alternating
+    gate, up: the B operand of the "swiglu_pairs" epilogue."""
+    if gate.shape != up.shape or gate.shape[-1] % block:
+        raise ValueError("interleave_gate_up: gate and up need the same shape, last dim % 16 == 0")
+    lead, F = gate.shape[:-1], gate.shape[-1]
+    g = gate.reshape(*lead, F // block, 1, block)
+    u = up.reshape(*lead, F // block, 1, block)
+    return torch.cat([g, u], dim=-2).reshape(*lead, 2 * F).contiguous()
+
+
 def int4_g64_matmul(x, w_packed, scale, zero, out=None, epilogue=None, aux=None):
     """y = x @ ((w - zero) * scale): x bf16 [M,K], w uint8 [K/2,N], scale bf16
     [K/64,N], zero uint8 [K/64,N] -> bf16 [M,N].  epilogue "add" gives
-    y = r(r(xW) + aux), "swiglu" y = r(r(aux * r(logistic(aux))) * r(xW))."""
+    y = r(r(xW) + aux), "swiglu" y = r(r(aux * r(logistic(aux))) * r(xW)),
+    "swiglu_pairs" (W from interleave_gate_up, no aux) y [M, N/2] =
+    silu(gate) * up as "swiglu" computes it."""
     _require(x, _BF16, "x")
     _require(w_packed, (torch.uint8,), "w_packed")
     _require(scale, _BF16, "scale")
@@ -69,7 +103,8 @@ def int4_g64_matmul(x, w_packed, scale, zero, out=None, epilogue=None, aux=None)
     N = w_packed.shape[1]
     if w_packed.shape[0] * 2 != K or scale.shape != (K // 64, N) or zero.shape != (K // 64, N):
         raise ValueError("int4_g64_matmul: inconsistent shapes")
-    y = out if out is not None else torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    NO = _out_cols(N, epilogue, "int4_g64_matmul")
+    y = out if out is not None else torch.empty((M, NO), dtype=torch.bfloat16, device=x.device)
     epi = _epilogue(epilogue, aux, (M, N), "int4_g64_matmul")
     nb = lib().mk_qmatmul_workspace_bytes(_lib.MK_QFMT_INT4_G64, M, K, N)
     ws = workspace(nb, x.device) if nb > 0 else None
@@ -112,14 +147,17 @@ def _bmk(a, b):
 
 def gemm_bf16(a, b, out_f32=False, out=None, epilogue=None, aux=None):
     """[batch,] M x K @ K x N in bf16 with f32 accumulation -> bf16 (or f32).
-    epilogue "add" / "swiglu" with aux (bf16, the output's shape) as in
-    int4_g64_matmul (bf16 output only)."""
+    epilogue "add" / "swiglu" with aux (bf16, the output's shape) or
+    "swiglu_pairs" (output N/2 columns) as in int4_g64_matmul (bf16 output
+    only)."""
     _require(a, _BF16, "a")
     _require(b, _BF16, "b")
     batch, M, N, K = _bmk(a, b)
     shape = (M, N) if a.dim() == 2 else (batch, M, N)
+    NO = _out_cols(N, epilogue, "gemm_bf16")
+    oshape = shape[:-1] + (NO,)
     c = out if out is not None else torch.empty(
-        shape, dtype=torch.float32 if out_f32 else torch.bfloat16, device=a.device)
+        oshape, dtype=torch.float32 if out_f32 else torch.bfloat16, device=a.device)
     epi = _epilogue(epilogue, aux, shape, "gemm_bf16")
     if epi == _lib.MK_EPI_NONE:
         check(lib().mk_gemm_bf16(_ptr(a), _ptr(b), _ptr(c), batch, M, N, K, 1 if out_f32 else 0,

@@ -215,12 +215,16 @@ def test_decoder_forward_matches_reference(attention):
     assert_rel_close(y.numpy(), ref.numpy(), BF16_RTOL, "decoder forward")
 
 
-def test_decoder_fused_epilogues_bit_identical():
+@pytest.mark.parametrize("seq", [128, 512])
+def test_decoder_fused_epilogues_bit_identical(seq):
     """Residual adds and SwiGLU fused into the projections' stores give the
-    same bits as the separate elementwise programs."""
+    same bits as the separate products and elementwise programs.  At 1024
+    tokens the gate and up projections are one paired product; at 256 the
+    fused form falls back to two."""
     need_gpu()
-    from mi355x import decoder
-    cfg = decoder.DecoderConfig(layers=2, hidden=256, heads=2, head_dim=128, ffn=512, batch=2, seq=128)
+    from mi355x import decoder, ops
+    cfg = decoder.DecoderConfig(layers=2, hidden=256, heads=2, head_dim=128, ffn=512, batch=2, seq=seq)
+    assert ops.int4_swiglu_pairs_supported(cfg.tokens, cfg.hidden, 2 * cfg.ffn) == (seq == 512)
     weights = decoder.init_weights(cfg, seed=6)
     cos, sin = decoder.rope_tables(cfg)
     x0 = torch.randn((cfg.tokens, cfg.hidden)).to(torch.bfloat16).cuda()

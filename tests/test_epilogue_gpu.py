@@ -102,3 +102,64 @@ def test_epilogue_rejects_bad_arguments():
                                    st) == _lib.MK_EINVAL
     with pytest.raises(ValueError):
         ops.gemm_bf16(a, b, epilogue="add", aux=torch.zeros((8, 8), dtype=torch.bfloat16, device="cuda"))
+
+
+# (512, 256, 256): the ring kernel; (256, 4096, 256): the pipelined kernel
+# (K >= 4096); (256, 64, 512): two 32-k stages per tile.
+@pytest.mark.parametrize("M,K,F", [(512, 256, 256), (256, 4096, 256), (256, 64, 512)])
+def test_gemm_swiglu_pairs_matches_two_products(M, K, F):
+    """One product against [Wg | Wu] (16-column blocks interleaved) equals,
+    bit for bit, g = x @ Wg and silu(g) * (x @ Wu) as the "swiglu" epilogue
+    (itself bit-identical to the elementwise program) computes it."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(M + K + F)
+    x = (torch.randn((M, K), generator=g) / 4).to(torch.bfloat16).cuda()
+    wg = (torch.randn((K, F), generator=g) / 8).to(torch.bfloat16).cuda()
+    wu = (torch.randn((K, F), generator=g) / 8).to(torch.bfloat16).cuda()
+    print(f"[epilogue] gemm swiglu_pairs M={M} K={K} F={F}", flush=True)
+    gate = ops.gemm_bf16(x, wg)
+    ref = ops.gemm_bf16(x, wu, epilogue="swiglu", aux=gate)
+    ref2 = _unfused(ops, ops.gemm_bf16(x, wu), gate, "swiglu")
+    y = ops.gemm_bf16(x, ops.interleave_gate_up(wg, wu), epilogue="swiglu_pairs")
+    torch.cuda.synchronize()
+    assert y.shape == (M, F)
+    assert torch.equal(ref, ref2)
+    assert torch.equal(y, ref)
+
+
+def test_int4_swiglu_pairs_matches_two_products():
+    """The decoder's form: int4 g64 gate and up weights interleaved by
+    column (scales and zero points alike), dequantise-then-GEMM route."""
+    ops = _ops()
+    M, K, F = 1024, 512, 256
+    rng = np.random.default_rng(11)
+    x, pg, sg, zg = quant.make_int4_case(rng, M, K, F)
+    _, pu, su, zu = quant.make_int4_case(rng, M, K, F)
+    xd = dev_bf16(x)
+    wg = (dev(pg), dev_bf16(sg), dev(zg))
+    wu = (dev(pu), dev_bf16(su), dev(zu))
+    print(f"[epilogue] int4 swiglu_pairs M={M} K={K} F={F}", flush=True)
+    gate = ops.int4_g64_matmul(xd, *wg)
+    ref = ops.int4_g64_matmul(xd, *wu, epilogue="swiglu", aux=gate)
+    wgu = [ops.interleave_gate_up(a, b) for a, b in zip(wg, wu)]
+    y = ops.int4_g64_matmul(xd, *wgu, epilogue="swiglu_pairs")
+    torch.cuda.synchronize()
+    assert y.shape == (M, F)
+    assert torch.equal(y, ref)
+
+
+def test_swiglu_pairs_rejects_unsupported_shapes():
+    ops = _ops()
+    from mi355x import _lib
+    L = _lib.lib()
+    st = torch.cuda.current_stream().cuda_stream
+    a = torch.zeros((200, 64), dtype=torch.bfloat16, device="cuda")
+    b = torch.zeros((64, 256), dtype=torch.bfloat16, device="cuda")
+    c = torch.empty((200, 128), dtype=torch.bfloat16, device="cuda")
+    assert L.mk_gemm_bf16_epilogue(a.data_ptr(), b.data_ptr(), c.data_ptr(), None, _lib.MK_EPI_SWIGLU_PAIRS, 1,
+                                   200, 256, 64, st) == _lib.MK_EUNSUPPORTED
+    # Decode-sized rows take the streaming kernels, which have no paired form.
+    rng = np.random.default_rng(2)
+    x, p, s, z = quant.make_int4_case(rng, 16, 256, 256)
+    with pytest.raises(RuntimeError):
+        ops.int4_g64_matmul(dev_bf16(x), dev(p), dev_bf16(s), dev(z), epilogue="swiglu_pairs")

@@ -300,3 +300,17 @@ def test_event_timeout_from_environment(monkeypatch):
         e.wait()  # negative timeout: the environment value
     assert ei.value.code == rt.DEADLINE_EXCEEDED
     assert "30 ms" in ei.value.message
+
+
+def test_interleave_gate_up_column_map():
+    """Column 32q + c of the interleaved weight is gate column 16q + c and
+    column 32q + 16 + c is up column 16q + c, for every per-column array."""
+    import torch
+    from mi355x import ops
+    g = torch.arange(3 * 64, dtype=torch.int32).reshape(3, 64)
+    u = -1 - g
+    w = ops.interleave_gate_up(g, u)
+    assert w.shape == (3, 128)
+    for q in range(4):
+        assert torch.equal(w[:, 32 * q:32 * q + 16], g[:, 16 * q:16 * q + 16])
+        assert torch.equal(w[:, 32 * q + 16:32 * q + 32], u[:, 16 * q:16 * q + 16])
