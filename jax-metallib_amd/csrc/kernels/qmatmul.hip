@@ -1022,6 +1022,12 @@ bool plan_stream(int fmt, int64_t K, int64_t N, QPlan* p) {
 // the fewest splits that give >= 192 workgroups (the most the 64 KB counter
 // region and G >= 1 allow).  Grids below 128 workgroups stay on the
 // 64-column kernels.  MK_QMM_WIDE=0 disables it.
+// Ring depth (32-k steps in flight per wave) of the wide kernel with G
+// groups per wave.  At the headline (G = 2, 4 steps per wave) a 2-step ring
+// measured 13.3 us against 13.7 us for 3 steps and 13.6 us for all 4 in
+// flight at once.
+constexpr int wide_ring(int G) { return G == 4 ? 4 : G == 2 ? 2 : 2 * G; }
+
 bool plan_wide(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p) {
   const char* env = getenv("MK_QMM_WIDE");
   if (fmt != MK_QFMT_INT4_G64 || N % mk::kWideTN != 0 || K % 512 != 0 || (env && env[0] == '0')) return false;
@@ -1041,7 +1047,7 @@ bool plan_wide(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p) {
   }
   if (best == 0 || (int64_t)ntiles * rb * best < 128) return false;
   const int G = (int)(K / ((int64_t)best * 512));
-  const int R = G == 4 ? 4 : 2 * G;
+  const int R = wide_ring(G);
   const int sb = ((G * mk::kWideTN * 2 + 1023) / 1024) * 1024, zb = ((G * mk::kWideTN + 1023) / 1024) * 1024;
   int wl = R * mk::kWideSlot + sb + zb;
   wl = std::max(wl, mk::kQRows * mk::kWideRedStride * 4);
@@ -1133,7 +1139,7 @@ hipError_t launch_reduce(int fmt, const mk::QArgs& a, hipStream_t st);
 
 template <int G>
 hipError_t launch_wide(const mk::QArgs& a, const QPlan& p, hipStream_t st) {
-  constexpr int R = G == 4 ? 4 : 2 * G;
+  constexpr int R = wide_ring(G);
   dim3 grid(p.ntiles * p.ks, p.rowblocks), block(8 * mk::kWave);
   hipError_t e = lds_opt_in((const void*)mk::int4g64_wide_kernel<G, R>, p.lds_bytes);
   if (e != hipSuccess) return e;
