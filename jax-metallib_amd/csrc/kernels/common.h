@@ -80,6 +80,15 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(lds_vptr)p;
 }
 
+// 16-byte LDS DMA of every lane (source per lane) to LDS byte address
+// lds_base + 16 * lane (lds_base wave-uniform), from inline asm: the
+// compiler does not see it, so it adds no vmcnt(0) before LDS accesses; the
+// caller waits with vm_wait (below) and a barrier.
+__device__ __forceinline__ void dma16_asm(const void* src, uint32_t lds_base) {
+  const uint32_t base = __builtin_amdgcn_readfirstlane(lds_base);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base) : "memory");
+}
+
 // s_waitcnt vmcnt(n) for a value the unrolled loops fold to a constant.
 __device__ __forceinline__ void vm_wait(int n) {
   switch (n) {

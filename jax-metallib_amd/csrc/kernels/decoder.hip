@@ -250,9 +250,20 @@ __device__ __forceinline__ int fa_vswz(int r) { return (2 * (r & 3)) | (8 * ((r 
 
 __device__ __forceinline__ float fa_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// K / V tiles and the workgroup's Q rows reach LDS by DMA
+// (global_load_lds): a ring of kFaRing stages (one K tile and one V tile,
+// 32 KB) issued kFaRing - 1 tiles ahead, so each tile's load latency hides
+// behind the previous tiles' MFMAs, plus the 128 Q rows (32 KB); 160 KB in
+// all.  The XOR swizzles are applied by choosing each DMA lane's source
+// chunk.
+constexpr int kFaRing = 4;
+constexpr int kFaStage = 2 * kFaKV * kHeadDim * 2;              // 32 KB
+constexpr int kFaLds = kFaRing * kFaStage + kFaQ * kHeadDim * 2;  // 160 KB
+
 __global__ __launch_bounds__(512) void attention_causal_kernel(AttnArgs a) {
   constexpr int D = kHeadDim, ROWB = D * 2;  // 256-byte rows
-  __shared__ __attribute__((aligned(16))) unsigned char kv[2][2][kFaKV * ROWB];  // [buffer][K | V]
+  constexpr int R = kFaRing;
+  extern __shared__ __attribute__((aligned(16))) unsigned char fa_smem[];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, l16 = lane & 15;
   const int BH = a.B * a.H;
@@ -262,53 +273,71 @@ __global__ __launch_bounds__(512) void attention_causal_kernel(AttnArgs a) {
   const uint16_t* Qg = a.q + (int64_t)bh * a.S * D;
   const uint16_t* Kg = a.k + (int64_t)bh * a.S * D;
   const uint16_t* Vg = a.v + (int64_t)bh * a.S * D;
+  const uint32_t sbase = lds_addr(fa_smem);
+  unsigned char* qs = fa_smem + R * kFaStage;
 
-  u32x4 qf[4];
+  // DMA instruction I = 2w + u (u = 0, 1) of a tile covers rows 4I .. 4I+3
+  // of K and of V: lane L fills row 4I + L/16, chunk position L%16, from
+  // the source chunk the swizzle puts there (K: c ^ (row % 16), V:
+  // c ^ fa_vswz(row)).  Q: each wave's 16 rows, 4 instructions, K's swizzle.
+  const uint16_t* ksrc[2];
+  const uint16_t* vsrc[2];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) qf[s] = *reinterpret_cast<const u32x4*>(Qg + (int64_t)(i0 + l16) * D + 32 * s + 8 * g);
+  for (int u = 0; u < 2; ++u) {
+    const int row = 4 * (2 * w + u) + (lane >> 4), p = lane & 15;
+    ksrc[u] = Kg + (int64_t)row * D + 8 * (p ^ (row & 15));
+    vsrc[u] = Vg + (int64_t)row * D + 8 * (p ^ fa_vswz(row));
+  }
+  auto issue = [&](int t, int slot) {
+    const uint32_t st = sbase + (uint32_t)(slot * kFaStage);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) dma16_asm(ksrc[u] + (int64_t)t * kFaKV * D, st + (uint32_t)((2 * w + u) * 1024));
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      dma16_asm(vsrc[u] + (int64_t)t * kFaKV * D, st + (uint32_t)(kFaKV * ROWB + (2 * w + u) * 1024));
+  };
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int row = 16 * w + 4 * u + (lane >> 4), p = lane & 15;  // row within the 128 Q rows
+    dma16_asm(Qg + (int64_t)(q0 + row) * D + 8 * (p ^ (row & 15)),
+              sbase + (uint32_t)(R * kFaStage + (4 * w + u) * 1024));
+  }
+  const int ntiles = (q0 + kFaQ) / kFaKV;  // >= 2
+  const int pre = ntiles < R - 1 ? ntiles : R - 1;
+  for (int t = 0; t < pre; ++t) issue(t, t);
 
   f32x4 o[8];
 #pragma unroll
   for (int n = 0; n < 8; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, lsum = 0.f;
-
-  // Tile loads: thread -> 16-byte chunks tid and tid + 512 of the K and V
-  // tiles (row = id / 16, chunk = id % 16).
-  u32x4 kr[2], vr[2];
-  auto gload = [&](int t) {
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int id = tid + 512 * u, j = id >> 4, c = id & 15;
-      const int64_t off = (int64_t)(t * kFaKV + j) * D + 8 * c;
-      kr[u] = *reinterpret_cast<const u32x4*>(Kg + off);
-      vr[u] = *reinterpret_cast<const u32x4*>(Vg + off);
-    }
-  };
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int id = tid + 512 * u, j = id >> 4, c = id & 15;
-      *reinterpret_cast<u32x4*>(&kv[buf][0][j * ROWB + 16 * (c ^ (j & 15))]) = kr[u];
-      *reinterpret_cast<u32x4*>(&kv[buf][1][j * ROWB + 16 * (c ^ fa_vswz(j))]) = vr[u];
-    }
-  };
+  u32x4 qf[4];
 
   // V fragment byte offsets (tile-relative): d tile n, 32-key block u, low /
   // high 4 keys.  Lane (g, r = (l%16)/4, q = l%4) reads row 32u + 4g + r
   // (+16), columns 16n + 4q .. +3.
   const int vr_r = (lane & 15) >> 2, vr_q = lane & 3;
 
-  const int ntiles = (q0 + kFaQ) / kFaKV;
-  gload(0);
-  lstore(0);
-  __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) gload(t + 1);
+    const int slot = t % R;
+    // Own DMAs of tile t (and of Q) landed; the tiles issued after it may
+    // still be in flight (R - 2 of them while the ring is full, fewer at
+    // the end, where the wait is for all).  After the barrier every wave's
+    // have landed and every wave is done with tile t-1's slot.
+    if (t + R - 1 <= ntiles) vm_wait(4 * (R - 2));
+    else vm_wait(0);
+    asm volatile("s_barrier" ::: "memory");
+    if (t + R - 1 < ntiles) issue(t + R - 1, (t + R - 1) % R);
+    if (t == 0) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int row = 16 * w + l16;
+        qf[s] = *reinterpret_cast<const u32x4*>(qs + row * ROWB + 16 * ((4 * s + g) ^ (row & 15)));
+      }
+    }
     const int kv0 = t * kFaKV;
     if (kv0 <= i0 + 15) {  // some key of the tile is visible to this wave's rows
-      const unsigned char* Ks = kv[buf][0];
-      const unsigned char* Vs = kv[buf][1];
+      const unsigned char* Ks = fa_smem + slot * kFaStage;
+      const unsigned char* Vs = Ks + kFaKV * ROWB;
       f32x4 sacc[4];
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) sacc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -369,8 +398,9 @@ __global__ __launch_bounds__(512) void attention_causal_kernel(AttnArgs a) {
           o[n] = mfma16x16x32(u32x4{l2.x, l2.y, h2.x, h2.y}, pf[u], o[n]);
         }
     }
-    if (t + 1 < ntiles) lstore(buf ^ 1);
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // This wave's reads of the slot are complete before the next barrier
+    // lets another wave's DMA refill it.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
 
   lsum += __shfl_xor(lsum, 16, 64);
@@ -515,9 +545,12 @@ extern "C" int mk_attention_causal_bf16(const void* q, const void* k, const void
   a.H = (int)H;
   a.S = (int)S;
   a.scale_log2 = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL(mk::attention_causal_kernel, dim3((unsigned)(B * H * (S / mk::kFaQ))), dim3(512), 0,
-                     static_cast<hipStream_t>(stream), a);
-  const hipError_t e = hipGetLastError();
+  hipError_t e = hipFuncSetAttribute((const void*)mk::attention_causal_kernel,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, mk::kFaLds);
+  if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: LDS opt-in failed: %s", fn, hipGetErrorString(e));
+  hipLaunchKernelGGL(mk::attention_causal_kernel, dim3((unsigned)(B * H * (S / mk::kFaQ))), dim3(512),
+                     mk::kFaLds, static_cast<hipStream_t>(stream), a);
+  e = hipGetLastError();
   if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
   return MK_OK;
 }

@@ -528,12 +528,6 @@ constexpr int kGemmStageBytes = 32 * 1024;
 
 __device__ __forceinline__ int swz_b2(int k, int c) { return c ^ ((2 * (k & 3)) | (((k >> 3) & 1) << 3)); }
 
-// 16-byte LDS DMA of every lane (source per lane) to LDS byte address
-// lds_base + 16 * lane (lds_base wave-uniform).
-__device__ __forceinline__ void dma16_asm(const void* src, uint32_t lds_base) {
-  const uint32_t base = __builtin_amdgcn_readfirstlane(lds_base);
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base) : "memory");
-}
 
 template <int WN_, bool PIPE>  // waves 2 x WN_; each 128 x (256 / WN_)
 __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs p) {
