@@ -142,6 +142,32 @@ enum { MK_EPI_NONE = 0, MK_EPI_ADD = 1, MK_EPI_SWIGLU = 2, MK_EPI_SWIGLU_PAIRS =
 int mk_gemm_bf16_epilogue(const void* a, const void* b, void* c, const void* aux, int epilogue,
                           int64_t batch, int64_t M, int64_t N, int64_t K, void* stream);
 
+/* mk_dot_general: the dot_general cases the tiled GEMMs do not take,
+ * with the reference's semantics (HandleDotGeneral,
+ * src/pjrt_plugin/ops/binary_ops.mm:644-1100):
+ *   - integer operands, exact in the result type (two's-complement
+ *     wraparound, :806-809): S8 S16 S32 S64 U8 U16 U32 U64 inputs, any
+ *     integer result (lax.dot preferred_element_type=int32 included);
+ *   - K == 1 is a plain product, keeping XLA's signed zero (:904-1004);
+ *   - any K and N, operands read through element strides (a transposed
+ *     operand or a vector needs no copy);
+ *   - F32 / BF16 / F16 inputs accumulate in f32 in k order; the result is
+ *     F32 or the input type (round to nearest even).
+ * C[b, m, n] = sum_k A[b, m, k] B[b, k, n]; A[b, m, k] is element
+ * b*a_strides[0] + m*a_strides[1] + k*a_strides[2] of a, B[b, k, n] element
+ * b*b_strides[0] + k*b_strides[1] + n*b_strides[2] of b; C is contiguous
+ * [batch, M, N].  Types use the PJRT_Buffer_Type numbering below; both
+ * operands must have the same type (MK_EUNSUPPORTED otherwise).  One
+ * thread per output element: not a throughput path. */
+enum {
+  MK_TYPE_S8 = 2, MK_TYPE_S16 = 3, MK_TYPE_S32 = 4, MK_TYPE_S64 = 5, MK_TYPE_U8 = 6, MK_TYPE_U16 = 7,
+  MK_TYPE_U32 = 8, MK_TYPE_U64 = 9, MK_TYPE_F16 = 10, MK_TYPE_F32 = 11, MK_TYPE_BF16 = 13
+};
+
+int mk_dot_general(int type_a, int type_b, int type_out, const void* a, const void* b, void* c, int64_t batch,
+                   int64_t M, int64_t N, int64_t K, const int64_t* a_strides, const int64_t* b_strides,
+                   void* stream);
+
 /* ------------------------------------------------------------------------
  * Last-axis row operations on X [rows, cols] (row-major).
  *

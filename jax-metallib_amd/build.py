@@ -40,6 +40,7 @@ KERNEL_SOURCES = [
     "kernels/qgemm.hip",
     "kernels/decoder.hip",
     "kernels/gemm.hip",
+    "kernels/dot_general.hip",
     "kernels/rowops.hip",
     "kernels/eltwise.hip",
     "runtime/shlo_parser.cpp",

@@ -354,6 +354,8 @@ class Planner {
   }
 
   // ---- GEMM ------------------------------------------------------------------
+  static bool is_int_type(int t) { return t >= DT_S8 && t <= DT_U64; }
+
   struct DotShape {
     int64_t batch = 1, M = 0, N = 0, K = 0;
   };
@@ -386,41 +388,163 @@ class Planner {
     return true;
   }
 
+  // Any dot_general with one contracting dimension, batch dimensions that
+  // come first on both sides, and operands that are arguments, computed
+  // values or transposes of them (read through strides, not copied).
+  // Batch dimensions, and the free dimensions of each side, are collapsed
+  // into one index when their strides allow it (always, for row-major
+  // operands without a transpose).
+  struct GeneralDot {
+    int a = -1, b = -1;  // source values (a folded transpose's input)
+    int64_t batch = 1, M = 1, N = 1, K = 0;
+    int64_t sa[3] = {0, 0, 0}, sb[3] = {0, 0, 0};
+    bool transposed = false;
+  };
+
+  bool general_dot(const Op& op, GeneralDot* g) const {
+    if (op.operands.size() != 2) return false;
+    std::vector<int64_t> lb = op.lhs_batch, rbt = op.rhs_batch, lc = op.lhs_contract, rc = op.rhs_contract;
+    const int ra = (int)type(op.operands[0]).dims.size(), rb = (int)type(op.operands[1]).dims.size();
+    if (op.name == "dot") {
+      if (ra < 1 || rb < 1 || rb > 2) return false;
+      lc = {ra - 1};
+      rc = {0};
+    }
+    if (lc.size() != 1 || rc.size() != 1 || lb.size() != rbt.size()) return false;
+    // Operand dims -> (source value, stride of each operand dim in the source).
+    auto layout = [&](int x, int* src, std::vector<int64_t>* st, bool* tr) {
+      const Op* d = def(x);
+      std::vector<int64_t> perm;
+      *src = x;
+      if (d && d->name == "transpose" && !d->operands.empty()) {
+        *src = d->operands[0];
+        perm = d->dims;
+      }
+      const std::vector<int64_t>& sd = type(*src).dims;
+      std::vector<int64_t> rs(sd.size(), 1);
+      for (int i = (int)sd.size() - 2; i >= 0; --i) rs[i] = rs[i + 1] * sd[i + 1];
+      const size_t r = type(x).dims.size();
+      st->assign(r, 0);
+      if (perm.empty()) {
+        if (sd.size() != r) return false;
+        for (size_t i = 0; i < r; ++i) (*st)[i] = rs[i];
+        return true;
+      }
+      if (perm.size() != r || sd.size() != r) return false;
+      for (size_t i = 0; i < r; ++i) {
+        if (perm[i] < 0 || perm[i] >= (int64_t)r) return false;
+        (*st)[i] = rs[perm[i]];
+        if (perm[i] != (int64_t)i) *tr = true;
+      }
+      return true;
+    };
+    std::vector<int64_t> as, bs;
+    if (!layout(op.operands[0], &g->a, &as, &g->transposed) || !layout(op.operands[1], &g->b, &bs, &g->transposed))
+      return false;
+    const std::vector<int64_t>& ad = type(op.operands[0]).dims;
+    const std::vector<int64_t>& bd = type(op.operands[1]).dims;
+    // Collapse a list of dims (in order) into one index with one stride.
+    auto collapse = [](const std::vector<int64_t>& dims, const std::vector<int64_t>& st,
+                       const std::vector<int>& idx, int64_t* size, int64_t* stride) {
+      *size = 1;
+      *stride = 0;
+      std::vector<int> keep;
+      for (int i : idx)
+        if (dims[i] != 1) keep.push_back(i);
+      for (int i : idx) *size *= dims[i];
+      if (keep.empty()) return true;
+      *stride = st[keep.back()];
+      for (size_t j = 0; j + 1 < keep.size(); ++j)
+        if (st[keep[j]] != st[keep[j + 1]] * dims[keep[j + 1]]) return false;
+      return true;
+    };
+    const int nb = (int)lb.size();
+    for (int i = 0; i < nb; ++i)
+      if (ad[lb[i]] != bd[rbt[i]]) return false;
+    std::vector<int> a_batch, b_batch, a_free, b_free;
+    for (int i = 0; i < nb; ++i) {
+      a_batch.push_back((int)lb[i]);
+      b_batch.push_back((int)rbt[i]);
+    }
+    // The result is [batch..., lhs free..., rhs free...]: batch dims must be
+    // the first nb dims of both operands for that order to be row-major here.
+    for (int i = 0; i < nb; ++i)
+      if (lb[i] != i || rbt[i] != i) return false;
+    for (int i = 0; i < ra; ++i)
+      if (i >= nb && i != lc[0]) a_free.push_back(i);
+    for (int i = 0; i < rb; ++i)
+      if (i >= nb && i != rc[0]) b_free.push_back(i);
+    g->K = ad[lc[0]];
+    if (bd[rc[0]] != g->K) return false;
+    int64_t bsz_a, bsz_b;
+    if (!collapse(ad, as, a_batch, &bsz_a, &g->sa[0]) || !collapse(bd, bs, b_batch, &bsz_b, &g->sb[0])) return false;
+    if (!collapse(ad, as, a_free, &g->M, &g->sa[1]) || !collapse(bd, bs, b_free, &g->N, &g->sb[2])) return false;
+    g->batch = bsz_a;
+    g->sa[2] = as[lc[0]];
+    g->sb[1] = bs[rc[0]];
+    return true;
+  }
+
   bool try_gemm(int v, const Op& op, int* out) {
     DotShape d;
-    if (!dot_shape(op, &d)) {
-      reject(&op, "dimension numbers other than [batch..., M, K] x [batch..., K, N]");
-      return false;
-    }
+    GeneralDot gd;
+    const bool general = general_dot(op, &gd);
     const int ta = type(op.operands[0]).dtype, tb = type(op.operands[1]).dtype, tr = type(v).dtype;
-    Step st;
-    if (ta == DT_F32 && tb == DT_F32 && tr == DT_F32) {
-      st.kind = ST_GEMM_F32;
-      st.dt = MK_DT_F32;
-    } else if (ta == DT_BF16 && tb == DT_BF16 && (tr == DT_BF16 || tr == DT_F32)) {
-      st.kind = ST_GEMM_BF16;
-      st.dt = MK_DT_BF16;
-      st.out_f32 = tr == DT_F32;
-    } else {
-      reject(&op, std::string("operand types ") + dtype_name(ta) + " x " + dtype_name(tb) + " -> " + dtype_name(tr));
-      return false;
+    const bool fast_types = (ta == DT_F32 && tb == DT_F32 && tr == DT_F32) ||
+                            (ta == DT_BF16 && tb == DT_BF16 && (tr == DT_BF16 || tr == DT_F32));
+    if (general && gd.K == 0) {
+      Step z;
+      z.kind = ST_ZERO;
+      z.bytes = type(v).bytes();
+      z.out = temp_for(v);
+      z.desc = "zero " + type(v).str() + " (empty contraction)";
+      plan_.steps.push_back(z);
+      *out = z.out;
+      return true;
     }
-    if (d.K == 0) {
-      st.kind = ST_ZERO;
-      st.bytes = type(v).bytes();
+    const bool fast = !(general && gd.transposed) && dot_shape(op, &d) && fast_types && d.K > 0 &&
+                      d.K % 8 == 0 && d.N % 8 == 0 && numel(v) == d.batch * d.M * d.N;
+    if (!fast) {
+      if (!general) {
+        reject(&op, "dimension numbers other than one contracting dimension with leading batch dimensions");
+        return false;
+      }
+      const bool ints = is_int_type(ta) && is_int_type(tr);
+      const bool floats = (ta == DT_F32 || ta == DT_BF16 || ta == DT_F16) && (tr == ta || tr == DT_F32);
+      if (ta != tb || !(ints || floats) || numel(v) != gd.batch * gd.M * gd.N) {
+        reject(&op, std::string("operand types ") + dtype_name(ta) + " x " + dtype_name(tb) + " -> " + dtype_name(tr));
+        return false;
+      }
+      Step st;
+      st.kind = ST_DOT_GENERIC;
+      st.type_a = ta;
+      st.type_out = tr;
+      st.in = {need(gd.a), need(gd.b)};
+      st.batch = gd.batch;
+      st.M = gd.M;
+      st.N = gd.N;
+      st.K = gd.K;
+      for (int i = 0; i < 3; ++i) {
+        st.sa[i] = gd.sa[i];
+        st.sb[i] = gd.sb[i];
+      }
       st.out = temp_for(v);
-      st.desc = "zero " + type(v).str() + " (empty contraction)";
+      std::ostringstream ds;
+      ds << "dot_general " << dtype_name(ta) << " batch=" << gd.batch << " M=" << gd.M << " N=" << gd.N
+         << " K=" << gd.K << (gd.transposed ? " (strided)" : "") << " -> " << dtype_name(tr);
+      st.desc = ds.str();
       plan_.steps.push_back(st);
       *out = st.out;
       return true;
     }
-    if (numel(v) != d.batch * d.M * d.N) {
-      reject(&op, "result type " + type(v).str() + " does not match the operands");
-      return false;
-    }
-    if (d.K % 8 != 0 || d.N % 8 != 0) {
-      reject(&op, "K and N must be multiples of 8 (K=" + std::to_string(d.K) + ", N=" + std::to_string(d.N) + ")");
-      return false;
+    Step st;
+    if (ta == DT_F32) {
+      st.kind = ST_GEMM_F32;
+      st.dt = MK_DT_F32;
+    } else {
+      st.kind = ST_GEMM_BF16;
+      st.dt = MK_DT_BF16;
+      st.out_f32 = tr == DT_F32;
     }
     st.in = {need(op.operands[0]), need(op.operands[1])};
     st.batch = d.batch;

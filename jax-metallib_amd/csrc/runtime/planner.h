@@ -38,7 +38,8 @@ enum StepKind {
   ST_REDUCE,
   ST_EW,
   ST_COPY,
-  ST_ZERO
+  ST_ZERO,
+  ST_DOT_GENERIC
 };
 
 struct Step {
@@ -56,6 +57,8 @@ struct Step {
   int prog_out = 0;
   int64_t n = 0;      // elementwise element count
   int64_t bytes = 0;  // copy / zero size
+  int type_a = 0, type_out = 0;            // ST_DOT_GENERIC: PJRT element types
+  int64_t sa[3] = {0, 0, 0}, sb[3] = {0, 0, 0};  // ST_DOT_GENERIC strides (batch, m, k) / (batch, k, n)
   std::string desc;
 };
 

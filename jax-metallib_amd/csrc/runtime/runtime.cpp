@@ -372,6 +372,9 @@ int run_step(const mkrt::Step& st, const std::vector<void*>& mem, void* ws, int6
       if (st.bytes == 0) return MK_OK;
       return hipMemcpyAsync(out, in(0), (size_t)st.bytes, hipMemcpyDeviceToDevice, s) == hipSuccess ? MK_OK
                                                                                                      : MK_ELAUNCH;
+    case mkrt::ST_DOT_GENERIC:
+      return mk_dot_general(st.type_a, st.type_a, st.type_out, in(0), in(1), out, st.batch, st.M, st.N, st.K, st.sa,
+                            st.sb, s);
     case mkrt::ST_ZERO:
       if (st.bytes == 0) return MK_OK;
       return hipMemsetAsync(out, 0, (size_t)st.bytes, s) == hipSuccess ? MK_OK : MK_ELAUNCH;

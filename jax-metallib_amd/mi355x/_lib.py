@@ -38,6 +38,8 @@ SIGNATURES = {
     "mk_version": (ctypes.c_char_p, []),
     "mk_qmatmul_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64]),
     "mk_qmatmul_epilogue_supported": (_i32, [_i32, _i64, _i64, _i64, _i32]),
+    "mk_dot_general": (_i32, [_i32, _i32, _i32, _p, _p, _p, _i64, _i64, _i64, _i64, ctypes.POINTER(_i64),
+                              ctypes.POINTER(_i64), _p]),
     "mk_int4g64_matmul_bf16": (_i32, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p]),
     "mk_int8pc_matmul_bf16": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p]),
     "mk_gemm_bf16": (_i32, [_p, _p, _p, _i64, _i64, _i64, _i64, _i32, _p]),

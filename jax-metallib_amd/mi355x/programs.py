@@ -49,6 +49,54 @@ def matmul(M, K, N, dt="bf16", batch=None, preferred_f32=False):
     return _module("jit_matmul", [ta, tb], [tc], body)
 
 
+_MLIR_DT = {"int8": "i8", "uint8": "ui8", "int16": "i16", "uint16": "ui16", "int32": "i32", "uint32": "ui32",
+            "int64": "i64", "uint64": "ui64", "float16": "f16", "float32": "f32", "bfloat16": "bf16"}
+
+
+def dot_general(shape_a, shape_b, dt, out_dt=None, batch=0, contract=(None, None), transpose_b=None,
+                self_transpose=False):
+    """One stablehlo.dot_general as jax.jit(...).lower().as_text() prints it:
+    batch leading batching dims on both sides, contracting dims `contract`
+    (default: last of a, first non-batch of b).  transpose_b = a
+    permutation applied to b by a stablehlo.transpose first (the operand
+    is then the transpose's result); self_transpose: b is the transpose of
+    argument 0 (a @ a.T, one argument).  dt / out_dt are numpy dtype names."""
+    t = _MLIR_DT[dt]
+    to = _MLIR_DT[out_dt or dt]
+    ta = _t(shape_a, t)
+    tb0 = _t(shape_b, t) if shape_b is not None else None
+    lc = contract[0] if contract[0] is not None else len(shape_a) - 1
+    body, args = [], [ta] if self_transpose else [ta, tb0]
+    bname = "%arg1"
+    b_shape = list(shape_b) if shape_b is not None else None
+    if self_transpose:
+        perm = list(range(len(shape_a)))
+        perm[-1], perm[-2] = perm[-2], perm[-1]
+        b_shape = [shape_a[p] for p in perm]
+        body.append(f"%0 = stablehlo.transpose %arg0, dims = [{', '.join(map(str, perm))}] : ({ta}) -> {_t(b_shape, t)}")
+        bname = "%0"
+    elif transpose_b is not None:
+        b_shape = [shape_b[p] for p in transpose_b]
+        body.append(f"%0 = stablehlo.transpose %arg1, dims = [{', '.join(map(str, transpose_b))}] : ({tb0}) -> "
+                    f"{_t(b_shape, t)}")
+        bname = "%0"
+    rc = contract[1] if contract[1] is not None else batch
+    a_free = [shape_a[i] for i in range(batch, len(shape_a)) if i != lc]
+    b_free = [b_shape[i] for i in range(batch, len(b_shape)) if i != rc]
+    out_shape = list(shape_a[:batch]) + a_free + b_free
+    tc = _t(out_shape, to)
+    dims = []
+    if batch:
+        bl = ", ".join(str(i) for i in range(batch))
+        dims.append(f"batching_dims = [{bl}] x [{bl}]")
+    dims.append(f"contracting_dims = [{lc}] x [{rc}]")
+    res = "%1" if body else "%0"
+    body.append(f"{res} = stablehlo.dot_general %arg0, {bname}, {', '.join(dims)}, precision = [DEFAULT, DEFAULT] : "
+                f"({ta}, {_t(b_shape, t)}) -> {tc}")
+    body.append(f"return {res} : {tc}")
+    return _module("jit_dot", args, [tc], body)
+
+
 def softmax(R, C, dt="f32"):
     """jax.nn.softmax(x, axis=-1) on x [R, C]."""
     tx, tr, tr1 = _t([R, C], dt), _t([R], dt), _t([R, 1], dt)

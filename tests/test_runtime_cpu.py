@@ -201,18 +201,30 @@ def test_unsupported_ops_fail_at_compile_with_a_list():
         assert op in msg, msg
 
 
-def test_non_canonical_dot_is_rejected():
-    # x @ w.T as a contraction over both last dims: not the [M,K] x [K,N] form.
+def test_non_canonical_dot_takes_the_general_kernel():
+    # x @ w.T as a contraction over both last dims: not the [M,K] x [K,N]
+    # form, so the strided general kernel reads w in place.
     text = _wrap(["tensor<16x64xbf16>", "tensor<32x64xbf16>"], ["tensor<16x32xbf16>"], [
         "%0 = stablehlo.dot_general %arg0, %arg1, contracting_dims = [1] x [1] : "
         "(tensor<16x64xbf16>, tensor<32x64xbf16>) -> tensor<16x32xbf16>",
         "return %0 : tensor<16x32xbf16>",
     ])
+    plan, n = rt.compile_check(text)
+    assert plan.strip() == "dot_general bf16 batch=1 M=16 N=32 K=64 -> bf16" and n == 1
+
+
+def test_two_contracting_dims_are_rejected_at_compile():
+    text = _wrap(["tensor<4x8x8xf32>", "tensor<8x8x3xf32>"], ["tensor<4x3xf32>"], [
+        "%0 = stablehlo.dot_general %arg0, %arg1, contracting_dims = [1, 2] x [0, 1] : "
+        "(tensor<4x8x8xf32>, tensor<8x8x3xf32>) -> tensor<4x3xf32>",
+        "return %0 : tensor<4x3xf32>",
+    ])
     assert "stablehlo.dot_general" in _unsupported(text)
 
 
-def test_gemm_alignment_is_checked_at_compile():
-    assert "multiples of 8" in _unsupported(P.matmul(16, 60, 32))
+def test_unaligned_gemm_takes_the_general_kernel():
+    plan, _ = rt.compile_check(P.matmul(16, 60, 32))
+    assert plan.strip() == "dot_general bf16 batch=1 M=16 N=32 K=60 -> bf16"
 
 
 def test_broken_softmax_is_not_fused():
@@ -314,3 +326,23 @@ def test_interleave_gate_up_column_map():
     for q in range(4):
         assert torch.equal(w[:, 32 * q:32 * q + 16], g[:, 16 * q:16 * q + 16])
         assert torch.equal(w[:, 32 * q + 16:32 * q + 32], u[:, 16 * q:16 * q + 16])
+
+
+@pytest.mark.parametrize("args,kw,expect", [
+    (((5, 7), (7, 3), "int8"), {}, "dot_general i8 batch=1 M=5 N=3 K=7 -> i8"),
+    (((7,), (7, 3), "int16"), {}, "dot_general i16 batch=1 M=1 N=3 K=7 -> i16"),
+    (((2, 3, 4, 5), (2, 3, 5, 6), "uint32"), {"batch": 2}, "dot_general ui32 batch=6 M=4 N=6 K=5 -> ui32"),
+    (((5, 7), None, "int8"), {"self_transpose": True}, "dot_general i8 batch=1 M=5 N=5 K=7 (strided) -> i8"),
+    (((5, 7), (7, 3), "int8"), {"out_dt": "int32"}, "dot_general i8 batch=1 M=5 N=3 K=7 -> i32"),
+    (((4, 1), (1, 3), "float32"), {}, "dot_general f32 batch=1 M=4 N=3 K=1 -> f32"),
+    (((64, 64), (64, 64), "bfloat16"), {}, "gemm_bf16 batch=1 M=64 N=64 K=64 -> bf16"),
+    (((6, 0), (0, 3), "float32"), {}, "zero tensor<6x3xf32> (empty contraction)"),
+])
+def test_dot_general_routes(args, kw, expect):
+    """Integer dots, K = 1, K or N off the multiple of 8, vectors and
+    transposed operands take the general dot_general kernel; canonical
+    bf16 / f32 shapes keep the tiled GEMMs (the reference's routing of
+    HandleDotGeneral, src/pjrt_plugin/ops/binary_ops.mm:644-1100)."""
+    from mi355x import programs as P
+    plan, n = rt.compile_check(P.dot_general(*args, **kw))
+    assert plan.strip() == expect and n == 1, plan
