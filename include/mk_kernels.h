@@ -183,11 +183,13 @@ int mk_dot_general(int type_a, int type_b, int type_out, const void* a, const vo
  *
  * dtype: MK_DT_F32 or MK_DT_BF16 (x, g and y share it; argmax writes int32).
  * softmax: a row whose max is NaN or +-inf becomes all NaN.  argmax: index
- * of the first NaN, else of the first maximum, -0 == +0.  max: NaN
- * propagates, -0 < +0.  sum: f32 accumulation, result in dtype.
+ * of the first NaN, else of the first maximum, -0 == +0.  max / min: NaN
+ * propagates, -0 < +0.  sum: f32 accumulation, result in dtype.  The
+ * planner flattens a reduce over several trailing dims into one row and
+ * combines a non-neutral init value afterwards (mps_executable.mm:955-975).
  * ---------------------------------------------------------------------- */
 enum { MK_DT_F32 = 0, MK_DT_BF16 = 1 };
-enum { MK_REDUCE_SUM = 0, MK_REDUCE_MAX = 1 };
+enum { MK_REDUCE_SUM = 0, MK_REDUCE_MAX = 1, MK_REDUCE_MIN = 2 };
 
 int mk_softmax_lastdim(int dtype, const void* x, void* y, int64_t rows, int64_t cols, void* stream);
 

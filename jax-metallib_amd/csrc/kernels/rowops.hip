@@ -30,7 +30,9 @@ namespace mk {
 
 constexpr int kRowThreads = 256;
 
-enum RowOp { ROW_SOFTMAX = 0, ROW_RMSNORM = 1, ROW_ARGMAX = 2, ROW_SUM = 3, ROW_MAX = 4 };
+// ROW_MIN is max of the negated row, negated back: negation is exact, NaN
+// still propagates and -0 < +0 holds.
+enum RowOp { ROW_SOFTMAX = 0, ROW_RMSNORM = 1, ROW_ARGMAX = 2, ROW_SUM = 3, ROW_MAX = 4, ROW_MIN = 5 };
 
 struct RowArgs {
   const void* x;
@@ -264,15 +266,16 @@ __global__ __launch_bounds__(kRowThreads) void row_cached_kernel(RowArgs a) {
         for (int e = 0; e < E; ++e) s += v[q][e];
     s = block_sum(s, redf);
     if (tid == 0) V::store1(a.y, row, s);
-  } else {  // ROW_MAX
+  } else {  // ROW_MAX, ROW_MIN
+    const float sg = OP == ROW_MIN ? -1.f : 1.f;
     float m = -INFINITY;
 #pragma unroll
     for (int q = 0; q < VPT; ++q)
       if (ok[q])
 #pragma unroll
-        for (int e = 0; e < E; ++e) m = xmax(m, v[q][e]);
+        for (int e = 0; e < E; ++e) m = xmax(m, sg * v[q][e]);
     m = block_max(m, redf);
-    if (tid == 0) V::store1(a.y, row, m);
+    if (tid == 0) V::store1(a.y, row, sg * m);
   }
 }
 
@@ -344,11 +347,12 @@ __global__ __launch_bounds__(kRowThreads) void row_stream_kernel(RowArgs a) {
     for (int64_t c = tid; c < a.cols; c += kRowThreads) s += V::load1(a.x, base + c);
     s = block_sum(s, redf);
     if (tid == 0) V::store1(a.y, row, s);
-  } else {
+  } else {  // ROW_MAX, ROW_MIN
+    const float sg = OP == ROW_MIN ? -1.f : 1.f;
     float m = -INFINITY;
-    for (int64_t c = tid; c < a.cols; c += kRowThreads) m = xmax(m, V::load1(a.x, base + c));
+    for (int64_t c = tid; c < a.cols; c += kRowThreads) m = xmax(m, sg * V::load1(a.x, base + c));
     m = block_max(m, redf);
-    if (tid == 0) V::store1(a.y, row, m);
+    if (tid == 0) V::store1(a.y, row, sg * m);
   }
 }
 
@@ -419,6 +423,8 @@ extern "C" int mk_reduce_lastdim(int dtype, int op, const void* x, void* y, int6
     return run_row<mk::ROW_SUM>("mk_reduce_lastdim", dtype, x, nullptr, y, rows, cols, 0.f, stream);
   if (op == MK_REDUCE_MAX)
     return run_row<mk::ROW_MAX>("mk_reduce_lastdim", dtype, x, nullptr, y, rows, cols, 0.f, stream);
+  if (op == MK_REDUCE_MIN)
+    return run_row<mk::ROW_MIN>("mk_reduce_lastdim", dtype, x, nullptr, y, rows, cols, 0.f, stream);
   mkc::clear_error();
   return mkc::fail(MK_EUNSUPPORTED, "mk_reduce_lastdim: op %d", op);
 }

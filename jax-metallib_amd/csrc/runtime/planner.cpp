@@ -261,6 +261,35 @@ class Planner {
     return x;
   }
 
+  // Reduce over the trailing dims (one or several, in order) with an add,
+  // maximum or minimum body and a splat init: the input, the kernel op, the
+  // flattened row length and whether the init is the body's neutral value.
+  bool reduce_trailing(int v, int* x, int* op_kind, int64_t* cols, double* init, bool* neutral) const {
+    const Op* op = def(v);
+    if (!op || op->name != "reduce" || op->operands.size() != 2 || op->dims.empty()) return false;
+    *x = op->operands[0];
+    const std::vector<int64_t>& xd = type(*x).dims;
+    const int rank = (int)xd.size(), nd = (int)op->dims.size();
+    for (int i = 0; i < nd; ++i)
+      if (op->dims[i] != rank - nd + i) return false;
+    if (!splat(op->operands[1], init)) return false;
+    *cols = 1;
+    for (int i = rank - nd; i < rank; ++i) *cols *= xd[i];
+    if (op->reduce_body == "add") {
+      *op_kind = MK_REDUCE_SUM;
+      *neutral = *init == 0.0;
+    } else if (op->reduce_body == "maximum") {
+      *op_kind = MK_REDUCE_MAX;
+      *neutral = *init == -INFINITY;
+    } else if (op->reduce_body == "minimum") {
+      *op_kind = MK_REDUCE_MIN;
+      *neutral = *init == INFINITY;
+    } else {
+      return false;
+    }
+    return true;
+  }
+
   // ---- materialisation -----------------------------------------------------
   int need(int v) {
     if (slot_of_[v] >= 0) return slot_of_[v];
@@ -878,33 +907,50 @@ class Planner {
       r = def(v)->operands[0];
       if (!is(r, "reduce") || dt != DT_BF16 || type(r).dtype != DT_F32) return false;
     }
-    const char* body = nullptr;
     int op = 0;
-    if ((x = reduce_last_input(r, "add")) >= 0) {
-      body = "sum";
-      op = MK_REDUCE_SUM;
-    } else if ((x = reduce_last_input(r, "maximum")) >= 0) {
-      body = "max";
-      op = MK_REDUCE_MAX;
-    } else {
-      return false;
-    }
+    int64_t cols = 0;
+    double init = 0.0;
+    bool neutral = true;
+    if (!reduce_trailing(r, &x, &op, &cols, &init, &neutral)) return false;
+    static const char* const kBody[] = {"sum", "max", "min"};
     if (r != v) {
+      // bf16 sum accumulated in f32 (jnp.sum of bf16): convert -> reduce -> convert.
       x = peel_cvt(x);
-      if (type(x).dtype != DT_BF16 || op != MK_REDUCE_SUM) return false;
+      if (type(x).dtype != DT_BF16 || op != MK_REDUCE_SUM || !neutral) return false;
     }
-    if (mk_dt(dt) < 0 || type(x).dtype != dt || numel(v) * last_dim(x) != numel(x)) return false;
+    if (mk_dt(dt) < 0 || type(x).dtype != dt || cols <= 0 || numel(v) * cols != numel(x)) return false;
     Step st;
     st.kind = ST_REDUCE;
     st.dt = mk_dt(dt);
     st.reduce_op = op;
     st.in = {need(x)};
-    st.cols = last_dim(x);
-    st.rows = st.cols ? numel(x) / st.cols : 0;
+    st.cols = cols;
+    st.rows = numel(x) / cols;
     st.out = temp_for(v);
-    st.desc = std::string("reduce_") + body + " rows=" + std::to_string(st.rows) + " cols=" +
+    st.desc = std::string("reduce_") + kBody[op] + " rows=" + std::to_string(st.rows) + " cols=" +
               std::to_string(st.cols) + " " + dtype_name(dt);
     plan_.steps.push_back(st);
+    if (!neutral) {
+      // lax.reduce with a non-neutral init: the init joins the reduction
+      // once (mps_executable.mm:955-975), as an elementwise step on the
+      // reduced rows.
+      Step e;
+      e.kind = ST_EW;
+      e.dt = mk_dt(dt);
+      e.in = {st.out};
+      e.in_numel = {st.rows};
+      const int32_t ew_op = op == MK_REDUCE_SUM ? MK_EW_ADD : op == MK_REDUCE_MAX ? MK_EW_MAX : MK_EW_MIN;
+      e.prog = {mk_ew_instr{MK_EW_LOAD, 0, 0, 0, 0, 0.f}, mk_ew_instr{MK_EW_CONST, 1, 0, 0, 0, (float)init},
+                mk_ew_instr{ew_op, 2, 0, 1, 0, 0.f}};
+      e.prog_out = 2;
+      e.n = st.rows;
+      e.out = temp_for(v);
+      e.desc = "elementwise 3 instr, 1 inputs, n=" + std::to_string(st.rows) + " " + dtype_name(dt) +
+               " (reduce init)";
+      plan_.steps.push_back(e);
+      *out = e.out;
+      return true;
+    }
     *out = st.out;
     return true;
   }

@@ -16,7 +16,7 @@ MK_OK, MK_EINVAL, MK_EUNSUPPORTED, MK_EWORKSPACE, MK_ELAUNCH = 0, 1, 2, 3, 4
 MK_QFMT_INT4_G64, MK_QFMT_INT8_PC = 0, 1
 MK_DT_F32, MK_DT_BF16 = 0, 1
 MK_EPI_NONE, MK_EPI_ADD, MK_EPI_SWIGLU, MK_EPI_SWIGLU_PAIRS = 0, 1, 2, 3
-MK_REDUCE_SUM, MK_REDUCE_MAX = 0, 1
+MK_REDUCE_SUM, MK_REDUCE_MAX, MK_REDUCE_MIN = 0, 1, 2
 EW_OPS = ["LOAD", "CONST", "ADD", "SUB", "MUL", "DIV", "MAX", "MIN", "POW", "NEG", "ABS", "EXP", "LOG",
           "LOG1P", "EXPM1", "TANH", "RSQRT", "SQRT", "LOGISTIC", "FLOOR", "CEIL", "CMP_EQ", "CMP_NE",
           "CMP_LT", "CMP_LE", "CMP_GT", "CMP_GE", "SELECT", "ROUND_BF16"]

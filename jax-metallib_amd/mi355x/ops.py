@@ -229,7 +229,7 @@ def reduce_lastdim(x, op="sum", out=None):
     _require(x, (torch.float32,) + _BF16, "x")
     rows, cols = _rows_cols(x)
     y = out if out is not None else torch.empty(x.shape[:-1], dtype=x.dtype, device=x.device)
-    code = {"sum": _lib.MK_REDUCE_SUM, "max": _lib.MK_REDUCE_MAX}[op]
+    code = {"sum": _lib.MK_REDUCE_SUM, "max": _lib.MK_REDUCE_MAX, "min": _lib.MK_REDUCE_MIN}[op]
     check(lib().mk_reduce_lastdim(_dt(x), code, _ptr(x), _ptr(y), rows, cols, _stream(x.device)))
     return y
 

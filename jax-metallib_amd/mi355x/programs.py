@@ -227,6 +227,41 @@ def reduce(R, C, op="sum", dt="f32"):
     return _module(f"jit_{op}", [tx], [tr], body)
 
 
+_POS_INF = {"f32": "0x7F800000", "bf16": "0x7F80"}
+
+
+def reduce_trailing(shape, ndims, op="sum", dt="f32", init=None):
+    """jnp.sum / jnp.max / jnp.min / jnp.mean of x over its last `ndims`
+    axes (op "sum" / "max" / "min" / "mean"), or, with `init`, lax.reduce
+    with that init value and the op's body (add / max / min).  f32 only for
+    "mean" (jnp.mean of f32 divides the f32 sum by the count)."""
+    rank = len(shape)
+    dims = list(range(rank - ndims, rank))
+    out = list(shape[:rank - ndims])
+    tx, tr, ts = _t(shape, dt), _t(out, dt), _t([], dt)
+    body_op = {"sum": "add", "mean": "add", "max": "maximum", "min": "minimum"}[op]
+    if init is not None:
+        cst = f"{float(init):.6e}"
+    elif op in ("sum", "mean"):
+        cst = "0.000000e+00"
+    else:
+        cst = (_NEG_INF if op == "max" else _POS_INF)[dt]
+    body = [f"%cst = stablehlo.constant dense<{cst}> : {ts}",
+            f"%0 = stablehlo.reduce(%arg0 init: %cst) applies stablehlo.{body_op} across dimensions = "
+            f"[{', '.join(map(str, dims))}] : ({tx}, {ts}) -> {tr}"]
+    res = "%0"
+    if op == "mean":
+        count = 1
+        for d in dims:
+            count *= shape[d]
+        body += [f"%cst_0 = stablehlo.constant dense<{float(count):.6e}> : {ts}",
+                 f"%1 = stablehlo.broadcast_in_dim %cst_0, dims = [] : ({ts}) -> {tr}",
+                 f"%2 = stablehlo.divide %0, %1 : {tr}"]
+        res = "%2"
+    body.append(f"return {res} : {tr}")
+    return _module(f"jit_{op}", [tx], [tr], body)
+
+
 def chain6(R, C, dt="f32"):
     """The workload's 6-op chain on x [R, C]:
     a = x * 1.5; b = a + 0.5; y = jnp.where(x > 0, jnp.maximum(jnp.log1p(jnp.exp(b)), x), b)."""

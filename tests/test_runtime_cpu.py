@@ -346,3 +346,18 @@ def test_dot_general_routes(args, kw, expect):
     from mi355x import programs as P
     plan, n = rt.compile_check(P.dot_general(*args, **kw))
     assert plan.strip() == expect and n == 1, plan
+
+
+@pytest.mark.parametrize("args,expect", [
+    (((8, 16), 1, "min"), ["reduce_min rows=8 cols=16 f32"]),
+    (((4, 5, 6), 2, "sum"), ["reduce_sum rows=4 cols=30 f32"]),
+    (((4, 5, 6), 2, "max", "bf16"), ["reduce_max rows=4 cols=30 bf16"]),
+    (((8, 16), 1, "mean"), ["reduce_sum rows=8 cols=16 f32", "elementwise 3 instr, 1 inputs, n=8 f32"]),
+    (((8, 16), 1, "sum", "f32", 2.5), ["reduce_sum rows=8 cols=16 f32",
+                                       "elementwise 3 instr, 1 inputs, n=8 f32 (reduce init)"]),
+])
+def test_reduce_routes(args, expect):
+    """min, several trailing axes, mean (sum then an elementwise divide) and a
+    non-neutral init (combined once after the reduction, as the reference's
+    mps_executable.mm:955-975 does)."""
+    assert plan(P.reduce_trailing(*args)) == expect

@@ -315,3 +315,77 @@ def test_memory_stats_track_buffers(client):
     used2, _ = client.memory_stats()
     assert used2 == used0
     assert client.platform_name == "mi355x"
+
+
+def _reduce_case(rng, shape, specials=True):
+    x = (rng.standard_normal(shape) * np.sqrt(2)).astype(np.float32)
+    if specials:
+        c = shape[-1]
+        flat = x.reshape(-1, c)       # rows 0..3 fall in different output rows for every case below
+        rows = [0, flat.shape[0] // 3, 2 * flat.shape[0] // 3, flat.shape[0] - 1]
+        flat[rows[0], 3 % c] = np.nan  # NaN propagates through min / max / sum
+        flat[rows[1], :] = 0.0
+        flat[rows[1], 2 % c] = -0.0    # min of a zero row with one -0 is -0, max +0
+        flat[rows[2], 5 % c] = np.inf
+        flat[rows[3], 6 % c] = -np.inf
+    return x
+
+
+@pytest.mark.parametrize("op", ["min", "max", "sum", "mean"])
+@pytest.mark.parametrize("shape,nd", [((64, 48), 1), ((6, 8, 40), 2), ((3, 4, 5, 7), 3)])
+def test_reduce_trailing_axes(client, op, shape, nd):
+    """jnp.min / max / sum / mean over the trailing axes, f32: min and max
+    exact with NaN propagation and -0 < +0; sum and mean at f32 tolerance."""
+    rng = np.random.default_rng(len(shape) * 7 + nd)
+    x = _reduce_case(rng, shape)
+    axes = tuple(range(len(shape) - nd, len(shape)))
+    (y,) = run(client, P.reduce_trailing(shape, nd, op), x)
+    ref = {"min": np.min, "max": np.max, "sum": np.sum, "mean": np.mean}[op](x.astype(np.float64), axis=axes)
+    y = y.reshape(ref.shape)
+    assert np.array_equal(np.isnan(y), np.isnan(ref))
+    fin = np.isfinite(ref)
+    if op in ("min", "max"):
+        assert np.array_equal(y[~np.isnan(ref)], ref[~np.isnan(ref)].astype(np.float32))
+        # -0 < +0 (StableHLO minimum / maximum; numpy does not order them):
+        # a zero minimum is -0 when any zero of the row is -0, a zero
+        # maximum is -0 only when every zero of the row is.
+        rows = np.moveaxis(x, axes, tuple(range(-nd, 0))).reshape(ref.size, -1)
+        neg = np.signbit(rows) & (rows == 0)
+        pos = ~np.signbit(rows) & (rows == 0)
+        want = neg.any(axis=1) if op == "min" else ~pos.any(axis=1)
+        zero = (ref == 0).reshape(-1)
+        assert np.array_equal(np.signbit(y.reshape(-1)[zero]), want[zero])
+    else:
+        assert np.array_equal(y[~fin & ~np.isnan(ref)], ref[~fin & ~np.isnan(ref)])
+        assert_rel_close(y[fin], ref[fin], F32_RTOL, f"{op} {shape}")
+
+
+def test_reduce_min_bf16(client):
+    rng = np.random.default_rng(5)
+    x = _reduce_case(rng, (32, 64))
+    xb = f32_to_bf16_bits(x)
+    (y,) = run(client, P.reduce_trailing((32, 64), 1, "min", "bf16"), bf16(xb))
+    xf = bf16_bits_to_f32(xb)
+    ref = np.min(xf, axis=1)
+    yf = bf16_bits_to_f32(y)
+    assert np.array_equal(np.isnan(yf), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    assert np.array_equal(yf[ok], ref[ok])
+    zero = ref == 0  # -0 < +0: the zero row holds one -0
+    assert np.array_equal(np.signbit(yf[zero]), (np.signbit(xf) & (xf == 0)).any(axis=1)[zero])
+
+
+@pytest.mark.parametrize("op,init", [("sum", 2.5), ("max", 0.0), ("min", 0.25)])
+def test_reduce_non_neutral_init(client, op, init):
+    """lax.reduce with an init that is not the body's identity: the init
+    joins the reduction once."""
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal((16, 40)) * 0.5).astype(np.float32)
+    (y,) = run(client, P.reduce_trailing((16, 40), 1, op, "f32", init), x)
+    x64 = x.astype(np.float64)
+    ref = {"sum": lambda: x64.sum(1) + init, "max": lambda: np.maximum(x64.max(1), init),
+           "min": lambda: np.minimum(x64.min(1), init)}[op]()
+    if op == "sum":
+        assert_rel_close(y, ref, F32_RTOL, "sum init")
+    else:
+        assert np.array_equal(y, ref.astype(np.float32))
