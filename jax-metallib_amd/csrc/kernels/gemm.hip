@@ -641,7 +641,7 @@ __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs
       dma16_asm(bsrc[u] + (size_t)ks * BK * N,
                 sbase + (uint32_t)(slot * kGemmStageBytes + ABYTES + (DI * wave + u) * 1024));
     };
-    // The host only picks this kernel when KT >= 2 S (K >= 4096).
+    // The host only picks this kernel when KT >= 2 S.
     for (int s = 0; s < S; ++s) {
 #pragma unroll
       for (int u = 0; u < DI; ++u) issue_a(s, s, u);
@@ -870,14 +870,18 @@ int run_gemm_bf16(const char* fn, const void* a, const void* b, void* c, const v
     const dim3 grid((unsigned)((M / 256) * (N / 256)), 1, (unsigned)batch);
     const char* w = getenv("MK_GEMM_WAVES");
     const char* pv = getenv("MK_GEMM_PIPE");
-    // The pipelined kernel (fragment prefetch + 5-stage ring) for long K
-    // loops without an epilogue operand.  It has no registers left to
-    // preload one, so ADD / SWIGLU calls keep the kernel that does.  At
-    // K = 2048 it is 3-5 % faster alone but ran the decoder's sequence of
-    // K = 2048 projections 1 % slower end to end (5.51 vs 5.45 ms): the
-    // clock under it (GRBM_GUI_ACTIVE per ns) is ~2.1 GHz against ~2.35 GHz,
-    // which slows the kernels around it.  From K = 4096 it gains 7-9 %.
-    const bool pipe = !(pv && atoi(pv) == 0) && (p.epi == MK_EPI_NONE || p.epi == MK_EPI_SWIGLU_PAIRS) && K >= 4096;
+    // The pipelined kernel (fragment prefetch + 5-stage ring) for K loops
+    // of 2048 and more without an epilogue operand.  It has no registers
+    // left to preload one, so ADD / SWIGLU calls keep the kernel that does.
+    // Alone it is 3-5 % faster at K = 2048 and 7-9 % from K = 4096.  It runs
+    // at a lower clock (GRBM_GUI_ACTIVE per ns ~2.1 against ~2.35 GHz),
+    // which slows the kernels around it; in the decoder (QKV and paired
+    // gate/up products) it still gains 2 % end to end (5.00 vs 5.09 ms).
+    // MK_GEMM_PIPE_K moves the threshold.
+    const char* pk = getenv("MK_GEMM_PIPE_K");
+    const int64_t pipe_k = pk ? atoll(pk) : 2048;
+    const bool pipe = !(pv && atoi(pv) == 0) && (p.epi == MK_EPI_NONE || p.epi == MK_EPI_SWIGLU_PAIRS) &&
+                      K >= pipe_k && K >= 2 * 32 * mk::kPipeStages;
     if (w && atoi(w) == 4) {
       e = lds_opt_in((const void*)mk::gemm_bf16_256dma_kernel<2, false>, lds);
       if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256dma_kernel<2, false>), grid, dim3(256), lds, st, p);

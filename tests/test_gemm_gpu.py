@@ -129,11 +129,12 @@ def test_gemm_bf16_large_tile_path(batch, M, N, K, monkeypatch):
     assert_rel_close(cb.float().cpu().numpy().reshape(ref.shape), ref, BF16_RTOL, "256 tile bf16 out")
 
 
-@pytest.mark.parametrize("batch,M,N,K", [(1, 256, 512, 4096), (2, 512, 256, 4128), (1, 256, 256, 4160)])
+@pytest.mark.parametrize("batch,M,N,K", [(1, 256, 512, 4096), (2, 512, 256, 4128), (1, 256, 256, 4160),
+                                         (1, 512, 512, 2048), (1, 256, 256, 2080)])
 def test_gemm_bf16_pipelined_path(batch, M, N, K, monkeypatch):
-    """The pipelined 256x256 kernel (K >= 4096, no epilogue): the K loop ends
-    with 6 (K = 4096), 5 (K = 4128) or 6 (K = 4160) iterations that issue no
-    further DMA, covering both tails.  Checked against float64 on every
+    """The pipelined 256x256 kernel (K >= 2048, no epilogue operand): the K
+    loop ends with 6 (K = 4096, 2048) or 5 (K = 4128, 2080) iterations that
+    issue no further DMA, covering both tails.  Checked against float64 on every
     element, and bit for bit against the other 256x256 kernel with f32
     output: both accumulate each k in the same order in the same MFMA."""
     ops = _ops()
