@@ -87,14 +87,14 @@ def time_graph_launches(torch, fn, nsets, steps, warmup):
 
 
 def bench_int4(torch, ops, steps, warmup, M=16, K=4096, N=14336):
-    from oracle import quant
+    from mi355x import synthetic
 
     per_set = int4_bytes(M, K, N)
     nsets = max(2, -(-300 * 2 ** 20 // per_set))  # > 256 MB Infinity Cache
     rng = np.random.default_rng(0)
     sets = []
     for _ in range(nsets):
-        x, packed, s, z = quant.make_int4_case(rng, M, K, N)
+        x, packed, s, z = synthetic.int4_case(rng, M, K, N)
         sets.append((
             torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).cuda(),
             torch.from_numpy(packed).cuda(),
@@ -114,14 +114,14 @@ def bench_int4(torch, ops, steps, warmup, M=16, K=4096, N=14336):
 
 
 def bench_int8(torch, ops, steps, warmup, M=16, K=4096, N=14336):
-    from oracle import quant
+    from mi355x import synthetic
 
     per_set = int8_bytes(M, K, N)
     nsets = max(2, -(-300 * 2 ** 20 // per_set))
     rng = np.random.default_rng(0)
     sets = []
     for _ in range(nsets):
-        x, w, s = quant.make_int8_case(rng, M, K, N)
+        x, w, s = synthetic.int8_case(rng, M, K, N)
         sets.append((
             torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).cuda(),
             torch.from_numpy(w).cuda(), torch.from_numpy(s).cuda(),
@@ -305,10 +305,10 @@ def profile_run(torch, ops, kind, steps):
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
         if kind == "int4":
-            from oracle import quant
+            from mi355x import synthetic
             M, K, N = 16, 4096, 14336
             rng = np.random.default_rng(0)
-            x, packed, s, z = quant.make_int4_case(rng, M, K, N)
+            x, packed, s, z = synthetic.int4_case(rng, M, K, N)
             xd = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).cuda()
             wd, zd = torch.from_numpy(packed).cuda(), torch.from_numpy(z).cuda()
             sd = torch.from_numpy(s.view(np.int16)).view(torch.bfloat16).cuda()

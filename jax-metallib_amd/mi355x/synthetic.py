@@ -1,0 +1,51 @@
+"""Seeded synthetic inputs of the workload's quantized shapes, for the
+benchmark and profiling runs (there is no dataset or checkpoint on this
+path; the weights are random draws of the right format).
+
+Formats (the ones ``ops.int4_g64_matmul`` / ``ops.int8_pc_matmul`` take):
+  int4 g64: x bf16 [M, K]; W packed uint8 [K/2, N], byte (i, n) holding
+            k = 2i in its low nibble and k = 2i + 1 in its high nibble;
+            scale bf16 [K/64, N]; zero point uint8 [K/64, N] (0..15).
+  int8 pc:  x bf16 [M, K]; W int8 [K, N]; scale f32 [N].
+
+Draws, in this order from one ``numpy.random.Generator``:
+  x ~ N(0, 1); q ~ U{0..15}; s ~ U(1e-3, 1e-2); z ~ U{0..15}   (int4)
+  x ~ N(0, 1); W ~ U{-127..127}; s ~ U(1e-3, 1e-2)              (int8)
+bf16 values are the round-to-nearest-even bf16 of the f32 draw, returned as
+uint16 bit patterns.
+"""
+
+import numpy as np
+
+GROUP = 64
+
+
+def bf16_bits(x):
+    """float32 array -> uint16 bf16 bit patterns, round to nearest even
+    (finite inputs: every draw here is finite)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def pack_nibbles(q):
+    """uint8 [K, N] values 0..15 -> uint8 [K/2, N], even k in the low nibble."""
+    q = np.asarray(q, dtype=np.uint8)
+    return (q[0::2] | (q[1::2] << 4)).astype(np.uint8)
+
+
+def int4_case(rng, M, K, N):
+    """(x bf16 bits [M, K], W packed [K/2, N], scale bf16 bits [K/64, N],
+    zero uint8 [K/64, N])."""
+    x = bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    q = rng.integers(0, 16, size=(K, N), dtype=np.uint8)
+    s = bf16_bits(rng.uniform(1e-3, 1e-2, size=(K // GROUP, N)).astype(np.float32))
+    z = rng.integers(0, 16, size=(K // GROUP, N), dtype=np.uint8)
+    return x, pack_nibbles(q), s, z
+
+
+def int8_case(rng, M, K, N):
+    """(x bf16 bits [M, K], W int8 [K, N], scale f32 [N])."""
+    x = bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    w = rng.integers(-127, 128, size=(K, N), dtype=np.int16).astype(np.int8)
+    s = rng.uniform(1e-3, 1e-2, size=(N,)).astype(np.float32)
+    return x, w, s

@@ -266,13 +266,17 @@ def test_int4_wide_kernel_deterministic_across_calls():
 
 def test_int4_wide_and_split_k_paths_share_a_workspace():
     """Wide-kernel calls (counters in the workspace's first 64 KB) interleaved
-    with 64-column split-K calls (partials after it) through one workspace."""
+    with 64-column split-K calls and the dequantise-then-GEMM path (both
+    write after the counters) through one workspace."""
     ops = _ops()
     rng = np.random.default_rng(23)
     for (M, K, N) in [(16, 4096, 14336), (16, 4096, 1024), (1, 8192, 8192), (5, 4096, 512),
-                      (16, 4096, 14336)]:
+                      (800, 1024, 2048), (16, 4096, 14336)]:
         x, packed, s, z = quant.make_int4_case(rng, M, K, N)
         y = ops.int4_g64_matmul(dev_bf16(x), dev(packed), dev_bf16(s), dev(z))
         torch.cuda.synchronize()
         ref = cport.int4_g64_matmul(x, packed, s, z)
         assert_rel_close(host_bf16(y), ref, BF16_RTOL, f"int4 mixed {M}x{K}x{N}")
+    # Every completed call leaves the arrival counters at zero.
+    ws = ops.workspace(1, "cuda:0")
+    assert int(ws[: 64 * 1024].count_nonzero()) == 0
