@@ -590,6 +590,19 @@ __device__ __forceinline__ void ld4_sc1(const float* p0, const float* p1, const 
       : "memory");
 }
 
+// Two device-coherent 16-byte stores (sc1: written through past the per-XCD
+// L2) and the wait for their acknowledgement, in one block: no instruction
+// may overwrite a store's data registers before the store has read them (a
+// hazard the compiler does not see inside inline asm).
+__device__ __forceinline__ void st2_sc1_wait(float* p0, const f32x4& v0, float* p1, const f32x4& v1) {
+  asm volatile(
+      "global_store_dwordx4 %0, %2, off sc1\n\t"
+      "global_store_dwordx4 %1, %3, off sc1\n\t"
+      "s_waitcnt vmcnt(0)" ::"v"(p0),
+      "v"(p1), "v"(v0), "v"(v1)
+      : "memory");
+}
+
 // y quads of this thread = the KS split-K partials (this workgroup's among
 // them, already acknowledged) summed in k order.
 template <int KS>
@@ -774,15 +787,9 @@ __global__ __launch_bounds__(8 * kWave) void int4g64_wide_kernel(QArgs a) {
   const int ntiles = a.N / TN;
   if (a.ks > 1) {
     const size_t tbase = ((size_t)(rb * ntiles + tile) * a.ks) * kQRows * TN;
-    // Device-coherent 16-byte stores (sc1: written through past the per-XCD
-    // L2), then wait for their acknowledgement.
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      const int q = threadIdx.x + 8 * kWave * it;
-      float* dst = a.part + tbase + (size_t)ksi * kQRows * TN + 4 * q;
-      asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(dst), "v"(own[it]) : "memory");
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // partial stores acknowledged
+    // Device-coherent stores of the partial, acknowledged.
+    float* dst = a.part + tbase + (size_t)ksi * kQRows * TN + 4 * threadIdx.x;
+    st2_sc1_wait(dst, own[0], dst + 4 * 8 * kWave, own[1]);
     __syncthreads();  // (also: every wave is done reading the spills)
     // The flag lives in dynamic LDS: a static __shared__ would shift the
     // dynamic base off the 256-byte alignment the swizzled addressing needs.
