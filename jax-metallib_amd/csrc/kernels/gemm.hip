@@ -871,17 +871,17 @@ int run_gemm_bf16(const char* fn, const void* a, const void* b, void* c, const v
     const char* w = getenv("MK_GEMM_WAVES");
     const char* pv = getenv("MK_GEMM_PIPE");
     // The pipelined kernel (fragment prefetch + 5-stage ring) for K loops
-    // of 2048 and more without an epilogue operand.  It has no registers
-    // left to preload one, so ADD / SWIGLU calls keep the kernel that does.
+    // of 2048 and more, every epilogue included (it has no registers left
+    // to preload an ADD / SWIGLU operand, so it reads it at the store).
     // Alone it is 3-5 % faster at K = 2048 and 7-9 % from K = 4096.  It runs
     // at a lower clock (GRBM_GUI_ACTIVE per ns ~2.1 against ~2.35 GHz),
-    // which slows the kernels around it; in the decoder (QKV and paired
-    // gate/up products) it still gains 2 % end to end (5.00 vs 5.09 ms).
-    // MK_GEMM_PIPE_K moves the threshold.
+    // which slows the kernels around it; in the decoder it still gains end
+    // to end: QKV and paired gate/up 2 % (5.00 vs 5.09 ms), then the output
+    // and down projections with their residual-add epilogue another 2.5 %
+    // (4.82 vs 4.95 ms).  MK_GEMM_PIPE_K moves the threshold.
     const char* pk = getenv("MK_GEMM_PIPE_K");
     const int64_t pipe_k = pk ? atoll(pk) : 2048;
-    const bool pipe = !(pv && atoi(pv) == 0) && (p.epi == MK_EPI_NONE || p.epi == MK_EPI_SWIGLU_PAIRS) &&
-                      K >= pipe_k && K >= 2 * 32 * mk::kPipeStages;
+    const bool pipe = !(pv && atoi(pv) == 0) && K >= pipe_k && K >= 2 * 32 * mk::kPipeStages;
     if (w && atoi(w) == 4) {
       e = lds_opt_in((const void*)mk::gemm_bf16_256dma_kernel<2, false>, lds);
       if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256dma_kernel<2, false>), grid, dim3(256), lds, st, p);

@@ -31,8 +31,10 @@ def _unfused(ops, y, aux, epilogue):
 
 
 @pytest.mark.parametrize("epilogue", ["add", "swiglu"])
+# (1, 256, 256, 2048) and (2, 256, 512, 4096): the pipelined kernel (K >= 2048).
 @pytest.mark.parametrize("batch,M,N,K", [(1, 512, 512, 256), (1, 256, 768, 64), (2, 256, 256, 96),
-                                         (1, 200, 136, 64), (3, 64, 128, 32)])
+                                         (1, 200, 136, 64), (3, 64, 128, 32), (1, 256, 256, 2048),
+                                         (2, 256, 512, 4096)])
 def test_gemm_epilogue_matches_unfused(epilogue, batch, M, N, K):
     ops = _ops()
     g = torch.Generator().manual_seed(M + N + K + batch)
