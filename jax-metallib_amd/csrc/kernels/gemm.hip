@@ -743,6 +743,64 @@ __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs
   }
   }
 
+  // Pipelined kernel, bf16 output: the tile goes out through LDS.  Stored
+  // from the registers, each lane writes 4 columns of a row (8 bytes), so a
+  // wave's store touches 16 rows in 32-byte pieces and the end-of-kernel
+  // burst of such requests cost ~8 us at 4096^3.  Staged as bf16 (the
+  // rounding every path applies first), the tile is read back 16 bytes per
+  // lane along rows, and the epilogue operand is read the same way.
+  if constexpr (PIPE) {
+    if (!p.out_f32) {
+      constexpr int SROW = 272;  // staged row stride (544 B: consecutive rows 8 banks apart)
+      uint16_t* st = reinterpret_cast<uint16_t*>(smem);
+      __syncthreads();  // every wave is done with the ring
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          *reinterpret_cast<u32x2*>(st + (wm * (16 * TM) + 16 * i + (lane & 15)) * SROW + wn * (16 * TN) + 16 * j +
+                                    4 * (lane >> 4)) =
+              u32x2{pack_bf16x2(acc[i][j].x, acc[i][j].y), pack_bf16x2(acc[i][j].z, acc[i][j].w)};
+      __syncthreads();
+      auto f4 = [](uint32_t lo, uint32_t hi) {
+        return f32x4{bf16_to_f32(lo & 0xffffu), bf16_to_f32(lo >> 16), bf16_to_f32(hi & 0xffffu),
+                     bf16_to_f32(hi >> 16)};
+      };
+      uint16_t* C = static_cast<uint16_t*>(p.c) + (size_t)blockIdx.z * p.sc;
+      if (p.epi == MK_EPI_SWIGLU_PAIRS) {
+        // Output column o of the tile: gate at staged column 32 (o / 16) +
+        // o % 16, up 16 further.  16 lanes cover a 128-column output row.
+        const int N2 = N / 2;
+#pragma unroll 2
+        for (int r = 0; r < BM / 32; ++r) {
+          const int row = 32 * r + (tid >> 4), o = 8 * (tid & 15);
+          const uint16_t* sp = st + row * SROW + 32 * (o >> 4) + (o & 15);
+          const u32x4 g = *reinterpret_cast<const u32x4*>(sp);
+          const u32x4 u = *reinterpret_cast<const u32x4*>(sp + 16);
+          const size_t off = (size_t)(m0 + row) * N2 + n0 / 2 + o;
+          epi_store_swiglu_pair(C, off, f4(g.x, g.y), f4(u.x, u.y));
+          epi_store_swiglu_pair(C, off + 4, f4(g.z, g.w), f4(u.z, u.w));
+        }
+      } else {
+        const uint16_t* X = p.aux + (size_t)blockIdx.z * p.sc;
+#pragma unroll 2
+        for (int r = 0; r < BM / 16; ++r) {
+          const int row = 16 * r + (tid >> 5), c8 = 8 * (tid & 31);
+          const u32x4 v = *reinterpret_cast<const u32x4*>(st + row * SROW + c8);
+          const size_t off = (size_t)(m0 + row) * N + n0 + c8;
+          if (p.epi == MK_EPI_NONE) {
+            *reinterpret_cast<u32x4*>(C + off) = v;
+          } else {
+            const u32x4 w = *reinterpret_cast<const u32x4*>(X + off);
+            epi_store_bf16x4_v(C, u32x2{w.x, w.y}, p.epi, off, f4(v.x, v.y));
+            epi_store_bf16x4_v(C, u32x2{w.z, w.w}, p.epi, off + 4, f4(v.z, v.w));
+          }
+        }
+      }
+      return;
+    }
+  }
+
   // Epilogue (C^T tiles): lane owns row m, columns n..n+3 of each tile.
   if (p.epi == MK_EPI_SWIGLU_PAIRS) {
     // Blocks j (gate) and j+1 (up), j even, hold the same output columns.
