@@ -524,6 +524,8 @@ __global__ __launch_bounds__(WM_ * WN_ * 64) void gemm_bf16_256_kernel(GemmArgs 
 #endif
 constexpr int kGemmStages = MK_GEMM_STAGES;
 constexpr int kPipeStages = 5;  // 5 x 32 KB: all of the 160 KB LDS
+constexpr int kEpiStageRow = 272;                   // bf16 per staged output row (256 + 16 pad)
+constexpr int kEpiStageBytes = 256 * kEpiStageRow * 2;  // 139,264 B: the staged 256x256 tile
 constexpr int kGemmStageBytes = 32 * 1024;
 
 __device__ __forceinline__ int swz_b2(int k, int c) { return c ^ ((2 * (k & 3)) | (((k >> 3) & 1) << 3)); }
@@ -743,15 +745,16 @@ __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs
   }
   }
 
-  // Pipelined kernel, bf16 output: the tile goes out through LDS.  Stored
-  // from the registers, each lane writes 4 columns of a row (8 bytes), so a
-  // wave's store touches 16 rows in 32-byte pieces and the end-of-kernel
-  // burst of such requests cost ~8 us at 4096^3.  Staged as bf16 (the
-  // rounding every path applies first), the tile is read back 16 bytes per
-  // lane along rows, and the epilogue operand is read the same way.
-  if constexpr (PIPE) {
-    if (!p.out_f32) {
-      constexpr int SROW = 272;  // staged row stride (544 B: consecutive rows 8 banks apart)
+  // bf16 output through LDS (8-wave kernels; the ring kernel keeps its
+  // preloaded ADD / SWIGLU operand in registers and stores those directly).
+  // Stored from the registers, each lane writes 4 columns of a row (8
+  // bytes), so a wave's store touches 16 rows in 32-byte pieces and the
+  // end-of-kernel burst of such requests cost ~8 us at 4096^3.  Staged as
+  // bf16 (the rounding every path applies first), the tile is read back 16
+  // bytes per lane along rows, and the epilogue operand is read the same way.
+  if constexpr (WN_ == 4) {
+    if (!p.out_f32 && (PIPE || p.epi == MK_EPI_NONE || p.epi == MK_EPI_SWIGLU_PAIRS)) {
+      constexpr int SROW = kEpiStageRow;  // staged row stride (544 B: consecutive rows 8 banks apart)
       uint16_t* st = reinterpret_cast<uint16_t*>(smem);
       __syncthreads();  // every wave is done with the ring
 #pragma unroll
@@ -948,8 +951,11 @@ int run_gemm_bf16(const char* fn, const void* a, const void* b, void* c, const v
       e = lds_opt_in((const void*)mk::gemm_bf16_256dma_kernel<4, true>, lds_p);
       if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256dma_kernel<4, true>), grid, dim3(512), lds_p, st, p);
     } else {
-      e = lds_opt_in((const void*)mk::gemm_bf16_256dma_kernel<4, false>, lds);
-      if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256dma_kernel<4, false>), grid, dim3(512), lds, st, p);
+      // The ring takes 128 KB; the staged epilogue tile needs 136 KB (one
+      // workgroup per CU either way).
+      constexpr size_t lds4 = lds > (size_t)mk::kEpiStageBytes ? lds : (size_t)mk::kEpiStageBytes;
+      e = lds_opt_in((const void*)mk::gemm_bf16_256dma_kernel<4, false>, lds4);
+      if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256dma_kernel<4, false>), grid, dim3(512), lds4, st, p);
     }
     if (e == hipSuccess) e = hipGetLastError();
   } else if (tile == 256 && M % 256 == 0 && N % 256 == 0 && K % 64 == 0) {
