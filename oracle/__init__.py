@@ -41,4 +41,9 @@ PINS = {
     "rowops.argmax": "reference special-value matrices (first NaN, first max, -0 == +0) vs brute force",
     "rowops.reduce": "brute force; NaN propagation; -0/+0 max",
     "eltwise.chain6": "op-by-op closed forms (exp(0)=1, log1p(0)=0, select masks) + bf16 rounding points",
+    "cport.int4_g64_matmul": "numpy oracle (M > 64, ragged N, several groups, column slices), brute-force "
+                             "loop, nibble-order / zero-point closed form",
+    "cport.int8_pc_matmul": "numpy oracle, brute-force loop, identity weight with and without scales",
+    "cport.gemm_bf16": "numpy oracle (row slices), A @ I == A, ones (= K), K * m * n index matrices",
+    "cport.argmax_f32": "brute-force loop on the reference's special-value matrices, known rows",
 }

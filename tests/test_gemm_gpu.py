@@ -36,8 +36,6 @@ BF16_SHAPES = [
 @pytest.mark.parametrize("out_f32", [False, True])
 def test_gemm_bf16_matches_oracle(batch, M, N, K, out_f32):
     ops = _ops()
-    if (M, N, K) == (4096, 4096, 4096) and not out_f32:
-        pytest.skip("covered by the f32-output run of the same shape")
     rng = np.random.default_rng(batch * 131 + M + N + K)
     a = _case(rng, (batch, M, K), 1.0 / np.sqrt(np.sqrt(K)))
     b = _case(rng, (batch, K, N), 1.0 / np.sqrt(np.sqrt(K)))
@@ -145,6 +143,11 @@ def test_gemm_bf16_pipelined_path(batch, M, N, K, monkeypatch):
     ref, _ = gemm.matmul_bf16(a, b)
     c = ops.gemm_bf16(dev_bf16(a), dev_bf16(b), out_f32=True)
     assert_rel_close(c.cpu().numpy().reshape(ref.shape), ref, 8e-5, f"pipelined {batch}x{M}x{N}x{K}")
+    # bf16 output: the LDS-staged store rounds the same f32 accumulator.
+    cb = ops.gemm_bf16(dev_bf16(a), dev_bf16(b), out_f32=False)
+    cb_bits = cb.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(cb_bits, obf.f32_to_bf16_bits(c.cpu().numpy())), "bf16 store != r(f32 accumulator)"
+    assert_rel_close(cb.float().cpu().numpy().reshape(ref.shape), ref, BF16_RTOL, f"pipelined bf16 out")
     monkeypatch.setenv("MK_GEMM_PIPE", "0")
     c0 = ops.gemm_bf16(dev_bf16(a), dev_bf16(b), out_f32=True)
     torch.cuda.synchronize()

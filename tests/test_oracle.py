@@ -370,3 +370,259 @@ def test_eltwise_nan_and_signed_zero_max():
     y = eltwise.evaluate(prog, [a, b])
     assert np.isnan(y[0]) and np.isnan(y[1])
     assert y[2] == 0 and not np.signbit(y[2]) and not np.signbit(y[3])
+
+
+# ------------------------------------------------- the C port (oracle/c)
+#
+# oracle/c/oracle.c is the checker for the full-size quantized, GEMM and
+# argmax GPU tests and the bench's CPU baseline.  It accumulates in f32 (the
+# numpy restatements in float64), so it is held to the numpy oracle at a
+# relative 1e-5 of each output's magnitude, to brute-force loops, and to
+# closed forms that f32 accumulation reproduces exactly.  Shapes cover the
+# port's 64-row and 64-column chunking: M > 64 with a ragged last chunk, N not
+# a multiple of 64, several K groups, and column slices (n_range / m_range).
+
+def _cport():
+    from oracle import cport
+    try:
+        cport.lib()
+    except RuntimeError as e:  # pragma: no cover - the build step makes it
+        pytest.fail(str(e))
+    return cport
+
+
+def _close_f32_accum(out, ref, K):
+    """f32 accumulation of K products vs float64: |err| <= K * 2^-23 * sum|terms|,
+    bounded here by a normwise 1e-5 (K <= 512) and an elementwise check."""
+    out = np.asarray(out, np.float64)
+    ref = np.asarray(ref, np.float64)
+    scale = max(np.max(np.abs(ref)), 1e-30)
+    assert np.max(np.abs(out - ref)) <= 1e-5 * scale
+
+
+@pytest.mark.parametrize("M,K,N", [(70, 192, 100), (130, 128, 65), (1, 64, 8), (65, 256, 129)])
+def test_cport_int4_matches_numpy_oracle(M, K, N):
+    cport = _cport()
+    rng = np.random.default_rng(M * 1000 + K + N)
+    x, p, s, z = quant.make_int4_case(rng, M, K, N)
+    ref, _ = quant.int4_g64_matmul(x, p, s, z, round_w=True)
+    got = cport.int4_g64_matmul(x, p, s, z)
+    _close_f32_accum(got, ref, K)
+
+
+def test_cport_int4_brute_force_and_column_slice():
+    cport = _cport()
+    rng = np.random.default_rng(31)
+    x, p, s, z = quant.make_int4_case(rng, 3, 128, 5)
+    got = cport.int4_g64_matmul(x, p, s, z)
+    _close_f32_accum(got, _brute_int4(x, p, s, z, round_w=True), 128)
+    # Column slice: the columns in [n0, n1) equal the full result, the rest stay 0.
+    x, p, s, z = quant.make_int4_case(rng, 70, 128, 200)
+    full = cport.int4_g64_matmul(x, p, s, z)
+    part = cport.int4_g64_matmul(x, p, s, z, n_range=(37, 101))
+    np.testing.assert_array_equal(part[:, 37:101], full[:, 37:101])
+    assert not part[:, :37].any() and not part[:, 101:].any()
+
+
+def test_cport_int4_nibble_order_and_zero_point():
+    """A swapped nibble or a dropped zero-point fails these closed forms:
+    even k carries q = 1, odd k q = 3 (low nibble = even k), z = 1, s = 0.5,
+    x = 1 on even k and 0 on odd k -> every output is 0 (q - z = 0 on even k);
+    x = 1 on odd k only -> every output is (K/2) * (3 - 1) * 0.5 = K/2."""
+    cport = _cport()
+    K, N = 256, 70
+    q = np.zeros((K, N), np.uint8)
+    q[0::2] = 1
+    q[1::2] = 3
+    p = quant.pack_int4_k(q)
+    assert p[0, 0] == 0x31
+    s = np.full((K // 64, N), 0x3F00, np.uint16)   # 0.5
+    z = np.ones((K // 64, N), np.uint8)
+    x = np.zeros((2, K), np.float32)
+    x[0, 0::2] = 1.0
+    x[1, 1::2] = 1.0
+    y = cport.int4_g64_matmul(bf16.f32_to_bf16_bits(x), p, s, z)
+    assert np.all(y[0] == 0.0)
+    assert np.all(y[1] == K / 2)
+
+
+@pytest.mark.parametrize("M,K,N", [(70, 192, 100), (1, 64, 8), (130, 320, 65)])
+def test_cport_int8_matches_numpy_oracle(M, K, N):
+    cport = _cport()
+    rng = np.random.default_rng(M * 7 + K + N)
+    x, w, s = quant.make_int8_case(rng, M, K, N)
+    ref, _ = quant.int8_pc_matmul(x, w, s)
+    _close_f32_accum(cport.int8_pc_matmul(x, w, s), ref, K)
+    part = cport.int8_pc_matmul(x, w, s, n_range=(5, N - 3))
+    full = cport.int8_pc_matmul(x, w, s)
+    np.testing.assert_array_equal(part[:, 5:N - 3], full[:, 5:N - 3])
+
+
+def test_cport_int8_brute_force_and_identity():
+    cport = _cport()
+    rng = np.random.default_rng(33)
+    x, w, s = quant.make_int8_case(rng, 2, 64, 3)
+    xs = bf16.bf16_bits_to_f32(x)
+    ref = np.array([[sum(float(xs[m, k]) * int(w[k, n]) for k in range(64)) * float(s[n])
+                     for n in range(3)] for m in range(2)])
+    _close_f32_accum(cport.int8_pc_matmul(x, w, s), ref, 64)
+    # W = I, s = 1: Y = X exactly (a transposed W or a scale on the wrong
+    # axis fails this).
+    eye = np.eye(80, dtype=np.int8)
+    x8 = bf16.randn_bf16(rng, (3, 80))
+    y = cport.int8_pc_matmul(x8, eye, np.ones(80, np.float32))
+    np.testing.assert_array_equal(y, bf16.bf16_bits_to_f32(x8))
+    sc = np.arange(1, 81, dtype=np.float32)
+    y = cport.int8_pc_matmul(x8, eye, sc)
+    np.testing.assert_array_equal(y, bf16.bf16_bits_to_f32(x8) * sc[None, :])
+
+
+@pytest.mark.parametrize("M,K,N", [(70, 96, 33), (3, 512, 130)])
+def test_cport_gemm_bf16_matches_numpy_oracle(M, K, N):
+    cport = _cport()
+    rng = np.random.default_rng(M + K + N)
+    a = bf16.randn_bf16(rng, (M, K))
+    b = bf16.randn_bf16(rng, (K, N))
+    ref, _ = gemm.matmul_bf16(a, b)
+    _close_f32_accum(cport.gemm_bf16(a, b), ref, K)
+    part = cport.gemm_bf16(a, b, m_range=(1, M - 1))
+    np.testing.assert_array_equal(part[1:M - 1], cport.gemm_bf16(a, b)[1:M - 1])
+
+
+def test_cport_gemm_bf16_closed_forms():
+    """A @ I == A exactly; ones @ ones == K exactly; a non-square A @ B.T
+    transposition mistake changes the shape/values of the asymmetric case."""
+    cport = _cport()
+    rng = np.random.default_rng(34)
+    a = bf16.randn_bf16(rng, (9, 64))
+    eye = bf16.f32_to_bf16_bits(np.eye(64, dtype=np.float32))
+    np.testing.assert_array_equal(cport.gemm_bf16(a, eye), bf16.bf16_bits_to_f32(a))
+    ones_a = bf16.f32_to_bf16_bits(np.ones((4, 300), np.float32))
+    ones_b = bf16.f32_to_bf16_bits(np.ones((300, 7), np.float32))
+    assert np.all(cport.gemm_bf16(ones_a, ones_b) == 300)
+    # Row-index matrix times column-index matrix: C[m, n] = sum_k m * n = K m n.
+    K = 16
+    am = bf16.f32_to_bf16_bits(np.repeat(np.arange(5, dtype=np.float32)[:, None], K, axis=1))
+    bn = bf16.f32_to_bf16_bits(np.repeat(np.arange(3, dtype=np.float32)[None, :], K, axis=0))
+    c = cport.gemm_bf16(am, bn)
+    np.testing.assert_array_equal(c, K * np.outer(np.arange(5), np.arange(3)))
+
+
+@pytest.mark.parametrize("shape,seed", [((512, 37), 0), ((300, 1), 0), ((8, 2049), 3), ((64, 300), 5)])
+def test_cport_argmax_matches_brute(shape, seed):
+    cport = _cport()
+    x = _edge(shape, seed)
+    ref = [rowops.brute_argmax_row(list(row)) for row in x]
+    np.testing.assert_array_equal(cport.argmax_f32(x), ref)
+    np.testing.assert_array_equal(cport.argmax_f32(x), rowops.argmax(x))
+
+
+def test_cport_argmax_known_rows():
+    cport = _cport()
+    x = np.random.default_rng(1).standard_normal((6, 16)).astype(np.float32)
+    x[0] = np.nan
+    x[1, 5] = np.nan
+    x[1, 9] = np.nan
+    x[2] = 2.0
+    x[3, :4] = [np.inf, np.nan, -np.inf, np.nan]
+    x[4, -1] = np.nan
+    got = cport.argmax_f32(x)
+    assert got[:5].tolist() == [0, 5, 0, 1, 15]
+    z = np.array([[-0.0, 0.0], [0.0, -0.0], [-1.0, -0.0]], np.float32)
+    assert cport.argmax_f32(z).tolist() == [0, 0, 1]
+
+
+# ------------------------------------------------------- decoder layer
+
+def test_decoder_rope_closed_forms():
+    from oracle import decoder
+    cos, sin = decoder.rope_tables(8, 4)
+    x = np.array([1.0, 2.0, 3.0, 4.0])
+    # position 0: identity
+    np.testing.assert_array_equal(decoder.rope(x, cos[0], sin[0]), x)
+    # pair i rotates by angle pos * base^(-2i/D): pos 3, pair 0 by 3 rad, pair 1 by 3/100 rad
+    y = decoder.rope(x, cos[3], sin[3])
+    np.testing.assert_allclose(y[[0, 2]], [math.cos(3) - 3 * math.sin(3), 3 * math.cos(3) + math.sin(3)])
+    np.testing.assert_allclose(y[[1, 3]], [2 * math.cos(.03) - 4 * math.sin(.03), 4 * math.cos(.03) + 2 * math.sin(.03)])
+    # a rotation keeps each pair's norm
+    np.testing.assert_allclose(y[:2] ** 2 + y[2:] ** 2, x[:2] ** 2 + x[2:] ** 2)
+
+
+def test_decoder_attention_brute_force_and_closed_forms():
+    from oracle import decoder
+    rng = np.random.default_rng(40)
+    S, D = 9, 4
+    q, k, v = rng.standard_normal((S, D)), rng.standard_normal((S, D)), rng.standard_normal((S, D))
+    pos = np.arange(S)
+    out = decoder.attention_causal_rows(q, pos, k, v, 0.5)
+    np.testing.assert_array_equal(out[0], v[0])            # one visible key
+    for t in range(S):
+        w = [math.exp(0.5 * sum(q[t, d] * k[j, d] for d in range(D))) for j in range(t + 1)]
+        ref = [sum(w[j] * v[j, d] for j in range(t + 1)) / sum(w) for d in range(D)]
+        np.testing.assert_allclose(out[t], ref, rtol=1e-12)
+    # equal keys: uniform weights, the mean of the visible values (a mask
+    # that let later keys in would fail this)
+    out = decoder.attention_causal_rows(q, pos, np.ones((S, D)), v, 1.0)
+    for t in range(S):
+        np.testing.assert_allclose(out[t], v[:t + 1].mean(axis=0), rtol=1e-12)
+
+
+def _tiny_layer_weights(rng, hidden, A, F, zero_scale=False):
+    def w(K, N):
+        q = rng.integers(0, 16, size=(K, N), dtype=np.uint8)
+        s = np.zeros((K // 64, N), np.float32) if zero_scale else rng.uniform(4e-3, 6e-3, (K // 64, N))
+        return (quant.pack_int4_k(q), bf16.f32_to_bf16_bits(np.asarray(s, np.float32)),
+                rng.integers(0, 16, size=(K // 64, N), dtype=np.uint8))
+    g = bf16.f32_to_bf16_bits(rng.uniform(0.5, 1.5, hidden).astype(np.float32))
+    g2 = bf16.f32_to_bf16_bits(rng.uniform(0.5, 1.5, hidden).astype(np.float32))
+    return {"g_attn": g, "g_mlp": g2, "w_qkv": w(hidden, 3 * A), "w_o": w(A, hidden),
+            "w_gate": w(hidden, F), "w_up": w(hidden, F), "w_down": w(F, hidden)}
+
+
+def test_decoder_layer_zero_weights_is_identity():
+    from oracle import decoder
+    rng = np.random.default_rng(41)
+    x = bf16.round_bf16(rng.standard_normal((6, 128)))
+    w = _tiny_layer_weights(rng, 128, 128, 128, zero_scale=True)
+    out = decoder.layer_rows(x, np.arange(6), w, heads=1, head_dim=128)
+    np.testing.assert_array_equal(out, x)
+
+
+def test_decoder_layer_rows_brute_force():
+    """The subset evaluation equals a plain whole-sequence evaluation written
+    with explicit loops over heads and positions."""
+    from oracle import decoder
+    rng = np.random.default_rng(42)
+    S, hidden, H, D, F = 5, 128, 2, 64, 192
+    x = bf16.round_bf16(rng.standard_normal((S, hidden)))
+    w = _tiny_layer_weights(rng, hidden, H * D, F)
+    r = bf16.round_bf16
+    deq = {n: quant.int4_g64_dequant(*w[n]).astype(np.float64) for n in ("w_qkv", "w_o", "w_gate", "w_up", "w_down")}
+    g1 = bf16.bf16_bits_to_f32(w["g_attn"]).astype(np.float64)
+    g2 = bf16.bf16_bits_to_f32(w["g_mlp"]).astype(np.float64)
+    cos, sin = decoder.rope_tables(S, D)
+    ref = np.zeros((S, hidden))
+    h = np.array([r(x[t] / math.sqrt(np.mean(x[t].astype(np.float64) ** 2) + 1e-6) * g1) for t in range(S)])
+    qkv = r(h @ deq["w_qkv"])
+    for t in range(S):
+        a = np.zeros(H * D)
+        for hd in range(H):
+            def rot(vec, p):
+                half = D // 2
+                return np.array([vec[i] * cos[p, i] - vec[i + half] * sin[p, i] for i in range(half)] +
+                                [vec[i + half] * cos[p, i] + vec[i] * sin[p, i] for i in range(half)])
+            qv = r(rot(qkv[t, hd * D:(hd + 1) * D], t))
+            ks = [r(rot(qkv[j, H * D + hd * D:H * D + (hd + 1) * D], j)) for j in range(t + 1)]
+            vs = [qkv[j, 2 * H * D + hd * D:2 * H * D + (hd + 1) * D] for j in range(t + 1)]
+            sc = np.array([float(qv @ kk) / math.sqrt(D) for kk in ks])
+            p = np.exp(sc - sc.max())
+            p /= p.sum()
+            a[hd * D:(hd + 1) * D] = sum(p[j] * vs[j] for j in range(t + 1))
+        x1 = r(x[t] + r(r(a) @ deq["w_o"]))
+        h2 = r(x1 / math.sqrt(np.mean(x1.astype(np.float64) ** 2) + 1e-6) * g2)
+        gg, uu = r(h2 @ deq["w_gate"]), r(h2 @ deq["w_up"])
+        act = r(r(gg * r(1 / (1 + np.exp(-gg.astype(np.float64))))) * uu)
+        ref[t] = r(x1 + r(act @ deq["w_down"]))
+    pos = np.array([4, 0, 2])
+    out = decoder.layer_rows(x, pos, w, heads=H, head_dim=D)
+    np.testing.assert_allclose(out, ref[pos], rtol=2 ** -7, atol=1e-6)

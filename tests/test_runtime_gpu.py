@@ -203,7 +203,7 @@ def test_chain6(client, dt):
 
 def test_plumbing_tanh_matmul_sum(client):
     rng = np.random.default_rng(0)
-    n = 512
+    n = 1024
     a = rng.standard_normal((n, n)).astype(np.float32)
     b = rng.standard_normal((n, n)).astype(np.float32)
     (y,) = run(client, P.plumbing(n), a, b)

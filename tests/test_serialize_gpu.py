@@ -15,7 +15,10 @@ import pytest
 
 from mi355x import programs as P
 from mi355x import runtime as rt
-from oracle.bf16 import f32_to_bf16_bits
+from oracle import eltwise, rowops
+from oracle.bf16 import bf16_bits_to_f32, f32_to_bf16_bits
+
+from _gpu import BF16_RTOL, F32_RTOL, assert_rel_close
 
 pytestmark = pytest.mark.gpu
 
@@ -56,6 +59,19 @@ def _cases():
     ]
 
 
+def _oracle_check(name, arrays, out):
+    """The deserialized executable's output against the CPU oracle."""
+    if name == "chain6 bf16":
+        ref = eltwise.evaluate(eltwise.CHAIN6, [bf16_bits_to_f32(arrays[0][0])], "bf16")
+        assert_rel_close(bf16_bits_to_f32(out), ref, BF16_RTOL, name)
+    elif name == "softmax f32":
+        assert_rel_close(out, rowops.softmax(arrays[0]), F32_RTOL, name)
+    else:
+        a, b = arrays
+        ref = np.tanh(a.astype(np.float64) @ b.astype(np.float64)).sum(axis=1)
+        assert np.max(np.abs(out - ref)) <= 1e-5 * a.shape[0], name
+
+
 @pytest.mark.parametrize("name,text,arrays", _cases(), ids=[c[0] for c in _cases()])
 def test_round_trip_is_bit_identical(client, name, text, arrays):
     print(f"[serialize] {name}", flush=True)
@@ -70,6 +86,7 @@ def test_round_trip_is_bit_identical(client, name, text, arrays):
     for r, o in zip(ref, out):
         assert r.dtype == o.dtype and r.shape == o.shape
         assert np.array_equal(r.view(np.uint8), o.view(np.uint8)), name
+    _oracle_check(name, arrays, out[0])
     # Serializing the deserialized executable gives the same bytes.
     assert exe2.serialize() == blob
     exe2.close()
@@ -126,3 +143,4 @@ def test_deserialized_executable_compiles_nothing(client, tmp_path):
     compiles, disk_hits, _ = res["stats"]
     assert compiles == 0 and disk_hits == 0, res["stats"]
     assert bytes.fromhex(res["out"]) == ref.tobytes()
+    _oracle_check("chain6 bf16", [(x, rt.BF16)], ref.reshape(128, 256))
