@@ -97,6 +97,21 @@ int mk_int8pc_matmul_epilogue_bf16(const void* x, const void* w, const void* sca
                                    const void* aux, int epilogue, int64_t M, int64_t K, int64_t N,
                                    void* workspace, int64_t workspace_bytes, void* stream);
 
+/* mk_int4g64_matmul_bf16 without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * The workspace is a file-scope device array of 8 MiB per GPU, held until the
+ * process ends; shapes whose mk_qmatmul_workspace_bytes exceeds 8 MiB
+ * (for example M >= 768 at K = 4096, N = 14336) return MK_EWORKSPACE before
+ * any launch.  The first call on a device sets the array up (its address,
+ * and its counters cleared by a kernel on `stream`).  The call allocates
+ * nothing and gives bit-identical results to mk_int4g64_matmul_bf16.  Every
+ * call on one GPU shares the array: calls that overlap in time on one GPU
+ * (unordered streams) race. */
+int mk_int4g64_matmul_bf16_noalloc(const void* x, const void* w_packed, const void* scale,
+                                   const void* zero, void* y, int64_t M, int64_t K, int64_t N,
+                                   void* stream);
+
 /* ------------------------------------------------------------------------
  * dot_general GEMM (canonical batched NN form).
  *

@@ -1341,3 +1341,82 @@ extern "C" int mk_int8pc_matmul_epilogue_bf16(const void* x, const void* w, cons
   return run_q(MK_QFMT_INT8_PC, x, w, scale, nullptr, y, M, K, N, workspace, workspace_bytes, stream, aux,
                epilogue);
 }
+
+// ---------------------------------------------------------------------------
+// No-allocation entry point: the workspace is a file-scope device array.
+//
+// Each GPU the library runs on holds its own copy of `scratch` until the
+// process ends.  In host code the array's name is only a host-side stand-in,
+// so every host use goes through the per-device address that
+// hipGetSymbolAddress returns at set-up.  The first 64 KB are the wide
+// kernel's arrival counters, which must read zero before a call: set-up
+// clears them once per device with a fill kernel (not a memset node, so the
+// call can sit inside a captured graph), and every completed call leaves them
+// at zero again.  All calls on one GPU share the array: calls that overlap in
+// time on one GPU (different streams without ordering) race on it.
+// ---------------------------------------------------------------------------
+#include <mutex>
+
+namespace {
+
+constexpr int64_t kNoAllocScratchBytes = 8ll << 20;
+constexpr int kMaxDevices = 64;
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+__global__ void scratch_clear_kernel(uint32_t* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The calling thread's device's copy of `scratch`, set up on first use:
+// its address, and its counter region cleared on `stream`.
+int scratch_for_current_device(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return mkc::fail(MK_ELAUNCH, "mk_int4g64_matmul_bf16_noalloc: no current device (%s)", hipGetErrorString(e));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return mkc::fail(MK_ELAUNCH, "mk_int4g64_matmul_bf16_noalloc: hipGetSymbolAddress failed on device %d: %s",
+                       dev, hipGetErrorString(e));
+    const int words = (int)(mk::kWidePartOffset / 4);
+    hipLaunchKernelGGL(scratch_clear_kernel, dim3((words + 255) / 256), dim3(256), 0, stream,
+                       static_cast<uint32_t*>(ptr), words);
+    e = hipGetLastError();
+    if (e != hipSuccess)
+      return mkc::fail(MK_ELAUNCH, "mk_int4g64_matmul_bf16_noalloc: scratch clear failed: %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MK_OK;
+}
+
+}  // namespace
+
+extern "C" int mk_int4g64_matmul_bf16_noalloc(const void* x, const void* w_packed, const void* scale,
+                                              const void* zero, void* y, int64_t M, int64_t K, int64_t N,
+                                              void* stream) {
+  mkc::clear_error();
+  const int64_t need = mk_qmatmul_workspace_bytes(MK_QFMT_INT4_G64, M, K, N);
+  if (need > kNoAllocScratchBytes)
+    return mkc::fail(MK_EWORKSPACE,
+                     "mk_int4g64_matmul_bf16_noalloc: M=%lld K=%lld N=%lld needs %lld bytes of workspace; "
+                     "the no-allocation entry point holds %lld (use mk_int4g64_matmul_bf16 with a workspace)",
+                     (long long)M, (long long)K, (long long)N, (long long)need, (long long)kNoAllocScratchBytes);
+  // Shapes the plan rejects (need < 0) fail in run_q with its own message,
+  // before anything is set up or launched.
+  if (need < 0)
+    return run_q(MK_QFMT_INT4_G64, x, w_packed, scale, zero, y, M, K, N, nullptr, 0, stream);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  const int rc = scratch_for_current_device(st, &ws);
+  if (rc != MK_OK) return rc;
+  return run_q(MK_QFMT_INT4_G64, x, w_packed, scale, zero, y, M, K, N, ws, kNoAllocScratchBytes, stream);
+}

@@ -41,6 +41,7 @@ SIGNATURES = {
     "mk_dot_general": (_i32, [_i32, _i32, _i32, _p, _p, _p, _i64, _i64, _i64, _i64, ctypes.POINTER(_i64),
                               ctypes.POINTER(_i64), _p]),
     "mk_int4g64_matmul_bf16": (_i32, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p]),
+    "mk_int4g64_matmul_bf16_noalloc": (_i32, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "mk_int8pc_matmul_bf16": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p]),
     "mk_gemm_bf16": (_i32, [_p, _p, _p, _i64, _i64, _i64, _i64, _i32, _p]),
     "mk_gemm_bf16_epilogue": (_i32, [_p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _p]),
