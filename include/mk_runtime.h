@@ -146,9 +146,12 @@ void mkrt_executable_destroy(mkrt_executable* exe);
  * StableHLO text plus the gfx950 code objects of the executable's fused
  * elementwise programs, so a deserialized executable compiles nothing on
  * its first execute.  Layout (little-endian):
- *   "MKEX" | u32 version (1) | u32 flags (0) | u64 program bytes | program |
- *   u32 code objects | per object: u64 source bytes | source |
- *   u64 code bytes | code
+ *   "MKEX" | u32 version (2) | u32 flags (0) | u64 tag bytes | tag |
+ *   u64 program bytes | program | u32 code objects | per object:
+ *   u64 source bytes | source | u64 code bytes | code
+ * The tag names the hiprtc version and compile options of the code objects;
+ * a deserialize under another tag recompiles the elementwise programs
+ * instead of loading the embedded objects.
  * Errors as the reference's: empty or malformed data -> INVALID_ARGUMENT;
  * a program that does not compile -> its compile error.
  *

@@ -318,23 +318,26 @@ bool hiprtc_compile(const std::string& src, std::vector<char>* code, std::string
   return true;
 }
 
-// Code object of a source: memory, then disk, then hiprtc.  g_mu held.
-const std::vector<char>* code_for(const std::string& src, std::string* err) {
+// Code object of a source: memory, then disk, then hiprtc (only hiprtc when
+// `fresh`, which replaces whatever the caches held).  g_mu held.
+const std::vector<char>* code_for(const std::string& src, std::string* err, bool fresh = false) {
   auto it = g_code.find(src);
-  if (it != g_code.end()) {
+  if (it != g_code.end() && !fresh) {
     g_mem_hits.fetch_add(1);
     return &it->second;
   }
   std::vector<char> code;
   const std::string dir = cache_dir();
   const std::string path = dir.empty() ? "" : cache_path(dir, src);
-  if (!path.empty() && read_cached(path, src, &code)) {
+  if (!fresh && !path.empty() && read_cached(path, src, &code)) {
     g_disk_hits.fetch_add(1);
   } else {
     if (!hiprtc_compile(src, &code, err)) return nullptr;
     if (!path.empty()) write_cached(path, src, code);
   }
-  return &g_code.emplace(src, std::move(code)).first->second;
+  std::vector<char>& slot = g_code[src];
+  slot = std::move(code);
+  return &slot;
 }
 
 hipError_t load_module(const std::vector<char>& code, JitKernel* k, std::string* err) {
@@ -363,10 +366,17 @@ int ew_jit_get(int dtype, const mk_ew_instr* prog, int n_instr, int n_inputs, in
   auto it = g_cache.find(key);
   if (it == g_cache.end()) {
     std::string err;
-    const std::vector<char>* code = code_for(generate(dtype, prog, n_instr, n_inputs, out_slot), &err);
+    const std::string src = generate(dtype, prog, n_instr, n_inputs, out_slot);
+    const std::vector<char>* code = code_for(src, &err);
     if (!code) return fail(MK_ELAUNCH, "mk_elementwise: %s", err.c_str());
     JitKernel k;
     e = load_module(*code, &k, &err);
+    if (e != hipSuccess) {
+      // A cached or seeded object the runtime rejects: compile it afresh.
+      code = code_for(src, &err, true);
+      if (!code) return fail(MK_ELAUNCH, "mk_elementwise: %s", err.c_str());
+      e = load_module(*code, &k, &err);
+    }
     if (e != hipSuccess) return fail(MK_ELAUNCH, "mk_elementwise: %s", err.c_str());
     it = g_cache.emplace(key, k).first;
   }
@@ -384,6 +394,8 @@ int ew_jit_code(int dtype, const mk_ew_instr* prog, int n_instr, int n_inputs, i
   *code = *c;
   return MK_OK;
 }
+
+const std::string& ew_jit_tag() { return compile_tag(); }
 
 void ew_jit_seed(const std::string& source, const std::vector<char>& code) {
   std::lock_guard<std::mutex> lock(g_mu);

@@ -24,8 +24,15 @@ int ew_jit_get(int dtype, const mk_ew_instr* prog, int n_instr, int n_inputs, in
 int ew_jit_code(int dtype, const mk_ew_instr* prog, int n_instr, int n_inputs, int out_slot, std::string* source,
                 std::vector<char>* code);
 
+// Everything a code object depends on besides its source: the hiprtc
+// version and the compile options.  A serialized executable records it, and
+// its code objects are reused only when it matches.
+const std::string& ew_jit_tag();
+
 // Adds a code object for a source to the in-memory cache (a deserialized
-// executable's), so its first launch loads it instead of compiling.
+// executable's, built under the same tag), so its first launch loads it
+// instead of compiling.  A seeded object that fails to load is dropped and
+// the source compiled again.
 void ew_jit_seed(const std::string& source, const std::vector<char>& code);
 
 // Process totals: hiprtc compiles, disk-cache hits, memory-cache hits.

@@ -26,6 +26,8 @@
 
 #include <math.h>
 
+#include <algorithm>
+
 namespace mk {
 
 constexpr int kRowThreads = 256;
@@ -169,7 +171,10 @@ __global__ __launch_bounds__(kRowThreads) void row_cached_kernel(RowArgs a) {
   constexpr int E = V::N;
   __shared__ float redf[4];
   __shared__ int redi[4];
-  const int64_t row = blockIdx.x;
+  // Rows are strided over the grid (the launch caps it), so any row count
+  // fits a launch; every wave of a workgroup runs the same iterations, so
+  // the barriers inside the reductions stay uniform.
+  for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
   const int64_t base = row * a.cols;
   const int tid = threadIdx.x;
   float v[VPT][E];
@@ -277,6 +282,7 @@ __global__ __launch_bounds__(kRowThreads) void row_cached_kernel(RowArgs a) {
     m = block_max(m, redf);
     if (tid == 0) V::store1(a.y, row, sg * m);
   }
+  }
 }
 
 // Streaming row kernel for any cols: scalar strided passes over the row
@@ -286,7 +292,7 @@ __global__ __launch_bounds__(kRowThreads) void row_stream_kernel(RowArgs a) {
   using V = Vec<T>;
   __shared__ float redf[4];
   __shared__ int redi[4];
-  const int64_t row = blockIdx.x;
+  for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
   const int64_t base = row * a.cols;
   const int tid = threadIdx.x;
   if (OP == ROW_SOFTMAX) {
@@ -354,6 +360,7 @@ __global__ __launch_bounds__(kRowThreads) void row_stream_kernel(RowArgs a) {
     m = block_max(m, redf);
     if (tid == 0) V::store1(a.y, row, sg * m);
   }
+  }
 }
 
 }  // namespace mk
@@ -365,6 +372,8 @@ __global__ __launch_bounds__(kRowThreads) void row_stream_kernel(RowArgs a) {
 
 namespace {
 
+constexpr int64_t kMaxRowBlocks = 1 << 20;
+
 template <typename T, int OP>
 hipError_t launch_row(const mk::RowArgs& a, hipStream_t st) {
   constexpr int E = mk::Vec<T>::N;
@@ -372,7 +381,9 @@ hipError_t launch_row(const mk::RowArgs& a, hipStream_t st) {
                        (OP != mk::ROW_RMSNORM || (uintptr_t)a.g % 16 == 0);
   const int64_t vecs = (a.cols + E - 1) / E;
   const int64_t vpt = (vecs + mk::kRowThreads - 1) / mk::kRowThreads;
-  dim3 grid((unsigned)a.rows), block(mk::kRowThreads);
+  // One workgroup per row up to kMaxRowBlocks rows (2^28 work-items); more
+  // rows stride over that grid.
+  dim3 grid((unsigned)std::min<int64_t>(a.rows, kMaxRowBlocks)), block(mk::kRowThreads);
   if (aligned && vpt <= 16) {
     if (vpt <= 1) hipLaunchKernelGGL((mk::row_cached_kernel<T, OP, 1>), grid, block, 0, st, a);
     else if (vpt <= 2) hipLaunchKernelGGL((mk::row_cached_kernel<T, OP, 2>), grid, block, 0, st, a);

@@ -551,10 +551,12 @@ std::string fingerprint_of(const std::string& program) {
   return b;
 }
 
-// Serialized executable: "MKEX" | u32 version | u32 flags (0) | u64 program
-// bytes | program | u32 code objects | per object: u64 source bytes |
-// source | u64 code bytes | code.  Little-endian.
-constexpr uint32_t kSerialVersion = 1;
+// Serialized executable: "MKEX" | u32 version | u32 flags (0) | u64 tag
+// bytes | tag | u64 program bytes | program | u32 code objects | per object:
+// u64 source bytes | source | u64 code bytes | code.  Little-endian.  The
+// tag is the elementwise compile tag (hiprtc version and options) the code
+// objects were built under.
+constexpr uint32_t kSerialVersion = 2;
 
 void put_u32(std::string& b, uint32_t v) { b.append(reinterpret_cast<const char*>(&v), 4); }
 void put_u64(std::string& b, uint64_t v) { b.append(reinterpret_cast<const char*>(&v), 8); }
@@ -577,6 +579,9 @@ mkrt_error* serialize_plan(const std::string& program, const mkrt::Plan& plan, s
   b.append("MKEX", 4);
   put_u32(b, kSerialVersion);
   put_u32(b, 0);
+  const std::string& tag = mkc::ew_jit_tag();
+  put_u64(b, tag.size());
+  b += tag;
   put_u64(b, program.size());
   b += program;
   put_u32(b, (uint32_t)objs.size());
@@ -591,6 +596,7 @@ mkrt_error* serialize_plan(const std::string& program, const mkrt::Plan& plan, s
 
 // Parsed view of a serialized executable (pointers into the caller's bytes).
 struct SerialView {
+  std::string tag;
   const char* program = nullptr;
   uint64_t program_bytes = 0;
   std::vector<std::pair<std::string, std::vector<char>>> objs;
@@ -616,6 +622,11 @@ mkrt_error* parse_serialized(const void* bytes, int64_t size, SerialView* v, boo
   if (ver != kSerialVersion)
     return make_error(MKRT_INVALID_ARGUMENT, "DeserializeAndLoad: serialized format version %u, this build reads %u",
                       ver, kSerialVersion);
+  uint64_t tag_bytes = 0;
+  if (!take(&tag_bytes, 8) || (uint64_t)(end - p) < tag_bytes || tag_bytes > 4096)
+    return make_error(MKRT_INVALID_ARGUMENT, "DeserializeAndLoad: truncated compile tag");
+  v->tag.assign(p, tag_bytes);
+  p += tag_bytes;
   if (!take(&v->program_bytes, 8) || (uint64_t)(end - p) < v->program_bytes)
     return make_error(MKRT_INVALID_ARGUMENT, "DeserializeAndLoad: truncated program");
   v->program = p;
@@ -803,7 +814,10 @@ mkrt_error* mkrt_deserialize(mkrt_client* c, const void* bytes, int64_t size, mk
   *out = nullptr;
   SerialView v;
   if (mkrt_error* e = parse_serialized(bytes, size, &v, true)) return e;
-  for (const auto& o : v.objs) mkc::ew_jit_seed(o.first, o.second);
+  // Code objects built by another toolchain or with other options are not
+  // reused: the program's elementwise steps are then compiled again.
+  if (v.tag == mkc::ew_jit_tag())
+    for (const auto& o : v.objs) mkc::ew_jit_seed(o.first, o.second);
   mkrt_error* e = mkrt_compile(c, v.program, (int64_t)v.program_bytes, "mlir", out);
   if (e) {
     mkrt_error* w = make_error(e->code, "DeserializeAndLoad: %s", e->message.c_str());

@@ -185,8 +185,12 @@ def _qmm(x, w: Int4Weight, out, epilogue=None, aux=None):
     return ops.int4_g64_matmul(x, w.packed, w.scale, w.zero, out=out, epilogue=epilogue, aux=aux)
 
 
-def layer_forward(cfg: DecoderConfig, lw: LayerWeights, buf: Buffers, cos, sin):
-    """One decoder layer on buf.x, in place."""
+def layer_forward(cfg: DecoderConfig, lw: LayerWeights, buf: Buffers, cos, sin, taps=None):
+    """One decoder layer on buf.x, in place.  With a dict `taps`, copies of
+    the attention output ("attn"), the residual stream after the attention
+    block ("x1") and the SwiGLU activation ("act") are stored in it (for
+    stage-by-stage checks; the copies allocate, so leave taps None under
+    graph capture)."""
     B, S, H, D = cfg.batch, cfg.seq, cfg.heads, cfg.head_dim
     ops.rmsnorm(buf.x, lw.g_attn, eps=cfg.eps, out=buf.h)
     _qmm(buf.h, lw.w_qkv, buf.qkv)
@@ -199,25 +203,34 @@ def layer_forward(cfg: DecoderConfig, lw: LayerWeights, buf: Buffers, cos, sin):
         ops.merge_heads(buf.o, B, H, out=buf.attn)
     else:
         ops.attention_causal(buf.q, buf.k, buf.v, B, H, 1.0 / math.sqrt(D), out=buf.attn)
+    def tap(name, t):
+        if taps is not None:
+            taps[name] = t.clone()
+
+    tap("attn", buf.attn)
     if buf.fuse:
         # Residual adds and silu(g) * u ride on the projections' stores, and
         # the gate and up projections are one product (bit-identical to the
         # separate products and elementwise programs below).
         _qmm(buf.attn, lw.w_o, buf.x, epilogue="add", aux=buf.x)
+        tap("x1", buf.x)
         ops.rmsnorm(buf.x, lw.g_mlp, eps=cfg.eps, out=buf.h)
         if ops.int4_swiglu_pairs_supported(cfg.tokens, cfg.hidden, 2 * cfg.ffn):
             _qmm(buf.h, lw.w_gateup, buf.act, epilogue="swiglu_pairs")
         else:  # too few tokens for the many-row route: two products
             _qmm(buf.h, lw.w_gate, buf.gate)
             _qmm(buf.h, lw.w_up, buf.act, epilogue="swiglu", aux=buf.gate)
+        tap("act", buf.act)
         _qmm(buf.act, lw.w_down, buf.x, epilogue="add", aux=buf.x)
         return
     _qmm(buf.attn, lw.w_o, buf.proj)
     ops.elementwise(RESIDUAL_PROGRAM, [buf.x, buf.proj], out_slot=2, out=buf.x)
+    tap("x1", buf.x)
     ops.rmsnorm(buf.x, lw.g_mlp, eps=cfg.eps, out=buf.h)
     _qmm(buf.h, lw.w_gate, buf.gate)
     _qmm(buf.h, lw.w_up, buf.up)
     ops.elementwise(SWIGLU_PROGRAM, [buf.gate, buf.up], out_slot=4, out=buf.act)
+    tap("act", buf.act)
     _qmm(buf.act, lw.w_down, buf.proj)
     ops.elementwise(RESIDUAL_PROGRAM, [buf.x, buf.proj], out_slot=2, out=buf.x)
 

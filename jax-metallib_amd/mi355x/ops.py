@@ -33,14 +33,20 @@ def _require(t, dtypes, name):
 _BF16 = (torch.bfloat16, torch.int16, torch.uint16)
 
 
-def workspace(nbytes, device):
-    """A device workspace of at least nbytes, cached per device.  It starts
-    zero-filled (its first 64 KB are arrival counters that every completed
-    call leaves at zero)."""
-    key = torch.device(device).index or 0
+def workspace(nbytes, device, stream=None):
+    """A device workspace of at least nbytes, cached per (device, stream):
+    calls that share a workspace must be ordered, and calls on one stream
+    are.  It starts zero-filled (its first 64 KB are arrival counters that
+    every completed call leaves at zero).  A workspace that grows is replaced;
+    torch's caching allocator keeps the old block until the stream's work on
+    it is done."""
+    dev = torch.device(device)
+    index = dev.index if dev.index is not None else torch.cuda.current_device()
+    sid = stream if stream is not None else _stream(torch.device("cuda", index))
+    key = (index, int(sid or 0))
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+        ws = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=dev)
         _WORKSPACES[key] = ws
     return ws
 

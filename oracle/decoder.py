@@ -74,16 +74,10 @@ def _logistic(x):
     return 1.0 / (1.0 + np.exp(-x))
 
 
-def layer_rows(x, pos, w, heads, head_dim, eps=1e-6, rope_base=10000.0):
-    """One decoder layer of one sequence, evaluated at query positions `pos`.
-
-    x    float [S, hidden] -- the layer's bf16 input (as float values)
-    pos  int [R] -- query positions to return
-    w    dict: g_attn, g_mlp (bf16 bits [hidden]); w_qkv, w_o, w_gate, w_up,
-         w_down as (packed uint8 [K/2, N], scale bf16 bits [K/64, N],
-         zero uint8 [K/64, N])
-    Returns the layer output rows [R, hidden] (float64 values of bf16).
-    """
+def attention_block(x, pos, w, heads, head_dim, eps=1e-6, rope_base=10000.0):
+    """The attention half of a layer at query positions `pos` of one sequence
+    x [S, hidden]: {"attn": heads-merged attention output a, "attn_proj":
+    r(a @ Wo), "x1": r(x + r(a @ Wo))} for those rows."""
     x = np.asarray(x, dtype=np.float64)
     pos = np.asarray(pos, dtype=np.int64)
     S, hidden = x.shape
@@ -91,9 +85,7 @@ def layer_rows(x, pos, w, heads, head_dim, eps=1e-6, rope_base=10000.0):
     A = H * D
     last = int(pos.max()) + 1
     g1 = bf16_bits_to_f32(w["g_attn"]).astype(np.float64)
-    g2 = bf16_bits_to_f32(w["g_mlp"]).astype(np.float64)
     cos, sin = rope_tables(S, D, rope_base)
-
     h = round_bf16(rowops.rmsnorm(x[:last], g1, eps))
     wqkv = _w(w["w_qkv"])
     kv = round_bf16(h @ wqkv[:, A:])                        # k | v of positions 0..last-1
@@ -107,10 +99,46 @@ def layer_rows(x, pos, w, heads, head_dim, eps=1e-6, rope_base=10000.0):
     for hd in range(H):
         a[:, hd] = attention_causal_rows(q[:, hd], pos, k[:, hd], v[:, hd], scale)
     a = round_bf16(a.reshape(len(pos), A))
+    return {"attn": a, **output_residual(x[pos], a, w["w_o"])}
 
-    x1 = round_bf16(x[pos] + round_bf16(a @ _w(w["w_o"])))
-    h2 = round_bf16(rowops.rmsnorm(x1, g2, eps))
+
+def output_residual(x_rows, a_rows, w_o):
+    """{"attn_proj": r(a @ Wo), "x1": r(x + r(a @ Wo))} for given rows."""
+    attn_proj = round_bf16(np.asarray(a_rows, np.float64) @ _w(w_o))
+    return {"attn_proj": attn_proj, "x1": round_bf16(np.asarray(x_rows, np.float64) + attn_proj)}
+
+
+def mlp_act(x1_rows, w, eps=1e-6):
+    """act = r(r(g * r(logistic(g))) * u) with g = r(h2 @ Wg), u = r(h2 @ Wu),
+    h2 = r(rmsnorm(x1) * g_mlp), for rows of x1."""
+    g2 = bf16_bits_to_f32(w["g_mlp"]).astype(np.float64)
+    h2 = round_bf16(rowops.rmsnorm(np.asarray(x1_rows, np.float64), g2, eps))
     gt = round_bf16(h2 @ _w(w["w_gate"]))
     up = round_bf16(h2 @ _w(w["w_up"]))
-    act = round_bf16(round_bf16(gt * round_bf16(_logistic(gt))) * up)
-    return round_bf16(x1 + round_bf16(act @ _w(w["w_down"])))
+    return round_bf16(round_bf16(gt * round_bf16(_logistic(gt))) * up)
+
+
+def down_residual(x1_rows, act_rows, w_down):
+    """{"down": r(act @ Wd), "out": r(x1 + r(act @ Wd))} for given rows."""
+    down = round_bf16(np.asarray(act_rows, np.float64) @ _w(w_down))
+    return {"down": down, "out": round_bf16(np.asarray(x1_rows, np.float64) + down)}
+
+
+def layer_rows(x, pos, w, heads, head_dim, eps=1e-6, rope_base=10000.0, parts=False):
+    """One decoder layer of one sequence, evaluated at query positions `pos`.
+
+    x    float [S, hidden] -- the layer's bf16 input (as float values)
+    pos  int [R] -- query positions to return
+    w    dict: g_attn, g_mlp (bf16 bits [hidden]); w_qkv, w_o, w_gate, w_up,
+         w_down as (packed uint8 [K/2, N], scale bf16 bits [K/64, N],
+         zero uint8 [K/64, N])
+    Returns the layer output rows [R, hidden] (float64 values of bf16), or
+    with ``parts`` a dict of them ("out") and of every intermediate the
+    blocks above return ("attn", "attn_proj", "x1", "act", "down").
+    """
+    att = attention_block(x, pos, w, heads, head_dim, eps, rope_base)
+    act = mlp_act(att["x1"], w, eps)
+    dr = down_residual(att["x1"], act, w["w_down"])
+    if parts:
+        return {**att, "act": act, **dr}
+    return dr["out"]

@@ -154,3 +154,22 @@ def test_reduce_max_nan_and_signed_zero():
     assert m[1] == 0 and not np.signbit(m[1])
     assert m[2] == 0 and np.signbit(m[2])
     assert m[3] == 3
+
+
+@pytest.mark.parametrize("op", ["softmax", "argmax", "sum"])
+def test_more_rows_than_one_launch_row_each(op):
+    """More rows than the launch gives workgroups (2^20): rows stride over the
+    grid, and the last rows are computed like the first."""
+    ops = _ops()
+    rows, cols = (1 << 20) + 37, 16
+    x = _x((rows, cols), 21)
+    print(f"rows case {op} {rows}x{cols}", flush=True)
+    xd = dev(x)
+    if op == "softmax":
+        y = ops.softmax(xd).cpu().numpy()
+        assert_rel_close(y, rowops.softmax(x), F32_RTOL, "softmax many rows")
+    elif op == "argmax":
+        np.testing.assert_array_equal(ops.argmax(xd).cpu().numpy(), rowops.argmax(x))
+    else:
+        y = ops.reduce_lastdim(xd, "sum").cpu().numpy()
+        assert_rel_close(y, rowops.reduce_sum(x), F32_RTOL, "sum many rows")

@@ -27,8 +27,12 @@ PKG = os.path.join(REPO, "jax-metallib_amd")
 def _parse(blob):
     """The documented layout, read independently of the library."""
     assert blob[:4] == b"MKEX"
-    ver, flags, plen = struct.unpack_from("<IIQ", blob, 4)
+    ver, flags, tlen = struct.unpack_from("<IIQ", blob, 4)
     off = 20
+    tag = blob[off:off + tlen]
+    off += tlen
+    (plen,) = struct.unpack_from("<Q", blob, off)
+    off += 8
     program = blob[off:off + plen]
     off += plen
     (n,) = struct.unpack_from("<I", blob, off)
@@ -43,15 +47,17 @@ def _parse(blob):
         off += 8 + cl
         objs.append((src, code))
     assert off == len(blob)
-    return ver, flags, program, objs
+    return ver, flags, tag, program, objs
 
 
 def test_serialized_layout_and_code_objects(tmp_path, monkeypatch):
     monkeypatch.setenv("MK_CACHE_DIR", str(tmp_path))
     text = pg.chain6(256, 256, "bf16")
     blob = rt.serialize_program(text)
-    ver, flags, program, objs = _parse(blob)
-    assert (ver, flags) == (1, 0)
+    ver, flags, tag, program, objs = _parse(blob)
+    assert (ver, flags) == (2, 0)
+    # The compile tag names the hiprtc version and the options.
+    assert tag.startswith(b"hiprtc ") and b"--offload-arch=gfx950" in tag and b"-ffp-contract=off" in tag
     assert program == text.encode()
     assert len(objs) == 1
     src, code = objs[0]
@@ -73,13 +79,18 @@ def test_malformed_serializations_are_invalid_argument(tmp_path, monkeypatch):
     blob = rt.serialize_program(pg.chain6(64, 64, "f32"))
     _expect_invalid(b"")
     _expect_invalid(b"MKEY" + blob[4:])
-    _expect_invalid(blob[:4] + struct.pack("<I", 2) + blob[8:])
+    _expect_invalid(blob[:4] + struct.pack("<I", 1) + blob[8:])   # the format before the tag
+    _expect_invalid(blob[:4] + struct.pack("<I", 3) + blob[8:])
     _expect_invalid(blob + b"\0")
+    (tlen,) = struct.unpack_from("<Q", blob, 12)
+    poff = 20 + tlen
     # Every truncation point, header through the last code byte.
-    for cut in sorted({1, 4, 8, 12, 19, 20, 21, len(blob) // 2, len(blob) - 1}):
+    for cut in sorted({1, 4, 8, 12, 19, 20, 21, poff - 1, poff, poff + 7, poff + 8, len(blob) // 2,
+                       len(blob) - 1}):
         _expect_invalid(blob[:cut])
-    # A program length that runs past the end.
+    # A tag or program length that runs past the end.
     _expect_invalid(blob[:12] + struct.pack("<Q", len(blob)) + blob[20:])
+    _expect_invalid(blob[:poff] + struct.pack("<Q", len(blob)) + blob[poff + 8:])
 
 
 def test_serialize_rejects_unsupported_programs():

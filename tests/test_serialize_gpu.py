@@ -6,6 +6,7 @@ deserialized executable compiles nothing on its first execute in a fresh
 process with the disk cache off."""
 
 import json
+import struct
 import os
 import subprocess
 import sys
@@ -144,3 +145,30 @@ def test_deserialized_executable_compiles_nothing(client, tmp_path):
     assert compiles == 0 and disk_hits == 0, res["stats"]
     assert bytes.fromhex(res["out"]) == ref.tobytes()
     _oracle_check("chain6 bf16", [(x, rt.BF16)], ref.reshape(128, 256))
+
+
+def test_code_objects_under_another_compile_tag_are_recompiled(client, tmp_path):
+    """A blob written under another hiprtc version or other options (its tag
+    differs) is not trusted: the fresh process compiles the program again,
+    with the same result."""
+    text = P.chain6(128, 256, "bf16")
+    x = f32_to_bf16_bits(np.random.default_rng(4).standard_normal((128, 256)).astype(np.float32))
+    exe = client.compile(text)
+    (ref,) = _execute(client, exe, [(x, rt.BF16)])
+    blob = bytearray(exe.serialize())
+    exe.close()
+    (tlen,) = struct.unpack_from("<Q", blob, 12)
+    assert blob[20:27] == b"hiprtc "
+    blob[20 + tlen - 1] ^= 0x01   # another tag of the same length
+    blob_path, x_path = tmp_path / "exe.mkex", tmp_path / "x.npy"
+    blob_path.write_bytes(bytes(blob))
+    np.save(x_path, x)
+    env = dict(os.environ, MK_DISABLE_CACHE_PERSIST="1")
+    print("[serialize] fresh-process deserialize, foreign tag", flush=True)
+    r = subprocess.run([sys.executable, "-c", _CHILD.format(pkg=PKG), str(blob_path), str(x_path)], env=env,
+                       capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0, r.stderr
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    compiles, disk_hits, _ = res["stats"]
+    assert compiles == 1 and disk_hits == 0, res["stats"]
+    assert bytes.fromhex(res["out"]) == ref.tobytes()
