@@ -282,19 +282,47 @@ def _hbm_entry(gbs, us, extra=None):
     return e
 
 
+def sources_digest(paths):
+    """sha256 (16 hex digits) of the kernel sources a measurement was taken
+    with, paths relative to the repository root."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in paths:
+        with open(os.path.join(REPO, rel), "rb") as f:
+            h.update(rel.encode() + b"\0" + f.read())
+    return h.hexdigest()[:16]
+
+
 def traffic_from_profiles(kernel):
     """Measured HBM bytes per launch of `kernel`, from the committed rocprof
     PMC summary profiles/<kernel>_traffic.md (FETCH_SIZE + WRITE_SIZE per
-    dispatch, scaled by the copy-kernel calibration it records), or None."""
+    dispatch, scaled by the copy-kernel calibration it records).  The file
+    names the kernel sources it was measured with and their digest; when the
+    sources have changed since, the figure belongs to another kernel and None
+    is returned.  Returns (bytes or None, note)."""
     path = os.path.join(REPO, "profiles", f"{kernel}_traffic.md")
+    value, sources, digest = None, None, None
     try:
         with open(path) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":", 1)[1].strip())
+                    value = int(line.split(":", 1)[1].strip())
+                elif line.startswith("sources:"):
+                    sources = line.split(":", 1)[1].split()
+                elif line.startswith("sources_sha256:"):
+                    digest = line.split(":", 1)[1].strip()
     except OSError:
-        pass
-    return None
+        return None, "no traffic profile"
+    if value is None or not sources or not digest:
+        return None, "traffic profile without a source digest"
+    try:
+        now = sources_digest(sources)
+    except OSError:
+        return None, "traffic profile names missing sources"
+    if now != digest:
+        return None, f"stale: measured with sources {digest}, current {now}"
+    return value, f"measured with sources {digest} (current)"
 
 
 def profile_run(torch, ops, kind, steps):
@@ -324,6 +352,18 @@ def profile_run(torch, ops, kind, steps):
 
             def fn():
                 ops.gemm_bf16(a, b, out=c)
+        elif kind == "qgemm":
+            from mi355x import synthetic
+            M, K, N = 256, 4096, 14336
+            rng = np.random.default_rng(0)
+            x, packed, s, z = synthetic.int4_case(rng, M, K, N)
+            xd = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).cuda()
+            wd, zd = torch.from_numpy(packed).cuda(), torch.from_numpy(z).cuda()
+            sd = torch.from_numpy(s.view(np.int16)).view(torch.bfloat16).cuda()
+            yd = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+
+            def fn():
+                ops.int4_g64_matmul(xd, wd, sd, zd, out=yd)
         else:
             raise SystemExit(f"bench.py: unknown --profile kind {kind}")
         for _ in range(5):
@@ -344,17 +384,30 @@ def profile_run(torch, ops, kind, steps):
     return t
 
 
-def cpu_baseline_int4(target_s, M=16, K=4096, N=14336):
-    """Time the oracle's C port (OpenMP) on a column slice of the headline
-    case, sized to roughly target_s seconds; report GB/s of the same
-    algorithmic bytes per processed column."""
-    from oracle import cport, quant
-
+def available_cores():
+    """Cores this process may run on: the affinity mask, further limited by a
+    cgroup CPU quota when one is set (cpu.max: quota period)."""
     try:
         cores = len(os.sched_getaffinity(0))
     except AttributeError:
         cores = os.cpu_count() or 1
-    cores = min(cores, 16)
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota, period = f.read().split()[:2]
+        if quota != "max":
+            cores = max(1, min(cores, int(int(quota) // int(period))))
+    except (OSError, ValueError):
+        pass
+    return cores
+
+
+def cpu_baseline_int4(target_s, M=16, K=4096, N=14336):
+    """Time the oracle's C port (OpenMP, every available core) on a column
+    slice of the headline case, sized to roughly target_s seconds; report
+    GB/s of the same algorithmic bytes per processed column."""
+    from oracle import cport, quant
+
+    cores = available_cores()
     cport.threads(cores)
     rng = np.random.default_rng(0)
     x, packed, s, z = quant.make_int4_case(rng, M, K, N)
@@ -381,6 +434,89 @@ def cpu_baseline_int4(target_s, M=16, K=4096, N=14336):
                       f"{reps} run(s), {el:.1f}s, OpenMP threads={cores}"}
 
 
+def cpu_baseline_gemm(target_s, M=4096, K=4096, N=4096):
+    """The oracle's C port of the bf16 GEMM (f32 accumulation, OpenMP over
+    rows, every available core) on a row slice of the 4096^3 headline GEMM,
+    sized to roughly target_s seconds; TFLOP/s of the slice."""
+    from oracle import cport
+    from oracle.bf16 import f32_to_bf16_bits
+
+    cores = available_cores()
+    cport.threads(cores)
+    rng = np.random.default_rng(0)
+    sc = 1.0 / np.sqrt(np.sqrt(K))
+    a = f32_to_bf16_bits((rng.standard_normal((M, K)) * sc).astype(np.float32))
+    b = f32_to_bf16_bits((rng.standard_normal((K, N)) * sc).astype(np.float32))
+    rows = cores
+    t0 = time.perf_counter()
+    cport.gemm_bf16(a, b, m_range=(0, rows))
+    t1 = time.perf_counter() - t0
+    rows = int(min(M, max(cores, rows * target_s / max(t1, 1e-6))))
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        cport.gemm_bf16(a, b, m_range=(0, rows))
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= target_s:
+            break
+    tflops = 2.0 * rows * K * N / (el / reps) / 1e12
+    return {"value": round(tflops, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"oracle/c bf16 GEMM K={K} N={N}, rows [0,{rows}) of M={M}, {reps} run(s), {el:.1f}s, "
+                      f"OpenMP threads={cores}"}
+
+
+def bench_end_to_end(warmup=10, iters=50):
+    """The plugin path as jax drives it: compile the workload's StableHLO
+    once, then execute + await the completion event per call, with the inputs
+    already in device buffers (the reference's method, benchmarks/vs_cpu.py:
+    39-60: 1 compile, 10 warmups, 50 timed calls, median).  Reported apart
+    from kernel time: it includes the host-side launch, the output buffer
+    allocation and the completion wait."""
+    from mi355x import programs, runtime, synthetic
+
+    out = {}
+    client = runtime.Client()
+    try:
+        rng = np.random.default_rng(0)
+        x, packed, s, z = synthetic.int4_case(rng, 16, 4096, 14336)
+        a = (rng.standard_normal((4096, 4096)) / 8).astype(np.float32)
+        f32_to_bf16_bits = synthetic.bf16_bits
+        cases = {
+            "int4_g64_M16_K4096_N14336": (programs.int4_g64_matmul(16, 4096, 14336),
+                                          [(x, runtime.BF16), (packed, None), (s, runtime.BF16), (z, None)]),
+            "bf16_gemm_4096": (programs.matmul(4096, 4096, 4096),
+                               [(f32_to_bf16_bits(a), runtime.BF16), (f32_to_bf16_bits(a.T.copy()), runtime.BF16)]),
+        }
+        for name, (text, arrays) in cases.items():
+            t0 = time.perf_counter()
+            exe = client.compile(text)
+            compile_ms = (time.perf_counter() - t0) * 1e3
+            bufs = [client.buffer(arr, t) if t else client.buffer(arr) for arr, t in arrays]
+            times = []
+            for i in range(warmup + iters):
+                t0 = time.perf_counter()
+                outs, done = exe.execute(bufs)
+                done.wait()
+                dt = time.perf_counter() - t0
+                for o in outs:
+                    o.close()
+                if i == 0:
+                    first_ms = dt * 1e3
+                if i >= warmup:
+                    times.append(dt)
+            times.sort()
+            out[name] = {"compile_ms": round(compile_ms, 3), "first_call_ms": round(first_ms, 3),
+                         "median_us": round(times[len(times) // 2] * 1e6, 2), "min_us": round(times[0] * 1e6, 2),
+                         "p90_us": round(times[int(0.9 * (len(times) - 1))] * 1e6, 2), "iters": iters,
+                         "warmup": warmup}
+            for b in bufs:
+                b.close()
+            exe.close()
+    finally:
+        client.close()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -389,10 +525,10 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list of secondary workloads (int8,qmm_m,gemm,decoder,softmax,rmsnorm,argmax,chain6), "
+                    help="comma list of secondary workloads (int8,qmm_m,gemm,decoder,softmax,rmsnorm,argmax,chain6,e2e), "
                          "or 'none'")
     ap.add_argument("--profile", default="",
-                    help="int4 | gemm: eager launches of one kernel plus a 256 MiB copy calibration, "
+                    help="int4 | gemm | qgemm: eager launches of one kernel plus a 256 MiB copy calibration, "
                          "for rocprofv3 --pmc runs (prints the kernel's us/launch)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -456,12 +592,18 @@ def main():
         except Exception as e:  # the comparison is context only
             ref_tf = None
             log(f"[bench] torch.matmul comparison failed: {e}")
+        gemm_traffic, gemm_note = traffic_from_profiles("gemm_bf16_256dma_kernel_4096")
+        cpu_gemm = None
+        if not args.no_cpu:
+            cpu_gemm = cpu_baseline_gemm(args.cpu_seconds)
+            log(f"[bench] cpu gemm: {cpu_gemm['value']} TFLOP/s on {cpu_gemm['cores']} cores")
         secondary["bf16_gemm_4096"] = {
             "value": round(rg["tflops"], 2), "unit": "TFLOP/s", "us_per_call": round(rg["sec_per_call"] * 1e6, 3),
             "vendor_library_tflops": ref_tf,
             "roofline": {"bound": "mfma", "achieved": round(rg["tflops"], 2), "peak": BF16_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(rg["tflops"] / BF16_PEAK_TFLOPS, 4),
-                         "traffic": traffic_from_profiles("gemm_bf16_256dma_kernel_4096")}}
+                         "traffic": gemm_traffic, "traffic_note": gemm_note},
+            "cpu_baseline": cpu_gemm}
         rb = bench_gemm_bf16(torch, ops, max(50, args.steps // 20), 5, batch=16, M=2048, N=2048, K=128)
         gbs = rb["bytes"] / rb["sec_per_call"] / 1e9
         log(f"[bench] batched bf16 gemm: {rb['sec_per_call'] * 1e6:.1f} us, {rb['tflops']:.1f} TFLOP/s, {gbs:.0f} GB/s")
@@ -489,6 +631,15 @@ def main():
             log(f"[bench] {kind} {dt} 8192x8192: {r['sec_per_call'] * 1e6:.1f} us, {r['gbs']:.0f} GB/s")
             secondary[f"{kind}_{dt}_8192x8192"] = _hbm_entry(r["gbs"], r["sec_per_call"] * 1e6)
 
+    if want("e2e"):
+        e2e = bench_end_to_end()
+        for k, v in e2e.items():
+            log(f"[bench] end to end {k}: compile {v['compile_ms']} ms, first call {v['first_call_ms']} ms, "
+                f"median {v['median_us']} us per execute + await")
+        secondary["plugin_end_to_end"] = {
+            "what": "mkrt_compile once, then mkrt_execute + event await per call, inputs resident; "
+                    "wall clock on the host, not kernel time", **e2e}
+
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline (oracle C port) ...")
@@ -496,6 +647,7 @@ def main():
         log(f"[bench] cpu: {cpu['value']} GB/s on {cpu['cores']} cores")
 
     gbs = r4["gbs"]
+    int4_traffic, int4_note = traffic_from_profiles("int4g64_wide_kernel_M16_K4096_N14336")
     line = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -513,8 +665,8 @@ def main():
                                "(packed [2048,14336] u8, bf16 scale + u8 zero per 64 k), bf16 out",
                    "M": 16, "K": 4096, "N": 14336, "input_sets": r4["nsets"]},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_from_profiles("int4g64_wide_kernel_M16_K4096_N14336")},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": int4_traffic,
+                     "traffic_note": int4_note},
         "cpu_baseline": cpu,
         "secondary": secondary,
     }
