@@ -109,6 +109,39 @@ mkrt_error* mkrt_buffer_create_error(mkrt_client* client, int code, const char* 
  * the client's allocator. */
 void mkrt_buffer_destroy(mkrt_buffer* buf);
 
+/* PJRT_Client_BufferFromHostBuffer with byte strides (pjrt_client.cc:254-293,
+ * core/mps_client.mm:133-176): one byte stride per dimension; a non-dense
+ * host array is gathered into row-major order before the upload.  NULL
+ * strides (or num_strides 0) mean dense row-major. */
+mkrt_error* mkrt_buffer_from_host_strided(mkrt_client* client, const void* data, int type, const int64_t* dims,
+                                          int ndims, const int64_t* byte_strides, int num_strides,
+                                          mkrt_buffer** out, mkrt_event** done_with_host);
+/* PJRT_Buffer_CopyRawToHost (pjrt_buffer.cc:148-169): `size` bytes from
+ * byte `offset` of the buffer's row-major storage; waits for the producer. */
+mkrt_error* mkrt_buffer_copy_raw_to_host(mkrt_buffer* buf, void* dst, int64_t offset, int64_t size,
+                                         mkrt_event** done);
+/* PJRT_Client_CreateViewOfDeviceBuffer (pjrt_client.cc:295-332): a buffer
+ * over device memory the caller owns; on destroy or delete the runtime
+ * drains its stream and calls on_release(device_ptr, user) instead of
+ * freeing (on_release may be NULL). */
+typedef void (*mkrt_release_callback)(void* device_ptr, void* user);
+mkrt_error* mkrt_buffer_create_view(mkrt_client* client, void* device_ptr, int type, const int64_t* dims,
+                                    int ndims, mkrt_release_callback on_release, void* user, mkrt_buffer** out);
+/* PJRT_Client_CreateUninitializedBuffer (pjrt_client.cc:334-360). */
+mkrt_error* mkrt_buffer_create_uninitialized(mkrt_client* client, int type, const int64_t* dims, int ndims,
+                                             mkrt_buffer** out);
+/* PJRT_Buffer_CopyToDevice / _CopyToMemory (pjrt_buffer.cc:112-146): a new
+ * buffer holding a device-side copy, ready when the copy has run. */
+mkrt_error* mkrt_buffer_copy(mkrt_buffer* buf, mkrt_buffer** out);
+/* PJRT_Buffer_Delete / _IsDeleted (pjrt_buffer.cc:100-110): the device memory
+ * is released (after its producer), the handle stays valid; executing on or
+ * reading a deleted buffer is an error. */
+void mkrt_buffer_delete(mkrt_buffer* buf);
+int mkrt_buffer_is_deleted(const mkrt_buffer* buf);
+/* PJRT_Buffer_OpaqueDeviceMemoryDataPointer / _UnsafePointer: the device
+ * address (NULL once deleted, or for an error buffer). */
+void* mkrt_buffer_device_pointer(const mkrt_buffer* buf);
+
 /* Compile (PJRT_Client_Compile, pjrt_client.cc:178-244).  `format` "mlir"
  * takes StableHLO in MLIR text form (as jax's lowered.as_text() prints it);
  * unsupported ops fail here with a message listing them
@@ -124,6 +157,13 @@ mkrt_error* mkrt_compile_check(const char* code, int64_t code_bytes, const char*
                                int64_t plan_text_bytes, int* num_steps);
 int mkrt_executable_num_inputs(const mkrt_executable* exe);
 int mkrt_executable_num_outputs(const mkrt_executable* exe);
+/* Output signature (PJRT_Executable_OutputElementTypes / _OutputDimensions,
+ * pjrt_executable.cc:94-125) and the program text
+ * (PJRT_Executable_OptimizedProgram, :127-158). */
+int mkrt_executable_output_type(const mkrt_executable* exe, int i);
+int mkrt_executable_output_ndims(const mkrt_executable* exe, int i);
+const int64_t* mkrt_executable_output_dims(const mkrt_executable* exe, int i);
+const char* mkrt_executable_program(const mkrt_executable* exe, int64_t* size);
 /* Number of kernel launches per execute and a one-line-per-step plan
  * description ("" before the first execute) -- the plan trace. */
 int mkrt_executable_num_steps(const mkrt_executable* exe);

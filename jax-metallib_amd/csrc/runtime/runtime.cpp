@@ -250,6 +250,12 @@ struct mkrt_buffer {
   int64_t bytes = 0;
   void* data = nullptr;
   std::shared_ptr<EventState> ready;  // producer
+  // A view of memory the caller owns (CreateViewOfDeviceBuffer): released
+  // through the callback instead of the allocator.
+  bool view = false;
+  mkrt_release_callback on_release = nullptr;
+  void* release_user = nullptr;
+  bool deleted = false;  // device memory released, handle still valid
 };
 
 struct mkrt_event {
@@ -470,6 +476,7 @@ mkrt_error* mkrt_buffer_from_host(mkrt_client* c, const void* data, int type, co
 mkrt_error* mkrt_buffer_to_host(mkrt_buffer* b, void* dst, int64_t dst_bytes, mkrt_event** done) {
   if (!b) return make_error(MKRT_INVALID_ARGUMENT, "mkrt_buffer_to_host: null buffer");
   if (done) *done = nullptr;
+  if (b->deleted) return make_error(MKRT_FAILED_PRECONDITION, "mkrt_buffer_to_host: the buffer has been deleted");
   if (dst_bytes < b->bytes || (b->bytes > 0 && !dst))
     return make_error(MKRT_INVALID_ARGUMENT, "mkrt_buffer_to_host: destination holds %lld bytes, buffer has %lld",
                       (long long)dst_bytes, (long long)b->bytes);
@@ -506,17 +513,181 @@ mkrt_error* mkrt_buffer_create_error(mkrt_client* c, int code, const char* messa
   return nullptr;
 }
 
-void mkrt_buffer_destroy(mkrt_buffer* b) {
-  if (!b) return;
-  if (b->data) {
-    // Wait for the producer (core/mps_buffer.mm:656-662); later users of the
-    // memory are ordered behind every earlier reader on the stream.
+// Returns the buffer's device memory: waits for the producer
+// (core/mps_buffer.mm:656-662); later users of the memory are ordered behind
+// every earlier reader on the stream.  A view's memory goes back to its owner
+// through the release callback, after the stream has drained, since the
+// owner may reuse it at once.
+static void release_memory(mkrt_buffer* b) {
+  if (b->deleted) return;
+  b->deleted = true;
+  if (!b->data && !b->view) return;
+  {
     std::unique_lock<std::mutex> l(b->ready->mu);
     b->ready->cv.wait(l, [&] { return b->ready->ready; });
-    l.unlock();
+  }
+  if (b->view) {
+    {
+      std::lock_guard<std::mutex> g(b->client->stream_mu);
+      (void)hipStreamSynchronize(b->client->stream);
+    }
+    if (b->on_release) b->on_release(b->data, b->release_user);
+  } else {
     b->client->alloc.free(b->data);
   }
+  b->data = nullptr;
+}
+
+void mkrt_buffer_destroy(mkrt_buffer* b) {
+  if (!b) return;
+  release_memory(b);
   delete b;
+}
+
+void mkrt_buffer_delete(mkrt_buffer* b) {
+  if (b) release_memory(b);
+}
+
+int mkrt_buffer_is_deleted(const mkrt_buffer* b) { return !b || b->deleted ? 1 : 0; }
+
+void* mkrt_buffer_device_pointer(const mkrt_buffer* b) { return b && !b->deleted ? b->data : nullptr; }
+
+// Element count and bytes of a shape, rejecting negative dimensions and
+// types the runtime does not hold.
+static mkrt_error* shape_bytes(const char* fn, int type, const int64_t* dims, int ndims, int64_t* bytes) {
+  if ((ndims > 0 && !dims) || ndims < 0) return make_error(MKRT_INVALID_ARGUMENT, "%s: null dims", fn);
+  const int eb = mkrt::dtype_bytes(type);
+  if (eb == 0) return make_error(MKRT_INVALID_ARGUMENT, "%s: unsupported element type %d", fn, type);
+  int64_t n = 1;
+  for (int i = 0; i < ndims; ++i) {
+    if (dims[i] < 0) return make_error(MKRT_INVALID_ARGUMENT, "%s: negative dimension", fn);
+    if (dims[i] > 0 && n > ((int64_t)1 << 46) / dims[i]) return make_error(MKRT_INVALID_ARGUMENT, "%s: shape too large", fn);
+    n *= dims[i];
+  }
+  *bytes = n * eb;
+  return nullptr;
+}
+
+mkrt_error* mkrt_buffer_from_host_strided(mkrt_client* c, const void* data, int type, const int64_t* dims, int ndims,
+                                          const int64_t* byte_strides, int num_strides, mkrt_buffer** out,
+                                          mkrt_event** done_with_host) {
+  if (!c || !out) return make_error(MKRT_INVALID_ARGUMENT, "BufferFromHostBuffer: null argument");
+  *out = nullptr;
+  if (done_with_host) *done_with_host = nullptr;
+  if (!byte_strides || num_strides == 0)
+    return mkrt_buffer_from_host(c, data, type, dims, ndims, out, done_with_host);
+  int64_t bytes = 0;
+  if (mkrt_error* e = shape_bytes("BufferFromHostBuffer", type, dims, ndims, &bytes)) return e;
+  if (num_strides != ndims)
+    return make_error(MKRT_INVALID_ARGUMENT, "BufferFromHostBuffer: %d byte strides for %d dimensions", num_strides,
+                      ndims);
+  const int64_t eb = mkrt::dtype_bytes(type);
+  // Dense row-major already: one copy.
+  bool dense = true;
+  int64_t expect = eb;
+  for (int i = ndims - 1; i >= 0; --i) {
+    if (dims[i] > 1 && byte_strides[i] != expect) dense = false;
+    expect *= dims[i];
+  }
+  if (dense || bytes == 0) return mkrt_buffer_from_host(c, data, type, dims, ndims, out, done_with_host);
+  if (!data) return make_error(MKRT_INVALID_ARGUMENT, "BufferFromHostBuffer: null data");
+  // Gather the strided host array into a dense row-major staging copy
+  // (mps_client.mm:133-176 copies element by element the same way).
+  std::vector<unsigned char> dense_copy((size_t)bytes);
+  std::vector<int64_t> idx(ndims, 0);
+  const unsigned char* src = static_cast<const unsigned char*>(data);
+  const int64_t n = bytes / eb;
+  for (int64_t k = 0; k < n; ++k) {
+    int64_t off = 0;
+    for (int i = 0; i < ndims; ++i) off += idx[i] * byte_strides[i];
+    memcpy(dense_copy.data() + k * eb, src + off, (size_t)eb);
+    for (int i = ndims - 1; i >= 0; --i) {
+      if (++idx[i] < dims[i]) break;
+      idx[i] = 0;
+    }
+  }
+  return mkrt_buffer_from_host(c, dense_copy.data(), type, dims, ndims, out, done_with_host);
+}
+
+mkrt_error* mkrt_buffer_copy_raw_to_host(mkrt_buffer* b, void* dst, int64_t offset, int64_t size, mkrt_event** done) {
+  if (done) *done = nullptr;
+  if (!b || (!dst && size > 0)) return make_error(MKRT_INVALID_ARGUMENT, "CopyRawToHost: null argument");
+  if (b->deleted) return make_error(MKRT_FAILED_PRECONDITION, "CopyRawToHost: the buffer has been deleted");
+  if (offset < 0 || size < 0 || offset > b->bytes || size > b->bytes - offset)
+    return make_error(MKRT_INVALID_ARGUMENT, "CopyRawToHost: range [%lld, %lld) outside the buffer's %lld bytes",
+                      (long long)offset, (long long)(offset + size), (long long)b->bytes);
+  if (mkrt_error* err = await_state(b->ready, -1)) return err;
+  if (size > 0) {
+    std::lock_guard<std::mutex> g(b->client->stream_mu);
+    hipError_t e = hipMemcpyAsync(dst, static_cast<unsigned char*>(b->data) + offset, (size_t)size,
+                                  hipMemcpyDeviceToHost, b->client->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(b->client->stream);
+    if (e != hipSuccess) return hip_error("device-to-host copy", e);
+  }
+  if (done) *done = new mkrt_event{ready_state()};
+  return nullptr;
+}
+
+mkrt_error* mkrt_buffer_create_view(mkrt_client* c, void* device_ptr, int type, const int64_t* dims, int ndims,
+                                    mkrt_release_callback on_release, void* user, mkrt_buffer** out) {
+  if (!c || !out) return make_error(MKRT_INVALID_ARGUMENT, "CreateViewOfDeviceBuffer: null argument");
+  *out = nullptr;
+  if (!device_ptr) return make_error(MKRT_INVALID_ARGUMENT, "CreateViewOfDeviceBuffer: null device_buffer_ptr");
+  int64_t bytes = 0;
+  if (mkrt_error* e = shape_bytes("CreateViewOfDeviceBuffer", type, dims, ndims, &bytes)) return e;
+  mkrt_buffer* b = new_buffer(c, type, std::vector<int64_t>(dims, dims + ndims), device_ptr, bytes, ready_state());
+  b->view = true;
+  b->on_release = on_release;
+  b->release_user = user;
+  *out = b;
+  return nullptr;
+}
+
+mkrt_error* mkrt_buffer_create_uninitialized(mkrt_client* c, int type, const int64_t* dims, int ndims,
+                                             mkrt_buffer** out) {
+  if (!c || !out) return make_error(MKRT_INVALID_ARGUMENT, "CreateUninitializedBuffer: null argument");
+  *out = nullptr;
+  int64_t bytes = 0;
+  if (mkrt_error* e = shape_bytes("CreateUninitializedBuffer", type, dims, ndims, &bytes)) return e;
+  void* p = nullptr;
+  hipError_t e = c->alloc.alloc((size_t)bytes, &p);
+  if (e != hipSuccess)
+    return make_error(MKRT_RESOURCE_EXHAUSTED, "device allocation of %lld bytes: %s", (long long)bytes,
+                      hipGetErrorString(e));
+  *out = new_buffer(c, type, std::vector<int64_t>(dims, dims + ndims), p, bytes, ready_state());
+  return nullptr;
+}
+
+mkrt_error* mkrt_buffer_copy(mkrt_buffer* b, mkrt_buffer** out) {
+  if (!b || !out) return make_error(MKRT_INVALID_ARGUMENT, "CopyToDevice: null argument");
+  *out = nullptr;
+  if (b->deleted) return make_error(MKRT_FAILED_PRECONDITION, "CopyToDevice: the buffer has been deleted");
+  {
+    std::lock_guard<std::mutex> g(b->ready->mu);
+    if (b->ready->ready && b->ready->code != MKRT_OK) {
+      *out = new_buffer(b->client, b->type, b->dims, nullptr, b->bytes, ready_state(b->ready->code, b->ready->message));
+      return nullptr;
+    }
+  }
+  mkrt_client* c = b->client;
+  void* p = nullptr;
+  hipError_t e = c->alloc.alloc((size_t)b->bytes, &p);
+  if (e != hipSuccess)
+    return make_error(MKRT_RESOURCE_EXHAUSTED, "device allocation of %lld bytes: %s", (long long)b->bytes,
+                      hipGetErrorString(e));
+  auto st = std::make_shared<EventState>();
+  {
+    // The copy is queued behind the producer on the client's one stream.
+    std::lock_guard<std::mutex> g(c->stream_mu);
+    if (b->bytes > 0) e = hipMemcpyAsync(p, b->data, (size_t)b->bytes, hipMemcpyDeviceToDevice, c->stream);
+    if (e == hipSuccess) e = c->track(st);
+  }
+  if (e != hipSuccess) {
+    c->alloc.free(p);
+    return hip_error("device-to-device copy", e);
+  }
+  *out = new_buffer(c, b->type, b->dims, p, b->bytes, st);
+  return nullptr;
 }
 
 }  // extern "C"
@@ -692,6 +863,20 @@ mkrt_error* mkrt_compile_check(const char* code, int64_t code_bytes, const char*
 }
 
 int mkrt_executable_num_inputs(const mkrt_executable* x) { return x ? (int)x->plan.in_slot.size() : 0; }
+
+int mkrt_executable_output_type(const mkrt_executable* x, int i) {
+  return x && i >= 0 && i < (int)x->plan.out_type.size() ? x->plan.out_type[i].dtype : 0;
+}
+int mkrt_executable_output_ndims(const mkrt_executable* x, int i) {
+  return x && i >= 0 && i < (int)x->plan.out_type.size() ? (int)x->plan.out_type[i].dims.size() : 0;
+}
+const int64_t* mkrt_executable_output_dims(const mkrt_executable* x, int i) {
+  return x && i >= 0 && i < (int)x->plan.out_type.size() ? x->plan.out_type[i].dims.data() : nullptr;
+}
+const char* mkrt_executable_program(const mkrt_executable* x, int64_t* size) {
+  if (size) *size = x ? (int64_t)x->program.size() : 0;
+  return x ? x->program.data() : "";
+}
 int mkrt_executable_num_outputs(const mkrt_executable* x) { return x ? (int)x->plan.out_slot.size() : 0; }
 int mkrt_executable_num_steps(const mkrt_executable* x) { return x ? (int)x->plan.steps.size() : 0; }
 const char* mkrt_executable_plan(const mkrt_executable* x) { return x ? x->plan_text.c_str() : ""; }
@@ -708,6 +893,7 @@ mkrt_error* mkrt_execute(mkrt_executable* x, mkrt_buffer* const* inputs, int num
     const mkrt_buffer* b = inputs[i];
     if (!b) return make_error(MKRT_INVALID_ARGUMENT, "mkrt_execute: input %d is null", i);
     if (b->client != x->client) return make_error(MKRT_INVALID_ARGUMENT, "mkrt_execute: input %d from another client", i);
+    if (b->deleted) return make_error(MKRT_INVALID_ARGUMENT, "mkrt_execute: input %d has been deleted", i);
     if (b->type != p.in_type[i].dtype || b->dims != p.in_type[i].dims)
       return make_error(MKRT_INVALID_ARGUMENT, "mkrt_execute: input %d is %s, the program takes %s", i,
                         mkrt::TensorType{b->type, b->dims}.str().c_str(), p.in_type[i].str().c_str());

@@ -382,6 +382,70 @@ struct Builder {
   }
 };
 
+
+// Structural checks of one parsed op of the plugin's set, so that later
+// passes may index its operands, results and dimension attributes: operand
+// counts by op kind, one typed result, and every dimension number inside the
+// rank it refers to.  A malformed program is a ParseError (INVALID_ARGUMENT
+// at compile), never an out-of-bounds read.
+void validate_op(const Builder& B, const Op& op, const std::string& s) {
+  static const std::set<std::string> unary = {"negate", "abs", "exponential", "log", "log_plus_one",
+                                              "exponential_minus_one", "tanh", "rsqrt", "sqrt", "logistic",
+                                              "floor", "ceil", "convert", "not", "reshape", "broadcast_in_dim",
+                                              "transpose"};
+  static const std::set<std::string> binary = {"add", "subtract", "multiply", "divide", "maximum", "minimum",
+                                               "power", "compare", "and", "or", "dot_general", "dot",
+                                               "shift_right_logical"};
+  static const std::set<std::string> ternary = {"select", "clamp"};
+  const size_t n = op.operands.size();
+  auto bad = [&](const std::string& why) { throw ParseError(op.name + ": " + why + ": " + s); };
+  if (unary.count(op.name) && n != 1) bad("takes 1 operand, has " + std::to_string(n));
+  if (binary.count(op.name) && n != 2) bad("takes 2 operands, has " + std::to_string(n));
+  if (ternary.count(op.name) && n != 3) bad("takes 3 operands, has " + std::to_string(n));
+  if ((op.name == "constant" || op.name == "iota") && n != 0) bad("takes no operands");
+  if (op.name == "reduce" && (n < 2 || n % 2 != 0)) bad("needs input / init operand pairs");
+  if (op.name == "concatenate" && n < 1) bad("needs operands");
+  const bool known = unary.count(op.name) || binary.count(op.name) || ternary.count(op.name) ||
+                     op.name == "constant" || op.name == "iota" || op.name == "reduce" || op.name == "concatenate";
+  if (!known) return;
+  if (op.results.empty()) bad("has no result");
+  auto rank = [&](int v) { return (int64_t)B.fn.values[v].type.dims.size(); };
+  const int64_t rr = rank(op.results[0]);
+  auto in_range = [&](const std::vector<int64_t>& d, int64_t r, const char* what) {
+    std::set<int64_t> seen;
+    for (int64_t x : d)
+      if (x < 0 || x >= r || !seen.insert(x).second) bad(std::string(what) + " dimension out of range or repeated");
+  };
+  if (op.name == "dot_general") {
+    const int64_t ra = rank(op.operands[0]), rb = rank(op.operands[1]);
+    if (op.lhs_batch.size() != op.rhs_batch.size() || op.lhs_contract.size() != op.rhs_contract.size())
+      bad("batching / contracting dimension lists differ in length");
+    in_range(op.lhs_batch, ra, "lhs batching");
+    in_range(op.rhs_batch, rb, "rhs batching");
+    in_range(op.lhs_contract, ra, "lhs contracting");
+    in_range(op.rhs_contract, rb, "rhs contracting");
+    for (int64_t x : op.lhs_contract)
+      for (int64_t y : op.lhs_batch)
+        if (x == y) bad("a dimension both batching and contracting");
+    for (int64_t x : op.rhs_contract)
+      for (int64_t y : op.rhs_batch)
+        if (x == y) bad("a dimension both batching and contracting");
+  } else if (op.name == "broadcast_in_dim") {
+    if ((int64_t)op.dims.size() != rank(op.operands[0])) bad("needs one dimension per operand dimension");
+    for (int64_t x : op.dims)
+      if (x < 0 || x >= rr) bad("broadcast dimension out of range");
+  } else if (op.name == "transpose") {
+    if ((int64_t)op.dims.size() != rank(op.operands[0]) || rank(op.operands[0]) != rr) bad("permutation rank");
+    in_range(op.dims, rr, "permutation");
+  } else if (op.name == "reduce") {
+    in_range(op.dims, rank(op.operands[0]), "reduce");
+    for (size_t i = 1; i < n / 2; ++i)
+      if (rank(op.operands[i]) != rank(op.operands[0])) bad("inputs of different rank");
+  } else if (op.name == "iota" || op.name == "concatenate") {
+    if (op.dim < 0 || op.dim >= rr) bad("dimension out of range");
+  }
+}
+
 void parse_body(const RawFunc& f, const std::vector<RawFunc>& all, Builder& B, const std::vector<int>& arg_ids,
                 std::vector<int>* rets, int inline_depth);
 
@@ -551,6 +615,7 @@ void parse_statement(const std::string& stmt, const std::vector<RawFunc>& all, B
     op.results.push_back(v);
     B.names[nm] = v;
   }
+  validate_op(B, op, s);
   B.fn.ops.push_back(op);
 }
 

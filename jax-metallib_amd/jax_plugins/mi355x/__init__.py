@@ -8,10 +8,12 @@ are not read by the plugin's StableHLO front end, __init__.py:170-180), and
 call ``xla_bridge.register_plugin(name, priority=500, library_path=...,
 options={})``.
 
-The PJRT library is ``libmk_pjrt.so``: the GetPjrtApi table over the runtime
-C-ABI (include/mk_runtime.h), built against the pjrt_c_api.h of the
-installed jaxlib.  ``libmk_kernels.so`` carries the runtime itself and is
-usable without jax through ``mi355x.runtime``.
+The PJRT library is ``libmk_pjrt.so`` (built in-tree into
+jax-metallib_amd/lib by the package's build): its one exported symbol is
+GetPjrtApi, a PJRT API 0.114 table (include/pjrt_c_api_mi355x.h) over the
+runtime C-ABI (include/mk_runtime.h).  ``libmk_kernels.so`` next to it
+carries the runtime itself and is usable without jax through
+``mi355x.runtime``.
 """
 
 import os
@@ -59,8 +61,8 @@ def initialize():
     if library_path is None:
         searched = "\n".join(f"  - {p} ({d})" for p, d in _search_paths())
         raise MI355XPluginError(
-            f"Could not find {_LIB_NAME}. Searched:\n{searched}\nSet {_ENV} to its path; "
-            "it is built against the installed jaxlib's pjrt_c_api.h (see INTEGRATION.md).")
+            f"Could not find {_LIB_NAME}. Searched:\n{searched}\nSet {_ENV} to its path, or build it "
+            "(python jax-metallib_amd/build.py).")
     try:
         import jax
 

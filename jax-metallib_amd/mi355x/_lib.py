@@ -81,11 +81,24 @@ RUNTIME_SIGNATURES = {
     "mkrt_buffer_ready_event": (_p, [_p, _pp]),
     "mkrt_buffer_create_error": (_p, [_p, _i32, ctypes.c_char_p, _i32, ctypes.POINTER(_i64), _i32, _pp]),
     "mkrt_buffer_destroy": (None, [_p]),
+    "mkrt_buffer_from_host_strided": (_p, [_p, _p, _i32, ctypes.POINTER(_i64), _i32, ctypes.POINTER(_i64), _i32,
+                                           _pp, _pp]),
+    "mkrt_buffer_copy_raw_to_host": (_p, [_p, _p, _i64, _i64, _pp]),
+    "mkrt_buffer_create_view": (_p, [_p, _p, _i32, ctypes.POINTER(_i64), _i32, _p, _p, _pp]),
+    "mkrt_buffer_create_uninitialized": (_p, [_p, _i32, ctypes.POINTER(_i64), _i32, _pp]),
+    "mkrt_buffer_copy": (_p, [_p, _pp]),
+    "mkrt_buffer_delete": (None, [_p]),
+    "mkrt_buffer_is_deleted": (_i32, [_p]),
+    "mkrt_buffer_device_pointer": (_p, [_p]),
     "mkrt_compile": (_p, [_p, ctypes.c_char_p, _i64, ctypes.c_char_p, _pp]),
     "mkrt_compile_check": (_p, [ctypes.c_char_p, _i64, ctypes.c_char_p, ctypes.c_char_p, _i64,
                                 ctypes.POINTER(_i32)]),
     "mkrt_executable_num_inputs": (_i32, [_p]),
     "mkrt_executable_num_outputs": (_i32, [_p]),
+    "mkrt_executable_output_type": (_i32, [_p, _i32]),
+    "mkrt_executable_output_ndims": (_i32, [_p, _i32]),
+    "mkrt_executable_output_dims": (ctypes.POINTER(_i64), [_p, _i32]),
+    "mkrt_executable_program": (_p, [_p, ctypes.POINTER(_i64)]),
     "mkrt_executable_num_steps": (_i32, [_p]),
     "mkrt_executable_plan": (ctypes.c_char_p, [_p]),
     "mkrt_execute": (_p, [_p, _pp, _i32, _pp, _pp]),

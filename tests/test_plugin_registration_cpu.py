@@ -46,3 +46,19 @@ def test_without_jax_registration_fails_loudly(monkeypatch, tmp_path):
         with pytest.raises(plugin.MI355XPluginError) as ei:
             plugin.initialize()
     assert "xla_bridge" in str(ei.value)
+
+
+def test_in_tree_library_is_found_and_exports_the_table(monkeypatch):
+    """The in-tree build is found without the environment variable, and it is
+    a loadable PJRT plugin: GetPjrtApi returns a table of API 0.114."""
+    import ctypes
+    monkeypatch.delenv("MK_PJRT_LIBRARY_PATH", raising=False)
+    path = plugin.find_library()
+    assert path and path.endswith("libmk_pjrt.so") and os.path.isfile(path)
+    lib = ctypes.CDLL(path)
+    lib.GetPjrtApi.restype = ctypes.POINTER(ctypes.c_size_t * 5)
+    head = lib.GetPjrtApi().contents
+    # struct_size, extension_start, then PJRT_Api_Version {struct_size,
+    # extension_start, int major, int minor}: major/minor share one word.
+    assert head[0] == 1088
+    assert head[4] == (114 << 32)
