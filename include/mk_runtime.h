@@ -143,7 +143,9 @@ int mkrt_buffer_is_deleted(const mkrt_buffer* buf);
 void* mkrt_buffer_device_pointer(const mkrt_buffer* buf);
 
 /* Compile (PJRT_Client_Compile, pjrt_client.cc:178-244).  `format` "mlir"
- * takes StableHLO in MLIR text form (as jax's lowered.as_text() prints it);
+ * takes StableHLO as MLIR bytecode (the portable artifact jaxlib's PJRT
+ * client sends, vhlo dialect) or in MLIR text form (as jax's
+ * lowered.as_text() prints it);
  * unsupported ops fail here with a message listing them
  * (pjrt_client.cc:211-220).  The execution plan is built on the first
  * execute (core/mps_executable.mm:9152, BuildExecutionPlan :7627). */
@@ -155,11 +157,19 @@ mkrt_error* mkrt_compile(mkrt_client* client, const char* code, int64_t code_byt
  * (truncated to plan_text_bytes, NUL-terminated) and the step count. */
 mkrt_error* mkrt_compile_check(const char* code, int64_t code_bytes, const char* format, char* plan_text,
                                int64_t plan_text_bytes, int* num_steps);
+/* MLIR bytecode (the portable artifact compile takes) as MLIR text, as the
+ * reference's bytecodeToText does (core/stablehlo_parser.mm:597): written
+ * into text (truncated to text_bytes, NUL-terminated); text_size receives
+ * the full length.  Malformed bytes are INVALID_ARGUMENT, content outside
+ * what the reader decodes UNIMPLEMENTED. */
+mkrt_error* mkrt_bytecode_to_text(const char* data, int64_t size, char* text, int64_t text_bytes,
+                                  int64_t* text_size);
 int mkrt_executable_num_inputs(const mkrt_executable* exe);
 int mkrt_executable_num_outputs(const mkrt_executable* exe);
 /* Output signature (PJRT_Executable_OutputElementTypes / _OutputDimensions,
- * pjrt_executable.cc:94-125) and the program text
- * (PJRT_Executable_OptimizedProgram, :127-158). */
+ * pjrt_executable.cc:94-125) and the program as MLIR text
+ * (PJRT_Executable_OptimizedProgram, :127-158; a program compiled from
+ * bytecode gives its decoded text, as the reference prints its module). */
 int mkrt_executable_output_type(const mkrt_executable* exe, int i);
 int mkrt_executable_output_ndims(const mkrt_executable* exe, int i);
 const int64_t* mkrt_executable_output_dims(const mkrt_executable* exe, int i);

@@ -46,6 +46,7 @@ KERNEL_SOURCES = [
     "kernels/rowops.hip",
     "kernels/eltwise.hip",
     "runtime/shlo_parser.cpp",
+    "runtime/mlir_bytecode.cpp",
     "runtime/planner.cpp",
     "runtime/runtime.cpp",
 ]
@@ -104,8 +105,8 @@ def _build_pjrt():
 # linked with the uninstrumented device-code objects into lib/asan/.  The C
 # test harness tests/pjrt/pjrt_harness.c is built twice: with the sanitizers
 # (it drives lib/asan/ on the CPU) and without (for the GPU box).
-SAN_HOST_SOURCES = ["capi.cpp", "ew_jit.cpp", "runtime/shlo_parser.cpp", "runtime/planner.cpp",
-                    "runtime/runtime.cpp"]
+SAN_HOST_SOURCES = ["capi.cpp", "ew_jit.cpp", "runtime/shlo_parser.cpp", "runtime/mlir_bytecode.cpp",
+                    "runtime/planner.cpp", "runtime/runtime.cpp"]
 SAN_FLAGS = ["-fsanitize=address,undefined", "-fno-sanitize-recover=undefined", "-fno-omit-frame-pointer", "-g"]
 HARNESS_SOURCE = os.path.join(REPO, "tests", "pjrt", "pjrt_harness.c")
 

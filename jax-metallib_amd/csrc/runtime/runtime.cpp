@@ -32,6 +32,7 @@
 #include "../ew_jit.h"
 #include "mk_kernels.h"
 #include "mk_runtime.h"
+#include "mlir_bytecode.h"
 #include "planner.h"
 #include "shlo.h"
 
@@ -264,7 +265,8 @@ struct mkrt_event {
 
 struct mkrt_executable {
   mkrt_client* client = nullptr;
-  std::string program;      // the StableHLO text it was compiled from
+  std::string program;      // the program bytes it was compiled from (text or bytecode)
+  std::string program_text; // its MLIR text (the bytecode's decoded text)
   std::string fingerprint;  // 16 hex digits of FNV-1a 64 over program
   mkrt::Function fn;
   mkrt::Plan plan;
@@ -696,13 +698,22 @@ namespace {
 
 // Parse + plan (no device work): the compile-time support check.
 mkrt_error* compile_text(const char* code, int64_t code_bytes, const char* format, mkrt::Function* fn,
-                         mkrt::Plan* plan) {
+                         mkrt::Plan* plan, std::string* text_out = nullptr) {
   if (format && strcmp(format, "mlir") != 0)
     return make_error(MKRT_UNIMPLEMENTED, "program format '%s' is not supported (StableHLO MLIR text only)", format);
   std::string text(code, code_bytes >= 0 ? (size_t)code_bytes : strlen(code));
-  if (text.compare(0, 4, "ML\xefR") == 0)
-    return make_error(MKRT_UNIMPLEMENTED,
-                      "MLIR bytecode (VHLO portable artifact) is not read; pass the StableHLO text form");
+  if (mkrt::is_mlir_bytecode(text.data(), text.size())) {
+    // A portable artifact (pjrt_client.cc:178-244): bytecode -> MLIR text.
+    try {
+      text = mkrt::mlir_bytecode_to_text(text.data(), text.size());
+    } catch (const mkrt::BytecodeError& e) {
+      return make_error(e.kind == mkrt::BytecodeError::UNSUPPORTED ? MKRT_UNIMPLEMENTED : MKRT_INVALID_ARGUMENT,
+                        "MLIR bytecode: %s", e.what());
+    } catch (const std::exception& e) {
+      return make_error(MKRT_INVALID_ARGUMENT, "MLIR bytecode: %s", e.what());
+    }
+  }
+  if (text_out) *text_out = text;
   try {
     *fn = mkrt::parse_stablehlo_text(text);
     *plan = mkrt::build_plan(*fn);
@@ -835,7 +846,7 @@ mkrt_error* mkrt_compile(mkrt_client* c, const char* code, int64_t code_bytes, c
   *out = nullptr;
   mkrt_executable* x = new mkrt_executable;
   x->client = c;
-  if (mkrt_error* err = compile_text(code, code_bytes, format, &x->fn, &x->plan)) {
+  if (mkrt_error* err = compile_text(code, code_bytes, format, &x->fn, &x->plan, &x->program_text)) {
     delete x;
     return err;
   }
@@ -862,6 +873,27 @@ mkrt_error* mkrt_compile_check(const char* code, int64_t code_bytes, const char*
   return nullptr;
 }
 
+mkrt_error* mkrt_bytecode_to_text(const char* data, int64_t size, char* text, int64_t text_bytes,
+                                  int64_t* text_size) {
+  if (!data || size < 0) return make_error(MKRT_INVALID_ARGUMENT, "mkrt_bytecode_to_text: null or negative input");
+  std::string t;
+  try {
+    t = mkrt::mlir_bytecode_to_text(data, (size_t)size);
+  } catch (const mkrt::BytecodeError& e) {
+    return make_error(e.kind == mkrt::BytecodeError::UNSUPPORTED ? MKRT_UNIMPLEMENTED : MKRT_INVALID_ARGUMENT,
+                      "MLIR bytecode: %s", e.what());
+  } catch (const std::exception& e) {
+    return make_error(MKRT_INVALID_ARGUMENT, "MLIR bytecode: %s", e.what());
+  }
+  if (text_size) *text_size = (int64_t)t.size();
+  if (text && text_bytes > 0) {
+    const size_t n = std::min((size_t)text_bytes - 1, t.size());
+    memcpy(text, t.data(), n);
+    text[n] = 0;
+  }
+  return nullptr;
+}
+
 int mkrt_executable_num_inputs(const mkrt_executable* x) { return x ? (int)x->plan.in_slot.size() : 0; }
 
 int mkrt_executable_output_type(const mkrt_executable* x, int i) {
@@ -874,8 +906,8 @@ const int64_t* mkrt_executable_output_dims(const mkrt_executable* x, int i) {
   return x && i >= 0 && i < (int)x->plan.out_type.size() ? x->plan.out_type[i].dims.data() : nullptr;
 }
 const char* mkrt_executable_program(const mkrt_executable* x, int64_t* size) {
-  if (size) *size = x ? (int64_t)x->program.size() : 0;
-  return x ? x->program.data() : "";
+  if (size) *size = x ? (int64_t)x->program_text.size() : 0;
+  return x ? x->program_text.data() : "";
 }
 int mkrt_executable_num_outputs(const mkrt_executable* x) { return x ? (int)x->plan.out_slot.size() : 0; }
 int mkrt_executable_num_steps(const mkrt_executable* x) { return x ? (int)x->plan.steps.size() : 0; }

@@ -91,6 +91,7 @@ RUNTIME_SIGNATURES = {
     "mkrt_buffer_is_deleted": (_i32, [_p]),
     "mkrt_buffer_device_pointer": (_p, [_p]),
     "mkrt_compile": (_p, [_p, ctypes.c_char_p, _i64, ctypes.c_char_p, _pp]),
+    "mkrt_bytecode_to_text": (_p, [ctypes.c_char_p, _i64, ctypes.c_char_p, _i64, ctypes.POINTER(_i64)]),
     "mkrt_compile_check": (_p, [ctypes.c_char_p, _i64, ctypes.c_char_p, ctypes.c_char_p, _i64,
                                 ctypes.POINTER(_i32)]),
     "mkrt_executable_num_inputs": (_i32, [_p]),

@@ -61,6 +61,19 @@ def compile_check(text):
     return buf.value.decode(), n.value
 
 
+def bytecode_to_text(blob):
+    """MLIR bytecode (a StableHLO portable artifact) -> the MLIR text the
+    compile path reads (the reference's bytecodeToText,
+    core/stablehlo_parser.mm:597)."""
+    L = _lib.lib()
+    data = bytes(blob)
+    size = ctypes.c_int64(0)
+    _raise(L.mkrt_bytecode_to_text(data, len(data), None, 0, ctypes.byref(size)))
+    buf = ctypes.create_string_buffer(size.value + 1)
+    _raise(L.mkrt_bytecode_to_text(data, len(data), buf, len(buf), ctypes.byref(size)))
+    return buf.raw[:size.value].decode()
+
+
 def _take_serialized(handle):
     """bytes of an owned mkrt_serialized (freeing it)."""
     L = _lib.lib()

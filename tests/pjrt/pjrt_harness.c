@@ -455,9 +455,11 @@ static int mode_fuzz(int argc, char** argv, int is_text) {
       int c = run_copy(d, cut, is_text);
       check(c == 0 || c == 3 || c == 12, "truncation gives OK, INVALID_ARGUMENT or UNIMPLEMENTED");
     }
-    /* Byte flips over the first 4 KB (every header byte of a blob). */
+    /* Byte flips over the first 4 KB: every byte of a blob or of MLIR
+       bytecode, every 7th of a text program. */
     const long lim = n < 4096 ? n : 4096;
-    for (long k = 0; k < lim; k += (is_text ? 7 : 1), ++cases) {
+    const int every = is_text && !(n >= 4 && memcmp(d, "ML\xefR", 4) == 0) ? 7 : 1;
+    for (long k = 0; k < lim; k += every, ++cases) {
       char* m = (char*)malloc((size_t)n);
       memcpy(m, d, (size_t)n);
       m[k] ^= (char)(0x5A + (k & 0x7F));
@@ -612,7 +614,17 @@ static int mode_run(int argc, char** argv) {
   op.executable = ge.executable;
   op.program = &opp;
   ok(api->PJRT_Executable_OptimizedProgram(&op), "OptimizedProgram size query");
-  check(opp.code_size == (size_t)plen, "program size");
+  if (plen >= 4 && memcmp(prog, "ML\xefR", 4) == 0) {
+    /* Compiled from bytecode: the optimized program is its MLIR text. */
+    check(opp.code_size > 0, "program text of a bytecode program");
+    char* text = (char*)malloc(opp.code_size);
+    opp.code = text;
+    ok(api->PJRT_Executable_OptimizedProgram(&op), "OptimizedProgram text");
+    check(opp.code_size >= 6 && memcmp(text, "module", 6) == 0, "decoded program text starts with module");
+    free(text);
+  } else {
+    check(opp.code_size == (size_t)plen, "program size");
+  }
   ARGS(PJRT_LoadedExecutable_GetDeviceAssignment_Args, gd);
   gd.executable = le;
   ok(api->PJRT_LoadedExecutable_GetDeviceAssignment(&gd), "GetDeviceAssignment");

@@ -11,8 +11,8 @@
   OnReady, Set with an error, Await), the topology, argument-struct checks,
   and Client_Create failing with UNAVAILABLE when no device is visible.
 * The same harness runs the StableHLO parser and planner (mkrt_compile_check)
-  on every program the workload compiles and on every truncation and a set of
-  byte flips of each, and the serialized-executable reader
+  on every program the workload compiles, as text and as MLIR bytecode, and
+  on every truncation and a set of byte flips of each, and the serialized-executable reader
   (mkrt_serialized_inspect) on every truncation and header byte flip, all
   under the sanitizers: any out-of-bounds access, leak or undefined behaviour
   aborts the harness.
@@ -97,6 +97,23 @@ def test_parser_and_planner_under_sanitizers(tmp_path):
     for name, text in _corpus().items():
         p = tmp_path / f"{name}.mlir"
         p.write_text(text)
+        files.append(str(p))
+    out = _harness(["parse", ASAN_KERNELS] + files, timeout=1200)
+    assert "parse ok" in out
+
+
+def test_bytecode_reader_under_sanitizers(tmp_path):
+    """The MLIR-bytecode front end on portable artifacts of the corpus (and
+    builtin-dialect modules at other bytecode versions): every truncation and
+    a spread of byte flips."""
+    import _bytecode as B
+    _need(HARNESS_ASAN)
+    _need(ASAN_KERNELS)
+    files = []
+    for i, (name, text) in enumerate(sorted(_corpus().items())):
+        flavor, version = ("vhlo", 1) if i % 2 == 0 else ("builtin", 2 + i % 5)
+        p = tmp_path / f"{name}.mlirbc"
+        p.write_bytes(B.to_bytecode(text, flavor, version))
         files.append(str(p))
     out = _harness(["parse", ASAN_KERNELS] + files, timeout=1200)
     assert "parse ok" in out

@@ -14,6 +14,7 @@ import subprocess
 import numpy as np
 import pytest
 
+import _bytecode as B
 from _gpu import BF16_RTOL, F32_RTOL, assert_rel_close
 from mi355x import programs as P
 from oracle import cport, quant
@@ -90,3 +91,30 @@ def test_softmax_through_the_table(tmp_path):
     y = np.frombuffer(out.read_bytes(), dtype=np.float32).reshape(x.shape)
     from oracle import rowops
     assert_rel_close(y, rowops.softmax(x), F32_RTOL, "softmax via PJRT")
+
+
+def test_int4_headline_from_a_portable_artifact(tmp_path):
+    """The form jaxlib sends (MLIR bytecode of the vhlo dialect,
+    pjrt_client.cc:178-244) compiled and run through the table."""
+    M, K, N = 16, 4096, 14336
+    x, packed, s, z = quant.make_int4_case(np.random.default_rng(1), M, K, N)
+    prog = tmp_path / "int4.mlirbc"
+    prog.write_bytes(B.to_bytecode(P.int4_g64_matmul(M, K, N)))
+    out = tmp_path / "y.bin"
+    _run(["run", PJRT, str(prog), str(out), _spec(tmp_path, "x", x, BF16), _spec(tmp_path, "w", packed, U8),
+          _spec(tmp_path, "s", s, BF16), _spec(tmp_path, "z", z, U8)])
+    y = np.frombuffer(out.read_bytes(), dtype=np.uint16).reshape(M, N)
+    assert_rel_close(bf16_bits_to_f32(y), cport.int4_g64_matmul(x, packed, s, z), BF16_RTOL, "int4 via bytecode")
+
+
+def test_argmax_from_a_portable_artifact(tmp_path):
+    from oracle import rowops
+    x = np.random.default_rng(4).standard_normal((512, 4096)).astype(np.float32)
+    x[7, 100] = np.nan
+    x[9, :] = -np.inf
+    prog = tmp_path / "argmax.mlirbc"
+    prog.write_bytes(B.to_bytecode(P.argmax(512, 4096), "vhlo", 6))
+    out = tmp_path / "y.bin"
+    _run(["run", PJRT, str(prog), str(out), _spec(tmp_path, "x", x, F32)])
+    y = np.frombuffer(out.read_bytes(), dtype=np.int32)
+    assert np.array_equal(y, rowops.argmax(x))

@@ -255,10 +255,12 @@ def test_malformed_text_is_invalid_argument(text):
     assert ei.value.code == rt.INVALID_ARGUMENT
 
 
-def test_bytecode_is_unimplemented():
+def test_truncated_bytecode_is_invalid_argument():
+    # The bytecode magic routes to the MLIR-bytecode reader (tests in
+    # test_bytecode_cpu.py); a file cut inside its version is malformed.
     with pytest.raises(rt.PluginError) as ei:
         rt.compile_check(b"ML\xefR\x00\x01\x02")
-    assert ei.value.code == rt.UNIMPLEMENTED
+    assert ei.value.code == rt.INVALID_ARGUMENT
     assert "bytecode" in ei.value.message
 
 
