@@ -352,6 +352,17 @@ def profile_run(torch, ops, kind, steps):
 
             def fn():
                 ops.gemm_bf16(a, b, out=c)
+        elif kind == "int8":
+            from mi355x import synthetic
+            M, K, N = 16, 4096, 14336
+            rng = np.random.default_rng(0)
+            x, w8, s8 = synthetic.int8_case(rng, M, K, N)
+            xd = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).cuda()
+            wd, sd = torch.from_numpy(w8).cuda(), torch.from_numpy(s8).cuda()
+            yd = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+
+            def fn():
+                ops.int8_pc_matmul(xd, wd, sd, out=yd)
         elif kind == "qgemm":
             from mi355x import synthetic
             M, K, N = 256, 4096, 14336
@@ -528,7 +539,7 @@ def main():
                     help="comma list of secondary workloads (int8,qmm_m,gemm,decoder,softmax,rmsnorm,argmax,chain6,e2e), "
                          "or 'none'")
     ap.add_argument("--profile", default="",
-                    help="int4 | gemm | qgemm: eager launches of one kernel plus a 256 MiB copy calibration, "
+                    help="int4 | int8 | gemm | qgemm: eager launches of one kernel plus a 256 MiB copy calibration, "
                          "for rocprofv3 --pmc runs (prints the kernel's us/launch)")
     args = ap.parse_args()
     if args.gpus != 1:
