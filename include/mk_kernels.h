@@ -260,10 +260,17 @@ int mk_merge_heads_bf16(const void* o, void* out, int64_t B, int64_t H, int64_t 
  * (core/mps_executable.mm:7393-7508) and its opt-in generated fusion kernels
  * (FusionSnippet :4303-4351, GenerateFusedKernelSource :4445-4586).  The
  * executor lowers a chain of StableHLO elementwise ops to instructions over
- * 12 register slots; MK_EW_LOAD reads input `a` (n elements, or 1 element
- * broadcast), MK_EW_CONST writes `imm`, every other op reads slots a (b, c)
+ * 12 register slots; MK_EW_LOAD reads input `a` (n elements; 1 element,
+ * broadcast; or a divisor p of n elements read periodically, element i from
+ * i mod p -- a broadcast that adds leading dimensions, such as a [T, T] mask
+ * over [B, H, T, T] scores); its `b` field gives the input's element type
+ * (MK_EW_IN_DEFAULT: the program's dtype, MK_EW_IN_F32, MK_EW_IN_BF16 --
+ * the convert ops of mixed bf16 / f32 programs), MK_EW_CONST writes `imm`, every other op reads slots a (b, c)
  * and writes slot dst.  bf16 programs round each float result to bf16
- * (XLA:CPU's per-op rounding, reference ops/registry.h:273-287).
+ * (XLA:CPU's per-op rounding, reference ops/registry.h:273-287), except
+ * for ops or'ed with MK_EW_KEEP_F32: an f32-typed node of a program whose
+ * result is bf16 (f32 arithmetic between converts), computed and kept in
+ * f32 (a no-op flag in f32 programs).
  * Comparisons give 1.0 / 0.0; SELECT yields b where a != 0, else c.
  * At most 32 instructions and 4 inputs; every source slot must be written
  * before it is read (checked on the host).
@@ -280,6 +287,9 @@ enum {
   MK_EW_SELECT = 27, MK_EW_ROUND_BF16 = 28,
   MK_EW_NUM_OPS = 29
 };
+
+enum { MK_EW_IN_DEFAULT = 0, MK_EW_IN_F32 = 1, MK_EW_IN_BF16 = 2 };
+enum { MK_EW_KEEP_F32 = 64 };
 
 typedef struct mk_ew_instr {
   int32_t op;
@@ -299,6 +309,34 @@ int mk_elementwise(int dtype, const mk_ew_instr* prog, int n_instr, const void* 
  * precompiled register-program interpreter instead (same results). */
 int mk_elementwise_prepare(int dtype, const mk_ew_instr* prog, int n_instr, int n_inputs,
                            int out_slot);
+
+/* ------------------------------------------------------------------------
+ * Layout ops.
+ *
+ * mk_strided_copy replaces the reference's MPSGraph transpose / slice /
+ * broadcast_in_dim / concatenate handlers (ops/shape_ops.mm:
+ * HandleTranspose :304-333, HandleSlice :831-865, HandleBroadcastInDim
+ * :137-153, HandleConcatenate :1208-1265): for every index (i_0 .. i_{r-1})
+ * of `shape` (rank r <= 8),
+ *   dst[dst_offset + sum_d i_d dst_strides[d]] =
+ *       src[src_offset + sum_d i_d src_strides[d]]
+ * with strides and offsets in elements of `elem_bytes` (1, 2, 4 or 8)
+ * bytes.  A stride of 0 broadcasts; a concatenate is one call per operand
+ * with its destination offset.  Strides and offsets must be >= 0.
+ *
+ * mk_iota replaces HandleIota (ops/tensor_creation_ops.mm:126-148): a
+ * contiguous tensor of `shape` holding each element's index along `dim`,
+ * of element type `dtype` (PJRT_Buffer_Type numbering, below).
+ * ---------------------------------------------------------------------- */
+enum {
+  MK_IOTA_S8 = 2, MK_IOTA_S16 = 3, MK_IOTA_S32 = 4, MK_IOTA_S64 = 5, MK_IOTA_U8 = 6, MK_IOTA_U16 = 7,
+  MK_IOTA_U32 = 8, MK_IOTA_U64 = 9, MK_IOTA_F16 = 10, MK_IOTA_F32 = 11, MK_IOTA_F64 = 12, MK_IOTA_BF16 = 13
+};
+
+int mk_strided_copy(const void* src, void* dst, int elem_bytes, int rank, const int64_t* shape,
+                    const int64_t* src_strides, int64_t src_offset, const int64_t* dst_strides,
+                    int64_t dst_offset, void* stream);
+int mk_iota(void* dst, int dtype, int rank, const int64_t* shape, int dim, void* stream);
 
 #ifdef __cplusplus
 }  /* extern "C" */

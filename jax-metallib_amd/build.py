@@ -45,6 +45,7 @@ KERNEL_SOURCES = [
     "kernels/dot_general.hip",
     "kernels/rowops.hip",
     "kernels/eltwise.hip",
+    "kernels/layout.hip",
     "runtime/shlo_parser.cpp",
     "runtime/mlir_bytecode.cpp",
     "runtime/planner.cpp",

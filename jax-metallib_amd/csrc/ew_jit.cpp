@@ -185,31 +185,36 @@ std::string generate(int dtype, const mk_ew_instr* prog, int n_instr, int n_inpu
        "__device__ __forceinline__ void R2(float& a, float& b) {\n"
        "  const u32 w = P2(a, b); a = __uint_as_float(w << 16); b = __uint_as_float(w & 0xffff0000u); }\n"
        MK_EW_MATH_SRC "\n";
-  // Element loader: vector or scalar path, or a 1-element broadcast.
+  // Element loaders (bf16 and f32 inputs): vector or scalar path, a
+  // 1-element broadcast, or a periodic input (element i from i mod numel).
+  s += "__device__ __forceinline__ void ldh(const void* p, long long numel, long long idx, bool vec, long long n, float* o) {\n"
+       "  const u16* q = (const u16*)p;\n"
+       "  if (numel == 1) { float v = bf2f(q[0]); for (int e = 0; e < 8; ++e) o[e] = v; return; }\n"
+       "  if (numel != n) { idx %= numel; if (!vec) { for (int e = 0; e < 8; ++e) { long long j = idx + e;\n"
+       "      while (j >= numel) j -= numel; o[e] = bf2f(q[j]); } return; } }\n"
+       "  if (vec) { u4 w = *(const u4*)(q + idx);\n"
+       "    o[0] = bf2f(w.x & 0xffffu); o[1] = bf2f(w.x >> 16); o[2] = bf2f(w.y & 0xffffu); o[3] = bf2f(w.y >> 16);\n"
+       "    o[4] = bf2f(w.z & 0xffffu); o[5] = bf2f(w.z >> 16); o[6] = bf2f(w.w & 0xffffu); o[7] = bf2f(w.w >> 16); return; }\n"
+       "  for (int e = 0; e < 8; ++e) o[e] = (idx + e < n) ? bf2f(q[idx + e]) : 0.f;\n"
+       "}\n"
+       "__device__ __forceinline__ void ldf(const void* p, long long numel, long long idx, bool vec, long long n, float* o) {\n"
+       "  const float* q = (const float*)p;\n"
+       "  if (numel == 1) { float v = q[0]; for (int e = 0; e < 8; ++e) o[e] = v; return; }\n"
+       "  if (numel != n) { idx %= numel; if (!vec) { for (int e = 0; e < 8; ++e) { long long j = idx + e;\n"
+       "      while (j >= numel) j -= numel; o[e] = q[j]; } return; } }\n"
+       "  if (vec) { f4 a = *(const f4*)(q + idx); f4 b = *(const f4*)(q + idx + 4);\n"
+       "    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w; return; }\n"
+       "  for (int e = 0; e < 8; ++e) o[e] = (idx + e < n) ? q[idx + e] : 0.f;\n"
+       "}\n";
   if (bf) {
-    s += "__device__ __forceinline__ void ld(const void* p, long long numel, long long idx, bool vec, long long n, float* o) {\n"
-         "  const u16* q = (const u16*)p;\n"
-         "  if (numel == 1) { float v = bf2f(q[0]); for (int e = 0; e < 8; ++e) o[e] = v; return; }\n"
-         "  if (vec) { u4 w = *(const u4*)(q + idx);\n"
-         "    o[0] = bf2f(w.x & 0xffffu); o[1] = bf2f(w.x >> 16); o[2] = bf2f(w.y & 0xffffu); o[3] = bf2f(w.y >> 16);\n"
-         "    o[4] = bf2f(w.z & 0xffffu); o[5] = bf2f(w.z >> 16); o[6] = bf2f(w.w & 0xffffu); o[7] = bf2f(w.w >> 16); return; }\n"
-         "  for (int e = 0; e < 8; ++e) o[e] = (idx + e < n) ? bf2f(q[idx + e]) : 0.f;\n"
-         "}\n"
-         "__device__ __forceinline__ void st(void* p, long long idx, bool vec, long long n, const float* v) {\n"
+    s += "__device__ __forceinline__ void st(void* p, long long idx, bool vec, long long n, const float* v) {\n"
          "  u16* q = (u16*)p;\n"
          "  if (vec) { u4 w; w.x = P2(v[0], v[1]); w.y = P2(v[2], v[3]); w.z = P2(v[4], v[5]); w.w = P2(v[6], v[7]);\n"
          "    *(u4*)(q + idx) = w; return; }\n"
          "  for (int e = 0; e < 8; ++e) if (idx + e < n) q[idx + e] = (u16)P2(v[e], 0.f);\n"
          "}\n";
   } else {
-    s += "__device__ __forceinline__ void ld(const void* p, long long numel, long long idx, bool vec, long long n, float* o) {\n"
-         "  const float* q = (const float*)p;\n"
-         "  if (numel == 1) { float v = q[0]; for (int e = 0; e < 8; ++e) o[e] = v; return; }\n"
-         "  if (vec) { f4 a = *(const f4*)(q + idx); f4 b = *(const f4*)(q + idx + 4);\n"
-         "    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w; return; }\n"
-         "  for (int e = 0; e < 8; ++e) o[e] = (idx + e < n) ? q[idx + e] : 0.f;\n"
-         "}\n"
-         "__device__ __forceinline__ void st(void* p, long long idx, bool vec, long long n, const float* v) {\n"
+    s += "__device__ __forceinline__ void st(void* p, long long idx, bool vec, long long n, const float* v) {\n"
          "  float* q = (float*)p;\n"
          "  if (vec) { *(f4*)(q + idx) = f4{v[0], v[1], v[2], v[3]}; *(f4*)(q + idx + 4) = f4{v[4], v[5], v[6], v[7]}; return; }\n"
          "  for (int e = 0; e < 8; ++e) if (idx + e < n) q[idx + e] = v[e];\n"
@@ -222,12 +227,16 @@ std::string generate(int dtype, const mk_ew_instr* prog, int n_instr, int n_inpu
        "    const long long idx = c * 8;\n"
        "    const bool vec = vec_ok && idx + 8 <= n;\n";
   bool used[4] = {false, false, false, false};
+  bool half[4] = {bf, bf, bf, bf};  // input read as bf16 (else f32)
   for (int i = 0; i < n_instr; ++i)
-    if (prog[i].op == MK_EW_LOAD) used[prog[i].a] = true;
+    if (prog[i].op == MK_EW_LOAD) {
+      used[prog[i].a] = true;
+      if (prog[i].b != 0) half[prog[i].a] = prog[i].b == MK_EW_IN_BF16;
+    }
   for (int k = 0; k < n_inputs; ++k) {
     if (!used[k]) continue;
     char b[128];
-    snprintf(b, sizeof(b), "    float X%d[8]; ld(i%d, n%d, idx, vec, n, X%d);\n", k, k, k, k);
+    snprintf(b, sizeof(b), "    float X%d[8]; %s(i%d, n%d, idx, vec, n, X%d);\n", k, half[k] ? "ldh" : "ldf", k, k, k);
     s += b;
   }
   // bf16 programs evaluate two elements per iteration so that each op's
@@ -239,7 +248,9 @@ std::string generate(int dtype, const mk_ew_instr* prog, int n_instr, int n_inpu
   for (int i = 0; i < n_instr; ++i) {
     const mk_ew_instr& in = prog[i];
     const std::string v = "v" + std::to_string(i);
-    bool rnd = bf;
+    const int opc = in.op & ~MK_EW_KEEP_F32;
+    bool rnd = bf && !(in.op & MK_EW_KEEP_F32);  // rounded bf16 result (short exp / logistic forms)
+    const bool fast = rnd;
     std::string decl;
     for (int l = 0; l < lanes; ++l) {
       const std::string sfx = bf ? "_" + std::to_string(l) : std::string();
@@ -247,7 +258,7 @@ std::string generate(int dtype, const mk_ew_instr* prog, int n_instr, int n_inpu
       auto src = [&](int k) { return k >= 0 && k < 16 && !slot[k].empty() ? slot[k] + sfx : std::string(); };
       const std::string A = src(in.a), B = src(in.b), C = src(in.c);
       std::string ex;
-      switch (in.op) {
+      switch (opc) {
         case MK_EW_LOAD: ex = "X" + std::to_string(in.a) + (l ? "[e + 1]" : "[e]"); rnd = false; break;
         case MK_EW_CONST: ex = fmt_const(in.imm); rnd = false; break;
         case MK_EW_ADD: ex = A + " + " + B; break;
@@ -261,14 +272,14 @@ std::string generate(int dtype, const mk_ew_instr* prog, int n_instr, int n_inpu
         case MK_EW_ABS: ex = "fabsf(" + A + ")"; break;
         // bf16 programs round every result to 8 significant bits, so the
         // short exp form (relative error < 2^-16) suffices there.
-        case MK_EW_EXP: ex = (bf ? "mk_exp_bf(" : "mk_exp(") + A + ")"; break;
-        case MK_EW_LOG: ex = (bf ? "__logf(" : "logf(") + A + ")"; break;
+        case MK_EW_EXP: ex = (fast ? "mk_exp_bf(" : "mk_exp(") + A + ")"; break;
+        case MK_EW_LOG: ex = (fast ? "__logf(" : "logf(") + A + ")"; break;
         case MK_EW_LOG1P: ex = "mk_log1p(" + A + ")"; break;
         case MK_EW_EXPM1: ex = "expm1f(" + A + ")"; break;
         case MK_EW_TANH: ex = "tanhf(" + A + ")"; break;
         case MK_EW_RSQRT: ex = "1.0f / sqrtf(" + A + ")"; break;
         case MK_EW_SQRT: ex = "sqrtf(" + A + ")"; break;
-        case MK_EW_LOGISTIC: ex = (bf ? "mk_logistic_bf(" : "mk_logistic(") + A + ")"; break;
+        case MK_EW_LOGISTIC: ex = (fast ? "mk_logistic_bf(" : "mk_logistic(") + A + ")"; break;
         case MK_EW_FLOOR: ex = "floorf(" + A + ")"; break;
         case MK_EW_CEIL: ex = "ceilf(" + A + ")"; break;
         case MK_EW_CMP_EQ: ex = "(" + A + " == " + B + ") ? 1.f : 0.f"; rnd = false; break;

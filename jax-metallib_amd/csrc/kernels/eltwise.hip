@@ -78,6 +78,17 @@ __device__ __forceinline__ void ew_load(const void* p, int64_t numel, int64_t id
     for (int e = 0; e < kEwVec; ++e) o[e] = v;
     return;
   }
+  if (numel != n) {
+    // Periodic input (a broadcast over leading dimensions): element i is
+    // input element i mod numel.
+#pragma unroll
+    for (int e = 0; e < kEwVec; ++e) {
+      const int64_t i = idx + e;
+      const int64_t j = i % numel;
+      o[e] = i < n ? (BF16 ? bf16_to_f32(static_cast<const uint16_t*>(p)[j]) : static_cast<const float*>(p)[j]) : 0.f;
+    }
+    return;
+  }
   if (vec) {
     if (BF16) {
       const u32x4 v = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(p) + idx);
@@ -138,7 +149,9 @@ __global__ __launch_bounds__(256) void eltwise_kernel(EwArgs a) {
       const mk_ew_instr in = a.ins[i];
       f32x8 x, y = 0.f, z = 0.f, r;
       if (in.op == MK_EW_LOAD) {
-        ew_load<BF16>(a.in[in.a], a.in_numel[in.a], idx, vec, a.n, r);
+        const bool half = in.b == MK_EW_IN_BF16 || (in.b == MK_EW_IN_DEFAULT && BF16);
+        if (half) ew_load<true>(a.in[in.a], a.in_numel[in.a], idx, vec, a.n, r);
+        else ew_load<false>(a.in[in.a], a.in_numel[in.a], idx, vec, a.n, r);
         MK_EW_PUT(in.dst, r);
         continue;
       }
@@ -147,11 +160,13 @@ __global__ __launch_bounds__(256) void eltwise_kernel(EwArgs a) {
         MK_EW_PUT(in.dst, r);
         continue;
       }
+      const int opc = in.op & ~MK_EW_KEEP_F32;
       MK_EW_GET(in.a, x);
-      if ((in.op >= MK_EW_ADD && in.op <= MK_EW_POW) || (in.op >= MK_EW_CMP_EQ && in.op <= MK_EW_SELECT))
+      if ((opc >= MK_EW_ADD && opc <= MK_EW_POW) || (opc >= MK_EW_CMP_EQ && opc <= MK_EW_SELECT))
         MK_EW_GET(in.b, y);
-      if (in.op == MK_EW_SELECT) MK_EW_GET(in.c, z);
-      bool round = BF16;
+      if (opc == MK_EW_SELECT) MK_EW_GET(in.c, z);
+      // bf16 results use the short exp / logistic forms and are rounded.
+      bool round = BF16 && !(in.op & MK_EW_KEEP_F32);
       // One unrolled 8-element loop per case (the switch is wave-uniform).
 #define MK_EW_CASE(OPC, EXPR)                            \
   case OPC:                                              \
@@ -162,7 +177,7 @@ __global__ __launch_bounds__(256) void eltwise_kernel(EwArgs a) {
       r[e] = (EXPR);                                     \
     }                                                    \
     break;
-      switch (in.op) {
+      switch (opc) {
         MK_EW_CASE(MK_EW_ADD, u + v)
         MK_EW_CASE(MK_EW_SUB, u - v)
         MK_EW_CASE(MK_EW_MUL, u * v)
@@ -172,14 +187,14 @@ __global__ __launch_bounds__(256) void eltwise_kernel(EwArgs a) {
         MK_EW_CASE(MK_EW_POW, powf(u, v))
         MK_EW_CASE(MK_EW_NEG, -u)
         MK_EW_CASE(MK_EW_ABS, fabsf(u))
-        MK_EW_CASE(MK_EW_EXP, BF16 ? mk_exp_bf(u) : mk_exp(u))
+        MK_EW_CASE(MK_EW_EXP, round ? mk_exp_bf(u) : mk_exp(u))
         MK_EW_CASE(MK_EW_LOG, logf(u))
         MK_EW_CASE(MK_EW_LOG1P, mk_log1p(u))
         MK_EW_CASE(MK_EW_EXPM1, expm1f(u))
         MK_EW_CASE(MK_EW_TANH, tanhf(u))
         MK_EW_CASE(MK_EW_RSQRT, 1.0f / sqrtf(u))
         MK_EW_CASE(MK_EW_SQRT, sqrtf(u))
-        MK_EW_CASE(MK_EW_LOGISTIC, BF16 ? mk_logistic_bf(u) : mk_logistic(u))
+        MK_EW_CASE(MK_EW_LOGISTIC, round ? mk_logistic_bf(u) : mk_logistic(u))
         MK_EW_CASE(MK_EW_FLOOR, floorf(u))
         MK_EW_CASE(MK_EW_CEIL, ceilf(u))
         MK_EW_CASE(MK_EW_CMP_EQ, u == v ? 1.f : 0.f)
@@ -196,7 +211,7 @@ __global__ __launch_bounds__(256) void eltwise_kernel(EwArgs a) {
       }
 #undef MK_EW_CASE
       // Predicates and selects of already-rounded values need no rounding.
-      if (in.op >= MK_EW_CMP_EQ && in.op <= MK_EW_SELECT) round = false;
+      if (opc >= MK_EW_CMP_EQ && opc <= MK_EW_SELECT) round = false;
       if (round) {
 #pragma unroll
         for (int e = 0; e < kEwVec; ++e) r[e] = ew_bf16r(r[e]);
@@ -231,14 +246,24 @@ int validate_program(const char* fn, const mk_ew_instr* prog, int n_instr, int n
   bool defined[mk::kEwSlots] = {false};
   for (int i = 0; i < n_instr; ++i) {
     const mk_ew_instr& in = prog[i];
-    if (in.op < 0 || in.op >= MK_EW_NUM_OPS) return mkc::fail(MK_EINVAL, "%s: instr %d: bad op %d", fn, i, in.op);
+    const int opc = in.op & ~MK_EW_KEEP_F32;
+    if (in.op < 0 || opc >= MK_EW_NUM_OPS) return mkc::fail(MK_EINVAL, "%s: instr %d: bad op %d", fn, i, in.op);
+    // The flag marks float arithmetic only (loads, constants, predicates,
+    // selects and explicit roundings are never rounded anyway).
+    if ((in.op & MK_EW_KEEP_F32) && (opc < MK_EW_ADD || opc > MK_EW_CEIL))
+      return mkc::fail(MK_EINVAL, "%s: instr %d: MK_EW_KEEP_F32 on op %d", fn, i, opc);
     if (in.dst < 0 || in.dst >= mk::kEwSlots) return mkc::fail(MK_EINVAL, "%s: instr %d: bad dst", fn, i);
     int nsrc = 0;
-    if (in.op == MK_EW_LOAD) {
+    if (opc == MK_EW_LOAD) {
       if (in.a < 0 || in.a >= n_inputs) return mkc::fail(MK_EINVAL, "%s: instr %d: bad input %d", fn, i, in.a);
-    } else if (in.op != MK_EW_CONST) {
-      nsrc = (in.op == MK_EW_SELECT) ? 3 : ((in.op >= MK_EW_ADD && in.op <= MK_EW_POW) ||
-                                            (in.op >= MK_EW_CMP_EQ && in.op <= MK_EW_CMP_GE)) ? 2 : 1;
+      if (in.b != MK_EW_IN_DEFAULT && in.b != MK_EW_IN_F32 && in.b != MK_EW_IN_BF16)
+        return mkc::fail(MK_EINVAL, "%s: instr %d: bad input type %d", fn, i, in.b);
+      for (int k = 0; k < i; ++k)
+        if (prog[k].op == MK_EW_LOAD && prog[k].a == in.a && prog[k].b != in.b)
+          return mkc::fail(MK_EINVAL, "%s: input %d loaded with two element types", fn, in.a);
+    } else if (opc != MK_EW_CONST) {
+      nsrc = (opc == MK_EW_SELECT) ? 3 : ((opc >= MK_EW_ADD && opc <= MK_EW_POW) ||
+                                          (opc >= MK_EW_CMP_EQ && opc <= MK_EW_CMP_GE)) ? 2 : 1;
     }
     const int src[3] = {in.a, in.b, in.c};
     for (int k = 0; k < nsrc; ++k)
@@ -285,12 +310,13 @@ extern "C" int mk_elementwise(int dtype, const mk_ew_instr* prog, int n_instr, c
   bool aligned = ((uintptr_t)out % 16 == 0) && (n % mk::kEwVec == 0);
   for (int i = 0; i < n_inputs; ++i) {
     if (!inputs[i]) return mkc::fail(MK_EINVAL, "%s: input %d is null", fn, i);
-    if (input_numel[i] != 1 && input_numel[i] != n)
-      return mkc::fail(MK_EINVAL, "%s: input %d has %lld elements (need 1 or %lld)", fn, i,
+    if (input_numel[i] <= 0 || n % input_numel[i] != 0)
+      return mkc::fail(MK_EINVAL, "%s: input %d has %lld elements (need 1, %lld or a divisor of it)", fn, i,
                        (long long)input_numel[i], (long long)n);
     a.in[i] = inputs[i];
     a.in_numel[i] = input_numel[i];
-    if (input_numel[i] == n && (uintptr_t)inputs[i] % 16 != 0) aligned = false;
+    if (input_numel[i] != 1 && (uintptr_t)inputs[i] % 16 != 0) aligned = false;
+    if (input_numel[i] != 1 && input_numel[i] != n && input_numel[i] % mk::kEwVec != 0) aligned = false;
   }
   for (int i = n_inputs; i < mk::kEwMaxInputs; ++i) {
     a.in[i] = nullptr;

@@ -27,6 +27,7 @@
 #include <map>
 #include <set>
 #include <sstream>
+#include <stdexcept>
 
 #include "mk_runtime.h"
 
@@ -163,7 +164,20 @@ class Planner {
     if (op->name == "reshape" && numel(s) == numel(v) && type(s).dtype == type(v).dtype) return s;
     if (op->name == "convert" && type(s).dtype == type(v).dtype) return s;
     if (is_expand(*op, v) && type(s).dtype == type(v).dtype) return s;
+    if (op->name == "transpose" && trivial_perm(op->dims, type(s).dims)) return s;
     return -1;
+  }
+  // A permutation that keeps the relative order of every dimension larger
+  // than 1 leaves the element order unchanged.
+  static bool trivial_perm(const std::vector<int64_t>& perm, const std::vector<int64_t>& src_dims) {
+    int64_t last = -1;
+    for (int64_t p : perm) {
+      if (p < 0 || p >= (int64_t)src_dims.size()) return false;
+      if (src_dims[p] == 1) continue;
+      if (p < last) return false;
+      last = p;
+    }
+    return true;
   }
   int peel_view(int v) const {
     for (int s; (s = view_src(v)) >= 0;) v = s;
@@ -346,8 +360,131 @@ class Planner {
       if (try_reduce(v, &s)) return s;
     }
     if (is_elementwise(v)) return ew_root(v);
-    reject(op, op->name == "broadcast_in_dim" ? "broadcast of a non-scalar outside a fused pattern" : "");
+    {
+      int s;
+      if (try_layout(v, *op, &s)) return s;
+    }
+    reject(op, "");
     return dummy(v);
+  }
+
+  // ---- layout ops ------------------------------------------------------------
+  static std::vector<int64_t> row_strides(const std::vector<int64_t>& d) {
+    std::vector<int64_t> st(d.size(), 1);
+    for (int i = (int)d.size() - 2; i >= 0; --i) st[i] = st[i + 1] * d[i + 1];
+    return st;
+  }
+  static std::string dims_str(const std::vector<int64_t>& d) {
+    std::string r = "[";
+    for (size_t i = 0; i < d.size(); ++i) r += (i ? "," : "") + std::to_string(d[i]);
+    return r + "]";
+  }
+
+  void layout_step(int src_slot, int dst_slot, int eb, const std::vector<int64_t>& shape,
+                   const std::vector<int64_t>& ss, int64_t so, const std::vector<int64_t>& ds, int64_t dof,
+                   const std::string& desc) {
+    // The kernel cannot see buffer sizes: every element the copy touches
+    // must lie inside its two slots.
+    int64_t smax = so, dmax = dof;
+    bool empty = false;
+    for (size_t k = 0; k < shape.size(); ++k) {
+      empty = empty || shape[k] == 0;
+      smax += (shape[k] - 1) * ss[k];
+      dmax += (shape[k] - 1) * ds[k];
+    }
+    if (!empty && ((smax + 1) * eb > plan_.slots[src_slot].bytes || (dmax + 1) * eb > plan_.slots[dst_slot].bytes))
+      throw std::logic_error("layout step outside its buffers: " + desc);
+    Step st;
+    st.kind = ST_LAYOUT;
+    st.in = {src_slot};
+    st.out = dst_slot;
+    st.elem_bytes = eb;
+    st.shape = shape;
+    st.src_st = ss;
+    st.src_off = so;
+    st.dst_st = ds;
+    st.dst_off = dof;
+    st.desc = desc;
+    plan_.steps.push_back(st);
+  }
+
+  // transpose, slice, broadcast_in_dim, concatenate (one strided copy per
+  // operand) and iota, as kernel steps.
+  bool try_layout(int v, const Op& op, int* out) {
+    const TensorType& t = type(v);
+    const int eb = dtype_bytes(t.dtype);
+    const int rank = (int)t.dims.size();
+    if (eb == 0 || rank > 8) return false;
+    const std::vector<int64_t> ods = row_strides(t.dims);
+    const std::string ty = std::string(dtype_name(t.dtype)) + " " + dims_str(t.dims);
+    if (op.name == "iota") {
+      if (rank == 0 || op.dim < 0 || op.dim >= rank || !(is_int_type(t.dtype) || is_float(t.dtype))) return false;
+      Step st;
+      st.kind = ST_IOTA;
+      st.shape = t.dims;
+      st.iota_dim = (int)op.dim;
+      st.type_out = t.dtype;
+      st.out = temp_for(v);
+      st.desc = "iota " + ty + " dim=" + std::to_string(op.dim);
+      plan_.steps.push_back(st);
+      *out = st.out;
+      return true;
+    }
+    if (op.operands.empty()) return false;
+    if (op.name == "concatenate") {
+      if (op.dim < 0 || op.dim >= rank) return false;
+      std::vector<int> srcs;
+      for (int x : op.operands) {
+        if (type(x).dtype != t.dtype || (int)type(x).dims.size() != rank) return false;
+        srcs.push_back(need(x));
+      }
+      const int o = temp_for(v);
+      int64_t off = 0;
+      for (size_t i = 0; i < op.operands.size(); ++i) {
+        const int x = op.operands[i];
+        layout_step(srcs[i], o, eb, type(x).dims, row_strides(type(x).dims), 0, ods, off * ods[op.dim],
+                    "concatenate part " + std::to_string(i) + " " + dtype_name(t.dtype) + " " +
+                        dims_str(type(x).dims) + " -> " + dims_str(t.dims) + " dim=" + std::to_string(op.dim));
+        off += type(x).dims[op.dim];
+      }
+      *out = o;
+      return true;
+    }
+    const int x = op.operands[0];
+    if (type(x).dtype != t.dtype) return false;
+    const std::vector<int64_t>& xd = type(x).dims;
+    const std::vector<int64_t> xs = row_strides(xd);
+    std::vector<int64_t> ss(rank, 0);
+    int64_t so = 0;
+    std::string desc;
+    if (op.name == "transpose") {
+      if ((int)op.dims.size() != rank || (int)xd.size() != rank) return false;
+      for (int i = 0; i < rank; ++i) ss[i] = xs[op.dims[i]];
+      desc = "transpose " + ty + " perm=" + dims_str(op.dims);
+    } else if (op.name == "slice") {
+      if ((int)xd.size() != rank || (int)op.slice_start.size() != rank) return false;
+      for (int i = 0; i < rank; ++i) {
+        ss[i] = xs[i] * op.slice_stride[i];
+        so += op.slice_start[i] * xs[i];
+      }
+      desc = "slice " + dims_str(xd) + " -> " + ty;
+    } else if (op.name == "broadcast_in_dim") {
+      if (op.dims.size() != xd.size()) return false;
+      for (size_t j = 0; j < xd.size(); ++j) {
+        const int64_t i = op.dims[j];
+        if (i < 0 || i >= rank) return false;
+        if (xd[j] == t.dims[i]) ss[i] = xs[j];
+        else if (xd[j] != 1) return false;
+      }
+      desc = "broadcast " + dims_str(xd) + " -> " + ty;
+    } else {
+      return false;
+    }
+    const int src = need(x);
+    const int o = temp_for(v);
+    layout_step(src, o, eb, t.dims, ss, so, ods, 0, desc);
+    *out = o;
+    return true;
   }
 
   int dummy(int v) { return temp_for(v); }
@@ -533,6 +670,44 @@ class Planner {
     }
     const bool fast = !(general && gd.transposed) && dot_shape(op, &d) && fast_types && d.K > 0 &&
                       d.K % 8 == 0 && d.N % 8 == 0 && numel(v) == d.batch * d.M * d.N;
+    if (!fast && general && fast_types && gd.K > 0 && gd.K % 8 == 0 && gd.N % 8 == 0 &&
+        numel(v) == gd.batch * gd.M * gd.N && gd.M * gd.N * gd.K >= (int64_t(1) << 18)) {
+      // Operands in another layout (a transposed operand, e.g. q @ k^T written
+      // as einsum 'bhtd,bhsd->bhts') are copied to [batch, M, K] and
+      // [batch, K, N] first, then multiplied by the tiled GEMM.
+      const int eb = dtype_bytes(ta);
+      auto canon = [&](int src, const int64_t* st, int64_t R, int64_t C, const char* what) {
+        const int slot = need(src);
+        if (st[2] == 1 && st[1] == C && (gd.batch == 1 || st[0] == R * C)) return slot;
+        const std::vector<int64_t> shape = {gd.batch, R, C};
+        const int o = new_slot(Slot{SLOT_TEMP, gd.batch * R * C * eb, -1, {}});
+        layout_step(slot, o, eb, shape, {st[0], st[1], st[2]}, 0, row_strides(shape), 0,
+                    std::string("gemm operand ") + what + " to " + dims_str(shape));
+        return o;
+      };
+      Step st;
+      st.in = {canon(gd.a, gd.sa, gd.M, gd.K, "a"), canon(gd.b, gd.sb, gd.K, gd.N, "b")};
+      if (ta == DT_F32) {
+        st.kind = ST_GEMM_F32;
+        st.dt = MK_DT_F32;
+      } else {
+        st.kind = ST_GEMM_BF16;
+        st.dt = MK_DT_BF16;
+        st.out_f32 = tr == DT_F32;
+      }
+      st.batch = gd.batch;
+      st.M = gd.M;
+      st.N = gd.N;
+      st.K = gd.K;
+      st.out = temp_for(v);
+      std::ostringstream ds;
+      ds << (st.kind == ST_GEMM_F32 ? "gemm_f32" : "gemm_bf16") << " batch=" << gd.batch << " M=" << gd.M
+         << " N=" << gd.N << " K=" << gd.K << " -> " << dtype_name(tr);
+      st.desc = ds.str();
+      plan_.steps.push_back(st);
+      *out = st.out;
+      return true;
+    }
     if (!fast) {
       if (!general) {
         reject(&op, "dimension numbers other than one contracting dimension with leading batch dimensions");
@@ -971,6 +1146,7 @@ class Planner {
     std::vector<mk_ew_instr> prog;
     std::map<int, int> reg;  // value -> virtual register (instruction index)
     std::vector<int> loads;  // value ids of inputs
+    std::vector<int> load_slot;  // the input's slot when it is a folded constant, else -1
     std::vector<int64_t> load_numel;
     std::set<int> force;     // values to load instead of inlining
     std::string fail;        // reason the value cannot be expressed
@@ -992,21 +1168,199 @@ class Planner {
   }
 
   int ew_load(EwCtx& c, int u) {
+    // A broadcast that only adds leading dimensions repeats its operand:
+    // load the operand periodically instead of materialising it.
+    const int p = periodic_src(u);
+    if (p >= 0 && numel(p) > 1) u = p;
     const int64_t ne = numel(u);
-    if (ne != c.n && ne != 1) {
+    if (ne != c.n && ne != 1 && (ne <= 0 || c.n % ne != 0)) {
       c.fail = "broadcast of a non-scalar " + type(u).str() + " into an elementwise op";
       return -1;
     }
-    if (type(u).dtype != c.dt) {
-      c.fail = std::string("elementwise input of type ") + dtype_name(type(u).dtype) + " in a " +
-               dtype_name(c.dt) + " program";
-      return -1;
+    int slot = -1;
+    int elem = MK_EW_IN_DEFAULT;
+    const int ut = type(u).dtype;
+    if (ut != c.dt && (ut == DT_F32 || ut == DT_BF16)) {
+      elem = ut == DT_F32 ? MK_EW_IN_F32 : MK_EW_IN_BF16;  // the other float type, widened exactly
+    } else if (ut != c.dt) {
+      // Index-only values (iota / constant masks) are evaluated here and
+      // loaded as constants of the program's type.
+      slot = fold_const_slot(u, c.dt);
+      if (slot < 0) {
+        c.fail = std::string("elementwise input of type ") + dtype_name(ut) + " in a " + dtype_name(c.dt) +
+                 " program";
+        return -1;
+      }
     }
     for (size_t i = 0; i < c.loads.size(); ++i)
-      if (c.loads[i] == u) return ew_emit(c, MK_EW_LOAD, (int)i);
+      if (c.loads[i] == u && c.load_slot[i] == slot) return ew_emit(c, MK_EW_LOAD, (int)i, elem);
     c.loads.push_back(u);
+    c.load_slot.push_back(slot);
     c.load_numel.push_back(ne);
-    return ew_emit(c, MK_EW_LOAD, (int)c.loads.size() - 1);
+    return ew_emit(c, MK_EW_LOAD, (int)c.loads.size() - 1, elem);
+  }
+
+  // v = broadcast_in_dim(x) whose elements repeat x's in order: x's
+  // dimensions larger than 1 map, with equal sizes, onto a trailing block of
+  // v's.  Returns x or -1.
+  int periodic_src(int v) const {
+    const Op* op = def(v);
+    if (!op || op->name != "broadcast_in_dim" || op->operands.empty() || !monotonic(op->dims)) return -1;
+    const int x = op->operands[0];
+    const std::vector<int64_t>& xd = type(x).dims;
+    const std::vector<int64_t>& vd = type(v).dims;
+    if (op->dims.size() != xd.size() || type(x).dtype != type(v).dtype) return -1;
+    int first = (int)vd.size();
+    for (size_t j = 0; j < xd.size(); ++j)
+      if (xd[j] != 1) {
+        first = (int)op->dims[j];
+        break;
+      }
+    for (int i = first; i < (int)vd.size(); ++i) {
+      int j = -1;
+      for (size_t k = 0; k < op->dims.size(); ++k)
+        if (op->dims[k] == i) j = (int)k;
+      if (j < 0 || xd[j] != vd[i]) return -1;
+    }
+    return x;
+  }
+
+  // ---- compile-time folding of index values ------------------------------------
+  // Values computed only from iota and constants -- masks such as the causal
+  // lower triangle, jnp.arange(T)[:, None] >= jnp.arange(T)[None, :] -- are
+  // evaluated on the host (row-major, as doubles) up to kFoldMax elements.
+  static constexpr int64_t kFoldMax = int64_t(1) << 24;
+  std::map<int, std::vector<double>> folded_;
+  std::map<std::pair<int, int>, int> folded_slot_;
+
+  std::set<int> unfoldable_;
+
+  bool fold(int v, int depth = 0) {
+    if (folded_.count(v)) return true;
+    if (unfoldable_.count(v)) return false;
+    const bool ok = fold_uncached(v, depth);
+    if (!ok) unfoldable_.insert(v);
+    return ok;
+  }
+
+  bool fold_uncached(int v, int depth) {
+    if (depth > 64 || numel(v) > kFoldMax) return false;
+    const Op* op = def(v);
+    if (!op) return false;
+    static const std::set<std::string> foldable = {"constant", "iota", "reshape", "convert", "broadcast_in_dim",
+                                                   "transpose", "compare", "select", "and", "or", "not", "add",
+                                                   "subtract", "multiply", "maximum", "minimum", "negate"};
+    if (!foldable.count(op->name)) return false;
+    const TensorType& t = type(v);
+    const int64_t n = numel(v);
+    const std::vector<int64_t>& d = t.dims;
+    for (int o : op->operands)
+      if (!fold(o, depth + 1)) return false;
+    std::vector<double> out((size_t)n);
+    auto in = [&](int k) -> const std::vector<double>& { return folded_.at(op->operands[k]); };
+    const std::string& nm = op->name;
+    const int dt = t.dtype;
+    auto cast = [&](double x) {
+      if (dt == DT_PRED) return x != 0 ? 1.0 : 0.0;
+      if (is_int_type(dt)) return ::trunc(x);
+      return round_to(x, dt);
+    };
+    if (nm == "constant") {
+      if (op->const_values.empty()) return false;
+      for (int64_t i = 0; i < n; ++i)
+        out[i] = cast(op->const_values.size() == 1 ? op->const_values[0]
+                      : (size_t)i < op->const_values.size() ? op->const_values[i] : 0.0);
+    } else if (nm == "iota") {
+      if (op->dim < 0 || op->dim >= (int64_t)d.size()) return false;
+      int64_t inner = 1;
+      for (size_t k = op->dim + 1; k < d.size(); ++k) inner *= d[k];
+      for (int64_t i = 0; i < n; ++i) out[i] = cast((double)((i / inner) % d[op->dim]));
+    } else if (nm == "reshape" || nm == "convert") {
+      const std::vector<double>& a = in(0);
+      if ((int64_t)a.size() != n) return false;
+      for (int64_t i = 0; i < n; ++i) out[i] = cast(a[i]);
+    } else if (nm == "broadcast_in_dim" || nm == "transpose") {
+      const std::vector<double>& a = in(0);
+      const std::vector<int64_t>& xd = type(op->operands[0]).dims;
+      const std::vector<int64_t> xs = row_strides(xd);
+      std::vector<int64_t> st(d.size(), 0);
+      if (nm == "transpose") {
+        if (op->dims.size() != d.size()) return false;
+        for (size_t i = 0; i < d.size(); ++i) st[i] = xs[op->dims[i]];
+      } else {
+        if (op->dims.size() != xd.size()) return false;
+        for (size_t j = 0; j < xd.size(); ++j)
+          if (xd[j] != 1) st[op->dims[j]] = xs[j];
+      }
+      for (int64_t i = 0; i < n; ++i) {
+        int64_t r = i, src = 0;
+        for (int k = (int)d.size() - 1; k >= 0; --k) {
+          src += (r % d[k]) * st[k];
+          r /= d[k];
+        }
+        out[i] = a[src];
+      }
+    } else if (nm == "compare") {
+      const std::vector<double>&a = in(0), &b = in(1);
+      const std::string& c = op->compare_dir;
+      for (int64_t i = 0; i < n; ++i) {
+        const double x = a[i], y = b[i];
+        out[i] = (c == "EQ" ? x == y : c == "NE" ? x != y : c == "LT" ? x < y : c == "LE" ? x <= y
+                  : c == "GT" ? x > y : x >= y) ? 1.0 : 0.0;
+      }
+      if (c != "EQ" && c != "NE" && c != "LT" && c != "LE" && c != "GT" && c != "GE") return false;
+    } else if (nm == "select") {
+      const std::vector<double>&p = in(0), &a = in(1), &b = in(2);
+      for (int64_t i = 0; i < n; ++i) out[i] = p[i] != 0 ? a[i] : b[i];
+    } else if ((nm == "and" || nm == "or") && dt == DT_PRED) {
+      const std::vector<double>&a = in(0), &b = in(1);
+      for (int64_t i = 0; i < n; ++i) out[i] = nm == "and" ? (a[i] != 0 && b[i] != 0) : (a[i] != 0 || b[i] != 0);
+    } else if (nm == "not" && dt == DT_PRED) {
+      const std::vector<double>& a = in(0);
+      for (int64_t i = 0; i < n; ++i) out[i] = a[i] != 0 ? 0.0 : 1.0;
+    } else if ((nm == "add" || nm == "subtract" || nm == "multiply" || nm == "maximum" || nm == "minimum") &&
+               is_int_type(dt)) {
+      const std::vector<double>&a = in(0), &b = in(1);
+      for (int64_t i = 0; i < n; ++i)
+        out[i] = nm == "add" ? a[i] + b[i] : nm == "subtract" ? a[i] - b[i] : nm == "multiply" ? a[i] * b[i]
+                 : nm == "maximum" ? std::max(a[i], b[i]) : std::min(a[i], b[i]);
+    } else if (nm == "negate" && is_int_type(dt)) {
+      const std::vector<double>& a = in(0);
+      for (int64_t i = 0; i < n; ++i) out[i] = -a[i];
+    } else {
+      return false;
+    }
+    folded_[v] = std::move(out);
+    return true;
+  }
+
+  // The folded values of v as a constant slot of type dt (F32 or BF16), or -1.
+  int fold_const_slot(int v, int dt) {
+    const auto key = std::make_pair(v, dt);
+    auto it = folded_slot_.find(key);
+    if (it != folded_slot_.end()) return it->second;
+    if (!(type(v).dtype == DT_PRED || is_int_type(type(v).dtype)) || !fold(v)) return -1;
+    const std::vector<double>& a = folded_.at(v);
+    Slot s;
+    s.kind = SLOT_CONST;
+    const int eb = dt == DT_F32 ? 4 : 2;
+    s.bytes = (int64_t)a.size() * eb;
+    s.data.resize((size_t)s.bytes);
+    for (size_t i = 0; i < a.size(); ++i) {
+      if (dt == DT_F32) {
+        const float f = (float)a[i];
+        memcpy(s.data.data() + 4 * i, &f, 4);
+      } else {
+        const float f = to_bf16_value(a[i]);
+        uint32_t u;
+        memcpy(&u, &f, 4);
+        const uint16_t h = (uint16_t)(u >> 16);
+        memcpy(s.data.data() + 2 * i, &h, 2);
+      }
+    }
+    const int slot = new_slot(s);
+    folded_slot_[key] = slot;
+    return slot;
   }
 
   // Returns the virtual register holding u; `size` accumulates the number
@@ -1019,8 +1373,8 @@ class Planner {
     if (r < 0) return -1;
     const int sz = (int)c.prog.size() - before;
     *size += sz;
-    if (!root && sz > c.split_size && is_elementwise(u) && numel(u) == c.n && type(u).dtype == c.dt &&
-        !c.force.count(u)) {
+    if (!root && sz > c.split_size && is_elementwise(u) && numel(u) == c.n &&
+        (type(u).dtype == DT_F32 || type(u).dtype == DT_BF16) && !c.force.count(u)) {
       c.split_size = sz;
       c.split_hint = u;
     }
@@ -1039,17 +1393,23 @@ class Planner {
       return ew_value(c, vs, false, &dummy);
     }
     const Op* op = def(u);
+    if (op && !root && (t.dtype == DT_PRED || is_int_type(t.dtype)) && numel(u) <= kFoldMax && fold(u))
+      return ew_load(c, u);  // an index-only mask: a folded constant
     if (!op || (!root && c.force.count(u)) || !is_elementwise(u)) return ew_load(c, u);
+    // A convert of a product or reduction is that kernel's output type (the
+    // GEMM, dequant-matmul and reduce kernels write bf16 themselves): load it
+    // rather than pull the f32 value into this program.
+    if (!root && op->name == "convert" && (is(peel_view(op->operands[0]), "dot_general") ||
+                                          is(peel_view(op->operands[0]), "dot") ||
+                                          is(peel_view(op->operands[0]), "reduce")))
+      return ew_load(c, u);
     if (op->name == "broadcast_in_dim") return ew_load(c, op->operands[0]);  // scalar broadcast
-    // Per-node type rules: bf16 programs hold only bf16 (and predicate)
-    // values; f32 programs round bf16-typed nodes explicitly.
+    // Per-node type rules: f32 programs round bf16-typed nodes explicitly
+    // (MK_EW_ROUND_BF16); bf16 programs mark f32-typed arithmetic
+    // MK_EW_KEEP_F32 so that it is neither rounded nor shortened.
     const int dt = t.dtype;
     if (dt != DT_PRED && dt != DT_F32 && dt != DT_BF16) {
       c.fail = std::string("elementwise ") + op->name + " on " + dtype_name(dt);
-      return -1;
-    }
-    if (c.dt == DT_BF16 && dt == DT_F32) {
-      c.fail = std::string("f32 ") + op->name + " inside a bf16 elementwise chain";
       return -1;
     }
     std::vector<int> r;
@@ -1063,6 +1423,7 @@ class Planner {
       if (x < 0) return -1;
       r.push_back(x);
     }
+    const size_t first_new = c.prog.size();  // this node's own instructions start here
     int res = -1;
     const std::string& n = op->name;
     static const std::map<std::string, int> un = {
@@ -1122,8 +1483,9 @@ class Planner {
         const int z = ew_emit(c, MK_EW_CONST, 0, 0, 0, 0.f);
         res = ew_emit(c, MK_EW_CMP_NE, r[0], z);
       } else if (st == DT_PRED || st == DT_F32 || st == DT_BF16) {
+        // Widening (bf16 / i1 -> f32) is exact; f32 -> bf16 rounds.
         res = r[0];
-        if (dt == DT_BF16 && st == DT_F32 && c.dt == DT_F32) res = ew_emit(c, MK_EW_ROUND_BF16, r[0]);
+        if (dt == DT_BF16 && st == DT_F32) res = ew_emit(c, MK_EW_ROUND_BF16, r[0]);
         return res;
       } else {
         c.fail = std::string("convert ") + dtype_name(st) + " -> " + dtype_name(dt);
@@ -1135,11 +1497,15 @@ class Planner {
     }
     // bf16-typed results inside an f32 program round like XLA's bf16 ops.
     if (c.dt == DT_F32 && dt == DT_BF16) res = ew_emit(c, MK_EW_ROUND_BF16, res);
+    if (c.dt == DT_BF16 && dt == DT_F32)
+      for (size_t i = first_new; i < c.prog.size(); ++i)
+        if (c.prog[i].op >= MK_EW_ADD && c.prog[i].op <= MK_EW_CEIL) c.prog[i].op |= MK_EW_KEEP_F32;
     return res;
   }
 
   // Number of register operands an instruction reads.
   static int n_src(int op) {
+    op &= ~MK_EW_KEEP_F32;
     if (op == MK_EW_LOAD || op == MK_EW_CONST) return 0;
     if (op == MK_EW_SELECT) return 3;
     if ((op >= MK_EW_ADD && op <= MK_EW_POW) || (op >= MK_EW_CMP_EQ && op <= MK_EW_CMP_GE)) return 2;
@@ -1217,7 +1583,7 @@ class Planner {
       Step st;
       st.kind = ST_EW;
       st.dt = mk_dt(dt);
-      for (int u : c.loads) st.in.push_back(need(u));
+      for (size_t i = 0; i < c.loads.size(); ++i) st.in.push_back(c.load_slot[i] >= 0 ? c.load_slot[i] : need(c.loads[i]));
       st.in_numel = c.load_numel;
       st.prog = prog;
       st.prog_out = out_slot;

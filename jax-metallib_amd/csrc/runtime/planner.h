@@ -39,7 +39,9 @@ enum StepKind {
   ST_EW,
   ST_COPY,
   ST_ZERO,
-  ST_DOT_GENERIC
+  ST_DOT_GENERIC,
+  ST_LAYOUT,  // strided copy (transpose, slice, broadcast, one concatenate operand)
+  ST_IOTA
 };
 
 struct Step {
@@ -59,6 +61,12 @@ struct Step {
   int64_t bytes = 0;  // copy / zero size
   int type_a = 0, type_out = 0;            // ST_DOT_GENERIC: PJRT element types
   int64_t sa[3] = {0, 0, 0}, sb[3] = {0, 0, 0};  // ST_DOT_GENERIC strides (batch, m, k) / (batch, k, n)
+  // ST_LAYOUT: dst[dst_off + sum i_d dst_st[d]] = src[src_off + sum i_d src_st[d]]
+  // over `shape`, elements of elem_bytes; ST_IOTA: `shape`, iota_dim, type_out.
+  std::vector<int64_t> shape, src_st, dst_st;
+  int64_t src_off = 0, dst_off = 0;
+  int elem_bytes = 0;
+  int iota_dim = 0;
   std::string desc;
 };
 

@@ -386,6 +386,11 @@ int run_step(const mkrt::Step& st, const std::vector<void*>& mem, void* ws, int6
     case mkrt::ST_ZERO:
       if (st.bytes == 0) return MK_OK;
       return hipMemsetAsync(out, 0, (size_t)st.bytes, s) == hipSuccess ? MK_OK : MK_ELAUNCH;
+    case mkrt::ST_LAYOUT:
+      return mk_strided_copy(in(0), out, st.elem_bytes, (int)st.shape.size(), st.shape.data(), st.src_st.data(),
+                             st.src_off, st.dst_st.data(), st.dst_off, s);
+    case mkrt::ST_IOTA:
+      return mk_iota(out, st.type_out, (int)st.shape.size(), st.shape.data(), st.iota_dim, s);
   }
   return MK_EUNSUPPORTED;
 }

@@ -58,6 +58,7 @@ struct Op {
   // Attributes used by the planner.
   std::vector<int64_t> dims;  // broadcast_in_dim dims, reduce dimensions, transpose permutation
   int64_t dim = -1;           // iota / concatenate dimension
+  std::vector<int64_t> slice_start, slice_limit, slice_stride;  // slice
   std::vector<int64_t> lhs_batch, rhs_batch, lhs_contract, rhs_contract;
   std::string compare_dir;     // EQ NE LT LE GT GE
   std::string reduce_body;     // reduce: "add" "maximum" "minimum" "multiply" ... or "argmax" "argmin"

@@ -392,7 +392,7 @@ void validate_op(const Builder& B, const Op& op, const std::string& s) {
   static const std::set<std::string> unary = {"negate", "abs", "exponential", "log", "log_plus_one",
                                               "exponential_minus_one", "tanh", "rsqrt", "sqrt", "logistic",
                                               "floor", "ceil", "convert", "not", "reshape", "broadcast_in_dim",
-                                              "transpose"};
+                                              "transpose", "slice"};
   static const std::set<std::string> binary = {"add", "subtract", "multiply", "divide", "maximum", "minimum",
                                                "power", "compare", "and", "or", "dot_general", "dot",
                                                "shift_right_logical"};
@@ -443,6 +443,21 @@ void validate_op(const Builder& B, const Op& op, const std::string& s) {
       if (rank(op.operands[i]) != rank(op.operands[0])) bad("inputs of different rank");
   } else if (op.name == "iota" || op.name == "concatenate") {
     if (op.dim < 0 || op.dim >= rr) bad("dimension out of range");
+    if (op.name == "concatenate") {
+      for (int v : op.operands)
+        if (rank(v) != rr) bad("operands of different rank");
+    }
+  } else if (op.name == "slice") {
+    const TensorType& in = B.fn.values[op.operands[0]].type;
+    const TensorType& out = B.fn.values[op.results[0]].type;
+    const size_t r = in.dims.size();
+    if (op.slice_start.size() != r || op.slice_limit.size() != r || op.slice_stride.size() != r || out.dims.size() != r)
+      bad("slice ranges do not match the rank");
+    for (size_t i = 0; i < r; ++i) {
+      const int64_t a = op.slice_start[i], b = op.slice_limit[i], st = op.slice_stride[i];
+      if (a < 0 || b < a || b > in.dims[i] || st < 1) bad("slice range out of bounds");
+      if (out.dims[i] != (b - a + st - 1) / st) bad("slice result shape");
+    }
   }
 }
 
@@ -558,7 +573,7 @@ void parse_statement(const std::string& stmt, const std::vector<RawFunc>& all, B
       "add", "subtract", "multiply", "divide", "maximum", "minimum", "power", "compare", "and", "or", "not",
       "negate", "abs", "exponential", "log", "log_plus_one", "exponential_minus_one", "tanh", "rsqrt", "sqrt",
       "logistic", "floor", "ceil", "convert", "select", "clamp", "reshape", "broadcast_in_dim", "transpose",
-      "dot_general", "dot", "reduce", "constant", "iota", "concatenate", "shift_right_logical"};
+      "dot_general", "dot", "reduce", "constant", "iota", "concatenate", "shift_right_logical", "slice"};
   for (const std::string& n : opnd) {
     // Ops outside the plugin's set may carry region-local names; they are
     // rejected by name later, so unknown operands are skipped here.
@@ -586,6 +601,33 @@ void parse_statement(const std::string& stmt, const std::vector<RawFunc>& all, B
     size_t k = rhs.find("dim = ");
     if (k == std::string::npos) k = rhs.find("dimension = ");
     if (k != std::string::npos) op.dim = strtoll(rhs.c_str() + rhs.find('=', k) + 1, nullptr, 10);
+  } else if (opname == "slice") {
+    // Pretty form "stablehlo.slice %x [a:b, c:d:s]" or the generic
+    // start_indices / limit_indices / strides attributes.
+    if (!list_after(rhs, "start_indices = ", &op.slice_start)) {
+      const size_t lb = body.find('[');
+      const size_t rbk = body.find(']', lb == std::string::npos ? 0 : lb);
+      if (lb == std::string::npos || rbk == std::string::npos) throw ParseError("slice without its ranges: " + s);
+      const std::string r = body.substr(lb + 1, rbk - lb - 1);
+      size_t p0 = 0;
+      while (p0 <= r.size()) {
+        size_t e = r.find(',', p0);
+        if (e == std::string::npos) e = r.size();
+        const std::string item = trim(r.substr(p0, e - p0));
+        if (!item.empty()) {
+          const std::vector<int64_t> v = int_list(item);
+          if (v.size() < 2 || v.size() > 3 || item.find(':') == std::string::npos)
+            throw ParseError("bad slice range '" + item + "': " + s);
+          op.slice_start.push_back(v[0]);
+          op.slice_limit.push_back(v[1]);
+          op.slice_stride.push_back(v.size() == 3 ? v[2] : 1);
+        }
+        p0 = e + 1;
+      }
+    } else {
+      list_after(rhs, "limit_indices = ", &op.slice_limit);
+      if (!list_after(rhs, "strides = ", &op.slice_stride)) op.slice_stride.assign(op.slice_start.size(), 1);
+    }
   } else if (opname == "compare") {
     for (const char* d : {"EQ", "NE", "LT", "LE", "GT", "GE"}) {
       const std::string ds(d);

@@ -21,6 +21,8 @@ EW_OPS = ["LOAD", "CONST", "ADD", "SUB", "MUL", "DIV", "MAX", "MIN", "POW", "NEG
           "LOG1P", "EXPM1", "TANH", "RSQRT", "SQRT", "LOGISTIC", "FLOOR", "CEIL", "CMP_EQ", "CMP_NE",
           "CMP_LT", "CMP_LE", "CMP_GT", "CMP_GE", "SELECT", "ROUND_BF16"]
 EW = {name: i for i, name in enumerate(EW_OPS)}
+MK_EW_IN_DEFAULT, MK_EW_IN_F32, MK_EW_IN_BF16 = 0, 1, 2  # LOAD's b: the input's element type
+MK_EW_KEEP_F32 = 64  # or'ed into an op: an unrounded f32 result in a bf16 program
 
 
 class EwInstr(ctypes.Structure):
@@ -57,6 +59,8 @@ SIGNATURES = {
     "mk_argmax_lastdim": (_i32, [_i32, _p, _p, _i64, _i64, _p]),
     "mk_reduce_lastdim": (_i32, [_i32, _i32, _p, _p, _i64, _i64, _p]),
     "mk_elementwise": (_i32, [_i32, _p, _i32, _p, _p, _i32, _i32, _p, _i64, _p]),
+    "mk_strided_copy": (_i32, [_p, _p, _i32, _i32, _p, _p, _i64, _p, _i64, _p]),
+    "mk_iota": (_i32, [_p, _i32, _i32, _p, _i32, _p]),
     "mk_elementwise_prepare": (_i32, [_i32, _p, _i32, _i32, _i32]),
 }
 

@@ -242,22 +242,27 @@ def reduce_lastdim(x, op="sum", out=None):
 
 def elementwise(program, inputs, out_slot, out=None, dtype=None):
     """Evaluate an elementwise register program (list of (op, dst, a, b, c,
-    imm) tuples, op a name from mi355x._lib.EW_OPS) over same-shaped inputs
-    (or 1-element scalars)."""
+    imm) tuples, op a name from mi355x._lib.EW_OPS or an op code, possibly
+    or'ed with MK_EW_KEEP_F32) over inputs of the output's shape, 1-element
+    scalars or periodic inputs (a divisor of its size).  dtype
+    (torch.float32 / torch.bfloat16) is the program's and the output's type,
+    by default the first non-scalar input's; inputs of the other type are
+    loaded with MK_EW_IN_F32 / MK_EW_IN_BF16 in their LOAD's b."""
     import ctypes as _ct
 
     big = [t for t in inputs if t.numel() != 1]
     ref = big[0] if big else inputs[0]
     for t in inputs:
         _require(t, (torch.float32,) + _BF16, "input")
-    n = ref.numel()
-    dt = _dt(ref)
+    n = ref.numel() if out is None else out.numel()
+    out_dtype = dtype if dtype is not None else ref.dtype
+    dt = _lib.MK_DT_F32 if out_dtype == torch.float32 else _lib.MK_DT_BF16
     arr = (_lib.EwInstr * len(program))()
     for i, (op, dst, a, b, c, imm) in enumerate(program):
-        arr[i] = _lib.EwInstr(_lib.EW[op], dst, a, b, c, imm)
+        arr[i] = _lib.EwInstr(_lib.EW[op] if isinstance(op, str) else op, dst, a, b, c, imm)
     ptrs = (_ct.c_void_p * max(1, len(inputs)))(*[t.data_ptr() for t in inputs])
     numel = (_ct.c_int64 * max(1, len(inputs)))(*[t.numel() for t in inputs])
-    y = out if out is not None else torch.empty(ref.shape, dtype=ref.dtype, device=ref.device)
+    y = out if out is not None else torch.empty(ref.shape, dtype=out_dtype, device=ref.device)
     check(lib().mk_elementwise_prepare(dt, arr, len(program), len(inputs), out_slot))
     check(lib().mk_elementwise(dt, arr, len(program), ptrs, numel, len(inputs), out_slot, _ptr(y), n,
                                _stream(ref.device)))

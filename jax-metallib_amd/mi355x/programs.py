@@ -359,3 +359,196 @@ def plumbing(n=1024):
         f"return %2 : {tr}",
     ]
     return _module("jit_plumbing", [t, t], [tr], body)
+
+
+class _Body:
+    """SSA body builder: each call appends `%<n> = <rhs>` and returns %<n>."""
+
+    def __init__(self):
+        self.lines = []
+
+    def __call__(self, rhs):
+        name = f"%{len(self.lines)}"
+        self.lines.append(f"{name} = {rhs}")
+        return name
+
+    def const(self, value, dt):
+        return self(f"stablehlo.constant dense<{value}> : {_t([], dt)}")
+
+    def bcast(self, x, tx, dims, ty):
+        return self(f"stablehlo.broadcast_in_dim {x}, dims = [{', '.join(map(str, dims))}] : ({tx}) -> {ty}")
+
+    def splat(self, value, dt, shape):
+        return self.bcast(self.const(value, dt), _t([], dt), [], _t(shape, dt))
+
+    def bin(self, op, a, b, t):
+        return self(f"stablehlo.{op} {a}, {b} : {t}")
+
+    def un(self, op, a, t):
+        return self(f"stablehlo.{op} {a} : {t}")
+
+    def cvt(self, x, tx, ty):
+        return self(f"stablehlo.convert {x} : ({tx}) -> {ty}")
+
+    def reshape(self, x, tx, ty):
+        return self(f"stablehlo.reshape {x} : ({tx}) -> {ty}")
+
+    def transpose(self, x, tx, perm, ty):
+        return self(f"stablehlo.transpose {x}, dims = [{', '.join(map(str, perm))}] : ({tx}) -> {ty}")
+
+    def slice(self, x, tx, ranges, ty):
+        return self(f"stablehlo.slice {x} [{', '.join(f'{a}:{b}' for a, b in ranges)}] : ({tx}) -> {ty}")
+
+    def reduce(self, x, tx, init, ts, op, dims, tr):
+        return self(f"stablehlo.reduce({x} init: {init}) applies stablehlo.{op} across dimensions = "
+                    f"[{', '.join(map(str, dims))}] : ({tx}, {ts}) -> {tr}")
+
+
+def _rmsnorm_bf16(e, x, g, R, C, eps):
+    """x * rsqrt(mean(x * x, -1, keepdims=True) + eps) * g on bf16 x [R, C]
+    (jnp.mean sums in f32 and divides there)."""
+    tx, txf, tr, tr1, tr1b = _t([R, C], "bf16"), _t([R, C], "f32"), _t([R], "f32"), _t([R, 1], "f32"), _t([R, 1], "bf16")
+    sq = e.cvt(e.bin("multiply", x, x, tx), tx, txf)
+    ss = e.reduce(sq, txf, e.const("0.000000e+00", "f32"), "tensor<f32>", "add", [1], tr)
+    mean = e.bin("divide", e.bcast(ss, tr, [0], tr1), e.splat(f"{float(C):.6e}", "f32", [R, 1]), tr1)
+    r = e.un("rsqrt", e.bin("add", e.cvt(mean, tr1, tr1b), e.splat(eps, "bf16", [R, 1]), tr1b), tr1b)
+    xr = e.bin("multiply", x, e.bcast(r, tr1b, [0, 1], tx), tx)
+    gb = e.bcast(e.bcast(g, _t([C], "bf16"), [1], _t([1, C], "bf16")), _t([1, C], "bf16"), [0, 1], tx)
+    return e.bin("multiply", xr, gb, tx)
+
+
+def _int4_mm(e, x, p, s, z, M, K, N):
+    """x @ ((q - z) * s) as bf16 for the int4 g64 weight (p, s, z), written
+    like int4_g64_matmul's function."""
+    G = K // 64
+    tp, ts, tz = _t([K // 2, N], "ui8"), _t([G, N], "bf16"), _t([G, N], "ui8")
+    tp3, tc, tq, tqf = _t([K // 2, 1, N], "ui8"), _t([K // 2, 2, N], "ui8"), _t([K, N], "ui8"), _t([K, N], "f32")
+    lo = e.bin("and", p, e.splat("15", "ui8", [K // 2, N]), tp)
+    hi = e.bin("shift_right_logical", p, e.splat("4", "ui8", [K // 2, N]), tp)
+    cat = e(f"stablehlo.concatenate {e.bcast(lo, tp, [0, 2], tp3)}, {e.bcast(hi, tp, [0, 2], tp3)}, dim = 1 : "
+            f"({tp3}, {tp3}) -> {tc}")
+    q = e.reshape(cat, tc, tq)
+    zr = e.reshape(e.bcast(e.reshape(z, tz, _t([G, 1, N], "ui8")), _t([G, 1, N], "ui8"), [0, 1, 2],
+                           _t([G, 64, N], "ui8")), _t([G, 64, N], "ui8"), tq)
+    sr = e.reshape(e.bcast(e.reshape(s, ts, _t([G, 1, N], "bf16")), _t([G, 1, N], "bf16"), [0, 1, 2],
+                           _t([G, 64, N], "bf16")), _t([G, 64, N], "bf16"), _t([K, N], "bf16"))
+    w = e.bin("multiply", e.bin("subtract", e.cvt(q, tq, tqf), e.cvt(zr, tq, tqf), tqf),
+              e.cvt(sr, _t([K, N], "bf16"), tqf), tqf)
+    xf = e.cvt(x, _t([M, K], "bf16"), _t([M, K], "f32"))
+    y = e(f"stablehlo.dot_general {xf}, {w}, contracting_dims = [1] x [0], precision = [DEFAULT, DEFAULT] : "
+          f"({_t([M, K], 'f32')}, {tqf}) -> {_t([M, N], 'f32')}")
+    return e.cvt(y, _t([M, N], "f32"), _t([M, N], "bf16"))
+
+
+def _softmax_bf16(e, x, shape):
+    """jax.nn.softmax(x, axis=-1) on bf16 x of any rank (the sum upcast to f32)."""
+    r = len(shape)
+    tx, txf = _t(shape, "bf16"), _t(shape, "f32")
+    rows, rows1 = shape[:-1], shape[:-1] + [1]
+    tr, trf, tr1 = _t(rows, "bf16"), _t(rows, "f32"), _t(rows1, "bf16")
+    lead = list(range(r - 1))
+    m = e.reduce(x, tx, e.const(_NEG_INF["bf16"], "bf16"), "tensor<bf16>", "maximum", [r - 1], tr)
+    m = e.bin("maximum", e.splat(_NEG_INF["bf16"], "bf16", rows), m, tr)
+    mb = e.bcast(e.bcast(m, tr, lead, tr1), tr1, list(range(r)), tx)
+    ex = e.un("exponential", e.bin("subtract", x, mb, tx), tx)
+    sm = e.reduce(e.cvt(ex, tx, txf), txf, e.const("0.000000e+00", "f32"), "tensor<f32>", "add", [r - 1], trf)
+    sb = e.bcast(e.bcast(e.cvt(sm, trf, tr), tr, lead, tr1), tr1, list(range(r)), tx)
+    return e.bin("divide", ex, sb, tx)
+
+
+def decoder_layer(B, S, hidden, heads, head_dim, ffn, eps="9.99999997E-7"):
+    """One Llama-style decoder layer as jax.jit lowers it (bf16 activations,
+    int4 g64 projections), the reference's transformer-layer benchmark
+    (benchmarks/vs_cpu.py:603-626) with RMSNorm, rotate-half RoPE, a causal
+    mask and SwiGLU:
+
+        def layer(x, g1, wqkv, wo, g2, wg, wu, wd, cos, sin):  # w* = (p, s, z)
+            T, A = B * S, H * D
+            qkv = int4mm(rmsnorm(x, g1), *wqkv).reshape(B, S, 3, H, D)
+            q, k, v = qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
+            c, s = cos[None, :, None, :], sin[None, :, None, :]
+            def rope(t):
+                t = t.astype(f32); t0, t1 = t[..., :D // 2], t[..., D // 2:]
+                return jnp.concatenate([t0 * c - t1 * s, t1 * c + t0 * s], -1).astype(bf16)
+            q, k, v = (t.transpose(0, 2, 1, 3) for t in (rope(q), rope(k), v))
+            sc = (q @ jnp.swapaxes(k, -1, -2)) * D ** -0.5
+            mask = jnp.arange(S)[:, None] >= jnp.arange(S)[None, :]
+            p = jax.nn.softmax(jnp.where(mask, sc, -jnp.inf), axis=-1)
+            a = (p @ v).transpose(0, 2, 1, 3).reshape(T, A)
+            x1 = x + int4mm(a, *wo)
+            h2 = rmsnorm(x1, g2)
+            return x1 + int4mm(jax.nn.silu(int4mm(h2, *wg)) * int4mm(h2, *wu), *wd)
+
+    with rmsnorm and int4mm the functions of rmsnorm(dt="bf16") and
+    int4_g64_matmul.  Arguments: x bf16 [B*S, hidden]; g_attn bf16 [hidden];
+    w_qkv (3 arrays); w_o; g_mlp; w_gate; w_up; w_down; cos, sin f32
+    [S, head_dim/2].  The qkv columns are q | k | v, each heads x head_dim."""
+    H, D, T, A, F = heads, head_dim, B * S, heads * head_dim, ffn
+    Dh = D // 2
+    e = _Body()
+
+    def wargs(i, K, N):
+        return [f"%arg{i}", f"%arg{i + 1}", f"%arg{i + 2}"], [_t([K // 2, N], "ui8"), _t([K // 64, N], "bf16"),
+                                                             _t([K // 64, N], "ui8")]
+
+    args = [_t([T, hidden], "bf16"), _t([hidden], "bf16")]
+    wqkv, t = wargs(2, hidden, 3 * A); args += t
+    wo, t = wargs(5, A, hidden); args += t
+    args.append(_t([hidden], "bf16"))
+    wg, t = wargs(9, hidden, F); args += t
+    wu, t = wargs(12, hidden, F); args += t
+    wd, t = wargs(15, F, hidden); args += t
+    args += [_t([S, Dh], "f32"), _t([S, Dh], "f32")]
+
+    tb = _t([B, S, H, D], "bf16")
+    h = _rmsnorm_bf16(e, "%arg0", "%arg1", T, hidden, eps)
+    qkv = e.reshape(_int4_mm(e, h, *wqkv, T, hidden, 3 * A), _t([T, 3 * A], "bf16"), _t([B, S, 3, H, D], "bf16"))
+    parts = []
+    for j in range(3):
+        sl = e.slice(qkv, _t([B, S, 3, H, D], "bf16"), [(0, B), (0, S), (j, j + 1), (0, H), (0, D)],
+                     _t([B, S, 1, H, D], "bf16"))
+        parts.append(e.reshape(sl, _t([B, S, 1, H, D], "bf16"), tb))
+    q, k, v = parts
+    th, tf, t4 = _t([B, S, H, Dh], "f32"), _t([B, S, H, D], "f32"), _t([1, S, 1, Dh], "f32")
+    c = e.bcast(e.reshape("%arg18", _t([S, Dh], "f32"), t4), t4, [0, 1, 2, 3], th)
+    s = e.bcast(e.reshape("%arg19", _t([S, Dh], "f32"), t4), t4, [0, 1, 2, 3], th)
+
+    def rope(x):
+        xf = e.cvt(x, tb, tf)
+        x0 = e.slice(xf, tf, [(0, B), (0, S), (0, H), (0, Dh)], th)
+        x1 = e.slice(xf, tf, [(0, B), (0, S), (0, H), (Dh, D)], th)
+        lo = e.bin("subtract", e.bin("multiply", x0, c, th), e.bin("multiply", x1, s, th), th)
+        hi = e.bin("add", e.bin("multiply", x1, c, th), e.bin("multiply", x0, s, th), th)
+        cat = e(f"stablehlo.concatenate {lo}, {hi}, dim = 3 : ({th}, {th}) -> {tf}")
+        return e.cvt(cat, tf, tb)
+
+    tbh = _t([B, H, S, D], "bf16")
+    qt = e.transpose(rope(q), tb, [0, 2, 1, 3], tbh)
+    kt = e.transpose(rope(k), tb, [0, 2, 1, 3], tbh)
+    vt = e.transpose(v, tb, [0, 2, 1, 3], tbh)
+    tkT, tsc = _t([B, H, D, S], "bf16"), _t([B, H, S, S], "bf16")
+    kT = e.transpose(kt, tbh, [0, 1, 3, 2], tkT)
+    sc = e(f"stablehlo.dot_general {qt}, {kT}, batching_dims = [0, 1] x [0, 1], contracting_dims = [3] x [2], "
+           f"precision = [DEFAULT, DEFAULT] : ({tbh}, {tkT}) -> {tsc}")
+    sc = e.bin("multiply", sc, e.splat(f"{D ** -0.5:.6e}", "bf16", [B, H, S, S]), tsc)
+    ti, ti1, tm = _t([S], "i32"), _t([S, 1], "i32"), _t([S, S], "i32")
+    io = e(f"stablehlo.iota dim = 0 : {ti}")
+    r_ = e.bcast(e.bcast(io, ti, [0], ti1), ti1, [0, 1], tm)
+    c_ = e.bcast(e.bcast(io, ti, [1], _t([1, S], "i32")), _t([1, S], "i32"), [0, 1], tm)
+    mask = e(f"stablehlo.compare  GE, {r_}, {c_},  SIGNED : ({tm}, {tm}) -> {_t([S, S], 'i1')}")
+    maskb = e.bcast(mask, _t([S, S], "i1"), [2, 3], _t([B, H, S, S], "i1"))
+    sc = e(f"stablehlo.select {maskb}, {sc}, {e.splat(_NEG_INF['bf16'], 'bf16', [B, H, S, S])} : "
+           f"{_t([B, H, S, S], 'i1')}, {tsc}")
+    p = _softmax_bf16(e, sc, [B, H, S, S])
+    o = e(f"stablehlo.dot_general {p}, {vt}, batching_dims = [0, 1] x [0, 1], contracting_dims = [3] x [2], "
+          f"precision = [DEFAULT, DEFAULT] : ({tsc}, {tbh}) -> {tbh}")
+    a = e.reshape(e.transpose(o, tbh, [0, 2, 1, 3], tb), tb, _t([T, A], "bf16"))
+    tx = _t([T, hidden], "bf16")
+    x1 = e.bin("add", "%arg0", _int4_mm(e, a, *wo, T, A, hidden), tx)
+    h2 = _rmsnorm_bf16(e, x1, "%arg8", T, hidden, eps)
+    tfb = _t([T, F], "bf16")
+    gt = _int4_mm(e, h2, *wg, T, hidden, F)
+    up = _int4_mm(e, h2, *wu, T, hidden, F)
+    act = e.bin("multiply", e.bin("multiply", gt, e.un("logistic", gt, tfb), tfb), up, tfb)
+    out = e.bin("add", x1, _int4_mm(e, act, *wd, T, F, hidden), tx)
+    return _module("jit_layer", args, [tx], e.lines + [f"return {out} : {tx}"])

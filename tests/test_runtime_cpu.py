@@ -190,14 +190,14 @@ def _unsupported(text):
 
 def test_unsupported_ops_fail_at_compile_with_a_list():
     text = _wrap(["tensor<4x8xf32>", "tensor<8x4xf32>"], ["tensor<8x4xf32>", "tensor<4x8xf32>"], [
-        "%0 = stablehlo.transpose %arg0, dims = [1, 0] : (tensor<4x8xf32>) -> tensor<8x4xf32>",
+        "%0 = stablehlo.remainder %arg1, %arg1 : tensor<8x4xf32>",
         "%1 = stablehlo.cosine %arg1 : tensor<8x4xf32>",
         "%2 = stablehlo.add %0, %1 : tensor<8x4xf32>",
         "%3 = stablehlo.sine %arg0 : tensor<4x8xf32>",
         "return %2, %3 : tensor<8x4xf32>, tensor<4x8xf32>",
     ])
     msg = _unsupported(text)
-    for op in ("stablehlo.transpose", "stablehlo.cosine", "stablehlo.sine"):
+    for op in ("stablehlo.remainder", "stablehlo.cosine", "stablehlo.sine"):
         assert op in msg, msg
 
 
@@ -228,12 +228,55 @@ def test_unaligned_gemm_takes_the_general_kernel():
 
 
 def test_broken_softmax_is_not_fused():
-    # The max is taken over another tensor: not a softmax, and the row
-    # broadcast it needs has no elementwise route.
+    # The max is taken over another tensor: not a softmax.  It runs op by
+    # op: the reductions, the row broadcasts as layout copies, elementwise.
     text = P.softmax(8, 16).replace(
         "%0 = stablehlo.reduce(%arg0 init: %cst)", "%0 = stablehlo.reduce(%arg1 init: %cst)").replace(
         "@main(%arg0: tensor<8x16xf32>)", "@main(%arg0: tensor<8x16xf32>, %arg1: tensor<8x16xf32>)")
-    assert "broadcast" in _unsupported(text)
+    steps = plan(text)
+    assert not any(s.startswith("softmax") for s in steps), steps
+    assert "reduce_max rows=8 cols=16 f32" in steps and "reduce_sum rows=8 cols=16 f32" in steps
+    assert any(s.startswith("broadcast [8,1] -> f32 [8,16]") for s in steps), steps
+
+
+def test_f32_arithmetic_inside_a_bf16_program():
+    # (x.astype(f32) * y + 1).astype(bf16), y f32: one bf16 program that
+    # loads y as f32, keeps the product and sum in f32 and rounds once.
+    text = _wrap(["tensor<64xbf16>", "tensor<64xf32>"], ["tensor<64xbf16>"], [
+        "%0 = stablehlo.convert %arg0 : (tensor<64xbf16>) -> tensor<64xf32>",
+        "%1 = stablehlo.multiply %0, %arg1 : tensor<64xf32>",
+        "%cst = stablehlo.constant dense<1.000000e+00> : tensor<f32>",
+        "%2 = stablehlo.broadcast_in_dim %cst, dims = [] : (tensor<f32>) -> tensor<64xf32>",
+        "%3 = stablehlo.add %1, %2 : tensor<64xf32>",
+        "%4 = stablehlo.convert %3 : (tensor<64xf32>) -> tensor<64xbf16>",
+        "return %4 : tensor<64xbf16>",
+    ])
+    assert plan(text) == ["elementwise 6 instr, 2 inputs, n=64 bf16"]
+
+
+def test_residual_add_keeps_the_dequant_matmul():
+    # x + int4mm(h): the elementwise add loads the matmul's bf16 output; it
+    # does not pull the matmul's f32 product into its program.
+    t = P.int4_g64_matmul(16, 128, 256)
+    t = t.replace("-> (tensor<16x256xbf16>", "-> (tensor<16x256xbf16>").replace(
+        "    return %21 : tensor<16x256xbf16>",
+        "    %22 = stablehlo.add %21, %21 : tensor<16x256xbf16>\n    return %22 : tensor<16x256xbf16>")
+    assert plan(t) == ["int4_g64_matmul M=16 K=128 N=256 -> bf16", "elementwise 2 instr, 1 inputs, n=4096 bf16"]
+
+
+def test_decoder_layer_plans_onto_the_kernels():
+    """The Llama layer's StableHLO: projections on the dequant-matmul, norms
+    and softmax on their row kernels, the two attention products on the bf16
+    GEMM, everything else as layout copies and elementwise programs."""
+    steps = plan(P.decoder_layer(2, 64, 128, 2, 64, 256))
+    kinds = [s.split()[0] for s in steps]
+    assert kinds.count("int4_g64_matmul") == 5 and kinds.count("rmsnorm") == 2
+    assert kinds.count("softmax") == 1 and kinds.count("gemm_bf16") == 2
+    assert set(kinds) <= {"int4_g64_matmul", "rmsnorm", "softmax", "gemm_bf16", "gemm", "elementwise", "slice",
+                          "broadcast", "concatenate", "transpose"}, set(kinds)
+    assert "softmax rows=256 cols=64 bf16" in steps
+    # the causal mask is folded at compile time into the select's program
+    assert not any(s.startswith("iota") for s in steps)
 
 
 def test_argmax_values_result_is_rejected():
