@@ -395,6 +395,36 @@ def profile_run(torch, ops, kind, steps):
     return t
 
 
+def profile_layer(steps):
+    """One decoder layer (4 x 2048 tokens) compiled from its StableHLO and
+    executed `steps` times through the runtime (execute + await each), for
+    rocprofv3 kernel traces of the compiled path.  Returns seconds per call."""
+    from mi355x import programs, runtime, synthetic
+
+    client = runtime.Client()
+    try:
+        x, w, cos, sin = synthetic.decoder_layer_case(np.random.default_rng(0), 4, 2048, 2048, 16, 128, 8192)
+        exe = client.compile(programs.decoder_layer(4, 2048, 2048, 16, 128, 8192))
+        bufs = [client.buffer(a, runtime.BF16) if is_bf16 else client.buffer(a)
+                for a, is_bf16 in synthetic.decoder_layer_arguments(x, w, cos, sin)]
+        times = []
+        for i in range(steps + 2):
+            t0 = time.perf_counter()
+            outs, done = exe.execute(bufs)
+            done.wait()
+            if i >= 2:
+                times.append(time.perf_counter() - t0)
+            for o in outs:
+                o.close()
+        for b in bufs:
+            b.close()
+        exe.close()
+    finally:
+        client.close()
+    times.sort()
+    return times[len(times) // 2]
+
+
 def available_cores():
     """Cores this process may run on: the affinity mask, further limited by a
     cgroup CPU quota when one is set (cpu.max: quota period)."""
@@ -498,6 +528,12 @@ def bench_end_to_end(warmup=10, iters=50):
             "bf16_gemm_4096": (programs.matmul(4096, 4096, 4096),
                                [(f32_to_bf16_bits(a), runtime.BF16), (f32_to_bf16_bits(a.T.copy()), runtime.BF16)]),
         }
+        # one decoder layer (the workload's config 5 sizes) from its StableHLO
+        xl, wl, cos, sin = synthetic.decoder_layer_case(rng, 4, 2048, 2048, 16, 128, 8192)
+        cases["decoder_layer_B4_S2048"] = (
+            programs.decoder_layer(4, 2048, 2048, 16, 128, 8192),
+            [(arr, runtime.BF16 if is_bf16 else None)
+             for arr, is_bf16 in synthetic.decoder_layer_arguments(xl, wl, cos, sin)])
         for name, (text, arrays) in cases.items():
             t0 = time.perf_counter()
             exe = client.compile(text)
@@ -517,6 +553,7 @@ def bench_end_to_end(warmup=10, iters=50):
                     times.append(dt)
             times.sort()
             out[name] = {"compile_ms": round(compile_ms, 3), "first_call_ms": round(first_ms, 3),
+                         "steps": exe.num_steps,
                          "median_us": round(times[len(times) // 2] * 1e6, 2), "min_us": round(times[0] * 1e6, 2),
                          "p90_us": round(times[int(0.9 * (len(times) - 1))] * 1e6, 2), "iters": iters,
                          "warmup": warmup}
@@ -540,7 +577,8 @@ def main():
                          "or 'none'")
     ap.add_argument("--profile", default="",
                     help="int4 | int8 | gemm | qgemm: eager launches of one kernel plus a 256 MiB copy calibration, "
-                         "for rocprofv3 --pmc runs (prints the kernel's us/launch)")
+                         "for rocprofv3 --pmc runs (prints the kernel's us/launch); layer: the decoder layer's "
+                         "StableHLO compiled once and executed --steps times (median wall time per call)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one MI355X only (asked for --gpus {args.gpus}); "
@@ -553,7 +591,7 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     if args.profile:
-        t = profile_run(torch, ops, args.profile, args.steps)
+        t = profile_layer(args.steps) if args.profile == "layer" else profile_run(torch, ops, args.profile, args.steps)
         print(json.dumps({"profile": args.profile, "us_per_launch": round(t * 1e6, 3), "steps": args.steps}),
               flush=True)
         return

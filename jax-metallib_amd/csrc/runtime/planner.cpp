@@ -20,6 +20,7 @@
 #include "planner.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -28,6 +29,7 @@
 #include <set>
 #include <sstream>
 #include <stdexcept>
+#include <tuple>
 
 #include "mk_runtime.h"
 
@@ -335,6 +337,7 @@ class Planner {
     }
     if (n == "dot_general" || n == "dot") {
       int s;
+      if ((s = attention_merged(v)) >= 0) return unmerge_heads(v, s);
       if (try_qmm(v, &s)) return s;
       if (try_gemm(v, *op, &s)) return s;
       return dummy(v);
@@ -354,6 +357,10 @@ class Planner {
       int s;
       if (try_rmsnorm(v, &s)) return s;
     }
+    if (n == "add" || n == "multiply") {
+      int s;
+      if (try_qmm_epilogue(v, &s)) return s;
+    }
     if (n == "convert") {
       int s;
       if (try_qmm(v, &s)) return s;
@@ -362,10 +369,321 @@ class Planner {
     if (is_elementwise(v)) return ew_root(v);
     {
       int s;
+      if (n == "transpose" && (s = decoder_transpose(v)) >= 0) return s;
       if (try_layout(v, *op, &s)) return s;
     }
     reject(op, "");
     return dummy(v);
+  }
+
+  // ---- decoder patterns ------------------------------------------------------
+  // Causal attention and rotate-half RoPE as jnp writes them (the workload's
+  // decoder layer, the reference's transformer-layer benchmark,
+  // benchmarks/vs_cpu.py:603-626) run on the decoder kernels
+  // (mk_attention_causal_bf16, mk_rope_qkv_split_bf16) instead of op by op.
+  // The attention kernel keeps scores and probabilities in f32 until P @ V
+  // (P rounded to bf16) where the jnp form rounds each bf16 op: results agree
+  // at the bf16 tolerance, not bit for bit.  MK_PLAN_DECODER_FUSION=0 turns
+  // both routes off.
+  static bool decoder_fusion() {
+    const char* e = getenv("MK_PLAN_DECODER_FUSION");
+    return !(e && e[0] == '0');
+  }
+  static bool dims_eq(const std::vector<int64_t>& d, std::initializer_list<int64_t> w) {
+    return d == std::vector<int64_t>(w);
+  }
+
+  // t [B, S, H, D] = reshape(slice(x5, dim 2 = [j, j+1))) with x5 [B, S, 3, H, D]
+  // (qkv.reshape(B, S, 3, H, D)[:, :, j]); returns x5 and j through the pointers.
+  bool head_slice(int t, int* x5, int* j) const {
+    const std::vector<int64_t>& td = type(t).dims;
+    if (td.size() != 4 || type(t).dtype != DT_BF16) return false;
+    const Op* rs = def(t);
+    if (!rs || rs->name != "reshape") return false;
+    const int sl = rs->operands[0];
+    const Op* so = def(sl);
+    if (!so || so->name != "slice") return false;
+    const int x = so->operands[0];
+    const std::vector<int64_t>& xd = type(x).dims;
+    if (!(xd.size() == 5 && xd[0] == td[0] && xd[1] == td[1] && xd[2] == 3 && xd[3] == td[2] && xd[4] == td[3]))
+      return false;
+    for (int d = 0; d < 5; ++d) {
+      if (so->slice_stride[d] != 1) return false;
+      if (d == 2) continue;
+      if (so->slice_start[d] != 0 || so->slice_limit[d] != xd[d]) return false;
+    }
+    if (so->slice_limit[2] != so->slice_start[2] + 1) return false;
+    *x5 = x;
+    *j = (int)so->slice_start[2];
+    return true;
+  }
+
+  // cb [B, S, H, D/2] = table [S, D/2] broadcast over B and H (through a
+  // reshape to [1, S, 1, D/2]); returns the table or -1.
+  int rope_table(int cb, int64_t S, int64_t Dh) const {
+    const Op* b = def(cb);
+    if (!b || b->name != "broadcast_in_dim" || type(cb).dtype != DT_F32) return -1;
+    int u = b->operands[0];
+    if (dims_eq(b->dims, {1, 3}) && dims_eq(type(u).dims, {S, Dh})) return u;
+    if (!dims_eq(b->dims, {0, 1, 2, 3}) || !dims_eq(type(u).dims, {1, S, 1, Dh})) return -1;
+    const Op* r = def(u);
+    if (!r || r->name != "reshape" || !dims_eq(type(r->operands[0]).dims, {S, Dh})) return -1;
+    return r->operands[0];
+  }
+
+  // The two factors of a multiply, or false.
+  bool factors(int v, int* a, int* b) const {
+    const Op* m = def(v);
+    if (!m || m->name != "multiply" || m->operands.size() != 2) return false;
+    *a = m->operands[0];
+    *b = m->operands[1];
+    return true;
+  }
+  // v = x * t or t * x with t a broadcast RoPE table: returns x and the table.
+  bool rope_term(int v, int64_t S, int64_t Dh, int* x, int* table) const {
+    int a, b;
+    if (!factors(v, &a, &b)) return false;
+    int t;
+    if ((t = rope_table(b, S, Dh)) >= 0) {
+      *x = a;
+      *table = t;
+      return true;
+    }
+    if ((t = rope_table(a, S, Dh)) >= 0) {
+      *x = b;
+      *table = t;
+      return true;
+    }
+    return false;
+  }
+  // xs = slice(xf, last axis [lo, lo + Dh)) of xf [B, S, H, D]; returns xf or -1.
+  int half_slice(int xs, int64_t lo) const {
+    const Op* so = def(xs);
+    if (!so || so->name != "slice") return -1;
+    const int xf = so->operands[0];
+    const std::vector<int64_t>& d = type(xf).dims;
+    if (d.size() != 4) return -1;
+    for (int k = 0; k < 4; ++k) {
+      if (so->slice_stride[k] != 1) return -1;
+      const int64_t a = k == 3 ? lo : 0, b = k == 3 ? lo + d[3] / 2 : d[k];
+      if (so->slice_start[k] != a || so->slice_limit[k] != b) return -1;
+    }
+    return xf;
+  }
+
+  struct RopeMatch {
+    int x5 = -1, j = -1, cos = -1, sin = -1;
+    int64_t B = 0, S = 0, H = 0, D = 0;
+  };
+  // r [B, S, H, D] bf16 = concatenate([x0 c - x1 s, x1 c + x0 s], -1) in f32
+  // with x = head j of the fused qkv, x0 / x1 its halves, c / s the tables
+  // [S, D/2]: the rotate-half RoPE of mk_rope_qkv_split_bf16.
+  bool match_rope(int r, RopeMatch* m) const {
+    const Op* cv = def(r);
+    if (!cv || cv->name != "convert" || type(r).dtype != DT_BF16 || type(r).dims.size() != 4) return false;
+    const int cat = cv->operands[0];
+    const Op* co = def(cat);
+    if (!co || co->name != "concatenate" || co->operands.size() != 2 || co->dim != 3 ||
+        type(cat).dtype != DT_F32)
+      return false;
+    const std::vector<int64_t>& d = type(r).dims;
+    const int64_t S = d[1], Dh = d[3] / 2;
+    const Op* lo = def(co->operands[0]);
+    const Op* hi = def(co->operands[1]);
+    if (!lo || lo->name != "subtract" || !hi || hi->name != "add") return false;
+    int a0, t0, a1, t1;  // lo = a0 * t0 - a1 * t1
+    if (!rope_term(lo->operands[0], S, Dh, &a0, &t0) || !rope_term(lo->operands[1], S, Dh, &a1, &t1)) return false;
+    const int xf = half_slice(a0, 0);
+    if (xf < 0 || half_slice(a1, Dh) != xf) return false;
+    for (int order = 0; order < 2; ++order) {  // hi = x1 * c + x0 * s, either order
+      int b0, u0, b1, u1;
+      if (!rope_term(hi->operands[order], S, Dh, &b0, &u0) || !rope_term(hi->operands[1 - order], S, Dh, &b1, &u1))
+        continue;
+      if (b0 != a1 || u0 != t0 || b1 != a0 || u1 != t1) continue;
+      const Op* xc = def(xf);
+      if (!xc || xc->name != "convert" || type(xf).dtype != DT_F32) return false;
+      int x5, j;
+      if (!head_slice(xc->operands[0], &x5, &j) || j > 1) return false;
+      m->x5 = x5;
+      m->j = j;
+      m->cos = t0;
+      m->sin = t1;
+      m->B = d[0];
+      m->S = S;
+      m->H = d[2];
+      m->D = d[3];
+      return true;
+    }
+    return false;
+  }
+
+  struct RopeOut {
+    int q = -1, k = -1, v = -1;
+  };
+  std::map<std::tuple<int, int, int>, RopeOut> rope_steps_;  // (x5, cos, sin)
+  std::map<int, RopeOut> rope_by_qkv_;                       // x5 -> the first rope step on it
+
+  RopeOut rope_step(const RopeMatch& m) {
+    const auto key = std::make_tuple(m.x5, m.cos, m.sin);
+    auto it = rope_steps_.find(key);
+    if (it != rope_steps_.end()) return it->second;
+    Step st;
+    st.kind = ST_ROPE;
+    st.dt = MK_DT_BF16;
+    st.in = {need(m.x5), need(m.cos), need(m.sin)};
+    const int64_t bytes = m.B * m.H * m.S * m.D * 2;
+    RopeOut o;
+    for (int* p : {&o.q, &o.k, &o.v}) {
+      Slot t;
+      t.bytes = bytes;
+      *p = new_slot(t);
+    }
+    st.out = o.q;
+    st.outs = {o.k, o.v};
+    st.B = m.B;
+    st.S = m.S;
+    st.H = m.H;
+    st.D = m.D;
+    st.desc = "rope_qkv_split B=" + std::to_string(m.B) + " S=" + std::to_string(m.S) + " H=" + std::to_string(m.H) +
+              " D=" + std::to_string(m.D) + " bf16";
+    plan_.steps.push_back(st);
+    rope_steps_[key] = o;
+    if (!rope_by_qkv_.count(m.x5)) rope_by_qkv_[m.x5] = o;
+    return o;
+  }
+
+  // transpose(t, [0, 2, 1, 3]) of a RoPE'd head (q or k), of the v head of a
+  // fused qkv already split by a rope step, or of a fused attention's
+  // [B, H, S, D] output: the slot holding it, or -1.
+  int decoder_transpose(int v) {
+    if (!decoder_fusion()) return -1;
+    const Op* op = def(v);
+    if (!dims_eq(op->dims, {0, 2, 1, 3})) return -1;
+    const int t = op->operands[0];
+    int s;
+    if ((s = attention_merged(t)) >= 0) return s;
+    RopeMatch m;
+    if (match_rope(t, &m) && m.D == 128 && m.S % 64 == 0) {
+      const RopeOut o = rope_step(m);
+      return m.j == 0 ? o.q : o.k;
+    }
+    int x5, j;
+    if (head_slice(t, &x5, &j) && j == 2) {
+      auto it = rope_by_qkv_.find(x5);
+      if (it != rope_by_qkv_.end()) return it->second.v;
+    }
+    return -1;
+  }
+
+  struct AttnMatch {
+    int q = -1, k = -1, v = -1;
+    int64_t B = 0, H = 0, S = 0, D = 0;
+    float scale = 1.f;
+  };
+  // o [B, H, S, D] = softmax(where(causal, (q @ k^T) * scale, -inf)) @ v, all
+  // bf16, batched over (B, H); k^T a transpose of k or k contracted on its
+  // last axis; the mask i >= j a compile-time constant [S, S] broadcast over
+  // (B, H).
+  bool match_attention(int o, AttnMatch* m) {
+    const Op* pv = def(o);
+    if (!pv || pv->name != "dot_general" || pv->operands.size() != 2 || type(o).dtype != DT_BF16) return false;
+    const std::vector<int64_t>& od = type(o).dims;
+    if (od.size() != 4) return false;
+    if (!dims_eq(pv->lhs_batch, {0, 1}) || !dims_eq(pv->rhs_batch, {0, 1}) || !dims_eq(pv->lhs_contract, {3}) ||
+        !dims_eq(pv->rhs_contract, {2}))
+      return false;
+    const int64_t B = od[0], H = od[1], S = od[2], D = od[3];
+    const int p = pv->operands[0], v = pv->operands[1];
+    if (!dims_eq(type(p).dims, {B, H, S, S}) || !dims_eq(type(v).dims, {B, H, S, D}) ||
+        type(p).dtype != DT_BF16 || type(v).dtype != DT_BF16)
+      return false;
+    const int x = softmax_src(p);
+    if (x < 0) return false;
+    const Op* sel = def(x);
+    if (!sel || sel->name != "select" || !splat_is(sel->operands[2], -INFINITY)) return false;
+    int mask = sel->operands[0];
+    const int per = periodic_src(mask);
+    if (per >= 0) mask = per;
+    if (numel(mask) != S * S || !fold(mask)) return false;
+    const std::vector<double>& mv = folded_.at(mask);
+    for (int64_t i = 0; i < S; ++i)
+      for (int64_t jj = 0; jj < S; ++jj)
+        if ((mv[i * S + jj] != 0.0) != (i >= jj)) return false;
+    int sc = sel->operands[1];
+    double scale = 1.0;
+    int a, b;
+    if (factors(sc, &a, &b)) {
+      if (splat(b, &scale)) sc = a;
+      else if (splat(a, &scale)) sc = b;
+      else return false;
+    }
+    const Op* qk = def(sc);
+    if (!qk || qk->name != "dot_general" || !dims_eq(type(sc).dims, {B, H, S, S}) || type(sc).dtype != DT_BF16 ||
+        !dims_eq(qk->lhs_batch, {0, 1}) || !dims_eq(qk->rhs_batch, {0, 1}) || !dims_eq(qk->lhs_contract, {3}))
+      return false;
+    const int q = qk->operands[0], r = qk->operands[1];
+    if (!dims_eq(type(q).dims, {B, H, S, D}) || type(q).dtype != DT_BF16 || type(r).dtype != DT_BF16) return false;
+    int k = -1;
+    if (dims_eq(qk->rhs_contract, {3}) && dims_eq(type(r).dims, {B, H, S, D})) {
+      k = r;
+    } else if (dims_eq(qk->rhs_contract, {2}) && dims_eq(type(r).dims, {B, H, D, S})) {
+      const Op* tr = def(r);
+      if (!tr || tr->name != "transpose" || !dims_eq(tr->dims, {0, 1, 3, 2})) return false;
+      k = tr->operands[0];
+    } else {
+      return false;
+    }
+    if (D != 128 || S % 128 != 0) return false;
+    m->q = q;
+    m->k = k;
+    m->v = v;
+    m->B = B;
+    m->H = H;
+    m->S = S;
+    m->D = D;
+    m->scale = (float)scale;
+    return true;
+  }
+
+  std::map<int, int> attn_merged_;  // attention output o -> slot of o.transpose(0, 2, 1, 3)
+
+  int attention_merged(int o) {
+    auto it = attn_merged_.find(o);
+    if (it != attn_merged_.end()) return it->second;
+    int r = -1;
+    AttnMatch m;
+    if (decoder_fusion() && match_attention(o, &m)) {
+      Step st;
+      st.kind = ST_ATTN;
+      st.dt = MK_DT_BF16;
+      st.in = {need(m.q), need(m.k), need(m.v)};
+      Slot t;
+      t.bytes = type(o).bytes();
+      st.out = new_slot(t);
+      st.B = m.B;
+      st.H = m.H;
+      st.S = m.S;
+      st.D = m.D;
+      st.scale = m.scale;
+      std::ostringstream ds;
+      ds << "attention_causal B=" << m.B << " H=" << m.H << " S=" << m.S << " D=" << m.D << " scale=" << m.scale
+         << " bf16";
+      st.desc = ds.str();
+      plan_.steps.push_back(st);
+      r = st.out;
+    }
+    attn_merged_[o] = r;
+    return r;
+  }
+
+  // o [B, H, S, D] from the attention kernel's [B, S, H, D] output.
+  int unmerge_heads(int o, int merged) {
+    const std::vector<int64_t>& d = type(o).dims;
+    const int out = temp_for(o);
+    // o[b, h, s, e] = merged[b, s, h, e]
+    layout_step(merged, out, 2, d, {d[1] * d[2] * d[3], d[3], d[1] * d[3], 1}, 0, row_strides(d), 0,
+                "attention output to [B,H,S,D]");
+    return out;
   }
 
   // ---- layout ops ------------------------------------------------------------
@@ -846,8 +1164,14 @@ class Planner {
     return peel_view(op->operands[0]);
   }
 
-  bool try_qmm(int v, int* out) {
+  struct QmmMatch {
+    int fmt = -1;              // MK_QFMT_INT4_G64 / MK_QFMT_INT8_PC
+    int x = -1, w = -1, s = -1, z = -1;  // z: int4 only
+    int64_t M = 0, K = 0, N = 0;
+  };
+  bool match_qmm(int v, QmmMatch* q) const {
     const Op* top = def(v);
+    if (!top) return false;
     int dv = v;
     if (top->name == "convert") {
       dv = top->operands[0];
@@ -865,6 +1189,10 @@ class Planner {
     const Op* mul = def(w);
     if (!mul || mul->name != "multiply") return false;
     const int64_t K = d.K, N = d.N, M = d.M;
+    q->x = x;
+    q->M = M;
+    q->K = K;
+    q->N = N;
     for (int order = 0; order < 2; ++order) {
       const int f0 = mul->operands[order], f1 = mul->operands[1 - order];
       // int4: f0 = (q - z), f1 = repeat(s)
@@ -874,21 +1202,10 @@ class Planner {
         const int z = rep_rows(def(sub)->operands[1], K, N, 64);
         const int p = interleave_src(def(sub)->operands[0], K, N);
         if (s >= 0 && z >= 0 && p >= 0 && type(s).dtype == DT_BF16 && type(z).dtype == DT_U8) {
-          const int64_t ws = mk_qmatmul_workspace_bytes(MK_QFMT_INT4_G64, M, K, N);
-          if (ws < 0) return false;
-          Step st;
-          st.kind = ST_QMM_INT4;
-          st.dt = MK_DT_BF16;
-          st.in = {need(x), need(p), need(s), need(z)};
-          st.M = M;
-          st.K = K;
-          st.N = N;
-          st.out = temp_for(v);
-          plan_.workspace_bytes = std::max(plan_.workspace_bytes, ws);
-          st.desc = "int4_g64_matmul M=" + std::to_string(M) + " K=" + std::to_string(K) + " N=" +
-                    std::to_string(N) + " -> bf16";
-          plan_.steps.push_back(st);
-          *out = st.out;
+          q->fmt = MK_QFMT_INT4_G64;
+          q->w = p;
+          q->s = s;
+          q->z = z;
           return true;
         }
       }
@@ -899,57 +1216,130 @@ class Planner {
         if (sc < 0) continue;
         const int s = peel_cvt(sc);
         if (type(s).dtype != DT_F32 || numel(s) != N) continue;
-        const int64_t ws = mk_qmatmul_workspace_bytes(MK_QFMT_INT8_PC, M, K, N);
-        if (ws < 0) return false;
-        Step st;
-        st.kind = ST_QMM_INT8;
-        st.dt = MK_DT_BF16;
-        st.in = {need(x), need(wq), need(s)};
-        st.M = M;
-        st.K = K;
-        st.N = N;
-        st.out = temp_for(v);
-        plan_.workspace_bytes = std::max(plan_.workspace_bytes, ws);
-        st.desc = "int8_pc_matmul M=" + std::to_string(M) + " K=" + std::to_string(K) + " N=" + std::to_string(N) +
-                  " -> bf16";
-        plan_.steps.push_back(st);
-        *out = st.out;
+        q->fmt = MK_QFMT_INT8_PC;
+        q->w = wq;
+        q->s = s;
         return true;
       }
     }
     return false;
   }
 
+  // Emits the dequant-matmul q for value v, with a store epilogue against
+  // aux (a bf16 value of v's size) unless epi is MK_EPI_NONE.
+  bool emit_qmm(int v, const QmmMatch& q, int epi, int aux, int* out) {
+    const int64_t ws = mk_qmatmul_workspace_bytes(q.fmt, q.M, q.K, q.N);
+    if (ws < 0) return false;
+    Step st;
+    st.kind = q.fmt == MK_QFMT_INT4_G64 ? ST_QMM_INT4 : ST_QMM_INT8;
+    st.dt = MK_DT_BF16;
+    st.in = {need(q.x), need(q.w), need(q.s)};
+    if (q.fmt == MK_QFMT_INT4_G64) st.in.push_back(need(q.z));
+    st.epi = epi;
+    if (epi != MK_EPI_NONE) st.in.push_back(need(aux));
+    st.M = q.M;
+    st.K = q.K;
+    st.N = q.N;
+    st.out = temp_for(v);
+    plan_.workspace_bytes = std::max(plan_.workspace_bytes, ws);
+    static const char* epi_name[] = {"", " + add epilogue", " + swiglu epilogue", " + swiglu pairs"};
+    st.desc = std::string(q.fmt == MK_QFMT_INT4_G64 ? "int4_g64_matmul" : "int8_pc_matmul") +
+              " M=" + std::to_string(q.M) + " K=" + std::to_string(q.K) + " N=" + std::to_string(q.N) + " -> bf16" +
+              epi_name[epi];
+    plan_.steps.push_back(st);
+    *out = st.out;
+    return true;
+  }
+
+  bool try_qmm(int v, int* out) {
+    QmmMatch q;
+    return match_qmm(v, &q) && emit_qmm(v, q, MK_EPI_NONE, -1, out);
+  }
+
+  // Operand references of each value (ops and returns), counted once.
+  std::vector<int> uses_;
+  int uses(int v) {
+    if (uses_.empty()) {
+      uses_.assign(f_.values.size(), 0);
+      for (const Op& op : f_.ops)
+        for (int o : op.operands) ++uses_[o];
+      for (int r : f_.rets) ++uses_[r];
+    }
+    return uses_[v];
+  }
+
+  // bf16 `aux + qmm(...)` and `silu(g) * qmm(...)` (silu written g *
+  // logistic(g)) where nothing else reads the product: the dequant-matmul
+  // with its store epilogue (MK_EPI_ADD / MK_EPI_SWIGLU), which rounds where
+  // the elementwise program would, so the result is bit-identical.
+  // MK_PLAN_EPILOGUES=0 keeps the two steps.
+  bool try_qmm_epilogue(int v, int* out) {
+    const char* env = getenv("MK_PLAN_EPILOGUES");
+    if (env && env[0] == '0') return false;
+    const Op* op = def(v);
+    if (type(v).dtype != DT_BF16 || op->operands.size() != 2) return false;
+    for (int order = 0; order < 2; ++order) {
+      const int acc = op->operands[order], other = op->operands[1 - order];
+      if (uses(acc) != 1 || type(acc).dims != type(v).dims || type(other).dims != type(v).dims ||
+          type(other).dtype != DT_BF16)
+        continue;
+      QmmMatch q;
+      if (!match_qmm(acc, &q)) continue;
+      int epi = MK_EPI_ADD, aux = other;
+      if (op->name == "multiply") {
+        int a, b;
+        if (!factors(other, &a, &b)) continue;
+        if (is(b, "logistic") && def(b)->operands[0] == a) aux = a;
+        else if (is(a, "logistic") && def(a)->operands[0] == b) aux = b;
+        else continue;
+        epi = MK_EPI_SWIGLU;
+      } else if (op->name != "add") {
+        return false;
+      }
+      if (!mk_qmatmul_epilogue_supported(q.fmt, q.M, q.K, q.N, epi)) continue;
+      return emit_qmm(v, q, epi, aux, out);
+    }
+    return false;
+  }
+
   // ---- row patterns ----------------------------------------------------------------
-  // jax.nn.softmax: exp(x - max(x)) / sum(exp(x - max(x))) over the last axis;
-  // bf16 sums may be upcast to f32 and back (jnp.sum).
-  bool try_softmax(int v, int* out) {
+  // jax.nn.softmax: the input x of v = exp(x - max(x)) / sum(exp(x - max(x)))
+  // over the last axis (bf16 sums may be upcast to f32 and back, jnp.sum), or -1.
+  int softmax_src(int v) const {
     const Op* div = def(v);
     const int dt = type(v).dtype;
-    if (mk_dt(dt) < 0 || div->operands.size() != 2) return false;
+    if (!div || div->name != "divide" || mk_dt(dt) < 0 || div->operands.size() != 2) return -1;
     const int64_t C = last_dim(v);
     const int e = div->operands[0];
     int s = row_src(div->operands[1], C);
-    if (s < 0) return false;
+    if (s < 0) return -1;
     s = peel_cvt(s);
     const int ein = reduce_last_input(s, "add");
-    if (ein < 0 || peel_cvt(ein) != peel_view(e)) return false;
+    if (ein < 0 || peel_cvt(ein) != peel_view(e)) return -1;
     const int ev = peel_view(e);
-    if (!is(ev, "exponential") || type(ev).dtype != dt) return false;
+    if (!is(ev, "exponential") || type(ev).dtype != dt) return -1;
     const int dsub = peel_view(def(ev)->operands[0]);
-    if (!is(dsub, "subtract")) return false;
+    if (!is(dsub, "subtract")) return -1;
     const int x = peel_view(def(dsub)->operands[0]);
     int m = row_src(def(dsub)->operands[1], C);
-    if (m < 0) return false;
+    if (m < 0) return -1;
     m = peel_view(m);
     if (is(m, "maximum")) {  // jnp.max(..., initial=-inf)
       const Op* mx = def(m);
       if (splat_is(mx->operands[1], -INFINITY)) m = peel_view(mx->operands[0]);
       else if (splat_is(mx->operands[0], -INFINITY)) m = peel_view(mx->operands[1]);
-      else return false;
+      else return -1;
     }
     const int xm = reduce_last_input(m, "maximum");
-    if (xm < 0 || peel_view(xm) != x || type(x).dtype != dt || numel(x) != numel(v)) return false;
+    if (xm < 0 || peel_view(xm) != x || type(x).dtype != dt || numel(x) != numel(v)) return -1;
+    return x;
+  }
+
+  bool try_softmax(int v, int* out) {
+    const int dt = type(v).dtype;
+    const int64_t C = last_dim(v);
+    const int x = softmax_src(v);
+    if (x < 0) return false;
     Step st;
     st.kind = ST_SOFTMAX;
     st.dt = mk_dt(dt);

@@ -41,7 +41,9 @@ enum StepKind {
   ST_ZERO,
   ST_DOT_GENERIC,
   ST_LAYOUT,  // strided copy (transpose, slice, broadcast, one concatenate operand)
-  ST_IOTA
+  ST_IOTA,
+  ST_ROPE,    // mk_rope_qkv_split_bf16: in {qkv, cos, sin}, out q, outs {k, v}
+  ST_ATTN     // mk_attention_causal_bf16: in {q, k, v}, out [B, S, H, D]
 };
 
 struct Step {
@@ -51,6 +53,7 @@ struct Step {
   int out = -1;           // slot id
   int64_t batch = 1, M = 0, N = 0, K = 0;
   int out_f32 = 0;
+  int epi = MK_EPI_NONE;  // ST_QMM_*: store epilogue against in.back()
   int64_t rows = 0, cols = 0;
   float eps = 0.f;
   int reduce_op = MK_REDUCE_SUM;
@@ -67,6 +70,10 @@ struct Step {
   int64_t src_off = 0, dst_off = 0;
   int elem_bytes = 0;
   int iota_dim = 0;
+  // ST_ROPE / ST_ATTN: sizes, the score scale, further outputs.
+  int64_t B = 0, H = 0, S = 0, D = 0;
+  float scale = 1.f;
+  std::vector<int> outs;
   std::string desc;
 };
 

@@ -359,8 +359,14 @@ int run_step(const mkrt::Step& st, const std::vector<void*>& mem, void* ws, int6
     case mkrt::ST_GEMM_F32:
       return mk_gemm_f32(in(0), in(1), out, st.batch, st.M, st.N, st.K, s);
     case mkrt::ST_QMM_INT4:
+      if (st.epi != MK_EPI_NONE)
+        return mk_int4g64_matmul_epilogue_bf16(in(0), in(1), in(2), in(3), out, in(4), st.epi, st.M, st.K, st.N, ws,
+                                               ws_bytes, s);
       return mk_int4g64_matmul_bf16(in(0), in(1), in(2), in(3), out, st.M, st.K, st.N, ws, ws_bytes, s);
     case mkrt::ST_QMM_INT8:
+      if (st.epi != MK_EPI_NONE)
+        return mk_int8pc_matmul_epilogue_bf16(in(0), in(1), in(2), out, in(3), st.epi, st.M, st.K, st.N, ws, ws_bytes,
+                                              s);
       return mk_int8pc_matmul_bf16(in(0), in(1), in(2), out, st.M, st.K, st.N, ws, ws_bytes, s);
     case mkrt::ST_SOFTMAX:
       return mk_softmax_lastdim(st.dt, in(0), out, st.rows, st.cols, s);
@@ -391,6 +397,11 @@ int run_step(const mkrt::Step& st, const std::vector<void*>& mem, void* ws, int6
                              st.src_off, st.dst_st.data(), st.dst_off, s);
     case mkrt::ST_IOTA:
       return mk_iota(out, st.type_out, (int)st.shape.size(), st.shape.data(), st.iota_dim, s);
+    case mkrt::ST_ROPE:
+      return mk_rope_qkv_split_bf16(in(0), static_cast<const float*>(in(1)), static_cast<const float*>(in(2)), out,
+                                    mem[st.outs[0]], mem[st.outs[1]], st.B, st.S, st.H, st.D, 1, s);
+    case mkrt::ST_ATTN:
+      return mk_attention_causal_bf16(in(0), in(1), in(2), out, st.B, st.H, st.S, st.D, st.scale, s);
   }
   return MK_EUNSUPPORTED;
 }

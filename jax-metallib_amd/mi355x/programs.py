@@ -346,6 +346,23 @@ def int8_pc_matmul(M, K, N):
     return _module("jit_int8_pc_matmul", [tx, tw, ts], [ty], body)
 
 
+def qmm_epilogue(M, K, N, fmt="int4", op="add"):
+    """def f(aux, x, *w):  # aux bf16 [M, N]; (x, *w) as int4_g64_matmul / int8_pc_matmul
+           y = qmm(x, *w)
+           return aux + y                              # op "add"
+           return aux * jax.nn.sigmoid(aux) * y        # op "swiglu" (silu(aux) * y)"""
+    t = int4_g64_matmul(M, K, N) if fmt == "int4" else int8_pc_matmul(M, K, N)
+    ty = _t([M, N], "bf16")
+    last = "%21" if fmt == "int4" else "%6"
+    t = t.replace("func.func public @main(", f"func.func public @main(%aux: {ty}, ", 1)
+    if op == "add":
+        body = f"    %e0 = stablehlo.add %aux, {last} : {ty}\n    return %e0 : {ty}"
+    else:
+        body = (f"    %e0 = stablehlo.logistic %aux : {ty}\n    %e1 = stablehlo.multiply %aux, %e0 : {ty}\n"
+                f"    %e2 = stablehlo.multiply %e1, {last} : {ty}\n    return %e2 : {ty}")
+    return t.replace(f"    return {last} : {ty}", body)
+
+
 def plumbing(n=1024):
     """jnp.tanh(a @ b).sum(axis=1) on f32 [n, n]."""
     t, tr = _t([n, n], "f32"), _t([n], "f32")
@@ -454,6 +471,40 @@ def _softmax_bf16(e, x, shape):
     sm = e.reduce(e.cvt(ex, tx, txf), txf, e.const("0.000000e+00", "f32"), "tensor<f32>", "add", [r - 1], trf)
     sb = e.bcast(e.bcast(e.cvt(sm, trf, tr), tr, lead, tr1), tr1, list(range(r)), tx)
     return e.bin("divide", ex, sb, tx)
+
+
+def causal_attention(B, H, S, D, mask="GE", transpose_k=True):
+    """def f(q, k, v):  # bf16 [B, H, S, D]
+           sc = (q @ jnp.swapaxes(k, -1, -2)) * D ** -0.5   # or einsum("bhqd,bhkd->bhqk")
+           m = jnp.arange(S)[:, None] >= jnp.arange(S)[None, :]
+           p = jax.nn.softmax(jnp.where(m, sc, -jnp.inf), axis=-1)
+           return (p @ v).transpose(0, 2, 1, 3)             # [B, S, H, D]
+    mask: the comparison of row and column index (GE is causal);
+    transpose_k=False contracts k on its last axis instead of transposing."""
+    e = _Body()
+    t4, tkT, ts = _t([B, H, S, D], "bf16"), _t([B, H, D, S], "bf16"), _t([B, H, S, S], "bf16")
+    if transpose_k:
+        kT = e.transpose("%arg1", t4, [0, 1, 3, 2], tkT)
+        sc = e(f"stablehlo.dot_general %arg0, {kT}, batching_dims = [0, 1] x [0, 1], contracting_dims = [3] x [2], "
+               f"precision = [DEFAULT, DEFAULT] : ({t4}, {tkT}) -> {ts}")
+    else:
+        sc = e(f"stablehlo.dot_general %arg0, %arg1, batching_dims = [0, 1] x [0, 1], contracting_dims = [3] x [3], "
+               f"precision = [DEFAULT, DEFAULT] : ({t4}, {t4}) -> {ts}")
+    sc = e.bin("multiply", sc, e.splat(f"{D ** -0.5:.6e}", "bf16", [B, H, S, S]), ts)
+    ti, tm = _t([S], "i32"), _t([S, S], "i32")
+    io = e(f"stablehlo.iota dim = 0 : {ti}")
+    r = e.bcast(e.bcast(io, ti, [0], _t([S, 1], "i32")), _t([S, 1], "i32"), [0, 1], tm)
+    c = e.bcast(e.bcast(io, ti, [1], _t([1, S], "i32")), _t([1, S], "i32"), [0, 1], tm)
+    m = e(f"stablehlo.compare  {mask}, {r}, {c},  SIGNED : ({tm}, {tm}) -> {_t([S, S], 'i1')}")
+    mb = e.bcast(m, _t([S, S], "i1"), [2, 3], _t([B, H, S, S], "i1"))
+    x = e(f"stablehlo.select {mb}, {sc}, {e.splat(_NEG_INF['bf16'], 'bf16', [B, H, S, S])} : "
+          f"{_t([B, H, S, S], 'i1')}, {ts}")
+    p = _softmax_bf16(e, x, [B, H, S, S])
+    o = e(f"stablehlo.dot_general {p}, %arg2, batching_dims = [0, 1] x [0, 1], contracting_dims = [3] x [2], "
+          f"precision = [DEFAULT, DEFAULT] : ({ts}, {t4}) -> {t4}")
+    tout = _t([B, S, H, D], "bf16")
+    out = e.transpose(o, t4, [0, 2, 1, 3], tout)
+    return _module("jit_attention", [t4, t4, t4], [tout], e.lines + [f"return {out} : {tout}"])
 
 
 def decoder_layer(B, S, hidden, heads, head_dim, ffn, eps="9.99999997E-7"):

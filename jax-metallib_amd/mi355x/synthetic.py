@@ -49,3 +49,42 @@ def int8_case(rng, M, K, N):
     w = rng.integers(-127, 128, size=(K, N), dtype=np.int16).astype(np.int8)
     s = rng.uniform(1e-3, 1e-2, size=(N,)).astype(np.float32)
     return x, w, s
+
+
+def decoder_layer_case(rng, B, S, hidden, heads, head_dim, ffn, rope_base=10000.0):
+    """One random-init layer of the Llama-style decoder and its input:
+    (x bf16 bits [B*S, hidden], weights, cos, sin).  weights holds g_attn,
+    g_mlp (bf16 bits, U(0.5, 1.5)) and w_qkv, w_o, w_gate, w_up, w_down as
+    int4 g64 (packed, scale bf16 bits, zero) with s ~ U(0.004, 0.006), scales
+    that keep a random layer's activations O(1); cos / sin f32 [S, head_dim/2]
+    of positions 0..S-1 at frequencies rope_base^(-2i/head_dim)."""
+    A = heads * head_dim
+
+    def weight(K, N):
+        q = rng.integers(0, 16, size=(K, N), dtype=np.uint8)
+        s = bf16_bits(rng.uniform(0.004, 0.006, size=(K // GROUP, N)).astype(np.float32))
+        z = rng.integers(0, 16, size=(K // GROUP, N), dtype=np.uint8)
+        return pack_nibbles(q), s, z
+
+    x = bf16_bits(rng.standard_normal((B * S, hidden)).astype(np.float32))
+    g1 = bf16_bits(rng.uniform(0.5, 1.5, size=hidden).astype(np.float32))
+    g2 = bf16_bits(rng.uniform(0.5, 1.5, size=hidden).astype(np.float32))
+    w = {"g_attn": g1, "g_mlp": g2, "w_qkv": weight(hidden, 3 * A), "w_o": weight(A, hidden),
+         "w_gate": weight(hidden, ffn), "w_up": weight(hidden, ffn), "w_down": weight(ffn, hidden)}
+    half = head_dim // 2
+    inv = rope_base ** (-np.arange(half, dtype=np.float64) * 2.0 / head_dim)
+    ang = np.arange(S, dtype=np.float64)[:, None] * inv[None, :]
+    return x, w, np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+def decoder_layer_arguments(x, w, cos, sin):
+    """The arguments of programs.decoder_layer in order, as (array, is_bf16)."""
+    args = [(x, True), (w["g_attn"], True)]
+    for name in ("w_qkv", "w_o"):
+        p, s, z = w[name]
+        args += [(p, False), (s, True), (z, False)]
+    args.append((w["g_mlp"], True))
+    for name in ("w_gate", "w_up", "w_down"):
+        p, s, z = w[name]
+        args += [(p, False), (s, True), (z, False)]
+    return args + [(cos, False), (sin, False)]

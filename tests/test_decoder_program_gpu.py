@@ -14,9 +14,9 @@ import pytest
 
 from mi355x import programs as P
 from mi355x import runtime as rt
+from mi355x import synthetic
 from oracle import decoder as odec
-from oracle import quant
-from oracle.bf16 import bf16_bits_to_f32, f32_to_bf16_bits
+from oracle.bf16 import bf16_bits_to_f32
 
 from _gpu import BF16_RTOL
 
@@ -33,41 +33,15 @@ def client():
     c.close()
 
 
-def _weight(rng, K, N):
-    """int4 g64 weight (packed, scale bits, zero) with q, z ~ U{0..15} and
-    s ~ U(0.004, 0.006): scales that keep a random layer's activations O(1)."""
-    q = rng.integers(0, 16, size=(K, N), dtype=np.uint8)
-    s = f32_to_bf16_bits(rng.uniform(0.004, 0.006, size=(K // 64, N)).astype(np.float32))
-    z = rng.integers(0, 16, size=(K // 64, N), dtype=np.uint8)
-    return quant.pack_int4_k(q), s, z
-
-
-def _layer_case(seed, B, S, hidden, H, D, F):
-    rng = np.random.default_rng(seed)
-    A = H * D
-    x = f32_to_bf16_bits(rng.standard_normal((B * S, hidden)).astype(np.float32))
-    g1 = f32_to_bf16_bits(rng.uniform(0.5, 1.5, size=hidden).astype(np.float32))
-    g2 = f32_to_bf16_bits(rng.uniform(0.5, 1.5, size=hidden).astype(np.float32))
-    w = {"g_attn": g1, "g_mlp": g2, "w_qkv": _weight(rng, hidden, 3 * A), "w_o": _weight(rng, A, hidden),
-         "w_gate": _weight(rng, hidden, F), "w_up": _weight(rng, hidden, F), "w_down": _weight(rng, F, hidden)}
-    cos, sin = odec.rope_tables(S, D)
-    return x, w, cos.astype(np.float32), sin.astype(np.float32)
-
-
-def _run_layer(client, B, S, hidden, H, D, F, x, w, cos, sin):
+def _run_layer(client, B, S, hidden, H, D, F, seed):
+    """Compile the layer's StableHLO, run it once on a synthetic case;
+    returns (output [B, S, hidden] as float32, x bits, weights, plan text)."""
+    x, w, cos, sin = synthetic.decoder_layer_case(np.random.default_rng(seed), B, S, hidden, H, D, F)
     text = P.decoder_layer(B, S, hidden, H, D, F)
     print(f"[decoder-program] B={B} S={S} hidden={hidden} H={H} D={D} F={F}", flush=True)
     exe = client.compile(text)
-    bf = lambda a: client.buffer(np.ascontiguousarray(a, dtype=np.uint16), rt.BF16)
-    args = [bf(x), bf(w["g_attn"])]
-    for name in ("w_qkv", "w_o"):
-        p, s, z = w[name]
-        args += [client.buffer(p), bf(s), client.buffer(z)]
-    args.append(bf(w["g_mlp"]))
-    for name in ("w_gate", "w_up", "w_down"):
-        p, s, z = w[name]
-        args += [client.buffer(p), bf(s), client.buffer(z)]
-    args += [client.buffer(cos), client.buffer(sin)]
+    args = [client.buffer(a, rt.BF16) if is_bf16 else client.buffer(a)
+            for a, is_bf16 in synthetic.decoder_layer_arguments(x, w, cos, sin)]
     outs, done = exe.execute(args)
     done.wait()
     (y,) = [o.to_numpy() for o in outs]
@@ -75,7 +49,7 @@ def _run_layer(client, B, S, hidden, H, D, F, x, w, cos, sin):
     for b in args + outs:
         b.close()
     exe.close()
-    return bf16_bits_to_f32(y).reshape(B, S, hidden), plan
+    return bf16_bits_to_f32(y).reshape(B, S, hidden), x, w, plan
 
 
 def _check_rows(y, x, w, B, S, hidden, H, D, pos, batches):
@@ -89,24 +63,111 @@ def _check_rows(y, x, w, B, S, hidden, H, D, pos, batches):
         assert row_rel.max() <= BF16_RTOL, (b, pos[int(row_rel.argmax())], row_rel.max())
 
 
+@pytest.mark.parametrize("fused", [True, False], ids=["decoder-kernels", "op-by-op"])
 @pytest.mark.parametrize("B,S,hidden,H,D,F", [(1, 64, 128, 2, 64, 256), (2, 128, 256, 2, 128, 512)])
-def test_decoder_program_small_vs_oracle(client, B, S, hidden, H, D, F):
-    x, w, cos, sin = _layer_case(B * 1000 + S, B, S, hidden, H, D, F)
-    y, plan = _run_layer(client, B, S, hidden, H, D, F, x, w, cos, sin)
-    # the projections, norms and attention products run on their kernels
+def test_decoder_program_small_vs_oracle(client, monkeypatch, B, S, hidden, H, D, F, fused):
+    if not fused:
+        monkeypatch.setenv("MK_PLAN_DECODER_FUSION", "0")
+    y, x, w, plan = _run_layer(client, B, S, hidden, H, D, F, seed=B * 1000 + S)
+    # the projections and norms run on their kernels; RoPE and attention on
+    # the decoder kernels where their shapes allow (head_dim 128, S % 128)
     assert plan.count("int4_g64_matmul") == 5 and plan.count("rmsnorm") == 2
-    assert "softmax" in plan and plan.count("gemm_bf16") == 2
+    if fused and D == 128:
+        assert "rope_qkv_split" in plan and "attention_causal" in plan and "softmax" not in plan
+    else:
+        assert "softmax" in plan and plan.count("gemm_bf16") == 2 and "attention_causal" not in plan
     _check_rows(y, x, w, B, S, hidden, H, D, np.arange(S), range(B))
 
 
-def test_decoder_program_full_config_vs_oracle(client):
+@pytest.mark.parametrize("fused", [True, False], ids=["decoder-kernels", "op-by-op"])
+def test_decoder_program_full_config_vs_oracle(client, monkeypatch, fused):
     """The workload's decoder layer (hidden 2048, 16 x 128 heads, SwiGLU 8192,
     batch 4 x 2048 tokens) compiled from StableHLO, checked on batch elements
     0 and 3 at 16 positions (first and last rows, tile boundaries, random)."""
+    if not fused:
+        monkeypatch.setenv("MK_PLAN_DECODER_FUSION", "0")
     B, S, hidden, H, D, F = 4, 2048, 2048, 16, 128, 8192
-    x, w, cos, sin = _layer_case(7, B, S, hidden, H, D, F)
-    y, _ = _run_layer(client, B, S, hidden, H, D, F, x, w, cos, sin)
+    y, x, w, plan = _run_layer(client, B, S, hidden, H, D, F, seed=7)
+    assert ("attention_causal" in plan) == fused
     assert np.isfinite(y).all()
     rng = np.random.default_rng(3)
     pos = np.unique(np.concatenate([[0, 1, 63, 64, 1023, 2047], rng.integers(2, S - 1, size=10)]))
     _check_rows(y, x, w, B, S, hidden, H, D, pos, (0, B - 1))
+
+
+@pytest.mark.parametrize("fused", [True, False], ids=["decoder-kernels", "op-by-op"])
+@pytest.mark.parametrize("transpose_k", [True, False], ids=["k-transposed", "k-last-axis"])
+def test_causal_attention_program_vs_oracle(client, monkeypatch, transpose_k, fused):
+    """softmax(where(causal, q k^T / sqrt(D), -inf)) @ v from its StableHLO,
+    against the oracle's causal attention per (b, h) row block, at the bf16
+    measure per row; row 0 sees only key 0, so it must equal v[0] to bf16
+    rounding."""
+    if not fused:
+        monkeypatch.setenv("MK_PLAN_DECODER_FUSION", "0")
+    B, H, S, D = 2, 3, 256, 128
+    rng = np.random.default_rng(11)
+    q, k, v = (synthetic.bf16_bits(rng.standard_normal((B, H, S, D)).astype(np.float32)) for _ in range(3))
+    print(f"[decoder-program] attention B={B} H={H} S={S} fused={fused} transpose_k={transpose_k}", flush=True)
+    exe = client.compile(P.causal_attention(B, H, S, D, transpose_k=transpose_k))
+    assert ("attention_causal" in exe.plan) == fused
+    args = [client.buffer(a, rt.BF16) for a in (q, k, v)]
+    outs, done = exe.execute(args)
+    done.wait()
+    y = bf16_bits_to_f32(outs[0].to_numpy()).astype(np.float64)  # [B, S, H, D]
+    for b_ in args + outs:
+        b_.close()
+    exe.close()
+    qf, kf, vf = (bf16_bits_to_f32(a).astype(np.float64) for a in (q, k, v))
+    scale = float(bf16_bits_to_f32(synthetic.bf16_bits(np.array([D ** -0.5], np.float32)))[0])
+    pos = np.arange(S)
+    for b_ in range(B):
+        for h in range(H):
+            ref = odec.attention_causal_rows(qf[b_, h], pos, kf[b_, h], vf[b_, h], scale)
+            got = y[b_, :, h]
+            row_rel = np.abs(got - ref).max(axis=1) / np.abs(ref).max(axis=1)
+            assert row_rel.max() <= BF16_RTOL, (b_, h, row_rel.max())
+            assert np.allclose(got[0], vf[b_, h, 0], rtol=2 ** -7, atol=0)
+
+
+def test_store_epilogues_are_bit_identical(client, monkeypatch):
+    """The planner folds the residual adds and silu(g) * u into the
+    dequant-matmul's store; the layer's output must equal, bit for bit, the
+    plan that runs them as elementwise programs."""
+    B, S, hidden, H, D, F = 2, 128, 256, 2, 128, 512
+    y1, _, _, plan1 = _run_layer(client, B, S, hidden, H, D, F, seed=21)
+    monkeypatch.setenv("MK_PLAN_EPILOGUES", "0")
+    y0, _, _, plan0 = _run_layer(client, B, S, hidden, H, D, F, seed=21)
+    assert "epilogue" in plan1 and "epilogue" not in plan0
+    assert np.array_equal(y1.view(np.uint32), y0.view(np.uint32))
+
+
+@pytest.mark.parametrize("op", ["add", "swiglu"])
+@pytest.mark.parametrize("fmt,M", [("int4", 16), ("int4", 256), ("int4", 1024), ("int8", 16), ("int8", 1024)])
+def test_qmm_epilogue_programs_bit_identical(client, monkeypatch, fmt, M, op):
+    """aux + qmm(x, W) and silu(aux) * qmm(x, W) at every quantized route
+    (streaming, fused many-row, dequantise-then-GEMM): the epilogue plan
+    against the two-step plan, bit for bit."""
+    K, N = 256, 512
+    rng = np.random.default_rng(M + len(op))
+    if fmt == "int4":
+        x, p, s_, z = synthetic.int4_case(rng, M, K, N)
+        w = [(x, rt.BF16), (p, None), (s_, rt.BF16), (z, None)]
+    else:
+        x, w8, s8 = synthetic.int8_case(rng, M, K, N)
+        w = [(x, rt.BF16), (w8, None), (s8, None)]
+    aux = synthetic.bf16_bits(rng.standard_normal((M, N)).astype(np.float32))
+    text = P.qmm_epilogue(M, K, N, fmt, op)
+    outs = []
+    for env in ("1", "0"):
+        monkeypatch.setenv("MK_PLAN_EPILOGUES", env)
+        print(f"[decoder-program] {fmt} M={M} {op} epilogues={env}", flush=True)
+        exe = client.compile(text)
+        assert ("epilogue" in exe.plan) == (env == "1")
+        args = [client.buffer(aux, rt.BF16)] + [client.buffer(a, t) if t else client.buffer(a) for a, t in w]
+        res, done = exe.execute(args)
+        done.wait()
+        outs.append(res[0].to_numpy())
+        for b_ in args + res:
+            b_.close()
+        exe.close()
+    assert np.array_equal(outs[0], outs[1])

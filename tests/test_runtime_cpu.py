@@ -264,6 +264,16 @@ def test_residual_add_keeps_the_dequant_matmul():
     assert plan(t) == ["int4_g64_matmul M=16 K=128 N=256 -> bf16", "elementwise 2 instr, 1 inputs, n=4096 bf16"]
 
 
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+def test_residual_and_swiglu_fold_into_the_dequant_matmul(fmt, monkeypatch):
+    name = "int4_g64_matmul" if fmt == "int4" else "int8_pc_matmul"
+    assert plan(P.qmm_epilogue(256, 128, 256, fmt, "add")) == [f"{name} M=256 K=128 N=256 -> bf16 + add epilogue"]
+    assert plan(P.qmm_epilogue(256, 128, 256, fmt, "swiglu")) == [f"{name} M=256 K=128 N=256 -> bf16 + swiglu epilogue"]
+    monkeypatch.setenv("MK_PLAN_EPILOGUES", "0")
+    assert plan(P.qmm_epilogue(256, 128, 256, fmt, "add")) == [f"{name} M=256 K=128 N=256 -> bf16",
+                                               "elementwise 3 instr, 2 inputs, n=65536 bf16"]
+
+
 def test_decoder_layer_plans_onto_the_kernels():
     """The Llama layer's StableHLO: projections on the dequant-matmul, norms
     and softmax on their row kernels, the two attention products on the bf16
@@ -277,6 +287,44 @@ def test_decoder_layer_plans_onto_the_kernels():
     assert "softmax rows=256 cols=64 bf16" in steps
     # the causal mask is folded at compile time into the select's program
     assert not any(s.startswith("iota") for s in steps)
+
+
+def test_decoder_layer_routes_rope_and_attention_to_the_decoder_kernels(monkeypatch):
+    """With head_dim 128 and S % 128 == 0 the RoPE chain becomes one
+    rope/split step and the masked-softmax attention one fused step writing
+    the merged [B, S, H, D] layout; MK_PLAN_DECODER_FUSION=0 keeps the
+    op-by-op plan."""
+    text = P.decoder_layer(2, 128, 256, 2, 128, 512)
+    assert plan(text) == [
+        "rmsnorm rows=256 cols=256 eps=9.98378e-07 bf16",
+        "int4_g64_matmul M=256 K=256 N=768 -> bf16",
+        "rope_qkv_split B=2 S=128 H=2 D=128 bf16",
+        "attention_causal B=2 H=2 S=128 D=128 scale=0.0883789 bf16",
+        "int4_g64_matmul M=256 K=256 N=256 -> bf16 + add epilogue",
+        "rmsnorm rows=256 cols=256 eps=9.98378e-07 bf16",
+        "int4_g64_matmul M=256 K=256 N=512 -> bf16",
+        "int4_g64_matmul M=256 K=256 N=512 -> bf16 + swiglu epilogue",
+        "int4_g64_matmul M=256 K=512 N=256 -> bf16 + add epilogue",
+    ]
+    monkeypatch.setenv("MK_PLAN_EPILOGUES", "0")
+    steps = plan(text)
+    assert not any("epilogue" in s for s in steps) and len(steps) == 12
+    monkeypatch.setenv("MK_PLAN_DECODER_FUSION", "0")
+    kinds = [s.split()[0] for s in plan(text)]
+    assert "attention_causal" not in kinds and "rope_qkv_split" not in kinds
+    assert kinds.count("softmax") == 1 and kinds.count("gemm_bf16") == 2
+
+
+def test_attention_route_needs_the_causal_mask():
+    want = ["attention_causal B=1 H=2 S=128 D=128 scale=0.0883789 bf16"]
+    assert plan(P.causal_attention(1, 2, 128, 128)) == want
+    # k contracted on its last axis (einsum 'bhqd,bhkd->bhqk'), no transpose
+    assert plan(P.causal_attention(1, 2, 128, 128, transpose_k=False)) == want
+    # an anti-causal or strict mask is not this kernel's: op by op
+    for op in ("LE", "GT"):
+        steps = plan(P.causal_attention(1, 2, 128, 128, mask=op))
+        assert not any(s.startswith("attention_causal") for s in steps), (op, steps)
+        assert any(s.startswith("softmax") for s in steps)
 
 
 def test_argmax_values_result_is_rejected():
