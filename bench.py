@@ -534,6 +534,12 @@ def bench_end_to_end(warmup=10, iters=50):
             programs.decoder_layer(4, 2048, 2048, 16, 128, 8192),
             [(arr, runtime.BF16 if is_bf16 else None)
              for arr, is_bf16 in synthetic.decoder_layer_arguments(xl, wl, cos, sin)])
+        # the workload's whole forward (4 layers) as one jitted function
+        xs, wss, cos, sin = synthetic.decoder_stack_case(rng, 4, 4, 2048, 2048, 16, 128, 8192)
+        cases["decoder_stack_4x_B4_S2048"] = (
+            programs.decoder_stack(4, 4, 2048, 2048, 16, 128, 8192),
+            [(arr, runtime.BF16 if is_bf16 else None)
+             for arr, is_bf16 in synthetic.decoder_stack_arguments(xs, wss, cos, sin)])
         for name, (text, arrays) in cases.items():
             t0 = time.perf_counter()
             exe = client.compile(text)
@@ -688,6 +694,21 @@ def main():
         secondary["plugin_end_to_end"] = {
             "what": "mkrt_compile once, then mkrt_execute + event await per call, inputs resident; "
                     "wall clock on the host, not kernel time", **e2e}
+        st = e2e.get("decoder_stack_4x_B4_S2048")
+        if st:
+            from mi355x import decoder
+            cfg = decoder.DecoderConfig()
+            ms = st["median_us"] / 1e3
+            tf = cfg.matmul_flops() / ms / 1e9
+            log(f"[bench] decoder forward through jit (compile -> execute): {ms:.3f} ms, "
+                f"{cfg.tokens / ms * 1e3:.0f} tokens/s, {tf:.1f} TFLOP/s")
+            secondary["llama_decoder_forward_jit_4x2048_b4s2048_int4"] = {
+                "what": "the 4-layer forward's StableHLO (mi355x/programs.decoder_stack) compiled once by the "
+                        "plugin runtime, median of execute + await (host wall clock)",
+                "value": round(cfg.tokens / ms * 1e3, 1), "unit": "tokens/s", "ms_per_forward": round(ms, 4),
+                "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                             "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None},
+                "plan_steps": st["steps"]}
 
     cpu = None
     if not args.no_cpu:

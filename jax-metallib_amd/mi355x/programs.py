@@ -534,25 +534,55 @@ def decoder_layer(B, S, hidden, heads, head_dim, ffn, eps="9.99999997E-7"):
     int4_g64_matmul.  Arguments: x bf16 [B*S, hidden]; g_attn bf16 [hidden];
     w_qkv (3 arrays); w_o; g_mlp; w_gate; w_up; w_down; cos, sin f32
     [S, head_dim/2].  The qkv columns are q | k | v, each heads x head_dim."""
+    e = _Body()
+    args, out = _decoder_args_and_layers(e, 1, B, S, hidden, heads, head_dim, ffn, eps)
+    tx = _t([B * S, hidden], "bf16")
+    return _module("jit_layer", args, [tx], e.lines + [f"return {out} : {tx}"])
+
+
+def decoder_stack(layers, B, S, hidden, heads, head_dim, ffn, eps="9.99999997E-7"):
+    """The decoder forward of `layers` layers as one jitted function
+    (jax.jit of ``for w in weights: x = layer(x, *w, cos, sin)``): arguments
+    x, then each layer's 17 weight arrays in decoder_layer's order, then cos
+    and sin; returns the last layer's output [B*S, hidden] bf16."""
+    e = _Body()
+    args, out = _decoder_args_and_layers(e, layers, B, S, hidden, heads, head_dim, ffn, eps)
+    tx = _t([B * S, hidden], "bf16")
+    return _module("jit_decoder", args, [tx], e.lines + [f"return {out} : {tx}"])
+
+
+def _decoder_args_and_layers(e, layers, B, S, hidden, heads, head_dim, ffn, eps):
+    """Argument types (x, per layer g_attn w_qkv(3) w_o(3) g_mlp w_gate(3)
+    w_up(3) w_down(3), cos, sin) and the ops of `layers` layers into e;
+    returns (arg types, name of the last output)."""
     H, D, T, A, F = heads, head_dim, B * S, heads * head_dim, ffn
     Dh = D // 2
-    e = _Body()
 
-    def wargs(i, K, N):
-        return [f"%arg{i}", f"%arg{i + 1}", f"%arg{i + 2}"], [_t([K // 2, N], "ui8"), _t([K // 64, N], "bf16"),
-                                                             _t([K // 64, N], "ui8")]
+    def w3(K, N):
+        return [_t([K // 2, N], "ui8"), _t([K // 64, N], "bf16"), _t([K // 64, N], "ui8")]
 
-    args = [_t([T, hidden], "bf16"), _t([hidden], "bf16")]
-    wqkv, t = wargs(2, hidden, 3 * A); args += t
-    wo, t = wargs(5, A, hidden); args += t
-    args.append(_t([hidden], "bf16"))
-    wg, t = wargs(9, hidden, F); args += t
-    wu, t = wargs(12, hidden, F); args += t
-    wd, t = wargs(15, F, hidden); args += t
-    args += [_t([S, Dh], "f32"), _t([S, Dh], "f32")]
+    per_layer = ([_t([hidden], "bf16")] + w3(hidden, 3 * A) + w3(A, hidden) + [_t([hidden], "bf16")] +
+                 w3(hidden, F) + w3(hidden, F) + w3(F, hidden))
+    args = [_t([T, hidden], "bf16")] + per_layer * layers + [_t([S, Dh], "f32"), _t([S, Dh], "f32")]
+    cos_arg, sin_arg = f"%arg{1 + 17 * layers}", f"%arg{2 + 17 * layers}"
+    th, t4 = _t([B, S, H, Dh], "f32"), _t([1, S, 1, Dh], "f32")
+    c = e.bcast(e.reshape(cos_arg, _t([S, Dh], "f32"), t4), t4, [0, 1, 2, 3], th)
+    s = e.bcast(e.reshape(sin_arg, _t([S, Dh], "f32"), t4), t4, [0, 1, 2, 3], th)
+    x = "%arg0"
+    for l in range(layers):
+        base = 1 + 17 * l
+        a = [f"%arg{base + i}" for i in range(17)]
+        x = _decoder_layer_ops(e, x, a, c, s, B, S, hidden, H, D, F, eps)
+    return args, x
 
+
+def _decoder_layer_ops(e, x, a, c, s, B, S, hidden, H, D, F, eps):
+    """One layer's ops: x [B*S, hidden]; a = the layer's 17 argument names;
+    c, s the broadcast RoPE tables [B, S, H, D/2]."""
+    T, A, Dh = B * S, H * D, D // 2
+    g1, wqkv, wo, g2, wg, wu, wd = a[0], a[1:4], a[4:7], a[7], a[8:11], a[11:14], a[14:17]
     tb = _t([B, S, H, D], "bf16")
-    h = _rmsnorm_bf16(e, "%arg0", "%arg1", T, hidden, eps)
+    h = _rmsnorm_bf16(e, x, g1, T, hidden, eps)
     qkv = e.reshape(_int4_mm(e, h, *wqkv, T, hidden, 3 * A), _t([T, 3 * A], "bf16"), _t([B, S, 3, H, D], "bf16"))
     parts = []
     for j in range(3):
@@ -560,16 +590,14 @@ def decoder_layer(B, S, hidden, heads, head_dim, ffn, eps="9.99999997E-7"):
                      _t([B, S, 1, H, D], "bf16"))
         parts.append(e.reshape(sl, _t([B, S, 1, H, D], "bf16"), tb))
     q, k, v = parts
-    th, tf, t4 = _t([B, S, H, Dh], "f32"), _t([B, S, H, D], "f32"), _t([1, S, 1, Dh], "f32")
-    c = e.bcast(e.reshape("%arg18", _t([S, Dh], "f32"), t4), t4, [0, 1, 2, 3], th)
-    s = e.bcast(e.reshape("%arg19", _t([S, Dh], "f32"), t4), t4, [0, 1, 2, 3], th)
+    th, tf = _t([B, S, H, Dh], "f32"), _t([B, S, H, D], "f32")
 
-    def rope(x):
-        xf = e.cvt(x, tb, tf)
-        x0 = e.slice(xf, tf, [(0, B), (0, S), (0, H), (0, Dh)], th)
-        x1 = e.slice(xf, tf, [(0, B), (0, S), (0, H), (Dh, D)], th)
-        lo = e.bin("subtract", e.bin("multiply", x0, c, th), e.bin("multiply", x1, s, th), th)
-        hi = e.bin("add", e.bin("multiply", x1, c, th), e.bin("multiply", x0, s, th), th)
+    def rope(t):
+        tf_ = e.cvt(t, tb, tf)
+        t0 = e.slice(tf_, tf, [(0, B), (0, S), (0, H), (0, Dh)], th)
+        t1 = e.slice(tf_, tf, [(0, B), (0, S), (0, H), (Dh, D)], th)
+        lo = e.bin("subtract", e.bin("multiply", t0, c, th), e.bin("multiply", t1, s, th), th)
+        hi = e.bin("add", e.bin("multiply", t1, c, th), e.bin("multiply", t0, s, th), th)
         cat = e(f"stablehlo.concatenate {lo}, {hi}, dim = 3 : ({th}, {th}) -> {tf}")
         return e.cvt(cat, tf, tb)
 
@@ -593,13 +621,12 @@ def decoder_layer(B, S, hidden, heads, head_dim, ffn, eps="9.99999997E-7"):
     p = _softmax_bf16(e, sc, [B, H, S, S])
     o = e(f"stablehlo.dot_general {p}, {vt}, batching_dims = [0, 1] x [0, 1], contracting_dims = [3] x [2], "
           f"precision = [DEFAULT, DEFAULT] : ({tsc}, {tbh}) -> {tbh}")
-    a = e.reshape(e.transpose(o, tbh, [0, 2, 1, 3], tb), tb, _t([T, A], "bf16"))
+    att = e.reshape(e.transpose(o, tbh, [0, 2, 1, 3], tb), tb, _t([T, A], "bf16"))
     tx = _t([T, hidden], "bf16")
-    x1 = e.bin("add", "%arg0", _int4_mm(e, a, *wo, T, A, hidden), tx)
-    h2 = _rmsnorm_bf16(e, x1, "%arg8", T, hidden, eps)
+    x1 = e.bin("add", x, _int4_mm(e, att, *wo, T, A, hidden), tx)
+    h2 = _rmsnorm_bf16(e, x1, g2, T, hidden, eps)
     tfb = _t([T, F], "bf16")
     gt = _int4_mm(e, h2, *wg, T, hidden, F)
     up = _int4_mm(e, h2, *wu, T, hidden, F)
     act = e.bin("multiply", e.bin("multiply", gt, e.un("logistic", gt, tfb), tfb), up, tfb)
-    out = e.bin("add", x1, _int4_mm(e, act, *wd, T, F, hidden), tx)
-    return _module("jit_layer", args, [tx], e.lines + [f"return {out} : {tx}"])
+    return e.bin("add", x1, _int4_mm(e, act, *wd, T, F, hidden), tx)

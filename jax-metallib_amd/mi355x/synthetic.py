@@ -51,7 +51,23 @@ def int8_case(rng, M, K, N):
     return x, w, s
 
 
-def decoder_layer_case(rng, B, S, hidden, heads, head_dim, ffn, rope_base=10000.0):
+def decoder_stack_case(rng, layers, B, S, hidden, heads, head_dim, ffn, rope_base=10000.0):
+    """decoder_layer_case for `layers` layers: (x, [weights per layer], cos, sin)."""
+    x, w, cos, sin = decoder_layer_case(rng, B, S, hidden, heads, head_dim, ffn, rope_base)
+    ws = [w] + [decoder_layer_case(rng, 1, 1, hidden, heads, head_dim, ffn, rope_base, weights_only=True)
+                for _ in range(layers - 1)]
+    return x, ws, cos, sin
+
+
+def decoder_stack_arguments(x, ws, cos, sin):
+    """The arguments of programs.decoder_stack in order, as (array, is_bf16)."""
+    args = [(x, True)]
+    for w in ws:
+        args += decoder_layer_arguments(None, w, None, None)[1:-2]
+    return args + [(cos, False), (sin, False)]
+
+
+def decoder_layer_case(rng, B, S, hidden, heads, head_dim, ffn, rope_base=10000.0, weights_only=False):
     """One random-init layer of the Llama-style decoder and its input:
     (x bf16 bits [B*S, hidden], weights, cos, sin).  weights holds g_attn,
     g_mlp (bf16 bits, U(0.5, 1.5)) and w_qkv, w_o, w_gate, w_up, w_down as
@@ -66,11 +82,13 @@ def decoder_layer_case(rng, B, S, hidden, heads, head_dim, ffn, rope_base=10000.
         z = rng.integers(0, 16, size=(K // GROUP, N), dtype=np.uint8)
         return pack_nibbles(q), s, z
 
-    x = bf16_bits(rng.standard_normal((B * S, hidden)).astype(np.float32))
+    x = None if weights_only else bf16_bits(rng.standard_normal((B * S, hidden)).astype(np.float32))
     g1 = bf16_bits(rng.uniform(0.5, 1.5, size=hidden).astype(np.float32))
     g2 = bf16_bits(rng.uniform(0.5, 1.5, size=hidden).astype(np.float32))
     w = {"g_attn": g1, "g_mlp": g2, "w_qkv": weight(hidden, 3 * A), "w_o": weight(A, hidden),
          "w_gate": weight(hidden, ffn), "w_up": weight(hidden, ffn), "w_down": weight(ffn, hidden)}
+    if weights_only:
+        return w
     half = head_dim // 2
     inv = rope_base ** (-np.arange(half, dtype=np.float64) * 2.0 / head_dim)
     ang = np.arange(S, dtype=np.float64)[:, None] * inv[None, :]

@@ -171,3 +171,31 @@ def test_qmm_epilogue_programs_bit_identical(client, monkeypatch, fmt, M, op):
             b_.close()
         exe.close()
     assert np.array_equal(outs[0], outs[1])
+
+
+def test_decoder_stack_vs_oracle(client):
+    """Two layers as one jitted function (programs.decoder_stack), against
+    the oracle's layer applied twice on every row, each oracle layer fed the
+    oracle's previous output."""
+    B, S, hidden, H, D, F, L = 2, 128, 256, 2, 128, 512, 2
+    x, ws, cos, sin = synthetic.decoder_stack_case(np.random.default_rng(31), L, B, S, hidden, H, D, F)
+    print(f"[decoder-program] stack L={L} B={B} S={S}", flush=True)
+    exe = client.compile(P.decoder_stack(L, B, S, hidden, H, D, F))
+    assert exe.plan.count("attention_causal") == L
+    args = [client.buffer(a, rt.BF16) if is_bf16 else client.buffer(a)
+            for a, is_bf16 in synthetic.decoder_stack_arguments(x, ws, cos, sin)]
+    outs, done = exe.execute(args)
+    done.wait()
+    y = bf16_bits_to_f32(outs[0].to_numpy()).reshape(B, S, hidden).astype(np.float64)
+    for b_ in args + outs:
+        b_.close()
+    exe.close()
+    x3 = bf16_bits_to_f32(x).reshape(B, S, hidden)
+    pos = np.arange(S)
+    for b in range(B):
+        ref = x3[b].astype(np.float64)
+        for w in ws:
+            ref = odec.layer_rows(ref, pos, w, H, D)
+        row_rel = np.abs(y[b] - ref).max(axis=1) / np.abs(ref).max(axis=1)
+        print(f"[decoder-program] stack batch {b}: worst row rel err {row_rel.max():.3e}", flush=True)
+        assert row_rel.max() <= BF16_RTOL, (b, row_rel.max())
