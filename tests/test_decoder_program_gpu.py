@@ -134,6 +134,7 @@ def test_store_epilogues_are_bit_identical(client, monkeypatch):
     dequant-matmul's store; the layer's output must equal, bit for bit, the
     plan that runs them as elementwise programs."""
     B, S, hidden, H, D, F = 2, 128, 256, 2, 128, 512
+    monkeypatch.setenv("MK_PLAN_EPILOGUES", "all")
     y1, _, _, plan1 = _run_layer(client, B, S, hidden, H, D, F, seed=21)
     monkeypatch.setenv("MK_PLAN_EPILOGUES", "0")
     y0, _, _, plan0 = _run_layer(client, B, S, hidden, H, D, F, seed=21)
@@ -158,11 +159,11 @@ def test_qmm_epilogue_programs_bit_identical(client, monkeypatch, fmt, M, op):
     aux = synthetic.bf16_bits(rng.standard_normal((M, N)).astype(np.float32))
     text = P.qmm_epilogue(M, K, N, fmt, op)
     outs = []
-    for env in ("1", "0"):
+    for env in ("all", "0"):
         monkeypatch.setenv("MK_PLAN_EPILOGUES", env)
         print(f"[decoder-program] {fmt} M={M} {op} epilogues={env}", flush=True)
         exe = client.compile(text)
-        assert ("epilogue" in exe.plan) == (env == "1")
+        assert ("epilogue" in exe.plan) == (env == "all")
         args = [client.buffer(aux, rt.BF16)] + [client.buffer(a, t) if t else client.buffer(a) for a, t in w]
         res, done = exe.execute(args)
         done.wait()

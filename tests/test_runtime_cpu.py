@@ -268,6 +268,9 @@ def test_residual_add_keeps_the_dequant_matmul():
 def test_residual_and_swiglu_fold_into_the_dequant_matmul(fmt, monkeypatch):
     name = "int4_g64_matmul" if fmt == "int4" else "int8_pc_matmul"
     assert plan(P.qmm_epilogue(256, 128, 256, fmt, "add")) == [f"{name} M=256 K=128 N=256 -> bf16 + add epilogue"]
+    assert plan(P.qmm_epilogue(256, 128, 256, fmt, "swiglu")) == [f"{name} M=256 K=128 N=256 -> bf16",
+                                                                   "elementwise 5 instr, 2 inputs, n=65536 bf16"]
+    monkeypatch.setenv("MK_PLAN_EPILOGUES", "all")
     assert plan(P.qmm_epilogue(256, 128, 256, fmt, "swiglu")) == [f"{name} M=256 K=128 N=256 -> bf16 + swiglu epilogue"]
     monkeypatch.setenv("MK_PLAN_EPILOGUES", "0")
     assert plan(P.qmm_epilogue(256, 128, 256, fmt, "add")) == [f"{name} M=256 K=128 N=256 -> bf16",
@@ -303,9 +306,12 @@ def test_decoder_layer_routes_rope_and_attention_to_the_decoder_kernels(monkeypa
         "int4_g64_matmul M=256 K=256 N=256 -> bf16 + add epilogue",
         "rmsnorm rows=256 cols=256 eps=9.98378e-07 bf16",
         "int4_g64_matmul M=256 K=256 N=512 -> bf16",
-        "int4_g64_matmul M=256 K=256 N=512 -> bf16 + swiglu epilogue",
+        "int4_g64_matmul M=256 K=256 N=512 -> bf16",
+        "elementwise 5 instr, 2 inputs, n=131072 bf16",
         "int4_g64_matmul M=256 K=512 N=256 -> bf16 + add epilogue",
     ]
+    monkeypatch.setenv("MK_PLAN_EPILOGUES", "all")
+    assert plan(text)[7] == "int4_g64_matmul M=256 K=256 N=512 -> bf16 + swiglu epilogue"
     monkeypatch.setenv("MK_PLAN_EPILOGUES", "0")
     steps = plan(text)
     assert not any("epilogue" in s for s in steps) and len(steps) == 12
