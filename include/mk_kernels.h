@@ -101,11 +101,14 @@ int mk_int8pc_matmul_epilogue_bf16(const void* x, const void* w, const void* sca
  * cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
  * The workspace is a file-scope device array of 8 MiB per GPU, held until the
- * process ends; shapes whose mk_qmatmul_workspace_bytes exceeds 8 MiB
- * (for example M >= 768 at K = 4096, N = 14336) return MK_EWORKSPACE before
- * any launch.  The first call on a device sets the array up (its address,
- * and its counters cleared by a kernel on `stream`).  The call allocates
- * nothing and gives bit-identical results to mk_int4g64_matmul_bf16.  Every
+ * process ends.  The many-row kernel (128 <= M < 768) runs here without its
+ * K split when the split's partials would not fit (at K = 4096, N = 14336:
+ * same results to the bf16 tolerance, not bit for bit); shapes whose plan
+ * still needs more than 8 MiB (the dequantise-then-GEMM route, for example
+ * M >= 768 at K = 4096, N = 14336) return MK_EWORKSPACE before any launch.
+ * The first call on a device sets the array up (its address, and its
+ * counters cleared by a kernel on `stream`).  The call allocates nothing and
+ * otherwise gives bit-identical results to mk_int4g64_matmul_bf16.  Every
  * call on one GPU shares the array: calls that overlap in time on one GPU
  * (unordered streams) race. */
 int mk_int4g64_matmul_bf16_noalloc(const void* x, const void* w_packed, const void* scale,

@@ -8,25 +8,36 @@
 //             zero uint8 [K/64, N]; y = x @ ((W - zero) * scale).
 //   int8 pc:  W int8 [K, N], scale f32 [N]; y = x @ (W * scale).
 //
-// Tile: 256 rows x 64 columns per workgroup, 4 waves of 64 rows each, 64 k
-// (one int4 scale group) per step; v_mfma_f32_16x16x32_bf16, 4 x 4 tiles per
-// wave.  Per step:
+// Tile: 256 rows x 128 columns per workgroup, 4 waves of 64 rows x 128
+// columns each, 64 k (one int4 scale group) per step; v_mfma_f32_16x16x32_bf16,
+// 4 x 8 tiles per wave (128 f32 accumulators per lane).  The x fragments go
+// straight from L2 into registers and each one feeds 8 MFMAs; the earlier
+// 64-column tile fed 4, and re-reading x from L2 (about 450 MB per call at
+// M = 256, K = 4096, N = 14336) was what bound it.  Per step:
 //   * every thread loads its share of the packed weight tile (int4: 2 packed
-//     rows x 4 columns plus their 4 scales and zero points; int8: 16 bytes of
-//     one k row) into registers kQgAhead steps ahead -- plain loads, so the
-//     compiler's own wait counts cover them;
-//   * all 256 threads dequantise the next step's tile into a bf16 [64 k][64 n]
+//     rows x 8 columns plus their 8 scales and zero points; int8: 32 bytes of
+//     one k row) into registers kQgAhead steps ahead;
+//   * all 256 threads dequantise the next step's tile into a bf16 [64 k][128 n]
 //     LDS buffer (double-buffered), each weight once per workgroup:
 //       int4: w = (q - z) * s, exact in f32 (q * s is exact inside the FMA and
 //             z * s has at most 16 significant bits), then rounded to bf16;
 //       int8: w exactly as bf16 (8 significant bits); the per-channel scale
 //             multiplies the f32 accumulator in the epilogue instead;
 //   * each wave reads its B fragments with ds_read_b64_tr_b16 (conflict-free
-//     through an XOR swizzle of the 16-byte chunks); its x fragments come
-//     straight from global memory into registers, loaded right after the
-//     MFMAs of two steps before have read that register set (x is shared by
-//     every workgroup of a row tile, so it is mostly served from L2).
+//     through an XOR swizzle of the 16-byte chunks); its x fragments are
+//     loaded right after the MFMAs of two steps before have read that
+//     register set.
 // One barrier per step.  Rows past M are clamped on load and not stored.
+//
+// Split K.  At M = 256 the grid has 112 tiles for 256 CUs, so the K range is
+// split in two (ks = 2, 224 workgroups).  Each workgroup stores its f32
+// partial with device-coherent (sc1) buffer stores -- plain compiler-visible
+// instructions, so the compiler keeps their data registers intact until they
+// are read -- waits for their acknowledgement, and bumps the tile's arrival
+// counter with a device-scope atomic; the second arriver loads the other
+// partial with sc1 loads, adds it to its own (two addends: the sum does not
+// depend on which one arrives last), applies the epilogue and resets the
+// counter.  No workgroup waits on another.
 //
 // Numerics vs. the f32 reference: int8 is exact up to f32 accumulation; int4
 // rounds each dequantised weight to bf16 once (relative 2^-9), well inside
@@ -35,12 +46,19 @@
 #include "epilogue.h"
 #include "qgemm.h"
 
+#include <stdlib.h>
+
 #include <algorithm>
 
 namespace mk {
 
-constexpr int kQgAhead = 3;      // weight loads run this many steps ahead
-constexpr int kQgBuf = 64 * 128;  // bf16 [64 k][64 n] tile
+constexpr int kQgRows = 256;
+constexpr int kQgCols = 128;
+constexpr int kQgAhead = 3;                // weight loads run this many steps ahead
+constexpr int kQgBuf = 64 * kQgCols * 2;   // bf16 [64 k][128 n] tile
+constexpr int kQgPart = kQgRows * kQgCols;  // f32 per partial tile
+constexpr uint32_t kBufWord3 = 0x00020000u;  // raw-buffer resource word 3 (gfx9 family)
+constexpr int kSc1 = 16;                   // buffer cache policy: sc1 (device scope)
 
 struct QgArgs {
   const uint16_t* x;
@@ -51,15 +69,19 @@ struct QgArgs {
   const uint16_t* aux;  // epilogue operand or null
   int epi;
   int M, K, N;
+  int ks;          // K split (1 or 2)
+  float* part;     // ks > 1: partial tiles [tile][ks][32][256 threads][4]
+  uint32_t* cnt;   // ks > 1: per-tile arrival counters (zero between calls)
 };
 
 typedef short qg_s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) qg_s16x4* qg_lds_s16x4_ptr;
 
-// Chunk swizzle of the bf16 tile (rows of 128 B = 8 chunks of 16 B).  With
-// it the 64 lanes of one ds_read_b64_tr_b16 (k rows 8g + r (+4), g, r < 4)
-// touch every bank exactly twice.
-__device__ __forceinline__ int qg_swz(int k, int c) { return c ^ ((((k >> 1) & 1) << 1) | (((k >> 3) & 1) << 2)); }
+// Chunk swizzle of the bf16 tile (rows of 256 B = 16 chunks of 16 B): chunk
+// c of k row k sits at c ^ (2 (k % 4) + 8 (k / 8 % 2)).  A transposing read
+// (k rows 8g + r (+4), g, r < 4; two chunks per row) then uses every bank
+// exactly twice, and a dequantisation store (4 rows x 16 chunks) four times.
+__device__ __forceinline__ int qg_swz(int k, int c) { return c ^ ((2 * (k & 3)) | (((k >> 3) & 1) << 3)); }
 
 // Two floats to bf16 (RNE) in one v_cvt_pk_bf16_f32, lo in the low half.
 typedef float qg_f2 __attribute__((ext_vector_type(2)));
@@ -69,55 +91,64 @@ __device__ __forceinline__ uint32_t qg_pack(float lo, float hi) {
 }
 
 // One thread's share of a step's packed weights.
-//   int4: packed rows 2 pp, 2 pp + 1 at columns 4 cq .. +3 (w0, w1), the 4
-//         bf16 scales (s) and 4 zero points (z) of those columns.
-//   int8: 16 bytes of k row kr at columns 16 cc .. +15 (v).
+//   int4: packed rows 2 pp, 2 pp + 1 at columns 8 cq .. +7 (w0, w1), their 8
+//         bf16 scales (s) and 8 zero points (z).
+//   int8: 32 bytes of k row kr at columns 32 cc .. +31 (v0, v1).
 struct QgW {
-  uint32_t w0, w1, z;
-  u32x2 s;
-  u32x4 v;
+  u32x2 w0, w1, z;
+  u32x4 s;
+  u32x4 v0, v1;
 };
 
 template <bool INT4>
 __global__ __launch_bounds__(256) void qgemm_kernel(QgArgs a) {
   constexpr int P = kQgAhead;
   __shared__ __attribute__((aligned(16))) unsigned char bbuf[2][kQgBuf];
+  __shared__ uint32_t last_flag;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int N = a.N, K = a.K, M = a.M;
-  const int tiles_n = N / 64;
+  const int tiles_n = N / kQgCols, tiles_m = (M + kQgRows - 1) / kQgRows;
+  // Logical id -> (column tile, row tile, K part): the row tiles of one
+  // column tile (which read the same weights) and the K parts of one tile
+  // are consecutive, and xcd_logical_id keeps consecutive ids on one XCD.
   const uint32_t L = xcd_logical_id(blockIdx.x, gridDim.x);
-  const int tm = (int)L / tiles_n, tn = (int)L - tm * tiles_n;
-  const int m0 = tm * 256, n0 = tn * 64;
-  const int KT = K / 64;
+  const int ksi = (int)(L % (uint32_t)a.ks);
+  const int tile = (int)(L / (uint32_t)a.ks);
+  const int tn = tile / tiles_m, tm = tile - tn * tiles_m;
+  const int m0 = tm * kQgRows, n0 = tn * kQgCols;
+  const int KT = K / a.ks / 64;       // steps of this workgroup
+  const int kt0 = ksi * KT;           // its first step (64-k group)
 
   // ---- weight loads (steps past the end reload the last one).  Every
   //      address is a wave-uniform per-step base plus a per-lane 32-bit byte
-  //      offset, so the per-step work is scalar. ----
+  //      offset. ----
   const int pp = tid >> 4, cq = tid & 15;  // int4
   const int kr = tid >> 2, cc = tid & 3;   // int8
-  const uint32_t woff = INT4 ? (uint32_t)(2 * pp * N + n0 + 4 * cq) : (uint32_t)(kr * N + n0 + 16 * cc);
-  const uint32_t soff = (uint32_t)(2 * (n0 + 4 * cq)), zoff = (uint32_t)(n0 + 4 * cq);
+  const uint32_t woff = INT4 ? (uint32_t)(2 * pp * N + n0 + 8 * cq) : (uint32_t)(kr * N + n0 + 32 * cc);
+  const uint32_t soff = (uint32_t)(2 * (n0 + 8 * cq)), zoff = (uint32_t)(n0 + 8 * cq);
   auto load_w = [&](int st, QgW& r) {
-    st = st < KT ? st : KT - 1;
+    st = kt0 + (st < KT ? st : KT - 1);
     if (INT4) {
       const uint32_t o = (uint32_t)st * (uint32_t)(32 * N) + woff;
-      r.w0 = *reinterpret_cast<const uint32_t*>(a.w + o);
-      r.w1 = *reinterpret_cast<const uint32_t*>(a.w + (o + (uint32_t)N));
-      r.s = *reinterpret_cast<const u32x2*>(static_cast<const uint8_t*>(a.s) + ((uint32_t)st * (uint32_t)(2 * N) + soff));
-      r.z = *reinterpret_cast<const uint32_t*>(a.z + ((uint32_t)st * (uint32_t)N + zoff));
+      r.w0 = *reinterpret_cast<const u32x2*>(a.w + o);
+      r.w1 = *reinterpret_cast<const u32x2*>(a.w + (o + (uint32_t)N));
+      r.s = *reinterpret_cast<const u32x4*>(static_cast<const uint8_t*>(a.s) + ((uint32_t)st * (uint32_t)(2 * N) + soff));
+      r.z = *reinterpret_cast<const u32x2*>(a.z + ((uint32_t)st * (uint32_t)N + zoff));
     } else {
-      r.v = *reinterpret_cast<const u32x4*>(a.w + ((uint32_t)st * (uint32_t)(64 * N) + woff));
+      const uint32_t o = (uint32_t)st * (uint32_t)(64 * N) + woff;
+      r.v0 = *reinterpret_cast<const u32x4*>(a.w + o);
+      r.v1 = *reinterpret_cast<const u32x4*>(a.w + o + 16);
     }
   };
 
   // ---- x fragments: tile i, half hh: row m0 + 64 wave + 16 i + lane%16,
-  //      k = 64 t + 32 hh + 8 (lane/16) .. +7 ----
+  //      k = 64 (kt0 + t) + 32 hh + 8 (lane/16) .. +7 ----
   uint32_t xoff[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = std::min(m0 + 64 * wave + 16 * i + (lane & 15), M - 1);
-    xoff[i] = (uint32_t)(2 * (r * K + 8 * (lane >> 4)));
+    xoff[i] = (uint32_t)(2 * (r * K + 64 * kt0 + 8 * (lane >> 4)));
   }
   auto load_x = [&](int t, u32x4 (&xa)[8]) {
     t = t < KT ? t : KT - 1;
@@ -134,86 +165,95 @@ __global__ __launch_bounds__(256) void qgemm_kernel(QgArgs a) {
   auto dequant = [&](int t, const QgW& r) {
     unsigned char* dst = bbuf[t & 1];
     if (INT4) {
-      float s[4], s16[4], zs[4];
+      float s[8], s16[8], zs[8];
+      const uint32_t sw[4] = {r.s.x, r.s.y, r.s.z, r.s.w};
+      const uint32_t zw[2] = {r.z.x, r.z.y};
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const uint32_t sb = (c < 2 ? r.s.x : r.s.y) >> (16 * (c & 1));
-        s[c] = bf16_to_f32(sb & 0xffffu);
+      for (int c = 0; c < 8; ++c) {
+        s[c] = bf16_to_f32((sw[c >> 1] >> (16 * (c & 1))) & 0xffffu);
         s16[c] = s[c] * 0.0625f;
-        zs[c] = (float)((r.z >> (8 * c)) & 0xffu) * s[c];
+        zs[c] = (float)((zw[c >> 2] >> (8 * (c & 3))) & 0xffu) * s[c];
       }
       // Rows k = 4 pp + {0, 1, 2, 3}: low / high nibbles of packed rows 2 pp
       // and 2 pp + 1.  High nibbles are converted as 16 q and scaled by s/16.
-      uint32_t lo[2] = {r.w0 & 0x0f0f0f0fu, r.w1 & 0x0f0f0f0fu};
-      uint32_t hi[2] = {r.w0 & 0xf0f0f0f0u, r.w1 & 0xf0f0f0f0u};
+      uint32_t lo[4] = {r.w0.x & 0x0f0f0f0fu, r.w0.y & 0x0f0f0f0fu, r.w1.x & 0x0f0f0f0fu, r.w1.y & 0x0f0f0f0fu};
+      uint32_t hi[4] = {r.w0.x & 0xf0f0f0f0u, r.w0.y & 0xf0f0f0f0u, r.w1.x & 0xf0f0f0f0u, r.w1.y & 0xf0f0f0f0u};
       // Keep the masked words as they are, so each byte converts with one
       // v_cvt_f32_ubyteN instead of a bit-field extract and a convert.
-      asm volatile("" : "+v"(lo[0]), "+v"(lo[1]), "+v"(hi[0]), "+v"(hi[1]));
+      asm volatile("" : "+v"(lo[0]), "+v"(lo[1]), "+v"(lo[2]), "+v"(lo[3]));
+      asm volatile("" : "+v"(hi[0]), "+v"(hi[1]), "+v"(hi[2]), "+v"(hi[3]));
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        const uint32_t src = (kk & 1) ? hi[kk >> 1] : lo[kk >> 1];
-        float v[4];
+        const int wsel = 2 * (kk >> 1);  // words of packed row 2 pp + kk / 2
+        float v[8];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const float q = (float)((src >> (8 * c)) & 0xffu);
+        for (int c = 0; c < 8; ++c) {
+          const uint32_t src = (kk & 1) ? hi[wsel + (c >> 2)] : lo[wsel + (c >> 2)];
+          const float q = (float)((src >> (8 * (c & 3))) & 0xffu);
           v[c] = __builtin_fmaf(q, (kk & 1) ? s16[c] : s[c], -zs[c]);
         }
         const int k = 4 * pp + kk;
-        *reinterpret_cast<u32x2*>(dst + 128 * k + 16 * qg_swz(k, cq >> 1) + 8 * (cq & 1)) =
-            u32x2{qg_pack(v[0], v[1]), qg_pack(v[2], v[3])};
+        *reinterpret_cast<u32x4*>(dst + 256 * k + 16 * qg_swz(k, cq)) =
+            u32x4{qg_pack(v[0], v[1]), qg_pack(v[2], v[3]), qg_pack(v[4], v[5]), qg_pack(v[6], v[7])};
       }
     } else {
-      uint32_t o[8];
+      const uint32_t wv[8] = {r.v0.x, r.v0.y, r.v0.z, r.v0.w, r.v1.x, r.v1.y, r.v1.z, r.v1.w};
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const uint32_t b = r.v[d] ^ 0x80808080u;  // w + 128 as u8
-        float f[4];
+      for (int h = 0; h < 4; ++h) {  // chunk 4 cc + h: columns 32 cc + 8 h .. +7
+        uint32_t o[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) f[e] = (float)((b >> (8 * e)) & 0xffu) - 128.0f;
-        o[2 * d] = qg_pack(f[0], f[1]);
-        o[2 * d + 1] = qg_pack(f[2], f[3]);
+        for (int d = 0; d < 2; ++d) {
+          const uint32_t b = wv[2 * h + d] ^ 0x80808080u;  // w + 128 as u8
+          float f[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) f[e] = (float)((b >> (8 * e)) & 0xffu) - 128.0f;
+          o[2 * d] = qg_pack(f[0], f[1]);
+          o[2 * d + 1] = qg_pack(f[2], f[3]);
+        }
+        *reinterpret_cast<u32x4*>(dst + 256 * kr + 16 * qg_swz(kr, 4 * cc + h)) = u32x4{o[0], o[1], o[2], o[3]};
       }
-      *reinterpret_cast<u32x4*>(dst + 128 * kr + 16 * qg_swz(kr, 2 * cc)) = u32x4{o[0], o[1], o[2], o[3]};
-      *reinterpret_cast<u32x4*>(dst + 128 * kr + 16 * qg_swz(kr, 2 * cc + 1)) = u32x4{o[4], o[5], o[6], o[7]};
     }
   };
 
   // ---- B fragment offsets: tile j; the k half h of 32-row block hh adds
-  //      the uniform 128 (32 hh + 4 h).  The swizzle term depends only on
+  //      the uniform 256 (32 hh + 4 h).  The swizzle term depends only on
   //      bits of the lane's k row 8g + r that 32 hh + 4 h does not change. ----
-  int boff[4];
+  int boff[8];
   {
     const int g = lane >> 4, r = (lane & 15) >> 2, q = lane & 3;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 8; ++j) {
       const int k = 8 * g + r, col = 16 * j + 4 * q;
-      boff[j] = 128 * k + 16 * qg_swz(k, col >> 3) + 2 * (col & 7);
+      boff[j] = 256 * k + 16 * qg_swz(k, col >> 3) + 2 * (col & 7);
     }
   }
 
-  f32x4 acc[4][4];
+  f32x4 acc[4][8];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // Both k halves' B fragments are read up front, so the second half's LDS
+  // latency runs under the first half's MFMAs.
   auto mma = [&](int t, const u32x4 (&xa)[8]) {
     const unsigned char* b = bbuf[t & 1];
+    u32x4 bf[2][8];
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      u32x4 bf[4];
+    for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const qg_s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((qg_lds_s16x4_ptr)(b + boff[j] + 4096 * hh));
-        const qg_s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((qg_lds_s16x4_ptr)(b + boff[j] + 4096 * hh + 512));
+      for (int j = 0; j < 8; ++j) {
+        const qg_s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((qg_lds_s16x4_ptr)(b + boff[j] + 8192 * hh));
+        const qg_s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((qg_lds_s16x4_ptr)(b + boff[j] + 8192 * hh + 1024));
         const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
-        bf[j] = u32x4{l2.x, l2.y, h2.x, h2.y};
+        bf[hh][j] = u32x4{l2.x, l2.y, h2.x, h2.y};
       }
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x32(bf[j], xa[4 * hh + i], acc[i][j]);
-    }
+        for (int j = 0; j < 8; ++j) acc[i][j] = mfma16x16x32(bf[hh][j], xa[4 * hh + i], acc[i][j]);
   };
 
   // ---- prologue: weights of steps 0 .. P-1, x of steps 0 and 1, step 0
@@ -258,13 +298,50 @@ __global__ __launch_bounds__(256) void qgemm_kernel(QgArgs a) {
   if (t + 3 < KT) iter(t + 3, wr[1], xa[1]);
   if (t + 4 < KT) iter(t + 4, wr[2], xa[0]);
 
+  // ---- split K: exchange the partials ----
+  if (a.ks > 1) {
+    // Partial (i, j) of thread tid at float offset 4 * ((32 ksi + 8 i + j) * 256 + tid)
+    // of the tile's region; every store and load below stays inside it
+    // (the resource's size bounds the accesses as well).
+    float* tp = a.part + (size_t)tile * a.ks * kQgPart;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(tp, 0, a.ks * kQgPart * 4, kBufWord3);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][j]), rs,
+                                               ((32 * ksi + 8 * i + j) * 256 + tid) * 16, 0, kSc1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // every partial store acknowledged
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t* ctr = a.cnt + tile;
+      asm volatile("" : "+v"(ctr));  // per-lane address: a vector atomic
+      const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t last = old == (uint32_t)(a.ks - 1);
+      if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last_flag = last;
+    }
+    __syncthreads();
+    if (!last_flag) return;
+    // The other partial (ks == 2), device-coherent loads, added to ours.
+    const int other = 1 - ksi;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, ((32 * other + 8 * i + j) * 256 + tid) * 16, 0,
+                                                              kSc1);
+        acc[i][j] += __builtin_bit_cast(f32x4, v);
+      }
+  }
+
   // ---- epilogue: lane owns row m, columns n .. n + 3 of each tile ----
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int m = m0 + 64 * wave + 16 * i + (lane & 15);
     if (m >= M) continue;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 8; ++j) {
       const int n = n0 + 16 * j + 4 * (lane >> 4);
       f32x4 v = acc[i][j];
       if (!INT4) {
@@ -282,12 +359,28 @@ namespace mkq {
 
 bool qgemm_supported(int64_t M, int64_t K, int64_t N) {
   // Per-lane offsets are 32-bit: the weight matrix and x stay under 2 GiB.
-  return M >= 1 && K >= 64 && K % 64 == 0 && N >= 64 && N % 64 == 0 && K * N < ((int64_t)1 << 31) &&
-         M * K * 2 < ((int64_t)1 << 31);
+  return M >= 1 && K >= 64 && K % 64 == 0 && N >= mk::kQgCols && N % mk::kQgCols == 0 &&
+         K * N < ((int64_t)1 << 31) && M * K * 2 < ((int64_t)1 << 31);
+}
+
+int qgemm_ks(int64_t M, int64_t K, int64_t N, int64_t workspace_cap) {
+  const int64_t tiles = ((M + mk::kQgRows - 1) / mk::kQgRows) * (N / mk::kQgCols);
+  const char* env = getenv("MK_QG_KS");
+  int ks = (tiles < 192 && K % 128 == 0 && K >= 256) ? 2 : 1;
+  if (env && (env[0] == '1' || env[0] == '2') && env[1] == '\0') ks = env[0] - '0';
+  if (ks == 2 && (K % 128 != 0 || tiles > kQgCounters || qgemm_workspace_bytes(M, K, N, 2) > workspace_cap)) ks = 1;
+  return ks;
+}
+
+int64_t qgemm_workspace_bytes(int64_t M, int64_t K, int64_t N, int ks) {
+  if (ks <= 1) return 0;
+  const int64_t tiles = ((M + mk::kQgRows - 1) / mk::kQgRows) * (N / mk::kQgCols);
+  return kQgPartOffset + tiles * ks * mk::kQgPart * 4;
 }
 
 hipError_t qgemm_launch(bool int4, const void* x, const void* w, const void* s, const void* z, void* y, int64_t M,
-                        int64_t K, int64_t N, const void* aux, int epi, hipStream_t stream) {
+                        int64_t K, int64_t N, const void* aux, int epi, int ks, void* workspace,
+                        hipStream_t stream) {
   mk::QgArgs a;
   a.x = static_cast<const uint16_t*>(x);
   a.w = static_cast<const uint8_t*>(w);
@@ -299,7 +392,10 @@ hipError_t qgemm_launch(bool int4, const void* x, const void* w, const void* s, 
   a.M = (int)M;
   a.K = (int)K;
   a.N = (int)N;
-  const dim3 grid((unsigned)(((M + 255) / 256) * (N / 64)));
+  a.ks = ks;
+  a.cnt = ks > 1 ? static_cast<uint32_t*>(workspace) : nullptr;
+  a.part = ks > 1 ? reinterpret_cast<float*>(static_cast<unsigned char*>(workspace) + kQgPartOffset) : nullptr;
+  const dim3 grid((unsigned)(((M + mk::kQgRows - 1) / mk::kQgRows) * (N / mk::kQgCols) * ks));
   if (int4)
     hipLaunchKernelGGL(mk::qgemm_kernel<true>, grid, dim3(256), 0, stream, a);
   else

@@ -970,7 +970,7 @@ struct QPlan {
   int ring;          // int8 streaming kernel: ring slots
   int wide_groups;   // > 0: wide int4 kernel with this many 64-k groups per wave
   int deq;           // 1: dequantise W to bf16 in the workspace, then the bf16 GEMM
-  int qg;            // 1: the many-row kernel of qgemm.hip (no workspace)
+  int qg;            // 1: the many-row kernel of qgemm.hip (K split ks ways)
   size_t lds_bytes;
   int64_t part_bytes;
 };
@@ -1084,13 +1084,18 @@ constexpr int kQgMinRows = 128;
 constexpr int kDeqMinRows = 768;
 constexpr int kDeqFallbackRows = 256;
 
-bool plan_q(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p) {
+// qg_cap bounds the workspace the many-row kernel's K split may use (the
+// no-allocation entry point passes its array's size; the kernel then runs
+// unsplit rather than ask for more).
+bool plan_q(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p, int64_t qg_cap = INT64_MAX) {
   *p = QPlan{};
   const int qg_m = env_int("MK_QMM_QG_M", kQgMinRows);
   const int deq_m = env_int("MK_QMM_DEQ_M", kDeqMinRows);
   const bool deq = deq_m > 0 && (M >= deq_m || M >= std::min(deq_m, kDeqFallbackRows));
   if (qg_m > 0 && M >= qg_m && !(deq_m > 0 && M >= deq_m) && mkq::qgemm_supported(M, K, N)) {
     p->qg = 1;
+    p->ks = mkq::qgemm_ks(M, K, N, qg_cap);
+    p->part_bytes = mkq::qgemm_workspace_bytes(M, K, N, p->ks);
     return true;
   }
   if (deq) {
@@ -1199,7 +1204,7 @@ hipError_t launch_reduce(int fmt, const mk::QArgs& a, hipStream_t st) {
 
 int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, void* y, int64_t M,
           int64_t K, int64_t N, void* ws, int64_t ws_bytes, void* stream, const void* aux = nullptr,
-          int epi = MK_EPI_NONE) {
+          int epi = MK_EPI_NONE, int64_t qg_cap = INT64_MAX) {
   const char* fn = fmt == MK_QFMT_INT4_G64 ? "mk_int4g64_matmul_bf16" : "mk_int8pc_matmul_bf16";
   if (epi != MK_EPI_NONE && epi != MK_EPI_ADD && epi != MK_EPI_SWIGLU && epi != MK_EPI_SWIGLU_PAIRS)
     return mkc::fail(MK_EINVAL, "%s: unknown epilogue %d", fn, epi);
@@ -1216,7 +1221,7 @@ int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, v
   if (M > (1 << 20) || K > (1 << 24) || N > (1 << 26) || (M * K) > (int64_t)1 << 31)
     return mkc::fail(MK_EINVAL, "%s: shape too large", fn);
   QPlan p;
-  if (!plan_q(fmt, M, K, N, &p))
+  if (!plan_q(fmt, M, K, N, &p, qg_cap))
     return mkc::fail(MK_EUNSUPPORTED, "%s: no launch configuration for K=%lld", fn, (long long)K);
   // The paired SwiGLU (interleaved gate / up columns, y [M, N/2]) is an
   // epilogue of the bf16 GEMM only: it needs the dequantise-then-GEMM route.
@@ -1248,7 +1253,7 @@ int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, v
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e;
   if (p.qg) {
-    e = mkq::qgemm_launch(fmt == MK_QFMT_INT4_G64, x, w, s, z, y, M, K, N, aux, epi, st);
+    e = mkq::qgemm_launch(fmt == MK_QFMT_INT4_G64, x, w, s, z, y, M, K, N, aux, epi, p.ks, ws, st);
     if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
     return MK_OK;
   }
@@ -1404,7 +1409,13 @@ extern "C" int mk_int4g64_matmul_bf16_noalloc(const void* x, const void* w_packe
                                               const void* zero, void* y, int64_t M, int64_t K, int64_t N,
                                               void* stream) {
   mkc::clear_error();
-  const int64_t need = mk_qmatmul_workspace_bytes(MK_QFMT_INT4_G64, M, K, N);
+  // The plan this entry point runs: the many-row kernel's K split only when
+  // its partials fit the array.
+  QPlan cp;
+  const int64_t need = (M > 0 && K > 0 && N > 0 && K % 64 == 0 &&
+                        plan_q(MK_QFMT_INT4_G64, M, K, N, &cp, kNoAllocScratchBytes))
+                           ? cp.part_bytes
+                           : -1;
   if (need > kNoAllocScratchBytes)
     return mkc::fail(MK_EWORKSPACE,
                      "mk_int4g64_matmul_bf16_noalloc: M=%lld K=%lld N=%lld needs %lld bytes of workspace; "
@@ -1418,5 +1429,6 @@ extern "C" int mk_int4g64_matmul_bf16_noalloc(const void* x, const void* w_packe
   void* ws = nullptr;
   const int rc = scratch_for_current_device(st, &ws);
   if (rc != MK_OK) return rc;
-  return run_q(MK_QFMT_INT4_G64, x, w_packed, scale, zero, y, M, K, N, ws, kNoAllocScratchBytes, stream);
+  return run_q(MK_QFMT_INT4_G64, x, w_packed, scale, zero, y, M, K, N, ws, kNoAllocScratchBytes, stream, nullptr,
+               MK_EPI_NONE, kNoAllocScratchBytes);
 }

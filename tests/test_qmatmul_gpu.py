@@ -113,12 +113,14 @@ def test_int8_pc_headline_shape():
     assert_rel_close(host_bf16(y), ref, BF16_RTOL, "int8 headline")
 
 
-# Many rows (M >= 128): the qgemm kernel (N % 64 == 0) or, for other N, W
-# dequantised to bf16 in the workspace and the bf16 GEMM.  The workload's
-# M = 256 and 4096 rows at reduced K, N; ragged M; K of 1, 2, 3 and 5 steps of
-# 64 (the kernel's loop tail); N = 776 takes the dequantise-then-GEMM path.
+# Many rows (M >= 128): the qgemm kernel (N % 128 == 0; K split in two when
+# the grid has fewer than 192 tiles) or, for other N, W dequantised to bf16 in
+# the workspace and the bf16 GEMM.  The workload's M = 256 and 4096 rows at
+# reduced K, N; ragged M; K of 1, 2, 3 and 5 steps of 64 (the kernel's loop
+# tail); N = 776 and N = 64 take the dequantise-then-GEMM path.
 LARGE_M_SHAPES = [(256, 4096, 2048), (4096, 512, 512), (300, 1024, 776), (512, 256, 14336),
-                  (130, 192, 128), (256, 64, 64), (1000, 320, 192), (128, 128, 640)]
+                  (130, 192, 128), (256, 64, 64), (1000, 320, 192), (128, 128, 640), (300, 1024, 256),
+                  (200, 384, 384)]
 
 
 @pytest.mark.parametrize("M,K,N", LARGE_M_SHAPES)
@@ -182,7 +184,7 @@ def test_qgemm_kernel_many_row_tiles(monkeypatch, fmt):
     ops = _ops()
     monkeypatch.setenv("MK_QMM_DEQ_M", "0")
     rng = np.random.default_rng(91)
-    M, K, N = 1000, 320, 192
+    M, K, N = 1000, 320, 256
     if fmt == "int4":
         x, packed, s, z = quant.make_int4_case(rng, M, K, N)
         y = ops.int4_g64_matmul(dev_bf16(x), dev(packed), dev_bf16(s), dev(z))
@@ -193,6 +195,38 @@ def test_qgemm_kernel_many_row_tiles(monkeypatch, fmt):
         ref = cport.int8_pc_matmul(x, w, s)
     torch.cuda.synchronize()
     assert_rel_close(host_bf16(y), ref, BF16_RTOL, f"{fmt} qgemm {M}x{K}x{N}")
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+@pytest.mark.parametrize("M,K,N", [(256, 4096, 2048), (300, 1024, 256), (128, 256, 128)])
+def test_qgemm_split_k(monkeypatch, fmt, M, K, N):
+    """The qgemm kernel with its K split in two (the second arriver adds the
+    other partial) against the unsplit kernel (MK_QG_KS=1) and the oracle; a
+    repeated split call is bit-identical (two addends: the arrival order
+    cannot change the sum), including after the unsplit call reused the
+    workspace's counters."""
+    ops = _ops()
+    rng = np.random.default_rng(5000 + M + K + N)
+    if fmt == "int4":
+        x, packed, s, z = quant.make_int4_case(rng, M, K, N)
+        args = (dev_bf16(x), dev(packed), dev_bf16(s), dev(z))
+        run, ref = ops.int4_g64_matmul, cport.int4_g64_matmul(x, packed, s, z)
+    else:
+        x, w, s = quant.make_int8_case(rng, M, K, N)
+        args = (dev_bf16(x), dev(w), dev(s))
+        run, ref = ops.int8_pc_matmul, cport.int8_pc_matmul(x, w, s)
+    print(f"qgemm split-K {fmt} M={M} K={K} N={N}", flush=True)
+    y2 = host_bf16_bits(run(*args))
+    monkeypatch.setenv("MK_QG_KS", "1")
+    y1 = host_bf16_bits(run(*args))
+    monkeypatch.delenv("MK_QG_KS")
+    y2b = host_bf16_bits(run(*args))
+    torch.cuda.synchronize()
+    assert np.array_equal(y2, y2b)
+    from oracle.bf16 import bf16_bits_to_f32
+    assert_rel_close(bf16_bits_to_f32(y2), ref, BF16_RTOL, f"{fmt} qgemm split")
+    assert_rel_close(bf16_bits_to_f32(y1), ref, BF16_RTOL, f"{fmt} qgemm unsplit")
+    assert_rel_close(bf16_bits_to_f32(y2), bf16_bits_to_f32(y1), BF16_RTOL, f"{fmt} split vs unsplit")
 
 
 def test_int4_g64_large_m_known_answer():

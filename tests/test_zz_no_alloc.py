@@ -54,3 +54,35 @@ def test_noalloc_rejects_shapes_beyond_the_array():
     rc = L.mk_int4g64_matmul_bf16_noalloc(fake, fake, fake, fake, fake, M, K, N, None)
     assert rc == _lib.MK_EWORKSPACE
     assert b"no-allocation" in L.mk_last_error()
+
+
+def test_noalloc_many_rows_runs_unsplit():
+    """M = 256 at the workload's K, N: the many-row kernel's split-K partials
+    (28 MB) do not fit the array, so this entry point runs it unsplit; the
+    result agrees with the workspace entry point (split) at the bf16
+    tolerance, and both with the oracle on sampled rows.  A smaller shape
+    whose partials fit runs split and is bit-identical."""
+    need_gpu()
+    from mi355x import _lib, ops
+    from oracle.bf16 import bf16_bits_to_f32
+    L = _lib.lib()
+    rng = np.random.default_rng(71)
+    M, K, N = 256, 4096, 14336
+    print(f"[noalloc] M={M} K={K} N={N}", flush=True)
+    x, packed, s, z = quant.make_int4_case(rng, M, K, N)
+    args = (dev_bf16(x), dev(packed), dev_bf16(s), dev(z))
+    y_na = host_bf16_bits(_noalloc(L, *args, M, K, N))
+    y_ws = host_bf16_bits(ops.int4_g64_matmul(*args))
+    torch.cuda.synchronize()
+    assert_rel_close(bf16_bits_to_f32(y_na), bf16_bits_to_f32(y_ws), BF16_RTOL, "noalloc vs workspace at M=256")
+    rows = np.array([0, 1, 127, 255])
+    ref = cport.int4_g64_matmul(x[rows], packed, s, z)
+    assert_rel_close(bf16_bits_to_f32(y_na)[rows], ref, BF16_RTOL, "noalloc M=256 rows vs oracle")
+    M2, K2, N2 = 256, 1024, 2048  # 4 MB of partials: split here too
+    print(f"[noalloc] M={M2} K={K2} N={N2}", flush=True)
+    x2, p2, s2, z2 = quant.make_int4_case(rng, M2, K2, N2)
+    a2 = (dev_bf16(x2), dev(p2), dev_bf16(s2), dev(z2))
+    y2_na = host_bf16_bits(_noalloc(L, *a2, M2, K2, N2))
+    y2_ws = host_bf16_bits(ops.int4_g64_matmul(*a2))
+    torch.cuda.synchronize()
+    assert np.array_equal(y2_na, y2_ws)
