@@ -46,13 +46,9 @@ struct RowArgs {
 
 __device__ __forceinline__ float bf16r(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
-// XLA max: NaN wins; +0 above -0.
-__device__ __forceinline__ float xmax(float a, float b) {
-  if (a != a) return a;
-  if (b != b) return b;
-  if (a == b) return (__float_as_uint(a) & 0x80000000u) ? b : a;
-  return a > b ? a : b;
-}
+// XLA max: NaN wins; +0 above -0 -- gfx950's IEEE 754-2019 maximum
+// (v_maximum_f32), one instruction.
+__device__ __forceinline__ float xmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -143,6 +139,16 @@ __device__ __forceinline__ float block_max(float v, float* red) {
   return xmax(xmax(red[0], red[1]), xmax(red[2], red[3]));
 }
 
+__device__ __forceinline__ int block_min_int(int v, int* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wv] = v;
+  __syncthreads();
+  return min(min(red[0], red[1]), min(red[2], red[3]));
+}
+
 __device__ __forceinline__ void block_argmax(float& v, int& i, float* redv, int* redi) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
@@ -210,11 +216,23 @@ __global__ __launch_bounds__(kRowThreads) void row_cached_kernel(RowArgs a) {
     s = block_sum(s, redf);
     if (V::bf16) s = bf16r(s);
     const float r = 1.0f / s;
+    // bf16: y = r(e / s) with e / s the IEEE f32 quotient (XLA:CPU divides in
+    // f32).  e and s carry 8 significant bits, so e / s is never an f32
+    // rounding tie: q = RN(e * RN(1 / s)) is within one ulp of it, and one
+    // Markstein correction, q + RN(1 / s) * (e - q s) with the remainder
+    // exact in an FMA, gives it exactly.
 #pragma unroll
     for (int q = 0; q < VPT; ++q)
       if (ok[q]) {
 #pragma unroll
-        for (int e = 0; e < E; ++e) v[q][e] = V::bf16 ? v[q][e] / s : v[q][e] * r;
+        for (int e = 0; e < E; ++e) {
+          if (V::bf16) {
+            const float q0 = v[q][e] * r;
+            v[q][e] = __builtin_fmaf(__builtin_fmaf(-q0, s, v[q][e]), r, q0);
+          } else {
+            v[q][e] = v[q][e] * r;
+          }
+        }
         V::store(a.y, base + (int64_t)(q * kRowThreads + tid) * E, v[q]);
       }
   } else if (OP == ROW_RMSNORM) {
@@ -237,31 +255,33 @@ __global__ __launch_bounds__(kRowThreads) void row_cached_kernel(RowArgs a) {
         V::store(a.y, base + c, v[q]);
       }
   } else if (OP == ROW_ARGMAX) {
-    float bv = -INFINITY;
-    int bi = 0x7FFFFFFF;
-    bool nan = false;
-    int nan_i = 0x7FFFFFFF;
+    // Two passes over the cached row: the NaN-propagating row maximum m,
+    // then the first index holding it (the first NaN when m is NaN; -0 and
+    // +0 compare equal, so the earlier zero wins).  Each thread's indices
+    // rise with (q, e), so a reverse walk that overwrites keeps its first.
+    float m = -INFINITY;
 #pragma unroll
     for (int q = 0; q < VPT; ++q)
       if (ok[q])
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-          const int idx = (q * kRowThreads + tid) * E + e;
-          const float x = v[q][e];
-          if (x != x) {
-            if (!nan) {
-              nan = true;
-              nan_i = idx;
-            }
-          } else if (x > bv || bi == 0x7FFFFFFF) {
-            bv = x;
-            bi = idx;
-          }
-        }
-    float rv = nan ? NAN : bv;
-    int ri = nan ? nan_i : bi;
-    block_argmax(rv, ri, redf, redi);
-    if (tid == 0) static_cast<int32_t*>(a.y)[row] = ri == 0x7FFFFFFF ? 0 : ri;
+        for (int e = 0; e < E; ++e) m = xmax(m, v[q][e]);
+    m = block_max(m, redf);
+    int bi = 0x7FFFFFFF;
+    if (m != m) {
+#pragma unroll
+      for (int q = VPT - 1; q >= 0; --q)
+        if (ok[q])
+#pragma unroll
+          for (int e = E - 1; e >= 0; --e) bi = v[q][e] != v[q][e] ? (q * kRowThreads + tid) * E + e : bi;
+    } else {
+#pragma unroll
+      for (int q = VPT - 1; q >= 0; --q)
+        if (ok[q])
+#pragma unroll
+          for (int e = E - 1; e >= 0; --e) bi = v[q][e] == m ? (q * kRowThreads + tid) * E + e : bi;
+    }
+    bi = block_min_int(bi, redi);
+    if (tid == 0) static_cast<int32_t*>(a.y)[row] = bi == 0x7FFFFFFF ? 0 : bi;
   } else if (OP == ROW_SUM) {
     float s = 0.f;
 #pragma unroll
@@ -315,7 +335,9 @@ __global__ __launch_bounds__(kRowThreads) void row_stream_kernel(RowArgs a) {
       if (V::bf16) d = bf16r(d);
       float ex = __expf(d);
       if (V::bf16) ex = bf16r(ex);
-      V::store1(a.y, base + c, V::bf16 ? ex / s : ex * r);
+      float y = ex * r;
+      if (V::bf16) y = __builtin_fmaf(__builtin_fmaf(-y, s, ex), r, y);  // the exact quotient, as above
+      V::store1(a.y, base + c, y);
     }
   } else if (OP == ROW_RMSNORM) {
     float s = 0.f;
