@@ -32,8 +32,13 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
   return (uint32_t)__builtin_bit_cast(uint16_t, h);
 }
 
+// Two floats -> packed bf16x2 (lo in bits 0-15), each rounded as
+// f32_to_bf16 rounds; one v_cvt_pk_bf16_f32 for the pair.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+  const bf16x2_t h = __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t);
+  return __builtin_bit_cast(uint32_t, h);
 }
 
 // v_perm_b32: byte i of the result is byte sel.byte[i] of the 64-bit value

@@ -633,6 +633,75 @@ __device__ __forceinline__ void wide_sum_partials(const float* tile_part, f32x4 
   }
 }
 
+// The end of both wide kernels.  Sum the 8 waves' y tiles through LDS;
+// with ks > 1 combine the split-K partials across workgroups (the last of a
+// tile's workgroups to arrive sums them in k order); store bf16 y, times the
+// int8 per-channel scale when FMT8.  Every DMA of the calling wave must have
+// landed: y is spilled into its own LDS region, over its ring.
+template <bool FMT8>
+__device__ __forceinline__ void wide_finish(const QArgs& a, unsigned char* smem, unsigned char* wl,
+                                            const f32x4 (&y)[kWideTN / 16], int tile, int ksi, int rb, int m0,
+                                            int mrows, int n0, int c, int j) {
+  constexpr int TN = kWideTN, NB = TN / 16;
+  const size_t N = (size_t)a.N;
+  const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+  // Sum the 8 waves: each spills y as [16 m][TN] f32 (padded rows) into its
+  // own region; lane (c, j) holds column 16b + c, rows 4j..4j+3.
+  float* red = reinterpret_cast<float*>(wl);
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[(4 * j + i) * kWideRedStride + 16 * b + c] = y[b][i];
+  __syncthreads();
+  f32x4 own[2];
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int q = threadIdx.x + 8 * kWave * it;  // quad index: 16 rows x 64 quads
+    const int m = q >> 6, n = 4 * (q & 63);
+    f32x4 acc = zero4;
+#pragma unroll
+    for (int w = 0; w < 8; ++w)
+      acc += *reinterpret_cast<const f32x4*>(smem + w * a.wave_lds + (m * kWideRedStride + n) * 4);
+    own[it] = acc;
+  }
+  const int ntiles = a.N / TN;
+  if (a.ks > 1) {
+    const size_t tbase = ((size_t)(rb * ntiles + tile) * a.ks) * kQRows * TN;
+    // Device-coherent stores of the partial, acknowledged.
+    float* dst = a.part + tbase + (size_t)ksi * kQRows * TN + 4 * threadIdx.x;
+    st2_sc1_wait(dst, own[0], dst + 4 * 8 * kWave, own[1]);
+    __syncthreads();  // (also: every wave is done reading the spills)
+    // The flag lives in dynamic LDS: a static __shared__ would shift the
+    // dynamic base off the 256-byte alignment the swizzled addressing needs.
+    volatile uint32_t* flag = reinterpret_cast<volatile uint32_t*>(smem);
+    if (threadIdx.x == 0) {
+      uint32_t* ctr = a.cnt + rb * ntiles + tile;
+      asm volatile("" : "+v"(ctr));  // per-lane address: a vector atomic
+      const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t last = old == (uint32_t)(a.ks - 1);
+      if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *flag = last;
+    }
+    __syncthreads();
+    if (!*flag) return;
+    // Device-coherent 16-byte loads (sc1: miss the local L2) of every
+    // partial, then the sum in k order.
+    switch (a.ks) {
+      case 2: wide_sum_partials<2>(a.part + tbase, own); break;
+      case 4: wide_sum_partials<4>(a.part + tbase, own); break;
+      default: wide_sum_partials<8>(a.part + tbase, own); break;
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int q = threadIdx.x + 8 * kWave * it;
+    const int m = q >> 6, n = n0 + 4 * (q & 63);
+    if (m >= mrows) continue;
+    if (FMT8) own[it] *= *reinterpret_cast<const f32x4*>(static_cast<const float*>(a.s) + n);
+    epi_store_bf16x4(a.y, a.aux, a.epi, (size_t)(m0 + m) * N + n, own[it]);
+  }
+}
+
 template <int G, int R>  // G 64-k groups per wave; ring of R 32-k steps
 __global__ __launch_bounds__(8 * kWave) void int4g64_wide_kernel(QArgs a) {
   constexpr int TN = kWideTN, NB = TN / 16, S = 2 * G;
@@ -764,60 +833,129 @@ __global__ __launch_bounds__(8 * kWave) void int4g64_wide_kernel(QArgs a) {
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  wide_finish<false>(a, smem, wl, y, tile, ksi, rb, m0, mrows, n0, c, j);
+}
 
-  // Sum the 8 waves: each spills y as [16 m][TN] f32 (padded rows) into its
-  // own region; lane (c, j) holds column 16b + c, rows 4j..4j+3.
-  float* red = reinterpret_cast<float*>(wl);
+// ---------------------------------------------------------------------------
+// Wide int8 kernel: the wide int4 kernel's layout for per-channel int8
+// weights.  The 64-column streaming kernel reads 64-byte strips of every
+// weight row, which HBM serves at about half the rate of 256-byte segments;
+// here a workgroup owns 256 output columns and K is split over `ks`
+// workgroups.  Each of the 8 waves covers all 256 columns over its own S
+// steps of 32 k with a private DMA ring of R steps: slot = 32 weight rows x
+// 256 B, 16-column chunk c of row r at position c ^ (r & 15), so a
+// transposing read of one chunk across 16 consecutive rows touches 16
+// distinct positions (conflict-free).  ds_read_b64_tr_b8 hands MFMA lane
+// (c, j) column c of one column block in rows 8j..8j+7 -- its B fragment of
+// that block, in natural k order.  Bytes become bf16 (w + 128) as in the
+// 64-column kernel; the offset is removed with the x row sums and the
+// per-channel scale is applied at the store.
+// ---------------------------------------------------------------------------
+constexpr int kWide8Slot = 8 * 1024;  // one 32-k step: 32 weight rows x 256 B
+
+// Sixteen transposing byte reads (one per column block) and their wait.
+__device__ __forceinline__ void lds_tr8x16(uint32_t wb, u32x2 (&o)[16]) {
+  asm volatile(
+      "ds_read_b64_tr_b8 %0, %16\n\t"
+      "ds_read_b64_tr_b8 %1, %17\n\t"
+      "ds_read_b64_tr_b8 %2, %18\n\t"
+      "ds_read_b64_tr_b8 %3, %19\n\t"
+      "ds_read_b64_tr_b8 %4, %20\n\t"
+      "ds_read_b64_tr_b8 %5, %21\n\t"
+      "ds_read_b64_tr_b8 %6, %22\n\t"
+      "ds_read_b64_tr_b8 %7, %23\n\t"
+      "ds_read_b64_tr_b8 %8, %24\n\t"
+      "ds_read_b64_tr_b8 %9, %25\n\t"
+      "ds_read_b64_tr_b8 %10, %26\n\t"
+      "ds_read_b64_tr_b8 %11, %27\n\t"
+      "ds_read_b64_tr_b8 %12, %28\n\t"
+      "ds_read_b64_tr_b8 %13, %29\n\t"
+      "ds_read_b64_tr_b8 %14, %30\n\t"
+      "ds_read_b64_tr_b8 %15, %31\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&v"(o[4]), "=&v"(o[5]), "=&v"(o[6]),
+        "=&v"(o[7]), "=&v"(o[8]), "=&v"(o[9]), "=&v"(o[10]), "=&v"(o[11]), "=&v"(o[12]), "=&v"(o[13]),
+        "=&v"(o[14]), "=&v"(o[15])
+      : "v"(wb), "v"(wb ^ 16u), "v"(wb ^ 32u), "v"(wb ^ 48u), "v"(wb ^ 64u), "v"(wb ^ 80u), "v"(wb ^ 96u),
+        "v"(wb ^ 112u), "v"(wb ^ 128u), "v"(wb ^ 144u), "v"(wb ^ 160u), "v"(wb ^ 176u), "v"(wb ^ 192u),
+        "v"(wb ^ 208u), "v"(wb ^ 224u), "v"(wb ^ 240u)
+      : "memory");
+}
+
+template <int S, int R>  // 32-k steps per wave; ring of R steps
+__global__ __launch_bounds__(8 * kWave) void int8pc_wide_kernel(QArgs a) {
+  constexpr int TN = kWideTN, NB = TN / 16;
+  constexpr int DPS = kWide8Slot / 1024;  // weight DMAs per step
+  static_assert(R >= 1 && R <= S, "ring of at most S steps");
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const uint32_t L = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int tile = (int)(L / (uint32_t)a.ks);
+  const int ksi = (int)(L - (uint32_t)tile * a.ks);
+  const int rb = blockIdx.y;
+  const int m0 = rb * kQRows;
+  const int mrows = min(kQRows, a.M - m0);
+  const int n0 = tile * TN;
+  const int c = lane & 15, j = lane >> 4;
+  const int kbeg = ksi * (a.K / a.ks) + wv * 32 * S;
+  const size_t N = (size_t)a.N;
+  unsigned char* wl = smem + wv * a.wave_lds;
+
+  // x of every step straight to registers (issued first): lane (c, j) holds
+  // x[m0 + c][kbeg + 32 t + 8 j .. +7], its A fragment of step t.
+  u32x4 xr[S];
+  {
+    const uint16_t* xp = a.x + (size_t)min(m0 + c, a.M - 1) * a.K + kbeg + 8 * j;
 #pragma unroll
-  for (int b = 0; b < NB; ++b)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) red[(4 * j + i) * kWideRedStride + 16 * b + c] = y[b][i];
-  __syncthreads();
-  f32x4 own[2];
-#pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int q = threadIdx.x + 8 * kWave * it;  // quad index: 16 rows x 64 quads
-    const int m = q >> 6, n = 4 * (q & 63);
-    f32x4 acc = zero4;
-#pragma unroll
-    for (int w = 0; w < 8; ++w)
-      acc += *reinterpret_cast<const f32x4*>(smem + w * a.wave_lds + (m * kWideRedStride + n) * 4);
-    own[it] = acc;
+    for (int t = 0; t < S; ++t) xr[t] = *reinterpret_cast<const u32x4*>(xp + 32 * t);
   }
-  const int ntiles = a.N / TN;
-  if (a.ks > 1) {
-    const size_t tbase = ((size_t)(rb * ntiles + tile) * a.ks) * kQRows * TN;
-    // Device-coherent stores of the partial, acknowledged.
-    float* dst = a.part + tbase + (size_t)ksi * kQRows * TN + 4 * threadIdx.x;
-    st2_sc1_wait(dst, own[0], dst + 4 * 8 * kWave, own[1]);
-    __syncthreads();  // (also: every wave is done reading the spills)
-    // The flag lives in dynamic LDS: a static __shared__ would shift the
-    // dynamic base off the 256-byte alignment the swizzled addressing needs.
-    volatile uint32_t* flag = reinterpret_cast<volatile uint32_t*>(smem);
-    if (threadIdx.x == 0) {
-      uint32_t* ctr = a.cnt + rb * ntiles + tile;
-      asm volatile("" : "+v"(ctr));  // per-lane address: a vector atomic
-      const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const uint32_t last = old == (uint32_t)(a.ks - 1);
-      if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      *flag = last;
-    }
-    __syncthreads();
-    if (!*flag) return;
-    // Device-coherent 16-byte loads (sc1: miss the local L2) of every
-    // partial, then the sum in k order.
-    switch (a.ks) {
-      case 2: wide_sum_partials<2>(a.part + tbase, own); break;
-      case 4: wide_sum_partials<4>(a.part + tbase, own); break;
-      default: wide_sum_partials<8>(a.part + tbase, own); break;
-    }
-  }
+  // Step t, DMA q: lane L fills slot row rr = 4 q + L / 16 (W row
+  // kbeg + 32 t + rr), position L % 16, from chunk (L % 16) ^ (rr & 15).
+  const uint8_t* wsrc[DPS];
 #pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int q = threadIdx.x + 8 * kWave * it;
-    const int m = q >> 6, n = n0 + 4 * (q & 63);
-    if (m < mrows) epi_store_bf16x4(a.y, a.aux, a.epi, (size_t)(m0 + m) * N + n, own[it]);
+  for (int q = 0; q < DPS; ++q) {
+    const int rr = 4 * q + (lane >> 4);
+    wsrc[q] = a.w + (size_t)(kbeg + rr) * N + n0 + 16 * ((lane & 15) ^ (rr & 15));
   }
+  auto issue = [&](int t) {
+    unsigned char* slot = wl + (t % R) * kWide8Slot;
+#pragma unroll
+    for (int q = 0; q < DPS; ++q) dma16(wsrc[q] + (size_t)(32 * t) * N, slot + q * 1024);
+  };
+#pragma unroll
+  for (int t = 0; t < R; ++t) issue(t);
+
+  // Transposing read of lane (c, j): lane pair (2r, 2r + 1) of the 16-lane
+  // group names the two 8-byte halves of chunk b in slot row 8 j + r, at
+  // position b ^ (row & 15): the address of block b is wb ^ (16 b).
+  const int wrow = 8 * j + ((lane & 15) >> 1);
+  const uint32_t woff = (uint32_t)(wrow * TN + 16 * (wrow & 15) + 8 * (lane & 1));
+  const uint32_t ring0 = lds_addr(wl);
+
+  const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0
+  const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[NB], xs = zero4;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) acc[b] = zero4;
+#pragma unroll
+  for (int t = 0; t < S; ++t) {
+    const int issued = (R + t < S) ? R + t : S;  // steps issued before this wait
+    vm_wait(DPS * (issued - (t + 1)));
+    u32x2 w8[NB];
+    lds_tr8x16(ring0 + (uint32_t)((t % R) * kWide8Slot) + woff, w8);
+    // This step's slot is read: refill it.
+    if (t + R < S) issue(t + R);
+    const u32x4 A = xr[t];
+    xs = mfma16x16x32(A, ones, xs);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[b] = mfma16x16x32(A, unpack_int8(w8[b].x, w8[b].y), acc[b]);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  f32x4 y[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) y[b] = acc[b] - 128.f * xs;
+  wide_finish<true>(a, smem, wl, y, tile, ksi, rb, m0, mrows, n0, c, j);
 }
 
 template <int S, int R>  // 32-k steps per wave, ring of R steps (3 KB each)
@@ -969,6 +1107,7 @@ struct QPlan {
   int stream_steps;  // > 0: streaming kernel with this many 32-k steps per wave
   int ring;          // int8 streaming kernel: ring slots
   int wide_groups;   // > 0: wide int4 kernel with this many 64-k groups per wave
+  int wide8_steps;   // > 0: wide int8 kernel with this many 32-k steps per wave
   int deq;           // 1: dequantise W to bf16 in the workspace, then the bf16 GEMM
   int qg;            // 1: the many-row kernel of qgemm.hip (K split ks ways)
   size_t lds_bytes;
@@ -1072,6 +1211,44 @@ bool plan_wide(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p) {
   return p->lds_bytes <= kMaxLds;
 }
 
+// Wide int8 kernel: N % 256 == 0, K = ks * 8 * 32 * S with S in {4, 8, 16};
+// the fewest splits that give >= 192 workgroups, as for int4 (the same
+// counter region bounds ks > 1).  A 2-step ring: 16 KB per wave, the size of
+// its y spill.  MK_QMM_WIDE=0 disables it.
+constexpr int kWide8Ring = 2;
+
+bool plan_wide8(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p) {
+  const char* env = getenv("MK_QMM_WIDE");
+  if (fmt != MK_QFMT_INT8_PC || N % mk::kWideTN != 0 || K % 1024 != 0 || (env && env[0] == '0')) return false;
+  const int ntiles = (int)(N / mk::kWideTN);
+  const int rb = (int)((M + mk::kQRows - 1) / mk::kQRows);
+  const int ks_env = env_int("MK_QMM_KS", 0);
+  int best = 0;
+  for (int ks = 1; ks <= 8; ks *= 2) {
+    if (ks_env > 0 && ks != ks_env) continue;
+    if (K % ((int64_t)ks * 1024) != 0) break;
+    const int64_t S = K / ((int64_t)ks * 256);
+    if (S != 4 && S != 8 && S != 16) continue;
+    if (ks > 1 && (int64_t)rb * ntiles > mk::kWideCounters) break;
+    best = ks;
+    if ((int64_t)ntiles * rb * ks >= 192) break;
+  }
+  if (best == 0 || (int64_t)ntiles * rb * best < 128) return false;
+  int wl = std::max(kWide8Ring * mk::kWide8Slot, mk::kQRows * mk::kWideRedStride * 4);
+  wl = (wl + 255) & ~255;
+  p->ks = best;
+  p->nw = 8;
+  p->ntiles = ntiles;
+  p->rowblocks = rb;
+  p->wide8_steps = (int)(K / ((int64_t)best * 256));
+  p->kwave = 32 * p->wide8_steps;
+  p->wave_lds = wl;
+  p->lds_bytes = (size_t)8 * wl;
+  p->part_bytes = best > 1 ? (int64_t)mk::kWidePartOffset + (int64_t)rb * ntiles * best * mk::kQRows * mk::kWideTN * 4
+                           : 0;
+  return p->lds_bytes <= kMaxLds;
+}
+
 // Many rows.  The streaming kernels re-read the weights once per 16 rows;
 // from kQgMinRows rows the qgemm.hip kernel (weights read once per 256 rows,
 // dequantised in LDS) takes over, and from kDeqMinRows rows W is dequantised
@@ -1105,6 +1282,8 @@ bool plan_q(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p, int64_t qg_cap =
   }
   if (plan_wide(fmt, M, K, N, p)) return true;
   p->wide_groups = 0;
+  if (plan_wide8(fmt, M, K, N, p)) return true;
+  p->wide8_steps = 0;
   p->ntiles = (int)((N + mk::kQCols - 1) / mk::kQCols);
   p->rowblocks = (int)((M + mk::kQRows - 1) / mk::kQRows);
   if (plan_stream(fmt, K, N, p)) {
@@ -1156,6 +1335,15 @@ hipError_t launch_wide(const mk::QArgs& a, const QPlan& p, hipStream_t st) {
   hipError_t e = lds_opt_in((const void*)mk::int4g64_wide_kernel<G, R>, p.lds_bytes);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((mk::int4g64_wide_kernel<G, R>), grid, block, p.lds_bytes, st, a);
+  return hipGetLastError();
+}
+
+template <int S>
+hipError_t launch_wide8(const mk::QArgs& a, const QPlan& p, hipStream_t st) {
+  dim3 grid(p.ntiles * p.ks, p.rowblocks), block(8 * mk::kWave);
+  hipError_t e = lds_opt_in((const void*)mk::int8pc_wide_kernel<S, kWide8Ring>, p.lds_bytes);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((mk::int8pc_wide_kernel<S, kWide8Ring>), grid, block, p.lds_bytes, st, a);
   return hipGetLastError();
 }
 
@@ -1278,6 +1466,13 @@ int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, v
       case 1: e = launch_wide<1>(a, p, st); break;
       case 2: e = launch_wide<2>(a, p, st); break;
       default: e = launch_wide<4>(a, p, st); break;
+    }
+  } else if (p.wide8_steps > 0) {
+    if (p.part_bytes > 0) a.cnt = static_cast<uint32_t*>(ws);
+    switch (p.wide8_steps) {
+      case 4: e = launch_wide8<4>(a, p, st); break;
+      case 8: e = launch_wide8<8>(a, p, st); break;
+      default: e = launch_wide8<16>(a, p, st); break;
     }
   } else if (p.stream_steps > 0) {
     switch (p.stream_steps) {

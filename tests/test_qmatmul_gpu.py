@@ -314,3 +314,53 @@ def test_int4_wide_and_split_k_paths_share_a_workspace():
     # Every completed call leaves the arrival counters at zero.
     ws = ops.workspace(1, "cuda:0")
     assert int(ws[: 64 * 1024].count_nonzero()) == 0
+
+
+# Shapes that take the 256-column int8 kernel (plan "wide8"): steps per wave
+# S = 4, 8, 16, split-K factors 1, 2, 4 with the in-kernel last-arriver
+# reduction, a partial second row block, and N not a multiple of the 64-column
+# kernels' 192-workgroup split.
+WIDE8_SHAPES = [
+    (16, 4096, 14336),   # ks = 4, S = 4 (the headline plan)
+    (20, 4096, 14336),   # two row blocks (the second has 4 rows), ks = 2, S = 8
+    (64, 4096, 14336),   # four row blocks, ks = 1, S = 16
+    (1, 4096, 8192),     # ks = 4, S = 4, 128 workgroups
+    (16, 8192, 14336),   # ks = 4, S = 8
+]
+
+
+@pytest.mark.parametrize("M,K,N", WIDE8_SHAPES)
+def test_int8_wide_kernel_matches_oracle(M, K, N):
+    ops = _ops()
+    rng = np.random.default_rng(11 * M + K + N)
+    x, w, s = quant.make_int8_case(rng, M, K, N)
+    print(f"int8 wide case M={M} K={K} N={N}", flush=True)
+    y = ops.int8_pc_matmul(dev_bf16(x), dev(w), dev(s))
+    torch.cuda.synchronize()
+    ref = cport.int8_pc_matmul(x, w, s)
+    assert_rel_close(host_bf16(y), ref, BF16_RTOL, f"int8 wide {M}x{K}x{N}")
+
+
+def test_int8_wide_kernel_is_planned_and_deterministic(monkeypatch):
+    """The headline shape plans the wide int8 kernel (its workspace holds the
+    split-K partials), repeated calls give the same bits, the arrival
+    counters return to zero, and the 64-column kernel (MK_QMM_WIDE=0) agrees
+    within the bf16 tolerance."""
+    ops = _ops()
+    from mi355x import _lib
+    M, K, N = 16, 4096, 14336
+    assert _lib.lib().mk_qmatmul_workspace_bytes(_lib.MK_QFMT_INT8_PC, M, K, N) == 64 * 1024 + 4 * 56 * 16 * 256 * 4
+    rng = np.random.default_rng(29)
+    x, w, s = quant.make_int8_case(rng, M, K, N)
+    args = (dev_bf16(x), dev(w), dev(s))
+    first = host_bf16_bits(ops.int8_pc_matmul(*args))
+    for _ in range(4):
+        assert np.array_equal(host_bf16_bits(ops.int8_pc_matmul(*args)), first)
+    ws = ops.workspace(1, "cuda:0")
+    assert int(ws[: 64 * 1024].count_nonzero()) == 0
+    monkeypatch.setenv("MK_QMM_WIDE", "0")
+    assert _lib.lib().mk_qmatmul_workspace_bytes(_lib.MK_QFMT_INT8_PC, M, K, N) == 0
+    y64 = ops.int8_pc_matmul(*args)
+    torch.cuda.synchronize()
+    ref = cport.int8_pc_matmul(x, w, s)
+    assert_rel_close(host_bf16(y64), ref, BF16_RTOL, "int8 64-column kernel")
