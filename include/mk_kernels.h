@@ -97,6 +97,29 @@ int mk_int8pc_matmul_epilogue_bf16(const void* x, const void* w, const void* sca
                                    const void* aux, int epilogue, int64_t M, int64_t K, int64_t N,
                                    void* workspace, int64_t workspace_bytes, void* stream);
 
+/* y = silu(x @ Wg) * (x @ Wu), bf16 [M, N], from two separate quantized
+ * weights of the same format and shape (int4: packed / scale / zero of each;
+ * int8: weight / scale of each), the SwiGLU of the reference's transformer
+ * benchmark (benchmarks/vs_cpu.py:603-626) as jax.jit lowers it.  No single
+ * reference handler does this: the reference runs the two products and the
+ * elementwise ops separately; the result here is bit-identical to that
+ * sequence (the two *_matmul_bf16 calls, then the SwiGLU elementwise
+ * program).  Both weights are dequantised into one interleaved bf16 buffer
+ * in the workspace and multiplied by one GEMM.  Many-row shapes only: the
+ * workspace size is 0 or more when the shape runs (M % 256 == 0,
+ * N % 128 == 0, K % 64 == 0, M on the dequantise-then-GEMM route), -1 when
+ * it does not (then the call returns MK_EUNSUPPORTED). */
+int64_t mk_qmatmul_swiglu_pair_workspace_bytes(int fmt, int64_t M, int64_t K, int64_t N);
+
+int mk_int4g64_matmul_swiglu_pair_bf16(const void* x, const void* wg_packed, const void* g_scale,
+                                       const void* g_zero, const void* wu_packed, const void* u_scale,
+                                       const void* u_zero, void* y, int64_t M, int64_t K, int64_t N,
+                                       void* workspace, int64_t workspace_bytes, void* stream);
+
+int mk_int8pc_matmul_swiglu_pair_bf16(const void* x, const void* wg, const void* g_scale, const void* wu,
+                                      const void* u_scale, void* y, int64_t M, int64_t K, int64_t N,
+                                      void* workspace, int64_t workspace_bytes, void* stream);
+
 /* mk_int4g64_matmul_bf16 without a workspace argument, for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.

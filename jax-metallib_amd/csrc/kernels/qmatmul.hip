@@ -1041,15 +1041,20 @@ __global__ __launch_bounds__(256) void qmm_splitk_reduce_kernel(QArgs a) {
 // exact in f32 (at most 12 significant bits) and rounded once to bf16 (RNE);
 // int8: w * s is rounded to f32, then to bf16.  One thread: 8
 // columns of one packed row (int4: k = 2r and 2r + 1) or of one k row (int8);
-// every load and store is a whole 8- or 16-byte vector.
+// every load and store is a whole 8- or 16-byte vector.  wd rows are ldd
+// elements apart; with half = 0 / 1 (gate / up of a paired SwiGLU product)
+// column n goes to 32 (n / 16) + n % 16 + 16 half of a [K, 2N] buffer, the
+// 16-column interleave the MK_EPI_SWIGLU_PAIRS epilogue reads (8-column
+// groups never straddle a 16-column block); half < 0 keeps column n.
 template <bool INT4>
-__global__ __launch_bounds__(256) void qmm_dequant_kernel(QArgs a, uint16_t* wd) {
+__global__ __launch_bounds__(256) void qmm_dequant_kernel(QArgs a, uint16_t* wd, int64_t ldd, int half) {
   const int N8 = a.N / 8;
   const int64_t rows = INT4 ? a.K / 2 : a.K;
   const int64_t total = rows * N8;
   for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += (int64_t)gridDim.x * 256) {
     const int64_t r = t / N8;
     const int c0 = (int)(t - r * N8) * 8;
+    const int64_t d0 = half < 0 ? c0 : 32 * (c0 / 16) + c0 % 16 + 16 * half;
     const u32x2 wb = *reinterpret_cast<const u32x2*>(a.w + r * a.N + c0);
     if (INT4) {
       const int64_t g = r / 32;  // 64-k group of rows 2r, 2r + 1
@@ -1072,8 +1077,8 @@ __global__ __launch_bounds__(256) void qmm_dequant_kernel(QArgs a, uint16_t* wd)
         lo[j / 2] = pack_bf16x2(e[0], e[1]);
         hi[j / 2] = pack_bf16x2(o[0], o[1]);
       }
-      *reinterpret_cast<u32x4*>(wd + (2 * r) * a.N + c0) = u32x4{lo[0], lo[1], lo[2], lo[3]};
-      *reinterpret_cast<u32x4*>(wd + (2 * r + 1) * a.N + c0) = u32x4{hi[0], hi[1], hi[2], hi[3]};
+      *reinterpret_cast<u32x4*>(wd + (2 * r) * ldd + d0) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+      *reinterpret_cast<u32x4*>(wd + (2 * r + 1) * ldd + d0) = u32x4{hi[0], hi[1], hi[2], hi[3]};
     } else {
       const float* sp = static_cast<const float*>(a.s) + c0;
       const f32x4 s0 = *reinterpret_cast<const f32x4*>(sp), s1 = *reinterpret_cast<const f32x4*>(sp + 4);
@@ -1085,7 +1090,7 @@ __global__ __launch_bounds__(256) void qmm_dequant_kernel(QArgs a, uint16_t* wd)
         const int8_t b1 = (int8_t)(((j < 4 ? wb.x : wb.y) >> (8 * ((j + 1) & 3))) & 0xffu);
         out[j / 2] = pack_bf16x2((float)b0 * sv[j], (float)b1 * sv[j + 1]);
       }
-      *reinterpret_cast<u32x4*>(wd + r * a.N + c0) = u32x4{out[0], out[1], out[2], out[3]};
+      *reinterpret_cast<u32x4*>(wd + r * ldd + d0) = u32x4{out[0], out[1], out[2], out[3]};
     }
   }
 }
@@ -1450,9 +1455,9 @@ int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, v
     const int64_t total = (fmt == MK_QFMT_INT4_G64 ? K / 2 : K) * (N / 8);
     const int blocks = (int)std::min<int64_t>((total + 255) / 256, 16384);
     if (fmt == MK_QFMT_INT4_G64)
-      hipLaunchKernelGGL(mk::qmm_dequant_kernel<true>, dim3(blocks), dim3(256), 0, st, a, wd);
+      hipLaunchKernelGGL(mk::qmm_dequant_kernel<true>, dim3(blocks), dim3(256), 0, st, a, wd, (int64_t)N, -1);
     else
-      hipLaunchKernelGGL(mk::qmm_dequant_kernel<false>, dim3(blocks), dim3(256), 0, st, a, wd);
+      hipLaunchKernelGGL(mk::qmm_dequant_kernel<false>, dim3(blocks), dim3(256), 0, st, a, wd, (int64_t)N, -1);
     e = hipGetLastError();
     if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: dequantise launch failed: %s", fn, hipGetErrorString(e));
     const int rc = epi == MK_EPI_NONE ? mk_gemm_bf16(x, wd, y, 1, M, N, K, 0, stream)
@@ -1540,6 +1545,90 @@ extern "C" int mk_int8pc_matmul_epilogue_bf16(const void* x, const void* w, cons
   mkc::clear_error();
   return run_q(MK_QFMT_INT8_PC, x, w, scale, nullptr, y, M, K, N, workspace, workspace_bytes, stream, aux,
                epilogue);
+}
+
+// ---------------------------------------------------------------------------
+// Paired SwiGLU product from two separate weights, silu(x @ Wg) * (x @ Wu):
+// both weights dequantised into one bf16 [K, 2N] buffer in the workspace,
+// their 16-column blocks interleaved (gate, up, gate, up, ...), then one bf16
+// GEMM whose MK_EPI_SWIGLU_PAIRS store writes silu(gate) * up.  The
+// dequantised values, the GEMM's k order and the epilogue's roundings are
+// those of the two products followed by the SwiGLU program, so the result is
+// bit-identical to that form; it saves the gate product's bf16 round trip
+// through HBM and one GEMM launch.  Many-row shapes only (the
+// dequantise-then-GEMM route, M % 256 == 0, N % 128 == 0).
+// ---------------------------------------------------------------------------
+namespace {
+
+int64_t pair_workspace(int fmt, int64_t M, int64_t K, int64_t N) {
+  if ((fmt != MK_QFMT_INT4_G64 && fmt != MK_QFMT_INT8_PC) || M <= 0 || K <= 0 || N <= 0 || K % 64 != 0 ||
+      N % 128 != 0 || M % 256 != 0)
+    return -1;
+  QPlan p;
+  if (!plan_q(fmt, M, K, N, &p) || !p.deq) return -1;
+  return (int64_t)mk::kWidePartOffset + K * (2 * N) * 2;
+}
+
+int run_pair(int fmt, const void* x, const void* wg, const void* sg, const void* zg, const void* wu, const void* su,
+             const void* zu, void* y, int64_t M, int64_t K, int64_t N, void* ws, int64_t ws_bytes, void* stream) {
+  const char* fn = fmt == MK_QFMT_INT4_G64 ? "mk_int4g64_matmul_swiglu_pair_bf16" : "mk_int8pc_matmul_swiglu_pair_bf16";
+  if (!x || !wg || !sg || !wu || !su || !y || (fmt == MK_QFMT_INT4_G64 && (!zg || !zu)))
+    return mkc::fail(MK_EINVAL, "%s: null pointer argument", fn);
+  if (M <= 0 || K <= 0 || N <= 0)
+    return mkc::fail(MK_EINVAL, "%s: M, K, N must be positive (got %lld, %lld, %lld)", fn, (long long)M,
+                     (long long)K, (long long)N);
+  if (M > (1 << 20) || K > (1 << 24) || N > (1 << 25) || (M * K) > (int64_t)1 << 31)
+    return mkc::fail(MK_EINVAL, "%s: shape too large", fn);
+  const int64_t need = pair_workspace(fmt, M, K, N);
+  if (need < 0)
+    return mkc::fail(MK_EUNSUPPORTED, "%s: needs the many-row route with M %% 256 == 0, N %% 128 == 0, "
+                     "K %% 64 == 0 (got M=%lld, K=%lld, N=%lld)", fn, (long long)M, (long long)K, (long long)N);
+  if (!ws || ws_bytes < need)
+    return mkc::fail(MK_EWORKSPACE, "%s: workspace of %lld bytes needed, %lld given", fn, (long long)need,
+                     (long long)ws_bytes);
+  uint16_t* wd = reinterpret_cast<uint16_t*>(static_cast<unsigned char*>(ws) + mk::kWidePartOffset);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t total = (fmt == MK_QFMT_INT4_G64 ? K / 2 : K) * (N / 8);
+  const int blocks = (int)std::min<int64_t>((total + 255) / 256, 16384);
+  for (int half = 0; half < 2; ++half) {
+    mk::QArgs a{};
+    a.w = static_cast<const uint8_t*>(half ? wu : wg);
+    a.s = half ? su : sg;
+    a.z = static_cast<const uint8_t*>(half ? zu : zg);
+    a.M = (int)M;
+    a.K = (int)K;
+    a.N = (int)N;
+    if (fmt == MK_QFMT_INT4_G64)
+      hipLaunchKernelGGL(mk::qmm_dequant_kernel<true>, dim3(blocks), dim3(256), 0, st, a, wd, 2 * N, half);
+    else
+      hipLaunchKernelGGL(mk::qmm_dequant_kernel<false>, dim3(blocks), dim3(256), 0, st, a, wd, 2 * N, half);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: dequantise launch failed: %s", fn, hipGetErrorString(e));
+  }
+  return mk_gemm_bf16_epilogue(x, wd, y, nullptr, MK_EPI_SWIGLU_PAIRS, 1, M, 2 * N, K, stream);
+}
+
+}  // namespace
+
+extern "C" int64_t mk_qmatmul_swiglu_pair_workspace_bytes(int fmt, int64_t M, int64_t K, int64_t N) {
+  return pair_workspace(fmt, M, K, N);
+}
+
+extern "C" int mk_int4g64_matmul_swiglu_pair_bf16(const void* x, const void* wg_packed, const void* g_scale,
+                                                  const void* g_zero, const void* wu_packed, const void* u_scale,
+                                                  const void* u_zero, void* y, int64_t M, int64_t K, int64_t N,
+                                                  void* workspace, int64_t workspace_bytes, void* stream) {
+  mkc::clear_error();
+  return run_pair(MK_QFMT_INT4_G64, x, wg_packed, g_scale, g_zero, wu_packed, u_scale, u_zero, y, M, K, N, workspace,
+                  workspace_bytes, stream);
+}
+
+extern "C" int mk_int8pc_matmul_swiglu_pair_bf16(const void* x, const void* wg, const void* g_scale, const void* wu,
+                                                 const void* u_scale, void* y, int64_t M, int64_t K, int64_t N,
+                                                 void* workspace, int64_t workspace_bytes, void* stream) {
+  mkc::clear_error();
+  return run_pair(MK_QFMT_INT8_PC, x, wg, g_scale, nullptr, wu, u_scale, nullptr, y, M, K, N, workspace,
+                  workspace_bytes, stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -359,6 +359,7 @@ class Planner {
     }
     if (n == "add" || n == "multiply") {
       int s;
+      if (n == "multiply" && try_qmm_pair(v, &s)) return s;
       if (try_qmm_epilogue(v, &s)) return s;
     }
     if (n == "convert") {
@@ -1277,6 +1278,53 @@ class Planner {
   // costs more than the separate program (the decoder layer measured 1.268
   // vs 1.255 ms per call with and without it), so it is folded only with
   // MK_PLAN_EPILOGUES=all; MK_PLAN_EPILOGUES=0 folds nothing.
+  // silu(x @ Wg) * (x @ Wu) with both products dequant-matmuls of one x, one
+  // format and one shape, read by nothing else, on the many-row route: one
+  // paired step (both weights dequantised into an interleaved buffer, one
+  // GEMM with the SwiGLU store), bit-identical to the two products and the
+  // SwiGLU program.  MK_PLAN_PAIRS=0 (or MK_PLAN_EPILOGUES=0) keeps them
+  // apart.
+  bool try_qmm_pair(int v, int* out) {
+    const char* env = getenv("MK_PLAN_EPILOGUES");
+    const char* pe = getenv("MK_PLAN_PAIRS");
+    if ((env && env[0] == '0') || (pe && pe[0] == '0')) return false;
+    const Op* op = def(v);
+    if (op->name != "multiply" || type(v).dtype != DT_BF16 || op->operands.size() != 2) return false;
+    for (int order = 0; order < 2; ++order) {
+      const int up = op->operands[order], act = op->operands[1 - order];
+      int a, b;
+      if (uses(up) != 1 || uses(act) != 1 || !factors(act, &a, &b)) continue;
+      int g = -1;
+      if (is(b, "logistic") && def(b)->operands[0] == a) g = a;
+      else if (is(a, "logistic") && def(a)->operands[0] == b) g = b;
+      if (g < 0 || uses(g) != 2 || uses(g == a ? b : a) != 1) continue;
+      QmmMatch qg, qu;
+      if (!match_qmm(g, &qg) || !match_qmm(up, &qu)) continue;
+      if (qg.x != qu.x || qg.fmt != qu.fmt || qg.M != qu.M || qg.K != qu.K || qg.N != qu.N) continue;
+      if (type(g).dims != type(v).dims || type(up).dims != type(v).dims) continue;
+      const int64_t ws = mk_qmatmul_swiglu_pair_workspace_bytes(qg.fmt, qg.M, qg.K, qg.N);
+      if (ws < 0) continue;
+      Step st;
+      st.kind = qg.fmt == MK_QFMT_INT4_G64 ? ST_QMM_PAIR_INT4 : ST_QMM_PAIR_INT8;
+      st.dt = MK_DT_BF16;
+      if (qg.fmt == MK_QFMT_INT4_G64)
+        st.in = {need(qg.x), need(qg.w), need(qg.s), need(qg.z), need(qu.w), need(qu.s), need(qu.z)};
+      else
+        st.in = {need(qg.x), need(qg.w), need(qg.s), need(qu.w), need(qu.s)};
+      st.M = qg.M;
+      st.K = qg.K;
+      st.N = qg.N;
+      st.out = temp_for(v);
+      plan_.workspace_bytes = std::max(plan_.workspace_bytes, ws);
+      st.desc = std::string(qg.fmt == MK_QFMT_INT4_G64 ? "int4_g64" : "int8_pc") + " swiglu pair matmul M=" +
+                std::to_string(qg.M) + " K=" + std::to_string(qg.K) + " N=" + std::to_string(qg.N) + " -> bf16";
+      plan_.steps.push_back(st);
+      *out = st.out;
+      return true;
+    }
+    return false;
+  }
+
   bool try_qmm_epilogue(int v, int* out) {
     const char* env = getenv("MK_PLAN_EPILOGUES");
     if (env && env[0] == '0') return false;

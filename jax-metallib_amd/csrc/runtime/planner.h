@@ -43,7 +43,9 @@ enum StepKind {
   ST_LAYOUT,  // strided copy (transpose, slice, broadcast, one concatenate operand)
   ST_IOTA,
   ST_ROPE,    // mk_rope_qkv_split_bf16: in {qkv, cos, sin}, out q, outs {k, v}
-  ST_ATTN     // mk_attention_causal_bf16: in {q, k, v}, out [B, S, H, D]
+  ST_ATTN,    // mk_attention_causal_bf16: in {q, k, v}, out [B, S, H, D]
+  ST_QMM_PAIR_INT4,  // mk_int4g64_matmul_swiglu_pair_bf16: in {x, wg, sg, zg, wu, su, zu}
+  ST_QMM_PAIR_INT8   // mk_int8pc_matmul_swiglu_pair_bf16: in {x, wg, sg, wu, su}
 };
 
 struct Step {

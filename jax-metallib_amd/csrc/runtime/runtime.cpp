@@ -368,6 +368,12 @@ int run_step(const mkrt::Step& st, const std::vector<void*>& mem, void* ws, int6
         return mk_int8pc_matmul_epilogue_bf16(in(0), in(1), in(2), out, in(3), st.epi, st.M, st.K, st.N, ws, ws_bytes,
                                               s);
       return mk_int8pc_matmul_bf16(in(0), in(1), in(2), out, st.M, st.K, st.N, ws, ws_bytes, s);
+    case mkrt::ST_QMM_PAIR_INT4:
+      return mk_int4g64_matmul_swiglu_pair_bf16(in(0), in(1), in(2), in(3), in(4), in(5), in(6), out, st.M, st.K,
+                                                st.N, ws, ws_bytes, s);
+    case mkrt::ST_QMM_PAIR_INT8:
+      return mk_int8pc_matmul_swiglu_pair_bf16(in(0), in(1), in(2), in(3), in(4), out, st.M, st.K, st.N, ws, ws_bytes,
+                                               s);
     case mkrt::ST_SOFTMAX:
       return mk_softmax_lastdim(st.dt, in(0), out, st.rows, st.cols, s);
     case mkrt::ST_RMSNORM:

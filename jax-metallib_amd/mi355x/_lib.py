@@ -49,6 +49,9 @@ SIGNATURES = {
     "mk_gemm_bf16_epilogue": (_i32, [_p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _p]),
     "mk_int4g64_matmul_epilogue_bf16": (_i32, [_p, _p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _p, _i64, _p]),
     "mk_int8pc_matmul_epilogue_bf16": (_i32, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _p, _i64, _p]),
+    "mk_qmatmul_swiglu_pair_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64]),
+    "mk_int4g64_matmul_swiglu_pair_bf16": (_i32, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p]),
+    "mk_int8pc_matmul_swiglu_pair_bf16": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p]),
     "mk_gemm_f32": (_i32, [_p, _p, _p, _i64, _i64, _i64, _i64, _p]),
     "mk_softmax_lastdim": (_i32, [_i32, _p, _p, _i64, _i64, _p]),
     "mk_rope_qkv_split_bf16": (_i32, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _p]),

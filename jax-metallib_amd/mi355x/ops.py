@@ -141,6 +141,43 @@ def int8_pc_matmul(x, w, scale, out=None):
     return y
 
 
+def swiglu_pair_matmul(x, wg, wu, out=None):
+    """y = silu(x @ Wg) * (x @ Wu) -> bf16 [M, N] from two separate quantized
+    weights: wg, wu = (w_packed, scale, zero) as for int4_g64_matmul, or
+    (w, scale) as for int8_pc_matmul.  Bit-identical to the two products
+    followed by the SwiGLU elementwise program; many-row shapes only (the C-ABI
+    returns MK_EUNSUPPORTED otherwise)."""
+    int4 = len(wg) == 3
+    if len(wu) != len(wg) or len(wg) not in (2, 3):
+        raise ValueError("swiglu_pair_matmul: wg and wu must both be int4 (3 arrays) or int8 (2 arrays)")
+    _require(x, _BF16, "x")
+    M, K = x.shape
+    N = wg[0].shape[1]
+    for w in (wg, wu):
+        if int4:
+            _require(w[0], (torch.uint8,), "w_packed")
+            _require(w[1], _BF16, "scale")
+            _require(w[2], (torch.uint8,), "zero")
+            if w[0].shape != (K // 2, N) or w[1].shape != (K // 64, N) or w[2].shape != (K // 64, N):
+                raise ValueError("swiglu_pair_matmul: inconsistent int4 shapes")
+        else:
+            _require(w[0], (torch.int8,), "w")
+            _require(w[1], (torch.float32,), "scale")
+            if w[0].shape != (K, N) or w[1].shape != (N,):
+                raise ValueError("swiglu_pair_matmul: inconsistent int8 shapes")
+    fmt = _lib.MK_QFMT_INT4_G64 if int4 else _lib.MK_QFMT_INT8_PC
+    y = out if out is not None else torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    nb = lib().mk_qmatmul_swiglu_pair_workspace_bytes(fmt, M, K, N)
+    ws = workspace(nb, x.device) if nb > 0 else None
+    if int4:
+        check(lib().mk_int4g64_matmul_swiglu_pair_bf16(_ptr(x), *(_ptr(a) for a in wg), *(_ptr(a) for a in wu),
+                                                       _ptr(y), M, K, N, _ptr(ws), max(nb, 0), _stream(x.device)))
+    else:
+        check(lib().mk_int8pc_matmul_swiglu_pair_bf16(_ptr(x), *(_ptr(a) for a in wg), *(_ptr(a) for a in wu),
+                                                      _ptr(y), M, K, N, _ptr(ws), max(nb, 0), _stream(x.device)))
+    return y
+
+
 def _bmk(a, b):
     if a.dim() == 2:
         a2, b2 = a.unsqueeze(0), b.unsqueeze(0)

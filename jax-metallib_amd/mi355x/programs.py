@@ -457,6 +457,37 @@ def _int4_mm(e, x, p, s, z, M, K, N):
     return e.cvt(y, _t([M, N], "f32"), _t([M, N], "bf16"))
 
 
+def _int8_mm(e, x, w, s, M, K, N):
+    """x @ (w * s[None, :]) as bf16 for the int8 per-channel weight (w, s),
+    written like int8_pc_matmul's function."""
+    tw, twf, t1n = _t([K, N], "i8"), _t([K, N], "f32"), _t([1, N], "f32")
+    wf = e.bin("multiply", e.cvt(w, tw, twf), e.bcast(e.bcast(s, _t([N], "f32"), [1], t1n), t1n, [0, 1], twf), twf)
+    xf = e.cvt(x, _t([M, K], "bf16"), _t([M, K], "f32"))
+    y = e(f"stablehlo.dot_general {xf}, {wf}, contracting_dims = [1] x [0], precision = [DEFAULT, DEFAULT] : "
+          f"({_t([M, K], 'f32')}, {twf}) -> {_t([M, N], 'f32')}")
+    return e.cvt(y, _t([M, N], "f32"), _t([M, N], "bf16"))
+
+
+def swiglu_mlp(M, K, N, fmt="int4"):
+    """The decoder's gated projection pair on its own:
+
+        def f(x, *wg, *wu):  # x bf16 [M, K]; wg, wu as int4_g64_matmul / int8_pc_matmul
+            return jax.nn.silu(qmm(x, *wg)) * qmm(x, *wu)"""
+    e = _Body()
+    ty = _t([M, N], "bf16")
+    if fmt == "int4":
+        G = K // 64
+        wt = [_t([K // 2, N], "ui8"), _t([G, N], "bf16"), _t([G, N], "ui8")]
+        g = _int4_mm(e, "%arg0", "%arg1", "%arg2", "%arg3", M, K, N)
+        u = _int4_mm(e, "%arg0", "%arg4", "%arg5", "%arg6", M, K, N)
+    else:
+        wt = [_t([K, N], "i8"), _t([N], "f32")]
+        g = _int8_mm(e, "%arg0", "%arg1", "%arg2", M, K, N)
+        u = _int8_mm(e, "%arg0", "%arg3", "%arg4", M, K, N)
+    act = e.bin("multiply", e.bin("multiply", g, e.un("logistic", g, ty), ty), u, ty)
+    return _module("jit_swiglu_mlp", [_t([M, K], "bf16")] + wt + wt, [ty], e.lines + [f"return {act} : {ty}"])
+
+
 def _softmax_bf16(e, x, shape):
     """jax.nn.softmax(x, axis=-1) on bf16 x of any rank (the sum upcast to f32)."""
     r = len(shape)

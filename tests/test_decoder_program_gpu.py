@@ -200,3 +200,44 @@ def test_decoder_stack_vs_oracle(client):
         row_rel = np.abs(y[b] - ref).max(axis=1) / np.abs(ref).max(axis=1)
         print(f"[decoder-program] stack batch {b}: worst row rel err {row_rel.max():.3e}", flush=True)
         assert row_rel.max() <= BF16_RTOL, (b, row_rel.max())
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+def test_swiglu_pair_program_bit_identical_and_vs_oracle(client, monkeypatch, fmt):
+    """silu(x @ Wg) * (x @ Wu) from its StableHLO at a many-row shape: the
+    paired plan (one step) against the two-product plan, bit for bit, and
+    against the float64 oracle at the bf16 tolerance."""
+    from oracle import quant
+    M, K, N = 1024, 512, 256
+    rng = np.random.default_rng(41 + len(fmt))
+    if fmt == "int4":
+        x, pg, sg, zg = synthetic.int4_case(rng, M, K, N)
+        _, pu, su, zu = synthetic.int4_case(rng, M, K, N)
+        args = [(x, rt.BF16), (pg, None), (sg, rt.BF16), (zg, None), (pu, None), (su, rt.BF16), (zu, None)]
+        g, _ = quant.int4_g64_matmul(x, pg, sg, zg)
+        u, _ = quant.int4_g64_matmul(x, pu, su, zu)
+    else:
+        x, wg, sg = synthetic.int8_case(rng, M, K, N)
+        _, wu, su = synthetic.int8_case(rng, M, K, N)
+        args = [(x, rt.BF16), (wg, None), (sg, None), (wu, None), (su, None)]
+        g, _ = quant.int8_pc_matmul(x, wg, sg)
+        u, _ = quant.int8_pc_matmul(x, wu, su)
+    text = P.swiglu_mlp(M, K, N, fmt)
+    outs = []
+    for env in ("1", "0"):
+        monkeypatch.setenv("MK_PLAN_PAIRS", env)
+        print(f"[decoder-program] swiglu pair {fmt} M={M} K={K} N={N} pairs={env}", flush=True)
+        exe = client.compile(text)
+        assert ("swiglu pair" in exe.plan) == (env == "1")
+        bufs = [client.buffer(a, t) if t else client.buffer(a) for a, t in args]
+        res, done = exe.execute(bufs)
+        done.wait()
+        outs.append(res[0].to_numpy())
+        for b_ in bufs + res:
+            b_.close()
+        exe.close()
+    assert np.array_equal(outs[0], outs[1])
+    ref = g / (1.0 + np.exp(-g)) * u
+    y = bf16_bits_to_f32(outs[0]).astype(np.float64)
+    row_rel = np.abs(y - ref).max(axis=1) / np.abs(ref).max(axis=1)
+    assert row_rel.max() <= BF16_RTOL, row_rel.max()

@@ -165,3 +165,45 @@ def test_swiglu_pairs_rejects_unsupported_shapes():
     x, p, s, z = quant.make_int4_case(rng, 16, 256, 256)
     with pytest.raises(RuntimeError):
         ops.int4_g64_matmul(dev_bf16(x), dev(p), dev_bf16(s), dev(z), epilogue="swiglu_pairs")
+
+
+# (1024, 512, 256) / (768, 2048, 1024): the dequantise-then-GEMM route with the
+# ring and the pipelined GEMM; (1024, 256, 384): N not a multiple of 256.
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+@pytest.mark.parametrize("M,K,N", [(1024, 512, 256), (768, 2048, 1024), (1024, 256, 384)])
+def test_swiglu_pair_from_separate_weights_matches_two_products(fmt, M, K, N):
+    """mk_*_matmul_swiglu_pair_bf16 (both weights dequantised into one
+    interleaved buffer, one GEMM) equals, bit for bit, the two products
+    followed by the SwiGLU elementwise program."""
+    ops = _ops()
+    rng = np.random.default_rng(M + K + N + len(fmt))
+    if fmt == "int4":
+        x, pg, sg, zg = quant.make_int4_case(rng, M, K, N)
+        _, pu, su, zu = quant.make_int4_case(rng, M, K, N)
+        wg, wu = (dev(pg), dev_bf16(sg), dev(zg)), (dev(pu), dev_bf16(su), dev(zu))
+        mm = ops.int4_g64_matmul
+    else:
+        x, wg8, sg = quant.make_int8_case(rng, M, K, N)
+        _, wu8, su = quant.make_int8_case(rng, M, K, N)
+        wg, wu = (dev(wg8), dev(sg)), (dev(wu8), dev(su))
+        mm = ops.int8_pc_matmul
+    xd = dev_bf16(x)
+    print(f"[epilogue] {fmt} swiglu pair from separate weights M={M} K={K} N={N}", flush=True)
+    ref = _unfused(ops, mm(xd, *wu), mm(xd, *wg), "swiglu")
+    y = ops.swiglu_pair_matmul(xd, wg, wu)
+    torch.cuda.synchronize()
+    assert torch.equal(y, ref)
+
+
+def test_swiglu_pair_rejects_decode_shapes():
+    ops = _ops()
+    from mi355x import _lib
+    L = _lib.lib()
+    assert L.mk_qmatmul_swiglu_pair_workspace_bytes(_lib.MK_QFMT_INT4_G64, 16, 256, 256) == -1
+    assert L.mk_qmatmul_swiglu_pair_workspace_bytes(_lib.MK_QFMT_INT4_G64, 1024, 256, 200) == -1
+    assert L.mk_qmatmul_swiglu_pair_workspace_bytes(_lib.MK_QFMT_INT8_PC, 1024, 256, 256) == 64 * 1024 + 256 * 512 * 2
+    rng = np.random.default_rng(3)
+    x, p, s, z = quant.make_int4_case(rng, 16, 256, 256)
+    w = (dev(p), dev_bf16(s), dev(z))
+    with pytest.raises(RuntimeError):
+        ops.swiglu_pair_matmul(dev_bf16(x), w, w)

@@ -277,6 +277,26 @@ def test_residual_and_swiglu_fold_into_the_dequant_matmul(fmt, monkeypatch):
                                                "elementwise 3 instr, 2 inputs, n=65536 bf16"]
 
 
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+def test_swiglu_pair_plans_one_step_on_the_many_row_route(fmt, monkeypatch):
+    name = "int4_g64" if fmt == "int4" else "int8_pc"
+    assert plan(P.swiglu_mlp(1024, 256, 512, fmt)) == [f"{name} swiglu pair matmul M=1024 K=256 N=512 -> bf16"]
+    # below the dequantise-then-GEMM route (and with pairing off) the two
+    # products and the SwiGLU program stay apart
+    mm = "int4_g64_matmul" if fmt == "int4" else "int8_pc_matmul"
+    apart = [f"{mm} M=256 K=256 N=512 -> bf16"] * 2 + ["elementwise 5 instr, 2 inputs, n=131072 bf16"]
+    assert plan(P.swiglu_mlp(256, 256, 512, fmt)) == apart
+    monkeypatch.setenv("MK_PLAN_PAIRS", "0")
+    assert plan(P.swiglu_mlp(1024, 256, 512, fmt)) == [s.replace("M=256", "M=1024").replace("131072", "524288")
+                                                       for s in apart]
+
+
+def test_decoder_layer_pairs_gate_and_up_at_many_rows():
+    steps = plan(P.decoder_layer(4, 256, 256, 2, 128, 512))
+    assert "int4_g64 swiglu pair matmul M=1024 K=256 N=512 -> bf16" in steps
+    assert not any(s.startswith("elementwise") for s in steps) and len(steps) == 8
+
+
 def test_decoder_layer_plans_onto_the_kernels():
     """The Llama layer's StableHLO: projections on the dequant-matmul, norms
     and softmax on their row kernels, the two attention products on the bf16
