@@ -873,17 +873,23 @@ class Planner {
     return true;
   }
 
-  // Any dot_general with one contracting dimension, batch dimensions that
-  // come first on both sides, and operands that are arguments, computed
-  // values or transposes of them (read through strides, not copied).
-  // Batch dimensions, and the free dimensions of each side, are collapsed
-  // into one index when their strides allow it (always, for row-major
-  // operands without a transpose).
+  // Any dot_general: batch, contracting and free dimensions anywhere on
+  // either side (the result is [batch..., lhs free..., rhs free...] in
+  // StableHLO's order), several contracting dimensions or none (K = 1), and
+  // operands that are arguments, computed values or transposes of them. Each
+  // group of dimensions collapses into one index with one stride when the
+  // strides allow it (always, for row-major operands whose groups are
+  // adjacent and in order); an operand whose groups do not collapse is
+  // copied to [batch, M, K] / [batch, K, N] first (copy_a / copy_b).
   struct GeneralDot {
     int a = -1, b = -1;  // source values (a folded transpose's input)
     int64_t batch = 1, M = 1, N = 1, K = 0;
     int64_t sa[3] = {0, 0, 0}, sb[3] = {0, 0, 0};
     bool transposed = false;
+    bool copy_a = false, copy_b = false;
+    // copy_*: the operand's dims in [batch, free, contract] (a) or
+    // [batch, contract, free] (b) order and their strides in the source.
+    std::vector<int64_t> a_shape, a_st, b_shape, b_st;
   };
 
   bool general_dot(const Op& op, GeneralDot* g) const {
@@ -895,7 +901,18 @@ class Planner {
       lc = {ra - 1};
       rc = {0};
     }
-    if (lc.size() != 1 || rc.size() != 1 || lb.size() != rbt.size()) return false;
+    if (lc.size() != rc.size() || lb.size() != rbt.size()) return false;
+    // Every dim named at most once per side, and in range.
+    auto distinct = [](const std::vector<int64_t>& x, const std::vector<int64_t>& y, int r) {
+      std::vector<bool> seen(r, false);
+      for (const auto* v : {&x, &y})
+        for (int64_t i : *v) {
+          if (i < 0 || i >= r || seen[i]) return false;
+          seen[i] = true;
+        }
+      return true;
+    };
+    if (!distinct(lb, lc, ra) || !distinct(rbt, rc, rb)) return false;
     // Operand dims -> (source value, stride of each operand dim in the source).
     auto layout = [&](int x, int* src, std::vector<int64_t>* st, bool* tr) {
       const Op* d = def(x);
@@ -943,31 +960,76 @@ class Planner {
         if (st[keep[j]] != st[keep[j + 1]] * dims[keep[j + 1]]) return false;
       return true;
     };
-    const int nb = (int)lb.size();
-    for (int i = 0; i < nb; ++i)
+    std::vector<int> a_batch, b_batch, a_con, b_con, a_free, b_free;
+    for (size_t i = 0; i < lb.size(); ++i) {
       if (ad[lb[i]] != bd[rbt[i]]) return false;
-    std::vector<int> a_batch, b_batch, a_free, b_free;
-    for (int i = 0; i < nb; ++i) {
       a_batch.push_back((int)lb[i]);
       b_batch.push_back((int)rbt[i]);
     }
-    // The result is [batch..., lhs free..., rhs free...]: batch dims must be
-    // the first nb dims of both operands for that order to be row-major here.
-    for (int i = 0; i < nb; ++i)
-      if (lb[i] != i || rbt[i] != i) return false;
+    for (size_t i = 0; i < lc.size(); ++i) {
+      if (ad[lc[i]] != bd[rc[i]]) return false;
+      a_con.push_back((int)lc[i]);
+      b_con.push_back((int)rc[i]);
+    }
+    auto named = [](const std::vector<int64_t>& x, int i) { return std::find(x.begin(), x.end(), i) != x.end(); };
     for (int i = 0; i < ra; ++i)
-      if (i >= nb && i != lc[0]) a_free.push_back(i);
+      if (!named(lb, i) && !named(lc, i)) a_free.push_back(i);
     for (int i = 0; i < rb; ++i)
-      if (i >= nb && i != rc[0]) b_free.push_back(i);
-    g->K = ad[lc[0]];
-    if (bd[rc[0]] != g->K) return false;
-    int64_t bsz_a, bsz_b;
-    if (!collapse(ad, as, a_batch, &bsz_a, &g->sa[0]) || !collapse(bd, bs, b_batch, &bsz_b, &g->sb[0])) return false;
-    if (!collapse(ad, as, a_free, &g->M, &g->sa[1]) || !collapse(bd, bs, b_free, &g->N, &g->sb[2])) return false;
-    g->batch = bsz_a;
-    g->sa[2] = as[lc[0]];
-    g->sb[1] = bs[rc[0]];
+      if (!named(rbt, i) && !named(rc, i)) b_free.push_back(i);
+    int64_t bsz, kb, n_, m_;
+    // lhs: batch, free (M), contract (K)
+    bool ok_a = collapse(ad, as, a_batch, &g->batch, &g->sa[0]) && collapse(ad, as, a_free, &g->M, &g->sa[1]) &&
+                collapse(ad, as, a_con, &g->K, &g->sa[2]);
+    bool ok_b = collapse(bd, bs, b_batch, &bsz, &g->sb[0]) && collapse(bd, bs, b_con, &kb, &g->sb[1]) &&
+                collapse(bd, bs, b_free, &g->N, &g->sb[2]);
+    if (!ok_a) {
+      // sizes of the groups, then the canonical copy's row-major strides
+      collapse(ad, std::vector<int64_t>(ra, 0), a_batch, &g->batch, &bsz);
+      collapse(ad, std::vector<int64_t>(ra, 0), a_free, &g->M, &m_);
+      collapse(ad, std::vector<int64_t>(ra, 0), a_con, &g->K, &kb);
+      g->copy_a = true;
+      for (const auto* grp : {&a_batch, &a_free, &a_con})
+        for (int i : *grp) {
+          g->a_shape.push_back(ad[i]);
+          g->a_st.push_back(as[i]);
+        }
+      g->sa[0] = g->M * g->K;
+      g->sa[1] = g->K;
+      g->sa[2] = 1;
+    }
+    if (!ok_b) {
+      collapse(bd, std::vector<int64_t>(rb, 0), b_free, &g->N, &n_);
+      g->copy_b = true;
+      for (const auto* grp : {&b_batch, &b_con, &b_free})
+        for (int i : *grp) {
+          g->b_shape.push_back(bd[i]);
+          g->b_st.push_back(bs[i]);
+        }
+      g->sb[0] = g->K * g->N;
+      g->sb[1] = g->N;
+      g->sb[2] = 1;
+    }
+    if ((g->copy_a && g->a_shape.size() > 8) || (g->copy_b && g->b_shape.size() > 8)) return false;
+    if (g->copy_a || g->copy_b) g->transposed = true;
     return true;
+  }
+
+  // The slot holding dot operand `which` (0: lhs, 1: rhs) in the layout
+  // general_dot's strides describe: the source value itself, or its copy in
+  // canonical order when the operand's dimension groups do not collapse.
+  int dot_operand(const GeneralDot& gd, int which, int eb) {
+    const bool copy = which == 0 ? gd.copy_a : gd.copy_b;
+    const int src = which == 0 ? gd.a : gd.b;
+    const int slot = need(src);
+    if (!copy) return slot;
+    const std::vector<int64_t>& shape = which == 0 ? gd.a_shape : gd.b_shape;
+    const std::vector<int64_t>& st = which == 0 ? gd.a_st : gd.b_st;
+    int64_t n = 1;
+    for (int64_t d : shape) n *= d;
+    const int o = new_slot(Slot{SLOT_TEMP, n * eb, -1, {}});
+    layout_step(slot, o, eb, shape, st, 0, row_strides(shape), 0,
+                std::string("dot operand ") + (which == 0 ? "a" : "b") + " to " + dims_str(shape));
+    return o;
   }
 
   bool try_gemm(int v, const Op& op, int* out) {
@@ -995,8 +1057,8 @@ class Planner {
       // as einsum 'bhtd,bhsd->bhts') are copied to [batch, M, K] and
       // [batch, K, N] first, then multiplied by the tiled GEMM.
       const int eb = dtype_bytes(ta);
-      auto canon = [&](int src, const int64_t* st, int64_t R, int64_t C, const char* what) {
-        const int slot = need(src);
+      auto canon = [&](int which, const int64_t* st, int64_t R, int64_t C, const char* what) {
+        const int slot = dot_operand(gd, which, eb);
         if (st[2] == 1 && st[1] == C && (gd.batch == 1 || st[0] == R * C)) return slot;
         const std::vector<int64_t> shape = {gd.batch, R, C};
         const int o = new_slot(Slot{SLOT_TEMP, gd.batch * R * C * eb, -1, {}});
@@ -1005,7 +1067,7 @@ class Planner {
         return o;
       };
       Step st;
-      st.in = {canon(gd.a, gd.sa, gd.M, gd.K, "a"), canon(gd.b, gd.sb, gd.K, gd.N, "b")};
+      st.in = {canon(0, gd.sa, gd.M, gd.K, "a"), canon(1, gd.sb, gd.K, gd.N, "b")};
       if (ta == DT_F32) {
         st.kind = ST_GEMM_F32;
         st.dt = MK_DT_F32;
@@ -1029,7 +1091,7 @@ class Planner {
     }
     if (!fast) {
       if (!general) {
-        reject(&op, "dimension numbers other than one contracting dimension with leading batch dimensions");
+        reject(&op, "dimension numbers whose operand layouts cannot be mapped (rank above 8 or mismatched sizes)");
         return false;
       }
       const bool ints = is_int_type(ta) && is_int_type(tr);
@@ -1042,7 +1104,7 @@ class Planner {
       st.kind = ST_DOT_GENERIC;
       st.type_a = ta;
       st.type_out = tr;
-      st.in = {need(gd.a), need(gd.b)};
+      st.in = {dot_operand(gd, 0, dtype_bytes(ta)), dot_operand(gd, 1, dtype_bytes(ta))};
       st.batch = gd.batch;
       st.M = gd.M;
       st.N = gd.N;

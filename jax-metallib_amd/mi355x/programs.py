@@ -97,6 +97,24 @@ def dot_general(shape_a, shape_b, dt, out_dt=None, batch=0, contract=(None, None
     return _module("jit_dot", args, [tc], body)
 
 
+def dot_general_dims(shape_a, shape_b, dt, lc, rc, lb=(), rb=(), out_dt=None):
+    """lax.dot_general(a, b, ((lc, rc), (lb, rb))) with any dimension numbers
+    (several contracting dims, none, batch dims anywhere), as jax.jit
+    lowers it: the result is [batch (in lb order), lhs free, rhs free]."""
+    t, to = _MLIR_DT[dt], _MLIR_DT[out_dt or dt]
+    ta, tb = _t(shape_a, t), _t(shape_b, t)
+    a_free = [shape_a[i] for i in range(len(shape_a)) if i not in lc and i not in lb]
+    b_free = [shape_b[i] for i in range(len(shape_b)) if i not in rc and i not in rb]
+    tc = _t([shape_a[i] for i in lb] + a_free + b_free, to)
+    dims = []
+    if lb:
+        dims.append(f"batching_dims = [{', '.join(map(str, lb))}] x [{', '.join(map(str, rb))}]")
+    dims.append(f"contracting_dims = [{', '.join(map(str, lc))}] x [{', '.join(map(str, rc))}]")
+    body = [f"%0 = stablehlo.dot_general %arg0, %arg1, {', '.join(dims)}, precision = [DEFAULT, DEFAULT] : "
+            f"({ta}, {tb}) -> {tc}", f"return %0 : {tc}"]
+    return _module("jit_dot_general", [ta, tb], [tc], body)
+
+
 def softmax(R, C, dt="f32"):
     """jax.nn.softmax(x, axis=-1) on x [R, C]."""
     tx, tr, tr1 = _t([R, C], dt), _t([R], dt), _t([R, 1], dt)

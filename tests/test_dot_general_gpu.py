@@ -149,3 +149,62 @@ def test_dot_general_c_abi_rejects_bad_arguments():
                             st) == _lib.MK_EINVAL
     assert L.mk_dot_general(4, 4, 11, a.data_ptr(), a.data_ptr(), a.data_ptr(), 1, 2, 2, 2, s, s,
                             st) == _lib.MK_EUNSUPPORTED
+
+
+# lax.dot_general dimension numbers beyond one contracting dimension with
+# leading batch dims (binary_ops.mm:644-1100 handles any): several
+# contracting dims (collapsing by strides, or not), none, batch dims in other
+# positions, and a shape large enough for the tiled GEMM.
+DIMS = [
+    ((4, 6, 8), (6, 8, 5), (1, 2), (0, 1), (), ()),
+    ((4, 6, 8), (8, 6, 5), (1, 2), (1, 0), (), ()),
+    ((6, 4, 8), (8, 5, 6), (0, 2), (2, 0), (), ()),
+    ((3, 4), (5, 6), (), (), (), ()),
+    ((2, 3, 4), (4, 3, 2), (1,), (1,), (0,), (2,)),
+    ((5, 7, 3, 2), (2, 5, 3, 9), (2,), (2,), (3, 0), (0, 1)),
+    ((64, 32, 16), (16, 32, 128), (1, 2), (1, 0), (), ()),
+]
+
+
+def _einsum_spec(ra, rb, lc, rc, lb, rb_):
+    letters = iter("abcdefghijklmnopqrstuvwxyz")
+    sa, sb = [None] * ra, [None] * rb
+    for i, j in zip(lb, rb_):
+        sa[i] = sb[j] = next(letters)
+    for i, j in zip(lc, rc):
+        sa[i] = sb[j] = next(letters)
+    for i in range(ra):
+        sa[i] = sa[i] or next(letters)
+    for j in range(rb):
+        sb[j] = sb[j] or next(letters)
+    out = [sa[i] for i in lb] + [sa[i] for i in range(ra) if i not in lc and i not in lb] + \
+          [sb[j] for j in range(rb) if j not in rc and j not in rb_]
+    return f"{''.join(sa)},{''.join(sb)}->{''.join(out)}"
+
+
+@pytest.mark.parametrize("sa,sb,lc,rc,lb,rb", DIMS, ids=[f"case{i}" for i in range(len(DIMS))])
+@pytest.mark.parametrize("dt", ["int32", "float32", "bfloat16"])
+def test_dimension_numbers_match_einsum(client, sa, sb, lc, rc, lb, rb, dt):
+    rng = np.random.default_rng(len(sa) * 7 + len(lc))
+    spec = _einsum_spec(len(sa), len(sb), lc, rc, lb, rb)
+    print(f"[dot] {dt} {sa} x {sb} {spec}", flush=True)
+    text = P.dot_general_dims(sa, sb, dt, lc, rc, lb, rb)
+    if dt == "int32":
+        a, b = _arr(rng, sa, "int32"), _arr(rng, sb, "int32")
+        y = run(client, text, a, b)
+        want = np.einsum(spec, a.astype(np.int64), b.astype(np.int64)).astype(np.int32)
+        assert y.dtype == np.int32 and np.array_equal(y, want)
+        return
+    af = rng.standard_normal(sa).astype(np.float32)
+    bf = rng.standard_normal(sb).astype(np.float32)
+    if dt == "bfloat16":
+        ab, bb = f32_to_bf16_bits(af), f32_to_bf16_bits(bf)
+        y = bf16_bits_to_f32(run(client, text, (ab, rt.BF16), (bb, rt.BF16)))
+        af, bf = bf16_bits_to_f32(ab), bf16_bits_to_f32(bb)
+        tol = 2e-2
+    else:
+        y = run(client, text, af, bf)
+        tol = 1e-5
+    want = np.einsum(spec, af.astype(np.float64), bf.astype(np.float64))
+    assert y.shape == want.shape
+    assert_rel_close(y.astype(np.float64), want, tol, f"{dt} {spec}")

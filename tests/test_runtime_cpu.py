@@ -213,10 +213,31 @@ def test_non_canonical_dot_takes_the_general_kernel():
     assert plan.strip() == "dot_general bf16 batch=1 M=16 N=32 K=64 -> bf16" and n == 1
 
 
-def test_two_contracting_dims_are_rejected_at_compile():
+def test_several_contracting_dims_plan():
+    """Contracting dims that collapse by strides need no copy; others are
+    copied to [batch, K, N] / [batch, M, K] first; none at all is K = 1."""
     text = _wrap(["tensor<4x8x8xf32>", "tensor<8x8x3xf32>"], ["tensor<4x3xf32>"], [
         "%0 = stablehlo.dot_general %arg0, %arg1, contracting_dims = [1, 2] x [0, 1] : "
         "(tensor<4x8x8xf32>, tensor<8x8x3xf32>) -> tensor<4x3xf32>",
+        "return %0 : tensor<4x3xf32>",
+    ])
+    assert plan(text) == ["dot_general f32 batch=1 M=4 N=3 K=64 -> f32"]
+    assert plan(P.dot_general_dims((4, 6, 8), (8, 6, 5), "float32", (1, 2), (1, 0))) == [
+        "dot operand b to [6,8,5]", "dot_general f32 batch=1 M=4 N=5 K=48 (strided) -> f32"]
+    assert plan(P.dot_general_dims((3, 4), (5, 6), "float32", (), ())) == [
+        "dot_general f32 batch=1 M=12 N=30 K=1 -> f32"]
+    # batch dims not leading: (a3, a0) x (b0, b1), result [2, 5, 7, 9]
+    assert plan(P.dot_general_dims((5, 7, 3, 2), (2, 5, 3, 9), "float32", (2,), (2,), (3, 0), (0, 1))) == [
+        "dot operand a to [2,5,7,3]", "dot_general f32 batch=10 M=7 N=9 K=3 (strided) -> f32"]
+    # large enough for the tiled GEMM: K = 32 x 16 collapses in place
+    assert plan(P.dot_general_dims((64, 32, 16), (32, 16, 128), "bfloat16", (1, 2), (0, 1))) == [
+        "gemm_bf16 batch=1 M=64 N=128 K=512 -> bf16"]
+
+
+def test_dot_with_mismatched_dimension_sizes_is_rejected():
+    text = _wrap(["tensor<4x8x8xf32>", "tensor<8x6x3xf32>"], ["tensor<4x3xf32>"], [
+        "%0 = stablehlo.dot_general %arg0, %arg1, contracting_dims = [1, 2] x [0, 1] : "
+        "(tensor<4x8x8xf32>, tensor<8x6x3xf32>) -> tensor<4x3xf32>",
         "return %0 : tensor<4x3xf32>",
     ])
     assert "stablehlo.dot_general" in _unsupported(text)
@@ -305,7 +326,7 @@ def test_decoder_layer_plans_onto_the_kernels():
     kinds = [s.split()[0] for s in steps]
     assert kinds.count("int4_g64_matmul") == 5 and kinds.count("rmsnorm") == 2
     assert kinds.count("softmax") == 1 and kinds.count("gemm_bf16") == 2
-    assert set(kinds) <= {"int4_g64_matmul", "rmsnorm", "softmax", "gemm_bf16", "gemm", "elementwise", "slice",
+    assert set(kinds) <= {"int4_g64_matmul", "rmsnorm", "softmax", "gemm_bf16", "gemm", "dot", "elementwise", "slice",
                           "broadcast", "concatenate", "transpose"}, set(kinds)
     assert "softmax rows=256 cols=64 bf16" in steps
     # the causal mask is folded at compile time into the select's program
