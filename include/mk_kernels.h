@@ -264,7 +264,8 @@ int mk_reduce_lastdim(int dtype, int op, const void* x, void* y, int64_t rows, i
  * mk_attention_causal_bf16: the three steps above in one pass (scores,
  *   causal softmax in f32 with the online max/sum rescaling, P rounded to
  *   bf16 for P @ V, f32 accumulation) from q, k, v [B*H, S, D] (k_rows = 1)
- *   straight to out [B*S, H*D].  Needs S % 128 == 0.
+ *   straight to out [B*S, H*D].  Needs S % 128 == 0 and a positive finite
+ *   scale (MK_EINVAL otherwise).
  * ---------------------------------------------------------------------- */
 int mk_rope_qkv_split_bf16(const void* qkv, const float* cos_table, const float* sin_table, void* q,
                            void* k, void* v, int64_t B, int64_t S, int64_t H, int64_t D, int k_rows,

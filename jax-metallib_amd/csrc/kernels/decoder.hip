@@ -350,34 +350,45 @@ __global__ __launch_bounds__(512) void attention_causal_kernel(AttnArgs a) {
           sacc[tt] = mfma16x16x32(kf, qf[s], sacc[tt]);
         }
       const int i = i0 + l16;
-      const bool diag = kv0 + kFaKV - 1 > i0;
+      // Only a tile that crosses the diagonal of this wave's rows is masked
+      // (a wave-uniform branch).
+      if (kv0 + kFaKV - 1 > i0) {
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (kv0 + 16 * tt + 4 * g + e > i) sacc[tt][e] = -INFINITY;
+      }
+      // The scale (log2 units) is positive, so the row max of the scaled
+      // scores is the scaled max of the raw ones (rounding is monotonic),
+      // and each probability takes one fma before its exp2.
       float mt = -INFINITY;
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float x = sacc[tt][e] * a.scale_log2;
-          if (diag && kv0 + 16 * tt + 4 * g + e > i) x = -INFINITY;
-          sacc[tt][e] = x;
-          mt = fmaxf(mt, x);
-        }
+        for (int e = 0; e < 4; ++e) mt = fmaxf(mt, sacc[tt][e]);
       mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
       mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-      const float mn = fmaxf(m, mt);
+      const float mn = fmaxf(m, mt * a.scale_log2);
       const float alpha = fa_exp2(m - mn);
+      // alpha is exactly 1 for a row whose max held; when that is every row
+      // of the wave the rescale is skipped.
+      const bool rescale = !__all(mn == m);
       m = mn;
       float ps = 0.f;
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float p = fa_exp2(sacc[tt][e] - mn);
+          const float p = fa_exp2(__builtin_fmaf(sacc[tt][e], a.scale_log2, -mn));
           sacc[tt][e] = p;
           ps += p;
         }
       lsum = lsum * alpha + ps;
+      if (rescale) {
 #pragma unroll
-      for (int n = 0; n < 8; ++n) o[n] *= alpha;
+        for (int n = 0; n < 8; ++n) o[n] *= alpha;
+      }
       u32x4 pf[2];
 #pragma unroll
       for (int u = 0; u < 2; ++u)
@@ -443,6 +454,7 @@ __global__ __launch_bounds__(256) void merge_heads_kernel(MergeArgs a) {
 #include "../capi_internal.h"
 
 #include <algorithm>
+#include <cmath>
 
 extern "C" int mk_rope_qkv_split_bf16(const void* qkv, const float* cos_table, const float* sin_table, void* q,
                                       void* k, void* v, int64_t B, int64_t S, int64_t H, int64_t D, int k_rows,
@@ -544,6 +556,8 @@ extern "C" int mk_attention_causal_bf16(const void* q, const void* k, const void
   a.B = (int)B;
   a.H = (int)H;
   a.S = (int)S;
+  if (!(scale > 0.f) || !std::isfinite(scale))
+    return mkc::fail(MK_EINVAL, "%s: scale must be positive and finite (got %g)", fn, (double)scale);
   a.scale_log2 = scale * 1.4426950408889634f;
   hipError_t e = hipFuncSetAttribute((const void*)mk::attention_causal_kernel,
                                      hipFuncAttributeMaxDynamicSharedMemorySize, mk::kFaLds);

@@ -24,6 +24,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <functional>
 #include <map>
 #include <set>
@@ -634,7 +635,9 @@ class Planner {
     } else {
       return false;
     }
-    if (D != 128 || S % 128 != 0) return false;
+    // The kernel takes a positive finite scale (its max is taken before
+    // scaling); anything else runs op by op.
+    if (D != 128 || S % 128 != 0 || !(scale > 0.0) || !std::isfinite(scale)) return false;
     m->q = q;
     m->k = k;
     m->v = v;

@@ -155,6 +155,10 @@ def test_decoder_kernels_reject_bad_shapes():
     z = torch.zeros((1, 192, 128), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(MKError):
         ops.attention_causal(z, z, z, 1, 1, 1.0)  # S % 128 != 0
+    z = torch.zeros((1, 128, 128), dtype=torch.bfloat16, device="cuda")
+    for bad in (0.0, -0.125, float("inf"), float("nan")):  # the kernel scales after its row max
+        with pytest.raises(MKError):
+            ops.attention_causal(z, z, z, 1, 1, bad)
 
 
 # ---------------------------------------------------------------------------

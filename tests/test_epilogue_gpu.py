@@ -54,10 +54,12 @@ def test_gemm_epilogue_matches_unfused(epilogue, batch, M, N, K):
 
 
 # M = 1 / 16: streaming and wide kernels; 130 / 256: many-row kernel; 800:
-# dequantise-then-GEMM; (16, 1024, 1024): split-K with the reduce pass.
+# dequantise-then-GEMM; (16, 1024, 1024): split-K with the reduce pass;
+# (16, 4096, 14336): the headline shape, on both wide kernels (int4, int8)
+# with their in-kernel split-K exchange.
 @pytest.mark.parametrize("epilogue", ["add", "swiglu"])
 @pytest.mark.parametrize("M,K,N", [(1, 512, 256), (16, 4096, 1024), (16, 1024, 14336), (130, 256, 192),
-                                   (256, 512, 512), (800, 256, 256), (5, 512, 136)])
+                                   (256, 512, 512), (800, 256, 256), (5, 512, 136), (16, 4096, 14336)])
 def test_quantized_epilogue_matches_unfused(epilogue, M, K, N):
     ops = _ops()
     rng = np.random.default_rng(M * 3 + K + N)

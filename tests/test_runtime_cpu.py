@@ -362,6 +362,15 @@ def test_decoder_layer_routes_rope_and_attention_to_the_decoder_kernels(monkeypa
     assert kinds.count("softmax") == 1 and kinds.count("gemm_bf16") == 2
 
 
+def test_attention_route_needs_a_positive_scale():
+    text = P.causal_attention(1, 2, 128, 128)
+    const = f"{128 ** -0.5:.6e}"
+    assert const in text
+    neg = text.replace(const, f"{-(128 ** -0.5):.6e}")
+    steps = plan(neg)
+    assert not any(s.startswith("attention_causal") for s in steps) and any(s.startswith("softmax") for s in steps)
+
+
 def test_attention_route_needs_the_causal_mask():
     want = ["attention_causal B=1 H=2 S=128 D=128 scale=0.0883789 bf16"]
     assert plan(P.causal_attention(1, 2, 128, 128)) == want
