@@ -579,7 +579,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list of secondary workloads (int8,qmm_m,gemm,decoder,softmax,rmsnorm,argmax,chain6,e2e), "
+                    help="comma list of secondary workloads (int8,qmm_m,shard,gemm,decoder,softmax,rmsnorm,argmax,chain6,e2e), "
                          "or 'none'")
     ap.add_argument("--profile", default="",
                     help="int4 | int8 | gemm | qgemm: eager launches of one kernel plus a 256 MiB copy calibration, "
@@ -636,6 +636,17 @@ def main():
                                           "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
                                           "traffic": None}}
                 secondary[f"{fmt}_dequant_matmul_M{M}"] = entry
+
+    if want("shard"):
+        # One GPU's share when the quantized matmul shards by N over 8 GPUs
+        # (N = 14336 / 8 = 1792 per GPU, no exchange): the per-shard kernel
+        # at its real shape.
+        for fmt, fn in (("int4", bench_int4), ("int8", bench_int8)):
+            r = fn(torch, ops, args.steps, 5, M=16, K=4096, N=1792)
+            log(f"[bench] {fmt} per-shard M=16 N=1792: {r['sec_per_call'] * 1e6:.2f} us, {r['gbs']:.0f} GB/s")
+            secondary[f"{fmt}_dequant_matmul_M16_shard_N1792"] = _hbm_entry(
+                r["gbs"], r["sec_per_call"] * 1e6,
+                {"what": "one of 8 GPUs' share of the headline shape when sharded by N (K=4096, N=1792)"})
 
     if want("gemm"):
         log("[bench] bf16 GEMM 4096^3 ...")

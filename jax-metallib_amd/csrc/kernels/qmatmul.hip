@@ -150,13 +150,62 @@ __device__ __forceinline__ void spill_y(unsigned char* wsm, const f32x4 (&y)[4],
         f32x4{y[0][i], y[1][i], y[2][i], y[3][i]};
 }
 
+// Four device-coherent 16-byte loads (sc1: they miss the local L2) in flight
+// together.
+__device__ __forceinline__ void ld4_sc1(const float* p0, const float* p1, const float* p2, const float* p3,
+                                        f32x4& v0, f32x4& v1, f32x4& v2, f32x4& v3) {
+  asm volatile(
+      "global_load_dwordx4 %0, %4, off sc1\n\t"
+      "global_load_dwordx4 %1, %5, off sc1\n\t"
+      "global_load_dwordx4 %2, %6, off sc1\n\t"
+      "global_load_dwordx4 %3, %7, off sc1\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3)
+      : "v"(p0), "v"(p1), "v"(p2), "v"(p3)
+      : "memory");
+}
+
+// Two device-coherent 16-byte stores (sc1: written through past the per-XCD
+// L2) and the wait for their acknowledgement, in one block: no instruction
+// may overwrite a store's data registers before the store has read them (a
+// hazard the compiler does not see inside inline asm).
+__device__ __forceinline__ void st2_sc1_wait(float* p0, const f32x4& v0, float* p1, const f32x4& v1) {
+  asm volatile(
+      "global_store_dwordx4 %0, %2, off sc1\n\t"
+      "global_store_dwordx4 %1, %3, off sc1\n\t"
+      "s_waitcnt vmcnt(0)" ::"v"(p0),
+      "v"(p1), "v"(v0), "v"(v1)
+      : "memory");
+}
+
+// One device-coherent 16-byte load.
+__device__ __forceinline__ f32x4 ld1_sc1(const float* p) {
+  f32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off sc1\n\ts_waitcnt vmcnt(0)" : "=&v"(v) : "v"(p) : "memory");
+  return v;
+}
+
+// One device-coherent 16-byte store and the wait for its acknowledgement
+// (one asm block, as for st2_sc1_wait below).
+__device__ __forceinline__ void st1_sc1_wait(float* p, const f32x4& v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_waitcnt vmcnt(0)" ::"v"(p), "v"(v) : "memory");
+}
+
 // Sum the NW wave tiles of the workgroup and emit bf16 y (ks == 1, with the
 // int8 per-channel scale when FMT8) or the f32 split-K partial (ks > 1).
+// With a.cnt set the split-K partials are combined here, as in the wide
+// kernels: device-coherent (sc1) stores of the partial, acknowledged, a
+// device-scope arrival count per tile, and the last arriver sums the ks
+// partials in k order from 0 (the separate reduce pass's order, so the two
+// give the same bits) and stores y.  Without a.cnt a second kernel
+// (qmm_splitk_reduce_kernel) does that.
 template <int NW, bool FMT8>
-__device__ __forceinline__ void reduce_and_store(const QArgs& a, const unsigned char* smem, int ksi,
+__device__ __forceinline__ void reduce_and_store(const QArgs& a, unsigned char* smem, int ksi,
                                                  int rb, int m0, int mrows, int n0) {
+  constexpr int kItems = kQRows * (kQCols / 4);
   __syncthreads();
-  for (int item = threadIdx.x; item < kQRows * (kQCols / 4); item += NW * kWave) {
+  const bool exchange = a.ks > 1 && a.cnt != nullptr;
+  for (int item = threadIdx.x; item < kItems; item += NW * kWave) {
     const int m = item / (kQCols / 4), ch = item % (kQCols / 4);
     const int n = n0 + 4 * ch;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -164,12 +213,52 @@ __device__ __forceinline__ void reduce_and_store(const QArgs& a, const unsigned 
     for (int w = 0; w < NW; ++w)
       acc += *reinterpret_cast<const f32x4*>(smem + w * a.wave_lds + (m * kQCols + 4 * ch) * 4);
     if (m >= mrows || n >= a.N) continue;
-    if (a.ks > 1) {
-      *reinterpret_cast<f32x4*>(a.part + ((size_t)(rb * a.ks + ksi) * kQRows + m) * a.N + n) = acc;
+    float* dst = a.part + ((size_t)(rb * a.ks + ksi) * kQRows + m) * a.N + n;
+    if (exchange) {
+      st1_sc1_wait(dst, acc);
+    } else if (a.ks > 1) {
+      *reinterpret_cast<f32x4*>(dst) = acc;
     } else {
       if (FMT8) acc *= *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(a.s) + n);
       epi_store_bf16x4(a.y, a.aux, a.epi, (size_t)(m0 + m) * a.N + n, acc);
     }
+  }
+  if (!exchange) return;
+  // Every thread's partial stores are acknowledged, and every wave is done
+  // reading the spills, before thread 0 counts this workgroup in.
+  __syncthreads();
+  volatile uint32_t* flag = reinterpret_cast<volatile uint32_t*>(smem);
+  if (threadIdx.x == 0) {
+    const int ntiles = (a.N + kQCols - 1) / kQCols;
+    uint32_t* ctr = a.cnt + rb * ntiles + n0 / kQCols;
+    asm volatile("" : "+v"(ctr));  // per-lane address: a vector atomic
+    const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t last = old == (uint32_t)(a.ks - 1);
+    if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag = last;
+  }
+  __syncthreads();
+  if (!*flag) return;
+  for (int item = threadIdx.x; item < kItems; item += NW * kWave) {
+    const int m = item / (kQCols / 4), ch = item % (kQCols / 4);
+    const int n = n0 + 4 * ch;
+    if (m >= mrows || n >= a.N) continue;
+    const float* src = a.part + ((size_t)rb * a.ks * kQRows + m) * a.N + n;
+    const size_t kstride = (size_t)kQRows * a.N;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    int k = 0;
+    for (; k + 4 <= a.ks; k += 4) {
+      f32x4 v0, v1, v2, v3;
+      ld4_sc1(src + k * kstride, src + (k + 1) * kstride, src + (k + 2) * kstride, src + (k + 3) * kstride, v0, v1,
+              v2, v3);
+      acc += v0;
+      acc += v1;
+      acc += v2;
+      acc += v3;
+    }
+    for (; k < a.ks; ++k) acc += ld1_sc1(src + k * kstride);
+    if (FMT8) acc *= *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(a.s) + n);
+    epi_store_bf16x4(a.y, a.aux, a.epi, (size_t)(m0 + m) * a.N + n, acc);
   }
 }
 
@@ -572,34 +661,6 @@ __device__ __forceinline__ void lds_scale_zero(uint32_t sa, uint32_t za, u32x2 (
       "s_waitcnt lgkmcnt(0)"
       : "=&v"(sv[0]), "=&v"(sv[1]), "=&v"(sv[2]), "=&v"(sv[3]), "=&v"(zv[0]), "=&v"(zv[1])
       : "v"(sa), "v"(za)
-      : "memory");
-}
-
-// Four device-coherent 16-byte loads (sc1: they miss the local L2) in flight
-// together.
-__device__ __forceinline__ void ld4_sc1(const float* p0, const float* p1, const float* p2, const float* p3,
-                                        f32x4& v0, f32x4& v1, f32x4& v2, f32x4& v3) {
-  asm volatile(
-      "global_load_dwordx4 %0, %4, off sc1\n\t"
-      "global_load_dwordx4 %1, %5, off sc1\n\t"
-      "global_load_dwordx4 %2, %6, off sc1\n\t"
-      "global_load_dwordx4 %3, %7, off sc1\n\t"
-      "s_waitcnt vmcnt(0)"
-      : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3)
-      : "v"(p0), "v"(p1), "v"(p2), "v"(p3)
-      : "memory");
-}
-
-// Two device-coherent 16-byte stores (sc1: written through past the per-XCD
-// L2) and the wait for their acknowledgement, in one block: no instruction
-// may overwrite a store's data registers before the store has read them (a
-// hazard the compiler does not see inside inline asm).
-__device__ __forceinline__ void st2_sc1_wait(float* p0, const f32x4& v0, float* p1, const f32x4& v1) {
-  asm volatile(
-      "global_store_dwordx4 %0, %2, off sc1\n\t"
-      "global_store_dwordx4 %1, %3, off sc1\n\t"
-      "s_waitcnt vmcnt(0)" ::"v"(p0),
-      "v"(p1), "v"(v0), "v"(v1)
       : "memory");
 }
 
@@ -1141,20 +1202,20 @@ bool fill_plan(int fmt, int64_t K, int ks, int nw, QPlan* p) {
 // workgroup whenever x fits in LDS and the grid already covers ~192+ CUs;
 // otherwise the smallest split that does.  Every wave gets a whole number of
 // 64-k groups.  MK_QMM_KS / MK_QMM_NW force a choice (tuning sweeps).
-// Streaming kernels: 8 waves, K = ks * 8 * 32 * S with S in {16, 8, 4}
+// Streaming kernels: 8 waves, K = ks * 8 * 32 * S with S in {16, 8, 4, 2}
 // (int4 needs S even), N % 16 == 0.  Prefer the fewest splits that still
 // give >= 192 workgroups.
 bool plan_stream(int fmt, int64_t K, int64_t N, QPlan* p) {
   if (N % 16 != 0 || N < 16 || getenv("MK_QMM_GENERIC")) return false;
   const int ks_env = env_int("MK_QMM_KS", 0);
-  const int steps[3] = {16, 8, 4};
+  const int steps[4] = {16, 8, 4, 2};
   for (int ks = 1; ks <= 64; ks *= 2) {
     if (ks_env > 0 && ks != ks_env) continue;
-    for (int i = 0; i < 3; ++i) {
+    for (int i = 0; i < 4; ++i) {
       const int S = steps[i];
       if (K != (int64_t)ks * 8 * 32 * S) continue;
       if ((int64_t)p->ntiles * p->rowblocks * ks < 192 && ks_env <= 0 && 2 * ks <= 64 &&
-          K % ((int64_t)2 * ks * 8 * 32 * 4) == 0)
+          K % ((int64_t)2 * ks * 8 * 32 * 2) == 0)
         break;  // a larger split would still divide K: try it for more workgroups
       p->ks = ks;
       p->nw = 8;
@@ -1364,7 +1425,7 @@ hipError_t launch_stream(int fmt, const mk::QArgs& a, const QPlan& p, hipStream_
   else
     hipLaunchKernelGGL((mk::int8pc_stream_kernel<S, (S < 4 ? S : 4)>), grid, block, p.lds_bytes, st, a);
   e = hipGetLastError();
-  if (e != hipSuccess || p.ks == 1) return e;
+  if (e != hipSuccess || p.ks == 1 || a.cnt) return e;
   return launch_reduce(fmt, a, st);
 }
 
@@ -1381,7 +1442,7 @@ hipError_t launch_q(int fmt, const mk::QArgs& a, const QPlan& p, hipStream_t st)
     hipLaunchKernelGGL(mk::int8pc_gemv_kernel<NW>, grid, block, p.lds_bytes, st, a);
   }
   e = hipGetLastError();
-  if (e != hipSuccess || p.ks == 1) return e;
+  if (e != hipSuccess || p.ks == 1 || a.cnt) return e;
   return launch_reduce(fmt, a, st);
 }
 
@@ -1480,16 +1541,26 @@ int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, v
       default: e = launch_wide8<16>(a, p, st); break;
     }
   } else if (p.stream_steps > 0) {
+    // Split-K partials combined in the kernel (the counters live in the
+    // workspace's first 64 KB), else by a second, reduce kernel
+    // (MK_QMM_REDUCE_PASS=1 forces the latter; same results, bit for bit).
+    if (p.ks > 1 && (int64_t)p.rowblocks * p.ntiles <= mk::kWideCounters && !env_int("MK_QMM_REDUCE_PASS", 0))
+      a.cnt = static_cast<uint32_t*>(ws);
     switch (p.stream_steps) {
       case 16: e = launch_stream<16>(fmt, a, p, st); break;
       case 8: e = launch_stream<8>(fmt, a, p, st); break;
-      default: e = launch_stream<4>(fmt, a, p, st); break;
+      case 4: e = launch_stream<4>(fmt, a, p, st); break;
+      default: e = launch_stream<2>(fmt, a, p, st); break;
     }
-  } else switch (p.nw) {
+  } else {
+    if (p.ks > 1 && (int64_t)p.rowblocks * p.ntiles <= mk::kWideCounters && !env_int("MK_QMM_REDUCE_PASS", 0))
+      a.cnt = static_cast<uint32_t*>(ws);
+    switch (p.nw) {
     case 1: e = launch_q<1>(fmt, a, p, st); break;
     case 2: e = launch_q<2>(fmt, a, p, st); break;
     case 4: e = launch_q<4>(fmt, a, p, st); break;
     default: e = launch_q<8>(fmt, a, p, st); break;
+    }
   }
   if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
   return MK_OK;

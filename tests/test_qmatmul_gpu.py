@@ -11,6 +11,7 @@ import pytest
 from _gpu import (BF16_RTOL, assert_rel_close, dev, dev_bf16, host_bf16, host_bf16_bits, need_gpu,
                   torch)
 from oracle import cport, quant
+from oracle.bf16 import bf16_bits_to_f32
 
 pytestmark = pytest.mark.gpu
 
@@ -364,3 +365,38 @@ def test_int8_wide_kernel_is_planned_and_deterministic(monkeypatch):
     torch.cuda.synchronize()
     ref = cport.int8_pc_matmul(x, w, s)
     assert_rel_close(host_bf16(y64), ref, BF16_RTOL, "int8 64-column kernel")
+
+
+# The 64-column kernels' split-K: partials combined in the kernel by the last
+# arriving workgroup (default) or by the separate reduce pass
+# (MK_QMM_REDUCE_PASS=1); both sum in k order from zero, so the results are
+# the same bits.  Shapes: per-shard (N = 1792), streaming ks = 2 / 4 with a
+# ragged row block, and the generic kernels (N % 16 != 0).
+SPLIT_SHAPES = [(16, 4096, 1792), (5, 2048, 1024), (20, 4096, 512), (3, 4096, 1032), (1, 8192, 256)]
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+@pytest.mark.parametrize("M,K,N", SPLIT_SHAPES)
+def test_split_k_exchange_matches_reduce_pass(monkeypatch, fmt, M, K, N):
+    ops = _ops()
+    from mi355x import _lib
+    rng = np.random.default_rng(M + K + N + len(fmt))
+    if fmt == "int4":
+        x, p, s, z = quant.make_int4_case(rng, M, K, N)
+        args = (dev_bf16(x), dev(p), dev_bf16(s), dev(z))
+        run, ref = ops.int4_g64_matmul, cport.int4_g64_matmul(x, p, s, z)
+    else:
+        x, w, s = quant.make_int8_case(rng, M, K, N)
+        args = (dev_bf16(x), dev(w), dev(s))
+        run, ref = ops.int8_pc_matmul, cport.int8_pc_matmul(x, w, s)
+    print(f"split-k exchange {fmt} M={M} K={K} N={N}", flush=True)
+    fmt_code = _lib.MK_QFMT_INT4_G64 if fmt == "int4" else _lib.MK_QFMT_INT8_PC
+    assert _lib.lib().mk_qmatmul_workspace_bytes(fmt_code, M, K, N) > 0  # the shape splits K
+    first = host_bf16_bits(run(*args))
+    for _ in range(3):  # the counters return to zero: repeated calls, same bits
+        assert np.array_equal(host_bf16_bits(run(*args)), first)
+    assert int(ops.workspace(1, "cuda:0")[: 64 * 1024].count_nonzero()) == 0
+    monkeypatch.setenv("MK_QMM_REDUCE_PASS", "1")
+    two_pass = host_bf16_bits(run(*args))
+    assert np.array_equal(two_pass, first)
+    assert_rel_close(bf16_bits_to_f32(first), ref, BF16_RTOL, f"{fmt} split-K {M}x{K}x{N}")
