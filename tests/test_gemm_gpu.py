@@ -88,6 +88,21 @@ def test_gemm_f32_matches_oracle(batch, M, N, K):
     assert_rel_close(c.cpu().numpy().reshape(ref.shape), ref, F32_RTOL, f"f32 gemm {batch}x{M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("batch,M,N,K", [(1, 1024, 1024, 1024), (1, 100, 136, 48), (3, 200, 72, 96)])
+def test_gemm_f32_tiles_agree(batch, M, N, K, monkeypatch):
+    """The 64 x 64 tiles (small grids) and the 128 x 128 tiles run k in the
+    same order: the same bits, ragged edges included."""
+    ops = _ops()
+    rng = np.random.default_rng(M + N + K)
+    a = dev(rng.standard_normal((batch, M, K)).astype(np.float32))
+    b = dev(rng.standard_normal((batch, K, N)).astype(np.float32))
+    outs = []
+    for t in ("64", "128"):
+        monkeypatch.setenv("MK_GEMM_F32_TILE", t)
+        outs.append(ops.gemm_f32(a, b).cpu())
+    assert torch.equal(outs[0], outs[1])
+
+
 @pytest.mark.parametrize("scale", [1.0, 1e3, 1e5])
 def test_gemm_f32_precision_scales(scale):
     """The reference's f32 GEMM precision test: rel <= 2e-5 at scales 1, 1e3,
