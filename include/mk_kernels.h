@@ -183,6 +183,18 @@ enum { MK_EPI_NONE = 0, MK_EPI_ADD = 1, MK_EPI_SWIGLU = 2, MK_EPI_SWIGLU_PAIRS =
 int mk_gemm_bf16_epilogue(const void* a, const void* b, void* c, const void* aux, int epilogue,
                           int64_t batch, int64_t M, int64_t N, int64_t K, void* stream);
 
+/* mk_gemm_bf16_nt: mk_gemm_bf16_epilogue with B given transposed, bt bf16
+ * [batch, N, K] (k contiguous): C = A @ bt^T, the dot_general whose rhs
+ * contracts its last dimension (x @ W.T, q @ k^T), which the reference
+ * lowers with a transpose inside HandleDotGeneral
+ * (src/pjrt_plugin/ops/binary_ops.mm:644-1100).  Epilogues as above.
+ * Results equal, bit for bit, mk_gemm_bf16_epilogue on the transposed copy
+ * of bt: the fragments reach the matrix cores with the same values in the
+ * same k order.  Needs M % 256 == 0, N % 256 == 0, K % 32 == 0 (else
+ * MK_EUNSUPPORTED). */
+int mk_gemm_bf16_nt(const void* a, const void* bt, void* c, const void* aux, int epilogue, int64_t batch,
+                    int64_t M, int64_t N, int64_t K, void* stream);
+
 /* mk_dot_general: the dot_general cases the tiled GEMMs do not take,
  * with the reference's semantics (HandleDotGeneral,
  * src/pjrt_plugin/ops/binary_ops.mm:644-1100):

@@ -531,7 +531,11 @@ constexpr int kGemmStageBytes = 32 * 1024;
 __device__ __forceinline__ int swz_b2(int k, int c) { return c ^ ((2 * (k & 3)) | (((k >> 3) & 1) << 3)); }
 
 
-template <int WN_, bool PIPE>  // waves 2 x WN_; each 128 x (256 / WN_)
+// BT: B arrives as B^T [N, K] (k contiguous).  Its stage then has A's layout
+// (256 n rows of 64 B, the same swizzle) and each B fragment is one
+// ds_read_b128 instead of two transposing reads; the registers hold the same
+// values, so the results are the same bits as with B [K, N].
+template <int WN_, bool PIPE, bool BT = false>  // waves 2 x WN_; each 128 x (256 / WN_)
 __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs p) {
   constexpr int BM = 256, BN = 256, BK = 32, TM = 8, TN = 256 / WN_ / 16;
   constexpr int NW = 2 * WN_, DI = 16 / NW;  // waves; DMA instructions per wave for A (and B)
@@ -544,8 +548,10 @@ __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs
   tile_coords(xcd_logical_id(blockIdx.x, gridDim.x), tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const uint16_t* A = static_cast<const uint16_t*>(p.a) + (size_t)blockIdx.z * p.sa + (size_t)m0 * p.K;
-  const uint16_t* B = static_cast<const uint16_t*>(p.b) + (size_t)blockIdx.z * p.sb + n0;
+  const uint16_t* B = static_cast<const uint16_t*>(p.b) + (size_t)blockIdx.z * p.sb + (BT ? (size_t)n0 * p.K : n0);
   const int K = p.K, N = p.N;
+  // Elements between consecutive stages of one B DMA source.
+  const size_t bstep = BT ? (size_t)BK : (size_t)BK * N;
 
   // DMA sources.  A instruction i (rows 16i..16i+15): lane L fills row
   // 16i + L/4, position L%4.  B instruction i (k rows 2i, 2i+1): lane L
@@ -558,8 +564,12 @@ __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs
     const int i = DI * wave + u;
     const int row = 16 * i + (lane >> 2), pa = lane & 3;
     asrc[u] = A + (size_t)row * K + 8 * (pa ^ ((row >> 1) & 3));
-    const int kr = 2 * i + (lane >> 5), pb = lane & 31;
-    bsrc[u] = B + (size_t)kr * N + 8 * swz_b2(kr, pb);
+    if constexpr (BT) {
+      bsrc[u] = B + (size_t)row * K + 8 * (pa ^ ((row >> 1) & 3));
+    } else {
+      const int kr = 2 * i + (lane >> 5), pb = lane & 31;
+      bsrc[u] = B + (size_t)kr * N + 8 * swz_b2(kr, pb);
+    }
   }
   const uint32_t sbase = lds_addr(smem);
   auto issue = [&](int kt) {
@@ -568,7 +578,7 @@ __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs
     for (int u = 0; u < DI; ++u) dma16_asm(asrc[u] + kt * BK, st + (uint32_t)((DI * wave + u) * 1024));
 #pragma unroll
     for (int u = 0; u < DI; ++u)
-      dma16_asm(bsrc[u] + (size_t)kt * BK * N, st + (uint32_t)(ABYTES + (DI * wave + u) * 1024));
+      dma16_asm(bsrc[u] + (size_t)kt * bstep, st + (uint32_t)(ABYTES + (DI * wave + u) * 1024));
   };
 
   // Fragment offsets within a stage.  A tile i of this wave: row
@@ -578,7 +588,15 @@ __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs
   const int arow = wm * 128 + (lane & 15);
   const int aoff = arow * 64 + 16 * ((lane >> 4) ^ ((arow >> 1) & 3));
   int boff[2 * TN];
-  {
+  if constexpr (BT) {
+    // B^T tile j: n row wn*64 + 16j + (lane & 15), chunk lane >> 4 (A's read).
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int nrow = wn * (16 * TN) + 16 * j + (lane & 15);
+      boff[j] = ABYTES + nrow * 64 + 16 * ((lane >> 4) ^ ((nrow >> 1) & 3));
+      boff[TN + j] = 0;
+    }
+  } else {
     const int g = lane >> 4, r = (lane & 15) >> 2, q = lane & 3;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
@@ -625,6 +643,11 @@ __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs
     // feed alone takes ~70 us and the MFMA + fragment loop alone ~94 us, so
     // the kernel is bound by how well the two overlap (~126 us).
     auto read_b = [&](const unsigned char* st, u32x4* bf) {
+      if constexpr (BT) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const u32x4*>(st + boff[j]);
+        return;
+      }
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(st + boff[2 * j]));
@@ -640,7 +663,7 @@ __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs
       dma16_asm(asrc[u] + ks * BK, sbase + (uint32_t)(slot * kGemmStageBytes + (DI * wave + u) * 1024));
     };
     auto issue_b = [&](int ks, int slot, int u) {
-      dma16_asm(bsrc[u] + (size_t)ks * BK * N,
+      dma16_asm(bsrc[u] + (size_t)ks * bstep,
                 sbase + (uint32_t)(slot * kGemmStageBytes + ABYTES + (DI * wave + u) * 1024));
     };
     // The host only picks this kernel when KT >= 2 S.
@@ -731,6 +754,10 @@ __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs
     u32x4 bf[TN];
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
+      if constexpr (BT) {
+        bf[j] = *reinterpret_cast<const u32x4*>(st + boff[j]);
+        continue;
+      }
       const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(st + boff[2 * j]));
       const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(st + boff[2 * j + 1]));
       const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
@@ -899,8 +926,9 @@ int env_tile() {
 
 namespace {
 
+// bt: b is B^T [N, K] (only the DMA-fed 256 x 256 kernel takes it).
 int run_gemm_bf16(const char* fn, const void* a, const void* b, void* c, const void* aux, int epi, int64_t batch,
-                  int64_t M, int64_t N, int64_t K, int out_f32, void* stream) {
+                  int64_t M, int64_t N, int64_t K, int out_f32, void* stream, bool bt = false) {
   mkc::clear_error();
   int rc = check_gemm(fn, a, b, c, batch, M, N, K);
   if (rc != MK_OK) return rc;
@@ -910,6 +938,9 @@ int run_gemm_bf16(const char* fn, const void* a, const void* b, void* c, const v
     return mkc::fail(MK_EINVAL, "%s: an epilogue needs a bf16 output and an aux operand", fn);
   const char* dma_env = getenv("MK_GEMM_DMA");
   const bool dma = !(dma_env && dma_env[0] == '0');
+  if (bt && !(M % 256 == 0 && N % 256 == 0 && K % 32 == 0))
+    return mkc::fail(MK_EUNSUPPORTED, "%s: needs M %% 256 == 0, N %% 256 == 0, K %% 32 == 0 "
+                     "(got M=%lld, N=%lld, K=%lld)", fn, (long long)M, (long long)N, (long long)K);
   if (epi == MK_EPI_SWIGLU_PAIRS && !(dma && M % 256 == 0 && N % 256 == 0 && K % 32 == 0))
     return mkc::fail(MK_EUNSUPPORTED, "%s: paired SwiGLU needs M %% 256 == 0, N %% 256 == 0, K %% 32 == 0 "
                      "(got M=%lld, N=%lld, K=%lld)", fn, (long long)M, (long long)N, (long long)K);
@@ -926,7 +957,25 @@ int run_gemm_bf16(const char* fn, const void* a, const void* b, void* c, const v
   if (tile == 0) tile = big_tiles >= 128 ? 256 : 128;
   if (epi == MK_EPI_SWIGLU_PAIRS) tile = 256;
   hipError_t e;
-  if (tile == 256 && dma && M % 256 == 0 && N % 256 == 0 && K % 32 == 0) {
+  if (bt) {
+    const dim3 grid((unsigned)((M / 256) * (N / 256)), 1, (unsigned)batch);
+    const char* pv = getenv("MK_GEMM_PIPE");
+    const char* pk = getenv("MK_GEMM_PIPE_K");
+    const int64_t pipe_k = pk ? atoll(pk) : 2048;
+    if (!(pv && atoi(pv) == 0) && K >= pipe_k && K >= 2 * 32 * mk::kPipeStages) {
+      constexpr size_t lds_p = (size_t)mk::kPipeStages * mk::kGemmStageBytes;
+      e = lds_opt_in((const void*)mk::gemm_bf16_256dma_kernel<4, true, true>, lds_p);
+      if (e == hipSuccess)
+        hipLaunchKernelGGL((mk::gemm_bf16_256dma_kernel<4, true, true>), grid, dim3(512), lds_p, st, p);
+    } else {
+      constexpr size_t lds = (size_t)mk::kGemmStages * mk::kGemmStageBytes;
+      constexpr size_t lds4 = lds > (size_t)mk::kEpiStageBytes ? lds : (size_t)mk::kEpiStageBytes;
+      e = lds_opt_in((const void*)mk::gemm_bf16_256dma_kernel<4, false, true>, lds4);
+      if (e == hipSuccess)
+        hipLaunchKernelGGL((mk::gemm_bf16_256dma_kernel<4, false, true>), grid, dim3(512), lds4, st, p);
+    }
+    if (e == hipSuccess) e = hipGetLastError();
+  } else if (tile == 256 && dma && M % 256 == 0 && N % 256 == 0 && K % 32 == 0) {
     constexpr size_t lds = (size_t)mk::kGemmStages * mk::kGemmStageBytes;
     const dim3 grid((unsigned)((M / 256) * (N / 256)), 1, (unsigned)batch);
     const char* w = getenv("MK_GEMM_WAVES");
@@ -989,6 +1038,11 @@ extern "C" int mk_gemm_bf16(const void* a, const void* b, void* c, int64_t batch
 extern "C" int mk_gemm_bf16_epilogue(const void* a, const void* b, void* c, const void* aux, int epilogue,
                                      int64_t batch, int64_t M, int64_t N, int64_t K, void* stream) {
   return run_gemm_bf16("mk_gemm_bf16_epilogue", a, b, c, aux, epilogue, batch, M, N, K, 0, stream);
+}
+
+extern "C" int mk_gemm_bf16_nt(const void* a, const void* bt, void* c, const void* aux, int epilogue,
+                               int64_t batch, int64_t M, int64_t N, int64_t K, void* stream) {
+  return run_gemm_bf16("mk_gemm_bf16_nt", a, bt, c, aux, epilogue, batch, M, N, K, 0, stream, true);
 }
 
 

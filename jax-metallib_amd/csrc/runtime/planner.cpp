@@ -1070,7 +1070,16 @@ class Planner {
         return o;
       };
       Step st;
-      st.in = {canon(0, gd.sa, gd.M, gd.K, "a"), canon(1, gd.sb, gd.K, gd.N, "b")};
+      // An rhs that already is B^T [batch, N, K] (its contracting dimension
+      // last: x @ W.T, q @ k^T) on shapes the 256 x 256 kernel takes goes to
+      // the GEMM that reads B^T as it lies: no copy, the same bits
+      // (MK_PLAN_GEMM_NT=0 copies it instead).
+      const char* pnt = getenv("MK_PLAN_GEMM_NT");
+      st.b_t = ta == DT_BF16 && tr == DT_BF16 && !gd.copy_b && gd.sb[1] == 1 && gd.sb[2] == gd.K &&
+               (gd.batch == 1 || gd.sb[0] == gd.N * gd.K) && gd.M % 256 == 0 && gd.N % 256 == 0 &&
+               gd.K % 32 == 0 && !(pnt && pnt[0] == '0');
+      st.in = {canon(0, gd.sa, gd.M, gd.K, "a"),
+               st.b_t ? dot_operand(gd, 1, eb) : canon(1, gd.sb, gd.K, gd.N, "b")};
       if (ta == DT_F32) {
         st.kind = ST_GEMM_F32;
         st.dt = MK_DT_F32;
@@ -1085,8 +1094,8 @@ class Planner {
       st.K = gd.K;
       st.out = temp_for(v);
       std::ostringstream ds;
-      ds << (st.kind == ST_GEMM_F32 ? "gemm_f32" : "gemm_bf16") << " batch=" << gd.batch << " M=" << gd.M
-         << " N=" << gd.N << " K=" << gd.K << " -> " << dtype_name(tr);
+      ds << (st.kind == ST_GEMM_F32 ? "gemm_f32" : st.b_t ? "gemm_bf16_nt" : "gemm_bf16") << " batch=" << gd.batch
+         << " M=" << gd.M << " N=" << gd.N << " K=" << gd.K << " -> " << dtype_name(tr);
       st.desc = ds.str();
       plan_.steps.push_back(st);
       *out = st.out;

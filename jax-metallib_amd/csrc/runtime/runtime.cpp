@@ -355,6 +355,7 @@ int run_step(const mkrt::Step& st, const std::vector<void*>& mem, void* ws, int6
   void* out = mem[st.out];
   switch (st.kind) {
     case mkrt::ST_GEMM_BF16:
+      if (st.b_t) return mk_gemm_bf16_nt(in(0), in(1), out, nullptr, MK_EPI_NONE, st.batch, st.M, st.N, st.K, s);
       return mk_gemm_bf16(in(0), in(1), out, st.batch, st.M, st.N, st.K, st.out_f32, s);
     case mkrt::ST_GEMM_F32:
       return mk_gemm_f32(in(0), in(1), out, st.batch, st.M, st.N, st.K, s);

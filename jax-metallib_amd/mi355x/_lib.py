@@ -47,6 +47,7 @@ SIGNATURES = {
     "mk_int8pc_matmul_bf16": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p]),
     "mk_gemm_bf16": (_i32, [_p, _p, _p, _i64, _i64, _i64, _i64, _i32, _p]),
     "mk_gemm_bf16_epilogue": (_i32, [_p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _p]),
+    "mk_gemm_bf16_nt": (_i32, [_p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _p]),
     "mk_int4g64_matmul_epilogue_bf16": (_i32, [_p, _p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _p, _i64, _p]),
     "mk_int8pc_matmul_epilogue_bf16": (_i32, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _p, _i64, _p]),
     "mk_qmatmul_swiglu_pair_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64]),

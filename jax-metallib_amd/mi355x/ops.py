@@ -213,6 +213,27 @@ def gemm_bf16(a, b, out_f32=False, out=None, epilogue=None, aux=None):
     return c
 
 
+def gemm_bf16_nt(a, bt, out=None, epilogue=None, aux=None):
+    """[batch,] M x K @ (N x K)^T in bf16 with f32 accumulation -> bf16: the
+    rhs given with K contiguous (x @ W.T, q @ k^T).  The same bits as
+    gemm_bf16(a, bt.transpose(-1, -2).contiguous(), ...).  Needs M and N
+    multiples of 256 and K of 32."""
+    _require(a, _BF16, "a")
+    _require(bt, _BF16, "bt")
+    if a.dim() != bt.dim() or a.dim() not in (2, 3) or a.shape[-1] != bt.shape[-1] or \
+            (a.dim() == 3 and a.shape[0] != bt.shape[0]):
+        raise ValueError(f"gemm_bf16_nt: incompatible shapes {tuple(a.shape)} x {tuple(bt.shape)}^T")
+    batch = a.shape[0] if a.dim() == 3 else 1
+    M, K, N = a.shape[-2], a.shape[-1], bt.shape[-2]
+    shape = (M, N) if a.dim() == 2 else (batch, M, N)
+    NO = _out_cols(N, epilogue, "gemm_bf16_nt")
+    c = out if out is not None else torch.empty(shape[:-1] + (NO,), dtype=torch.bfloat16, device=a.device)
+    epi = _epilogue(epilogue, aux, shape, "gemm_bf16_nt")
+    check(lib().mk_gemm_bf16_nt(_ptr(a), _ptr(bt), _ptr(c), _ptr(aux) if aux is not None else None, epi, batch,
+                                M, N, K, _stream(a.device)))
+    return c
+
+
 def gemm_f32(a, b, out=None):
     """[batch,] M x K @ K x N in f32."""
     _require(a, (torch.float32,), "a")

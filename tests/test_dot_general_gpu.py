@@ -208,3 +208,31 @@ def test_dimension_numbers_match_einsum(client, sa, sb, lc, rc, lb, rb, dt):
     want = np.einsum(spec, af.astype(np.float64), bf.astype(np.float64))
     assert y.shape == want.shape
     assert_rel_close(y.astype(np.float64), want, tol, f"{dt} {spec}")
+
+
+@pytest.mark.parametrize("sa,sb,lc,rc,lb,rb", [
+    ((512, 256), (768, 256), (1,), (1,), (), ()),              # x @ W.T
+    ((2, 256, 64), (2, 512, 64), (2,), (2,), (0,), (0,)),      # q @ k^T per batch
+])
+def test_rhs_contracting_last_runs_on_the_nt_gemm(client, monkeypatch, sa, sb, lc, rc, lb, rb):
+    """An rhs whose contracting dimension is last is read in place by the
+    GEMM that takes B^T: no operand copy in the plan, and the same bits as
+    the copy-then-GEMM plan (MK_PLAN_GEMM_NT=0)."""
+    rng = np.random.default_rng(sum(sa) + sum(sb))
+    text = P.dot_general_dims(sa, sb, "bfloat16", lc, rc, lb, rb)
+    ab = f32_to_bf16_bits(rng.standard_normal(sa).astype(np.float32))
+    bb = f32_to_bf16_bits(rng.standard_normal(sb).astype(np.float32))
+    print(f"[dot] nt {sa} x {sb}", flush=True)
+    exe = client.compile(text)
+    assert "gemm_bf16_nt" in exe.plan and "gemm operand b" not in exe.plan, exe.plan
+    exe.close()
+    y_nt = run(client, text, (ab, rt.BF16), (bb, rt.BF16))
+    monkeypatch.setenv("MK_PLAN_GEMM_NT", "0")
+    exe = client.compile(text)
+    assert "gemm_bf16_nt" not in exe.plan, exe.plan
+    exe.close()
+    y_cp = run(client, text, (ab, rt.BF16), (bb, rt.BF16))
+    assert np.array_equal(np.asarray(y_nt).view(np.uint16), np.asarray(y_cp).view(np.uint16))
+    want = np.einsum(_einsum_spec(len(sa), len(sb), lc, rc, lb, rb), bf16_bits_to_f32(ab).astype(np.float64),
+                     bf16_bits_to_f32(bb).astype(np.float64))
+    assert_rel_close(bf16_bits_to_f32(y_nt).astype(np.float64), want, 2e-2, f"nt {sa} x {sb}")

@@ -167,3 +167,42 @@ def test_gemm_bf16_pipelined_path(batch, M, N, K, monkeypatch):
     c0 = ops.gemm_bf16(dev_bf16(a), dev_bf16(b), out_f32=True)
     torch.cuda.synchronize()
     assert np.array_equal(c.cpu().numpy(), c0.cpu().numpy()), "pipelined and ring kernels differ"
+
+
+@pytest.mark.parametrize("batch,M,N,K", [(1, 256, 256, 32), (2, 256, 512, 320), (1, 512, 768, 2048),
+                                         (1, 256, 256, 4160), (1, 1024, 512, 1056)])
+@pytest.mark.parametrize("epilogue", [None, "add", "swiglu", "swiglu_pairs"])
+def test_gemm_bf16_nt_bit_identical(batch, M, N, K, epilogue, monkeypatch):
+    """B given transposed (bt [N, K]): the same bits as the [K, N] product of
+    its transposed copy, on the ring kernel (K < 2048) and the pipelined one
+    (both loop tails), with every epilogue; and against float64."""
+    ops = _ops()
+    rng = np.random.default_rng(batch * 7 + M + N + K)
+    a = dev_bf16(_case(rng, (batch, M, K), 1.0 / np.sqrt(np.sqrt(K))))
+    bt_h = _case(rng, (batch, N, K), 1.0 / np.sqrt(np.sqrt(K)))
+    bt = dev_bf16(bt_h)
+    b = bt.transpose(-1, -2).contiguous()
+    aux = None
+    if epilogue in ("add", "swiglu"):
+        aux = dev_bf16(_case(rng, (batch, M, N), 1.0))
+    print(f"gemm nt case b={batch} M={M} N={N} K={K} epilogue={epilogue}", flush=True)
+    c_nt = ops.gemm_bf16_nt(a, bt, epilogue=epilogue, aux=aux)
+    c_nn = ops.gemm_bf16(a, b, epilogue=epilogue, aux=aux)
+    torch.cuda.synchronize()
+    assert torch.equal(c_nt.view(torch.int16), c_nn.view(torch.int16)), "NT and NN products differ"
+    if epilogue is None:
+        monkeypatch.setenv("MK_GEMM_PIPE", "0")
+        c_ring = ops.gemm_bf16_nt(a, bt)
+        torch.cuda.synchronize()
+        assert torch.equal(c_nt.view(torch.int16), c_ring.view(torch.int16)), "NT pipelined and ring differ"
+        ah = obf.bf16_bits_to_f32(a.view(torch.int16).cpu().numpy().view(np.uint16)).astype(np.float64)
+        ref = np.matmul(ah, obf.bf16_bits_to_f32(bt_h).astype(np.float64).transpose(0, 2, 1))
+        assert_rel_close(c_nt.float().cpu().numpy(), ref, BF16_RTOL, f"nt {batch}x{M}x{N}x{K}")
+
+
+def test_gemm_bf16_nt_rejects_unaligned_shapes():
+    ops = _ops()
+    a = torch.zeros((200, 64), dtype=torch.bfloat16, device="cuda")
+    bt = torch.zeros((256, 64), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(Exception, match="M % 256 == 0"):
+        ops.gemm_bf16_nt(a, bt)

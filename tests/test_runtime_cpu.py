@@ -234,6 +234,23 @@ def test_several_contracting_dims_plan():
         "gemm_bf16 batch=1 M=64 N=128 K=512 -> bf16"]
 
 
+def test_rhs_contracting_last_plans_the_nt_gemm(monkeypatch):
+    """x @ W.T and q @ k^T (rhs contracting its last dim) read the rhs in
+    place on 256-aligned bf16 shapes; other shapes, f32 and
+    MK_PLAN_GEMM_NT=0 copy it to [batch, K, N] first."""
+    assert plan(P.dot_general_dims((512, 256), (768, 256), "bfloat16", (1,), (1,))) == [
+        "gemm_bf16_nt batch=1 M=512 N=768 K=256 -> bf16"]
+    assert plan(P.dot_general_dims((2, 256, 64), (2, 512, 64), "bfloat16", (2,), (2,), (0,), (0,))) == [
+        "gemm_bf16_nt batch=2 M=256 N=512 K=64 -> bf16"]
+    assert plan(P.dot_general_dims((500, 256), (768, 256), "bfloat16", (1,), (1,))) == [
+        "gemm operand b to [1,256,768]", "gemm_bf16 batch=1 M=500 N=768 K=256 -> bf16"]
+    assert plan(P.dot_general_dims((512, 256), (768, 256), "float32", (1,), (1,))) == [
+        "gemm operand b to [1,256,768]", "gemm_f32 batch=1 M=512 N=768 K=256 -> f32"]
+    monkeypatch.setenv("MK_PLAN_GEMM_NT", "0")
+    assert plan(P.dot_general_dims((512, 256), (768, 256), "bfloat16", (1,), (1,))) == [
+        "gemm operand b to [1,256,768]", "gemm_bf16 batch=1 M=512 N=768 K=256 -> bf16"]
+
+
 def test_dot_with_mismatched_dimension_sizes_is_rejected():
     text = _wrap(["tensor<4x8x8xf32>", "tensor<8x6x3xf32>"], ["tensor<4x3xf32>"], [
         "%0 = stablehlo.dot_general %arg0, %arg1, contracting_dims = [1, 2] x [0, 1] : "
