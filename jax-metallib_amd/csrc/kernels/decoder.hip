@@ -218,21 +218,23 @@ __global__ __launch_bounds__(256) void softmax_causal_kernel(CausalArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Causal attention in one pass (flash-attention style): per (b, h) and 128
-// query rows, loop over 64-key tiles up to the diagonal; scores, the online
-// softmax and P @ V stay on chip, and the output goes straight to the merged
-// [B*S, H*D] layout.  8 waves, 16 query rows each; v_mfma_f32_16x16x32_bf16
-// throughout.
+// Causal attention in one pass (flash-attention style): per (b, h) and
+// 8 x 16 RB query rows, loop over 64-key tiles up to the diagonal; scores, the
+// online softmax and P @ V stay on chip, and the output goes straight to the
+// merged [B*S, H*D] layout.  8 waves, each 16 RB query rows (RB row blocks of
+// 16); v_mfma_f32_16x16x32_bf16 throughout.  Every K and V fragment read
+// from LDS feeds RB MFMAs, so RB = 2 (S % 256 == 0) halves the LDS reads per
+// MFMA of RB = 1.
 //   S = Q K^T: first operand K rows (lane: key 16t + l%16, 8 consecutive d
-//     from an XOR-swizzled LDS tile), second Q rows (registers) -> lane holds
-//     row i = l%16 and keys 4(l/16) .. +3 of each 16-key block.
+//     from an XOR-swizzled LDS tile), second Q rows (registers, loaded from
+//     global memory once) -> lane holds row i = l%16 of its block and keys
+//     4(l/16) .. +3 of each 16-key block.
 //   P @ V: second operand P straight from those registers (bf16); its 8
 //     k-slots per lane are keys {4g .. 4g+3} and {16 + 4g .. 16 + 4g + 3} of
 //     a 32-key block (g = l/16), and the V fragment is read with
 //     ds_read_b64_tr_b16 from exactly those rows, so no shuffle is needed.
 // Scores are scaled into log2 units; exp2 is the hardware v_exp_f32.
 // ---------------------------------------------------------------------------
-constexpr int kFaQ = 128;  // query rows per workgroup
 constexpr int kFaKV = 64;  // keys per tile
 
 struct AttnArgs {
@@ -250,36 +252,42 @@ __device__ __forceinline__ int fa_vswz(int r) { return (2 * (r & 3)) | (8 * ((r 
 
 __device__ __forceinline__ float fa_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// K / V tiles and the workgroup's Q rows reach LDS by DMA
-// (global_load_lds): a ring of kFaRing stages (one K tile and one V tile,
-// 32 KB) issued kFaRing - 1 tiles ahead, so each tile's load latency hides
-// behind the previous tiles' MFMAs, plus the 128 Q rows (32 KB); 160 KB in
-// all.  The XOR swizzles are applied by choosing each DMA lane's source
-// chunk.
+// K / V tiles reach LDS by DMA (global_load_lds): a ring of kFaRing stages
+// (one K tile and one V tile, 32 KB) issued kFaRing - 1 tiles ahead, so each
+// tile's load latency hides behind the previous tiles' MFMAs; 128 KB in all.
+// The XOR swizzles are applied by choosing each DMA lane's source chunk.
 constexpr int kFaRing = 4;
-constexpr int kFaStage = 2 * kFaKV * kHeadDim * 2;              // 32 KB
-constexpr int kFaLds = kFaRing * kFaStage + kFaQ * kHeadDim * 2;  // 160 KB
+constexpr int kFaStage = 2 * kFaKV * kHeadDim * 2;  // 32 KB
+constexpr int kFaLds = kFaRing * kFaStage;          // 128 KB
 
+template <int RB>
 __global__ __launch_bounds__(512) void attention_causal_kernel(AttnArgs a) {
   constexpr int D = kHeadDim, ROWB = D * 2;  // 256-byte rows
-  constexpr int R = kFaRing;
+  constexpr int R = kFaRing, QW = 16 * RB, QT = 8 * QW;  // rows per wave / per workgroup
   extern __shared__ __attribute__((aligned(16))) unsigned char fa_smem[];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 4, l16 = lane & 15;
   const int BH = a.B * a.H;
   const int bh = (int)(blockIdx.x % BH);
-  const int qt = a.S / kFaQ - 1 - (int)(blockIdx.x / BH);  // longest rows first
-  const int q0 = qt * kFaQ, i0 = q0 + 16 * w;
+  const int qt = a.S / QT - 1 - (int)(blockIdx.x / BH);  // longest rows first
+  const int q0 = qt * QT, i0 = q0 + QW * w;
   const uint16_t* Qg = a.q + (int64_t)bh * a.S * D;
   const uint16_t* Kg = a.k + (int64_t)bh * a.S * D;
   const uint16_t* Vg = a.v + (int64_t)bh * a.S * D;
   const uint32_t sbase = lds_addr(fa_smem);
-  unsigned char* qs = fa_smem + R * kFaStage;
+
+  // This wave's Q fragments: block rb, d chunk 4s + g of row i0 + 16 rb + l16.
+  u32x4 qf[RB][4];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      qf[rb][s] = *reinterpret_cast<const u32x4*>(Qg + (int64_t)(i0 + 16 * rb + l16) * D + 8 * (4 * s + g));
 
   // DMA instruction I = 2w + u (u = 0, 1) of a tile covers rows 4I .. 4I+3
   // of K and of V: lane L fills row 4I + L/16, chunk position L%16, from
   // the source chunk the swizzle puts there (K: c ^ (row % 16), V:
-  // c ^ fa_vswz(row)).  Q: each wave's 16 rows, 4 instructions, K's swizzle.
+  // c ^ fa_vswz(row)).
   const uint16_t* ksrc[2];
   const uint16_t* vsrc[2];
 #pragma unroll
@@ -296,21 +304,21 @@ __global__ __launch_bounds__(512) void attention_causal_kernel(AttnArgs a) {
     for (int u = 0; u < 2; ++u)
       dma16_asm(vsrc[u] + (int64_t)t * kFaKV * D, st + (uint32_t)(kFaKV * ROWB + (2 * w + u) * 1024));
   };
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int row = 16 * w + 4 * u + (lane >> 4), p = lane & 15;  // row within the 128 Q rows
-    dma16_asm(Qg + (int64_t)(q0 + row) * D + 8 * (p ^ (row & 15)),
-              sbase + (uint32_t)(R * kFaStage + (4 * w + u) * 1024));
-  }
-  const int ntiles = (q0 + kFaQ) / kFaKV;  // >= 2
+  const int ntiles = (q0 + QT) / kFaKV;  // >= 2
   const int pre = ntiles < R - 1 ? ntiles : R - 1;
   for (int t = 0; t < pre; ++t) issue(t, t);
 
-  f32x4 o[8];
+  f32x4 o[RB][8];
 #pragma unroll
-  for (int n = 0; n < 8; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY, lsum = 0.f;
-  u32x4 qf[4];
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int n = 0; n < 8; ++n) o[rb][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m[RB], lsum[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    m[rb] = -INFINITY;
+    lsum[rb] = 0.f;
+  }
 
   // V fragment byte offsets (tile-relative): d tile n, 32-key block u, low /
   // high 4 keys.  Lane (g, r = (l%16)/4, q = l%4) reads row 32u + 4g + r
@@ -319,82 +327,88 @@ __global__ __launch_bounds__(512) void attention_causal_kernel(AttnArgs a) {
 
   for (int t = 0; t < ntiles; ++t) {
     const int slot = t % R;
-    // Own DMAs of tile t (and of Q) landed; the tiles issued after it may
-    // still be in flight (R - 2 of them while the ring is full, fewer at
-    // the end, where the wait is for all).  After the barrier every wave's
-    // have landed and every wave is done with tile t-1's slot.
+    // Own DMAs of tile t landed; the tiles issued after it may still be in
+    // flight (R - 2 of them while the ring is full, fewer at the end, where
+    // the wait is for all).  After the barrier every wave's have landed and
+    // every wave is done with tile t-1's slot.
     if (t + R - 1 <= ntiles) vm_wait(4 * (R - 2));
     else vm_wait(0);
     asm volatile("s_barrier" ::: "memory");
     if (t + R - 1 < ntiles) issue(t + R - 1, (t + R - 1) % R);
-    if (t == 0) {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int row = 16 * w + l16;
-        qf[s] = *reinterpret_cast<const u32x4*>(qs + row * ROWB + 16 * ((4 * s + g) ^ (row & 15)));
-      }
-    }
     const int kv0 = t * kFaKV;
-    if (kv0 <= i0 + 15) {  // some key of the tile is visible to this wave's rows
+    // Some key of the tile is visible to this wave's rows.  kv0 - i0 is a
+    // multiple of 16 RB, so then kv0 <= i0: every row of every block sees
+    // at least key kv0, and no row max below is -inf.
+    if (kv0 <= i0 + QW - 1) {
       const unsigned char* Ks = fa_smem + slot * kFaStage;
       const unsigned char* Vs = Ks + kFaKV * ROWB;
-      f32x4 sacc[4];
+      f32x4 sacc[RB][4];
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) sacc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) sacc[rb][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) {
           const int j = 16 * tt + l16;
           const u32x4 kf = *reinterpret_cast<const u32x4*>(Ks + j * ROWB + 16 * ((4 * s + g) ^ (j & 15)));
-          sacc[tt] = mfma16x16x32(kf, qf[s], sacc[tt]);
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb) sacc[rb][tt] = mfma16x16x32(kf, qf[rb][s], sacc[rb][tt]);
         }
-      const int i = i0 + l16;
       // Only a tile that crosses the diagonal of this wave's rows is masked
       // (a wave-uniform branch).
       if (kv0 + kFaKV - 1 > i0) {
 #pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+          const int i = i0 + 16 * rb + l16;
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (kv0 + 16 * tt + 4 * g + e > i) sacc[rb][tt][e] = -INFINITY;
+        }
+      }
+      u32x4 pf[RB][2];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        // The scale (log2 units) is positive, so the row max of the scaled
+        // scores is the scaled max of the raw ones (rounding is monotonic),
+        // and each probability takes one fma before its exp2.
+        float mt = -INFINITY;
+#pragma unroll
         for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (kv0 + 16 * tt + 4 * g + e > i) sacc[tt][e] = -INFINITY;
-      }
-      // The scale (log2 units) is positive, so the row max of the scaled
-      // scores is the scaled max of the raw ones (rounding is monotonic),
-      // and each probability takes one fma before its exp2.
-      float mt = -INFINITY;
+          for (int e = 0; e < 4; ++e) mt = fmaxf(mt, sacc[rb][tt][e]);
+        mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        const float mn = fmaxf(m[rb], mt * a.scale_log2);
+        const float alpha = fa_exp2(m[rb] - mn);
+        // alpha is exactly 1 for a row whose max held; when that is every
+        // row of the block the rescale is skipped.
+        const bool rescale = !__all(mn == m[rb]);
+        m[rb] = mn;
+        float ps = 0.f;
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
+        for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) mt = fmaxf(mt, sacc[tt][e]);
-      mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-      const float mn = fmaxf(m, mt * a.scale_log2);
-      const float alpha = fa_exp2(m - mn);
-      // alpha is exactly 1 for a row whose max held; when that is every row
-      // of the wave the rescale is skipped.
-      const bool rescale = !__all(mn == m);
-      m = mn;
-      float ps = 0.f;
+          for (int e = 0; e < 4; ++e) {
+            const float p = fa_exp2(__builtin_fmaf(sacc[rb][tt][e], a.scale_log2, -mn));
+            sacc[rb][tt][e] = p;
+            ps += p;
+          }
+        lsum[rb] = lsum[rb] * alpha + ps;
+        if (rescale) {
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float p = fa_exp2(__builtin_fmaf(sacc[tt][e], a.scale_log2, -mn));
-          sacc[tt][e] = p;
-          ps += p;
+          for (int n = 0; n < 8; ++n) o[rb][n] *= alpha;
         }
-      lsum = lsum * alpha + ps;
-      if (rescale) {
 #pragma unroll
-        for (int n = 0; n < 8; ++n) o[n] *= alpha;
+        for (int u = 0; u < 2; ++u)
+          pf[rb][u] = u32x4{pack_bf16x2(sacc[rb][2 * u][0], sacc[rb][2 * u][1]),
+                            pack_bf16x2(sacc[rb][2 * u][2], sacc[rb][2 * u][3]),
+                            pack_bf16x2(sacc[rb][2 * u + 1][0], sacc[rb][2 * u + 1][1]),
+                            pack_bf16x2(sacc[rb][2 * u + 1][2], sacc[rb][2 * u + 1][3])};
       }
-      u32x4 pf[2];
-#pragma unroll
-      for (int u = 0; u < 2; ++u)
-        pf[u] = u32x4{pack_bf16x2(sacc[2 * u][0], sacc[2 * u][1]), pack_bf16x2(sacc[2 * u][2], sacc[2 * u][3]),
-                      pack_bf16x2(sacc[2 * u + 1][0], sacc[2 * u + 1][1]),
-                      pack_bf16x2(sacc[2 * u + 1][2], sacc[2 * u + 1][3])};
 #pragma unroll
       for (int n = 0; n < 8; ++n)
 #pragma unroll
@@ -406,7 +420,9 @@ __global__ __launch_bounds__(512) void attention_causal_kernel(AttnArgs a) {
           const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
               (lds_s16x4_t)(Vs + r1 * ROWB + 16 * (c ^ fa_vswz(r1)) + hb));
           const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
-          o[n] = mfma16x16x32(u32x4{l2.x, l2.y, h2.x, h2.y}, pf[u], o[n]);
+          const u32x4 vf = u32x4{l2.x, l2.y, h2.x, h2.y};
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb) o[rb][n] = mfma16x16x32(vf, pf[rb][u], o[rb][n]);
         }
     }
     // This wave's reads of the slot are complete before the next barrier
@@ -414,15 +430,19 @@ __global__ __launch_bounds__(512) void attention_causal_kernel(AttnArgs a) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
 
-  lsum += __shfl_xor(lsum, 16, 64);
-  lsum += __shfl_xor(lsum, 32, 64);
-  const float inv = 1.0f / lsum;
   const int b = bh / a.H, h = bh - b * a.H;
-  uint16_t* out = a.out + ((int64_t)b * a.S + i0 + l16) * (a.H * D) + h * D + 4 * g;
 #pragma unroll
-  for (int n = 0; n < 8; ++n)
-    *reinterpret_cast<u32x2*>(out + 16 * n) =
-        u32x2{pack_bf16x2(o[n].x * inv, o[n].y * inv), pack_bf16x2(o[n].z * inv, o[n].w * inv)};
+  for (int rb = 0; rb < RB; ++rb) {
+    float l = lsum[rb];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    const float inv = 1.0f / l;
+    uint16_t* out = a.out + ((int64_t)b * a.S + i0 + 16 * rb + l16) * (a.H * D) + h * D + 4 * g;
+#pragma unroll
+    for (int n = 0; n < 8; ++n)
+      *reinterpret_cast<u32x2*>(out + 16 * n) = u32x2{pack_bf16x2(o[rb][n].x * inv, o[rb][n].y * inv),
+                                                      pack_bf16x2(o[rb][n].z * inv, o[rb][n].w * inv)};
+  }
 }
 
 struct MergeArgs {
@@ -455,6 +475,7 @@ __global__ __launch_bounds__(256) void merge_heads_kernel(MergeArgs a) {
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 
 extern "C" int mk_rope_qkv_split_bf16(const void* qkv, const float* cos_table, const float* sin_table, void* q,
                                       void* k, void* v, int64_t B, int64_t S, int64_t H, int64_t D, int k_rows,
@@ -544,9 +565,9 @@ extern "C" int mk_attention_causal_bf16(const void* q, const void* k, const void
   if (!q || !k || !v || !out) return mkc::fail(MK_EINVAL, "%s: null pointer", fn);
   if (B <= 0 || S <= 0 || H <= 0 || D <= 0) return mkc::fail(MK_EINVAL, "%s: sizes must be positive", fn);
   if (D != mk::kHeadDim) return mkc::fail(MK_EUNSUPPORTED, "%s: head dim %lld (only 128)", fn, (long long)D);
-  if (S % mk::kFaQ != 0)
+  if (S % 128 != 0)
     return mkc::fail(MK_EUNSUPPORTED, "%s: sequence length %lld not a multiple of 128", fn, (long long)S);
-  if (B * H * (S / mk::kFaQ) > (1 << 30) || B * H * S * D > ((int64_t)1 << 40))
+  if (B * H * (S / 128) > (1 << 30) || B * H * S * D > ((int64_t)1 << 40))
     return mkc::fail(MK_EINVAL, "%s: shape too large", fn);
   mk::AttnArgs a;
   a.q = static_cast<const uint16_t*>(q);
@@ -559,11 +580,18 @@ extern "C" int mk_attention_causal_bf16(const void* q, const void* k, const void
   if (!(scale > 0.f) || !std::isfinite(scale))
     return mkc::fail(MK_EINVAL, "%s: scale must be positive and finite (got %g)", fn, (double)scale);
   a.scale_log2 = scale * 1.4426950408889634f;
-  hipError_t e = hipFuncSetAttribute((const void*)mk::attention_causal_kernel,
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, mk::kFaLds);
+  // 32 query rows per wave when S allows (256 per workgroup), else 16.
+  // MK_ATTN_RB=1 keeps 16; the results are the same bits either way.
+  const char* rbv = getenv("MK_ATTN_RB");
+  const bool rb2 = S % 256 == 0 && !(rbv && atoi(rbv) == 1);
+  const void* kfn = rb2 ? (const void*)mk::attention_causal_kernel<2> : (const void*)mk::attention_causal_kernel<1>;
+  hipError_t e = hipFuncSetAttribute(kfn, hipFuncAttributeMaxDynamicSharedMemorySize, mk::kFaLds);
   if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: LDS opt-in failed: %s", fn, hipGetErrorString(e));
-  hipLaunchKernelGGL(mk::attention_causal_kernel, dim3((unsigned)(B * H * (S / mk::kFaQ))), dim3(512),
-                     mk::kFaLds, static_cast<hipStream_t>(stream), a);
+  const dim3 grid((unsigned)(B * H * (S / (rb2 ? 256 : 128))));
+  if (rb2)
+    hipLaunchKernelGGL(mk::attention_causal_kernel<2>, grid, dim3(512), mk::kFaLds, static_cast<hipStream_t>(stream), a);
+  else
+    hipLaunchKernelGGL(mk::attention_causal_kernel<1>, grid, dim3(512), mk::kFaLds, static_cast<hipStream_t>(stream), a);
   e = hipGetLastError();
   if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
   return MK_OK;

@@ -106,7 +106,7 @@ def _attention_ref(q, k, v, scale):
     return torch.softmax(s, dim=-1) @ v.double()
 
 
-@pytest.mark.parametrize("B,H,S", [(1, 1, 128), (2, 3, 256), (1, 2, 1024)])
+@pytest.mark.parametrize("B,H,S", [(1, 1, 128), (2, 3, 256), (1, 2, 1024), (1, 2, 384), (2, 2, 2048)])
 def test_attention_causal_fused(B, H, S):
     ops = _ops()
     g = torch.Generator().manual_seed(B * 7 + H * 3 + S)
@@ -120,6 +120,22 @@ def test_attention_causal_fused(B, H, S):
     # Row 0 of every head attends to key 0 only: exactly v[0] (bf16).
     y0 = y.reshape(B, S, H, 128)[:, 0]
     assert torch.equal(y0, v.reshape(B, H, S, 128)[:, :, 0].float())
+
+
+@pytest.mark.parametrize("B,H,S", [(2, 2, 512), (1, 4, 2048)])
+def test_attention_row_blocks_bit_identical(B, H, S, monkeypatch):
+    """32 query rows per wave (S % 256 == 0, the default there) and 16
+    (MK_ATTN_RB=1): every row sees the same tiles in the same order, so the
+    outputs are the same bits."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(S + H)
+    q, k, v = (torch.randn((B * H, S, 128), generator=g).to(torch.bfloat16).cuda() for _ in range(3))
+    scale = 1.0 / math.sqrt(128)
+    y2 = ops.attention_causal(q, k, v, B, H, scale)
+    monkeypatch.setenv("MK_ATTN_RB", "1")
+    y1 = ops.attention_causal(q, k, v, B, H, scale)
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
 
 
 def test_attention_fused_vs_composed_accuracy():
