@@ -610,10 +610,12 @@ def main():
     if not only or "int8" in only:
         r8 = bench_int8(torch, ops, args.steps, args.warmup)
         log(f"[bench] int8: {r8['sec_per_call'] * 1e6:.2f} us/call, {r8['gbs']:.1f} GB/s")
+        int8_traffic, int8_note = traffic_from_profiles("int8pc_wide_kernel_M16_K4096_N14336")
         secondary["int8_pc_dequant_matmul_M16"] = {
             "value": round(r8["gbs"], 2), "unit": "GB/s", "us_per_call": round(r8["sec_per_call"] * 1e6, 3),
             "roofline": {"bound": "hbm", "achieved": round(r8["gbs"], 2), "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(r8["gbs"] / HBM_PEAK_GBS, 4), "traffic": None},
+                         "unit": "GB/s", "frac": round(r8["gbs"] / HBM_PEAK_GBS, 4), "traffic": int8_traffic,
+                         "traffic_note": int8_note},
         }
 
     def want(name):
@@ -635,6 +637,9 @@ def main():
                              "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS,
                                           "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
                                           "traffic": None}}
+                    if M == 256 and fmt == "int4":
+                        qt, qn = traffic_from_profiles("qgemm_kernel_M256_K4096_N14336")
+                        entry["roofline"].update({"traffic": qt, "traffic_note": qn})
                 secondary[f"{fmt}_dequant_matmul_M{M}"] = entry
 
     if want("shard"):
