@@ -62,6 +62,7 @@ struct EventState {
   int code = MKRT_OK;
   std::string message;
   std::vector<std::pair<mkrt_event_callback, void*>> callbacks;
+  std::atomic<bool> done{false};  // `ready`, readable without the mutex
 
   void set(int c, const std::string& m) {
     std::vector<std::pair<mkrt_event_callback, void*>> cbs;
@@ -72,6 +73,7 @@ struct EventState {
       code = c;
       message = m;
       cbs.swap(callbacks);
+      done.store(true, std::memory_order_release);
     }
     cv.notify_all();
     for (auto& cb : cbs) cb.first(c == MKRT_OK ? nullptr : new mkrt_error{c, m}, cb.second);
@@ -81,9 +83,33 @@ struct EventState {
 std::shared_ptr<EventState> ready_state(int code = MKRT_OK, const std::string& msg = std::string()) {
   auto s = std::make_shared<EventState>();
   s->ready = true;
+  s->done.store(true, std::memory_order_relaxed);
   s->code = code;
   s->message = msg;
   return s;
+}
+
+// Completions are first polled for up to this long (MK_COMPLETION_SPIN_US,
+// default 200 us; 0 disables) before the waiting thread blocks: a blocking
+// wait's wake-up costs more than a short kernel takes.
+int64_t spin_us() {
+  static const int64_t v = [] {
+    const char* e = getenv("MK_COMPLETION_SPIN_US");
+    return e && *e ? std::max<int64_t>(0, atoll(e)) : 200;
+  }();
+  return v;
+}
+
+// Polls `ready()` until it holds or spin_us() has passed; true if it held.
+template <typename F>
+bool spin_until(F ready) {
+  const int64_t us = spin_us();
+  if (us <= 0) return ready();
+  const auto end = std::chrono::steady_clock::now() + std::chrono::microseconds(us);
+  for (int i = 0;; ++i) {
+    if (ready()) return true;
+    if ((i & 63) == 63 && std::chrono::steady_clock::now() >= end) return ready();
+  }
 }
 
 int64_t default_timeout_ms() {
@@ -215,7 +241,9 @@ struct mkrt_client {
         item = queue.front();
         queue.pop_front();
       }
-      const hipError_t e = hipEventSynchronize(item.first);
+      hipError_t e = hipErrorNotReady;
+      spin_until([&] { return (e = hipEventQuery(item.first)) != hipErrorNotReady; });
+      if (e == hipErrorNotReady) e = hipEventSynchronize(item.first);
       {
         std::lock_guard<std::mutex> g(ev_pool_mu);
         ev_pool.push_back(item.first);
@@ -291,6 +319,7 @@ mkrt_error* hip_error(const char* what, hipError_t e) {
 
 mkrt_error* await_state(const std::shared_ptr<EventState>& st, int64_t timeout_ms) {
   if (timeout_ms < 0) timeout_ms = default_timeout_ms();
+  spin_until([&] { return st->done.load(std::memory_order_acquire); });
   std::unique_lock<std::mutex> l(st->mu);
   if (!st->cv.wait_for(l, std::chrono::milliseconds(timeout_ms), [&] { return st->ready; }))
     return make_error(MKRT_DEADLINE_EXCEEDED, "completion not signalled within %lld ms (MK_COMPLETION_TIMEOUT_MS)",
