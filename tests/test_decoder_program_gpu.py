@@ -7,7 +7,21 @@ layer (oracle/decoder.py) at the workload's bf16 tolerance per token.
 The program rounds where jax's bf16 ops round (RMSNorm's x * x, the
 scores, softmax's exp and quotient) and the oracle rounds once per block,
 so the comparison is the bf16 measure max |err| / max |ref| per row, not an
-elementwise one."""
+elementwise one.
+
+The oracle's weight convention follows the route the plan takes for the
+layer's row count: below 128 rows the streaming dequant-matmul kernels apply
+(q - z) * s exactly (exact_weights=True); from 128 rows the many-row kernels
+(the fused qgemm kernel, or the dequantise-then-GEMM pass) round each
+dequantised weight to bf16 once, as XLA:CPU rounds a bf16 (q - z) * s.  The
+two conventions alone move a 4-layer stack by up to ~4e-2 per row, so the
+oracle must use the one the kernels use."""
+
+QMM_MANY_ROWS = 128  # qmatmul.hip kQgMinRows: from here the dequantised weight is rounded to bf16
+
+
+def _exact_route(rows):
+    return rows < QMM_MANY_ROWS
 
 import numpy as np
 import pytest
@@ -16,7 +30,7 @@ from mi355x import programs as P
 from mi355x import runtime as rt
 from mi355x import synthetic
 from oracle import decoder as odec
-from oracle.bf16 import bf16_bits_to_f32
+from oracle.bf16 import bf16_bits_to_f32, round_bf16
 
 from _gpu import BF16_RTOL
 
@@ -55,7 +69,7 @@ def _run_layer(client, B, S, hidden, H, D, F, seed):
 def _check_rows(y, x, w, B, S, hidden, H, D, pos, batches):
     x3 = bf16_bits_to_f32(x).reshape(B, S, hidden)
     for b in batches:
-        ref = odec.layer_rows(x3[b], pos, w, H, D)
+        ref = odec.layer_rows(x3[b], pos, w, H, D, exact_weights=_exact_route(B * S))
         o = y[b, pos].astype(np.float64)
         assert np.isfinite(o).all()
         row_rel = np.abs(o - ref).max(axis=1) / np.abs(ref).max(axis=1)
@@ -196,7 +210,7 @@ def test_decoder_stack_vs_oracle(client):
     for b in range(B):
         ref = x3[b].astype(np.float64)
         for w in ws:
-            ref = odec.layer_rows(ref, pos, w, H, D)
+            ref = odec.layer_rows(ref, pos, w, H, D, exact_weights=_exact_route(B * S))
         row_rel = np.abs(y[b] - ref).max(axis=1) / np.abs(ref).max(axis=1)
         print(f"[decoder-program] stack batch {b}: worst row rel err {row_rel.max():.3e}", flush=True)
         assert row_rel.max() <= BF16_RTOL, (b, row_rel.max())
@@ -241,3 +255,125 @@ def test_swiglu_pair_program_bit_identical_and_vs_oracle(client, monkeypatch, fm
     y = bf16_bits_to_f32(outs[0]).astype(np.float64)
     row_rel = np.abs(y - ref).max(axis=1) / np.abs(ref).max(axis=1)
     assert row_rel.max() <= BF16_RTOL, row_rel.max()
+
+
+def _hand_fused_weights(ws):
+    """The synthetic layer weights (numpy bits) as the hand-fused forward's
+    LayerWeights on cuda:0."""
+    import torch
+    from mi355x import decoder
+
+    def bf16(bits):
+        return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).cuda()
+
+    def int4(w):
+        packed, s, z = w
+        return decoder.Int4Weight(torch.from_numpy(packed).cuda(), bf16(s), torch.from_numpy(z).cuda())
+
+    layers = []
+    for w in ws:
+        lw = decoder.LayerWeights(g_attn=bf16(w["g_attn"]), w_qkv=int4(w["w_qkv"]), w_o=int4(w["w_o"]),
+                                  g_mlp=bf16(w["g_mlp"]), w_gate=int4(w["w_gate"]), w_up=int4(w["w_up"]),
+                                  w_down=int4(w["w_down"]))
+        lw.w_gateup = decoder.interleave_int4(lw.w_gate, lw.w_up)
+        layers.append(lw)
+    return layers
+
+
+def _oracle_stack(x_rows, ws, H, D, exact):
+    """The oracle's layer stack on one sequence prefix."""
+    ref = x_rows
+    for w in ws:
+        ref = odec.layer_rows(ref, np.arange(len(x_rows)), w, H, D, exact_weights=exact)
+    return ref
+
+
+def _row_measures(got, ref):
+    """(per-row max measure max|err|/max|ref|, per-row relative L2, normwise
+    over the whole block)."""
+    d = got - ref
+    return (np.abs(d).max(axis=1) / np.abs(ref).max(axis=1),
+            np.linalg.norm(d, axis=1) / np.linalg.norm(ref, axis=1),
+            np.abs(d).max() / np.abs(ref).max())
+
+
+def test_decoder_stack_full_config(client):
+    """The 4-layer forward bench.py times: programs.decoder_stack(4, 4, 2048,
+    2048, 16, 128, 8192) compiled from its StableHLO and run once.
+
+    * every output finite and every token changed by the stack;
+    * batches 0 and 3 against the oracle's 4 layers on the position prefix
+      [0, P) (causal attention makes a prefix self-contained, so the oracle
+      needs only P rows per layer), and the hand-fused forward
+      (mi355x/decoder.forward) on the same weights held to the same checks:
+      - normwise over the block, max|err| / max|ref| <= 2e-2 (the workload's
+        bf16 measure);
+      - per row (max measure and relative L2) within the oracle's own
+        sensitivity.  This random-init stack amplifies perturbations about
+        11x per layer: moving 1 % of the input elements by one bf16 ulp moves
+        the oracle's 4-layer output by ~2e-2 per row (median) and ~4e-2
+        (worst), so any evaluation that rounds to bf16 at other points than
+        the oracle carries that much.  The test measures this spread live
+        (the oracle run twice, on x and on x with 1 % of its elements one ulp
+        up) and asserts each GPU row within max(2e-2, the spread's worst
+        row);
+    * every row of the program within twice that bound of the hand-fused
+      forward (each is within the bound of the exact stack; triangle
+      inequality)."""
+    import torch
+    from mi355x import decoder
+
+    L, B, S, hidden, H, D, F = 4, 4, 2048, 2048, 16, 128, 8192
+    P_ = 192
+    x, ws, cos, sin = synthetic.decoder_stack_case(np.random.default_rng(43), L, B, S, hidden, H, D, F)
+    print(f"[decoder-program] full stack L={L} B={B} S={S} hidden={hidden}", flush=True)
+    exe = client.compile(P.decoder_stack(L, B, S, hidden, H, D, F))
+    assert exe.plan.count("attention_causal") == L
+    args = [client.buffer(a, rt.BF16) if is_bf16 else client.buffer(a)
+            for a, is_bf16 in synthetic.decoder_stack_arguments(x, ws, cos, sin)]
+    outs, done = exe.execute(args)
+    done.wait()
+    y = bf16_bits_to_f32(outs[0].to_numpy()).reshape(B, S, hidden).astype(np.float64)
+    for b_ in args + outs:
+        b_.close()
+    exe.close()
+    x3 = bf16_bits_to_f32(x).reshape(B, S, hidden).astype(np.float64)
+    assert np.isfinite(y).all()
+    changed = np.any(y != x3, axis=2)
+    assert changed.all(), f"{int((~changed).sum())} tokens unchanged by the stack"
+
+    print("[decoder-program] full stack: hand-fused forward on the same weights", flush=True)
+    cfg = decoder.DecoderConfig(layers=L, hidden=hidden, heads=H, head_dim=D, ffn=F, batch=B, seq=S)
+    buf = decoder.Buffers(cfg)
+    buf.x.copy_(torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).reshape(B * S, hidden).cuda())
+    decoder.forward(cfg, _hand_fused_weights(ws), buf, torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda())
+    torch.cuda.synchronize()
+    hf = buf.x.float().cpu().numpy().reshape(B, S, hidden).astype(np.float64)
+
+    exact = _exact_route(B * S)
+    bounds = []
+    for b in (0, B - 1):
+        print(f"[decoder-program] full stack: oracle, batch {b}, positions [0, {P_})", flush=True)
+        x0 = x3[b, :P_]
+        ref = _oracle_stack(x0, ws, H, D, exact)
+        up = np.random.default_rng(100 + b).random(x0.shape) < 0.01
+        xp = x0.copy()
+        xp[up] = round_bf16(x0[up] * (1 + 2.0 ** -7))
+        sp_max, sp_l2, _ = _row_measures(_oracle_stack(xp, ws, H, D, exact), ref)
+        bound_max, bound_l2 = max(BF16_RTOL, sp_max.max()), max(BF16_RTOL, sp_l2.max())
+        bounds.append(bound_max)
+        print(f"[decoder-program] oracle spread (1% of inputs +1 ulp), batch {b}: per-row max measure worst "
+              f"{sp_max.max():.3e} median {np.median(sp_max):.3e}; L2 worst {sp_l2.max():.3e}", flush=True)
+        for name, got in (("program", y), ("hand-fused", hf)):
+            rr, l2, nw = _row_measures(got[b, :P_], ref)
+            print(f"[decoder-program] full stack {name} vs oracle, batch {b}: normwise {nw:.3e}; per-row max "
+                  f"measure worst {rr.max():.3e} median {np.median(rr):.3e} (bound {bound_max:.3e}); per-row L2 "
+                  f"worst {l2.max():.3e} (bound {bound_l2:.3e})", flush=True)
+            assert nw <= BF16_RTOL, (name, b, nw)
+            assert rr.max() <= bound_max, (name, b, int(rr.argmax()), rr.max())
+            assert l2.max() <= bound_l2, (name, b, int(l2.argmax()), l2.max())
+
+    row_rel = np.abs(y - hf).max(axis=2) / np.abs(hf).max(axis=2)
+    print(f"[decoder-program] full stack vs hand-fused, all {row_rel.size} rows: per-row max measure worst "
+          f"{row_rel.max():.3e}, median {np.median(row_rel):.3e} (bound {2 * max(bounds):.3e})", flush=True)
+    assert row_rel.max() <= 2 * max(bounds), (np.unravel_index(int(row_rel.argmax()), row_rel.shape), row_rel.max())

@@ -588,16 +588,19 @@ def test_decoder_layer_zero_weights_is_identity():
     np.testing.assert_array_equal(out, x)
 
 
-def test_decoder_layer_rows_brute_force():
+@pytest.mark.parametrize("exact", [False, True])
+def test_decoder_layer_rows_brute_force(exact):
     """The subset evaluation equals a plain whole-sequence evaluation written
-    with explicit loops over heads and positions."""
+    with explicit loops over heads and positions, with the dequantised
+    weights rounded to bf16 or (exact_weights) exact."""
     from oracle import decoder
     rng = np.random.default_rng(42)
     S, hidden, H, D, F = 5, 128, 2, 64, 192
     x = bf16.round_bf16(rng.standard_normal((S, hidden)))
     w = _tiny_layer_weights(rng, hidden, H * D, F)
     r = bf16.round_bf16
-    deq = {n: quant.int4_g64_dequant(*w[n]).astype(np.float64) for n in ("w_qkv", "w_o", "w_gate", "w_up", "w_down")}
+    names = ("w_qkv", "w_o", "w_gate", "w_up", "w_down")
+    deq = {n: quant.int4_g64_dequant(*w[n], round_to_bf16=not exact).astype(np.float64) for n in names}
     g1 = bf16.bf16_bits_to_f32(w["g_attn"]).astype(np.float64)
     g2 = bf16.bf16_bits_to_f32(w["g_mlp"]).astype(np.float64)
     cos, sin = decoder.rope_tables(S, D)
@@ -624,5 +627,25 @@ def test_decoder_layer_rows_brute_force():
         act = r(r(gg * r(1 / (1 + np.exp(-gg.astype(np.float64))))) * uu)
         ref[t] = r(x1 + r(act @ deq["w_down"]))
     pos = np.array([4, 0, 2])
-    out = decoder.layer_rows(x, pos, w, heads=H, head_dim=D)
+    out = decoder.layer_rows(x, pos, w, heads=H, head_dim=D, exact_weights=exact)
     np.testing.assert_allclose(out, ref[pos], rtol=2 ** -7, atol=1e-6)
+
+
+def test_decoder_exact_weights_only_change_the_weight_rounding():
+    """With power-of-two scales every (q - z) * s is a bf16 value, so the
+    exact and bf16-rounded weight conventions give identical layers; with
+    general scales they differ (the flag is not ignored)."""
+    from oracle import decoder
+    rng = np.random.default_rng(44)
+    S, hidden, H, D, F = 4, 128, 2, 64, 192
+    x = bf16.round_bf16(rng.standard_normal((S, hidden)))
+    w = _tiny_layer_weights(rng, hidden, H * D, F)
+    pos = np.arange(S)
+    general = [decoder.layer_rows(x, pos, w, heads=H, head_dim=D, exact_weights=e) for e in (False, True)]
+    assert not np.array_equal(general[0], general[1])
+    for n in ("w_qkv", "w_o", "w_gate", "w_up", "w_down"):
+        p_, s_, z_ = w[n]
+        pow2 = 2.0 ** rng.integers(-9, -6, size=s_.shape)
+        w[n] = (p_, bf16.f32_to_bf16_bits(pow2.astype(np.float32)), z_)
+    same = [decoder.layer_rows(x, pos, w, heads=H, head_dim=D, exact_weights=e) for e in (False, True)]
+    np.testing.assert_array_equal(same[0], same[1])

@@ -79,7 +79,7 @@ def test_plumbing_through_the_table(tmp_path):
     _run(["run", PJRT, str(prog), str(out), _spec(tmp_path, "a", a, F32), _spec(tmp_path, "b", b, F32)])
     y = np.frombuffer(out.read_bytes(), dtype=np.float32)
     ref = np.tanh(a.astype(np.float64) @ b.astype(np.float64)).sum(axis=1)
-    assert np.max(np.abs(y - ref)) <= 1e-5 * n
+    assert_rel_close(y, ref, F32_RTOL, "plumbing via PJRT", elem=False)
 
 
 def test_softmax_through_the_table(tmp_path):

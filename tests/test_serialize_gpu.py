@@ -70,7 +70,7 @@ def _oracle_check(name, arrays, out):
     else:
         a, b = arrays
         ref = np.tanh(a.astype(np.float64) @ b.astype(np.float64)).sum(axis=1)
-        assert np.max(np.abs(out - ref)) <= 1e-5 * a.shape[0], name
+        assert_rel_close(out, ref, F32_RTOL, name, elem=False)
 
 
 @pytest.mark.parametrize("name,text,arrays", _cases(), ids=[c[0] for c in _cases()])

@@ -50,8 +50,20 @@ def test_noalloc_rejects_shapes_beyond_the_array():
     L = _lib.lib()
     M, K, N = 4096, 4096, 14336  # dequantise-then-GEMM: 117 MB of workspace
     assert L.mk_qmatmul_workspace_bytes(_lib.MK_QFMT_INT4_G64, M, K, N) > 8 << 20
-    fake = 0x1000  # never dereferenced: the size check fails first
-    rc = L.mk_int4g64_matmul_bf16_noalloc(fake, fake, fake, fake, fake, M, K, N, None)
+    # Real device buffers of the full shapes (contents unused: the size check
+    # fails before any launch).  Should that check ever regress, the call
+    # reads and writes valid memory and fails the asserts below; it cannot
+    # touch an address that was never allocated.
+    dev0 = dict(device="cuda:0")
+    x = torch.empty((M, K), dtype=torch.bfloat16, **dev0)
+    w = torch.empty((K // 2, N), dtype=torch.uint8, **dev0)
+    s = torch.empty((K // 64, N), dtype=torch.bfloat16, **dev0)
+    z = torch.empty((K // 64, N), dtype=torch.uint8, **dev0)
+    y = torch.empty((M, N), dtype=torch.bfloat16, **dev0)
+    stream = torch.cuda.current_stream().cuda_stream
+    rc = L.mk_int4g64_matmul_bf16_noalloc(x.data_ptr(), w.data_ptr(), s.data_ptr(), z.data_ptr(), y.data_ptr(),
+                                          M, K, N, stream)
+    torch.cuda.synchronize()
     assert rc == _lib.MK_EWORKSPACE
     assert b"no-allocation" in L.mk_last_error()
 
