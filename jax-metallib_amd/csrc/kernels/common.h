@@ -63,6 +63,11 @@ __device__ __forceinline__ float load_agent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Raw buffer resources and the cache-policy operand of the buffer builtins.
+constexpr uint32_t kBufWord3 = 0x00020000u;  // raw-buffer resource word 3 (gfx9 family)
+constexpr int kSc0 = 1;                      // cache policy sc0: the access misses the CU's L1
+constexpr int kSc1 = 16;                     // cache policy sc1: device scope (past the XCD's L2)
+
 // Logical workgroup id that keeps runs of consecutive ids on one XCD.  The
 // dispatcher hands workgroup b to XCD b % 8; when the grid is a multiple of 8
 // this maps the b-th workgroup to logical id (b % 8) * (n / 8) + b / 8, so the

@@ -57,8 +57,6 @@ constexpr int kQgCols = 128;
 constexpr int kQgAhead = 3;                // weight loads run this many steps ahead
 constexpr int kQgBuf = 64 * kQgCols * 2;   // bf16 [64 k][128 n] tile
 constexpr int kQgPart = kQgRows * kQgCols;  // f32 per partial tile
-constexpr uint32_t kBufWord3 = 0x00020000u;  // raw-buffer resource word 3 (gfx9 family)
-constexpr int kSc1 = 16;                   // buffer cache policy: sc1 (device scope)
 
 struct QgArgs {
   const uint16_t* x;

@@ -42,6 +42,8 @@
 #include "epilogue.h"
 
 #include <algorithm>
+#include <atomic>
+#include <cstring>
 
 namespace mk {
 
@@ -63,6 +65,7 @@ struct QArgs {
   uint32_t* cnt;     // wide kernel, ks > 1: per-tile arrival counters (zero between calls)
   const uint16_t* aux;  // epilogue operand (bf16 [M, N]) or null
   int epi;              // MK_EPI_* applied by every kernel's bf16 store
+  int xch_local;        // wide int4 kernel: split-K exchange inside one XCD's L2 (see wide_finish)
 };
 
 // Stage this wave's x block [16 rows][kwave] into LDS as 16-byte MFMA A
@@ -666,30 +669,58 @@ __device__ __forceinline__ void lds_scale_zero(uint32_t sa, uint32_t za, u32x2 (
 
 // y quads of this thread = the KS split-K partials (this workgroup's among
 // them, already acknowledged) summed in k order.
-template <int KS>
-__device__ __forceinline__ void wide_sum_partials(const float* tile_part, f32x4 (&own)[2]) {
-  f32x4 v[2][KS];
-  const float* src[2][KS];
+template <int NW, int KS>
+__device__ __forceinline__ void wide_sum_partials(const float* tile_part, f32x4 (&own)[16 / NW]) {
+  constexpr int IT = 16 / NW;  // quads per thread: 16 rows x 64 quads over NW waves
+  f32x4 v[IT][KS];
+  const float* src[IT][KS];
 #pragma unroll
-  for (int it = 0; it < 2; ++it)
+  for (int it = 0; it < IT; ++it)
 #pragma unroll
     for (int k2 = 0; k2 < KS; ++k2)
-      src[it][k2] = tile_part + (size_t)k2 * kQRows * kWideTN + 4 * (threadIdx.x + 8 * kWave * it);
+      src[it][k2] = tile_part + (size_t)k2 * kQRows * kWideTN + 4 * (threadIdx.x + NW * kWave * it);
   if constexpr (KS == 2) {
-    ld4_sc1(src[0][0], src[0][1], src[1][0], src[1][1], v[0][0], v[0][1], v[1][0], v[1][1]);
+#pragma unroll
+    for (int it = 0; it < IT; it += 2)
+      ld4_sc1(src[it][0], src[it][1], src[it + 1][0], src[it + 1][1], v[it][0], v[it][1], v[it + 1][0],
+              v[it + 1][1]);
   } else {
 #pragma unroll
-    for (int it = 0; it < 2; ++it)
+    for (int it = 0; it < IT; ++it)
 #pragma unroll
       for (int k2 = 0; k2 < KS; k2 += 4)
         ld4_sc1(src[it][k2], src[it][k2 + 1], src[it][k2 + 2], src[it][k2 + 3], v[it][k2], v[it][k2 + 1],
                 v[it][k2 + 2], v[it][k2 + 3]);
   }
 #pragma unroll
-  for (int it = 0; it < 2; ++it) {
+  for (int it = 0; it < IT; ++it) {
     f32x4 acc = v[it][0];
 #pragma unroll
     for (int k2 = 1; k2 < KS; ++k2) acc += v[it][k2];
+    own[it] = acc;
+  }
+}
+
+#ifndef XCH_STORE_POLICY
+#define XCH_STORE_POLICY kSc1
+#endif
+// The same sum for the exchange inside one XCD's L2: loads that miss only
+// the CU's L1 (sc0), through the tile's buffer resource `rs`.
+template <int NW, int KS>
+__device__ __forceinline__ void wide_sum_partials_l2(__amdgpu_buffer_rsrc_t rs, f32x4 (&own)[16 / NW]) {
+  constexpr int IT = 16 / NW;
+  u32x4 v[IT][KS];
+#pragma unroll
+  for (int it = 0; it < IT; ++it)
+#pragma unroll
+    for (int k2 = 0; k2 < KS; ++k2)
+      v[it][k2] = __builtin_amdgcn_raw_buffer_load_b128(
+          rs, (k2 * kQRows * kWideTN + 4 * (threadIdx.x + NW * kWave * it)) * 4, 0, kSc0);
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    f32x4 acc = __builtin_bit_cast(f32x4, v[it][0]);
+#pragma unroll
+    for (int k2 = 1; k2 < KS; ++k2) acc += __builtin_bit_cast(f32x4, v[it][k2]);
     own[it] = acc;
   }
 }
@@ -699,14 +730,15 @@ __device__ __forceinline__ void wide_sum_partials(const float* tile_part, f32x4 
 // tile's workgroups to arrive sums them in k order); store bf16 y, times the
 // int8 per-channel scale when FMT8.  Every DMA of the calling wave must have
 // landed: y is spilled into its own LDS region, over its ring.
-template <bool FMT8>
+template <int NW, bool FMT8>
 __device__ __forceinline__ void wide_finish(const QArgs& a, unsigned char* smem, unsigned char* wl,
                                             const f32x4 (&y)[kWideTN / 16], int tile, int ksi, int rb, int m0,
                                             int mrows, int n0, int c, int j) {
   constexpr int TN = kWideTN, NB = TN / 16;
+  constexpr int IT = 16 / NW;  // output quads per thread (16 rows x 64 quads)
   const size_t N = (size_t)a.N;
   const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
-  // Sum the 8 waves: each spills y as [16 m][TN] f32 (padded rows) into its
+  // Sum the NW waves: each spills y as [16 m][TN] f32 (padded rows) into its
   // own region; lane (c, j) holds column 16b + c, rows 4j..4j+3.
   float* red = reinterpret_cast<float*>(wl);
 #pragma unroll
@@ -714,23 +746,60 @@ __device__ __forceinline__ void wide_finish(const QArgs& a, unsigned char* smem,
 #pragma unroll
     for (int i = 0; i < 4; ++i) red[(4 * j + i) * kWideRedStride + 16 * b + c] = y[b][i];
   __syncthreads();
-  f32x4 own[2];
+  f32x4 own[IT];
 #pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int q = threadIdx.x + 8 * kWave * it;  // quad index: 16 rows x 64 quads
+  for (int it = 0; it < IT; ++it) {
+    const int q = threadIdx.x + NW * kWave * it;  // quad index: 16 rows x 64 quads
     const int m = q >> 6, n = 4 * (q & 63);
     f32x4 acc = zero4;
 #pragma unroll
-    for (int w = 0; w < 8; ++w)
+    for (int w = 0; w < NW; ++w)
       acc += *reinterpret_cast<const f32x4*>(smem + w * a.wave_lds + (m * kWideRedStride + n) * 4);
     own[it] = acc;
   }
   const int ntiles = a.N / TN;
-  if (a.ks > 1) {
+  if (a.ks > 1 && a.xch_local) {
+    // Every workgroup of this tile runs on this XCD (the host checked that
+    // the grid deals each tile's ks workgroups to one XCD), so the exchange
+    // stays in its L2: plain stores (acknowledged by the L2), a
+    // workgroup-scope atomic (performed in the L2), and loads that miss
+    // only the CU's own L1 (sc0).  The ordering argument is the
+    // device-scope one below with the L2 as the common coherence point.
+    const size_t tbase = ((size_t)(rb * ntiles + tile) * a.ks) * kQRows * TN;
+    float* tp = a.part + tbase;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(tp, 0, a.ks * kQRows * TN * 4, kBufWord3);
+#pragma unroll
+    for (int it = 0; it < IT; ++it)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, own[it]), rs,
+                                             (ksi * kQRows * TN + 4 * (threadIdx.x + NW * kWave * it)) * 4, 0,
+                                             XCH_STORE_POLICY);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // every partial store acknowledged
+    __syncthreads();  // (also: every wave is done reading the spills)
+    volatile uint32_t* flag = reinterpret_cast<volatile uint32_t*>(smem);
+    if (threadIdx.x == 0) {
+      uint32_t* ctr = a.cnt + rb * ntiles + tile;
+      asm volatile("" : "+v"(ctr));  // per-lane address: a vector atomic
+      const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      const uint32_t last = old == (uint32_t)(a.ks - 1);
+      if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      *flag = last;
+    }
+    __syncthreads();
+    if (!*flag) return;
+    // Every partial (this workgroup's own included, as in the device-scope
+    // path), all loads in flight together, then summed in k order.
+    switch (a.ks) {
+      case 2: wide_sum_partials_l2<NW, 2>(rs, own); break;
+      case 4: wide_sum_partials_l2<NW, 4>(rs, own); break;
+      default: wide_sum_partials_l2<NW, 8>(rs, own); break;
+    }
+  } else if (a.ks > 1) {
     const size_t tbase = ((size_t)(rb * ntiles + tile) * a.ks) * kQRows * TN;
     // Device-coherent stores of the partial, acknowledged.
     float* dst = a.part + tbase + (size_t)ksi * kQRows * TN + 4 * threadIdx.x;
-    st2_sc1_wait(dst, own[0], dst + 4 * 8 * kWave, own[1]);
+#pragma unroll
+    for (int it = 0; it < IT; it += 2)
+      st2_sc1_wait(dst + 4 * NW * kWave * it, own[it], dst + 4 * NW * kWave * (it + 1), own[it + 1]);
     __syncthreads();  // (also: every wave is done reading the spills)
     // The flag lives in dynamic LDS: a static __shared__ would shift the
     // dynamic base off the 256-byte alignment the swizzled addressing needs.
@@ -748,14 +817,14 @@ __device__ __forceinline__ void wide_finish(const QArgs& a, unsigned char* smem,
     // Device-coherent 16-byte loads (sc1: miss the local L2) of every
     // partial, then the sum in k order.
     switch (a.ks) {
-      case 2: wide_sum_partials<2>(a.part + tbase, own); break;
-      case 4: wide_sum_partials<4>(a.part + tbase, own); break;
-      default: wide_sum_partials<8>(a.part + tbase, own); break;
+      case 2: wide_sum_partials<NW, 2>(a.part + tbase, own); break;
+      case 4: wide_sum_partials<NW, 4>(a.part + tbase, own); break;
+      default: wide_sum_partials<NW, 8>(a.part + tbase, own); break;
     }
   }
 #pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int q = threadIdx.x + 8 * kWave * it;
+  for (int it = 0; it < IT; ++it) {
+    const int q = threadIdx.x + NW * kWave * it;
     const int m = q >> 6, n = n0 + 4 * (q & 63);
     if (m >= mrows) continue;
     if (FMT8) own[it] *= *reinterpret_cast<const f32x4*>(static_cast<const float*>(a.s) + n);
@@ -763,8 +832,8 @@ __device__ __forceinline__ void wide_finish(const QArgs& a, unsigned char* smem,
   }
 }
 
-template <int G, int R>  // G 64-k groups per wave; ring of R 32-k steps
-__global__ __launch_bounds__(8 * kWave) void int4g64_wide_kernel(QArgs a) {
+template <int NW, int G, int R>  // NW waves; G 64-k groups per wave; ring of R 32-k steps
+__global__ __launch_bounds__(NW * kWave) void int4g64_wide_kernel(QArgs a) {
   constexpr int TN = kWideTN, NB = TN / 16, S = 2 * G;
   constexpr int DPS = TN / 64;                             // weight DMAs per step
   constexpr int SB = ((G * TN * 2 + 1023) / 1024) * 1024;  // scale block bytes
@@ -894,7 +963,7 @@ __global__ __launch_bounds__(8 * kWave) void int4g64_wide_kernel(QArgs a) {
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  wide_finish<false>(a, smem, wl, y, tile, ksi, rb, m0, mrows, n0, c, j);
+  wide_finish<NW, false>(a, smem, wl, y, tile, ksi, rb, m0, mrows, n0, c, j);
 }
 
 // ---------------------------------------------------------------------------
@@ -1016,7 +1085,7 @@ __global__ __launch_bounds__(8 * kWave) void int8pc_wide_kernel(QArgs a) {
   f32x4 y[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) y[b] = acc[b] - 128.f * xs;
-  wide_finish<true>(a, smem, wl, y, tile, ksi, rb, m0, mrows, n0, c, j);
+  wide_finish<8, true>(a, smem, wl, y, tile, ksi, rb, m0, mrows, n0, c, j);
 }
 
 template <int S, int R>  // 32-k steps per wave, ring of R steps (3 KB each)
@@ -1234,23 +1303,33 @@ bool plan_stream(int fmt, int64_t K, int64_t N, QPlan* p) {
 // the fewest splits that give >= 192 workgroups (the most the 64 KB counter
 // region and G >= 1 allow).  Grids below 128 workgroups stay on the
 // 64-column kernels.  MK_QMM_WIDE=0 disables it.
-// Ring depth (32-k steps in flight per wave) of the wide kernel with G
-// groups per wave.  At the headline (G = 2, 4 steps per wave) a 2-step ring
-// measured 13.3 us against 13.7 us for 3 steps and 13.6 us for all 4 in
-// flight at once.
-constexpr int wide_ring(int G) { return G == 4 ? 4 : G == 2 ? 2 : 2 * G; }
+// Ring depth (32-k steps in flight per wave) of the wide kernel with NW
+// waves of G groups.  At the headline with 8 waves (G = 2, 4 steps per wave)
+// a 2-step ring measured 13.3 us against 13.7 us for 3 steps and 13.6 us
+// for all 4 in flight at once.  MK_QMM_WIDE_RING overrides it (sweeps).
+constexpr int kWideWaves = 8;
+int wide_ring(int nw, int G) {
+  const int r = env_int("MK_QMM_WIDE_RING", 0);
+  if (r >= 2 && r <= 2 * G && (r == 2 || r == 4 || r == 8)) return r;
+  if (nw == 4) return G == 4 ? 4 : 2 * G;
+  return G == 4 ? 4 : G == 2 ? 2 : 2 * G;
+}
 
 bool plan_wide(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p) {
   const char* env = getenv("MK_QMM_WIDE");
-  if (fmt != MK_QFMT_INT4_G64 || N % mk::kWideTN != 0 || K % 512 != 0 || (env && env[0] == '0')) return false;
+  if (fmt != MK_QFMT_INT4_G64 || N % mk::kWideTN != 0 || (env && env[0] == '0')) return false;
+  const int nw = env_int("MK_QMM_WIDE_NW", kWideWaves);
+  if (nw != 4 && nw != 8) return false;
+  const int64_t kunit = (int64_t)nw * 64;  // k per workgroup and group-per-wave
+  if (K % kunit != 0) return false;
   const int ntiles = (int)(N / mk::kWideTN);
   const int rb = (int)((M + mk::kQRows - 1) / mk::kQRows);
   const int ks_env = env_int("MK_QMM_KS", 0);
   int best = 0;
   for (int ks = 1; ks <= 8; ks *= 2) {
     if (ks_env > 0 && ks != ks_env) continue;
-    if (K % ((int64_t)ks * 512) != 0) break;
-    const int64_t G = K / ((int64_t)ks * 512);
+    if (K % ((int64_t)ks * kunit) != 0) break;
+    const int64_t G = K / ((int64_t)ks * kunit);
     if (G > 4) continue;
     if (G != 1 && G != 2 && G != 4) continue;
     if (ks > 1 && (int64_t)rb * ntiles > mk::kWideCounters) break;
@@ -1258,20 +1337,20 @@ bool plan_wide(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p) {
     if ((int64_t)ntiles * rb * ks >= 192) break;
   }
   if (best == 0 || (int64_t)ntiles * rb * best < 128) return false;
-  const int G = (int)(K / ((int64_t)best * 512));
-  const int R = wide_ring(G);
+  const int G = (int)(K / ((int64_t)best * kunit));
+  const int R = wide_ring(nw, G);
   const int sb = ((G * mk::kWideTN * 2 + 1023) / 1024) * 1024, zb = ((G * mk::kWideTN + 1023) / 1024) * 1024;
   int wl = R * mk::kWideSlot + sb + zb;
   wl = std::max(wl, mk::kQRows * mk::kWideRedStride * 4);
   wl = (wl + 255) & ~255;
   p->ks = best;
-  p->nw = 8;
+  p->nw = nw;
   p->ntiles = ntiles;
   p->rowblocks = rb;
   p->wide_groups = G;
   p->kwave = 64 * G;
   p->wave_lds = wl;
-  p->lds_bytes = (size_t)8 * wl;
+  p->lds_bytes = (size_t)nw * wl;
   p->part_bytes = best > 1 ? (int64_t)mk::kWidePartOffset + (int64_t)rb * ntiles * best * mk::kQRows * mk::kWideTN * 4
                            : 0;
   return p->lds_bytes <= kMaxLds;
@@ -1394,14 +1473,23 @@ hipError_t lds_opt_in(const void* fn, size_t bytes) {
 
 hipError_t launch_reduce(int fmt, const mk::QArgs& a, hipStream_t st);
 
-template <int G>
-hipError_t launch_wide(const mk::QArgs& a, const QPlan& p, hipStream_t st) {
-  constexpr int R = wide_ring(G);
-  dim3 grid(p.ntiles * p.ks, p.rowblocks), block(8 * mk::kWave);
-  hipError_t e = lds_opt_in((const void*)mk::int4g64_wide_kernel<G, R>, p.lds_bytes);
+template <int NW, int G, int R>
+hipError_t launch_wide_nwgr(const mk::QArgs& a, const QPlan& p, hipStream_t st) {
+  dim3 grid(p.ntiles * p.ks, p.rowblocks), block(NW * mk::kWave);
+  hipError_t e = lds_opt_in((const void*)mk::int4g64_wide_kernel<NW, G, R>, p.lds_bytes);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((mk::int4g64_wide_kernel<G, R>), grid, block, p.lds_bytes, st, a);
+  hipLaunchKernelGGL((mk::int4g64_wide_kernel<NW, G, R>), grid, block, p.lds_bytes, st, a);
   return hipGetLastError();
+}
+
+template <int NW, int G>
+hipError_t launch_wide(const mk::QArgs& a, const QPlan& p, hipStream_t st) {
+  switch (wide_ring(NW, G)) {
+    case 2: return launch_wide_nwgr<NW, G, 2>(a, p, st);
+    case 4: if constexpr (2 * G >= 4) return launch_wide_nwgr<NW, G, 4>(a, p, st); break;
+    case 8: if constexpr (2 * G >= 8) return launch_wide_nwgr<NW, G, 8>(a, p, st); break;
+  }
+  return hipErrorInvalidValue;
 }
 
 template <int S>
@@ -1456,6 +1544,48 @@ hipError_t launch_reduce(int fmt, const mk::QArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+// Workgroup placement.  The wide int4 kernel's split-K exchange can stay in
+// one XCD's L2 when every workgroup of a tile runs on the same XCD.  In the
+// GPU's single-partition mode the dispatcher deals workgroups to the 8 XCDs
+// round-robin (linear workgroup id i on XCD i % 8); with gridDim.x % 8 == 0
+// and (gridDim.x / 8) % ks == 0, xcd_logical_id then gives each tile's ks
+// workgroups one XCD.  That dealing is checked once per device, outside graph
+// capture, by a probe launch of the same grid shape that compares each
+// workgroup's hardware XCC id with its linear id; until a probe has passed
+// (and under MK_QMM_XCH=device) the exchange goes through device scope.
+__global__ void xcd_probe_kernel(uint32_t* bad) {
+  uint32_t xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  const uint32_t lin = blockIdx.x + blockIdx.y * gridDim.x;
+  if (threadIdx.x == 0 && (xcc & 7u) != (lin & 7u)) atomicOr(bad, 1u);
+}
+
+constexpr int kXcdMaxDevices = 64;
+std::atomic<int> g_xcd_state[kXcdMaxDevices];  // 0 unknown, 1 round-robin, 2 other
+
+// True when workgroups of `grid` are dealt round-robin to the 8 XCDs on the
+// current device.  Probes (synchronously on `st`, using the first word of
+// `word` as scratch) the first time it is asked outside graph capture.
+bool xcd_round_robin(dim3 grid, hipStream_t st, uint32_t* word) {
+  const char* env = getenv("MK_QMM_XCH");
+  if (env && std::strcmp(env, "device") == 0) return false;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kXcdMaxDevices) return false;
+  const int state = g_xcd_state[dev].load(std::memory_order_acquire);
+  if (state != 0) return state == 1;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
+  uint32_t bad = 1;
+  if (hipMemsetAsync(word, 0, sizeof(uint32_t), st) != hipSuccess) return false;
+  hipLaunchKernelGGL(xcd_probe_kernel, grid, dim3(64), 0, st, word);
+  if (hipGetLastError() != hipSuccess) return false;
+  if (hipMemcpyAsync(&bad, word, sizeof(uint32_t), hipMemcpyDeviceToHost, st) != hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess)
+    return false;
+  g_xcd_state[dev].store(bad == 0 ? 1 : 2, std::memory_order_release);
+  return bad == 0;
+}
+
 int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, void* y, int64_t M,
           int64_t K, int64_t N, void* ws, int64_t ws_bytes, void* stream, const void* aux = nullptr,
           int epi = MK_EPI_NONE, int64_t qg_cap = INT64_MAX) {
@@ -1502,6 +1632,7 @@ int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, v
   a.kwave = p.kwave;
   a.wave_lds = p.wave_lds;
   a.cnt = nullptr;
+  a.xch_local = 0;
   a.aux = static_cast<const uint16_t*>(aux);
   a.epi = epi;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -1528,10 +1659,16 @@ int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, v
   }
   if (p.wide_groups > 0) {
     if (p.part_bytes > 0) a.cnt = static_cast<uint32_t*>(ws);
-    switch (p.wide_groups) {
-      case 1: e = launch_wide<1>(a, p, st); break;
-      case 2: e = launch_wide<2>(a, p, st); break;
-      default: e = launch_wide<4>(a, p, st); break;
+    const int gx = p.ntiles * p.ks;
+    a.xch_local = p.ks > 1 && gx % 8 == 0 && (gx / 8) % p.ks == 0 &&
+                  xcd_round_robin(dim3(gx, p.rowblocks), st, reinterpret_cast<uint32_t*>(a.part));
+    switch (p.wide_groups * (p.nw == 4 ? -1 : 1)) {
+      case 1: e = launch_wide<8, 1>(a, p, st); break;
+      case 2: e = launch_wide<8, 2>(a, p, st); break;
+      case 4: e = launch_wide<8, 4>(a, p, st); break;
+      case -1: e = launch_wide<4, 1>(a, p, st); break;
+      case -2: e = launch_wide<4, 2>(a, p, st); break;
+      default: e = launch_wide<4, 4>(a, p, st); break;
     }
   } else if (p.wide8_steps > 0) {
     if (p.part_bytes > 0) a.cnt = static_cast<uint32_t*>(ws);

@@ -286,6 +286,32 @@ def test_int4_wide_kernel_matches_oracle(M, K, N):
     assert_rel_close(host_bf16(y), ref, BF16_RTOL, f"int4 wide {M}x{K}x{N}")
 
 
+@pytest.mark.parametrize("nw", ["8", "4"])
+@pytest.mark.parametrize("M,K,N", [(16, 4096, 14336), (20, 4096, 8192), (1, 8192, 8192), (40, 2048, 14336)])
+def test_int4_wide_exchange_in_l2_matches_device_scope(monkeypatch, nw, M, K, N):
+    """The split-K exchange inside one XCD's L2 (taken when the placement
+    probe has seen round-robin dealing) against the device-scope exchange
+    (MK_QMM_XCH=device): both sum the partials in k order from memory, so the
+    outputs are bit-identical; with 8 and 4 waves per workgroup, one and
+    several row blocks (2D grids)."""
+    ops = _ops()
+    monkeypatch.setenv("MK_QMM_WIDE_NW", nw)
+    rng = np.random.default_rng(5 * M + K + N)
+    x, packed, s, z = quant.make_int4_case(rng, M, K, N)
+    args = (dev_bf16(x), dev(packed), dev_bf16(s), dev(z))
+    print(f"int4 wide exchange case M={M} K={K} N={N} waves={nw}", flush=True)
+    local = [host_bf16_bits(ops.int4_g64_matmul(*args)) for _ in range(3)]
+    monkeypatch.setenv("MK_QMM_XCH", "device")
+    dev_ = host_bf16_bits(ops.int4_g64_matmul(*args))
+    torch.cuda.synchronize()
+    for y in local:
+        assert np.array_equal(y, dev_)
+    ref = cport.int4_g64_matmul(x, packed, s, z)
+    assert_rel_close(bf16_bits_to_f32(local[0]), ref, BF16_RTOL, f"int4 wide {M}x{K}x{N} waves={nw}")
+    ws = ops.workspace(1, "cuda:0")
+    assert int(ws[: 64 * 1024].count_nonzero()) == 0
+
+
 def test_int4_wide_kernel_deterministic_across_calls():
     """The split-K sum runs in k order whichever workgroup arrives last, and
     every call returns the arrival counters to zero: repeated calls give the
