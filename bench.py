@@ -509,6 +509,84 @@ def cpu_baseline_gemm(target_s, M=4096, K=4096, N=4096):
                       f"OpenMP threads={cores}"}
 
 
+_CPU_ROWS_X = {}
+
+
+def _cpu_rows_input(dtype, rows, cols):
+    """X [rows, cols] ~ N(0, 2) on the host (f32, or bf16 bits), made once."""
+    key = (dtype, rows, cols)
+    if key not in _CPU_ROWS_X:
+        from oracle.bf16 import f32_to_bf16_bits
+        x = (np.random.default_rng(0).standard_normal((rows, cols), dtype=np.float32) * np.float32(np.sqrt(2.0)))
+        _CPU_ROWS_X[key] = x if dtype == "f32" else f32_to_bf16_bits(x)
+    return _CPU_ROWS_X[key]
+
+
+def cpu_baseline_rowop(kind, dtype, target_s, rows=8192, cols=8192):
+    """The oracle's C port of softmax / RMSNorm / argmax / the 6-op chain
+    (OpenMP, every available core) on a row prefix of the 8192^2 case, sized
+    to roughly target_s seconds; GB/s of the GPU line's algorithmic bytes per
+    row (read + write, or read + the int32 index for argmax)."""
+    from oracle import cport
+
+    cores = available_cores()
+    cport.threads(cores)
+    x = _cpu_rows_input(dtype, rows, cols)
+    esz = 4 if dtype == "f32" else 2
+    g = np.random.default_rng(1).uniform(0.5, 1.5, cols).astype(np.float32)
+    if dtype == "bf16":
+        from oracle.bf16 import f32_to_bf16_bits
+        g = f32_to_bf16_bits(g)
+    per_row = cols * esz + 4 if kind == "argmax" else 2 * cols * esz
+
+    def run(r):
+        if kind == "softmax":
+            cport.softmax(x[:r])
+        elif kind == "rmsnorm":
+            cport.rmsnorm(x[:r], g)
+        elif kind == "argmax":
+            (cport.argmax_f32 if dtype == "f32" else cport.argmax_bf16)(x[:r])
+        else:
+            cport.chain6(x[:r])
+
+    r = 64
+    t0 = time.perf_counter()
+    run(r)
+    t1 = time.perf_counter() - t0
+    r = int(min(rows, max(64, r * (target_s / 4) / max(t1, 1e-6))))
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        run(r)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= target_s:
+            break
+    gbs = per_row * r / (el / reps) / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"oracle/c {kind} {dtype}, rows [0,{r}) of {rows}x{cols}, {reps} run(s), {el:.1f}s, "
+                      f"OpenMP threads={cores}"}
+
+
+def cpu_baseline_plumbing(target_s, n=1024):
+    """The oracle's C port of tanh(A @ B).sum(axis=1) on f32 [n, n] (OpenMP
+    over rows, every available core): median microseconds per whole call."""
+    from oracle import cport
+
+    cores = available_cores()
+    cport.threads(cores)
+    rng = np.random.default_rng(0)
+    a = rng.standard_normal((n, n)).astype(np.float32)
+    b = rng.standard_normal((n, n)).astype(np.float32)
+    times, t_end = [], time.perf_counter() + target_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        cport.plumbing(a, b)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return {"value": round(times[len(times) // 2] * 1e6, 1), "unit": "us/call", "cores": cores, "kind": "port",
+            "sample": f"oracle/c plumbing n={n}, all rows, {len(times)} call(s), median, OpenMP threads={cores}"}
+
+
 def bench_end_to_end(warmup=10, iters=50):
     """The plugin path as jax drives it: compile the workload's StableHLO
     once, then execute + await the completion event per call, with the inputs
@@ -525,7 +603,10 @@ def bench_end_to_end(warmup=10, iters=50):
         x, packed, s, z = synthetic.int4_case(rng, 16, 4096, 14336)
         a = (rng.standard_normal((4096, 4096)) / 8).astype(np.float32)
         f32_to_bf16_bits = synthetic.bf16_bits
+        pa = rng.standard_normal((1024, 1024)).astype(np.float32)
+        pb = rng.standard_normal((1024, 1024)).astype(np.float32)
         cases = {
+            "plumbing_tanh_matmul_sum_1024": (programs.plumbing(1024), [(pa, None), (pb, None)]),
             "int4_g64_M16_K4096_N14336": (programs.int4_g64_matmul(16, 4096, 14336),
                                           [(x, runtime.BF16), (packed, None), (s, runtime.BF16), (z, None)]),
             "bf16_gemm_4096": (programs.matmul(4096, 4096, 4096),
@@ -580,6 +661,8 @@ def main():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-row-seconds", type=float, default=2.5,
+                    help="CPU seconds per secondary line's cpu_baseline (row ops, chain, plumbing)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
                     help="comma list of secondary workloads (int8,qmm_m,shard,gemm,decoder,softmax,rmsnorm,argmax,chain6,e2e), "
@@ -703,13 +786,20 @@ def main():
         for dt in ("f32", "bf16"):
             r = bench_rowop(torch, ops, kind, dt, max(50, args.steps // 10), 5)
             log(f"[bench] {kind} {dt} 8192x8192: {r['sec_per_call'] * 1e6:.1f} us, {r['gbs']:.0f} GB/s")
-            secondary[f"{kind}_{dt}_8192x8192"] = _hbm_entry(r["gbs"], r["sec_per_call"] * 1e6)
+            entry = _hbm_entry(r["gbs"], r["sec_per_call"] * 1e6)
+            if not args.no_cpu:
+                entry["cpu_baseline"] = cpu_baseline_rowop(kind, dt, args.cpu_row_seconds)
+                log(f"[bench] cpu {kind} {dt}: {entry['cpu_baseline']['value']} GB/s")
+            secondary[f"{kind}_{dt}_8192x8192"] = entry
 
     if want("e2e"):
         e2e = bench_end_to_end()
         for k, v in e2e.items():
             log(f"[bench] end to end {k}: compile {v['compile_ms']} ms, first call {v['first_call_ms']} ms, "
                 f"median {v['median_us']} us per execute + await")
+        if not args.no_cpu and "plumbing_tanh_matmul_sum_1024" in e2e:
+            e2e["plumbing_tanh_matmul_sum_1024"]["cpu_baseline"] = cpu_baseline_plumbing(args.cpu_row_seconds)
+            log(f"[bench] cpu plumbing: {e2e['plumbing_tanh_matmul_sum_1024']['cpu_baseline']['value']} us/call")
         secondary["plugin_end_to_end"] = {
             "what": "mkrt_compile once, then mkrt_execute + event await per call, inputs resident; "
                     "wall clock on the host, not kernel time", **e2e}

@@ -24,6 +24,14 @@ def lib():
         L.orc_int8_pc_matmul.argtypes = [p, p, p, i64, i64, i64, i64, i64, p]
         L.orc_gemm_bf16.argtypes = [p, p, i64, i64, i64, i64, i64, p]
         L.orc_argmax_f32.argtypes = [p, i64, i64, p]
+        L.orc_argmax_bf16.argtypes = [p, i64, i64, p]
+        L.orc_softmax_f32.argtypes = [p, i64, i64, i64, p]
+        L.orc_softmax_bf16.argtypes = [p, i64, i64, i64, p]
+        L.orc_rmsnorm_f32.argtypes = [p, p, i64, ctypes.c_float, i64, i64, p]
+        L.orc_rmsnorm_bf16.argtypes = [p, p, i64, ctypes.c_float, i64, i64, p]
+        L.orc_chain6_f32.argtypes = [p, i64, p]
+        L.orc_chain6_bf16.argtypes = [p, i64, p]
+        L.orc_plumbing_f32.argtypes = [p, p, i64, i64, i64, p]
         _LIB = L
     return _LIB
 
@@ -74,3 +82,76 @@ def argmax_f32(x):
     out = np.zeros(rows, dtype=np.int32)
     lib().orc_argmax_f32(_ptr(x), rows, cols, _ptr(out))
     return out
+
+
+def argmax_bf16(x_bits):
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    rows, cols = x.shape
+    out = np.zeros(rows, dtype=np.int32)
+    lib().orc_argmax_bf16(_ptr(x), rows, cols, _ptr(out))
+    return out
+
+
+def _out_like(x, row_range):
+    """Output array: rows outside row_range stay zero; without a range every
+    row is written, so no fill is needed."""
+    return np.empty_like(x) if row_range is None else np.zeros_like(x)
+
+
+def _rows(x, row_range):
+    rows = x.shape[0]
+    return row_range or (0, rows)
+
+
+def softmax(x, row_range=None):
+    """f32 softmax over the last axis (f32 in, f32 out) or, for uint16 input,
+    bf16 softmax on bit patterns (bf16 bits out).  Rows outside row_range
+    are left zero."""
+    if x.dtype != np.uint16:
+        x = np.asarray(x, dtype=np.float32)
+    x = np.ascontiguousarray(x)
+    r0, r1 = _rows(x, row_range)
+    y = _out_like(x, row_range)
+    fn = lib().orc_softmax_bf16 if x.dtype == np.uint16 else lib().orc_softmax_f32
+    fn(_ptr(x), x.shape[1], r0, r1, _ptr(y))
+    return y
+
+
+def rmsnorm(x, g, eps=1e-6, row_range=None):
+    """RMSNorm over the last axis: f32 (float32 x, g) or bf16 bits (uint16 x, g)."""
+    x = np.ascontiguousarray(x)
+    g = np.ascontiguousarray(g)
+    r0, r1 = _rows(x, row_range)
+    if x.dtype == np.uint16:
+        y = _out_like(x, row_range)
+        lib().orc_rmsnorm_bf16(_ptr(x), _ptr(g), x.shape[1], eps, r0, r1, _ptr(y))
+    else:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        g = np.ascontiguousarray(g, dtype=np.float32)
+        y = _out_like(x, row_range)
+        lib().orc_rmsnorm_f32(_ptr(x), _ptr(g), x.shape[1], eps, r0, r1, _ptr(y))
+    return y
+
+
+def chain6(x):
+    """The workload's 6-op elementwise chain: f32, or bf16 bits for uint16 input."""
+    x = np.ascontiguousarray(x)
+    if x.dtype == np.uint16:
+        y = np.empty_like(x)
+        lib().orc_chain6_bf16(_ptr(x), x.size, _ptr(y))
+    else:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty_like(x)
+        lib().orc_chain6_f32(_ptr(x), x.size, _ptr(y))
+    return y
+
+
+def plumbing(a, b, row_range=None):
+    """tanh(A @ B).sum(axis=1) in f32 for rows in row_range (others zero)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    n = a.shape[0]
+    r0, r1 = row_range or (0, n)
+    y = np.zeros(n, dtype=np.float32)
+    lib().orc_plumbing_f32(_ptr(a), _ptr(b), n, r0, r1, _ptr(y))
+    return y

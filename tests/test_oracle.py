@@ -532,6 +532,109 @@ def test_cport_argmax_known_rows():
     assert cport.argmax_f32(z).tolist() == [0, 0, 1]
 
 
+@pytest.mark.parametrize("shape,seed", [((512, 37), 0), ((8, 2049), 3), ((64, 300), 5)])
+def test_cport_argmax_bf16_matches_numpy(shape, seed):
+    cport = _cport()
+    xb = bf16.f32_to_bf16_bits(_edge(shape, seed))
+    xf = bf16.bf16_bits_to_f32(xb)
+    np.testing.assert_array_equal(cport.argmax_bf16(xb), rowops.argmax(xf))
+    ties = bf16.f32_to_bf16_bits(np.round(np.random.default_rng(seed).standard_normal((32, 512)) * 2) / 2)
+    np.testing.assert_array_equal(cport.argmax_bf16(ties), rowops.argmax(bf16.bf16_bits_to_f32(ties)))
+
+
+def _rows_case(rows, cols, seed):
+    x = (np.random.default_rng(seed).standard_normal((rows, cols)) * np.sqrt(2)).astype(np.float32)
+    # the reference's special softmax rows (tests/test_native_softmax.py:26-35)
+    x[0] = np.nan
+    x[1] = -np.inf
+    x[2, 3] = np.inf
+    x[3] = 80.0
+    return x
+
+
+def test_cport_softmax_f32_matches_numpy_and_special_rows():
+    cport = _cport()
+    x = _rows_case(40, 1000, 11)
+    y = cport.softmax(x)
+    ref = rowops.softmax(x)
+    assert np.array_equal(np.isnan(y), np.isnan(ref))
+    fin = ~np.isnan(ref)
+    np.testing.assert_allclose(y[fin], ref[fin], rtol=1e-5, atol=1e-12)
+    np.testing.assert_allclose(y[3], 1.0 / 1000, rtol=1e-6)  # constant row: uniform
+    np.testing.assert_allclose(y[4:].sum(axis=1), 1.0, rtol=1e-5)
+    part = cport.softmax(x, row_range=(5, 9))
+    np.testing.assert_array_equal(part[5:9], y[5:9])
+    assert not part[:5].any() and not part[9:].any()
+
+
+def test_cport_softmax_bf16_matches_numpy_rounding_points():
+    cport = _cport()
+    xb = bf16.f32_to_bf16_bits(_rows_case(40, 1000, 12))
+    got = cport.softmax(xb)
+    ref = rowops.softmax_bf16(xb)
+    gf, rf = bf16.bf16_bits_to_f32(got), bf16.bf16_bits_to_f32(ref)
+    assert np.array_equal(np.isnan(gf), np.isnan(rf))
+    fin = ~np.isnan(rf)
+    # the same rounding points; expf may move a rounding by one bf16 ulp
+    np.testing.assert_array_less(np.abs(gf[fin] - rf[fin]), 2.0 ** -7 * np.abs(rf[fin]) + 1e-30)
+    assert np.mean(got[fin] == ref[fin]) > 0.99
+
+
+def test_cport_rmsnorm_matches_numpy():
+    cport = _cport()
+    rng = np.random.default_rng(13)
+    x = (rng.standard_normal((33, 777)) * np.sqrt(2)).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, 777).astype(np.float32)
+    ref = rowops.rmsnorm(x, g)
+    np.testing.assert_allclose(cport.rmsnorm(x, g), ref, rtol=1e-5, atol=1e-7)
+    # closed form: a constant row c gives c / sqrt(c^2 + eps) * g
+    c = np.full((2, 64), 3.0, np.float32)
+    np.testing.assert_allclose(cport.rmsnorm(c, np.ones(64, np.float32)), 3.0 / np.sqrt(9.0 + 1e-6), rtol=1e-6)
+    xb, gb = bf16.f32_to_bf16_bits(x), bf16.f32_to_bf16_bits(g)
+    got = bf16.bf16_bits_to_f32(cport.rmsnorm(xb, gb))
+    refb = rowops.rmsnorm(bf16.bf16_bits_to_f32(xb), bf16.bf16_bits_to_f32(gb))
+    np.testing.assert_array_less(np.abs(got - refb), 2.0 ** -8 * np.abs(refb) * 1.01 + 1e-30)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_cport_chain6_matches_numpy(dtype):
+    cport = _cport()
+    rng = np.random.default_rng(14)
+    x = (rng.standard_normal(20000) * np.sqrt(2) * 8).astype(np.float32)
+    x[:6] = [0.0, -0.0, np.nan, np.inf, -np.inf, 100.0]
+    if dtype == "f32":
+        got = cport.chain6(x)
+        ref = eltwise.evaluate(eltwise.CHAIN6, [x], "f32")
+        assert np.array_equal(np.isnan(got), np.isnan(ref))
+        fin = ~np.isnan(ref)
+        np.testing.assert_allclose(got[fin], ref[fin], rtol=4e-7, atol=0)
+    else:
+        xb = bf16.f32_to_bf16_bits(x)
+        got = bf16.bf16_bits_to_f32(cport.chain6(xb))
+        ref = eltwise.evaluate(eltwise.CHAIN6, [bf16.bf16_bits_to_f32(xb)], "bf16")
+        assert np.array_equal(np.isnan(got), np.isnan(ref))
+        inf = np.isinf(ref)
+        np.testing.assert_array_equal(got[inf], ref[inf])
+        fin = np.isfinite(ref)
+        np.testing.assert_array_less(np.abs(got[fin] - ref[fin]), 2.0 ** -7 * np.abs(ref[fin]) + 1e-30)
+        assert np.mean(got[fin] == ref[fin]) > 0.99
+
+
+def test_cport_plumbing_matches_float64():
+    cport = _cport()
+    rng = np.random.default_rng(0)
+    n = 96
+    a = rng.standard_normal((n, n)).astype(np.float32)
+    b = rng.standard_normal((n, n)).astype(np.float32)
+    ref = np.tanh(a.astype(np.float64) @ b.astype(np.float64)).sum(axis=1)
+    y = cport.plumbing(a, b)
+    assert np.max(np.abs(y - ref)) / np.max(np.abs(ref)) <= 1e-5
+    # closed form: B = 0 gives tanh(0) = 0 everywhere
+    assert not cport.plumbing(a, np.zeros_like(b)).any()
+    part = cport.plumbing(a, b, row_range=(10, 20))
+    np.testing.assert_array_equal(part[10:20], y[10:20])
+
+
 # ------------------------------------------------------- decoder layer
 
 def test_decoder_rope_closed_forms():
