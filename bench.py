@@ -516,9 +516,9 @@ def _cpu_rows_input(dtype, rows, cols):
     """X [rows, cols] ~ N(0, 2) on the host (f32, or bf16 bits), made once."""
     key = (dtype, rows, cols)
     if key not in _CPU_ROWS_X:
-        from oracle.bf16 import f32_to_bf16_bits
+        from mi355x import synthetic
         x = (np.random.default_rng(0).standard_normal((rows, cols), dtype=np.float32) * np.float32(np.sqrt(2.0)))
-        _CPU_ROWS_X[key] = x if dtype == "f32" else f32_to_bf16_bits(x)
+        _CPU_ROWS_X[key] = x if dtype == "f32" else synthetic.bf16_bits(x)
     return _CPU_ROWS_X[key]
 
 
