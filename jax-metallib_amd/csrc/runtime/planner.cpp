@@ -330,6 +330,10 @@ class Planner {
     const int src = view_src(v);
     if (src >= 0) return need(src);
     if (numel(v) == 0) return temp_for(v);  // nothing to compute
+    if (op->name == "slice") {
+      const int sv = slice_view(v, *op);
+      if (sv >= 0) return sv;
+    }
     const std::string& n = op->name;
     if (n == "constant") {
       double c;
@@ -807,6 +811,41 @@ class Planner {
     layout_step(src, o, eb, t.dims, ss, so, ods, 0, desc);
     *out = o;
     return true;
+  }
+
+  // A slice that is one contiguous run of its operand's elements (leading
+  // dimensions of extent 1 in the result, one partial dimension, full
+  // trailing ones, unit strides) of an argument or constant -- read-only
+  // buffers -- is a view at a byte offset: no copy.  A scanned layer stack
+  // takes each layer's weights this way.  Otherwise -1.
+  int slice_view(int v, const Op& op) {
+    const int x = op.operands[0];
+    const std::vector<int64_t>& xd = type(x).dims;
+    const size_t r = xd.size();
+    if (type(x).dtype != type(v).dtype || op.slice_start.size() != r || r == 0) return -1;
+    size_t k = 0;  // the partial dimension
+    while (k < r && op.slice_limit[k] - op.slice_start[k] == 1) ++k;
+    for (size_t i = 0; i < r; ++i) {
+      if (op.slice_stride[i] != 1) return -1;
+      if (i > k && (op.slice_start[i] != 0 || op.slice_limit[i] != xd[i])) return -1;
+    }
+    const std::vector<int64_t> xs = row_strides(xd);
+    int64_t off = 0;
+    for (size_t i = 0; i < r; ++i) off += op.slice_start[i] * xs[i];
+    int base = need(x);
+    off *= dtype_bytes(type(v).dtype);
+    if (plan_.slots[base].kind == SLOT_VIEW) {
+      off += plan_.slots[base].offset;
+      base = plan_.slots[base].base;
+    }
+    if (plan_.slots[base].kind != SLOT_ARG && plan_.slots[base].kind != SLOT_CONST) return -1;
+    Slot s;
+    s.kind = SLOT_VIEW;
+    s.bytes = type(v).bytes();
+    s.base = base;
+    s.offset = off;
+    if (off < 0 || off + s.bytes > plan_.slots[base].bytes) return -1;
+    return new_slot(s);
   }
 
   int dummy(int v) { return temp_for(v); }

@@ -16,7 +16,7 @@
 
 namespace mkrt {
 
-enum SlotKind { SLOT_ARG = 0, SLOT_TEMP = 1, SLOT_CONST = 2 };
+enum SlotKind { SLOT_ARG = 0, SLOT_TEMP = 1, SLOT_CONST = 2, SLOT_VIEW = 3 };
 
 // A device buffer the plan reads or writes.  Arguments are the caller's
 // buffers; temporaries are allocated per execute; constants are uploaded once.
@@ -25,6 +25,8 @@ struct Slot {
   int64_t bytes = 0;
   int arg_index = -1;
   std::vector<uint8_t> data;  // SLOT_CONST contents
+  int base = -1;              // SLOT_VIEW: the argument or constant slot it reads (an earlier slot)
+  int64_t offset = 0;         // SLOT_VIEW: byte offset into that slot
 };
 
 enum StepKind {

@@ -1000,6 +1000,9 @@ mkrt_error* mkrt_execute(mkrt_executable* x, mkrt_buffer* const* inputs, int num
       mem[i] = inputs[s.arg_index]->data;
     } else if (s.kind == mkrt::SLOT_CONST) {
       mem[i] = x->const_mem[i];
+    } else if (s.kind == mkrt::SLOT_VIEW) {
+      // A contiguous slice of an earlier argument or constant slot.
+      mem[i] = static_cast<char*>(mem[s.base]) + s.offset;
     } else {
       hipError_t e = c->alloc.alloc((size_t)s.bytes, &mem[i]);
       if (e != hipSuccess)

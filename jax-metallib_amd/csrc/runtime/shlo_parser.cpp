@@ -9,6 +9,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <set>
 
@@ -249,6 +250,39 @@ void parse_dense(const std::string& s, int dtype, Op* op) {
   op->const_splat = vals.size() == 1;
 }
 
+// Joins raw body lines into statements: an op line that opens a region
+// (by '{' balance) continues until the region closes, and a line starting a
+// pretty-form region of the previous op ("reducer", "cond", "do") is
+// appended to that op.
+std::vector<std::string> join_statements(const std::vector<std::string>& raw) {
+  std::vector<std::string> out;
+  std::string pending;
+  int pdepth = 0;
+  for (const std::string& l : raw) {
+    const std::string s = trim(l);
+    int d = 0;
+    for (char c : s) d += (c == '{') - (c == '}');
+    if (!pending.empty() || (d > 0 && !s.empty())) {
+      if (pending.empty() && !out.empty() &&
+          (starts_with(s, "reducer") || starts_with(s, "cond") || starts_with(s, "do ") || starts_with(s, "do{"))) {
+        pending = out.back();
+        out.pop_back();
+      }
+      pending += (pending.empty() ? "" : "\n") + s;
+      pdepth += d;
+      if (pdepth <= 0) {
+        out.push_back(pending);
+        pending.clear();
+        pdepth = 0;
+      }
+      continue;
+    }
+    if (!s.empty()) out.push_back(s);
+  }
+  if (!pending.empty()) out.push_back(pending);  // unbalanced: the op parser reports it
+  return out;
+}
+
 struct RawFunc {
   std::string name;
   bool is_public = false;
@@ -296,8 +330,7 @@ std::vector<RawFunc> split_functions(const std::string& text) {
     // Body: lines until the function's closing brace (depth tracking).
     int bd = 0;
     for (char c : l) bd += (c == '{') - (c == '}');
-    std::string pending;
-    int pdepth = 0;
+    std::vector<std::string> raw;
     for (++i; i < lines.size() && bd > 0; ++i) {
       const std::string s = trim(lines[i]);
       int d = 0;
@@ -307,25 +340,9 @@ std::vector<RawFunc> split_functions(const std::string& text) {
         break;
       }
       bd += d;
-      if (!pending.empty() || (d > 0 && !s.empty())) {
-        // A region that continues the previous op (pretty-printed reduce
-        // "reducer(...) {", while "cond {" / "do {").
-        if (pending.empty() && !f.lines.empty() &&
-            (starts_with(s, "reducer") || starts_with(s, "cond") || starts_with(s, "do ") || starts_with(s, "do{"))) {
-          pending = f.lines.back();
-          f.lines.pop_back();
-        }
-        pending += (pending.empty() ? "" : "\n") + s;
-        pdepth += d;
-        if (pdepth <= 0) {
-          f.lines.push_back(pending);
-          pending.clear();
-          pdepth = 0;
-        }
-        continue;
-      }
-      if (!s.empty()) f.lines.push_back(s);
+      raw.push_back(s);
     }
+    f.lines = join_statements(raw);
     --i;
     fns.push_back(f);
   }
@@ -464,8 +481,25 @@ void validate_op(const Builder& B, const Op& op, const std::string& s) {
 void parse_body(const RawFunc& f, const std::vector<RawFunc>& all, Builder& B, const std::vector<int>& arg_ids,
                 std::vector<int>* rets, int inline_depth);
 
+void parse_while(const std::string& stmt, const std::vector<RawFunc>& all, Builder& B, int inline_depth);
+bool fold_scalar(const Builder& B, int v, double* out, int depth = 0);
+
+// The op name of a statement's first line ("while", "add", ...).
+std::string statement_op(const std::string& stmt) {
+  std::string first = stmt.substr(0, stmt.find('\n'));
+  const size_t eq = first.find(" = ");
+  std::string rhs = (!first.empty() && first[0] == '%' && eq != std::string::npos) ? trim(first.substr(eq + 3)) : first;
+  size_t te = 0;
+  while (te < rhs.size() && !isspace((unsigned char)rhs[te]) && rhs[te] != '(') ++te;
+  return strip_dialect(rhs.substr(0, te));
+}
+
 void parse_statement(const std::string& stmt, const std::vector<RawFunc>& all, Builder& B,
                      std::vector<int>* rets, int inline_depth) {
+  if (statement_op(stmt) == "while") {
+    parse_while(stmt, all, B, inline_depth);
+    return;
+  }
   std::string s = stmt;
   // Separate a region body (reduce comparators) from the op line.
   // Multi-line statements: the op header is the first line, plus the last
@@ -479,7 +513,8 @@ void parse_statement(const std::string& stmt, const std::vector<RawFunc>& all, B
     s = s.substr(0, nl);
     if (starts_with(last, "})")) s += " " + last;
   }
-  if (starts_with(s, "return") || starts_with(s, "func.return") || starts_with(s, "\"func.return\"")) {
+  if (starts_with(s, "return") || starts_with(s, "func.return") || starts_with(s, "\"func.return\"") ||
+      starts_with(s, "stablehlo.return") || starts_with(s, "\"stablehlo.return\"")) {
     const size_t tc = type_colon(s);
     for (const std::string& n : value_names(s.substr(0, tc))) rets->push_back(B.lookup(n));
     return;
@@ -541,6 +576,40 @@ void parse_statement(const std::string& stmt, const std::vector<RawFunc>& all, B
   op.text = s;
   // Operands: SSA names in the op body (excluding region-internal names).
   std::vector<std::string> opnd = value_names(body);
+  if (opname == "dynamic_slice" && !opnd.empty()) {
+    // With start indices that fold to constants (a counted loop unrolled
+    // above, or constant operands) it is a static slice.  StableHLO clamps
+    // each start to [0, dim - size].
+    std::vector<int64_t> sizes;
+    if (!list_after(rhs, "slice_sizes = ", &sizes)) list_after(rhs, "sizes = ", &sizes);
+    const int src = B.lookup(opnd[0]);
+    const TensorType& st = B.fn.values[src].type;
+    bool folded = sizes.size() == st.dims.size() && opnd.size() == st.dims.size() + 1;
+    std::vector<int64_t> start;
+    for (size_t i = 1; folded && i < opnd.size(); ++i) {
+      double c;
+      folded = fold_scalar(B, B.lookup(opnd[i]), &c);
+      const int64_t size = sizes[i - 1];
+      if (folded && (size < 0 || size > st.dims[i - 1])) throw ParseError("dynamic_slice size out of bounds: " + s);
+      if (folded) start.push_back(std::min(std::max<int64_t>((int64_t)c, 0), st.dims[i - 1] - size));
+    }
+    if (folded) {
+      op.name = "slice";
+      op.operands = {src};
+      op.slice_start = start;
+      for (size_t i = 0; i < start.size(); ++i) op.slice_limit.push_back(start[i] + sizes[i]);
+      op.slice_stride.assign(start.size(), 1);
+      std::vector<TensorType> rt = all_types(types.substr(types.rfind("->") == std::string::npos ? 0 : types.rfind("->") + 2));
+      if (rt.empty() || res_names.size() != 1) throw ParseError("cannot read dynamic_slice result: " + s);
+      const int v = B.new_value(rt.back(), res_names[0]);
+      B.fn.values[v].def_op = (int)B.fn.ops.size();
+      op.results.push_back(v);
+      B.names[res_names[0]] = v;
+      validate_op(B, op, s);
+      B.fn.ops.push_back(op);
+      return;
+    }
+  }
   if (opname == "reduce") {
     // Operands become inputs then init values.  Pretty form pairs them,
     // "(%x init: %c), (%y init: %d)"; the generic form already lists inputs
@@ -659,6 +728,254 @@ void parse_statement(const std::string& stmt, const std::vector<RawFunc>& all, B
   }
   validate_op(B, op, s);
   B.fn.ops.push_back(op);
+  // Integer and predicate scalars computed from constants (a counted loop's
+  // index math once the loop is unrolled, and converts of it) become
+  // constants, as the reference folds the index math of unrolled loops.
+  auto int_like = [](int dt) { return dt != DT_F16 && dt != DT_F32 && dt != DT_F64 && dt != DT_BF16; };
+  if (op.results.size() == 1 && op.name != "constant" && !op.operands.empty() &&
+      B.fn.values[op.results[0]].type.numel() == 1 &&
+      (int_like(B.fn.values[op.results[0]].type.dtype) ||
+       (op.name == "convert" && int_like(B.fn.values[op.operands[0]].type.dtype)))) {
+    double c;
+    if (fold_scalar(B, op.results[0], &c)) {
+      Op& k = B.fn.ops.back();
+      k.name = "constant";
+      k.operands.clear();
+      k.const_values = {c};
+      k.const_splat = true;
+    }
+  }
+}
+
+// Scalar value of v when it folds to a compile-time constant: a constant op
+// (splat), or an integer/float scalar op (convert, reshape, broadcast of a
+// scalar, add, subtract, multiply, maximum, minimum, negate, compare,
+// select, and, or, not, clamp) of constants.
+bool fold_scalar(const Builder& B, int v, double* out, int depth) {
+  if (v < 0 || depth > 64) return false;
+  const Value& val = B.fn.values[v];
+  if (val.def_op < 0 || val.type.numel() != 1) return false;
+  const Op& op = B.fn.ops[val.def_op];
+  const bool is_int = val.type.dtype != DT_F16 && val.type.dtype != DT_F32 && val.type.dtype != DT_F64 &&
+                      val.type.dtype != DT_BF16;
+  if (op.name == "constant") {
+    if (op.const_values.empty()) return false;
+    *out = op.const_values[0];
+    return true;
+  }
+  std::vector<double> a(op.operands.size());
+  for (size_t i = 0; i < op.operands.size(); ++i) {
+    const int u = op.operands[i];
+    if (B.fn.values[u].type.numel() != 1 || !fold_scalar(B, u, &a[i], depth + 1)) return false;
+  }
+  auto as_int = [&](double x) { return is_int ? (double)(int64_t)x : x; };
+  const size_t n = a.size();
+  if ((op.name == "convert" || op.name == "reshape" || op.name == "broadcast_in_dim") && n == 1) {
+    *out = val.type.dtype == DT_PRED ? (a[0] != 0) : as_int(a[0]);
+    return true;
+  }
+  if (op.name == "negate" && n == 1) { *out = -a[0]; return true; }
+  if (op.name == "not" && n == 1) {
+    if (val.type.dtype != DT_PRED) return false;
+    *out = a[0] == 0;
+    return true;
+  }
+  if (n == 2) {
+    if (op.name == "add") { *out = as_int(a[0] + a[1]); return true; }
+    if (op.name == "subtract") { *out = as_int(a[0] - a[1]); return true; }
+    if (op.name == "multiply") { *out = as_int(a[0] * a[1]); return true; }
+    if (op.name == "maximum") { *out = std::max(a[0], a[1]); return true; }
+    if (op.name == "minimum") { *out = std::min(a[0], a[1]); return true; }
+    if (op.name == "and") { *out = (a[0] != 0 && a[1] != 0); return true; }
+    if (op.name == "or") { *out = (a[0] != 0 || a[1] != 0); return true; }
+    if (op.name == "compare") {
+      const std::string& d = op.compare_dir;
+      if (d == "EQ") *out = a[0] == a[1];
+      else if (d == "NE") *out = a[0] != a[1];
+      else if (d == "LT") *out = a[0] < a[1];
+      else if (d == "LE") *out = a[0] <= a[1];
+      else if (d == "GT") *out = a[0] > a[1];
+      else if (d == "GE") *out = a[0] >= a[1];
+      else return false;
+      return true;
+    }
+  }
+  if (n == 3 && op.name == "select") { *out = a[0] != 0 ? a[1] : a[2]; return true; }
+  if (n == 3 && op.name == "clamp") { *out = std::min(std::max(a[1], a[0]), a[2]); return true; }
+  return false;
+}
+
+// The text between the '{' at `open` and its matching '}'; `close` receives
+// the position of that '}'.
+std::string braced(const std::string& s, size_t open, size_t* close) {
+  int d = 0;
+  for (size_t i = open; i < s.size(); ++i) {
+    if (s[i] == '{') ++d;
+    if (s[i] == '}' && --d == 0) {
+      *close = i;
+      return s.substr(open + 1, i - open - 1);
+    }
+  }
+  throw ParseError("unbalanced region braces in: " + s.substr(0, s.find('\n')));
+}
+
+std::vector<std::string> split_lines(const std::string& t) {
+  std::vector<std::string> v;
+  size_t p = 0;
+  while (p <= t.size()) {
+    size_t e = t.find('\n', p);
+    if (e == std::string::npos) e = t.size();
+    v.push_back(t.substr(p, e - p));
+    p = e + 1;
+  }
+  return v;
+}
+
+// A region of a while op: its block-argument names and statements.
+struct WhileRegion {
+  std::vector<std::string> args;
+  std::vector<std::string> stmts;
+};
+
+WhileRegion while_region(const std::string& text, const std::vector<std::string>& pretty_args) {
+  WhileRegion r;
+  std::vector<std::string> lines = split_lines(text);
+  std::vector<std::string> raw;
+  for (const std::string& l0 : lines) {
+    const std::string l = trim(l0);
+    if (l.empty()) continue;
+    if (starts_with(l, "^bb") && r.args.empty() && raw.empty()) {
+      // "^bb0(%arg2: tensor<i32>, %arg3: tensor<..>):" (generic form)
+      const size_t lp = l.find('('), rp = l.rfind(')');
+      const std::string a = l.substr(lp + 1, rp - lp - 1);
+      size_t q = 0;
+      while ((q = a.find('%', q)) != std::string::npos) {
+        size_t e = q + 1;
+        while (e < a.size() && (isalnum((unsigned char)a[e]) || a[e] == '_' || a[e] == '.')) ++e;
+        r.args.push_back(a.substr(q, e - q));
+        q = e;
+      }
+      continue;
+    }
+    raw.push_back(l);
+  }
+  if (r.args.empty()) r.args = pretty_args;
+  r.stmts = join_statements(raw);
+  return r;
+}
+
+// stablehlo.while, unrolled at parse time when it is a counted loop: the
+// condition must fold to a constant for the loop-carried values of every
+// trip (jax's lax.scan / fori_loop counters), and at most kMaxTrips trips
+// run.  The body is inlined once per trip; loop-carried values flow from one
+// copy to the next, and dynamic_slice ops indexed by the counter become
+// static slices.  The reference unrolls short counted loops before planning
+// the same way (core/stablehlo_parser.mm:462-519).  Other loops are an error
+// naming the reason.
+void parse_while(const std::string& stmt, const std::vector<RawFunc>& all, Builder& B, int inline_depth) {
+  constexpr int kMaxTrips = 16;
+  const size_t nl = stmt.find('\n');
+  const std::string head = nl == std::string::npos ? stmt : stmt.substr(0, nl);
+  // Results: "%0:3 = ..." or "%a, %b = ...".
+  std::vector<std::string> res_names;
+  int nres = 0;
+  const size_t eq = head.find(" = ");
+  if (eq == std::string::npos || head[0] != '%') throw ParseError("stablehlo.while without results: " + head);
+  {
+    const std::string lhs = head.substr(0, eq);
+    const size_t colon = lhs.find(':');
+    if (colon != std::string::npos) {
+      nres = atoi(lhs.c_str() + colon + 1);
+      const std::string base = trim(lhs.substr(0, colon));
+      for (int i = 0; i < nres; ++i) res_names.push_back(nres > 1 ? base + "#" + std::to_string(i) : base);
+    } else {
+      res_names = value_names(lhs);
+      nres = (int)res_names.size();
+    }
+  }
+  const std::string rhs = trim(head.substr(eq + 3));
+  const bool generic = starts_with(rhs, "\"stablehlo.while\"");
+  std::vector<int> inits;
+  std::vector<std::string> pretty_args;
+  std::string cond_text, body_text;
+  std::vector<TensorType> rtypes;
+  const size_t lp = rhs.find('(');
+  if (lp == std::string::npos) throw ParseError("stablehlo.while without operands: " + head);
+  if (generic) {
+    const size_t rp = rhs.find(')', lp);
+    for (const std::string& n : value_names(rhs.substr(lp, rp - lp))) inits.push_back(B.lookup(n));
+    const size_t o1 = stmt.find('{', nl == std::string::npos ? 0 : stmt.find(") ({", 0) + 3);
+    size_t c1 = 0, c2 = 0;
+    cond_text = braced(stmt, o1, &c1);
+    const size_t o2 = stmt.find('{', c1 + 1);
+    if (o2 == std::string::npos) throw ParseError("stablehlo.while without its body region");
+    body_text = braced(stmt, o2, &c2);
+    const std::string tail = stmt.substr(c2 + 1);
+    const size_t arrow = tail.rfind("->");
+    rtypes = all_types(arrow == std::string::npos ? tail : tail.substr(arrow + 2));
+  } else {
+    // "stablehlo.while(%iterArg = %c, %iterArg_0 = %x) : tensor<i32>, tensor<..>"
+    int d = 0;
+    size_t rp = lp;
+    for (; rp < rhs.size(); ++rp) {
+      if (rhs[rp] == '(') ++d;
+      if (rhs[rp] == ')' && --d == 0) break;
+    }
+    const std::string pairs = rhs.substr(lp + 1, rp - lp - 1);
+    const std::vector<std::string> names = value_names(pairs);
+    if (names.size() % 2) throw ParseError("stablehlo.while operand list: " + head);
+    for (size_t i = 0; i < names.size(); i += 2) {
+      pretty_args.push_back(names[i]);
+      inits.push_back(B.lookup(names[i + 1]));
+    }
+    const size_t colon = rhs.find(':', rp);
+    if (colon != std::string::npos) rtypes = all_types(rhs.substr(colon + 1));
+    const size_t cpos = stmt.find("cond", nl == std::string::npos ? stmt.size() : nl);
+    if (cpos == std::string::npos) throw ParseError("stablehlo.while without its cond region");
+    size_t c1 = 0, c2 = 0;
+    cond_text = braced(stmt, stmt.find('{', cpos), &c1);
+    const size_t dpos = stmt.find("do", c1);
+    if (dpos == std::string::npos) throw ParseError("stablehlo.while without its do region");
+    body_text = braced(stmt, stmt.find('{', dpos), &c2);
+  }
+  if ((int)inits.size() != nres || (int)rtypes.size() != nres)
+    throw ParseError("stablehlo.while: " + std::to_string(inits.size()) + " operands, " + std::to_string(nres) +
+                     " results, " + std::to_string(rtypes.size()) + " result types");
+  for (int i = 0; i < nres; ++i)
+    if (!(B.fn.values[inits[i]].type == rtypes[i]))
+      throw ParseError("stablehlo.while: operand " + std::to_string(i) + " type differs from its result type");
+  const WhileRegion cond = while_region(cond_text, pretty_args);
+  const WhileRegion body = while_region(body_text, pretty_args);
+  if ((int)cond.args.size() != nres || (int)body.args.size() != nres)
+    throw ParseError("stablehlo.while: region arguments differ from the loop-carried values");
+
+  std::vector<int> carried = inits;
+  for (int trip = 0;; ++trip) {
+    std::map<std::string, int> saved = B.names;
+    for (int i = 0; i < nres; ++i) B.names[cond.args[i]] = carried[i];
+    std::vector<int> cret;
+    for (const std::string& st : cond.stmts) parse_statement(st, all, B, &cret, inline_depth);
+    B.names = saved;
+    double c = 0;
+    if (cret.size() != 1 || !fold_scalar(B, cret[0], &c))
+      throw ParseError("stablehlo.while: the loop condition does not fold to a constant; only counted loops of at "
+                       "most " + std::to_string(kMaxTrips) + " trips are unrolled");
+    if (c == 0) break;
+    if (trip >= kMaxTrips)
+      throw ParseError("stablehlo.while: more than " + std::to_string(kMaxTrips) +
+                       " trips; only counted loops of at most " + std::to_string(kMaxTrips) + " trips are unrolled");
+    saved = B.names;
+    for (int i = 0; i < nres; ++i) B.names[body.args[i]] = carried[i];
+    std::vector<int> bret;
+    for (const std::string& st : body.stmts) parse_statement(st, all, B, &bret, inline_depth);
+    B.names = saved;
+    if ((int)bret.size() != nres) throw ParseError("stablehlo.while: the body returns the wrong number of values");
+    for (int i = 0; i < nres; ++i)
+      if (!(B.fn.values[bret[i]].type == rtypes[i]))
+        throw ParseError("stablehlo.while: the body changes the type of loop-carried value " + std::to_string(i));
+    carried = bret;
+  }
+  for (int i = 0; i < nres; ++i) B.names[res_names[i]] = carried[i];
 }
 
 void parse_body(const RawFunc& f, const std::vector<RawFunc>& all, Builder& B, const std::vector<int>& arg_ids,

@@ -600,6 +600,92 @@ def decoder_stack(layers, B, S, hidden, heads, head_dim, ffn, eps="9.99999997E-7
     return _module("jit_decoder", args, [tx], e.lines + [f"return {out} : {tx}"])
 
 
+def decoder_stack_scan(layers, B, S, hidden, heads, head_dim, ffn, eps="9.99999997E-7"):
+    """The decoder forward written with lax.scan over stacked layer weights
+    (the usual way to write a layer stack):
+
+        def f(x, *stacked_w, cos, sin):     # each weight array [layers, ...]
+            def step(x, w):
+                return layer(x, *w, cos, sin), None
+            return jax.lax.scan(step, x, stacked_w)[0]
+
+    lowered as jax lowers a scan: a stablehlo.while whose carry is (counter,
+    x, stacked weights), a cond of counter < layers, and a body that wraps a
+    negative index (select(i < 0, i + layers, i)), takes each layer's weights
+    with dynamic_slice + reshape, runs the layer and returns counter + 1.
+    Arguments: x, the 17 stacked weight arrays in decoder_layer's order,
+    cos, sin; returns the last layer's output [B*S, hidden] bf16."""
+    e = _Body()
+    H, D, T, A, F = heads, head_dim, B * S, heads * head_dim, ffn
+    Dh = D // 2
+
+    def w3(K, N):
+        return [([K // 2, N], "ui8"), ([K // 64, N], "bf16"), ([K // 64, N], "ui8")]
+
+    per_layer = ([([hidden], "bf16")] + w3(hidden, 3 * A) + w3(A, hidden) + [([hidden], "bf16")] +
+                 w3(hidden, F) + w3(hidden, F) + w3(F, hidden))
+    stacked = [_t([layers] + d, dt) for d, dt in per_layer]
+    tx = _t([T, hidden], "bf16")
+    ti = _t([], "i32")
+    args = [tx] + stacked + [_t([S, Dh], "f32"), _t([S, Dh], "f32")]
+    cos_arg, sin_arg = f"%arg{1 + len(per_layer)}", f"%arg{2 + len(per_layer)}"
+    th, t4 = _t([B, S, H, Dh], "f32"), _t([1, S, 1, Dh], "f32")
+    c = e.bcast(e.reshape(cos_arg, _t([S, Dh], "f32"), t4), t4, [0, 1, 2, 3], th)
+    s = e.bcast(e.reshape(sin_arg, _t([S, Dh], "f32"), t4), t4, [0, 1, 2, 3], th)
+    zero = e.const(0, "i32")
+    names = ["%iterArg", "%iterArg_0"] + [f"%iterArg_{i + 1}" for i in range(len(per_layer))]
+    inits = [zero, "%arg0"] + [f"%arg{i + 1}" for i in range(len(per_layer))]
+    types = [ti, tx] + stacked
+    loop = f"%{len(e.lines)}"
+    e.lines.append(f"{loop}:{len(names)} = stablehlo.while(" +
+                   ", ".join(f"{a} = {b}" for a, b in zip(names, inits)) + ") : " + ", ".join(types))
+    e.lines.append("cond {")
+    n_layers = e.const(layers, "i32")
+    more = e(f"stablehlo.compare  LT, %iterArg, {n_layers},  SIGNED : ({ti}, {ti}) -> {_t([], 'i1')}")
+    e.lines.append(f"stablehlo.return {more} : {_t([], 'i1')}")
+    e.lines.append("} do {")
+    c0 = e.const(0, "i32")
+    neg = e(f"stablehlo.compare  LT, %iterArg, {c0},  SIGNED : ({ti}, {ti}) -> {_t([], 'i1')}")
+    wrapped = e.bin("add", "%iterArg", e.const(layers, "i32"), ti)
+    idx = e(f"stablehlo.select {neg}, {wrapped}, %iterArg : {_t([], 'i1')}, {ti}")
+    w = []
+    for k, (d, dt) in enumerate(per_layer):
+        starts = ", ".join([idx] + [c0] * len(d))
+        t1 = _t([1] + d, dt)
+        ds = e(f"stablehlo.dynamic_slice {names[2 + k]}, {starts}, sizes = [{', '.join(map(str, [1] + d))}] : "
+               f"({stacked[k]}, {', '.join([ti] * (len(d) + 1))}) -> {t1}")
+        w.append(e.reshape(ds, t1, _t(d, dt)))
+    x_new = _decoder_layer_ops(e, "%iterArg_0", w, c, s, B, S, hidden, H, D, F, eps)
+    nxt = e.bin("add", "%iterArg", e.const(1, "i32"), ti)
+    e.lines.append(f"stablehlo.return {nxt}, {x_new}, " + ", ".join(names[2:]) + " : " + ", ".join(types))
+    e.lines.append("}")
+    return _module("jit_decoder_scan", args, [tx], e.lines + [f"return {loop}#1 : {tx}"])
+
+
+def counted_loop(trips, n=8, cond="LT", step=1, start=0):
+    """A fori_loop the plugin unrolls: def f(x): return lax.fori_loop(start,
+    trips, lambda i, x: x * 2 + i.astype(f32), x) on f32 [n], lowered as a
+    stablehlo.while over (counter, x) with the given comparison and counter
+    step (a non-counted or too long loop is an error at compile)."""
+    e = _Body()
+    tx, ti = _t([n], "f32"), _t([], "i32")
+    c0 = e.const(start, "i32")
+    loop = f"%{len(e.lines)}"
+    e.lines.append(f"{loop}:2 = stablehlo.while(%iterArg = {c0}, %iterArg_0 = %arg0) : {ti}, {tx}")
+    e.lines.append("cond {")
+    lim = e.const(trips, "i32")
+    more = e(f"stablehlo.compare  {cond}, %iterArg, {lim},  SIGNED : ({ti}, {ti}) -> {_t([], 'i1')}")
+    e.lines.append(f"stablehlo.return {more} : {_t([], 'i1')}")
+    e.lines.append("} do {")
+    two = e.splat("2.000000e+00", "f32", [n])
+    fi = e.bcast(e.cvt("%iterArg", ti, _t([], "f32")), _t([], "f32"), [], tx)
+    y = e.bin("add", e.bin("multiply", "%iterArg_0", two, tx), fi, tx)
+    nxt = e.bin("add", "%iterArg", e.const(step, "i32"), ti)
+    e.lines.append(f"stablehlo.return {nxt}, {y} : {ti}, {tx}")
+    e.lines.append("}")
+    return _module("jit_loop", [tx], [tx], e.lines + [f"return {loop}#1 : {tx}"])
+
+
 def _decoder_args_and_layers(e, layers, B, S, hidden, heads, head_dim, ffn, eps):
     """Argument types (x, per layer g_attn w_qkv(3) w_o(3) g_mlp w_gate(3)
     w_up(3) w_down(3), cos, sin) and the ops of `layers` layers into e;

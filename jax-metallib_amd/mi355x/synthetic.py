@@ -67,6 +67,16 @@ def decoder_stack_arguments(x, ws, cos, sin):
     return args + [(cos, False), (sin, False)]
 
 
+def decoder_stack_scan_arguments(x, ws, cos, sin):
+    """The arguments of programs.decoder_stack_scan in order, as (array,
+    is_bf16): each of a layer's 17 weight arrays stacked over the layers."""
+    per = [decoder_layer_arguments(None, w, None, None)[1:-2] for w in ws]
+    args = [(x, True)]
+    for k in range(len(per[0])):
+        args.append((np.ascontiguousarray(np.stack([p[k][0] for p in per])), per[0][k][1]))
+    return args + [(cos, False), (sin, False)]
+
+
 def decoder_layer_case(rng, B, S, hidden, heads, head_dim, ffn, rope_base=10000.0, weights_only=False):
     """One random-init layer of the Llama-style decoder and its input:
     (x bf16 bits [B*S, hidden], weights, cos, sin).  weights holds g_attn,

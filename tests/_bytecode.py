@@ -228,12 +228,12 @@ class _Reader:
             attrs.append(("sym_visibility", ("str", "private")))
         return Op("func.func", attrs=attrs, regions=[[(block_args, ops)]], isolated=True)
 
-    def body(self, env):
+    def body(self, env, end=("}",)):
         ops = []
         while True:
             line = self.lines[self.i]
             self.i += 1
-            if line == "}":
+            if line in end:
                 return ops
             ops.append(self.stmt(line, env))
 
@@ -310,6 +310,32 @@ class _Reader:
                     lhs.append(v0)
                     rhs_args.append(v1)
                 regions = [[(lhs + rhs_args, self.body(renv))]]
+        elif short == "while":
+            # "stablehlo.while(%iterArg = %a, ...) : types", then "cond {" ...
+            # "} do {" ... "}": two regions over the loop-carried values.
+            pairs = re.findall(r"(%[\w.$]+) = (%[\w.$#]+)", rest.split(")")[0])
+            operands = [self.ref(env, b) for _, b in pairs]
+            outs = [v.type for v in operands]
+            regions = []
+            for end in (("} do {",), ("}",)):
+                head = self.lines[self.i]
+                self.i += 1
+                assert head in ("cond {", "} do {") or head.startswith("cond"), head
+                renv = dict(env)
+                args = [Value(v.type) for v in operands]
+                for (a, _), v in zip(pairs, args):
+                    renv[a] = v
+                regions.append([(args, self.body(renv, end))])
+                if end == ("} do {",):
+                    self.i -= 1  # the "} do {" line opens the next region
+        elif short == "slice":
+            ranges = [r.split(":") for r in re.search(r"\[(.*?)\]", rest).group(1).split(",")]
+            attrs = [("start_indices", ("dims", [int(r[0]) for r in ranges])),
+                     ("limit_indices", ("dims", [int(r[1]) for r in ranges])),
+                     ("strides", ("dims", [int(r[2]) if len(r) > 2 else 1 for r in ranges]))]
+        elif short == "dynamic_slice":
+            attrs = [("slice_sizes", ("dims", _list(re.search(r"sizes = \[(.*?)\]", body).group(1))))]
+            refs = re.findall(r"%[\w.$#]+", rest.split("sizes")[0])
         elif short == "call":
             callee = re.search(r"@([\w.$]+)", body).group(1)
             attrs = [("callee", ("symbol", callee))]

@@ -377,3 +377,48 @@ def test_decoder_stack_full_config(client):
     print(f"[decoder-program] full stack vs hand-fused, all {row_rel.size} rows: per-row max measure worst "
           f"{row_rel.max():.3e}, median {np.median(row_rel):.3e} (bound {2 * max(bounds):.3e})", flush=True)
     assert row_rel.max() <= 2 * max(bounds), (np.unravel_index(int(row_rel.argmax()), row_rel.shape), row_rel.max())
+
+
+def _run_program(client, text, arrays):
+    args = [client.buffer(a, rt.BF16) if is_bf16 else client.buffer(a) for a, is_bf16 in arrays]
+    exe = client.compile(text)
+    outs, done = exe.execute(args)
+    done.wait()
+    y = outs[0].to_numpy()
+    plan = exe.plan
+    for b_ in args + outs:
+        b_.close()
+    exe.close()
+    return y, plan
+
+
+@pytest.mark.parametrize("cfg", [(3, 2, 128, 256, 2, 128, 512), (4, 4, 2048, 2048, 16, 128, 8192)],
+                         ids=["small", "full"])
+def test_scan_decoder_bit_identical_to_inline_stack(client, cfg):
+    """The decoder written with lax.scan over stacked weights (a counted
+    stablehlo.while, unrolled at compile; each layer's weights a view of the
+    stacked arrays) against the stack written layer by layer: the same
+    kernels on the same bytes, so the same bits."""
+    L, B, S, hidden, H, D, F = cfg
+    x, ws, cos, sin = synthetic.decoder_stack_case(np.random.default_rng(51), L, B, S, hidden, H, D, F)
+    print(f"[decoder-program] scan vs inline L={L} B={B} S={S} hidden={hidden}", flush=True)
+    y_scan, plan_scan = _run_program(client, P.decoder_stack_scan(L, B, S, hidden, H, D, F),
+                                     synthetic.decoder_stack_scan_arguments(x, ws, cos, sin))
+    y_inline, plan_inline = _run_program(client, P.decoder_stack(L, B, S, hidden, H, D, F),
+                                         synthetic.decoder_stack_arguments(x, ws, cos, sin))
+    assert plan_scan == plan_inline
+    assert np.array_equal(y_scan, y_inline)
+    assert np.isfinite(bf16_bits_to_f32(y_scan)).all()
+
+
+@pytest.mark.parametrize("trips", [0, 3, 16])
+def test_counted_loop_numerics(client, trips):
+    """fori_loop(0, trips, x * 2 + i) unrolled: every step is exact or one
+    f32 rounding, evaluated in the same order as numpy's float32 loop, so the
+    bits agree."""
+    x = np.random.default_rng(trips).standard_normal(8).astype(np.float32)
+    y, _ = _run_program(client, P.counted_loop(trips), [(x, False)])
+    ref = x.copy()
+    for i in range(trips):
+        ref = (ref * np.float32(2.0) + np.float32(i)).astype(np.float32)
+    assert np.array_equal(y, ref), (y, ref)
