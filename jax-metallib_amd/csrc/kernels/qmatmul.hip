@@ -651,6 +651,35 @@ __device__ __forceinline__ void lds_tr8x8(const uint32_t (&ad)[8], u32x2 (&o)[8]
       : "memory");
 }
 
+// Four transposing byte reads (the column split's 8 blocks) and their wait.
+__device__ __forceinline__ void lds_tr8x4(const uint32_t (&ad)[4], u32x2 (&o)[4]) {
+  asm volatile(
+      "ds_read_b64_tr_b8 %0, %4\n\t"
+      "ds_read_b64_tr_b8 %1, %5\n\t"
+      "ds_read_b64_tr_b8 %2, %6\n\t"
+      "ds_read_b64_tr_b8 %3, %7\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3])
+      : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3])
+      : "memory");
+}
+
+// Scales and zero points of one group for 8 column blocks (2 tr16 reads, 1
+// tr8 read): sv[0], sv[1] and zv[0] as lds_scale_zero fills them.
+__device__ __forceinline__ void lds_scale_zero_half(uint32_t sa, uint32_t za, u32x2 (&sv)[4], u32x2 (&zv)[2]) {
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %3\n\t"
+      "ds_read_b64_tr_b16 %1, %3 offset:128\n\t"
+      "ds_read_b64_tr_b8 %2, %4\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(sv[0]), "=&v"(sv[1]), "=&v"(zv[0])
+      : "v"(sa), "v"(za)
+      : "memory");
+  sv[2] = sv[0];
+  sv[3] = sv[1];
+  zv[1] = zv[0];
+}
+
 // Scales of one group for all 16 column blocks (4 tr16 reads: 4 blocks
 // each) and its zero points (2 tr8 reads: 8 blocks each).
 __device__ __forceinline__ void lds_scale_zero(uint32_t sa, uint32_t za, u32x2 (&sv)[4], u32x2 (&zv)[2]) {
@@ -730,31 +759,37 @@ __device__ __forceinline__ void wide_sum_partials_l2(__amdgpu_buffer_rsrc_t rs, 
 // tile's workgroups to arrive sums them in k order); store bf16 y, times the
 // int8 per-channel scale when FMT8.  Every DMA of the calling wave must have
 // landed: y is spilled into its own LDS region, over its ring.
-template <int NW, bool FMT8>
+// CS = 1: every wave holds all TN columns of its k range.  CS = 2: wave w
+// holds columns [128 (w % 2), +128) of its k range (NB = 8 blocks), and each
+// output column sums the NW / 2 waves of its half.
+template <int NW, bool FMT8, int CS = 1>
 __device__ __forceinline__ void wide_finish(const QArgs& a, unsigned char* smem, unsigned char* wl,
-                                            const f32x4 (&y)[kWideTN / 16], int tile, int ksi, int rb, int m0,
+                                            const f32x4 (&y)[kWideTN / 16 / CS], int tile, int ksi, int rb, int m0,
                                             int mrows, int n0, int c, int j) {
-  constexpr int TN = kWideTN, NB = TN / 16;
+  constexpr int TN = kWideTN, NB = TN / 16 / CS;
   constexpr int IT = 16 / NW;  // output quads per thread (16 rows x 64 quads)
   const size_t N = (size_t)a.N;
   const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
-  // Sum the NW waves: each spills y as [16 m][TN] f32 (padded rows) into its
-  // own region; lane (c, j) holds column 16b + c, rows 4j..4j+3.
+  // Sum the waves: each spills y as [16 m][TN] f32 (padded rows; its own
+  // columns only) into its own region; lane (c, j) holds column
+  // col0 + 16b + c, rows 4j..4j+3.
   float* red = reinterpret_cast<float*>(wl);
+  const int col0 = CS == 1 ? 0 : (TN / CS) * ((threadIdx.x >> 6) % CS);
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[(4 * j + i) * kWideRedStride + 16 * b + c] = y[b][i];
+    for (int i = 0; i < 4; ++i) red[(4 * j + i) * kWideRedStride + col0 + 16 * b + c] = y[b][i];
   __syncthreads();
   f32x4 own[IT];
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
     const int q = threadIdx.x + NW * kWave * it;  // quad index: 16 rows x 64 quads
     const int m = q >> 6, n = 4 * (q & 63);
+    const int wh = CS == 1 ? 0 : n / (TN / CS);  // the waves holding column n: wh, wh + CS, ...
     f32x4 acc = zero4;
 #pragma unroll
-    for (int w = 0; w < NW; ++w)
-      acc += *reinterpret_cast<const f32x4*>(smem + w * a.wave_lds + (m * kWideRedStride + n) * 4);
+    for (int w = 0; w < NW / CS; ++w)
+      acc += *reinterpret_cast<const f32x4*>(smem + (CS * w + wh) * a.wave_lds + (m * kWideRedStride + n) * 4);
     own[it] = acc;
   }
   const int ntiles = a.N / TN;
@@ -832,12 +867,23 @@ __device__ __forceinline__ void wide_finish(const QArgs& a, unsigned char* smem,
   }
 }
 
-template <int NW, int G, int R>  // NW waves; G 64-k groups per wave; ring of R 32-k steps
+// Column split CS = 2: 128-byte slot rows (8 chunks), chunk ch of slot row r
+// at position ch ^ (r & 2).  The transposing read of chunk pair (b, b+1),
+// b even, takes rows 4j .. 4j+3: rows 4j, 4j+2 put the pair at positions
+// {b, b+1} and {b^2, b^3} and rows 4j+1, 4j+3 lie 128 bytes further (the
+// other half of the 64 banks), so a 16-lane group touches 16 distinct
+// 8-byte bank pairs.
+__device__ __forceinline__ int wide2_swz(int r) { return r & 2; }
+
+template <int NW, int G, int R, int CS>  // NW waves; G 64-k groups per wave; ring of R 32-k steps; column split
 __global__ __launch_bounds__(NW * kWave) void int4g64_wide_kernel(QArgs a) {
-  constexpr int TN = kWideTN, NB = TN / 16, S = 2 * G;
-  constexpr int DPS = TN / 64;                             // weight DMAs per step
-  constexpr int SB = ((G * TN * 2 + 1023) / 1024) * 1024;  // scale block bytes
-  constexpr int ZB = ((G * TN + 1023) / 1024) * 1024;      // zero-point block bytes
+  constexpr int TN = kWideTN, TNW = TN / CS, NB = TNW / 16, S = 2 * G;
+  constexpr int DPS = TNW / 64;                             // weight DMAs per step
+  constexpr int SLOT = 16 * TNW;                            // one 32-k step: 16 weight rows x TNW bytes
+  constexpr int LPR = TNW / 16, RPD = 64 / LPR;             // DMA lanes per slot row, slot rows per DMA
+  constexpr int SB = ((G * TNW * 2 + 1023) / 1024) * 1024;  // scale block bytes
+  constexpr int ZB = ((G * TNW + 1023) / 1024) * 1024;      // zero-point block bytes
+  static_assert(CS == 1 || CS == 2, "column split 1 or 2");
   static_assert(R >= 2 && R <= S && G <= 4, "ring holds both steps of a group");
   extern __shared__ __align__(16) unsigned char smem[];
   const int lane = threadIdx.x & 63;
@@ -850,11 +896,13 @@ __global__ __launch_bounds__(NW * kWave) void int4g64_wide_kernel(QArgs a) {
   const int mrows = min(kQRows, a.M - m0);
   const int n0 = tile * TN;
   const int c = lane & 15, j = lane >> 4;
-  const int kbeg = ksi * (a.K / a.ks) + wv * 64 * G;
+  // wave wv: columns [TNW (wv % CS), +TNW) of the tile, k part wv / CS
+  const int n0w = n0 + TNW * (wv % CS);
+  const int kbeg = ksi * (a.K / a.ks) + (wv / CS) * 64 * G;
   const size_t N = (size_t)a.N;
   unsigned char* wl = smem + wv * a.wave_lds;
   unsigned char* ring = wl;
-  unsigned char* sblk = wl + R * kWideSlot;
+  unsigned char* sblk = wl + R * SLOT;
   unsigned char* zblk = sblk + SB;
 
   // k order inside each 64-k group g: MFMA lane group j, half h (of the two
@@ -875,28 +923,29 @@ __global__ __launch_bounds__(NW * kWave) void int4g64_wide_kernel(QArgs a) {
 #pragma unroll
   for (int q = 0; q < SB / 1024; ++q) {
     const int b = q * 1024 + 16 * lane;
-    const int g = min(b / (2 * TN), G - 1), col = (b % (2 * TN)) / 2;
-    dma16(reinterpret_cast<const uint16_t*>(a.s) + (size_t)((kbeg >> 6) + g) * N + n0 + col, sblk + q * 1024);
+    const int g = min(b / (2 * TNW), G - 1), col = (b % (2 * TNW)) / 2;
+    dma16(reinterpret_cast<const uint16_t*>(a.s) + (size_t)((kbeg >> 6) + g) * N + n0w + col, sblk + q * 1024);
   }
 #pragma unroll
   for (int q = 0; q < ZB / 1024; ++q) {
     const int b = q * 1024 + 16 * lane;
-    const int g = min(b / TN, G - 1), col = b % TN;
-    dma16(a.z + (size_t)((kbeg >> 6) + g) * N + n0 + col, zblk + q * 1024);
+    const int g = min(b / TNW, G - 1), col = b % TNW;
+    dma16(a.z + (size_t)((kbeg >> 6) + g) * N + n0w + col, zblk + q * 1024);
   }
 
-  // Step t = 2g + h: weight DMA q (= MFMA lane group j) lane L fills slot
-  // row rr = 4q + L/16 (W row kbeg/2 + 32 g + 8 q + 4 h + L/16), chunk
-  // position p = L%16 from global chunk wide_chunk(p, rr).
+  // Step t = 2g + h: weight DMA q lane L fills slot row rr = RPD q + L/LPR,
+  // chunk position p = L % LPR, from W row kbeg/2 + 32 g + 4 h + 8 (rr/4)
+  // + rr%4 (slot rows 4j .. 4j+3 are MFMA lane group j's) at the global
+  // chunk stored in position p of row rr.
   const uint8_t* wsrc[DPS];
-  int wch[DPS];
 #pragma unroll
   for (int q = 0; q < DPS; ++q) {
-    const int rr = 4 * q + (lane >> 4);
-    wsrc[q] = a.w + (size_t)(kbeg / 2 + 8 * q + (lane >> 4)) * N + n0 + 16 * wide_chunk(lane & 15, rr);
+    const int rr = RPD * q + lane / LPR, pp = lane % LPR;
+    const int ch = CS == 1 ? wide_chunk(pp, rr) : (pp ^ wide2_swz(rr));
+    wsrc[q] = a.w + (size_t)(kbeg / 2 + 8 * (rr >> 2) + (rr & 3)) * N + n0w + 16 * ch;
   }
   auto issue = [&](int t) {
-    unsigned char* slot = ring + (t % R) * kWideSlot;
+    unsigned char* slot = ring + (t % R) * SLOT;
     const int g = t >> 1, h = t & 1;
 #pragma unroll
     for (int q = 0; q < DPS; ++q) dma16(wsrc[q] + (size_t)(32 * g + 4 * h) * N, slot + q * 1024);
@@ -912,7 +961,8 @@ __global__ __launch_bounds__(NW * kWave) void int4g64_wide_kernel(QArgs a) {
   // is wbase ^ (16 b).
   const int r8 = (lane & 15) >> 1, hi = r8 >> 2;
   const int wrow = 4 * j + (r8 & 3);
-  const uint32_t woff = (uint32_t)(wrow * TN + 8 * (lane & 1) + 16 * wide_pos(hi, wrow));
+  const uint32_t woff =
+      (uint32_t)(wrow * TNW + 8 * (lane & 1) + 16 * (CS == 1 ? wide_pos(hi, wrow) : (hi ^ wide2_swz(wrow))));
   const uint32_t ring0 = lds_addr(ring);
   // Scale tr16 read: lane 4r + q of a group names row (block) r, columns 4q..4q+3.
   const uint32_t soff = lds_addr(sblk) + (uint32_t)(((lane & 15) >> 2) * 32 + 8 * (lane & 3));
@@ -929,13 +979,14 @@ __global__ __launch_bounds__(NW * kWave) void int4g64_wide_kernel(QArgs a) {
     const int g = t >> 1, h = t & 1;
     const int issued = (R + t < S) ? R + t : S;  // steps issued before this wait
     vm_wait(DPS * (issued - (t + 1)));
-    const uint32_t wb = ring0 + (uint32_t)((t % R) * kWideSlot) + woff;
+    const uint32_t wb = ring0 + (uint32_t)((t % R) * SLOT) + woff;
     u32x2 w2[NB / 2];
     {
-      uint32_t ad[8];
+      uint32_t ad[NB / 2];
 #pragma unroll
-      for (int p = 0; p < 8; ++p) ad[p] = wb ^ (uint32_t)(32 * p);
-      lds_tr8x8(ad, w2);
+      for (int p = 0; p < NB / 2; ++p) ad[p] = wb ^ (uint32_t)(32 * p);
+      if constexpr (CS == 1) lds_tr8x8(ad, w2);
+      else lds_tr8x4(ad, w2);
     }
     // This step's slot is read: refill it.
     if (t + R < S) issue(t + R);
@@ -950,7 +1001,8 @@ __global__ __launch_bounds__(NW * kWave) void int4g64_wide_kernel(QArgs a) {
       acc[b] = mfma16x16x32(A, unpack_int4((b & 1) ? w2[b >> 1].y : w2[b >> 1].x), h ? acc[b] : zero4);
     if (h) {
       u32x2 sv[4], zv[2];
-      lds_scale_zero(soff + (uint32_t)(g * 2 * TN), zoff + (uint32_t)(g * TN), sv, zv);
+      if constexpr (CS == 1) lds_scale_zero(soff + (uint32_t)(g * 2 * TN), zoff + (uint32_t)(g * TN), sv, zv);
+      else lds_scale_zero_half(soff + (uint32_t)(g * 2 * TNW), zoff + (uint32_t)(g * TNW), sv, zv);
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         const uint32_t sw = (b & 2) ? sv[b >> 2].y : sv[b >> 2].x;
@@ -963,7 +1015,7 @@ __global__ __launch_bounds__(NW * kWave) void int4g64_wide_kernel(QArgs a) {
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  wide_finish<NW, false>(a, smem, wl, y, tile, ksi, rb, m0, mrows, n0, c, j);
+  wide_finish<NW, false, CS>(a, smem, wl, y, tile, ksi, rb, m0, mrows, n0, c, j);
 }
 
 // ---------------------------------------------------------------------------
@@ -1242,6 +1294,7 @@ struct QPlan {
   int stream_steps;  // > 0: streaming kernel with this many 32-k steps per wave
   int ring;          // int8 streaming kernel: ring slots
   int wide_groups;   // > 0: wide int4 kernel with this many 64-k groups per wave
+  int wide_cs;       // wide int4 kernel: column split (1: waves split K only; 2: also the columns in halves)
   int wide8_steps;   // > 0: wide int8 kernel with this many 32-k steps per wave
   int deq;           // 1: dequantise W to bf16 in the workspace, then the bf16 GEMM
   int qg;            // 1: the many-row kernel of qgemm.hip (K split ks ways)
@@ -1307,10 +1360,15 @@ bool plan_stream(int fmt, int64_t K, int64_t N, QPlan* p) {
 // waves of G groups.  At the headline with 8 waves (G = 2, 4 steps per wave)
 // a 2-step ring measured 13.3 us against 13.7 us for 3 steps and 13.6 us
 // for all 4 in flight at once.  MK_QMM_WIDE_RING overrides it (sweeps).
+// Column split (the default): 2 KB steps, 2 in flight per wave; at the
+// headline it measured 11.96 us against 12.46 us with 4 in flight, 13.34 with
+// 8, and 12.61 us for the unsplit 4 KB steps (same box, same run).
 constexpr int kWideWaves = 8;
-int wide_ring(int nw, int G) {
+constexpr int kWideColumnSplit = 2;
+int wide_ring(int nw, int G, int cs = 1) {
   const int r = env_int("MK_QMM_WIDE_RING", 0);
   if (r >= 2 && r <= 2 * G && (r == 2 || r == 4 || r == 8)) return r;
+  if (cs == 2) return 2;
   if (nw == 4) return G == 4 ? 4 : 2 * G;
   return G == 4 ? 4 : G == 2 ? 2 : 2 * G;
 }
@@ -1319,8 +1377,9 @@ bool plan_wide(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p) {
   const char* env = getenv("MK_QMM_WIDE");
   if (fmt != MK_QFMT_INT4_G64 || N % mk::kWideTN != 0 || (env && env[0] == '0')) return false;
   const int nw = env_int("MK_QMM_WIDE_NW", kWideWaves);
-  if (nw != 4 && nw != 8) return false;
-  const int64_t kunit = (int64_t)nw * 64;  // k per workgroup and group-per-wave
+  const int cs = nw == 8 ? env_int("MK_QMM_WIDE_CS", kWideColumnSplit) : 1;
+  if ((nw != 4 && nw != 8) || (cs != 1 && cs != 2)) return false;
+  const int64_t kunit = (int64_t)(nw / cs) * 64;  // k per workgroup and group-per-wave
   if (K % kunit != 0) return false;
   const int ntiles = (int)(N / mk::kWideTN);
   const int rb = (int)((M + mk::kQRows - 1) / mk::kQRows);
@@ -1338,13 +1397,15 @@ bool plan_wide(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p) {
   }
   if (best == 0 || (int64_t)ntiles * rb * best < 128) return false;
   const int G = (int)(K / ((int64_t)best * kunit));
-  const int R = wide_ring(nw, G);
-  const int sb = ((G * mk::kWideTN * 2 + 1023) / 1024) * 1024, zb = ((G * mk::kWideTN + 1023) / 1024) * 1024;
-  int wl = R * mk::kWideSlot + sb + zb;
+  const int R = wide_ring(nw, G, cs);
+  const int tnw = mk::kWideTN / cs;
+  const int sb = ((G * tnw * 2 + 1023) / 1024) * 1024, zb = ((G * tnw + 1023) / 1024) * 1024;
+  int wl = R * 16 * tnw + sb + zb;
   wl = std::max(wl, mk::kQRows * mk::kWideRedStride * 4);
   wl = (wl + 255) & ~255;
   p->ks = best;
   p->nw = nw;
+  p->wide_cs = cs;
   p->ntiles = ntiles;
   p->rowblocks = rb;
   p->wide_groups = G;
@@ -1473,21 +1534,21 @@ hipError_t lds_opt_in(const void* fn, size_t bytes) {
 
 hipError_t launch_reduce(int fmt, const mk::QArgs& a, hipStream_t st);
 
-template <int NW, int G, int R>
+template <int NW, int G, int R, int CS>
 hipError_t launch_wide_nwgr(const mk::QArgs& a, const QPlan& p, hipStream_t st) {
   dim3 grid(p.ntiles * p.ks, p.rowblocks), block(NW * mk::kWave);
-  hipError_t e = lds_opt_in((const void*)mk::int4g64_wide_kernel<NW, G, R>, p.lds_bytes);
+  hipError_t e = lds_opt_in((const void*)mk::int4g64_wide_kernel<NW, G, R, CS>, p.lds_bytes);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((mk::int4g64_wide_kernel<NW, G, R>), grid, block, p.lds_bytes, st, a);
+  hipLaunchKernelGGL((mk::int4g64_wide_kernel<NW, G, R, CS>), grid, block, p.lds_bytes, st, a);
   return hipGetLastError();
 }
 
-template <int NW, int G>
+template <int NW, int G, int CS = 1>
 hipError_t launch_wide(const mk::QArgs& a, const QPlan& p, hipStream_t st) {
-  switch (wide_ring(NW, G)) {
-    case 2: return launch_wide_nwgr<NW, G, 2>(a, p, st);
-    case 4: if constexpr (2 * G >= 4) return launch_wide_nwgr<NW, G, 4>(a, p, st); break;
-    case 8: if constexpr (2 * G >= 8) return launch_wide_nwgr<NW, G, 8>(a, p, st); break;
+  switch (wide_ring(NW, G, CS)) {
+    case 2: return launch_wide_nwgr<NW, G, 2, CS>(a, p, st);
+    case 4: if constexpr (2 * G >= 4) return launch_wide_nwgr<NW, G, 4, CS>(a, p, st); break;
+    case 8: if constexpr (2 * G >= 8) return launch_wide_nwgr<NW, G, 8, CS>(a, p, st); break;
   }
   return hipErrorInvalidValue;
 }
@@ -1662,13 +1723,21 @@ int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, v
     const int gx = p.ntiles * p.ks;
     a.xch_local = p.ks > 1 && gx % 8 == 0 && (gx / 8) % p.ks == 0 &&
                   xcd_round_robin(dim3(gx, p.rowblocks), st, reinterpret_cast<uint32_t*>(a.part));
-    switch (p.wide_groups * (p.nw == 4 ? -1 : 1)) {
-      case 1: e = launch_wide<8, 1>(a, p, st); break;
-      case 2: e = launch_wide<8, 2>(a, p, st); break;
-      case 4: e = launch_wide<8, 4>(a, p, st); break;
-      case -1: e = launch_wide<4, 1>(a, p, st); break;
-      case -2: e = launch_wide<4, 2>(a, p, st); break;
-      default: e = launch_wide<4, 4>(a, p, st); break;
+    if (p.wide_cs == 2) {
+      switch (p.wide_groups) {
+        case 1: e = launch_wide<8, 1, 2>(a, p, st); break;
+        case 2: e = launch_wide<8, 2, 2>(a, p, st); break;
+        default: e = launch_wide<8, 4, 2>(a, p, st); break;
+      }
+    } else {
+      switch (p.wide_groups * (p.nw == 4 ? -1 : 1)) {
+        case 1: e = launch_wide<8, 1>(a, p, st); break;
+        case 2: e = launch_wide<8, 2>(a, p, st); break;
+        case 4: e = launch_wide<8, 4>(a, p, st); break;
+        case -1: e = launch_wide<4, 1>(a, p, st); break;
+        case -2: e = launch_wide<4, 2>(a, p, st); break;
+        default: e = launch_wide<4, 4>(a, p, st); break;
+      }
     }
   } else if (p.wide8_steps > 0) {
     if (p.part_bytes > 0) a.cnt = static_cast<uint32_t*>(ws);

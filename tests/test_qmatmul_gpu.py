@@ -274,12 +274,17 @@ WIDE_SHAPES = [
 ]
 
 
+@pytest.mark.parametrize("cs", ["1", "2"], ids=["all-columns", "column-split"])
 @pytest.mark.parametrize("M,K,N", WIDE_SHAPES)
-def test_int4_wide_kernel_matches_oracle(M, K, N):
+def test_int4_wide_kernel_matches_oracle(monkeypatch, M, K, N, cs):
+    """Both wave layouts of the wide kernel: every wave over all 256 columns
+    (MK_QMM_WIDE_CS=1) and waves split over two 128-column halves (the
+    default), against the C oracle."""
     ops = _ops()
+    monkeypatch.setenv("MK_QMM_WIDE_CS", cs)
     rng = np.random.default_rng(7 * M + K + N)
     x, packed, s, z = quant.make_int4_case(rng, M, K, N)
-    print(f"int4 wide case M={M} K={K} N={N}", flush=True)
+    print(f"int4 wide case M={M} K={K} N={N} cs={cs}", flush=True)
     y = ops.int4_g64_matmul(dev_bf16(x), dev(packed), dev_bf16(s), dev(z))
     torch.cuda.synchronize()
     ref = cport.int4_g64_matmul(x, packed, s, z)
