@@ -255,11 +255,6 @@ def bench_rowop(torch, ops, kind, dtype, steps, warmup, rows=8192, cols=8192):
     else:
         out = torch.empty((rows, cols), dtype=tdt, device="cuda")
         moved = 2 * per + (cols * esz if kind == "rmsnorm" else 0)
-    prog = [("LOAD", 0, 0, 0, 0, 0.0), ("CONST", 1, 0, 0, 0, 1.5), ("MUL", 2, 0, 1, 0, 0.0),
-            ("CONST", 1, 0, 0, 0, 0.5), ("ADD", 3, 2, 1, 0, 0.0), ("EXP", 4, 3, 0, 0, 0.0),
-            ("LOG1P", 5, 4, 0, 0, 0.0), ("MAX", 6, 5, 0, 0, 0.0), ("CONST", 1, 0, 0, 0, 0.0),
-            ("CMP_GT", 7, 0, 1, 0, 0.0), ("SELECT", 8, 7, 6, 3, 0.0)]
-
     def fn(i):
         x = xs[i]
         if kind == "softmax":
@@ -269,17 +264,20 @@ def bench_rowop(torch, ops, kind, dtype, steps, warmup, rows=8192, cols=8192):
         elif kind == "argmax":
             ops.argmax(x, out=out)
         else:
-            ops.elementwise(prog, [x], out_slot=8, out=out)
+            ops.elementwise(CHAIN6, [x], out_slot=8, out=out)
 
     secs, n = time_graph_launches(torch, fn, nsets, steps, warmup)
     t = secs / n
     return {"sec_per_call": t, "gbs": moved / t / 1e9, "bytes": moved}
 
 
-def _hbm_entry(gbs, us, extra=None):
+def _hbm_entry(gbs, us, extra=None, profile=None):
+    """A secondary HBM-bound line; `profile` names the committed counter
+    summary (profiles/<profile>_traffic.md) its roofline.traffic comes from."""
+    traffic, note = traffic_from_profiles(profile) if profile else (None, "no traffic profile")
     e = {"value": round(gbs, 2), "unit": "GB/s", "us_per_call": round(us, 3),
          "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
+                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_note": note}}
     if extra:
         e.update(extra)
     return e
@@ -328,74 +326,107 @@ def traffic_from_profiles(kernel):
     return value, f"measured with sources {digest} (current)"
 
 
-def profile_run(torch, ops, kind, steps):
-    """Eager (no graph) launches of one kernel for PMC collection, followed by
-    a plain 256 MiB device copy (8 times) that calibrates FETCH_SIZE and
-    WRITE_SIZE.  Returns the kernel's mean time per launch (HIP events on the
-    launch stream)."""
+# The 6-op elementwise chain of the row-op lines: select(x > 0, max(log1p(exp(1.5 x + 0.5)), 0), 1.5 x + 0.5).
+CHAIN6 = [("LOAD", 0, 0, 0, 0, 0.0), ("CONST", 1, 0, 0, 0, 1.5), ("MUL", 2, 0, 1, 0, 0.0),
+          ("CONST", 1, 0, 0, 0, 0.5), ("ADD", 3, 2, 1, 0, 0.0), ("EXP", 4, 3, 0, 0, 0.0),
+          ("LOG1P", 5, 4, 0, 0, 0.0), ("MAX", 6, 5, 0, 0, 0.0), ("CONST", 1, 0, 0, 0, 0.0),
+          ("CMP_GT", 7, 0, 1, 0, 0.0), ("SELECT", 8, 7, 6, 3, 0.0)]
+
+PROFILE_KINDS = ("int4", "int8", "gemm", "qgemm", "int4_m1", "int8_m1", "int4_shard", "int8_shard", "bmm",
+                 "dequant4096", "attention", "softmax_f32", "softmax_bf16", "rmsnorm_f32", "rmsnorm_bf16",
+                 "argmax_f32", "argmax_bf16", "chain6_f32", "chain6_bf16")
+
+
+def _profile_case(torch, ops, kind):
+    """One input set of a bench line's workload, resident on the device, and
+    the call that runs it once (eagerly, on the current stream)."""
+    from mi355x import synthetic
+
+    def bf(a):
+        return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).cuda()
+
+    rng = np.random.default_rng(0)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    quant = {"int4": (16, 14336), "qgemm": (256, 14336), "int4_m1": (1, 14336), "int4_shard": (16, 1792),
+             "dequant4096": (4096, 14336)}
+    if kind in quant:
+        M, N = quant[kind]
+        x, packed, s, z = synthetic.int4_case(rng, M, 4096, N)
+        xd, wd, sd, zd = bf(x), torch.from_numpy(packed).cuda(), bf(s), torch.from_numpy(z).cuda()
+        yd = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+        return lambda: ops.int4_g64_matmul(xd, wd, sd, zd, out=yd)
+    if kind in ("int8", "int8_m1", "int8_shard"):
+        M, N = {"int8": (16, 14336), "int8_m1": (1, 14336), "int8_shard": (16, 1792)}[kind]
+        x, w8, s8 = synthetic.int8_case(rng, M, 4096, N)
+        xd, wd, sd = bf(x), torch.from_numpy(w8).cuda(), torch.from_numpy(s8).cuda()
+        yd = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+        return lambda: ops.int8_pc_matmul(xd, wd, sd, out=yd)
+    if kind in ("gemm", "bmm"):
+        batch, M, N, K = (1, 4096, 4096, 4096) if kind == "gemm" else (16, 2048, 2048, 128)
+        sc = 1.0 / np.sqrt(np.sqrt(K))
+        a = (torch.randn((batch, M, K), device="cuda", generator=g) * sc).to(torch.bfloat16)
+        b = (torch.randn((batch, K, N), device="cuda", generator=g) * sc).to(torch.bfloat16)
+        c = torch.empty((batch, M, N), dtype=torch.bfloat16, device="cuda")
+        if kind == "gemm":
+            a, b, c = a[0], b[0], c[0]
+        return lambda: ops.gemm_bf16(a, b, out=c)
+    if kind == "attention":
+        # The decoder's attention at the workload's shape: 4 x 16 heads of
+        # 2048 positions x 128, causal, heads merged on output.
+        B, H, S, D = 4, 16, 2048, 128
+        q, k, v = [torch.randn((B * H, S, D), device="cuda", generator=g).to(torch.bfloat16) for _ in range(3)]
+        o = torch.empty((B * S, H * D), dtype=torch.bfloat16, device="cuda")
+        return lambda: ops.attention_causal(q, k, v, B, H, 1.0 / np.sqrt(D), out=o)
+    op, dt = kind.rsplit("_", 1)
+    tdt = torch.float32 if dt == "f32" else torch.bfloat16
+    x = (torch.randn((8192, 8192), device="cuda", generator=g) * np.sqrt(2.0)).to(tdt)
+    gam = (torch.rand((8192,), device="cuda", generator=g) + 0.5).to(tdt)
+    if op == "argmax":
+        out = torch.empty((8192,), dtype=torch.int32, device="cuda")
+        return lambda: ops.argmax(x, out=out)
+    out = torch.empty_like(x)
+    if op == "softmax":
+        return lambda: ops.softmax(x, out=out)
+    if op == "rmsnorm":
+        return lambda: ops.rmsnorm(x, gam, out=out)
+    return lambda: ops.elementwise(CHAIN6, [x], out_slot=8, out=out)
+
+
+def profile_run(torch, ops, kinds, steps):
+    """Eager (no graph) launches of each listed workload in turn (5 warm-up
+    calls + `steps` timed ones, one input set each), for rocprofv3 --pmc and
+    kernel-trace runs, followed by a plain 256 MiB device copy (8 times) that
+    calibrates FETCH_SIZE and WRITE_SIZE.  Returns {kind: seconds per call}
+    (HIP events on the launch stream)."""
+    times = {}
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
-        if kind == "int4":
-            from mi355x import synthetic
-            M, K, N = 16, 4096, 14336
-            rng = np.random.default_rng(0)
-            x, packed, s, z = synthetic.int4_case(rng, M, K, N)
-            xd = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).cuda()
-            wd, zd = torch.from_numpy(packed).cuda(), torch.from_numpy(z).cuda()
-            sd = torch.from_numpy(s.view(np.int16)).view(torch.bfloat16).cuda()
-            yd = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
-
-            def fn():
-                ops.int4_g64_matmul(xd, wd, sd, zd, out=yd)
-        elif kind == "gemm":
-            g = torch.Generator(device="cuda").manual_seed(0)
-            a = (torch.randn((4096, 4096), device="cuda", generator=g) / 8).to(torch.bfloat16)
-            b = (torch.randn((4096, 4096), device="cuda", generator=g) / 8).to(torch.bfloat16)
-            c = torch.empty((4096, 4096), dtype=torch.bfloat16, device="cuda")
-
-            def fn():
-                ops.gemm_bf16(a, b, out=c)
-        elif kind == "int8":
-            from mi355x import synthetic
-            M, K, N = 16, 4096, 14336
-            rng = np.random.default_rng(0)
-            x, w8, s8 = synthetic.int8_case(rng, M, K, N)
-            xd = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).cuda()
-            wd, sd = torch.from_numpy(w8).cuda(), torch.from_numpy(s8).cuda()
-            yd = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
-
-            def fn():
-                ops.int8_pc_matmul(xd, wd, sd, out=yd)
-        elif kind == "qgemm":
-            from mi355x import synthetic
-            M, K, N = 256, 4096, 14336
-            rng = np.random.default_rng(0)
-            x, packed, s, z = synthetic.int4_case(rng, M, K, N)
-            xd = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).cuda()
-            wd, zd = torch.from_numpy(packed).cuda(), torch.from_numpy(z).cuda()
-            sd = torch.from_numpy(s.view(np.int16)).view(torch.bfloat16).cuda()
-            yd = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
-
-            def fn():
-                ops.int4_g64_matmul(xd, wd, sd, zd, out=yd)
-        else:
-            raise SystemExit(f"bench.py: unknown --profile kind {kind}")
-        for _ in range(5):
-            fn()
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for _ in range(steps):
-            fn()
-        end.record(stream)
-        torch.cuda.synchronize()
-        t = start.elapsed_time(end) / 1e3 / steps
+        for kind in kinds:
+            if kind not in PROFILE_KINDS:
+                raise SystemExit(f"bench.py: unknown --profile kind {kind} (one of {', '.join(PROFILE_KINDS)})")
+            # A one-thread spin kernel marks where this workload's
+            # dispatches begin in the profiler's dispatch-ordered output.
+            torch.cuda._sleep(100)
+            fn = _profile_case(torch, ops, kind)
+            for _ in range(5):
+                fn()
+            torch.cuda.synchronize()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            for _ in range(steps):
+                fn()
+            end.record(stream)
+            torch.cuda.synchronize()
+            times[kind] = start.elapsed_time(end) / 1e3 / steps
+            print(f"[profile] {kind}: {times[kind] * 1e6:.3f} us per call", flush=True)
+            del fn
+            torch.cuda.empty_cache()
         src = torch.empty(256 * 2 ** 20, dtype=torch.uint8, device="cuda").fill_(1)
         dst = torch.empty_like(src)
         for _ in range(8):
             dst.copy_(src)
         torch.cuda.synchronize()
-    return t
+    return times
 
 
 def profile_layer(steps):
@@ -668,8 +699,9 @@ def main():
                     help="comma list of secondary workloads (int8,qmm_m,shard,gemm,decoder,softmax,rmsnorm,argmax,chain6,e2e), "
                          "or 'none'")
     ap.add_argument("--profile", default="",
-                    help="int4 | int8 | gemm | qgemm: eager launches of one kernel plus a 256 MiB copy calibration, "
-                         "for rocprofv3 --pmc runs (prints the kernel's us/launch); layer: the decoder layer's "
+                    help="comma list of workloads (" + ", ".join(PROFILE_KINDS) + "): eager launches of each in turn "
+                         "plus a 256 MiB copy calibration, for rocprofv3 --pmc runs (prints us/launch); layer: the "
+                         "decoder layer's "
                          "StableHLO compiled once and executed --steps times (median wall time per call)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -683,9 +715,12 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     if args.profile:
-        t = profile_layer(args.steps) if args.profile == "layer" else profile_run(torch, ops, args.profile, args.steps)
-        print(json.dumps({"profile": args.profile, "us_per_launch": round(t * 1e6, 3), "steps": args.steps}),
-              flush=True)
+        if args.profile == "layer":
+            t = {"layer": profile_layer(args.steps)}
+        else:
+            t = profile_run(torch, ops, args.profile.split(","), args.steps)
+        print(json.dumps({"profile": args.profile, "us_per_launch": {k: round(v * 1e6, 3) for k, v in t.items()},
+                          "steps": args.steps}), flush=True)
         return
     only = set(filter(None, args.only.split(",")))
 
@@ -716,7 +751,8 @@ def main():
                 tf = 2 * M * 4096 * 14336 / r["sec_per_call"] / 1e12
                 log(f"[bench] {fmt} M={M}: {r['sec_per_call'] * 1e6:.1f} us, {r['gbs']:.0f} GB/s, {tf:.1f} TFLOP/s")
                 if M == 1:
-                    entry = _hbm_entry(r["gbs"], r["sec_per_call"] * 1e6, {"tflops": round(tf, 2)})
+                    entry = _hbm_entry(r["gbs"], r["sec_per_call"] * 1e6, {"tflops": round(tf, 2)},
+                                       profile=f"{'int4g64' if fmt == 'int4' else 'int8pc'}_M1_K4096_N14336")
                 else:
                     entry = {"value": round(tf, 2), "unit": "TFLOP/s", "us_per_call": round(r["sec_per_call"] * 1e6, 3),
                              "gbs": round(r["gbs"], 2),
@@ -726,6 +762,11 @@ def main():
                     if M == 256 and fmt == "int4":
                         qt, qn = traffic_from_profiles("qgemm_kernel_M256_K4096_N14336")
                         entry["roofline"].update({"traffic": qt, "traffic_note": qn})
+                    if M == 4096 and fmt == "int4":
+                        # The route's HBM-bound first pass (W int4 -> bf16), beside the GEMM's MFMA roofline.
+                        dt, dn = traffic_from_profiles("qmm_dequant_kernel_int4_K4096_N14336")
+                        entry["dequant_pass"] = {"kernel": "qmm_dequant_kernel<true>", "algorithmic_bytes": 149553152,
+                                                 "traffic": dt, "traffic_note": dn}
                 secondary[f"{fmt}_dequant_matmul_M{M}"] = entry
 
     if want("shard"):
@@ -737,7 +778,8 @@ def main():
             log(f"[bench] {fmt} per-shard M=16 N=1792: {r['sec_per_call'] * 1e6:.2f} us, {r['gbs']:.0f} GB/s")
             secondary[f"{fmt}_dequant_matmul_M16_shard_N1792"] = _hbm_entry(
                 r["gbs"], r["sec_per_call"] * 1e6,
-                {"what": "one of 8 GPUs' share of the headline shape when sharded by N (K=4096, N=1792)"})
+                {"what": "one of 8 GPUs' share of the headline shape when sharded by N (K=4096, N=1792)"},
+                profile=f"{'int4g64' if fmt == 'int4' else 'int8pc'}_shard_M16_K4096_N1792")
 
     if want("gemm"):
         log("[bench] bf16 GEMM 4096^3 ...")
@@ -765,7 +807,8 @@ def main():
         gbs = rb["bytes"] / rb["sec_per_call"] / 1e9
         log(f"[bench] batched bf16 gemm: {rb['sec_per_call'] * 1e6:.1f} us, {rb['tflops']:.1f} TFLOP/s, {gbs:.0f} GB/s")
         secondary["bf16_bmm_16x2048x128x2048"] = _hbm_entry(gbs, rb["sec_per_call"] * 1e6,
-                                                           {"tflops": round(rb["tflops"], 2)})
+                                                           {"tflops": round(rb["tflops"], 2)},
+                                                           profile="gemm_bf16_batched_16x2048x128x2048")
         rf = bench_gemm_f32(torch, ops, max(50, args.steps // 20), 5)
         log(f"[bench] f32 gemm 2048^3: {rf['sec_per_call'] * 1e6:.1f} us, {rf['tflops']:.1f} TFLOP/s")
         secondary["f32_gemm_2048"] = {
@@ -786,7 +829,9 @@ def main():
         for dt in ("f32", "bf16"):
             r = bench_rowop(torch, ops, kind, dt, max(50, args.steps // 10), 5)
             log(f"[bench] {kind} {dt} 8192x8192: {r['sec_per_call'] * 1e6:.1f} us, {r['gbs']:.0f} GB/s")
-            entry = _hbm_entry(r["gbs"], r["sec_per_call"] * 1e6)
+            prof = (f"mk_ew_jit_chain6_{dt}_8192x8192" if kind == "chain6"
+                    else f"row_cached_kernel_{kind}_{dt}_8192x8192")
+            entry = _hbm_entry(r["gbs"], r["sec_per_call"] * 1e6, profile=prof)
             if not args.no_cpu:
                 entry["cpu_baseline"] = cpu_baseline_rowop(kind, dt, args.cpu_row_seconds)
                 log(f"[bench] cpu {kind} {dt}: {entry['cpu_baseline']['value']} GB/s")

@@ -168,6 +168,17 @@ __device__ __forceinline__ void ld4_sc1(const float* p0, const float* p1, const 
       : "memory");
 }
 
+// Two device-coherent 16-byte loads in flight together.
+__device__ __forceinline__ void ld2_sc1(const float* p0, const float* p1, f32x4& v0, f32x4& v1) {
+  asm volatile(
+      "global_load_dwordx4 %0, %2, off sc1\n\t"
+      "global_load_dwordx4 %1, %3, off sc1\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=&v"(v0), "=&v"(v1)
+      : "v"(p0), "v"(p1)
+      : "memory");
+}
+
 // Two device-coherent 16-byte stores (sc1: written through past the per-XCD
 // L2) and the wait for their acknowledgement, in one block: no instruction
 // may overwrite a store's data registers before the store has read them (a
@@ -698,17 +709,19 @@ __device__ __forceinline__ void lds_scale_zero(uint32_t sa, uint32_t za, u32x2 (
 
 // y quads of this thread = the KS split-K partials (this workgroup's among
 // them, already acknowledged) summed in k order.
-template <int NW, int KS>
-__device__ __forceinline__ void wide_sum_partials(const float* tile_part, f32x4 (&own)[16 / NW]) {
-  constexpr int IT = 16 / NW;  // quads per thread: 16 rows x 64 quads over NW waves
+template <int NW, int KS, int TN = kWideTN>
+__device__ __forceinline__ void wide_sum_partials(const float* tile_part, f32x4 (&own)[TN / 16 / NW]) {
+  constexpr int IT = TN / 16 / NW;  // quads per thread: 16 rows x TN/4 quads over NW waves
   f32x4 v[IT][KS];
   const float* src[IT][KS];
 #pragma unroll
   for (int it = 0; it < IT; ++it)
 #pragma unroll
     for (int k2 = 0; k2 < KS; ++k2)
-      src[it][k2] = tile_part + (size_t)k2 * kQRows * kWideTN + 4 * (threadIdx.x + NW * kWave * it);
-  if constexpr (KS == 2) {
+      src[it][k2] = tile_part + (size_t)k2 * kQRows * TN + 4 * (threadIdx.x + NW * kWave * it);
+  if constexpr (KS == 2 && IT == 1) {
+    ld2_sc1(src[0][0], src[0][1], v[0][0], v[0][1]);
+  } else if constexpr (KS == 2) {
 #pragma unroll
     for (int it = 0; it < IT; it += 2)
       ld4_sc1(src[it][0], src[it][1], src[it + 1][0], src[it + 1][1], v[it][0], v[it][1], v[it + 1][0],
@@ -733,26 +746,40 @@ __device__ __forceinline__ void wide_sum_partials(const float* tile_part, f32x4 
 #ifndef XCH_STORE_POLICY
 #define XCH_STORE_POLICY kSc1
 #endif
-// The same sum for the exchange inside one XCD's L2: loads that miss only
-// the CU's L1 (sc0), through the tile's buffer resource `rs`.
-template <int NW, int KS>
-__device__ __forceinline__ void wide_sum_partials_l2(__amdgpu_buffer_rsrc_t rs, f32x4 (&own)[16 / NW]) {
-  constexpr int IT = 16 / NW;
-  u32x4 v[IT][KS];
+// The sum for the exchange inside one XCD's L2: loads served by the L2
+// (first touch of these lines on this CU), through the tile's buffer
+// resource `rs`, with this
+// workgroup's own partial (split ksi) taken from registers: it was never
+// stored.  The sum is the device-scope path's k-order sum, bit for bit.
+template <int NW, int KS, int TN>
+__device__ __forceinline__ void wide_sum_partials_l2_own(__amdgpu_buffer_rsrc_t rs, int ksi,
+                                                         f32x4 (&own)[TN / 16 / NW]) {
+  constexpr int IT = TN / 16 / NW;
+  // v[it][i]: split i + (i >= ksi), every load in flight together (no
+  // branches between them).
+  u32x4 v[IT][KS - 1];
 #pragma unroll
   for (int it = 0; it < IT; ++it)
 #pragma unroll
-    for (int k2 = 0; k2 < KS; ++k2)
-      v[it][k2] = __builtin_amdgcn_raw_buffer_load_b128(
-          rs, (k2 * kQRows * kWideTN + 4 * (threadIdx.x + NW * kWave * it)) * 4, 0, kSc0);
+    for (int i = 0; i < KS - 1; ++i)
+      v[it][i] = __builtin_amdgcn_raw_buffer_load_b128(
+          rs, ((i + (i >= ksi)) * kQRows * TN + 4 * (threadIdx.x + NW * kWave * it)) * 4, 0, kSc0);
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
-    f32x4 acc = __builtin_bit_cast(f32x4, v[it][0]);
+    f32x4 p[KS];
 #pragma unroll
-    for (int k2 = 1; k2 < KS; ++k2) acc += __builtin_bit_cast(f32x4, v[it][k2]);
+    for (int k2 = 0; k2 < KS; ++k2) {
+      const f32x4 below = __builtin_bit_cast(f32x4, v[it][k2 < KS - 1 ? k2 : KS - 2]);
+      const f32x4 above = __builtin_bit_cast(f32x4, v[it][k2 > 0 ? k2 - 1 : 0]);
+      p[k2] = k2 < ksi ? below : (k2 == ksi ? own[it] : above);
+    }
+    f32x4 acc = p[0];
+#pragma unroll
+    for (int k2 = 1; k2 < KS; ++k2) acc += p[k2];
     own[it] = acc;
   }
 }
+
 
 // The end of both wide kernels.  Sum the 8 waves' y tiles through LDS;
 // with ks > 1 combine the split-K partials across workgroups (the last of a
@@ -761,13 +788,15 @@ __device__ __forceinline__ void wide_sum_partials_l2(__amdgpu_buffer_rsrc_t rs, 
 // landed: y is spilled into its own LDS region, over its ring.
 // CS = 1: every wave holds all TN columns of its k range.  CS = 2: wave w
 // holds columns [128 (w % 2), +128) of its k range (NB = 8 blocks), and each
-// output column sums the NW / 2 waves of its half.
-template <int NW, bool FMT8, int CS = 1>
+// output column sums the NW / 2 waves of its half.  TN: the tile's columns
+// (256, or 128 for the narrow tiles, whose waves all hold the whole tile).
+template <int NW, bool FMT8, int CS = 1, int TN = kWideTN>
 __device__ __forceinline__ void wide_finish(const QArgs& a, unsigned char* smem, unsigned char* wl,
-                                            const f32x4 (&y)[kWideTN / 16 / CS], int tile, int ksi, int rb, int m0,
+                                            const f32x4 (&y)[TN / 16 / CS], int tile, int ksi, int rb, int m0,
                                             int mrows, int n0, int c, int j) {
-  constexpr int TN = kWideTN, NB = TN / 16 / CS;
-  constexpr int IT = 16 / NW;  // output quads per thread (16 rows x 64 quads)
+  constexpr int NB = TN / 16 / CS, QPR = TN / 4;  // y blocks per wave; output quads per row
+  constexpr int RS = TN + 4;                      // padded f32 row of the y spill
+  constexpr int IT = 16 * QPR / (NW * kWave);     // output quads per thread
   const size_t N = (size_t)a.N;
   const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
   // Sum the waves: each spills y as [16 m][TN] f32 (padded rows; its own
@@ -778,28 +807,33 @@ __device__ __forceinline__ void wide_finish(const QArgs& a, unsigned char* smem,
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[(4 * j + i) * kWideRedStride + col0 + 16 * b + c] = y[b][i];
+    for (int i = 0; i < 4; ++i) red[(4 * j + i) * RS + col0 + 16 * b + c] = y[b][i];
   __syncthreads();
   f32x4 own[IT];
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
-    const int q = threadIdx.x + NW * kWave * it;  // quad index: 16 rows x 64 quads
-    const int m = q >> 6, n = 4 * (q & 63);
+    const int q = threadIdx.x + NW * kWave * it;  // quad index: 16 rows x QPR quads
+    const int m = q / QPR, n = 4 * (q % QPR);
     const int wh = CS == 1 ? 0 : n / (TN / CS);  // the waves holding column n: wh, wh + CS, ...
     f32x4 acc = zero4;
 #pragma unroll
     for (int w = 0; w < NW / CS; ++w)
-      acc += *reinterpret_cast<const f32x4*>(smem + (CS * w + wh) * a.wave_lds + (m * kWideRedStride + n) * 4);
+      acc += *reinterpret_cast<const f32x4*>(smem + (CS * w + wh) * a.wave_lds + (m * RS + n) * 4);
     own[it] = acc;
   }
   const int ntiles = a.N / TN;
+  uint32_t* ctr = a.cnt + rb * ntiles + tile;
+  asm volatile("" : "+v"(ctr));  // per-lane address: a vector atomic
   if (a.ks > 1 && a.xch_local) {
     // Every workgroup of this tile runs on this XCD (the host checked that
     // the grid deals each tile's ks workgroups to one XCD), so the exchange
-    // stays in its L2: plain stores (acknowledged by the L2), a
-    // workgroup-scope atomic (performed in the L2), and loads that miss
-    // only the CU's own L1 (sc0).  The ordering argument is the
-    // device-scope one below with the L2 as the common coherence point.
+    // stays in its L2: stores acknowledged by the L2, a workgroup-scope
+    // atomic (performed in the L2), and loads the L2 serves (the CU's L1
+    // holds no line of the tile's partials: it starts the kernel
+    // invalidated, and only the tile's last arriver loads them, once).  The
+    // ordering argument is the device-scope one below with the L2 as the
+    // common coherence point; the last arriver takes its own partial from
+    // registers.
     const size_t tbase = ((size_t)(rb * ntiles + tile) * a.ks) * kQRows * TN;
     float* tp = a.part + tbase;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(tp, 0, a.ks * kQRows * TN * 4, kBufWord3);
@@ -812,8 +846,6 @@ __device__ __forceinline__ void wide_finish(const QArgs& a, unsigned char* smem,
     __syncthreads();  // (also: every wave is done reading the spills)
     volatile uint32_t* flag = reinterpret_cast<volatile uint32_t*>(smem);
     if (threadIdx.x == 0) {
-      uint32_t* ctr = a.cnt + rb * ntiles + tile;
-      asm volatile("" : "+v"(ctr));  // per-lane address: a vector atomic
       const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       const uint32_t last = old == (uint32_t)(a.ks - 1);
       if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -821,27 +853,27 @@ __device__ __forceinline__ void wide_finish(const QArgs& a, unsigned char* smem,
     }
     __syncthreads();
     if (!*flag) return;
-    // Every partial (this workgroup's own included, as in the device-scope
-    // path), all loads in flight together, then summed in k order.
     switch (a.ks) {
-      case 2: wide_sum_partials_l2<NW, 2>(rs, own); break;
-      case 4: wide_sum_partials_l2<NW, 4>(rs, own); break;
-      default: wide_sum_partials_l2<NW, 8>(rs, own); break;
+      case 2: wide_sum_partials_l2_own<NW, 2, TN>(rs, ksi, own); break;
+      case 4: wide_sum_partials_l2_own<NW, 4, TN>(rs, ksi, own); break;
+      default: wide_sum_partials_l2_own<NW, 8, TN>(rs, ksi, own); break;
     }
   } else if (a.ks > 1) {
     const size_t tbase = ((size_t)(rb * ntiles + tile) * a.ks) * kQRows * TN;
     // Device-coherent stores of the partial, acknowledged.
     float* dst = a.part + tbase + (size_t)ksi * kQRows * TN + 4 * threadIdx.x;
+    if constexpr (IT == 1) {
+      st1_sc1_wait(dst, own[0]);
+    } else {
 #pragma unroll
-    for (int it = 0; it < IT; it += 2)
-      st2_sc1_wait(dst + 4 * NW * kWave * it, own[it], dst + 4 * NW * kWave * (it + 1), own[it + 1]);
+      for (int it = 0; it < IT; it += 2)
+        st2_sc1_wait(dst + 4 * NW * kWave * it, own[it], dst + 4 * NW * kWave * (it + 1), own[it + 1]);
+    }
     __syncthreads();  // (also: every wave is done reading the spills)
     // The flag lives in dynamic LDS: a static __shared__ would shift the
     // dynamic base off the 256-byte alignment the swizzled addressing needs.
     volatile uint32_t* flag = reinterpret_cast<volatile uint32_t*>(smem);
     if (threadIdx.x == 0) {
-      uint32_t* ctr = a.cnt + rb * ntiles + tile;
-      asm volatile("" : "+v"(ctr));  // per-lane address: a vector atomic
       const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       const uint32_t last = old == (uint32_t)(a.ks - 1);
       if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -852,15 +884,15 @@ __device__ __forceinline__ void wide_finish(const QArgs& a, unsigned char* smem,
     // Device-coherent 16-byte loads (sc1: miss the local L2) of every
     // partial, then the sum in k order.
     switch (a.ks) {
-      case 2: wide_sum_partials<NW, 2>(a.part + tbase, own); break;
-      case 4: wide_sum_partials<NW, 4>(a.part + tbase, own); break;
-      default: wide_sum_partials<NW, 8>(a.part + tbase, own); break;
+      case 2: wide_sum_partials<NW, 2, TN>(a.part + tbase, own); break;
+      case 4: wide_sum_partials<NW, 4, TN>(a.part + tbase, own); break;
+      default: wide_sum_partials<NW, 8, TN>(a.part + tbase, own); break;
     }
   }
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
     const int q = threadIdx.x + NW * kWave * it;
-    const int m = q >> 6, n = n0 + 4 * (q & 63);
+    const int m = q / QPR, n = n0 + 4 * (q % QPR);
     if (m >= mrows) continue;
     if (FMT8) own[it] *= *reinterpret_cast<const f32x4*>(static_cast<const float*>(a.s) + n);
     epi_store_bf16x4(a.y, a.aux, a.epi, (size_t)(m0 + m) * N + n, own[it]);
@@ -875,15 +907,17 @@ __device__ __forceinline__ void wide_finish(const QArgs& a, unsigned char* smem,
 // 8-byte bank pairs.
 __device__ __forceinline__ int wide2_swz(int r) { return r & 2; }
 
-template <int NW, int G, int R, int CS>  // NW waves; G 64-k groups per wave; ring of R 32-k steps; column split
+// NW waves; G 64-k groups per wave; ring of R 32-k steps; column split CS;
+// tile of TN columns (TNW = TN / CS per wave: 256 or 128).
+template <int NW, int G, int R, int CS, int TN = kWideTN>
 __global__ __launch_bounds__(NW * kWave) void int4g64_wide_kernel(QArgs a) {
-  constexpr int TN = kWideTN, TNW = TN / CS, NB = TNW / 16, S = 2 * G;
+  constexpr int TNW = TN / CS, NB = TNW / 16, S = 2 * G;
   constexpr int DPS = TNW / 64;                             // weight DMAs per step
   constexpr int SLOT = 16 * TNW;                            // one 32-k step: 16 weight rows x TNW bytes
   constexpr int LPR = TNW / 16, RPD = 64 / LPR;             // DMA lanes per slot row, slot rows per DMA
   constexpr int SB = ((G * TNW * 2 + 1023) / 1024) * 1024;  // scale block bytes
   constexpr int ZB = ((G * TNW + 1023) / 1024) * 1024;      // zero-point block bytes
-  static_assert(CS == 1 || CS == 2, "column split 1 or 2");
+  static_assert((CS == 1 || CS == 2) && (TNW == 256 || TNW == 128), "128 or 256 columns per wave");
   static_assert(R >= 2 && R <= S && G <= 4, "ring holds both steps of a group");
   extern __shared__ __align__(16) unsigned char smem[];
   const int lane = threadIdx.x & 63;
@@ -941,7 +975,7 @@ __global__ __launch_bounds__(NW * kWave) void int4g64_wide_kernel(QArgs a) {
 #pragma unroll
   for (int q = 0; q < DPS; ++q) {
     const int rr = RPD * q + lane / LPR, pp = lane % LPR;
-    const int ch = CS == 1 ? wide_chunk(pp, rr) : (pp ^ wide2_swz(rr));
+    const int ch = TNW == 256 ? wide_chunk(pp, rr) : (pp ^ wide2_swz(rr));
     wsrc[q] = a.w + (size_t)(kbeg / 2 + 8 * (rr >> 2) + (rr & 3)) * N + n0w + 16 * ch;
   }
   auto issue = [&](int t) {
@@ -962,7 +996,7 @@ __global__ __launch_bounds__(NW * kWave) void int4g64_wide_kernel(QArgs a) {
   const int r8 = (lane & 15) >> 1, hi = r8 >> 2;
   const int wrow = 4 * j + (r8 & 3);
   const uint32_t woff =
-      (uint32_t)(wrow * TNW + 8 * (lane & 1) + 16 * (CS == 1 ? wide_pos(hi, wrow) : (hi ^ wide2_swz(wrow))));
+      (uint32_t)(wrow * TNW + 8 * (lane & 1) + 16 * (TNW == 256 ? wide_pos(hi, wrow) : (hi ^ wide2_swz(wrow))));
   const uint32_t ring0 = lds_addr(ring);
   // Scale tr16 read: lane 4r + q of a group names row (block) r, columns 4q..4q+3.
   const uint32_t soff = lds_addr(sblk) + (uint32_t)(((lane & 15) >> 2) * 32 + 8 * (lane & 3));
@@ -985,7 +1019,7 @@ __global__ __launch_bounds__(NW * kWave) void int4g64_wide_kernel(QArgs a) {
       uint32_t ad[NB / 2];
 #pragma unroll
       for (int p = 0; p < NB / 2; ++p) ad[p] = wb ^ (uint32_t)(32 * p);
-      if constexpr (CS == 1) lds_tr8x8(ad, w2);
+      if constexpr (TNW == 256) lds_tr8x8(ad, w2);
       else lds_tr8x4(ad, w2);
     }
     // This step's slot is read: refill it.
@@ -1001,7 +1035,7 @@ __global__ __launch_bounds__(NW * kWave) void int4g64_wide_kernel(QArgs a) {
       acc[b] = mfma16x16x32(A, unpack_int4((b & 1) ? w2[b >> 1].y : w2[b >> 1].x), h ? acc[b] : zero4);
     if (h) {
       u32x2 sv[4], zv[2];
-      if constexpr (CS == 1) lds_scale_zero(soff + (uint32_t)(g * 2 * TN), zoff + (uint32_t)(g * TN), sv, zv);
+      if constexpr (TNW == 256) lds_scale_zero(soff + (uint32_t)(g * 2 * TNW), zoff + (uint32_t)(g * TNW), sv, zv);
       else lds_scale_zero_half(soff + (uint32_t)(g * 2 * TNW), zoff + (uint32_t)(g * TNW), sv, zv);
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
@@ -1015,7 +1049,7 @@ __global__ __launch_bounds__(NW * kWave) void int4g64_wide_kernel(QArgs a) {
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  wide_finish<NW, false, CS>(a, smem, wl, y, tile, ksi, rb, m0, mrows, n0, c, j);
+  wide_finish<NW, false, CS, TN>(a, smem, wl, y, tile, ksi, rb, m0, mrows, n0, c, j);
 }
 
 // ---------------------------------------------------------------------------
@@ -1295,6 +1329,7 @@ struct QPlan {
   int ring;          // int8 streaming kernel: ring slots
   int wide_groups;   // > 0: wide int4 kernel with this many 64-k groups per wave
   int wide_cs;       // wide int4 kernel: column split (1: waves split K only; 2: also the columns in halves)
+  int wide_tn;       // wide int4 kernel: tile columns (256, or 128 for narrow tiles)
   int wide8_steps;   // > 0: wide int8 kernel with this many 32-k steps per wave
   int deq;           // 1: dequantise W to bf16 in the workspace, then the bf16 GEMM
   int qg;            // 1: the many-row kernel of qgemm.hip (K split ks ways)
@@ -1365,23 +1400,26 @@ bool plan_stream(int fmt, int64_t K, int64_t N, QPlan* p) {
 // 8, and 12.61 us for the unsplit 4 KB steps (same box, same run).
 constexpr int kWideWaves = 8;
 constexpr int kWideColumnSplit = 2;
-int wide_ring(int nw, int G, int cs = 1) {
+constexpr int kWideTileColumns = 128;
+int wide_ring(int nw, int G, int tnw = 256) {
   const int r = env_int("MK_QMM_WIDE_RING", 0);
   if (r >= 2 && r <= 2 * G && (r == 2 || r == 4 || r == 8)) return r;
-  if (cs == 2) return 2;
+  if (tnw == 128) return 2;
   if (nw == 4) return G == 4 ? 4 : 2 * G;
   return G == 4 ? 4 : G == 2 ? 2 : 2 * G;
 }
 
 bool plan_wide(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p) {
   const char* env = getenv("MK_QMM_WIDE");
-  if (fmt != MK_QFMT_INT4_G64 || N % mk::kWideTN != 0 || (env && env[0] == '0')) return false;
+  if (fmt != MK_QFMT_INT4_G64 || N % 128 != 0 || (env && env[0] == '0')) return false;
   const int nw = env_int("MK_QMM_WIDE_NW", kWideWaves);
-  const int cs = nw == 8 ? env_int("MK_QMM_WIDE_CS", kWideColumnSplit) : 1;
-  if ((nw != 4 && nw != 8) || (cs != 1 && cs != 2)) return false;
+  int tn = nw == 8 ? env_int("MK_QMM_WIDE_TN", kWideTileColumns) : mk::kWideTN;
+  if (tn != 128 && tn != 256) return false;
+  const int cs = nw == 8 && tn == 256 ? env_int("MK_QMM_WIDE_CS", kWideColumnSplit) : 1;
+  if ((nw != 4 && nw != 8) || (cs != 1 && cs != 2) || N % tn != 0) return false;
   const int64_t kunit = (int64_t)(nw / cs) * 64;  // k per workgroup and group-per-wave
   if (K % kunit != 0) return false;
-  const int ntiles = (int)(N / mk::kWideTN);
+  const int ntiles = (int)(N / tn);
   const int rb = (int)((M + mk::kQRows - 1) / mk::kQRows);
   const int ks_env = env_int("MK_QMM_KS", 0);
   int best = 0;
@@ -1397,23 +1435,23 @@ bool plan_wide(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p) {
   }
   if (best == 0 || (int64_t)ntiles * rb * best < 128) return false;
   const int G = (int)(K / ((int64_t)best * kunit));
-  const int R = wide_ring(nw, G, cs);
-  const int tnw = mk::kWideTN / cs;
+  const int tnw = tn / cs;
+  const int R = wide_ring(nw, G, tnw);
   const int sb = ((G * tnw * 2 + 1023) / 1024) * 1024, zb = ((G * tnw + 1023) / 1024) * 1024;
   int wl = R * 16 * tnw + sb + zb;
-  wl = std::max(wl, mk::kQRows * mk::kWideRedStride * 4);
+  wl = std::max(wl, mk::kQRows * (tn + 4) * 4);  // the y spill
   wl = (wl + 255) & ~255;
   p->ks = best;
   p->nw = nw;
   p->wide_cs = cs;
+  p->wide_tn = tn;
   p->ntiles = ntiles;
   p->rowblocks = rb;
   p->wide_groups = G;
   p->kwave = 64 * G;
   p->wave_lds = wl;
   p->lds_bytes = (size_t)nw * wl;
-  p->part_bytes = best > 1 ? (int64_t)mk::kWidePartOffset + (int64_t)rb * ntiles * best * mk::kQRows * mk::kWideTN * 4
-                           : 0;
+  p->part_bytes = best > 1 ? (int64_t)mk::kWidePartOffset + (int64_t)rb * ntiles * best * mk::kQRows * tn * 4 : 0;
   return p->lds_bytes <= kMaxLds;
 }
 
@@ -1534,21 +1572,21 @@ hipError_t lds_opt_in(const void* fn, size_t bytes) {
 
 hipError_t launch_reduce(int fmt, const mk::QArgs& a, hipStream_t st);
 
-template <int NW, int G, int R, int CS>
+template <int NW, int G, int R, int CS, int TN>
 hipError_t launch_wide_nwgr(const mk::QArgs& a, const QPlan& p, hipStream_t st) {
   dim3 grid(p.ntiles * p.ks, p.rowblocks), block(NW * mk::kWave);
-  hipError_t e = lds_opt_in((const void*)mk::int4g64_wide_kernel<NW, G, R, CS>, p.lds_bytes);
+  hipError_t e = lds_opt_in((const void*)mk::int4g64_wide_kernel<NW, G, R, CS, TN>, p.lds_bytes);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((mk::int4g64_wide_kernel<NW, G, R, CS>), grid, block, p.lds_bytes, st, a);
+  hipLaunchKernelGGL((mk::int4g64_wide_kernel<NW, G, R, CS, TN>), grid, block, p.lds_bytes, st, a);
   return hipGetLastError();
 }
 
-template <int NW, int G, int CS = 1>
+template <int NW, int G, int CS = 1, int TN = mk::kWideTN>
 hipError_t launch_wide(const mk::QArgs& a, const QPlan& p, hipStream_t st) {
-  switch (wide_ring(NW, G, CS)) {
-    case 2: return launch_wide_nwgr<NW, G, 2, CS>(a, p, st);
-    case 4: if constexpr (2 * G >= 4) return launch_wide_nwgr<NW, G, 4, CS>(a, p, st); break;
-    case 8: if constexpr (2 * G >= 8) return launch_wide_nwgr<NW, G, 8, CS>(a, p, st); break;
+  switch (wide_ring(NW, G, TN / CS)) {
+    case 2: return launch_wide_nwgr<NW, G, 2, CS, TN>(a, p, st);
+    case 4: if constexpr (2 * G >= 4) return launch_wide_nwgr<NW, G, 4, CS, TN>(a, p, st); break;
+    case 8: if constexpr (2 * G >= 8) return launch_wide_nwgr<NW, G, 8, CS, TN>(a, p, st); break;
   }
   return hipErrorInvalidValue;
 }
@@ -1723,7 +1761,13 @@ int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, v
     const int gx = p.ntiles * p.ks;
     a.xch_local = p.ks > 1 && gx % 8 == 0 && (gx / 8) % p.ks == 0 &&
                   xcd_round_robin(dim3(gx, p.rowblocks), st, reinterpret_cast<uint32_t*>(a.part));
-    if (p.wide_cs == 2) {
+    if (p.wide_tn == 128) {
+      switch (p.wide_groups) {
+        case 1: e = launch_wide<8, 1, 1, 128>(a, p, st); break;
+        case 2: e = launch_wide<8, 2, 1, 128>(a, p, st); break;
+        default: e = launch_wide<8, 4, 1, 128>(a, p, st); break;
+      }
+    } else if (p.wide_cs == 2) {
       switch (p.wide_groups) {
         case 1: e = launch_wide<8, 1, 2>(a, p, st); break;
         case 2: e = launch_wide<8, 2, 2>(a, p, st); break;

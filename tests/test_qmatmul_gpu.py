@@ -262,49 +262,61 @@ def test_workspace_too_small_is_rejected_before_launch():
     assert b"workspace" in L.mk_last_error()
 
 
-# Shapes that take the 256-column kernel (mk_qmatmul plan "wide"): every
-# group count per wave (G = 1, 2, 4), split-K factors 1..8 with the in-kernel
+# Shapes that take the wide kernel: every group
+# count per wave (G = 1, 2, 4), split-K factors 1..8 with the in-kernel
 # last-arriver reduction, and two row blocks with a partial second block.
 WIDE_SHAPES = [
-    (16, 4096, 14336),   # ks = 4, G = 2 (the headline plan)
-    (16, 2048, 14336),   # ks = 4, G = 1
-    (1, 8192, 8192),     # ks = 8, G = 2
-    (20, 4096, 8192),    # two row blocks, ks = 4
-    (1, 2048, 65536),    # ks = 1, G = 4: no split
+    (16, 4096, 14336),   # the headline
+    (16, 2048, 14336),
+    (1, 8192, 8192),
+    (20, 4096, 8192),    # two row blocks
+    (1, 2048, 65536),    # no split at the 256-column tiles
 ]
 
+# Wave layouts: (tile columns, column split).  256 / 1: every wave over all
+# 256 columns; 256 / 2: waves split over two 128-column halves; 128 / 1:
+# narrow tiles, every wave over all 128 columns.
+WIDE_LAYOUTS = {"all-columns": ("256", "1"), "column-split": ("256", "2"), "narrow": ("128", "1")}
 
-@pytest.mark.parametrize("cs", ["1", "2"], ids=["all-columns", "column-split"])
-@pytest.mark.parametrize("M,K,N", WIDE_SHAPES)
-def test_int4_wide_kernel_matches_oracle(monkeypatch, M, K, N, cs):
-    """Both wave layouts of the wide kernel: every wave over all 256 columns
-    (MK_QMM_WIDE_CS=1) and waves split over two 128-column halves (the
-    default), against the C oracle."""
+
+@pytest.mark.parametrize("layout", list(WIDE_LAYOUTS))
+@pytest.mark.parametrize("M,K,N", WIDE_SHAPES + [(16, 4096, 4992)])
+def test_int4_wide_kernel_matches_oracle(monkeypatch, M, K, N, layout):
+    """Every wave layout of the wide kernel against the C oracle (N = 4992
+    = 39 x 128: narrow tiles only, with 39 tiles the exchange goes through
+    device scope)."""
     ops = _ops()
+    tn, cs = WIDE_LAYOUTS[layout]
+    if N % int(tn) != 0:
+        pytest.skip(f"N={N} is not a multiple of {tn} columns")
+    monkeypatch.setenv("MK_QMM_WIDE_TN", tn)
     monkeypatch.setenv("MK_QMM_WIDE_CS", cs)
     rng = np.random.default_rng(7 * M + K + N)
     x, packed, s, z = quant.make_int4_case(rng, M, K, N)
-    print(f"int4 wide case M={M} K={K} N={N} cs={cs}", flush=True)
+    print(f"int4 wide case M={M} K={K} N={N} layout={layout}", flush=True)
     y = ops.int4_g64_matmul(dev_bf16(x), dev(packed), dev_bf16(s), dev(z))
     torch.cuda.synchronize()
     ref = cport.int4_g64_matmul(x, packed, s, z)
-    assert_rel_close(host_bf16(y), ref, BF16_RTOL, f"int4 wide {M}x{K}x{N}")
+    assert_rel_close(host_bf16(y), ref, BF16_RTOL, f"int4 wide {M}x{K}x{N} {layout}")
 
 
-@pytest.mark.parametrize("nw", ["8", "4"])
-@pytest.mark.parametrize("M,K,N", [(16, 4096, 14336), (20, 4096, 8192), (1, 8192, 8192), (40, 2048, 14336)])
-def test_int4_wide_exchange_in_l2_matches_device_scope(monkeypatch, nw, M, K, N):
+@pytest.mark.parametrize("nw,tn", [("8", "256"), ("8", "128"), ("4", "256")], ids=["8w", "8w-narrow", "4w"])
+@pytest.mark.parametrize("M,K,N", [(16, 4096, 14336), (20, 4096, 8192), (1, 8192, 8192), (40, 2048, 14336),
+                                   (16, 4096, 2048)])
+def test_int4_wide_exchange_in_l2_matches_device_scope(monkeypatch, nw, tn, M, K, N):
     """The split-K exchange inside one XCD's L2 (taken when the placement
     probe has seen round-robin dealing) against the device-scope exchange
     (MK_QMM_XCH=device): both sum the partials in k order from memory, so the
-    outputs are bit-identical; with 8 and 4 waves per workgroup, one and
-    several row blocks (2D grids)."""
+    outputs are bit-identical; with 8 and 4 waves per workgroup, 256- and
+    128-column tiles, one and several row blocks (2D grids), K split 2, 4
+    and 8 ways (N = 2048 at 128 columns: 8)."""
     ops = _ops()
     monkeypatch.setenv("MK_QMM_WIDE_NW", nw)
+    monkeypatch.setenv("MK_QMM_WIDE_TN", tn)
     rng = np.random.default_rng(5 * M + K + N)
     x, packed, s, z = quant.make_int4_case(rng, M, K, N)
     args = (dev_bf16(x), dev(packed), dev_bf16(s), dev(z))
-    print(f"int4 wide exchange case M={M} K={K} N={N} waves={nw}", flush=True)
+    print(f"int4 wide exchange case M={M} K={K} N={N} waves={nw} tile={tn}", flush=True)
     local = [host_bf16_bits(ops.int4_g64_matmul(*args)) for _ in range(3)]
     monkeypatch.setenv("MK_QMM_XCH", "device")
     dev_ = host_bf16_bits(ops.int4_g64_matmul(*args))
@@ -312,7 +324,7 @@ def test_int4_wide_exchange_in_l2_matches_device_scope(monkeypatch, nw, M, K, N)
     for y in local:
         assert np.array_equal(y, dev_)
     ref = cport.int4_g64_matmul(x, packed, s, z)
-    assert_rel_close(bf16_bits_to_f32(local[0]), ref, BF16_RTOL, f"int4 wide {M}x{K}x{N} waves={nw}")
+    assert_rel_close(bf16_bits_to_f32(local[0]), ref, BF16_RTOL, f"int4 wide {M}x{K}x{N} waves={nw} tile={tn}")
     ws = ops.workspace(1, "cuda:0")
     assert int(ws[: 64 * 1024].count_nonzero()) == 0
 
