@@ -602,29 +602,32 @@ __global__ __launch_bounds__(8 * kWave) void int4g64_stream_kernel(QArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Wide int4 kernel: 256 output columns per workgroup.
+// Wide int4 kernel: 256 (or 128) output columns per workgroup.
 //
 // The 64-column kernel above streams 64-byte strips of every weight row and
 // DMAs one 1 KB x slice per 1 KB of weights, so half of its L2->LDS traffic is
-// re-reads of x.  Here a workgroup owns 256 columns (256-byte row segments;
-// x is 1/5 of the traffic) and K is split over `ks` workgroups to fill the
-// chip.  Each of the 8 waves covers all 256 columns over its own G groups of
-// 64 k, with a private DMA ring of R 32-k steps (normally all of them, issued
-// at once): slot = 16 weight rows x 256 B, 16-column chunk c of row r at
-// position c ^ (r & 7) ^ 8 (c & 1), so the transposing reads below are
-// conflict-free.  x goes straight to registers as whole lines.
-// ds_read_b64_tr_b8 hands MFMA lane (c, j) the bytes of column c of two
-// column blocks in rows 4j..4j+3 of a step, i.e. its B fragments for two
-// MFMAs; the bytes become bf16 (128 + q) in registers as in the kernels above.  Scales
-// and zero points come from tr16 / tr8 reads of the wave's scale block.
+// re-reads of x.  Here a workgroup owns a tile of 256 columns (128 when N is
+// not a multiple of 256) and K is split over `ks` workgroups to fill the
+// chip.  Each wave covers TNW = 256 or 128 columns of the tile over its own G
+// groups of 64 k (with the column split, waves w and w + 1 take the two
+// 128-column halves of the same k range), with a private DMA ring of R 32-k
+// steps: slot = 16 weight rows x TNW bytes, 16-column chunks swizzled so the
+// transposing reads below are conflict-free.  ds_read_b64_tr_b8 hands MFMA
+// lane (c, j) the bytes of column c of two column blocks in rows 4j..4j+3 of
+// a step, i.e. its B fragments for two MFMAs; the bytes become bf16
+// (128 + q) in registers as in the kernels above.  Scales and zero points
+// come from tr16 / tr8 reads of the wave's scale block, x from two 16-byte
+// reads of its x block; all three arrive by LDS DMA ahead of the ring.
 //
 // Split-K partials are combined in the kernel: every workgroup writes its
-// f32 partial with device-coherent (sc1) stores, waits for them, and bumps
-// the tile's arrival counter with a device-scope atomic; the last arriver
-// reads the other partials with device-coherent loads, sums all of them in
-// k order (so results do not depend on arrival order), writes bf16 y and
-// resets the counter.  No workgroup waits on another and no cache-wide
-// fence is needed.
+// f32 partial, waits for the stores' acknowledgement, and bumps the tile's
+// arrival counter with an atomic; the last arriver sums all partials in k
+// order (its own from registers, so results do not depend on arrival
+// order), writes bf16 y and resets the counter.  No workgroup waits on
+// another and no cache-wide fence is needed.  When the grid deals each
+// tile's workgroups to one XCD (checked once per device by a probe) the
+// exchange stays in that XCD's L2; otherwise it goes through device-coherent
+// (sc1) stores and loads.
 // ---------------------------------------------------------------------------
 constexpr int kWideTN = 256;
 constexpr int kWideSlot = 4 * 1024;   // one 32-k step: 16 weight rows x 256 B
@@ -663,6 +666,24 @@ __device__ __forceinline__ void lds_tr8x8(const uint32_t (&ad)[8], u32x2 (&o)[8]
 }
 
 // Four transposing byte reads (the column split's 8 blocks) and their wait.
+// One 16-byte LDS read and its wait.
+__device__ __forceinline__ u32x4 lds_read_b128(uint32_t a0) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(a0) : "memory");
+  return v;
+}
+
+// Two 16-byte LDS reads and their wait (x fragments of one 64-k group).
+__device__ __forceinline__ void lds_read2_b128(uint32_t a0, uint32_t a1, u32x4& v0, u32x4& v1) {
+  asm volatile(
+      "ds_read_b128 %0, %2\n\t"
+      "ds_read_b128 %1, %3\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v0), "=&v"(v1)
+      : "v"(a0), "v"(a1)
+      : "memory");
+}
+
 __device__ __forceinline__ void lds_tr8x4(const uint32_t (&ad)[4], u32x2 (&o)[4]) {
   asm volatile(
       "ds_read_b64_tr_b8 %0, %4\n\t"
@@ -917,6 +938,7 @@ __global__ __launch_bounds__(NW * kWave) void int4g64_wide_kernel(QArgs a) {
   constexpr int LPR = TNW / 16, RPD = 64 / LPR;             // DMA lanes per slot row, slot rows per DMA
   constexpr int SB = ((G * TNW * 2 + 1023) / 1024) * 1024;  // scale block bytes
   constexpr int ZB = ((G * TNW + 1023) / 1024) * 1024;      // zero-point block bytes
+  constexpr int XB = G * 2048;                              // x block bytes: [G][16 rows][64 k] bf16
   static_assert((CS == 1 || CS == 2) && (TNW == 256 || TNW == 128), "128 or 256 columns per wave");
   static_assert(R >= 2 && R <= S && G <= 4, "ring holds both steps of a group");
   extern __shared__ __align__(16) unsigned char smem[];
@@ -938,20 +960,27 @@ __global__ __launch_bounds__(NW * kWave) void int4g64_wide_kernel(QArgs a) {
   unsigned char* ring = wl;
   unsigned char* sblk = wl + R * SLOT;
   unsigned char* zblk = sblk + SB;
+  unsigned char* xblk = zblk + ZB;
 
   // k order inside each 64-k group g: MFMA lane group j, half h (of the two
   // MFMAs) covers k = kbeg + 64 g + 16 j + 8 h .. +7, so a lane's x for a
   // group is 16 contiguous bf16 and a row of x is read as whole lines.  x
-  // goes straight to registers (all groups, issued first).
-  u32x4 xr[G][2];
+  // comes by LDS DMA like everything else the wave streams (issued first),
+  // so every load of the wave is one kind and the ring's counted waits
+  // cover it: block [G][16 rows][8 chunks of 16 B], chunk q of row r at
+  // position q ^ (r & 7), which makes the two 16-byte reads per lane below
+  // conflict-free.  Rows past M repeat row M - 1 (never stored).
   {
-    const uint16_t* xp = a.x + (size_t)min(m0 + c, a.M - 1) * a.K + kbeg + 16 * j;
+    const int r = lane >> 3, q = (lane & 7) ^ (lane >> 3);
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      xr[g][0] = *reinterpret_cast<const u32x4*>(xp + 64 * g);
-      xr[g][1] = *reinterpret_cast<const u32x4*>(xp + 64 * g + 8);
-    }
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb)
+        dma16(a.x + (size_t)min(m0 + r + 8 * hb, a.M - 1) * a.K + kbeg + 64 * g + 8 * q,
+              xblk + g * 2048 + hb * 1024);
   }
+  const uint32_t xoff = lds_addr(xblk) + (uint32_t)(c * 128);
+  const uint32_t xlo = 16u * (uint32_t)((2 * j) ^ (c & 7)), xhi = 16u * (uint32_t)((2 * j + 1) ^ (c & 7));
   // Scale rows [G][TN] bf16 and zero rows [G][TN] u8 of this wave's groups
   // (rows past G repeat the last one; never used).
 #pragma unroll
@@ -1005,6 +1034,7 @@ __global__ __launch_bounds__(NW * kWave) void int4g64_wide_kernel(QArgs a) {
   const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0
   const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
   f32x4 y[NB], acc[NB], xs;
+  u32x4 xg[2];
 #pragma unroll
   for (int b = 0; b < NB; ++b) y[b] = zero4;
 
@@ -1026,7 +1056,8 @@ __global__ __launch_bounds__(NW * kWave) void int4g64_wide_kernel(QArgs a) {
     if (t + R < S) issue(t + R);
 
     // x slot order k0 k2 k4 k6 k1 k3 k5 k7 (matches unpack_int4).
-    const u32x4 v = xr[g][h];
+    if (h == 0) lds_read2_b128(xoff + (uint32_t)(g * 2048) + xlo, xoff + (uint32_t)(g * 2048) + xhi, xg[0], xg[1]);
+    const u32x4 v = xg[h];
     const u32x4 A = {perm(v.y, v.x, 0x05040100u), perm(v.w, v.z, 0x05040100u), perm(v.y, v.x, 0x07060302u),
                      perm(v.w, v.z, 0x07060302u)};
     xs = mfma16x16x32(A, ones, h ? xs : zero4);
@@ -1118,14 +1149,28 @@ __global__ __launch_bounds__(8 * kWave) void int8pc_wide_kernel(QArgs a) {
   const size_t N = (size_t)a.N;
   unsigned char* wl = smem + wv * a.wave_lds;
 
-  // x of every step straight to registers (issued first): lane (c, j) holds
-  // x[m0 + c][kbeg + 32 t + 8 j .. +7], its A fragment of step t.
-  u32x4 xr[S];
-  {
+  // x of every step, issued first: lane (c, j) uses x[m0 + c][kbeg + 32 t +
+  // 8 j .. +7], its A fragment of step t.  With S <= 4 it comes by LDS DMA
+  // like the weights (every load of the wave one kind, so the ring's counted
+  // waits cover it; with register loads in flight beside LDS DMAs the
+  // compiler waits for all of them before the first step): block
+  // [S][16 rows][4 chunks of 16 B], chunk q of row r at position
+  // q ^ ((r >> 2) & 3), which makes the 16-byte reads conflict-free.  Longer
+  // waves keep it in registers (the LDS would not hold it).
+  constexpr bool XL = S <= 4;
+  unsigned char* xblk = wl + R * kWide8Slot;
+  u32x4 xr[XL ? 1 : S];
+  if constexpr (XL) {
+    const int r = lane >> 2, q = (lane & 3) ^ ((lane >> 4) & 3);
+#pragma unroll
+    for (int t = 0; t < S; ++t)
+      dma16(a.x + (size_t)min(m0 + r, a.M - 1) * a.K + kbeg + 32 * t + 8 * q, xblk + t * 1024);
+  } else {
     const uint16_t* xp = a.x + (size_t)min(m0 + c, a.M - 1) * a.K + kbeg + 8 * j;
 #pragma unroll
     for (int t = 0; t < S; ++t) xr[t] = *reinterpret_cast<const u32x4*>(xp + 32 * t);
   }
+  const uint32_t xa = lds_addr(xblk) + (uint32_t)(c * 64 + 16 * (j ^ ((c >> 2) & 3)));
   // Step t, DMA q: lane L fills slot row rr = 4 q + L / 16 (W row
   // kbeg + 32 t + rr), position L % 16, from chunk (L % 16) ^ (rr & 15).
   const uint8_t* wsrc[DPS];
@@ -1162,7 +1207,9 @@ __global__ __launch_bounds__(8 * kWave) void int8pc_wide_kernel(QArgs a) {
     lds_tr8x16(ring0 + (uint32_t)((t % R) * kWide8Slot) + woff, w8);
     // This step's slot is read: refill it.
     if (t + R < S) issue(t + R);
-    const u32x4 A = xr[t];
+    u32x4 A;
+    if constexpr (XL) A = lds_read_b128(xa + (uint32_t)(t * 1024));
+    else A = xr[t];
     xs = mfma16x16x32(A, ones, xs);
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[b] = mfma16x16x32(A, unpack_int8(w8[b].x, w8[b].y), acc[b]);
@@ -1387,33 +1434,47 @@ bool plan_stream(int fmt, int64_t K, int64_t N, QPlan* p) {
   return false;
 }
 
-// Wide int4 kernel: N % 256 == 0, K = ks * 8 * 64 * G with G in {1, 2, 4};
-// the fewest splits that give >= 192 workgroups (the most the 64 KB counter
-// region and G >= 1 allow).  Grids below 128 workgroups stay on the
-// 64-column kernels.  MK_QMM_WIDE=0 disables it.
+// Wide int4 kernel: N % 128 == 0, K = ks * (NW / CS) * 64 * G with G in
+// {1, 2, 4}; the fewest splits that give >= 192 workgroups (the most the
+// 64 KB counter region and G >= 1 allow).  Grids below 128 workgroups stay
+// on the 64-column kernels.  MK_QMM_WIDE=0 disables it.
 // Ring depth (32-k steps in flight per wave) of the wide kernel with NW
-// waves of G groups.  At the headline with 8 waves (G = 2, 4 steps per wave)
-// a 2-step ring measured 13.3 us against 13.7 us for 3 steps and 13.6 us
-// for all 4 in flight at once.  MK_QMM_WIDE_RING overrides it (sweeps).
-// Column split (the default): 2 KB steps, 2 in flight per wave; at the
-// headline it measured 11.96 us against 12.46 us with 4 in flight, 13.34 with
-// 8, and 12.61 us for the unsplit 4 KB steps (same box, same run).
+// waves of G groups; MK_QMM_WIDE_RING overrides it (sweeps), and it is
+// halved until the workgroup's LDS fits.  At the headline (8 waves, column
+// split, ks 4, G 4), one box, one run: 2 steps in flight 11.37 us, 4 steps
+// 11.79; 128-column tiles (ks 2) 11.55 us (2 steps) and 11.92 (ks 4);
+// unsplit 256-column waves 12.47 us; 4 waves 13.11 us; ks 8 17.0 us.  The
+// x block by LDS DMA instead of register loads took the column split from
+// 12.02 to 11.43 us: with register loads in flight beside LDS DMAs the
+// compiler waits for every outstanding load before the first step.
 constexpr int kWideWaves = 8;
 constexpr int kWideColumnSplit = 2;
-constexpr int kWideTileColumns = 128;
-int wide_ring(int nw, int G, int tnw = 256) {
-  const int r = env_int("MK_QMM_WIDE_RING", 0);
-  if (r >= 2 && r <= 2 * G && (r == 2 || r == 4 || r == 8)) return r;
-  if (tnw == 128) return 2;
-  if (nw == 4) return G == 4 ? 4 : 2 * G;
-  return G == 4 ? 4 : G == 2 ? 2 : 2 * G;
+constexpr int kWideTileColumns = 256;
+// LDS bytes of one wave of the wide int4 kernel: ring, scale and zero-point
+// blocks, x block; at least the y spill of a tile of tnw * cs columns.
+int wide_wave_lds(int G, int tnw, int cs, int R) {
+  const int sb = ((G * tnw * 2 + 1023) / 1024) * 1024, zb = ((G * tnw + 1023) / 1024) * 1024;
+  const int wl = std::max(R * 16 * tnw + sb + zb + G * 2048, mk::kQRows * (tnw * cs + 4) * 4);
+  return (wl + 255) & ~255;
+}
+
+int wide_ring(int nw, int G, int tnw = 256, int cs = 1) {
+  int r = env_int("MK_QMM_WIDE_RING", 0);
+  if (!(r >= 2 && r <= 2 * G && (r == 2 || r == 4 || r == 8))) {
+    if (tnw == 128) r = 2;
+    else if (nw == 4) r = G == 4 ? 4 : 2 * G;
+    else r = G == 4 ? 4 : G == 2 ? 2 : 2 * G;
+  }
+  while (r > 2 && (size_t)nw * wide_wave_lds(G, tnw, cs, r) > kMaxLds) r /= 2;  // what fits
+  return r;
 }
 
 bool plan_wide(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p) {
   const char* env = getenv("MK_QMM_WIDE");
   if (fmt != MK_QFMT_INT4_G64 || N % 128 != 0 || (env && env[0] == '0')) return false;
   const int nw = env_int("MK_QMM_WIDE_NW", kWideWaves);
-  int tn = nw == 8 ? env_int("MK_QMM_WIDE_TN", kWideTileColumns) : mk::kWideTN;
+  // 256-column tiles where N allows, else 128 (MK_QMM_WIDE_TN forces one).
+  int tn = nw == 8 ? env_int("MK_QMM_WIDE_TN", N % kWideTileColumns == 0 ? kWideTileColumns : 128) : mk::kWideTN;
   if (tn != 128 && tn != 256) return false;
   const int cs = nw == 8 && tn == 256 ? env_int("MK_QMM_WIDE_CS", kWideColumnSplit) : 1;
   if ((nw != 4 && nw != 8) || (cs != 1 && cs != 2) || N % tn != 0) return false;
@@ -1436,11 +1497,8 @@ bool plan_wide(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p) {
   if (best == 0 || (int64_t)ntiles * rb * best < 128) return false;
   const int G = (int)(K / ((int64_t)best * kunit));
   const int tnw = tn / cs;
-  const int R = wide_ring(nw, G, tnw);
-  const int sb = ((G * tnw * 2 + 1023) / 1024) * 1024, zb = ((G * tnw + 1023) / 1024) * 1024;
-  int wl = R * 16 * tnw + sb + zb;
-  wl = std::max(wl, mk::kQRows * (tn + 4) * 4);  // the y spill
-  wl = (wl + 255) & ~255;
+  const int R = wide_ring(nw, G, tnw, cs);
+  const int wl = wide_wave_lds(G, tnw, cs, R);
   p->ks = best;
   p->nw = nw;
   p->wide_cs = cs;
@@ -1478,7 +1536,9 @@ bool plan_wide8(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p) {
     if ((int64_t)ntiles * rb * ks >= 192) break;
   }
   if (best == 0 || (int64_t)ntiles * rb * best < 128) return false;
-  int wl = std::max(kWide8Ring * mk::kWide8Slot, mk::kQRows * mk::kWideRedStride * 4);
+  const int64_t S = K / ((int64_t)best * 256);
+  // ring, the x block when the kernel stages x in LDS (S <= 4), the y spill
+  int wl = std::max(kWide8Ring * mk::kWide8Slot + (S <= 4 ? (int)S * 1024 : 0), mk::kQRows * mk::kWideRedStride * 4);
   wl = (wl + 255) & ~255;
   p->ks = best;
   p->nw = 8;
@@ -1583,7 +1643,7 @@ hipError_t launch_wide_nwgr(const mk::QArgs& a, const QPlan& p, hipStream_t st) 
 
 template <int NW, int G, int CS = 1, int TN = mk::kWideTN>
 hipError_t launch_wide(const mk::QArgs& a, const QPlan& p, hipStream_t st) {
-  switch (wide_ring(NW, G, TN / CS)) {
+  switch (wide_ring(NW, G, TN / CS, CS)) {
     case 2: return launch_wide_nwgr<NW, G, 2, CS, TN>(a, p, st);
     case 4: if constexpr (2 * G >= 4) return launch_wide_nwgr<NW, G, 4, CS, TN>(a, p, st); break;
     case 8: if constexpr (2 * G >= 8) return launch_wide_nwgr<NW, G, 8, CS, TN>(a, p, st); break;
