@@ -65,7 +65,7 @@ __device__ __forceinline__ float load_agent(const float* p) {
 
 // Raw buffer resources and the cache-policy operand of the buffer builtins.
 constexpr uint32_t kBufWord3 = 0x00020000u;  // raw-buffer resource word 3 (gfx9 family)
-constexpr int kSc0 = 1;                      // cache policy sc0: the access misses the CU's L1
+constexpr int kSc0 = 1;                      // cache policy sc0: workgroup scope (a load may hit the CU's L1)
 constexpr int kSc1 = 16;                     // cache policy sc1: device scope (past the XCD's L2)
 
 // Logical workgroup id that keeps runs of consecutive ids on one XCD.  The

@@ -28,8 +28,19 @@ int64_t qgemm_workspace_bytes(int64_t M, int64_t K, int64_t N, int ks);
 // int8: w int8 [K, N], s f32 [N], z unused.  x bf16 [M, K], y bf16 [M, N].
 // aux / epi: the bf16 store epilogue (epilogue.h), MK_EPI_NONE for none.
 // ks > 1 needs qgemm_workspace_bytes of workspace with zeroed counters.
+// xch_local: the caller has seen the dispatcher deal workgroups to the XCDs
+// round-robin on this device, so a tile's K parts (consecutive logical ids)
+// share one XCD when qgemm_tile_on_one_xcd holds for the grid, and the
+// split-K exchange can stay in that XCD's L2.
 hipError_t qgemm_launch(bool int4, const void* x, const void* w, const void* s, const void* z, void* y, int64_t M,
                         int64_t K, int64_t N, const void* aux, int epi, int ks, void* workspace,
-                        hipStream_t stream);
+                        hipStream_t stream, bool xch_local);
+
+// Workgroups of the kernel's grid for this shape and split.
+unsigned qgemm_grid(int64_t M, int64_t N, int ks);
+
+// Whether a grid of gx workgroups keeps each tile's ks K parts on one XCD
+// under round-robin dealing (see xcd_logical_id).
+bool qgemm_tile_on_one_xcd(unsigned gx, int ks);
 
 }  // namespace mkq

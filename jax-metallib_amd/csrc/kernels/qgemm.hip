@@ -70,6 +70,7 @@ struct QgArgs {
   int ks;          // K split (1 or 2)
   float* part;     // ks > 1: partial tiles [tile][ks][32][256 threads][4]
   uint32_t* cnt;   // ks > 1: per-tile arrival counters (zero between calls)
+  int xch_local;   // ks > 1: every tile's K parts run on one XCD (exchange in its L2)
 };
 
 typedef short qg_s16x4 __attribute__((ext_vector_type(4)));
@@ -97,6 +98,69 @@ struct QgW {
   u32x4 s;
   u32x4 v0, v1;
 };
+
+// Dequantise one step's share of thread `pt` (0..255) of the weights in r
+// into the bf16 [64 k][128 n] tile dst (swizzled):
+//   int4: rows k = 4 pp + {0..3} (pp = pt / 16) at columns 8 cq .. +7
+//         (cq = pt % 16): w = (q - z) * s, exact in f32 (q * s is exact
+//         inside the FMA and z * s has at most 16 significant bits), then
+//         rounded to bf16;
+//   int8: row kr = pt / 4 at columns 32 cc .. +31 (cc = pt % 4): w exactly
+//         as bf16 (8 significant bits).
+template <bool INT4>
+__device__ __forceinline__ void qg_dequant(unsigned char* dst, const QgW& r, int pt) {
+  const int pp = pt >> 4, cq = pt & 15;
+  const int kr = pt >> 2, cc = pt & 3;
+  if (INT4) {
+    float s[8], s16[8], zs[8];
+    const uint32_t sw[4] = {r.s.x, r.s.y, r.s.z, r.s.w};
+    const uint32_t zw[2] = {r.z.x, r.z.y};
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      s[c] = bf16_to_f32((sw[c >> 1] >> (16 * (c & 1))) & 0xffffu);
+      s16[c] = s[c] * 0.0625f;
+      zs[c] = (float)((zw[c >> 2] >> (8 * (c & 3))) & 0xffu) * s[c];
+    }
+    // Rows k = 4 pp + {0, 1, 2, 3}: low / high nibbles of packed rows 2 pp
+    // and 2 pp + 1.  High nibbles are converted as 16 q and scaled by s/16.
+    uint32_t lo[4] = {r.w0.x & 0x0f0f0f0fu, r.w0.y & 0x0f0f0f0fu, r.w1.x & 0x0f0f0f0fu, r.w1.y & 0x0f0f0f0fu};
+    uint32_t hi[4] = {r.w0.x & 0xf0f0f0f0u, r.w0.y & 0xf0f0f0f0u, r.w1.x & 0xf0f0f0f0u, r.w1.y & 0xf0f0f0f0u};
+    // Keep the masked words as they are, so each byte converts with one
+    // v_cvt_f32_ubyteN instead of a bit-field extract and a convert.
+    asm volatile("" : "+v"(lo[0]), "+v"(lo[1]), "+v"(lo[2]), "+v"(lo[3]));
+    asm volatile("" : "+v"(hi[0]), "+v"(hi[1]), "+v"(hi[2]), "+v"(hi[3]));
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int wsel = 2 * (kk >> 1);  // words of packed row 2 pp + kk / 2
+      float v[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const uint32_t src = (kk & 1) ? hi[wsel + (c >> 2)] : lo[wsel + (c >> 2)];
+        const float q = (float)((src >> (8 * (c & 3))) & 0xffu);
+        v[c] = __builtin_fmaf(q, (kk & 1) ? s16[c] : s[c], -zs[c]);
+      }
+      const int k = 4 * pp + kk;
+      *reinterpret_cast<u32x4*>(dst + 256 * k + 16 * qg_swz(k, cq)) =
+          u32x4{qg_pack(v[0], v[1]), qg_pack(v[2], v[3]), qg_pack(v[4], v[5]), qg_pack(v[6], v[7])};
+    }
+  } else {
+    const uint32_t wv[8] = {r.v0.x, r.v0.y, r.v0.z, r.v0.w, r.v1.x, r.v1.y, r.v1.z, r.v1.w};
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {  // chunk 4 cc + h: columns 32 cc + 8 h .. +7
+      uint32_t o[4];
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        const uint32_t b = wv[2 * h + d] ^ 0x80808080u;  // w + 128 as u8
+        float f[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) f[e] = (float)((b >> (8 * e)) & 0xffu) - 128.0f;
+        o[2 * d] = qg_pack(f[0], f[1]);
+        o[2 * d + 1] = qg_pack(f[2], f[3]);
+      }
+      *reinterpret_cast<u32x4*>(dst + 256 * kr + 16 * qg_swz(kr, 4 * cc + h)) = u32x4{o[0], o[1], o[2], o[3]};
+    }
+  }
+}
 
 template <bool INT4>
 __global__ __launch_bounds__(256) void qgemm_kernel(QgArgs a) {
@@ -161,56 +225,7 @@ __global__ __launch_bounds__(256) void qgemm_kernel(QgArgs a) {
 
   // ---- dequantisation of one step into bbuf[t & 1] ----
   auto dequant = [&](int t, const QgW& r) {
-    unsigned char* dst = bbuf[t & 1];
-    if (INT4) {
-      float s[8], s16[8], zs[8];
-      const uint32_t sw[4] = {r.s.x, r.s.y, r.s.z, r.s.w};
-      const uint32_t zw[2] = {r.z.x, r.z.y};
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        s[c] = bf16_to_f32((sw[c >> 1] >> (16 * (c & 1))) & 0xffffu);
-        s16[c] = s[c] * 0.0625f;
-        zs[c] = (float)((zw[c >> 2] >> (8 * (c & 3))) & 0xffu) * s[c];
-      }
-      // Rows k = 4 pp + {0, 1, 2, 3}: low / high nibbles of packed rows 2 pp
-      // and 2 pp + 1.  High nibbles are converted as 16 q and scaled by s/16.
-      uint32_t lo[4] = {r.w0.x & 0x0f0f0f0fu, r.w0.y & 0x0f0f0f0fu, r.w1.x & 0x0f0f0f0fu, r.w1.y & 0x0f0f0f0fu};
-      uint32_t hi[4] = {r.w0.x & 0xf0f0f0f0u, r.w0.y & 0xf0f0f0f0u, r.w1.x & 0xf0f0f0f0u, r.w1.y & 0xf0f0f0f0u};
-      // Keep the masked words as they are, so each byte converts with one
-      // v_cvt_f32_ubyteN instead of a bit-field extract and a convert.
-      asm volatile("" : "+v"(lo[0]), "+v"(lo[1]), "+v"(lo[2]), "+v"(lo[3]));
-      asm volatile("" : "+v"(hi[0]), "+v"(hi[1]), "+v"(hi[2]), "+v"(hi[3]));
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const int wsel = 2 * (kk >> 1);  // words of packed row 2 pp + kk / 2
-        float v[8];
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const uint32_t src = (kk & 1) ? hi[wsel + (c >> 2)] : lo[wsel + (c >> 2)];
-          const float q = (float)((src >> (8 * (c & 3))) & 0xffu);
-          v[c] = __builtin_fmaf(q, (kk & 1) ? s16[c] : s[c], -zs[c]);
-        }
-        const int k = 4 * pp + kk;
-        *reinterpret_cast<u32x4*>(dst + 256 * k + 16 * qg_swz(k, cq)) =
-            u32x4{qg_pack(v[0], v[1]), qg_pack(v[2], v[3]), qg_pack(v[4], v[5]), qg_pack(v[6], v[7])};
-      }
-    } else {
-      const uint32_t wv[8] = {r.v0.x, r.v0.y, r.v0.z, r.v0.w, r.v1.x, r.v1.y, r.v1.z, r.v1.w};
-#pragma unroll
-      for (int h = 0; h < 4; ++h) {  // chunk 4 cc + h: columns 32 cc + 8 h .. +7
-        uint32_t o[4];
-#pragma unroll
-        for (int d = 0; d < 2; ++d) {
-          const uint32_t b = wv[2 * h + d] ^ 0x80808080u;  // w + 128 as u8
-          float f[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) f[e] = (float)((b >> (8 * e)) & 0xffu) - 128.0f;
-          o[2 * d] = qg_pack(f[0], f[1]);
-          o[2 * d + 1] = qg_pack(f[2], f[3]);
-        }
-        *reinterpret_cast<u32x4*>(dst + 256 * kr + 16 * qg_swz(kr, 4 * cc + h)) = u32x4{o[0], o[1], o[2], o[3]};
-      }
-    }
+    qg_dequant<INT4>(bbuf[t & 1], r, tid);
   };
 
   // ---- B fragment offsets: tile j; the k half h of 32-row block hh adds
@@ -314,24 +329,254 @@ __global__ __launch_bounds__(256) void qgemm_kernel(QgArgs a) {
     if (tid == 0) {
       uint32_t* ctr = a.cnt + tile;
       asm volatile("" : "+v"(ctr));  // per-lane address: a vector atomic
-      const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // Local exchange: both K parts run on this XCD, so the atomic is
+      // performed in its L2 at workgroup scope; otherwise at device scope.
+      const uint32_t old = a.xch_local ? __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)
+                                       : __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       const uint32_t last = old == (uint32_t)(a.ks - 1);
       if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       last_flag = last;
     }
     __syncthreads();
     if (!last_flag) return;
-    // The other partial (ks == 2), device-coherent loads, added to ours.
+    // The other partial (ks == 2), added to ours.  Device scope: sc1 loads
+    // (they miss this XCD's L2).  Local: loads the L2 serves -- this CU's L1
+    // holds no line of the tile's partials (it starts the kernel
+    // invalidated and only the tile's second arriver loads them, once).
     const int other = 1 - ksi;
+    if (a.xch_local) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, ((32 * other + 8 * i + j) * 256 + tid) * 16, 0, 0);
+          acc[i][j] += __builtin_bit_cast(f32x4, v);
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, ((32 * other + 8 * i + j) * 256 + tid) * 16, 0,
+                                                                kSc1);
+          acc[i][j] += __builtin_bit_cast(f32x4, v);
+        }
+    }
+  }
+
+  // ---- epilogue: lane owns row m, columns n .. n + 3 of each tile ----
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + 64 * wave + 16 * i + (lane & 15);
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int n = n0 + 16 * j + 4 * (lane >> 4);
+      f32x4 v = acc[i][j];
+      if (!INT4) {
+        const f32x4 sc = *reinterpret_cast<const f32x4*>(static_cast<const float*>(a.s) + n);
+        v = f32x4{v.x * sc.x, v.y * sc.y, v.z * sc.z, v.w * sc.w};
+      }
+      epi_store_bf16x4(a.y, a.aux, a.epi, (size_t)m * N + n, v);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Warp-specialised variant: the same tile (256 rows x 128 columns), steps,
+// B swizzle, dequantisation and MFMA order as qgemm_kernel -- the results
+// are bit-identical -- with 8 waves.  Waves 0-3 (consumers) hold the
+// accumulators and do nothing but read fragments from LDS and issue MFMAs;
+// waves 4-7 (producers) stream every operand by LDS DMA and dequantise.  The
+// dispatcher puts wave w on SIMD w % 4, so each SIMD runs one consumer and
+// one producer, and the producer's VALU work overlaps the consumer's MFMAs
+// (the one-wave-per-SIMD kernel above serialises them).  LDS:
+//   bbuf [2][64 k][128 n] bf16    the dequantised weights (as above)
+//   xbuf [3][256 rows][64 k] bf16 x, 16-byte chunk q of row r at q ^ (r & 7)
+//                                 (conflict-free 16-byte fragment reads)
+//   wst  [4 producers][2][...]    each producer's own share of the packed
+//                                 weights, scales and zero points
+// Iteration t (between barriers): consumers multiply step t (bbuf[t % 2],
+// xbuf[t % 3]); producers issue the DMAs of step t + 2, wait for their own
+// DMAs of step t + 1, and dequantise it into bbuf[(t + 1) % 2].  Every DMA a
+// producer waits for is its own (it dequantises exactly the weights it
+// fetched), so the one barrier per step is the only cross-wave
+// synchronisation, as in the kernel above.
+// ---------------------------------------------------------------------------
+constexpr int kQgXBuf = kQgRows * 64 * 2;  // bf16 x [256 rows][64 k]
+constexpr int kQgWSt = 2048 + 512;         // packed weights (int4 1 KB, int8 2 KB) + scales 256 B + zeros 128 B
+constexpr int kQgWsLds = 2 * kQgBuf + 3 * kQgXBuf + 4 * 2 * kQgWSt + 16;
+
+template <bool INT4>
+__global__ __launch_bounds__(512) void qgemm_ws_kernel(QgArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  unsigned char* bbuf = smem;                      // [2][kQgBuf]
+  unsigned char* xbuf = smem + 2 * kQgBuf;         // [3][kQgXBuf]
+  unsigned char* wst = xbuf + 3 * kQgXBuf;         // [4][2][kQgWSt]
+  volatile uint32_t* last_flag = reinterpret_cast<volatile uint32_t*>(wst + 4 * 2 * kQgWSt);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool producer = wave >= 4;
+  const int N = a.N, K = a.K, M = a.M;
+  const int tiles_m = (M + kQgRows - 1) / kQgRows;
+  const uint32_t L = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int ksi = (int)(L % (uint32_t)a.ks);
+  const int tile = (int)(L / (uint32_t)a.ks);
+  const int tn = tile / tiles_m, tm = tile - tn * tiles_m;
+  const int m0 = tm * kQgRows, n0 = tn * kQgCols;
+  const int KT = K / a.ks / 64;
+  const int kt0 = ksi * KT;
+
+  f32x4 acc[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (producer) {
+    // ---- producers: every operand by LDS DMA, then the dequantisation ----
+    const int pw = wave - 4;   // producer index
+    const int pt = tid - 256;  // producer thread 0..255
+    unsigned char* mywst = wst + pw * 2 * kQgWSt;
+    const int xq = (lane & 7) ^ (lane >> 3);  // x chunk of this lane (row & 7 == lane / 8)
+    const uint8_t* xbase = reinterpret_cast<const uint8_t*>(a.x) + 2 * ((size_t)64 * kt0 + 8 * xq);
+    // weights: int4 packed rows 8 pw .. +7 (1 KB), int8 k rows 16 pw .. +15
+    // (2 KB), natural layout; int4 scales (256 B) and zero points (128 B).
+    const uint8_t* wsrc = a.w + (size_t)((INT4 ? 8 : 16) * pw + (lane >> 3)) * N + n0 + 16 * (lane & 7) +
+                          (size_t)kt0 * (INT4 ? 32 * N : 64 * N);
+    const uint8_t* szsrc = lane < 16 ? static_cast<const uint8_t*>(a.s) + 2 * ((size_t)kt0 * N + n0) + 16 * lane
+                                     : a.z + ((size_t)kt0 * N + n0) + 16 * (lane - 16);
+    // DMAs of step st into stage buffer st % 2 and
+    // xbuf[st % 3]: 8 of x (rows 64 pw + 8 d + lane / 8, position lane % 8
+    // holding chunk xq) and 2 of weights (int4: weights, scales and zero
+    // points; int8: weights).
+    auto issue = [&](int st) {
+      unsigned char* xb = xbuf + (st % 3) * kQgXBuf + (64 * pw) * 128;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        const int r = std::min(m0 + 64 * pw + 8 * d + (lane >> 3), M - 1);
+        dma16(xbase + 2 * (size_t)r * K + (size_t)st * 128, xb + d * 1024);
+      }
+      unsigned char* wb = mywst + (st & 1) * kQgWSt;
+      if (INT4) {
+        dma16(wsrc + (size_t)st * 32 * N, wb);
+        if (lane < 24) dma16(szsrc + (size_t)st * (lane < 16 ? 2 * N : N), wb + 2048);
+      } else {
+        dma16(wsrc + (size_t)st * 64 * N, wb);
+        dma16(wsrc + (size_t)st * 64 * N + (size_t)8 * N, wb + 1024);
+      }
+    };
+    // Read this thread's share of stage st % 2 and dequantise it.
+    auto dequant = [&](int st) {
+      const unsigned char* wb = mywst + (st & 1) * kQgWSt;
+      QgW r;
+      if (INT4) {
+        const int ppl = (pt >> 4) & 3, cq = pt & 15;  // packed rows 2 ppl, 2 ppl + 1 of this producer's 8
+        r.w0 = *reinterpret_cast<const u32x2*>(wb + (2 * ppl) * 128 + 8 * cq);
+        r.w1 = *reinterpret_cast<const u32x2*>(wb + (2 * ppl + 1) * 128 + 8 * cq);
+        r.s = *reinterpret_cast<const u32x4*>(wb + 2048 + 16 * cq);
+        r.z = *reinterpret_cast<const u32x2*>(wb + 2048 + 256 + 8 * cq);
+      } else {
+        const int krl = (pt >> 2) & 15, cc = pt & 3;  // k row of this producer's 16, 32 columns
+        r.v0 = *reinterpret_cast<const u32x4*>(wb + krl * 128 + 32 * cc);
+        r.v1 = *reinterpret_cast<const u32x4*>(wb + krl * 128 + 32 * cc + 16);
+      }
+      qg_dequant<INT4>(bbuf + (st & 1) * kQgBuf, r, pt);
+    };
+    constexpr int kDmaPerStep = 10;  // 8 for x, 2 for the weights (the DMA counter is per wave)
+    issue(0);
+    if (KT > 1) issue(1);
+    vm_wait(KT > 1 ? kDmaPerStep : 0);  // own DMAs of step 0 landed (step 1's may not have)
+    dequant(0);
+    for (int t = 0; t < KT; ++t) {
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if (t + 2 < KT) issue(t + 2);
+      vm_wait(t + 2 < KT ? kDmaPerStep : 0);  // own DMAs of step t + 1 landed
+      if (t + 1 < KT) dequant(t + 1);
+    }
+  } else {
+    // ---- consumers: fragments from LDS, MFMAs ----
+    // B fragment of column block j: k row 8 g + r (g = lane / 16,
+    // r = lane % 16 / 4), columns 16 j + 4 q .. +3 (q = lane % 4); the
+    // swizzled address is bbase ^ (32 j) (the bits of 32 j and of the
+    // lane's swizzle term do not overlap any other part of the address).
+    uint32_t bbase;
+    {
+      const int g = lane >> 4, r = (lane & 15) >> 2, q = lane & 3;
+      const int k = 8 * g + r, col = 4 * q;
+      bbase = (uint32_t)(256 * k + 16 * qg_swz(k, col >> 3) + 2 * (col & 7));
+    }
+    // x fragment (row block i, k half hh): row 64 wave + 16 i + lane % 16,
+    // chunk 4 hh + lane / 16 at position chunk ^ (lane % 8).
+    const uint32_t xrow = (uint32_t)((64 * wave + (lane & 15)) * 128);
+    const uint32_t xpos0 = 16u * (uint32_t)((lane >> 4) ^ (lane & 7)), xpos1 = 16u * (uint32_t)((4 + (lane >> 4)) ^ (lane & 7));
+    for (int t = 0; t < KT; ++t) {
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      const unsigned char* b = bbuf + (t & 1) * kQgBuf;
+      const unsigned char* xb = xbuf + (t % 3) * kQgXBuf;
+      u32x4 bf[2][8], xa[8];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t o = (bbase ^ (uint32_t)(32 * j)) + 8192u * hh;
+          const qg_s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((qg_lds_s16x4_ptr)(b + o));
+          const qg_s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((qg_lds_s16x4_ptr)(b + o + 1024));
+          const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+          bf[hh][j] = u32x4{l2.x, l2.y, h2.x, h2.y};
+        }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        xa[i] = *reinterpret_cast<const u32x4*>(xb + xrow + 2048 * i + xpos0);
+        xa[4 + i] = *reinterpret_cast<const u32x4*>(xb + xrow + 2048 * i + xpos1);
+      }
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[i][j] = mfma16x16x32(bf[hh][j], xa[4 * hh + i], acc[i][j]);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // ---- split K: exchange the partials (consumers' threads 0..255 hold them) ----
+  if (a.ks > 1) {
+    float* tp = a.part + (size_t)tile * a.ks * kQgPart;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(tp, 0, a.ks * kQgPart * 4, kBufWord3);
+    if (!producer) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][j]), rs,
+                                                 ((32 * ksi + 8 * i + j) * 256 + tid) * 16, 0, kSc1);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // every partial store acknowledged
+    }
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t* ctr = a.cnt + tile;
+      asm volatile("" : "+v"(ctr));  // per-lane address: a vector atomic
+      const uint32_t old = a.xch_local ? __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)
+                                       : __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t last = old == (uint32_t)(a.ks - 1);
+      if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *last_flag = last;
+    }
+    __syncthreads();
+    if (!*last_flag || producer) return;
+    const int other = 1 - ksi;
+    const int pol = a.xch_local ? 0 : kSc1;  // local: the L2 serves it (first touch on this CU)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, ((32 * other + 8 * i + j) * 256 + tid) * 16, 0,
-                                                              kSc1);
+        const u32x4 v = pol ? __builtin_amdgcn_raw_buffer_load_b128(rs, ((32 * other + 8 * i + j) * 256 + tid) * 16, 0, kSc1)
+                            : __builtin_amdgcn_raw_buffer_load_b128(rs, ((32 * other + 8 * i + j) * 256 + tid) * 16, 0, 0);
         acc[i][j] += __builtin_bit_cast(f32x4, v);
       }
   }
+  if (producer) return;
 
   // ---- epilogue: lane owns row m, columns n .. n + 3 of each tile ----
 #pragma unroll
@@ -354,6 +599,16 @@ __global__ __launch_bounds__(256) void qgemm_kernel(QgArgs a) {
 }  // namespace mk
 
 namespace mkq {
+
+unsigned qgemm_grid(int64_t M, int64_t N, int ks) {
+  return (unsigned)(((M + mk::kQgRows - 1) / mk::kQgRows) * (N / mk::kQgCols) * ks);
+}
+
+bool qgemm_tile_on_one_xcd(unsigned gx, int ks) {
+  // xcd_logical_id runs of gx / 8 consecutive ids share an XCD when the
+  // dispatcher deals round-robin; a tile's ks consecutive ids stay in one run.
+  return gx % 8 == 0 && (gx / 8) % (unsigned)ks == 0;
+}
 
 bool qgemm_supported(int64_t M, int64_t K, int64_t N) {
   // Per-lane offsets are 32-bit: the weight matrix and x stay under 2 GiB.
@@ -378,7 +633,7 @@ int64_t qgemm_workspace_bytes(int64_t M, int64_t K, int64_t N, int ks) {
 
 hipError_t qgemm_launch(bool int4, const void* x, const void* w, const void* s, const void* z, void* y, int64_t M,
                         int64_t K, int64_t N, const void* aux, int epi, int ks, void* workspace,
-                        hipStream_t stream) {
+                        hipStream_t stream, bool xch_local) {
   mk::QgArgs a;
   a.x = static_cast<const uint16_t*>(x);
   a.w = static_cast<const uint8_t*>(w);
@@ -393,7 +648,20 @@ hipError_t qgemm_launch(bool int4, const void* x, const void* w, const void* s, 
   a.ks = ks;
   a.cnt = ks > 1 ? static_cast<uint32_t*>(workspace) : nullptr;
   a.part = ks > 1 ? reinterpret_cast<float*>(static_cast<unsigned char*>(workspace) + kQgPartOffset) : nullptr;
-  const dim3 grid((unsigned)(((M + mk::kQgRows - 1) / mk::kQgRows) * (N / mk::kQgCols) * ks));
+  const dim3 grid(qgemm_grid(M, N, ks));
+  a.xch_local = ks > 1 && xch_local && qgemm_tile_on_one_xcd(grid.x, ks);
+  const char* ws_env = getenv("MK_QG_WS");
+  if (!(ws_env && ws_env[0] == '0')) {
+    // Warp-specialised kernel (8 waves, 140 KB of LDS).
+    const void* fn = int4 ? (const void*)mk::qgemm_ws_kernel<true> : (const void*)mk::qgemm_ws_kernel<false>;
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, mk::kQgWsLds);
+    if (e != hipSuccess) return e;
+    if (int4)
+      hipLaunchKernelGGL(mk::qgemm_ws_kernel<true>, grid, dim3(512), mk::kQgWsLds, stream, a);
+    else
+      hipLaunchKernelGGL(mk::qgemm_ws_kernel<false>, grid, dim3(512), mk::kQgWsLds, stream, a);
+    return hipGetLastError();
+  }
   if (int4)
     hipLaunchKernelGGL(mk::qgemm_kernel<true>, grid, dim3(256), 0, stream, a);
   else

@@ -1797,7 +1797,12 @@ int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, v
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e;
   if (p.qg) {
-    e = mkq::qgemm_launch(fmt == MK_QFMT_INT4_G64, x, w, s, z, y, M, K, N, aux, epi, p.ks, ws, st);
+    // The split-K exchange stays in one XCD's L2 when the placement probe
+    // has seen round-robin dealing (as for the wide kernel below).
+    const unsigned gx = mkq::qgemm_grid(M, N, p.ks);
+    const bool local = p.ks > 1 && mkq::qgemm_tile_on_one_xcd(gx, p.ks) &&
+                       xcd_round_robin(dim3(gx), st, reinterpret_cast<uint32_t*>(a.part));
+    e = mkq::qgemm_launch(fmt == MK_QFMT_INT4_G64, x, w, s, z, y, M, K, N, aux, epi, p.ks, ws, st, local);
     if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
     return MK_OK;
   }

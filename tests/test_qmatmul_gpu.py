@@ -230,6 +230,71 @@ def test_qgemm_split_k(monkeypatch, fmt, M, K, N):
     assert_rel_close(bf16_bits_to_f32(y2), bf16_bits_to_f32(y1), BF16_RTOL, f"{fmt} split vs unsplit")
 
 
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+@pytest.mark.parametrize("M,K,N", [(256, 4096, 14336), (256, 4096, 2048), (200, 1024, 1024)])
+def test_qgemm_exchange_in_l2_matches_device_scope(monkeypatch, fmt, M, K, N):
+    """The qgemm kernel's split-K exchange inside one XCD's L2 (taken when the
+    placement probe has seen round-robin dealing and the grid keeps each
+    tile's two K parts on one XCD) against the device-scope exchange
+    (MK_QMM_XCH=device): both add the other partial to their own, so the
+    outputs are bit-identical, on repeated calls too; the counters return to
+    zero."""
+    ops = _ops()
+    rng = np.random.default_rng(6000 + M + K + N)
+    if fmt == "int4":
+        x, packed, s, z = quant.make_int4_case(rng, M, K, N)
+        args = (dev_bf16(x), dev(packed), dev_bf16(s), dev(z))
+        run, ref = ops.int4_g64_matmul, cport.int4_g64_matmul(x[:64], packed, s, z)
+    else:
+        x, w, s = quant.make_int8_case(rng, M, K, N)
+        args = (dev_bf16(x), dev(w), dev(s))
+        run, ref = ops.int8_pc_matmul, cport.int8_pc_matmul(x[:64], w, s)
+    print(f"qgemm exchange {fmt} M={M} K={K} N={N}", flush=True)
+    local = [host_bf16_bits(run(*args)) for _ in range(3)]
+    monkeypatch.setenv("MK_QMM_XCH", "device")
+    dev_ = host_bf16_bits(run(*args))
+    torch.cuda.synchronize()
+    for y in local:
+        assert np.array_equal(y, dev_)
+    from oracle.bf16 import bf16_bits_to_f32
+    assert_rel_close(bf16_bits_to_f32(local[0])[:64], ref, BF16_RTOL, f"{fmt} qgemm {M}x{K}x{N} rows 0..63")
+    ws = ops.workspace(1, "cuda:0")
+    assert int(ws[: 64 * 1024].count_nonzero()) == 0
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8"])
+@pytest.mark.parametrize("M,K,N", [(256, 4096, 14336), (1000, 320, 256), (256, 64, 128), (200, 1024, 1024),
+                                   (512, 2048, 640)])
+def test_qgemm_warp_specialised_bit_identical(monkeypatch, fmt, M, K, N):
+    """The warp-specialised qgemm kernel (producer waves stream and
+    dequantise, consumer waves multiply) runs the same tile, k order,
+    dequantisation and split as the one-wave-per-SIMD kernel
+    (MK_QG_WS=0): the outputs are bit-identical, for split and unsplit K,
+    one step (K = 64), ragged row tiles; and within the bf16 tolerance of
+    the oracle on sampled rows."""
+    ops = _ops()
+    monkeypatch.setenv("MK_QMM_DEQ_M", "0")
+    rng = np.random.default_rng(7000 + M + K + N)
+    rows = np.array([0, 1, M // 2, M - 1])
+    if fmt == "int4":
+        x, packed, s, z = quant.make_int4_case(rng, M, K, N)
+        args = (dev_bf16(x), dev(packed), dev_bf16(s), dev(z))
+        run, ref = ops.int4_g64_matmul, cport.int4_g64_matmul(x[rows], packed, s, z)
+    else:
+        x, w, s = quant.make_int8_case(rng, M, K, N)
+        args = (dev_bf16(x), dev(w), dev(s))
+        run, ref = ops.int8_pc_matmul, cport.int8_pc_matmul(x[rows], w, s)
+    print(f"qgemm warp-specialised {fmt} M={M} K={K} N={N}", flush=True)
+    y_ws = [host_bf16_bits(run(*args)) for _ in range(2)]
+    monkeypatch.setenv("MK_QG_WS", "0")
+    y_old = host_bf16_bits(run(*args))
+    torch.cuda.synchronize()
+    assert np.array_equal(y_ws[0], y_old)
+    assert np.array_equal(y_ws[1], y_old)
+    from oracle.bf16 import bf16_bits_to_f32
+    assert_rel_close(bf16_bits_to_f32(y_ws[0])[rows], ref, BF16_RTOL, f"{fmt} qgemm ws {M}x{K}x{N}")
+
+
 def test_int4_g64_large_m_known_answer():
     """x = 1, q = 15, z = 14, s = 0.5 at M = 512: every output is K * 0.5."""
     ops = _ops()
