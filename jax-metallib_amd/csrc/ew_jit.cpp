@@ -245,6 +245,10 @@ std::string generate(int dtype, const mk_ew_instr* prog, int n_instr, int n_inpu
   s += bf ? "    float res[8];\n#pragma unroll\n    for (int e = 0; e < 8; e += 2) {\n"
           : "    float res[8];\n#pragma unroll\n    for (int e = 0; e < 8; ++e) {\n";
   std::string slot[16];
+  // Whether a slot's value is a bf16 value (8 significant bits): bf16 loads,
+  // bf16-representable constants, every rounded result, compare results,
+  // selects of two such values.  log1p of such a value takes the short form.
+  bool exact[16] = {};
   for (int i = 0; i < n_instr; ++i) {
     const mk_ew_instr& in = prog[i];
     const std::string v = "v" + std::to_string(i);
@@ -274,7 +278,9 @@ std::string generate(int dtype, const mk_ew_instr* prog, int n_instr, int n_inpu
         // short exp form (relative error < 2^-16) suffices there.
         case MK_EW_EXP: ex = (fast ? "mk_exp_bf(" : "mk_exp(") + A + ")"; break;
         case MK_EW_LOG: ex = (fast ? "__logf(" : "logf(") + A + ")"; break;
-        case MK_EW_LOG1P: ex = "mk_log1p(" + A + ")"; break;
+        case MK_EW_LOG1P:
+          ex = (fast && in.a >= 0 && in.a < 16 && exact[in.a] ? "mk_log1p_bf(" : "mk_log1p(") + A + ")";
+          break;
         case MK_EW_EXPM1: ex = "expm1f(" + A + ")"; break;
         case MK_EW_TANH: ex = "tanhf(" + A + ")"; break;
         case MK_EW_RSQRT: ex = "1.0f / sqrtf(" + A + ")"; break;
@@ -296,6 +302,18 @@ std::string generate(int dtype, const mk_ew_instr* prog, int n_instr, int n_inpu
     }
     s += decl + ";\n";
     if (rnd) s += "      R2(" + v + "_0, " + v + "_1);\n";
+    {
+      uint32_t ib;
+      memcpy(&ib, &in.imm, 4);
+      auto ex_of = [&](int k) { return k >= 0 && k < 16 && exact[k]; };
+      bool e = rnd;
+      if (opc == MK_EW_LOAD) e = bf && half[in.a];
+      else if (opc == MK_EW_CONST) e = (ib & 0xFFFFu) == 0u;
+      else if (opc >= MK_EW_CMP_EQ && opc <= MK_EW_CMP_GE) e = true;
+      else if (opc == MK_EW_SELECT) e = ex_of(in.b) && ex_of(in.c);
+      else if (opc == MK_EW_ROUND_BF16) e = true;
+      if (in.dst >= 0 && in.dst < 16) exact[in.dst] = e;
+    }
     slot[in.dst] = v;
   }
   s += bf ? "      res[e] = " + slot[out_slot] + "_0; res[e + 1] = " + slot[out_slot] + "_1;\n"

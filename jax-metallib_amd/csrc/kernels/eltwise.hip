@@ -189,7 +189,8 @@ __global__ __launch_bounds__(256) void eltwise_kernel(EwArgs a) {
         MK_EW_CASE(MK_EW_ABS, fabsf(u))
         MK_EW_CASE(MK_EW_EXP, round ? mk_exp_bf(u) : mk_exp(u))
         MK_EW_CASE(MK_EW_LOG, logf(u))
-        MK_EW_CASE(MK_EW_LOG1P, mk_log1p(u))
+        // A bf16-valued operand (low 16 bits clear) takes the short form.
+        MK_EW_CASE(MK_EW_LOG1P, round && (__float_as_uint(u) & 0xFFFFu) == 0u ? mk_log1p_bf(u) : mk_log1p(u))
         MK_EW_CASE(MK_EW_EXPM1, expm1f(u))
         MK_EW_CASE(MK_EW_TANH, tanhf(u))
         MK_EW_CASE(MK_EW_RSQRT, 1.0f / sqrtf(u))

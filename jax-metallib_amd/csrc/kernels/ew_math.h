@@ -18,7 +18,13 @@
 //             the reciprocal would flush.
 // bf16 programs round every op's result to 8 significant bits, so exp and
 // logistic use the short forms mk_exp_bf (2^(x*log2e), relative error
-// < 2^-16) and mk_logistic_bf.
+// < 2^-16) and mk_logistic_bf, and log1p of a bf16 value uses mk_log1p_bf:
+// for |x| >= 2^-15, u = 1 + x is exact in f32 (x has 8 significant bits, the
+// lowest at or above 2^-22; above 2^24 u rounds by at most 2^-24
+// relative), so log2(u) * ln2 is within ~2 f32 ulp of log1p(x); below,
+// log1p(x) = x (1 - x/2 + ...) rounds to x itself in bf16.  Infinities,
+// NaN, -1 and below come out of the log as log1p defines them, and -0 stays
+// -0 on the short branch.
 // maximum/minimum are the IEEE 754-2019 operations (v_maximum3/v_minimum3 on
 // gfx950): NaN propagates and -0 < +0, the StableHLO semantics.
 #pragma once
@@ -39,6 +45,9 @@
     const float c = (x - (u - 1.0f)) * __builtin_amdgcn_rcpf(u + 0x1p-100f); \
     const float y = __builtin_fmaf(__builtin_amdgcn_logf(u), LN2, c);                   \
     return u == __builtin_inff() ? u : (x == 0.0f ? x : y); /* log1p(-0) = -0 */     \
+  }                                                                                     \
+  __device__ __forceinline__ float mk_log1p_bf(float x) {                               \
+    return __builtin_fabsf(x) < 0x1p-15f ? x : __builtin_amdgcn_logf(1.0f + x) * 0.693147182f; \
   }                                                                                     \
   __device__ __forceinline__ float mk_exp_bf(float x) {                                 \
     return __builtin_exp2f(x * 1.44269502f);                                            \
