@@ -326,15 +326,15 @@ def traffic_from_profiles(kernel):
     return value, f"measured with sources {digest} (current)"
 
 
-# The 6-op elementwise chain of the row-op lines: select(x > 0, max(log1p(exp(1.5 x + 0.5)), 0), 1.5 x + 0.5).
+# The 6-op elementwise chain of the row-op lines: select(x > 0, max(log1p(exp(1.5 x + 0.5)), x), 1.5 x + 0.5).
 CHAIN6 = [("LOAD", 0, 0, 0, 0, 0.0), ("CONST", 1, 0, 0, 0, 1.5), ("MUL", 2, 0, 1, 0, 0.0),
           ("CONST", 1, 0, 0, 0, 0.5), ("ADD", 3, 2, 1, 0, 0.0), ("EXP", 4, 3, 0, 0, 0.0),
           ("LOG1P", 5, 4, 0, 0, 0.0), ("MAX", 6, 5, 0, 0, 0.0), ("CONST", 1, 0, 0, 0, 0.0),
           ("CMP_GT", 7, 0, 1, 0, 0.0), ("SELECT", 8, 7, 6, 3, 0.0)]
 
-PROFILE_KINDS = ("int4", "int8", "gemm", "qgemm", "int4_m1", "int8_m1", "int4_shard", "int8_shard", "bmm",
-                 "dequant4096", "attention", "softmax_f32", "softmax_bf16", "rmsnorm_f32", "rmsnorm_bf16",
-                 "argmax_f32", "argmax_bf16", "chain6_f32", "chain6_bf16")
+PROFILE_KINDS = ("int4", "int8", "gemm", "gemm_f32", "qgemm", "qgemm8", "int4_m1", "int8_m1", "int4_shard",
+                 "int8_shard", "bmm", "dequant4096", "dequant4096_8", "attention", "softmax_f32", "softmax_bf16",
+                 "rmsnorm_f32", "rmsnorm_bf16", "argmax_f32", "argmax_bf16", "chain6_f32", "chain6_bf16")
 
 
 def _profile_case(torch, ops, kind):
@@ -355,8 +355,9 @@ def _profile_case(torch, ops, kind):
         xd, wd, sd, zd = bf(x), torch.from_numpy(packed).cuda(), bf(s), torch.from_numpy(z).cuda()
         yd = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
         return lambda: ops.int4_g64_matmul(xd, wd, sd, zd, out=yd)
-    if kind in ("int8", "int8_m1", "int8_shard"):
-        M, N = {"int8": (16, 14336), "int8_m1": (1, 14336), "int8_shard": (16, 1792)}[kind]
+    if kind in ("int8", "int8_m1", "int8_shard", "qgemm8", "dequant4096_8"):
+        M, N = {"int8": (16, 14336), "int8_m1": (1, 14336), "int8_shard": (16, 1792), "qgemm8": (256, 14336),
+                "dequant4096_8": (4096, 14336)}[kind]
         x, w8, s8 = synthetic.int8_case(rng, M, 4096, N)
         xd, wd, sd = bf(x), torch.from_numpy(w8).cuda(), torch.from_numpy(s8).cuda()
         yd = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
@@ -370,6 +371,11 @@ def _profile_case(torch, ops, kind):
         if kind == "gemm":
             a, b, c = a[0], b[0], c[0]
         return lambda: ops.gemm_bf16(a, b, out=c)
+    if kind == "gemm_f32":
+        a = torch.randn((2048, 2048), device="cuda", generator=g)
+        b = torch.randn((2048, 2048), device="cuda", generator=g)
+        c = torch.empty((2048, 2048), device="cuda")
+        return lambda: ops.gemm_f32(a, b, out=c)
     if kind == "attention":
         # The decoder's attention at the workload's shape: 4 x 16 heads of
         # 2048 positions x 128, causal, heads merged on output.
@@ -683,7 +689,44 @@ def bench_end_to_end(warmup=10, iters=50):
             exe.close()
     finally:
         client.close()
+    out["int4_g64_M16_K4096_N14336"].update(_c_side_timing(x, packed, s, z, warmup, iters))
     return out
+
+
+def _c_side_timing(x, packed, s, z, warmup, iters):
+    """The int4 headline call timed from C, without Python in the loop: the
+    PJRT table as a C caller (jaxlib) drives it, and the host floor under it
+    (the kernel library's C-ABI launch plus an event polled to completion),
+    both by the harness jax-metallib_amd/lib/test/pjrt_harness."""
+    import subprocess
+    import tempfile
+
+    lib = os.path.join(REPO, "jax-metallib_amd", "lib")
+    harness = os.path.join(lib, "test", "pjrt_harness")
+    if not os.path.exists(harness):
+        return {"c_side": "pjrt_harness not built"}
+    from mi355x import programs
+
+    res = {}
+    with tempfile.TemporaryDirectory() as d:
+        specs = []
+        for name, arr, ptype in (("x", x, 13), ("w", packed, 6), ("s", s, 13), ("z", z, 6)):
+            path = os.path.join(d, name + ".bin")
+            with open(path, "wb") as f:
+                f.write(np.ascontiguousarray(arr).tobytes())
+            specs.append(f"{ptype}:{'x'.join(str(v) for v in arr.shape)}:{path}")
+        prog = os.path.join(d, "int4.mlir")
+        with open(prog, "w") as f:
+            f.write(programs.int4_g64_matmul(16, 4096, 14336))
+        runs = {"c_table": ["time", os.path.join(lib, "libmk_pjrt.so"), prog, str(warmup), str(iters)] + specs,
+                "hip_floor": ["floor", os.path.join(lib, "libmk_kernels.so"), "/opt/rocm/lib/libamdhip64.so",
+                              str(warmup), str(iters)]}
+        for key, args in runs.items():
+            r = subprocess.run([harness] + args, capture_output=True, text=True, timeout=120)
+            if r.returncode != 0:
+                raise SystemExit(f"bench.py: pjrt_harness {args[0]} failed ({r.returncode}): {r.stderr[-2000:]}")
+            res[key] = json.loads(r.stdout.strip().splitlines()[-1])
+    return res
 
 
 def main():
@@ -759,14 +802,22 @@ def main():
                              "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS,
                                           "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
                                           "traffic": None}}
-                    if M == 256 and fmt == "int4":
-                        qt, qn = traffic_from_profiles("qgemm_kernel_M256_K4096_N14336")
+                    if M == 256:
+                        qt, qn = traffic_from_profiles(
+                            "qgemm_ws_kernel_M256_K4096_N14336" if fmt == "int4"
+                            else "qgemm_ws_kernel_int8_M256_K4096_N14336")
                         entry["roofline"].update({"traffic": qt, "traffic_note": qn})
-                    if M == 4096 and fmt == "int4":
-                        # The route's HBM-bound first pass (W int4 -> bf16), beside the GEMM's MFMA roofline.
-                        dt, dn = traffic_from_profiles("qmm_dequant_kernel_int4_K4096_N14336")
-                        entry["dequant_pass"] = {"kernel": "qmm_dequant_kernel<true>", "algorithmic_bytes": 149553152,
-                                                 "traffic": dt, "traffic_note": dn}
+                    if M == 4096:
+                        # The route's GEMM (the MFMA roofline above; same
+                        # kernel and shape for both formats) and its
+                        # HBM-bound first pass (W -> bf16) beside it.
+                        gt, gn = traffic_from_profiles("gemm_bf16_256dma_kernel_4096x14336x4096")
+                        entry["roofline"].update({"traffic": gt, "traffic_note": gn})
+                        dt, dn = traffic_from_profiles(f"qmm_dequant_kernel_{fmt}_K4096_N14336")
+                        entry["dequant_pass"] = {
+                            "kernel": f"qmm_dequant_kernel<{'true' if fmt == 'int4' else 'false'}>",
+                            "algorithmic_bytes": 149553152 if fmt == "int4" else 176218112,
+                            "traffic": dt, "traffic_note": dn}
                 secondary[f"{fmt}_dequant_matmul_M{M}"] = entry
 
     if want("shard"):
@@ -811,10 +862,12 @@ def main():
                                                            profile="gemm_bf16_batched_16x2048x128x2048")
         rf = bench_gemm_f32(torch, ops, max(50, args.steps // 20), 5)
         log(f"[bench] f32 gemm 2048^3: {rf['sec_per_call'] * 1e6:.1f} us, {rf['tflops']:.1f} TFLOP/s")
+        ft, fnote = traffic_from_profiles("gemm_f32_kernel_2048")
         secondary["f32_gemm_2048"] = {
             "value": round(rf["tflops"], 2), "unit": "TFLOP/s", "us_per_call": round(rf["sec_per_call"] * 1e6, 3),
             "roofline": {"bound": "mfma", "achieved": round(rf["tflops"], 2), "peak": 157.3,
-                         "unit": "TFLOP/s", "frac": round(rf["tflops"] / 157.3, 4), "traffic": None}}
+                         "unit": "TFLOP/s", "frac": round(rf["tflops"] / 157.3, 4), "traffic": ft,
+                         "traffic_note": fnote}}
     if want("decoder"):
         rd = bench_decoder(torch)
         log(f"[bench] decoder forward: {rd['ms']:.3f} ms, {rd['tokens_per_s']:.0f} tokens/s, {rd['tflops']:.1f} TFLOP/s")

@@ -25,14 +25,28 @@
  *                                  Also checks Serialize / DeserializeAndLoad,
  *                                  output metadata, the device assignment,
  *                                  CopyRawToHost, buffer deletion.
+ *   time LIB PROGRAM WARMUP ITERS IN...
+ *                                  the plugin path as a C caller drives it:
+ *                                  Compile once, then per call Execute,
+ *                                  Event_Await and Buffer_Destroy of the
+ *                                  outputs, inputs resident; prints one
+ *                                  JSON line of per-call wall-clock times
+ *   floor KLIB HIPLIB WARMUP ITERS the host floor under that path: the int4
+ *                                  g64 M=16 K=4096 N=14336 product called
+ *                                  straight through the kernel library's
+ *                                  C-ABI on a stream of its own, an event
+ *                                  recorded behind it and polled until
+ *                                  ready, per call; same JSON line
  *
  * Exit status 0 on success; a failing check prints "FAIL: ..." and exits 1.
  */
+#define _POSIX_C_SOURCE 200809L
 #include <dlfcn.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 #include "pjrt_c_api_mi355x.h"
 
@@ -727,12 +741,157 @@ static int mode_run(int argc, char** argv) {
   return 0;
 }
 
+static double now_us(void) {
+  struct timespec t;
+  clock_gettime(CLOCK_MONOTONIC, &t);
+  return (double)t.tv_sec * 1e6 + (double)t.tv_nsec * 1e-3;
+}
+
+static int cmp_double(const void* a, const void* b) {
+  const double x = *(const double*)a, y = *(const double*)b;
+  return (x > y) - (x < y);
+}
+
+static void report(const char* what, double* t, int n) {
+  qsort(t, (size_t)n, sizeof(double), cmp_double);
+  printf("{\"what\": \"%s\", \"median_us\": %.2f, \"min_us\": %.2f, \"p90_us\": %.2f, \"iters\": %d}\n", what,
+         t[n / 2], t[0], t[(int)(0.9 * (n - 1))], n);
+}
+
+static int mode_time(int argc, char** argv) {
+  void* h = load(argv[2]);
+  const PJRT_Api* (*get)(void) = (const PJRT_Api* (*)(void))dlsym(h, "GetPjrtApi");
+  check(get != NULL, "GetPjrtApi");
+  api = get();
+  PJRT_Client* c = create_client(1);
+  long plen = 0;
+  char* prog = read_file(argv[3], &plen);
+  PJRT_LoadedExecutable* le = compile_program(c, prog, plen);
+  const int warmup = atoi(argv[4]), iters = atoi(argv[5]);
+  check(warmup >= 0 && iters > 0, "WARMUP >= 0, ITERS > 0");
+  const size_t nin = (size_t)(argc - 6);
+  PJRT_Buffer** in = (PJRT_Buffer**)calloc(nin + 1, sizeof(PJRT_Buffer*));
+  for (size_t i = 0; i < nin; ++i) in[i] = upload(c, argv[6 + i]);
+  ARGS(PJRT_LoadedExecutable_GetExecutable_Args, ge);
+  ge.loaded_executable = le;
+  ok(api->PJRT_LoadedExecutable_GetExecutable(&ge), "GetExecutable");
+  ARGS(PJRT_Executable_NumOutputs_Args, no);
+  no.executable = ge.executable;
+  ok(api->PJRT_Executable_NumOutputs(&no), "NumOutputs");
+  PJRT_Buffer** out = (PJRT_Buffer**)calloc(no.num_outputs + 1, sizeof(PJRT_Buffer*));
+  double* t = (double*)malloc(sizeof(double) * (size_t)iters);
+  for (int i = 0; i < warmup + iters; ++i) {
+    const double t0 = now_us();
+    execute(le, in, nin, out);
+    for (size_t r = 0; r < no.num_outputs; ++r) destroy_buffer(out[r]);
+    if (i >= warmup) t[i - warmup] = now_us() - t0;
+  }
+  report("PJRT table from C: Execute + Event_Await + Buffer_Destroy", t, iters);
+  for (size_t i = 0; i < nin; ++i) destroy_buffer(in[i]);
+  ARGS(PJRT_Executable_Destroy_Args, xd);
+  xd.executable = ge.executable;
+  ok(api->PJRT_Executable_Destroy(&xd), "Executable_Destroy");
+  ARGS(PJRT_LoadedExecutable_Destroy_Args, ld);
+  ld.executable = le;
+  ok(api->PJRT_LoadedExecutable_Destroy(&ld), "LoadedExecutable_Destroy");
+  destroy_client(c);
+  free(t);
+  free(in);
+  free(out);
+  free(prog);
+  return 0;
+}
+
+/* HIP runtime entry points used by the floor mode, resolved with dlsym (the
+ * harness is plain C with no HIP headers); hipError_t is an int, 0 success,
+ * 600 hipErrorNotReady. */
+typedef int (*hip_malloc_fn)(void**, size_t);
+typedef int (*hip_memset_fn)(void*, int, size_t);
+typedef int (*hip_free_fn)(void*);
+typedef int (*hip_handle_fn)(void**);
+typedef int (*hip_event_create_fn)(void**, unsigned);
+typedef int (*hip_record_fn)(void*, void*);
+typedef int (*hip_query_fn)(void*);
+typedef int (*hip_destroy_fn)(void*);
+typedef int (*hip_sync_fn)(void);
+typedef int64_t (*mk_ws_fn)(int, int64_t, int64_t, int64_t);
+typedef int (*mk_int4_fn)(const void*, const void*, const void*, const void*, void*, int64_t, int64_t, int64_t, void*,
+                          int64_t, void*);
+
+static void* sym(void* h, const char* name) {
+  void* f = dlsym(h, name);
+  if (!f) {
+    fprintf(stderr, "FAIL: symbol %s: %s\n", name, dlerror());
+    exit(1);
+  }
+  return f;
+}
+
+static int mode_floor(char** argv) {
+  void* hk = load(argv[2]);
+  void* hh = load(argv[3]);
+  const int warmup = atoi(argv[4]), iters = atoi(argv[5]);
+  check(warmup >= 0 && iters > 0, "WARMUP >= 0, ITERS > 0");
+  hip_malloc_fn hmalloc = (hip_malloc_fn)sym(hh, "hipMalloc");
+  hip_memset_fn hmemset = (hip_memset_fn)sym(hh, "hipMemset");
+  hip_free_fn hfree = (hip_free_fn)sym(hh, "hipFree");
+  hip_handle_fn hstream = (hip_handle_fn)sym(hh, "hipStreamCreate");
+  hip_event_create_fn hevent = (hip_event_create_fn)sym(hh, "hipEventCreateWithFlags");
+  hip_record_fn hrecord = (hip_record_fn)sym(hh, "hipEventRecord");
+  hip_query_fn hquery = (hip_query_fn)sym(hh, "hipEventQuery");
+  hip_destroy_fn hsdestroy = (hip_destroy_fn)sym(hh, "hipStreamDestroy");
+  hip_destroy_fn hedestroy = (hip_destroy_fn)sym(hh, "hipEventDestroy");
+  hip_sync_fn hsync = (hip_sync_fn)sym(hh, "hipDeviceSynchronize");
+  mk_ws_fn ws_bytes = (mk_ws_fn)sym(hk, "mk_qmatmul_workspace_bytes");
+  mk_int4_fn int4 = (mk_int4_fn)sym(hk, "mk_int4g64_matmul_bf16");
+  const int64_t M = 16, K = 4096, N = 14336;
+  /* x bf16 [M,K], w [K/2,N], scale bf16 [K/64,N], zero [K/64,N], y bf16 [M,N];
+   * zero-filled (the kernel's time does not depend on the values). */
+  const size_t bytes[5] = {(size_t)(M * K * 2), (size_t)(K / 2 * N), (size_t)(K / 64 * N * 2), (size_t)(K / 64 * N),
+                           (size_t)(M * N * 2)};
+  void* d[5];
+  for (int i = 0; i < 5; ++i) {
+    check(hmalloc(&d[i], bytes[i]) == 0, "hipMalloc");
+    check(hmemset(d[i], 0, bytes[i]) == 0, "hipMemset");
+  }
+  const int64_t wsb = ws_bytes(0, M, K, N);
+  void* ws = NULL;
+  if (wsb > 0) {
+    check(hmalloc(&ws, (size_t)wsb) == 0, "hipMalloc workspace");
+    check(hmemset(ws, 0, (size_t)wsb) == 0, "hipMemset workspace");
+  }
+  void *stream = NULL, *ev = NULL;
+  check(hstream(&stream) == 0, "hipStreamCreate");
+  check(hevent(&ev, 2u /* hipEventDisableTiming */) == 0, "hipEventCreateWithFlags");
+  check(hsync() == 0, "hipDeviceSynchronize");
+  double* t = (double*)malloc(sizeof(double) * (size_t)iters);
+  for (int i = 0; i < warmup + iters; ++i) {
+    const double t0 = now_us();
+    check(int4(d[0], d[1], d[2], d[3], d[4], M, K, N, ws, wsb, stream) == 0, "mk_int4g64_matmul_bf16");
+    check(hrecord(ev, stream) == 0, "hipEventRecord");
+    int q;
+    while ((q = hquery(ev)) == 600) {
+    }
+    check(q == 0, "hipEventQuery");
+    if (i >= warmup) t[i - warmup] = now_us() - t0;
+  }
+  report("kernel C-ABI launch + hipEventRecord + hipEventQuery poll", t, iters);
+  check(hedestroy(ev) == 0 && hsdestroy(stream) == 0, "destroy stream and event");
+  for (int i = 0; i < 5; ++i) hfree(d[i]);
+  if (ws) hfree(ws);
+  free(t);
+  return 0;
+}
+
 int main(int argc, char** argv) {
   if (argc >= 4 && strcmp(argv[1], "api") == 0) return mode_api(argv[2], argv[3]);
   if (argc >= 4 && strcmp(argv[1], "parse") == 0) return mode_fuzz(argc, argv, 1);
   if (argc >= 4 && strcmp(argv[1], "inspect") == 0) return mode_fuzz(argc, argv, 0);
   if (argc >= 5 && strcmp(argv[1], "run") == 0) return mode_run(argc, argv);
+  if (argc >= 6 && strcmp(argv[1], "time") == 0) return mode_time(argc, argv);
+  if (argc == 6 && strcmp(argv[1], "floor") == 0) return mode_floor(argv);
   fprintf(stderr, "usage: pjrt_harness api LIB gpu|nogpu | parse KLIB FILE... | inspect KLIB FILE... | "
-                  "run LIB PROGRAM OUT TYPE:DIMS:PATH...\n");
+                  "run LIB PROGRAM OUT TYPE:DIMS:PATH... | time LIB PROGRAM WARMUP ITERS TYPE:DIMS:PATH... | "
+                  "floor KLIB HIPLIB WARMUP ITERS\n");
   return 2;
 }

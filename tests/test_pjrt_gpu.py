@@ -118,3 +118,19 @@ def test_argmax_from_a_portable_artifact(tmp_path):
     _run(["run", PJRT, str(prog), str(out), _spec(tmp_path, "x", x, F32)])
     y = np.frombuffer(out.read_bytes(), dtype=np.int32)
     assert np.array_equal(y, rowops.argmax(x))
+
+
+def test_timing_modes(tmp_path):
+    """The harness's two timing modes (bench.py's C-side figures for the
+    decode-shaped call) run and report per-call times."""
+    import json
+    M, K, N = 16, 4096, 14336
+    x, packed, s, z = quant.make_int4_case(np.random.default_rng(2), M, K, N)
+    prog = tmp_path / "int4.mlir"
+    prog.write_text(P.int4_g64_matmul(M, K, N))
+    specs = [_spec(tmp_path, "x", x, BF16), _spec(tmp_path, "w", packed, U8), _spec(tmp_path, "s", s, BF16),
+             _spec(tmp_path, "z", z, U8)]
+    for args in (["time", PJRT, str(prog), "2", "5"] + specs,
+                 ["floor", os.path.join(LIB, "libmk_kernels.so"), "/opt/rocm/lib/libamdhip64.so", "2", "5"]):
+        rep = json.loads(_run(args).strip().splitlines()[-1])
+        assert rep["iters"] == 5 and 0 < rep["min_us"] <= rep["median_us"] <= rep["p90_us"], rep
