@@ -863,6 +863,294 @@ __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs
   }
 }
 
+// ---------------------------------------------------------------------------
+// Short-K kernel (K <= 256, e.g. the batched [2048,128] x [128,2048] product):
+// output-store bound, the 256 x 256 kernel runs one workgroup per CU and
+// serialises its loads, its 128 KB of MFMA work and its 128 KB of stores.
+// Here a 128 x 128 tile keeps all of K in LDS (16 KB per 32 k: A [128][32]
+// then B [32][128], the same chunk swizzles as above), so at K = 128 a
+// workgroup takes 64 KB and two run on a CU: one's stores drain while the
+// other loads and multiplies.  Four waves of 64 x 64 (4 x 4 MFMA tiles); all
+// DMAs are issued up front and each 32-k stage is multiplied once it has
+// landed.  The bf16 tile is then staged in LDS over A / B (rows of 272 B) and
+// written out in 256-byte row pieces, with the ADD / SWIGLU epilogue applied
+// on the way.  Each k runs in the same order in the same MFMA as in the 256
+// x 256 kernels, so the f32 accumulators, and the bf16 results, are the
+// same bits.
+// ---------------------------------------------------------------------------
+constexpr int kShortStageBytes = 16 * 1024;
+constexpr int kShortEpiRow = 136;  // bf16 per staged row (128 + 8 pad: consecutive rows 4 banks apart)
+constexpr int kShortEpiBytes = 128 * kShortEpiRow * 2;
+
+__host__ __device__ constexpr int short_lds_bytes(int kt) {
+  return kt * kShortStageBytes > kShortEpiBytes ? kt * kShortStageBytes : kShortEpiBytes;
+}
+
+template <int KT>
+__global__ __launch_bounds__(256) void gemm_bf16_shortk_kernel(GemmArgs p) {
+  constexpr int BM = 128, BN = 128, BK = 32, TM = 4, TN = 4;
+  constexpr int ABYTES = BM * BK * 2;  // 8 KB
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tiles_m = p.M / BM, tiles_n = p.N / BN;
+  int tm, tn;
+  tile_coords(xcd_logical_id(blockIdx.x, gridDim.x), tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int K = p.K, N = p.N;
+  const uint16_t* A = static_cast<const uint16_t*>(p.a) + (size_t)blockIdx.z * p.sa + (size_t)m0 * K;
+  const uint16_t* B = static_cast<const uint16_t*>(p.b) + (size_t)blockIdx.z * p.sb + n0;
+  const uint32_t sbase = lds_addr(smem);
+
+  // DMA, per 32-k stage, 8 A and 8 B instructions of 1 KB, two of each per
+  // wave.  A instruction i: lane L fills row 16i + L/4, 16-byte chunk L%4.
+  // B instruction i: lane L fills k row 4i + L/16, chunk L%16.
+  {
+    const uint16_t* asrc[2];
+    const uint16_t* bsrc[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = 2 * wave + u;
+      const int row = 16 * i + (lane >> 2), pa = lane & 3;
+      asrc[u] = A + (size_t)row * K + 8 * (pa ^ ((row >> 1) & 3));
+      const int kr = 4 * i + (lane >> 4), pb = lane & 15;
+      bsrc[u] = B + (size_t)kr * N + 8 * swz_b2(kr, pb);
+    }
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+      const uint32_t st = sbase + (uint32_t)(kt * kShortStageBytes);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) dma16_asm(asrc[u] + kt * BK, st + (uint32_t)((2 * wave + u) * 1024));
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        dma16_asm(bsrc[u] + (size_t)kt * BK * N, st + (uint32_t)(ABYTES + (2 * wave + u) * 1024));
+    }
+  }
+
+  // Fragment offsets within a stage (as in the 256 x 256 kernel, for 128-row
+  // A stages and 256-byte B rows).
+  const int arow = wm * 64 + (lane & 15);
+  const int aoff = arow * 64 + 16 * ((lane >> 4) ^ ((arow >> 1) & 3));
+  int boff[2 * TN];
+  {
+    const int g = lane >> 4, r = (lane & 15) >> 2, q = lane & 3;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = wn * 64 + 16 * j + 4 * q;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int k1 = 8 * g + r + 4 * h;
+        boff[2 * j + h] = ABYTES + k1 * (BN * 2) + 16 * swz_b2(k1, col >> 3) + 2 * (col & 7);
+      }
+    }
+  }
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) {
+    // This wave's DMAs of stages 0..kt have landed (4 per stage, in order).
+    vm_wait(4 * (KT - 1 - kt));
+    asm volatile("s_barrier" ::: "memory");
+    const unsigned char* st = smem + kt * kShortStageBytes;
+    u32x4 bf[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(st + boff[2 * j]));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(st + boff[2 * j + 1]));
+      const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+      bf[j] = u32x4{l2.x, l2.y, h2.x, h2.y};
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const u32x4 af = *reinterpret_cast<const u32x4*>(st + aoff + 1024 * i);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(bf[j], af, acc[i][j]);
+    }
+  }
+
+  // Stage the bf16 tile over the operands (lane: row lane & 15 of its 16-row
+  // block, columns 4 (lane >> 4) .. +3 of its 16-column block), then write
+  // rows out 16 bytes per lane.
+  uint16_t* stg = reinterpret_cast<uint16_t*>(smem);
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      *reinterpret_cast<u32x2*>(stg + (wm * 64 + 16 * i + (lane & 15)) * kShortEpiRow + wn * 64 + 16 * j +
+                                4 * (lane >> 4)) =
+          u32x2{pack_bf16x2(acc[i][j].x, acc[i][j].y), pack_bf16x2(acc[i][j].z, acc[i][j].w)};
+  __syncthreads();
+  uint16_t* C = static_cast<uint16_t*>(p.c) + (size_t)blockIdx.z * p.sc;
+  const uint16_t* X = p.aux ? p.aux + (size_t)blockIdx.z * p.sc : nullptr;
+  auto f4 = [](uint32_t lo, uint32_t hi) {
+    return f32x4{bf16_to_f32(lo & 0xffffu), bf16_to_f32(lo >> 16), bf16_to_f32(hi & 0xffffu), bf16_to_f32(hi >> 16)};
+  };
+#pragma unroll 4
+  for (int r = 0; r < BM / 16; ++r) {
+    const int row = 16 * r + (tid >> 4), c8 = 8 * (tid & 15);
+    const u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * kShortEpiRow + c8);
+    const size_t off = (size_t)(m0 + row) * N + n0 + c8;
+    if (p.epi == MK_EPI_NONE) {
+      *reinterpret_cast<u32x4*>(C + off) = v;
+    } else {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(X + off);
+      epi_store_bf16x4_v(C, u32x2{w.x, w.y}, p.epi, off, f4(v.x, v.y));
+      epi_store_bf16x4_v(C, u32x2{w.z, w.w}, p.epi, off + 4, f4(v.z, v.w));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Persistent short-K kernel (K <= 128): 256 x 256 tiles as in the kernel
+// above (2 x 4 waves of 128 x 64, the same stage layout, swizzles and MFMA
+// order, so the same bits), one workgroup per CU walking tiles t, t + grid,
+// ....  All of K fits the ring (KT stages of 32 KB), so as soon as a tile's
+// MFMAs are done the next tile's DMAs are issued, and the current tile is
+// stored while they are in flight: loads, MFMAs and the 128 KB of stores of
+// consecutive tiles overlap instead of following each other.  The stores go
+// through a 2 KB LDS buffer per wave (16 rows x 128 B, 16-byte chunks XOR
+// row % 8): each 16 x 64 block of the wave's accumulators is written 8 bytes
+// per lane and read back as full 128-byte row pieces, with no workgroup
+// barrier, so the ring is never touched by the epilogue.
+// ---------------------------------------------------------------------------
+constexpr int kPersistWaveStage = 2048;
+
+__host__ __device__ constexpr int persist_lds_bytes(int kt) { return kt * kGemmStageBytes + 8 * kPersistWaveStage; }
+
+template <int KT>
+__global__ __launch_bounds__(512) void gemm_bf16_persist_kernel(GemmArgs p, int batch) {
+  constexpr int BM = 256, BN = 256, BK = 32, TM = 8, TN = 4, DI = 2;
+  constexpr int ABYTES = BM * BK * 2;  // 16 KB
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
+  const int tiles_m = p.M / BM, tiles_n = p.N / BN, per_batch = tiles_m * tiles_n;
+  const int total = per_batch * batch;
+  const int K = p.K, N = p.N;
+  const uint32_t sbase = lds_addr(smem);
+  unsigned char* wstage = smem + KT * kGemmStageBytes + wave * kPersistWaveStage;
+
+  auto coords = [&](int t, int& z, int& m0, int& n0) {
+    z = t / per_batch;
+    int tm, tn;
+    tile_coords((uint32_t)(t - z * per_batch), tiles_m, tiles_n, tm, tn);
+    m0 = tm * BM;
+    n0 = tn * BN;
+  };
+  // DMA of all KT stages of tile t (as the ring kernel: A instruction i fills
+  // rows 16i..16i+15, B instruction i k rows 2i, 2i+1; two of each per wave).
+  auto issue = [&](int t) {
+    int z, m0, n0;
+    coords(t, z, m0, n0);
+    const uint16_t* A = static_cast<const uint16_t*>(p.a) + (size_t)z * p.sa + (size_t)m0 * K;
+    const uint16_t* B = static_cast<const uint16_t*>(p.b) + (size_t)z * p.sb + n0;
+#pragma unroll
+    for (int u = 0; u < DI; ++u) {
+      const int i = DI * wave + u;
+      const int row = 16 * i + (lane >> 2), pa = lane & 3;
+      const uint16_t* as = A + (size_t)row * K + 8 * (pa ^ ((row >> 1) & 3));
+      const int kr = 2 * i + (lane >> 5), pb = lane & 31;
+      const uint16_t* bs = B + (size_t)kr * N + 8 * swz_b2(kr, pb);
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        const uint32_t st = sbase + (uint32_t)(kt * kGemmStageBytes);
+        dma16_asm(as + kt * BK, st + (uint32_t)(i * 1024));
+        dma16_asm(bs + (size_t)kt * BK * N, st + (uint32_t)(ABYTES + i * 1024));
+      }
+    }
+  };
+
+  const int arow = wm * 128 + (lane & 15);
+  const int aoff = arow * 64 + 16 * ((lane >> 4) ^ ((arow >> 1) & 3));
+  int boff[2 * TN];
+  {
+    const int g = lane >> 4, r = (lane & 15) >> 2, q = lane & 3;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = wn * 64 + 16 * j + 4 * q;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int k1 = 8 * g + r + 4 * h;
+        boff[2 * j + h] = ABYTES + k1 * (BN * 2) + 16 * swz_b2(k1, col >> 3) + 2 * (col & 7);
+      }
+    }
+  }
+  // Wave staging: element (row, col) of a 16 x 64 block at row * 128 +
+  // 16 * ((col / 8) ^ (row % 8)) + 2 * (col % 8).
+  const int sr = lane & 15, sg = lane >> 4;
+  const int rrow = lane >> 3, rchunk = lane & 7;
+  auto f4 = [](uint32_t lo, uint32_t hi) {
+    return f32x4{bf16_to_f32(lo & 0xffffu), bf16_to_f32(lo >> 16), bf16_to_f32(hi & 0xffffu), bf16_to_f32(hi >> 16)};
+  };
+
+  int t = blockIdx.x;
+  if (t < total) issue(t);
+  for (; t < total; t += gridDim.x) {
+    // Tile t's operands have landed (and the previous tile's stores are done).
+    vm_wait(0);
+    asm volatile("s_barrier" ::: "memory");
+    f32x4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+      const unsigned char* st = smem + kt * kGemmStageBytes;
+      u32x4 bf[TN];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(st + boff[2 * j]));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(st + boff[2 * j + 1]));
+        const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+        bf[j] = u32x4{l2.x, l2.y, h2.x, h2.y};
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const u32x4 af = *reinterpret_cast<const u32x4*>(st + aoff + 1024 * i);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(bf[j], af, acc[i][j]);
+      }
+    }
+    // Every wave's fragment reads of this tile are done: the ring is free.
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (t + (int)gridDim.x < total) issue(t + gridDim.x);
+
+    int z, m0, n0;
+    coords(t, z, m0, n0);
+    uint16_t* C = static_cast<uint16_t*>(p.c) + (size_t)z * p.sc;
+    const uint16_t* X = p.aux ? p.aux + (size_t)z * p.sc : nullptr;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int col = 16 * j + 4 * sg;
+        *reinterpret_cast<u32x2*>(wstage + sr * 128 + 16 * ((col >> 3) ^ (sr & 7)) + 2 * (col & 7)) =
+            u32x2{pack_bf16x2(acc[i][j].x, acc[i][j].y), pack_bf16x2(acc[i][j].z, acc[i][j].w)};
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int row = rrow + 8 * h;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(wstage + row * 128 + 16 * (rchunk ^ (row & 7)));
+        const size_t off = (size_t)(m0 + wm * 128 + 16 * i + row) * N + n0 + wn * 64 + 8 * rchunk;
+        if (p.epi == MK_EPI_NONE) {
+          *reinterpret_cast<u32x4*>(C + off) = v;
+        } else {
+          const u32x4 w = *reinterpret_cast<const u32x4*>(X + off);
+          epi_store_bf16x4_v(C, u32x2{w.x, w.y}, p.epi, off, f4(v.x, v.y));
+          epi_store_bf16x4_v(C, u32x2{w.z, w.w}, p.epi, off + 4, f4(v.z, v.w));
+        }
+      }
+    }
+  }
+}
+
 }  // namespace mk
 
 // ---------------------------------------------------------------------------
@@ -871,6 +1159,7 @@ __global__ __launch_bounds__(2 * WN_ * 64) void gemm_bf16_256dma_kernel(GemmArgs
 #include "../capi_internal.h"
 
 #include <algorithm>
+#include <atomic>
 
 namespace {
 
@@ -917,6 +1206,18 @@ int check_gemm(const char* fn, const void* a, const void* b, void* c, int64_t ba
   return MK_OK;
 }
 
+// Compute units of the current device (queried once per device).
+int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+  cache[dev].store(v, std::memory_order_relaxed);
+  return v;
+}
+
 int env_tile() {
   const char* v = getenv("MK_GEMM_TILE");
   return v ? atoi(v) : 0;
@@ -957,7 +1258,57 @@ int run_gemm_bf16(const char* fn, const void* a, const void* b, void* c, const v
   if (tile == 0) tile = big_tiles >= 128 ? 256 : 128;
   if (epi == MK_EPI_SWIGLU_PAIRS) tile = 256;
   hipError_t e;
-  if (bt) {
+  // Short K on 128-multiples that are not 256-multiples: the 128 x 128
+  // kernel with all of K in LDS (two workgroups per CU at K <= 128), faster
+  // there than the generic 128 x 128 kernel (16 x 2048^2 x 128: 59 against
+  // 73 us).  MK_GEMM_SHORTK sets the largest K it takes (0: never, up to
+  // 256; with 256-multiples it is taken only when the persistent kernel
+  // below is off).
+  const char* sk = getenv("MK_GEMM_SHORTK");
+  const int64_t shortk_max = std::min<int64_t>(sk ? atoll(sk) : 128, 256);
+  const bool shortk = !bt && !out_f32 && (epi == MK_EPI_NONE || epi == MK_EPI_ADD || epi == MK_EPI_SWIGLU) &&
+                      M % 128 == 0 && N % 128 == 0 && K % 32 == 0 && K <= shortk_max;
+  // K <= 128 on 256 x 256 tiles: the persistent kernel (one workgroup per
+  // CU, the next tile's loads under the current tile's stores): 16 x 2048^2
+  // x 128 50.1 against 54 us for the ring kernel, x 64 32.7 against 42 us,
+  // 8192^2 x 128 41.9 against 56 us.  MK_GEMM_PERSIST=0 turns it off.
+  const char* pe = getenv("MK_GEMM_PERSIST");
+  const bool persist = !(pe && pe[0] == '0') && dma && !bt && !out_f32 &&
+                       (epi == MK_EPI_NONE || epi == MK_EPI_ADD || epi == MK_EPI_SWIGLU) && M % 256 == 0 &&
+                       N % 256 == 0 && K % 32 == 0 && K <= 128;
+  if (persist) {
+    const int64_t total = (M / 256) * (N / 256) * batch;
+    const int cus = device_cus();
+    const dim3 grid((unsigned)std::min<int64_t>(total, cus));
+    switch (K / 32) {
+#define MK_PERSIST_CASE(KT)                                                                              \
+  case KT:                                                                                               \
+    e = lds_opt_in((const void*)mk::gemm_bf16_persist_kernel<KT>, (size_t)mk::persist_lds_bytes(KT));   \
+    if (e == hipSuccess)                                                                                 \
+      hipLaunchKernelGGL((mk::gemm_bf16_persist_kernel<KT>), grid, dim3(512), mk::persist_lds_bytes(KT), st, p, \
+                         (int)batch);                                                                    \
+    break;
+      MK_PERSIST_CASE(1) MK_PERSIST_CASE(2) MK_PERSIST_CASE(3) MK_PERSIST_CASE(4)
+#undef MK_PERSIST_CASE
+      default: e = hipErrorInvalidValue;
+    }
+    if (e == hipSuccess) e = hipGetLastError();
+  } else if (shortk) {
+    const dim3 grid((unsigned)((M / 128) * (N / 128)), 1, (unsigned)batch);
+    switch (K / 32) {
+#define MK_SHORTK_CASE(KT)                                                                           \
+  case KT:                                                                                           \
+    e = lds_opt_in((const void*)mk::gemm_bf16_shortk_kernel<KT>, (size_t)mk::short_lds_bytes(KT));  \
+    if (e == hipSuccess)                                                                             \
+      hipLaunchKernelGGL((mk::gemm_bf16_shortk_kernel<KT>), grid, dim3(256), mk::short_lds_bytes(KT), st, p); \
+    break;
+      MK_SHORTK_CASE(1) MK_SHORTK_CASE(2) MK_SHORTK_CASE(3) MK_SHORTK_CASE(4)
+      MK_SHORTK_CASE(5) MK_SHORTK_CASE(6) MK_SHORTK_CASE(7) MK_SHORTK_CASE(8)
+#undef MK_SHORTK_CASE
+      default: e = hipErrorInvalidValue;
+    }
+    if (e == hipSuccess) e = hipGetLastError();
+  } else if (bt) {
     const dim3 grid((unsigned)((M / 256) * (N / 256)), 1, (unsigned)batch);
     const char* pv = getenv("MK_GEMM_PIPE");
     const char* pk = getenv("MK_GEMM_PIPE_K");

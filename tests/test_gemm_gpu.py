@@ -145,9 +145,12 @@ def test_gemm_f32_overflow_case():
 @pytest.mark.parametrize("batch,M,N,K", [(1, 256, 256, 64), (3, 512, 768, 320), (2, 1024, 256, 1024)])
 def test_gemm_bf16_large_tile_path(batch, M, N, K, monkeypatch):
     """The 256x256 kernel (transposing LDS reads for B) on shapes small enough
-    for a full float64 check, forced with MK_GEMM_TILE=256."""
+    for a full float64 check, forced with MK_GEMM_TILE=256 (and the short-K
+    kernel off)."""
     ops = _ops()
     monkeypatch.setenv("MK_GEMM_TILE", "256")
+    monkeypatch.setenv("MK_GEMM_SHORTK", "0")
+    monkeypatch.setenv("MK_GEMM_PERSIST", "0")
     rng = np.random.default_rng(batch + M + N + K)
     a = _case(rng, (batch, M, K), 1.0 / np.sqrt(np.sqrt(K)))
     b = _case(rng, (batch, K, N), 1.0 / np.sqrt(np.sqrt(K)))
@@ -224,3 +227,54 @@ def test_gemm_bf16_nt_rejects_unaligned_shapes():
     bt = torch.zeros((256, 64), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(Exception, match="M % 256 == 0"):
         ops.gemm_bf16_nt(a, bt)
+
+
+@pytest.mark.parametrize("batch,M,N,K", [(1, 256, 256, 32), (16, 256, 512, 128), (2, 512, 768, 96),
+                                         (1, 256, 256, 256), (3, 384, 640, 64), (1, 128, 128, 160),
+                                         (16, 2048, 2048, 128), (5, 512, 256, 64), (1, 4096, 4096, 128)])
+@pytest.mark.parametrize("epilogue", [None, "add", "swiglu"])
+def test_gemm_bf16_short_k_kernels(batch, M, N, K, epilogue, monkeypatch):
+    """The two short-K kernels: the 128 x 128 one with all of K in LDS
+    (MK_GEMM_SHORTK=256, K <= 256) and the persistent 256 x 256 one (K <=
+    128, M and N multiples of 256; the default there).  Against float64 on
+    every element, bit for bit against each other and the 256 x 256 ring
+    kernel (each k in the same order in the same MFMA), and with the ADD /
+    SWIGLU epilogue bit for bit against the plain product followed by the
+    elementwise program.  The persistent grid holds one workgroup per CU, so
+    the larger shapes walk several tiles per workgroup."""
+    ops = _ops()
+    rng = np.random.default_rng(batch * 5 + M + N + K)
+    a_h = _case(rng, (batch, M, K), 1.0 / np.sqrt(np.sqrt(K)))
+    b_h = _case(rng, (batch, K, N), 1.0 / np.sqrt(np.sqrt(K)))
+    a, b = dev_bf16(a_h), dev_bf16(b_h)
+    aux = dev_bf16(_case(rng, (batch, M, N), 1.0)) if epilogue else None
+    print(f"gemm short-k case b={batch} M={M} N={N} K={K} epilogue={epilogue}", flush=True)
+
+    def run(shortk, persist, tile="0"):
+        monkeypatch.setenv("MK_GEMM_SHORTK", shortk)
+        monkeypatch.setenv("MK_GEMM_PERSIST", persist)
+        monkeypatch.setenv("MK_GEMM_TILE", tile)
+        out = ops.gemm_bf16(a, b, epilogue=epilogue, aux=aux)
+        torch.cuda.synchronize()
+        return out
+
+    c = run("256", "0")
+    if epilogue is None:
+        if batch * M * N * K <= 2 ** 30:
+            ref, _ = gemm.matmul_bf16(a_h, b_h)
+            assert_rel_close(c.float().cpu().numpy().reshape(ref.shape), ref, BF16_RTOL, f"short-k {batch}x{M}x{N}x{K}")
+    else:
+        plain = ops.gemm_bf16(a, b)
+        prog = ([("LOAD", 0, 0, 0, 0, 0.0), ("LOAD", 1, 1, 0, 0, 0.0), ("ADD", 2, 0, 1, 0, 0.0)]
+                if epilogue == "add" else
+                [("LOAD", 0, 0, 0, 0, 0.0), ("LOAD", 1, 1, 0, 0, 0.0), ("LOGISTIC", 2, 1, 0, 0, 0.0),
+                 ("MUL", 3, 1, 2, 0, 0.0), ("MUL", 4, 3, 0, 0, 0.0)])
+        want = ops.elementwise(prog, [plain, aux], out_slot=2 if epilogue == "add" else 4)
+        torch.cuda.synchronize()
+        assert torch.equal(c.view(torch.int16), want.view(torch.int16)), f"short-k {epilogue} epilogue"
+    if M % 256 == 0 and N % 256 == 0:
+        ring = run("0", "0", "256")
+        assert torch.equal(c.view(torch.int16), ring.view(torch.int16)), "short-k and ring kernels differ"
+        if K <= 128:
+            pers = run("0", "1")
+            assert torch.equal(pers.view(torch.int16), ring.view(torch.int16)), "persistent and ring kernels differ"
