@@ -195,6 +195,71 @@ int mk_gemm_bf16_epilogue(const void* a, const void* b, void* c, const void* aux
 int mk_gemm_bf16_nt(const void* a, const void* bt, void* c, const void* aux, int epilogue, int64_t batch,
                     int64_t M, int64_t N, int64_t K, void* stream);
 
+/* Routes of the bf16 product (B [K, N]): the kernels mk_gemm_bf16 and
+ * mk_gemm_bf16_epilogue choose between by shape.  Every route computes
+ * each output's k in the same order in the same MFMA, so all give the same
+ * bits; they differ only in speed.
+ *   RING        256 x 256 tiles, 4-stage LDS DMA ring   (M, N % 256, K % 32)
+ *   PIPE        the same with fragment prefetch, 5 stages (and K >= 320)
+ *   PERSIST     256 x 256, one workgroup per CU over the tiles
+ *               (K <= 128, bf16 output, no paired epilogue)
+ *   SHORT       128 x 128 with all of K in LDS (M, N % 128, K % 32,
+ *               K <= 256, bf16 output, no paired epilogue)
+ *   REG256      256 x 256, register-staged operands (M, N % 256, K % 64)
+ *   GENERIC256, GENERIC128  any shape (no paired epilogue)
+ * The reference picks between its GEMM variants the same way, by timing
+ * them at the first plan build and keeping the fastest per device and
+ * shape (AutotuneGemm, src/pjrt_plugin/core/mps_executable.mm:3433-3725;
+ * its persistent cache :3270-3420). */
+enum {
+  MK_GEMM_ROUTE_DEFAULT = 0,
+  MK_GEMM_ROUTE_RING = 1,
+  MK_GEMM_ROUTE_PIPE = 2,
+  MK_GEMM_ROUTE_PERSIST = 3,
+  MK_GEMM_ROUTE_SHORT = 4,
+  MK_GEMM_ROUTE_REG256 = 5,
+  MK_GEMM_ROUTE_GENERIC256 = 6,
+  MK_GEMM_ROUTE_GENERIC128 = 7,
+  MK_GEMM_ROUTE_COUNT = 8
+};
+
+/* mk_gemm_bf16_epilogue (epilogue MK_EPI_NONE: mk_gemm_bf16, with
+ * out_f32) on a given route; MK_GEMM_ROUTE_DEFAULT is the built-in choice.
+ * A route that does not take the product is MK_EUNSUPPORTED. */
+int mk_gemm_bf16_route(const void* a, const void* b, void* c, const void* aux, int epilogue, int64_t batch,
+                       int64_t M, int64_t N, int64_t K, int out_f32, int route, void* stream);
+
+/* 1 when the route takes the product, else 0.  Host-only. */
+int mk_gemm_bf16_route_fits(int route, int64_t M, int64_t N, int64_t K, int epilogue, int out_f32);
+
+/* Times every route that takes the product on `stream` (warm-up and timed
+ * launches: MK_GEMM_AUTOTUNE_WARMUP, default 2, and MK_GEMM_AUTOTUNE_ITERS,
+ * default 5, HIP events, the median per route), records the fastest in
+ * the process's route table for the current device (architecture and CU
+ * count), shape, epilogue class and output type, and returns it in *route
+ * (and its median in *us); it creates and destroys two HIP events, and
+ * allocates no device memory.  c holds the product afterwards.  Not under
+ * stream capture, and aux may not be c (MK_EINVAL: every timed launch
+ * rewrites c). */
+int mk_gemm_bf16_autotune(const void* a, const void* b, void* c, const void* aux, int epilogue, int64_t batch,
+                          int64_t M, int64_t N, int64_t K, int out_f32, void* stream, int* route, float* us);
+
+/* The route table's entry for the product on the current device, or
+ * MK_GEMM_ROUTE_DEFAULT when it has none. */
+int mk_gemm_tuned_route(int64_t batch, int64_t M, int64_t N, int64_t K, int epilogue, int out_f32);
+
+/* The route table as a text file: a header line "mk-gemm-autotune 1",
+ * then one line per entry, "<arch> <CUs> <batch> <M> <N> <K>
+ * <epilogue class> <out_f32> <route> <us>".  save writes it atomically
+ * (a temporary file renamed) and returns the number of entries; load
+ * merges a file's entries into the table and returns their number.  Both
+ * return -MK_EINVAL on failure (load: a missing file, another header or a
+ * malformed line, the table unchanged).  clear empties the table.
+ * Host-only. */
+int mk_gemm_autotune_save(const char* path);
+int mk_gemm_autotune_load(const char* path);
+void mk_gemm_autotune_clear(void);
+
 /* mk_dot_general: the dot_general cases the tiled GEMMs do not take,
  * with the reference's semantics (HandleDotGeneral,
  * src/pjrt_plugin/ops/binary_ops.mm:644-1100):

@@ -1158,8 +1158,15 @@ __global__ __launch_bounds__(512) void gemm_bf16_persist_kernel(GemmArgs p, int 
 // ---------------------------------------------------------------------------
 #include "../capi_internal.h"
 
+#include <unistd.h>
+
 #include <algorithm>
 #include <atomic>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
 
 namespace {
 
@@ -1218,6 +1225,11 @@ int device_cus() {
   return v;
 }
 
+int env_int_gemm(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return v ? atoi(v) : dflt;
+}
+
 int env_tile() {
   const char* v = getenv("MK_GEMM_TILE");
   return v ? atoi(v) : 0;
@@ -1228,8 +1240,162 @@ int env_tile() {
 namespace {
 
 // bt: b is B^T [N, K] (only the DMA-fed 256 x 256 kernel takes it).
+// Routes: the kernel choices of the [K, N] bf16 product (MK_GEMM_ROUTE_*).
+// Every route computes each output's k in the same order in the same MFMA,
+// so all of them give the same bits; they differ only in speed.
+bool route_fits(int route, int64_t M, int64_t N, int64_t K, int epi, int out_f32) {
+  const bool a256 = M % 256 == 0 && N % 256 == 0;
+  const bool simple_epi = epi == MK_EPI_NONE || epi == MK_EPI_ADD || epi == MK_EPI_SWIGLU;
+  switch (route) {
+    case MK_GEMM_ROUTE_RING:
+      return a256 && K % 32 == 0;
+    case MK_GEMM_ROUTE_PIPE:
+      return a256 && K % 32 == 0 && K >= 2 * 32 * mk::kPipeStages;
+    case MK_GEMM_ROUTE_PERSIST:
+      return a256 && K % 32 == 0 && K <= 128 && !out_f32 && simple_epi;
+    case MK_GEMM_ROUTE_SHORT:
+      return M % 128 == 0 && N % 128 == 0 && K % 32 == 0 && K <= 256 && !out_f32 && simple_epi;
+    case MK_GEMM_ROUTE_REG256:
+      return a256 && K % 64 == 0 && simple_epi;
+    case MK_GEMM_ROUTE_GENERIC256:
+    case MK_GEMM_ROUTE_GENERIC128:
+      return simple_epi;
+    default:
+      return false;
+  }
+}
+
+// The built-in choice (what MK_GEMM_* environment knobs steer).
+int default_route(int64_t batch, int64_t M, int64_t N, int64_t K, int epi, int out_f32) {
+  const char* dma_env = getenv("MK_GEMM_DMA");
+  const bool dma = !(dma_env && dma_env[0] == '0');
+  const bool simple_epi = epi == MK_EPI_NONE || epi == MK_EPI_ADD || epi == MK_EPI_SWIGLU;
+  const int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256) * batch;
+  int tile = env_tile();
+  if (tile == 0) tile = big_tiles >= 128 ? 256 : 128;
+  if (epi == MK_EPI_SWIGLU_PAIRS) tile = 256;
+  // K <= 128 on 256 x 256 tiles: the persistent kernel (one workgroup per
+  // CU, the next tile's loads under the current tile's stores): 16 x 2048^2
+  // x 128 50.1 against 54 us for the ring kernel, x 64 32.7 against 42 us,
+  // 8192^2 x 128 41.9 against 56 us.  MK_GEMM_PERSIST=0 turns it off.
+  const char* pe = getenv("MK_GEMM_PERSIST");
+  if (!(pe && pe[0] == '0') && dma && route_fits(MK_GEMM_ROUTE_PERSIST, M, N, K, epi, out_f32))
+    return MK_GEMM_ROUTE_PERSIST;
+  // Short K on 128-multiples that are not 256-multiples: the 128 x 128
+  // kernel with all of K in LDS (two workgroups per CU at K <= 128), faster
+  // there than the generic 128 x 128 kernel (16 x 2048^2 x 128: 59 against
+  // 73 us).  MK_GEMM_SHORTK sets the largest K it takes (0: never, up to
+  // 256; with 256-multiples it is taken only when the persistent kernel
+  // is off).
+  const char* sk = getenv("MK_GEMM_SHORTK");
+  const int64_t shortk_max = std::min<int64_t>(sk ? atoll(sk) : 128, 256);
+  if (K <= shortk_max && route_fits(MK_GEMM_ROUTE_SHORT, M, N, K, epi, out_f32)) return MK_GEMM_ROUTE_SHORT;
+  if (tile == 256 && dma && M % 256 == 0 && N % 256 == 0 && K % 32 == 0) {
+    // The pipelined kernel (fragment prefetch + 5-stage ring) for K loops
+    // of 2048 and more, every epilogue included (it has no registers left
+    // to preload an ADD / SWIGLU operand, so it reads it at the store).
+    // Alone it is 3-5 % faster at K = 2048 and 7-9 % from K = 4096.  It runs
+    // at a lower clock (GRBM_GUI_ACTIVE per ns ~2.1 against ~2.35 GHz),
+    // which slows the kernels around it; in the decoder it still gains end
+    // to end: QKV and paired gate/up 2 % (5.00 vs 5.09 ms), then the output
+    // and down projections with their residual-add epilogue another 2.5 %
+    // (4.82 vs 4.95 ms).  MK_GEMM_PIPE_K moves the threshold.
+    const char* pv = getenv("MK_GEMM_PIPE");
+    const char* pk = getenv("MK_GEMM_PIPE_K");
+    const int64_t pipe_k = pk ? atoll(pk) : 2048;
+    const bool pipe = !(pv && atoi(pv) == 0) && K >= pipe_k;
+    return pipe && route_fits(MK_GEMM_ROUTE_PIPE, M, N, K, epi, out_f32) ? MK_GEMM_ROUTE_PIPE : MK_GEMM_ROUTE_RING;
+  }
+  if (!simple_epi) return MK_GEMM_ROUTE_RING;  // paired SwiGLU: checked aligned by the caller
+  if (tile == 256 && route_fits(MK_GEMM_ROUTE_REG256, M, N, K, epi, out_f32)) return MK_GEMM_ROUTE_REG256;
+  return tile == 256 ? MK_GEMM_ROUTE_GENERIC256 : MK_GEMM_ROUTE_GENERIC128;
+}
+
+hipError_t launch_route(int route, const mk::GemmArgs& p, int64_t batch, hipStream_t st) {
+  hipError_t e = hipErrorInvalidValue;
+  const int64_t M = p.M, N = p.N, K = p.K;
+  const char* w = getenv("MK_GEMM_WAVES");
+  const bool four_waves = w && atoi(w) == 4;
+  switch (route) {
+    case MK_GEMM_ROUTE_PERSIST: {
+      const int64_t total = (M / 256) * (N / 256) * batch;
+      const dim3 grid((unsigned)std::min<int64_t>(total, device_cus()));
+      switch (K / 32) {
+#define MK_PERSIST_CASE(KT)                                                                              \
+  case KT:                                                                                               \
+    e = lds_opt_in((const void*)mk::gemm_bf16_persist_kernel<KT>, (size_t)mk::persist_lds_bytes(KT));   \
+    if (e == hipSuccess)                                                                                 \
+      hipLaunchKernelGGL((mk::gemm_bf16_persist_kernel<KT>), grid, dim3(512), mk::persist_lds_bytes(KT), st, p, \
+                         (int)batch);                                                                    \
+    break;
+        MK_PERSIST_CASE(1) MK_PERSIST_CASE(2) MK_PERSIST_CASE(3) MK_PERSIST_CASE(4)
+#undef MK_PERSIST_CASE
+        default: break;
+      }
+      break;
+    }
+    case MK_GEMM_ROUTE_SHORT: {
+      const dim3 grid((unsigned)((M / 128) * (N / 128)), 1, (unsigned)batch);
+      switch (K / 32) {
+#define MK_SHORTK_CASE(KT)                                                                           \
+  case KT:                                                                                           \
+    e = lds_opt_in((const void*)mk::gemm_bf16_shortk_kernel<KT>, (size_t)mk::short_lds_bytes(KT));  \
+    if (e == hipSuccess)                                                                             \
+      hipLaunchKernelGGL((mk::gemm_bf16_shortk_kernel<KT>), grid, dim3(256), mk::short_lds_bytes(KT), st, p); \
+    break;
+        MK_SHORTK_CASE(1) MK_SHORTK_CASE(2) MK_SHORTK_CASE(3) MK_SHORTK_CASE(4)
+        MK_SHORTK_CASE(5) MK_SHORTK_CASE(6) MK_SHORTK_CASE(7) MK_SHORTK_CASE(8)
+#undef MK_SHORTK_CASE
+        default: break;
+      }
+      break;
+    }
+    case MK_GEMM_ROUTE_RING:
+    case MK_GEMM_ROUTE_PIPE: {
+      constexpr size_t lds = (size_t)mk::kGemmStages * mk::kGemmStageBytes;
+      const dim3 grid((unsigned)((M / 256) * (N / 256)), 1, (unsigned)batch);
+      if (four_waves) {
+        e = lds_opt_in((const void*)mk::gemm_bf16_256dma_kernel<2, false>, lds);
+        if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256dma_kernel<2, false>), grid, dim3(256), lds, st, p);
+      } else if (route == MK_GEMM_ROUTE_PIPE) {
+        constexpr size_t lds_p = (size_t)mk::kPipeStages * mk::kGemmStageBytes;
+        e = lds_opt_in((const void*)mk::gemm_bf16_256dma_kernel<4, true>, lds_p);
+        if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256dma_kernel<4, true>), grid, dim3(512), lds_p, st, p);
+      } else {
+        // The ring takes 128 KB; the staged epilogue tile needs 136 KB (one
+        // workgroup per CU either way).
+        constexpr size_t lds4 = lds > (size_t)mk::kEpiStageBytes ? lds : (size_t)mk::kEpiStageBytes;
+        e = lds_opt_in((const void*)mk::gemm_bf16_256dma_kernel<4, false>, lds4);
+        if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256dma_kernel<4, false>), grid, dim3(512), lds4, st, p);
+      }
+      break;
+    }
+    case MK_GEMM_ROUTE_REG256: {
+      constexpr size_t lds = (size_t)2 * (256 * 64 + 64 * 256) * 2;
+      const dim3 grid((unsigned)((M / 256) * (N / 256)), 1, (unsigned)batch);
+      if (four_waves) {
+        e = lds_opt_in((const void*)mk::gemm_bf16_256_kernel<2, 2>, lds);
+        if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256_kernel<2, 2>), grid, dim3(256), lds, st, p);
+      } else {
+        e = lds_opt_in((const void*)mk::gemm_bf16_256_kernel<2, 4>, lds);
+        if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256_kernel<2, 4>), grid, dim3(512), lds, st, p);
+      }
+      break;
+    }
+    case MK_GEMM_ROUTE_GENERIC256:
+      return launch_bf16<256, 256, 2, 2>(p, (int)batch, st);
+    case MK_GEMM_ROUTE_GENERIC128:
+      return launch_bf16<128, 128, 2, 2>(p, (int)batch, st);
+    default:
+      return hipErrorInvalidValue;
+  }
+  if (e == hipSuccess) e = hipGetLastError();
+  return e;
+}
+
 int run_gemm_bf16(const char* fn, const void* a, const void* b, void* c, const void* aux, int epi, int64_t batch,
-                  int64_t M, int64_t N, int64_t K, int out_f32, void* stream, bool bt = false) {
+                  int64_t M, int64_t N, int64_t K, int out_f32, void* stream, bool bt = false,
+                  int route = MK_GEMM_ROUTE_DEFAULT) {
   mkc::clear_error();
   int rc = check_gemm(fn, a, b, c, batch, M, N, K);
   if (rc != MK_OK) return rc;
@@ -1253,62 +1419,8 @@ int run_gemm_bf16(const char* fn, const void* a, const void* b, void* c, const v
   p.epi = epi;
   p.aux = static_cast<const uint16_t*>(aux);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256) * batch;
-  int tile = env_tile();
-  if (tile == 0) tile = big_tiles >= 128 ? 256 : 128;
-  if (epi == MK_EPI_SWIGLU_PAIRS) tile = 256;
   hipError_t e;
-  // Short K on 128-multiples that are not 256-multiples: the 128 x 128
-  // kernel with all of K in LDS (two workgroups per CU at K <= 128), faster
-  // there than the generic 128 x 128 kernel (16 x 2048^2 x 128: 59 against
-  // 73 us).  MK_GEMM_SHORTK sets the largest K it takes (0: never, up to
-  // 256; with 256-multiples it is taken only when the persistent kernel
-  // below is off).
-  const char* sk = getenv("MK_GEMM_SHORTK");
-  const int64_t shortk_max = std::min<int64_t>(sk ? atoll(sk) : 128, 256);
-  const bool shortk = !bt && !out_f32 && (epi == MK_EPI_NONE || epi == MK_EPI_ADD || epi == MK_EPI_SWIGLU) &&
-                      M % 128 == 0 && N % 128 == 0 && K % 32 == 0 && K <= shortk_max;
-  // K <= 128 on 256 x 256 tiles: the persistent kernel (one workgroup per
-  // CU, the next tile's loads under the current tile's stores): 16 x 2048^2
-  // x 128 50.1 against 54 us for the ring kernel, x 64 32.7 against 42 us,
-  // 8192^2 x 128 41.9 against 56 us.  MK_GEMM_PERSIST=0 turns it off.
-  const char* pe = getenv("MK_GEMM_PERSIST");
-  const bool persist = !(pe && pe[0] == '0') && dma && !bt && !out_f32 &&
-                       (epi == MK_EPI_NONE || epi == MK_EPI_ADD || epi == MK_EPI_SWIGLU) && M % 256 == 0 &&
-                       N % 256 == 0 && K % 32 == 0 && K <= 128;
-  if (persist) {
-    const int64_t total = (M / 256) * (N / 256) * batch;
-    const int cus = device_cus();
-    const dim3 grid((unsigned)std::min<int64_t>(total, cus));
-    switch (K / 32) {
-#define MK_PERSIST_CASE(KT)                                                                              \
-  case KT:                                                                                               \
-    e = lds_opt_in((const void*)mk::gemm_bf16_persist_kernel<KT>, (size_t)mk::persist_lds_bytes(KT));   \
-    if (e == hipSuccess)                                                                                 \
-      hipLaunchKernelGGL((mk::gemm_bf16_persist_kernel<KT>), grid, dim3(512), mk::persist_lds_bytes(KT), st, p, \
-                         (int)batch);                                                                    \
-    break;
-      MK_PERSIST_CASE(1) MK_PERSIST_CASE(2) MK_PERSIST_CASE(3) MK_PERSIST_CASE(4)
-#undef MK_PERSIST_CASE
-      default: e = hipErrorInvalidValue;
-    }
-    if (e == hipSuccess) e = hipGetLastError();
-  } else if (shortk) {
-    const dim3 grid((unsigned)((M / 128) * (N / 128)), 1, (unsigned)batch);
-    switch (K / 32) {
-#define MK_SHORTK_CASE(KT)                                                                           \
-  case KT:                                                                                           \
-    e = lds_opt_in((const void*)mk::gemm_bf16_shortk_kernel<KT>, (size_t)mk::short_lds_bytes(KT));  \
-    if (e == hipSuccess)                                                                             \
-      hipLaunchKernelGGL((mk::gemm_bf16_shortk_kernel<KT>), grid, dim3(256), mk::short_lds_bytes(KT), st, p); \
-    break;
-      MK_SHORTK_CASE(1) MK_SHORTK_CASE(2) MK_SHORTK_CASE(3) MK_SHORTK_CASE(4)
-      MK_SHORTK_CASE(5) MK_SHORTK_CASE(6) MK_SHORTK_CASE(7) MK_SHORTK_CASE(8)
-#undef MK_SHORTK_CASE
-      default: e = hipErrorInvalidValue;
-    }
-    if (e == hipSuccess) e = hipGetLastError();
-  } else if (bt) {
+  if (bt) {
     const dim3 grid((unsigned)((M / 256) * (N / 256)), 1, (unsigned)batch);
     const char* pv = getenv("MK_GEMM_PIPE");
     const char* pk = getenv("MK_GEMM_PIPE_K");
@@ -1326,54 +1438,13 @@ int run_gemm_bf16(const char* fn, const void* a, const void* b, void* c, const v
         hipLaunchKernelGGL((mk::gemm_bf16_256dma_kernel<4, false, true>), grid, dim3(512), lds4, st, p);
     }
     if (e == hipSuccess) e = hipGetLastError();
-  } else if (tile == 256 && dma && M % 256 == 0 && N % 256 == 0 && K % 32 == 0) {
-    constexpr size_t lds = (size_t)mk::kGemmStages * mk::kGemmStageBytes;
-    const dim3 grid((unsigned)((M / 256) * (N / 256)), 1, (unsigned)batch);
-    const char* w = getenv("MK_GEMM_WAVES");
-    const char* pv = getenv("MK_GEMM_PIPE");
-    // The pipelined kernel (fragment prefetch + 5-stage ring) for K loops
-    // of 2048 and more, every epilogue included (it has no registers left
-    // to preload an ADD / SWIGLU operand, so it reads it at the store).
-    // Alone it is 3-5 % faster at K = 2048 and 7-9 % from K = 4096.  It runs
-    // at a lower clock (GRBM_GUI_ACTIVE per ns ~2.1 against ~2.35 GHz),
-    // which slows the kernels around it; in the decoder it still gains end
-    // to end: QKV and paired gate/up 2 % (5.00 vs 5.09 ms), then the output
-    // and down projections with their residual-add epilogue another 2.5 %
-    // (4.82 vs 4.95 ms).  MK_GEMM_PIPE_K moves the threshold.
-    const char* pk = getenv("MK_GEMM_PIPE_K");
-    const int64_t pipe_k = pk ? atoll(pk) : 2048;
-    const bool pipe = !(pv && atoi(pv) == 0) && K >= pipe_k && K >= 2 * 32 * mk::kPipeStages;
-    if (w && atoi(w) == 4) {
-      e = lds_opt_in((const void*)mk::gemm_bf16_256dma_kernel<2, false>, lds);
-      if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256dma_kernel<2, false>), grid, dim3(256), lds, st, p);
-    } else if (pipe) {
-      constexpr size_t lds_p = (size_t)mk::kPipeStages * mk::kGemmStageBytes;
-      e = lds_opt_in((const void*)mk::gemm_bf16_256dma_kernel<4, true>, lds_p);
-      if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256dma_kernel<4, true>), grid, dim3(512), lds_p, st, p);
-    } else {
-      // The ring takes 128 KB; the staged epilogue tile needs 136 KB (one
-      // workgroup per CU either way).
-      constexpr size_t lds4 = lds > (size_t)mk::kEpiStageBytes ? lds : (size_t)mk::kEpiStageBytes;
-      e = lds_opt_in((const void*)mk::gemm_bf16_256dma_kernel<4, false>, lds4);
-      if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256dma_kernel<4, false>), grid, dim3(512), lds4, st, p);
-    }
-    if (e == hipSuccess) e = hipGetLastError();
-  } else if (tile == 256 && M % 256 == 0 && N % 256 == 0 && K % 64 == 0) {
-    constexpr size_t lds = (size_t)2 * (256 * 64 + 64 * 256) * 2;
-    const dim3 grid((unsigned)((M / 256) * (N / 256)), 1, (unsigned)batch);
-    const char* w = getenv("MK_GEMM_WAVES");
-    if (w && atoi(w) == 4) {
-      e = lds_opt_in((const void*)mk::gemm_bf16_256_kernel<2, 2>, lds);
-      if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256_kernel<2, 2>), grid, dim3(256), lds, st, p);
-    } else {
-      e = lds_opt_in((const void*)mk::gemm_bf16_256_kernel<2, 4>, lds);
-      if (e == hipSuccess) hipLaunchKernelGGL((mk::gemm_bf16_256_kernel<2, 4>), grid, dim3(512), lds, st, p);
-    }
-    if (e == hipSuccess) e = hipGetLastError();
-  } else if (tile == 256) {
-    e = launch_bf16<256, 256, 2, 2>(p, (int)batch, st);
   } else {
-    e = launch_bf16<128, 128, 2, 2>(p, (int)batch, st);
+    if (route == MK_GEMM_ROUTE_DEFAULT) route = default_route(batch, M, N, K, epi, out_f32);
+    else if (!route_fits(route, M, N, K, epi, out_f32))
+      return mkc::fail(MK_EUNSUPPORTED, "%s: route %d does not take this product (M=%lld, N=%lld, K=%lld, "
+                       "epilogue %d, f32 output %d)", fn, route, (long long)M, (long long)N, (long long)K, epi,
+                       out_f32);
+    e = launch_route(route, p, batch, st);
   }
   if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
   return MK_OK;
@@ -1396,6 +1467,202 @@ extern "C" int mk_gemm_bf16_nt(const void* a, const void* bt, void* c, const voi
   return run_gemm_bf16("mk_gemm_bf16_nt", a, bt, c, aux, epilogue, batch, M, N, K, 0, stream, true);
 }
 
+
+extern "C" int mk_gemm_bf16_route(const void* a, const void* b, void* c, const void* aux, int epilogue,
+                                  int64_t batch, int64_t M, int64_t N, int64_t K, int out_f32, int route,
+                                  void* stream) {
+  if (route < MK_GEMM_ROUTE_DEFAULT || route >= MK_GEMM_ROUTE_COUNT)
+    return mkc::fail(MK_EINVAL, "mk_gemm_bf16_route: unknown route %d", route);
+  return run_gemm_bf16("mk_gemm_bf16_route", a, b, c, aux, epilogue, batch, M, N, K, out_f32, stream, false, route);
+}
+
+extern "C" int mk_gemm_bf16_route_fits(int route, int64_t M, int64_t N, int64_t K, int epilogue, int out_f32) {
+  return route_fits(route, M, N, K, epilogue, out_f32) ? 1 : 0;
+}
+
+// ---------------------------------------------------------------------------
+// Measured route choice.  A product is keyed by the device (architecture
+// name and CU count) and its shape, epilogue class and output type; the
+// table holds the fastest route measured for it and that time.
+// ---------------------------------------------------------------------------
+namespace {
+
+struct TuneEntry {
+  int route;
+  float us;
+};
+std::mutex g_tune_mu;
+std::map<std::string, TuneEntry> g_tune;
+
+// "gfx950 256" of the current device, cached per device.
+std::string device_tag() {
+  static std::mutex mu;
+  static std::map<int, std::string> tags;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return "none 0";
+  std::lock_guard<std::mutex> g(mu);
+  auto it = tags.find(dev);
+  if (it != tags.end()) return it->second;
+  hipDeviceProp_t prop;
+  std::string tag = "none 0";
+  if (hipGetDeviceProperties(&prop, dev) == hipSuccess) {
+    std::string arch = prop.gcnArchName;
+    arch = arch.substr(0, arch.find(':'));
+    tag = arch + " " + std::to_string(prop.multiProcessorCount);
+  }
+  tags[dev] = tag;
+  return tag;
+}
+
+// ADD and SWIGLU cost the same (one aux read per output); the paired form
+// writes half the output.
+int epi_class(int epi) { return epi == MK_EPI_NONE ? 0 : epi == MK_EPI_SWIGLU_PAIRS ? 2 : 1; }
+
+std::string tune_key(const std::string& tag, int64_t batch, int64_t M, int64_t N, int64_t K, int ecls, int out_f32) {
+  char buf[160];
+  snprintf(buf, sizeof buf, "%s %lld %lld %lld %lld %d %d", tag.c_str(), (long long)batch, (long long)M,
+           (long long)N, (long long)K, ecls, out_f32 ? 1 : 0);
+  return buf;
+}
+
+constexpr const char* kTuneHeader = "mk-gemm-autotune 1";
+
+}  // namespace
+
+extern "C" int mk_gemm_bf16_autotune(const void* a, const void* b, void* c, const void* aux, int epilogue,
+                                     int64_t batch, int64_t M, int64_t N, int64_t K, int out_f32, void* stream,
+                                     int* route_out, float* us_out) {
+  const char* fn = "mk_gemm_bf16_autotune";
+  mkc::clear_error();
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+    return mkc::fail(MK_EINVAL, "%s: cannot time launches under stream capture", fn);
+  const int warm = std::max(0, env_int_gemm("MK_GEMM_AUTOTUNE_WARMUP", 2));
+  const int iters = std::max(1, env_int_gemm("MK_GEMM_AUTOTUNE_ITERS", 5));
+  if (aux && aux == c)
+    return mkc::fail(MK_EINVAL, "%s: aux may not be c here (every timed launch rewrites c)", fn);
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  if (hipEventCreate(&ev[0]) != hipSuccess || hipEventCreate(&ev[1]) != hipSuccess) {
+    if (ev[0]) (void)hipEventDestroy(ev[0]);
+    return mkc::fail(MK_ELAUNCH, "%s: event creation failed", fn);
+  }
+  int best = MK_GEMM_ROUTE_DEFAULT;
+  float best_us = 0.f;
+  int rc = MK_OK;
+  for (int r = 1; r < MK_GEMM_ROUTE_COUNT && rc == MK_OK; ++r) {
+    if (!route_fits(r, M, N, K, epilogue, out_f32)) continue;
+    std::vector<float> t;
+    for (int i = 0; i < warm + iters && rc == MK_OK; ++i) {
+      if (i >= warm && hipEventRecord(ev[0], st) != hipSuccess) rc = mkc::fail(MK_ELAUNCH, "%s: event record", fn);
+      if (rc == MK_OK) rc = run_gemm_bf16(fn, a, b, c, aux, epilogue, batch, M, N, K, out_f32, stream, false, r);
+      if (rc == MK_OK && i >= warm) {
+        float ms = 0.f;
+        if (hipEventRecord(ev[1], st) != hipSuccess || hipEventSynchronize(ev[1]) != hipSuccess ||
+            hipEventElapsedTime(&ms, ev[0], ev[1]) != hipSuccess)
+          rc = mkc::fail(MK_ELAUNCH, "%s: event timing failed", fn);
+        t.push_back(ms * 1e3f);
+      }
+    }
+    if (rc != MK_OK) break;
+    std::sort(t.begin(), t.end());
+    const float med = t[t.size() / 2];
+    if (best == MK_GEMM_ROUTE_DEFAULT || med < best_us) {
+      best = r;
+      best_us = med;
+    }
+  }
+  (void)hipEventDestroy(ev[0]);
+  (void)hipEventDestroy(ev[1]);
+  if (rc != MK_OK) return rc;
+  if (best == MK_GEMM_ROUTE_DEFAULT)
+    return mkc::fail(MK_EUNSUPPORTED, "%s: no route takes this product", fn);
+  // Leave c holding the chosen route's result (every route gives the same
+  // bits; this keeps the contract independent of that).
+  rc = run_gemm_bf16(fn, a, b, c, aux, epilogue, batch, M, N, K, out_f32, stream, false, best);
+  if (rc != MK_OK) return rc;
+  {
+    std::lock_guard<std::mutex> g(g_tune_mu);
+    g_tune[tune_key(device_tag(), batch, M, N, K, epi_class(epilogue), out_f32)] = TuneEntry{best, best_us};
+  }
+  if (route_out) *route_out = best;
+  if (us_out) *us_out = best_us;
+  return MK_OK;
+}
+
+extern "C" int mk_gemm_tuned_route(int64_t batch, int64_t M, int64_t N, int64_t K, int epilogue, int out_f32) {
+  const std::string key = tune_key(device_tag(), batch, M, N, K, epi_class(epilogue), out_f32);
+  std::lock_guard<std::mutex> g(g_tune_mu);
+  auto it = g_tune.find(key);
+  return it == g_tune.end() ? MK_GEMM_ROUTE_DEFAULT : it->second.route;
+}
+
+extern "C" int mk_gemm_autotune_save(const char* path) {
+  mkc::clear_error();
+  if (!path) return -mkc::fail(MK_EINVAL, "mk_gemm_autotune_save: null path");
+  const std::string tmp = std::string(path) + ".tmp" + std::to_string((long long)getpid());
+  FILE* f = fopen(tmp.c_str(), "w");
+  if (!f) return -mkc::fail(MK_EINVAL, "mk_gemm_autotune_save: cannot write %s", tmp.c_str());
+  int n = 0;
+  {
+    std::lock_guard<std::mutex> g(g_tune_mu);
+    fprintf(f, "%s\n", kTuneHeader);
+    for (const auto& [k, v] : g_tune) {
+      fprintf(f, "%s %d %.3f\n", k.c_str(), v.route, v.us);
+      ++n;
+    }
+  }
+  const bool ok = fflush(f) == 0 && fclose(f) == 0;
+  if (!ok || rename(tmp.c_str(), path) != 0) {
+    remove(tmp.c_str());
+    return -mkc::fail(MK_EINVAL, "mk_gemm_autotune_save: cannot write %s", path);
+  }
+  return n;
+}
+
+// Merges the entries of a file written by mk_gemm_autotune_save (entries of
+// other devices included; they are only looked up on such a device).
+// Returns the number read, or -MK_EINVAL for a missing or malformed file.
+extern "C" int mk_gemm_autotune_load(const char* path) {
+  mkc::clear_error();
+  if (!path) return -mkc::fail(MK_EINVAL, "mk_gemm_autotune_load: null path");
+  FILE* f = fopen(path, "r");
+  if (!f) return -mkc::fail(MK_EINVAL, "mk_gemm_autotune_load: cannot read %s", path);
+  char line[256];
+  if (!fgets(line, sizeof line, f) || strncmp(line, kTuneHeader, strlen(kTuneHeader)) != 0 ||
+      (line[strlen(kTuneHeader)] != '\n' && line[strlen(kTuneHeader)] != '\0')) {
+    fclose(f);
+    return -mkc::fail(MK_EINVAL, "mk_gemm_autotune_load: %s is not a route table (header \"%s\")", path, kTuneHeader);
+  }
+  std::vector<std::pair<std::string, TuneEntry>> got;
+  int lineno = 1;
+  while (fgets(line, sizeof line, f)) {
+    ++lineno;
+    char arch[64];
+    int cus = 0, ecls = 0, of = 0, route = 0;
+    long long b = 0, m = 0, n = 0, k = 0;
+    float us = 0.f;
+    char extra = 0;
+    if (line[0] == '\n') continue;
+    if (sscanf(line, "%63s %d %lld %lld %lld %lld %d %d %d %f %c", arch, &cus, &b, &m, &n, &k, &ecls, &of, &route,
+               &us, &extra) != 10 || cus <= 0 || b <= 0 || m <= 0 || n <= 0 || k <= 0 || ecls < 0 || ecls > 2 ||
+        (of != 0 && of != 1) || route <= MK_GEMM_ROUTE_DEFAULT || route >= MK_GEMM_ROUTE_COUNT || !(us >= 0.f)) {
+      fclose(f);
+      return -mkc::fail(MK_EINVAL, "mk_gemm_autotune_load: %s line %d is malformed", path, lineno);
+    }
+    got.emplace_back(tune_key(std::string(arch) + " " + std::to_string(cus), b, m, n, k, ecls, of),
+                     TuneEntry{route, us});
+  }
+  fclose(f);
+  std::lock_guard<std::mutex> g(g_tune_mu);
+  for (auto& [key, v] : got) g_tune[key] = v;
+  return (int)got.size();
+}
+
+extern "C" void mk_gemm_autotune_clear(void) {
+  std::lock_guard<std::mutex> g(g_tune_mu);
+  g_tune.clear();
+}
 
 extern "C" int mk_gemm_f32(const void* a, const void* b, void* c, int64_t batch, int64_t M,
                            int64_t N, int64_t K, void* stream) {

@@ -58,6 +58,7 @@ struct Step {
   int64_t batch = 1, M = 0, N = 0, K = 0;
   int out_f32 = 0;
   int b_t = 0;            // ST_GEMM_BF16: in[1] holds B^T [batch, N, K]
+  int route = 0;          // ST_GEMM_BF16: MK_GEMM_ROUTE_* chosen when the plan is prepared (0: built-in)
   int epi = MK_EPI_NONE;  // ST_QMM_*: store epilogue against in.back()
   int64_t rows = 0, cols = 0;
   float eps = 0.f;

@@ -16,6 +16,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <sys/stat.h>
 
 #include <algorithm>
 #include <atomic>
@@ -343,6 +344,89 @@ mkrt_buffer* new_buffer(mkrt_client* c, int type, const std::vector<int64_t>& di
 // First-execute preparation: constants uploaded, workspace allocated,
 // elementwise programs compiled (core/mps_executable.mm:9152 builds the
 // plan lazily under plan_mutex_, mps_executable.h:96-100).
+// GEMM routes measured at the first plan build, as the reference autotunes
+// its GEMM variants (AutotuneGemm, src/pjrt_plugin/core/mps_executable.mm:
+// 3433-3725): MK_GEMM_AUTOTUNE=0 keeps the built-in choice.  The route table
+// persists across processes in MK_AUTOTUNE_CACHE_DIR (default
+// $HOME/.cache/mi355x-mk)/gemm_routes.txt unless
+// MK_DISABLE_AUTOTUNE_CACHE_PERSIST=1 (the reference's cache,
+// :3270-3420).  Every route gives the same bits, so this only changes speed.
+bool gemm_autotune_enabled() {
+  const char* v = getenv("MK_GEMM_AUTOTUNE");
+  return !(v && v[0] == '0' && v[1] == '\0');
+}
+
+std::string gemm_route_cache_path() {
+  const char* v = getenv("MK_DISABLE_AUTOTUNE_CACHE_PERSIST");
+  if (v && v[0] == '1') return "";
+  std::string dir;
+  const char* d = getenv("MK_AUTOTUNE_CACHE_DIR");
+  if (d && d[0]) {
+    dir = d;
+  } else {
+    const char* home = getenv("HOME");
+    if (!home || !home[0]) return "";
+    dir = std::string(home) + "/.cache";
+    mkdir(dir.c_str(), 0755);
+    dir += "/mi355x-mk";
+  }
+  mkdir(dir.c_str(), 0755);
+  return dir + "/gemm_routes.txt";
+}
+
+std::mutex g_route_cache_mu;
+bool g_route_cache_loaded = false;
+
+// Fills st.route of every [K, N] bf16 GEMM step: the table's entry, or a
+// measurement on scratch operands of the step's sizes (bf16 0x3c3c, about
+// 0.0115, everywhere).  A failed measurement leaves the built-in choice.
+// Called with the client's stream lock held.
+void tune_gemm_steps(mkrt_executable* x) {
+  if (!gemm_autotune_enabled()) return;
+  mkrt_client* c = x->client;
+  const std::string path = gemm_route_cache_path();
+  {
+    std::lock_guard<std::mutex> g(g_route_cache_mu);
+    if (!g_route_cache_loaded && !path.empty()) {
+      FILE* f = fopen(path.c_str(), "r");
+      if (f) {
+        fclose(f);
+        mk_gemm_autotune_load(path.c_str());  // a malformed file is ignored
+      }
+    }
+    g_route_cache_loaded = true;
+  }
+  bool added = false;
+  for (mkrt::Step& st : x->plan.steps) {
+    if (st.kind != mkrt::ST_GEMM_BF16 || st.b_t) continue;
+    int r = mk_gemm_tuned_route(st.batch, st.M, st.N, st.K, MK_EPI_NONE, st.out_f32);
+    if (r == MK_GEMM_ROUTE_DEFAULT) {
+      const size_t ab = (size_t)(st.batch * st.M * st.K * 2), bb = (size_t)(st.batch * st.K * st.N * 2);
+      const size_t cb = (size_t)(st.batch * st.M * st.N * (st.out_f32 ? 4 : 2));
+      void *A = nullptr, *B = nullptr, *C = nullptr;
+      if (c->alloc.alloc(ab, &A) == hipSuccess && c->alloc.alloc(bb, &B) == hipSuccess &&
+          c->alloc.alloc(cb, &C) == hipSuccess && hipMemsetAsync(A, 0x3c, ab, c->stream) == hipSuccess &&
+          hipMemsetAsync(B, 0x3c, bb, c->stream) == hipSuccess) {
+        int route = 0;
+        float us = 0.f;
+        if (mk_gemm_bf16_autotune(A, B, C, nullptr, MK_EPI_NONE, st.batch, st.M, st.N, st.K, st.out_f32, c->stream,
+                                  &route, &us) == MK_OK) {
+          r = route;
+          added = true;
+        }
+      }
+      (void)hipStreamSynchronize(c->stream);
+      for (void* q : {A, B, C})
+        if (q) c->alloc.free(q);
+    }
+    st.route = r;
+  }
+  if (added && !path.empty()) {
+    std::lock_guard<std::mutex> g(g_route_cache_mu);
+    mk_gemm_autotune_save(path.c_str());  // best effort: an unwritable cache only costs a re-measurement
+  }
+}
+
 mkrt_error* prepare(mkrt_executable* x) {
   if (x->prepared.load(std::memory_order_acquire)) return nullptr;
   std::lock_guard<std::mutex> g(x->plan_mu);
@@ -375,6 +459,10 @@ mkrt_error* prepare(mkrt_executable* x) {
     if (mk_elementwise_prepare(st.dt, st.prog.data(), (int)st.prog.size(), (int)st.in.size(), st.prog_out) != MK_OK)
       return make_error(MKRT_INTERNAL, "elementwise program: %s", mk_last_error());
   }
+  {
+    std::lock_guard<std::mutex> sg(c->stream_mu);
+    tune_gemm_steps(x);
+  }
   x->prepared.store(true, std::memory_order_release);
   return nullptr;
 }
@@ -385,6 +473,9 @@ int run_step(const mkrt::Step& st, const std::vector<void*>& mem, void* ws, int6
   switch (st.kind) {
     case mkrt::ST_GEMM_BF16:
       if (st.b_t) return mk_gemm_bf16_nt(in(0), in(1), out, nullptr, MK_EPI_NONE, st.batch, st.M, st.N, st.K, s);
+      if (st.route != MK_GEMM_ROUTE_DEFAULT)
+        return mk_gemm_bf16_route(in(0), in(1), out, nullptr, MK_EPI_NONE, st.batch, st.M, st.N, st.K, st.out_f32,
+                                  st.route, s);
       return mk_gemm_bf16(in(0), in(1), out, st.batch, st.M, st.N, st.K, st.out_f32, s);
     case mkrt::ST_GEMM_F32:
       return mk_gemm_f32(in(0), in(1), out, st.batch, st.M, st.N, st.K, s);

@@ -16,6 +16,9 @@ MK_OK, MK_EINVAL, MK_EUNSUPPORTED, MK_EWORKSPACE, MK_ELAUNCH = 0, 1, 2, 3, 4
 MK_QFMT_INT4_G64, MK_QFMT_INT8_PC = 0, 1
 MK_DT_F32, MK_DT_BF16 = 0, 1
 MK_EPI_NONE, MK_EPI_ADD, MK_EPI_SWIGLU, MK_EPI_SWIGLU_PAIRS = 0, 1, 2, 3
+# bf16 GEMM routes (MK_GEMM_ROUTE_*)
+GEMM_ROUTES = {"default": 0, "ring": 1, "pipe": 2, "persist": 3, "short": 4, "reg256": 5, "generic256": 6,
+               "generic128": 7}
 MK_REDUCE_SUM, MK_REDUCE_MAX, MK_REDUCE_MIN = 0, 1, 2
 EW_OPS = ["LOAD", "CONST", "ADD", "SUB", "MUL", "DIV", "MAX", "MIN", "POW", "NEG", "ABS", "EXP", "LOG",
           "LOG1P", "EXPM1", "TANH", "RSQRT", "SQRT", "LOGISTIC", "FLOOR", "CEIL", "CMP_EQ", "CMP_NE",
@@ -48,6 +51,14 @@ SIGNATURES = {
     "mk_gemm_bf16": (_i32, [_p, _p, _p, _i64, _i64, _i64, _i64, _i32, _p]),
     "mk_gemm_bf16_epilogue": (_i32, [_p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _p]),
     "mk_gemm_bf16_nt": (_i32, [_p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _p]),
+    "mk_gemm_bf16_route": (_i32, [_p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _i32, _i32, _p]),
+    "mk_gemm_bf16_route_fits": (_i32, [_i32, _i64, _i64, _i64, _i32, _i32]),
+    "mk_gemm_bf16_autotune": (_i32, [_p, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _i32, _p,
+                                     ctypes.POINTER(_i32), ctypes.POINTER(ctypes.c_float)]),
+    "mk_gemm_tuned_route": (_i32, [_i64, _i64, _i64, _i64, _i32, _i32]),
+    "mk_gemm_autotune_save": (_i32, [ctypes.c_char_p]),
+    "mk_gemm_autotune_load": (_i32, [ctypes.c_char_p]),
+    "mk_gemm_autotune_clear": (None, []),
     "mk_int4g64_matmul_epilogue_bf16": (_i32, [_p, _p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _p, _i64, _p]),
     "mk_int8pc_matmul_epilogue_bf16": (_i32, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _p, _i64, _p]),
     "mk_qmatmul_swiglu_pair_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64]),

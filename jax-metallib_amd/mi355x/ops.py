@@ -5,6 +5,8 @@ runs in the gfx950 kernels of libmk_kernels.so.  bf16 tensors may be passed as
 torch.bfloat16 or as int16/uint16 bit patterns.
 """
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -211,6 +213,78 @@ def gemm_bf16(a, b, out_f32=False, out=None, epilogue=None, aux=None):
         check(lib().mk_gemm_bf16_epilogue(_ptr(a), _ptr(b), _ptr(c), _ptr(aux), epi, batch, M, N, K,
                                           _stream(a.device)))
     return c
+
+
+def _gemm_route_args(a, b, out_f32, out, epilogue, aux, name):
+    _require(a, _BF16, "a")
+    _require(b, _BF16, "b")
+    batch, M, N, K = _bmk(a, b)
+    shape = (M, N) if a.dim() == 2 else (batch, M, N)
+    NO = _out_cols(N, epilogue, name)
+    c = out if out is not None else torch.empty(
+        shape[:-1] + (NO,), dtype=torch.float32 if out_f32 else torch.bfloat16, device=a.device)
+    epi = _epilogue(epilogue, aux, shape, name)
+    if epi != _lib.MK_EPI_NONE and out_f32:
+        raise ValueError(f"{name}: epilogues write bf16")
+    return batch, M, N, K, c, epi
+
+
+def gemm_bf16_route(a, b, route, out_f32=False, out=None, epilogue=None, aux=None):
+    """gemm_bf16 on a given route ("ring", "pipe", "persist", "short",
+    "reg256", "generic256", "generic128" or "default"): every route gives
+    the same bits; a route that does not take the shape raises."""
+    batch, M, N, K, c, epi = _gemm_route_args(a, b, out_f32, out, epilogue, aux, "gemm_bf16_route")
+    check(lib().mk_gemm_bf16_route(_ptr(a), _ptr(b), _ptr(c), _ptr(aux) if aux is not None else None, epi, batch,
+                                   M, N, K, 1 if out_f32 else 0, _lib.GEMM_ROUTES[route], _stream(a.device)))
+    return c
+
+
+def gemm_route_fits(route, M, N, K, epilogue=None, out_f32=False):
+    epi = {None: _lib.MK_EPI_NONE, "add": _lib.MK_EPI_ADD, "swiglu": _lib.MK_EPI_SWIGLU,
+           "swiglu_pairs": _lib.MK_EPI_SWIGLU_PAIRS}[epilogue]
+    return bool(lib().mk_gemm_bf16_route_fits(_lib.GEMM_ROUTES[route], M, N, K, epi, 1 if out_f32 else 0))
+
+
+def gemm_bf16_autotune(a, b, out_f32=False, out=None, epilogue=None, aux=None):
+    """Times every route that takes the product and records the fastest in
+    the library's route table for this device and shape.  Returns (route
+    name, median us, the product)."""
+    batch, M, N, K, c, epi = _gemm_route_args(a, b, out_f32, out, epilogue, aux, "gemm_bf16_autotune")
+    route, us = ctypes.c_int(0), ctypes.c_float(0.0)
+    check(lib().mk_gemm_bf16_autotune(_ptr(a), _ptr(b), _ptr(c), _ptr(aux) if aux is not None else None, epi,
+                                      batch, M, N, K, 1 if out_f32 else 0, _stream(a.device), ctypes.byref(route),
+                                      ctypes.byref(us)))
+    names = {v: k for k, v in _lib.GEMM_ROUTES.items()}
+    return names[route.value], us.value, c
+
+
+def gemm_tuned_route(batch, M, N, K, epilogue=None, out_f32=False):
+    """The route table's entry for the product on the current device
+    ("default" when none)."""
+    epi = {None: _lib.MK_EPI_NONE, "add": _lib.MK_EPI_ADD, "swiglu": _lib.MK_EPI_SWIGLU,
+           "swiglu_pairs": _lib.MK_EPI_SWIGLU_PAIRS}[epilogue]
+    names = {v: k for k, v in _lib.GEMM_ROUTES.items()}
+    return names[lib().mk_gemm_tuned_route(batch, M, N, K, epi, 1 if out_f32 else 0)]
+
+
+def gemm_autotune_save(path):
+    """Writes the route table to `path`; returns the number of entries."""
+    n = lib().mk_gemm_autotune_save(str(path).encode())
+    if n < 0:
+        raise RuntimeError(lib().mk_last_error().decode())
+    return n
+
+
+def gemm_autotune_load(path):
+    """Merges a saved route table; returns the number of entries read."""
+    n = lib().mk_gemm_autotune_load(str(path).encode())
+    if n < 0:
+        raise RuntimeError(lib().mk_last_error().decode())
+    return n
+
+
+def gemm_autotune_clear():
+    lib().mk_gemm_autotune_clear()
 
 
 def gemm_bf16_nt(a, bt, out=None, epilogue=None, aux=None):

@@ -99,3 +99,56 @@ def test_rowops_reject_bad_args_on_host():
     assert L.mk_rmsnorm_lastdim(_lib.MK_DT_F32, fake, None, fake, 1, 8, 1e-6, None) == _lib.MK_EINVAL
     assert L.mk_reduce_lastdim(_lib.MK_DT_F32, 9, fake, fake, 1, 8, None) == _lib.MK_EUNSUPPORTED
     assert L.mk_gemm_bf16(fake, fake, fake, 1, 16, 12, 16, 0, None) == _lib.MK_EUNSUPPORTED
+
+
+def test_gemm_routes_fit_and_reject_on_host():
+    """Which route takes which product, and the host-side refusals of a
+    route call (nothing launched)."""
+    L = _lib.lib()
+    R, E = _lib.GEMM_ROUTES, _lib
+    fits = lambda r, M, N, K, epi=E.MK_EPI_NONE, f32=0: L.mk_gemm_bf16_route_fits(R[r], M, N, K, epi, f32)
+    assert fits("ring", 256, 512, 32) and not fits("ring", 384, 512, 32) and not fits("ring", 256, 512, 48)
+    assert fits("pipe", 256, 256, 320) and not fits("pipe", 256, 256, 288)
+    assert fits("persist", 512, 256, 128) and not fits("persist", 512, 256, 160)
+    assert not fits("persist", 512, 256, 64, f32=1) and not fits("persist", 512, 256, 64, E.MK_EPI_SWIGLU_PAIRS)
+    assert fits("short", 384, 640, 256) and not fits("short", 384, 640, 288) and not fits("short", 200, 640, 64)
+    assert fits("reg256", 256, 256, 64) and not fits("reg256", 256, 256, 32)
+    assert fits("generic128", 200, 264, 72) and fits("generic256", 7, 8, 8)
+    assert not fits("generic128", 256, 256, 64, E.MK_EPI_SWIGLU_PAIRS)
+    assert not fits("default", 256, 256, 64)
+    fake = ctypes.c_void_p(0x1000)
+    assert L.mk_gemm_bf16_route(fake, fake, fake, None, 0, 1, 256, 256, 64, 0, 99, None) == E.MK_EINVAL
+    assert L.mk_gemm_bf16_route(fake, fake, fake, None, 0, 1, 256, 256, 160, 0, R["persist"], None) == \
+        E.MK_EUNSUPPORTED
+    assert b"route 3" in L.mk_last_error()
+
+
+def test_gemm_route_table_file_round_trip(tmp_path):
+    """The route table's text file: load merges entries (any device's), save
+    writes them back byte for byte (sorted by key), and a file with another
+    header or a malformed line is refused with the table unchanged."""
+    L = _lib.lib()
+    L.mk_gemm_autotune_clear()
+    text = ("mk-gemm-autotune 1\n"
+            "gfx950 256 1 4096 4096 4096 0 0 2 112.500\n"
+            "gfx950 256 16 2048 2048 128 0 0 3 50.125\n"
+            "gfx942 304 1 384 640 64 1 0 4 9.000\n")
+    src = tmp_path / "routes.txt"
+    src.write_text(text)
+    assert L.mk_gemm_autotune_load(str(src).encode()) == 3
+    out = tmp_path / "saved.txt"
+    assert L.mk_gemm_autotune_save(str(out).encode()) == 3
+    lines = out.read_text().splitlines()
+    assert lines[0] == "mk-gemm-autotune 1" and sorted(lines[1:]) == lines[1:]
+    assert set(lines[1:]) == set(text.splitlines()[1:])
+    for bad in ("mk-gemm-autotune 2\n", "mk-gemm-autotune 1\ngfx950 256 1 64 64 64 0 0 9 1.0\n",
+                "mk-gemm-autotune 1\ngfx950 256 1 64 64 0 0 2 1.0\n",
+                "mk-gemm-autotune 1\ngfx950 256 1 64 64 64 0 0 2 1.0 extra\n"):
+        f = tmp_path / "bad.txt"
+        f.write_text(bad)
+        assert L.mk_gemm_autotune_load(str(f).encode()) == -_lib.MK_EINVAL, bad
+        assert L.mk_last_error()
+    assert L.mk_gemm_autotune_load(str(tmp_path / "missing.txt").encode()) == -_lib.MK_EINVAL
+    assert L.mk_gemm_autotune_save(str(out).encode()) == 3  # unchanged by the refused loads
+    L.mk_gemm_autotune_clear()
+    assert L.mk_gemm_autotune_save(str(out).encode()) == 0

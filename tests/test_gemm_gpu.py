@@ -278,3 +278,99 @@ def test_gemm_bf16_short_k_kernels(batch, M, N, K, epilogue, monkeypatch):
         if K <= 128:
             pers = run("0", "1")
             assert torch.equal(pers.view(torch.int16), ring.view(torch.int16)), "persistent and ring kernels differ"
+
+
+ROUTE_SHAPES = [(1, 256, 256, 64), (2, 512, 768, 320), (16, 256, 512, 128), (3, 384, 640, 96),
+                (1, 200, 264, 72), (1, 512, 512, 2048), (2, 256, 256, 4160), (1, 128, 384, 256)]
+
+
+@pytest.mark.parametrize("batch,M,N,K", ROUTE_SHAPES)
+@pytest.mark.parametrize("epilogue,out_f32", [(None, False), (None, True), ("add", False), ("swiglu", False)])
+def test_gemm_routes_bit_identical(batch, M, N, K, epilogue, out_f32):
+    """Every route that takes a product (the measured route choice picks
+    among them) gives the built-in choice's bits: the same k order in the
+    same MFMA on every kernel, ragged shapes and f32 outputs included."""
+    from mi355x import _lib as L
+    ops = _ops()
+    rng = np.random.default_rng(batch * 3 + M + N + K)
+    a = dev_bf16(_case(rng, (batch, M, K), 1.0 / np.sqrt(np.sqrt(K))))
+    b = dev_bf16(_case(rng, (batch, K, N), 1.0 / np.sqrt(np.sqrt(K))))
+    aux = dev_bf16(_case(rng, (batch, M, N), 1.0)) if epilogue else None
+    ref = ops.gemm_bf16(a, b, out_f32=out_f32, epilogue=epilogue, aux=aux)
+    bits = torch.int32 if out_f32 else torch.int16
+    ran = []
+    for route in L.GEMM_ROUTES:
+        if route == "default" or not ops.gemm_route_fits(route, M, N, K, epilogue, out_f32):
+            continue
+        print(f"gemm route {route} b={batch} M={M} N={N} K={K} epilogue={epilogue} f32={out_f32}", flush=True)
+        c = ops.gemm_bf16_route(a, b, route, out_f32=out_f32, epilogue=epilogue, aux=aux)
+        torch.cuda.synchronize()
+        assert torch.equal(c.view(bits), ref.view(bits)), f"route {route} differs"
+        ran.append(route)
+    assert len(ran) >= 2, ran
+
+
+@pytest.mark.parametrize("batch,M,N,K", [(1, 1024, 1024, 1024), (16, 256, 512, 128), (1, 384, 640, 64)])
+def test_gemm_autotune_records_a_fitting_route(batch, M, N, K, tmp_path):
+    """The measured choice: a route that takes the product, recorded in the
+    table for this device, the product left in c, and the table written and
+    read back."""
+    ops = _ops()
+    ops.gemm_autotune_clear()
+    rng = np.random.default_rng(M + N + K)
+    a = dev_bf16(_case(rng, (batch, M, K), 1.0 / np.sqrt(np.sqrt(K))))
+    b = dev_bf16(_case(rng, (batch, K, N), 1.0 / np.sqrt(np.sqrt(K))))
+    name, us, c = ops.gemm_bf16_autotune(a, b)
+    torch.cuda.synchronize()
+    print(f"autotune b={batch} M={M} N={N} K={K}: {name} {us:.1f} us", flush=True)
+    assert name != "default" and ops.gemm_route_fits(name, M, N, K) and us > 0
+    assert torch.equal(c.view(torch.int16), ops.gemm_bf16(a, b).view(torch.int16))
+    assert ops.gemm_tuned_route(batch, M, N, K) == name
+    assert ops.gemm_tuned_route(batch, M, N, K, out_f32=True) == "default"
+    path = tmp_path / "routes.txt"
+    assert ops.gemm_autotune_save(path) == 1
+    ops.gemm_autotune_clear()
+    assert ops.gemm_tuned_route(batch, M, N, K) == "default"
+    assert ops.gemm_autotune_load(path) == 1
+    assert ops.gemm_tuned_route(batch, M, N, K) == name
+    ops.gemm_autotune_clear()
+
+
+def test_runtime_tunes_gemm_steps(tmp_path, monkeypatch):
+    """The plugin runtime measures each bf16 GEMM step's route at the first
+    plan build and keeps the table in MK_AUTOTUNE_CACHE_DIR; the outputs
+    equal the untuned plan's bit for bit (MK_GEMM_AUTOTUNE=0)."""
+    from mi355x import programs
+    from mi355x import runtime as rt
+    ops = _ops()
+    monkeypatch.setenv("MK_AUTOTUNE_CACHE_DIR", str(tmp_path))
+    monkeypatch.delenv("MK_DISABLE_AUTOTUNE_CACHE_PERSIST", raising=False)
+    rng = np.random.default_rng(11)
+    M, K, N = 512, 320, 768
+    a = _case(rng, (M, K), 1.0 / np.sqrt(np.sqrt(K)))
+    b = _case(rng, (K, N), 1.0 / np.sqrt(np.sqrt(K)))
+    outs = {}
+    for tune in ("1", "0"):
+        monkeypatch.setenv("MK_GEMM_AUTOTUNE", tune)
+        ops.gemm_autotune_clear()
+        client = rt.Client()
+        try:
+            exe = client.compile(programs.matmul(M, K, N))
+            ba, bb = client.buffer(a, rt.BF16), client.buffer(b, rt.BF16)
+            (o,), done = exe.execute([ba, bb])
+            done.wait()
+            outs[tune] = o.to_numpy()
+            if tune == "1":
+                assert ops.gemm_tuned_route(1, M, N, K) != "default"
+            else:
+                assert ops.gemm_tuned_route(1, M, N, K) == "default"
+            for h in (ba, bb, o):
+                h.close()
+            exe.close()
+        finally:
+            client.close()
+    assert np.array_equal(outs["1"], outs["0"])
+    lines = (tmp_path / "gemm_routes.txt").read_text().splitlines()
+    assert lines[0] == "mk-gemm-autotune 1"
+    assert any(l.split()[2:6] == ["1", str(M), str(N), str(K)] for l in lines[1:]), lines
+    ops.gemm_autotune_clear()
