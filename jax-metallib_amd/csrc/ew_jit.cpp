@@ -382,6 +382,8 @@ hipError_t load_module(const std::vector<char>& code, JitKernel* k, std::string*
 
 }  // namespace
 
+std::string cache_directory() { return cache_dir(); }
+
 std::string ew_jit_source(int dtype, const mk_ew_instr* prog, int n_instr, int n_inputs, int out_slot) {
   return generate(dtype, prog, n_instr, n_inputs, out_slot);
 }

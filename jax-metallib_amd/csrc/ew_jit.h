@@ -38,4 +38,9 @@ void ew_jit_seed(const std::string& source, const std::vector<char>& code);
 // Process totals: hiprtc compiles, disk-cache hits, memory-cache hits.
 void ew_jit_stats(int64_t* compiles, int64_t* disk_hits, int64_t* mem_hits);
 
+// The library's on-disk cache directory (MK_CACHE_DIR, default
+// $HOME/.cache/mi355x-mk, created when missing); "" when
+// MK_DISABLE_CACHE_PERSIST is set or the directory is unusable.
+std::string cache_directory();
+
 }  // namespace mkc

@@ -16,7 +16,6 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
-#include <sys/stat.h>
 
 #include <algorithm>
 #include <atomic>
@@ -347,31 +346,18 @@ mkrt_buffer* new_buffer(mkrt_client* c, int type, const std::vector<int64_t>& di
 // GEMM routes measured at the first plan build, as the reference autotunes
 // its GEMM variants (AutotuneGemm, src/pjrt_plugin/core/mps_executable.mm:
 // 3433-3725): MK_GEMM_AUTOTUNE=0 keeps the built-in choice.  The route table
-// persists across processes in MK_AUTOTUNE_CACHE_DIR (default
-// $HOME/.cache/mi355x-mk)/gemm_routes.txt unless
-// MK_DISABLE_AUTOTUNE_CACHE_PERSIST=1 (the reference's cache,
-// :3270-3420).  Every route gives the same bits, so this only changes speed.
+// persists across processes as gemm_routes.txt in the library's cache
+// directory (MK_CACHE_DIR; none with MK_DISABLE_CACHE_PERSIST=1), as the
+// reference's cache does (:3270-3420).  Every route gives the same bits, so
+// this only changes speed.
 bool gemm_autotune_enabled() {
   const char* v = getenv("MK_GEMM_AUTOTUNE");
   return !(v && v[0] == '0' && v[1] == '\0');
 }
 
 std::string gemm_route_cache_path() {
-  const char* v = getenv("MK_DISABLE_AUTOTUNE_CACHE_PERSIST");
-  if (v && v[0] == '1') return "";
-  std::string dir;
-  const char* d = getenv("MK_AUTOTUNE_CACHE_DIR");
-  if (d && d[0]) {
-    dir = d;
-  } else {
-    const char* home = getenv("HOME");
-    if (!home || !home[0]) return "";
-    dir = std::string(home) + "/.cache";
-    mkdir(dir.c_str(), 0755);
-    dir += "/mi355x-mk";
-  }
-  mkdir(dir.c_str(), 0755);
-  return dir + "/gemm_routes.txt";
+  const std::string dir = mkc::cache_directory();
+  return dir.empty() ? dir : dir + "/gemm_routes.txt";
 }
 
 std::mutex g_route_cache_mu;

@@ -338,13 +338,13 @@ def test_gemm_autotune_records_a_fitting_route(batch, M, N, K, tmp_path):
 
 def test_runtime_tunes_gemm_steps(tmp_path, monkeypatch):
     """The plugin runtime measures each bf16 GEMM step's route at the first
-    plan build and keeps the table in MK_AUTOTUNE_CACHE_DIR; the outputs
-    equal the untuned plan's bit for bit (MK_GEMM_AUTOTUNE=0)."""
+    plan build and keeps the table in the cache directory (MK_CACHE_DIR);
+    the outputs equal the untuned plan's bit for bit (MK_GEMM_AUTOTUNE=0)."""
     from mi355x import programs
     from mi355x import runtime as rt
     ops = _ops()
-    monkeypatch.setenv("MK_AUTOTUNE_CACHE_DIR", str(tmp_path))
-    monkeypatch.delenv("MK_DISABLE_AUTOTUNE_CACHE_PERSIST", raising=False)
+    monkeypatch.setenv("MK_CACHE_DIR", str(tmp_path))
+    monkeypatch.delenv("MK_DISABLE_CACHE_PERSIST", raising=False)
     rng = np.random.default_rng(11)
     M, K, N = 512, 320, 768
     a = _case(rng, (M, K), 1.0 / np.sqrt(np.sqrt(K)))
