@@ -1265,47 +1265,57 @@ bool route_fits(int route, int64_t M, int64_t N, int64_t K, int epi, int out_f32
   }
 }
 
-// The built-in choice (what MK_GEMM_* environment knobs steer).
+// The built-in choice (what MK_GEMM_* environment knobs steer), from
+// timings with operands rotated past the 256 MB Infinity Cache (one box,
+// us):
+//   - K >= 512 on 256-multiples: the pipelined kernel (fragment prefetch,
+//     5-stage ring) at any tile count: 2048^3 51.1 against 54.2 (128-tile
+//     kernel) / 58.6 (ring); 1024^3 28.4 / 28.6 / 31.8; 16 x 1024^3 42.9 /
+//     77.3 / 45.2; 8192^2 x 1024 151.6 / 288.2 / 153.4; 256 x 14336 x 4096
+//     102.1 / 103.5 / 106.7 (8 x 512^2 x 4096: 106.4 / 103.7 / 114.0).  It
+//     runs at a lower clock (GRBM_GUI_ACTIVE per ns ~2.1 against
+//     ~2.35 GHz), which slows the kernels around it; in the decoder (K
+//     2048 and 8192) it still gains end to end: QKV and paired gate/up 2 %
+//     (5.00 vs 5.09 ms), the output and down projections another 2.5 %
+//     (4.82 vs 4.95 ms).  MK_GEMM_PIPE_K moves the threshold, MK_GEMM_PIPE=0
+//     keeps the ring kernel.
+//   - K <= 256 with fewer 256 x 256 tiles than CUs: the 128 x 128 kernel
+//     with all of K in LDS: 2048^2 x 256 7.9 against 12.1 (128-tile
+//     kernel); 1024^2 x 256 5.7 / 10.5; 4 x 1024^2 x 128 6.1 / 9.1 (9.9
+//     persistent).
+//   - K <= 128 with a tile per CU or more: the persistent kernel (the next
+//     tile's loads under the current tile's stores): 16 x 2048^2 x 128 48.5
+//     against 54.2 (ring) / 58.6 (128 x 128 all-K-in-LDS).
+//     MK_GEMM_PERSIST=0 turns it off.
+//   - MK_GEMM_SHORTK sets the largest K of the 128 x 128 all-K-in-LDS
+//     kernel (default 256 on 256-multiples, 128 on other 128-multiples;
+//     0: never).
 int default_route(int64_t batch, int64_t M, int64_t N, int64_t K, int epi, int out_f32) {
   const char* dma_env = getenv("MK_GEMM_DMA");
   const bool dma = !(dma_env && dma_env[0] == '0');
   const bool simple_epi = epi == MK_EPI_NONE || epi == MK_EPI_ADD || epi == MK_EPI_SWIGLU;
   const int64_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256) * batch;
-  int tile = env_tile();
+  const int env_t = env_tile();
+  int tile = env_t;
   if (tile == 0) tile = big_tiles >= 128 ? 256 : 128;
   if (epi == MK_EPI_SWIGLU_PAIRS) tile = 256;
-  // K <= 128 on 256 x 256 tiles: the persistent kernel (one workgroup per
-  // CU, the next tile's loads under the current tile's stores): 16 x 2048^2
-  // x 128 50.1 against 54 us for the ring kernel, x 64 32.7 against 42 us,
-  // 8192^2 x 128 41.9 against 56 us.  MK_GEMM_PERSIST=0 turns it off.
-  const char* pe = getenv("MK_GEMM_PERSIST");
-  if (!(pe && pe[0] == '0') && dma && route_fits(MK_GEMM_ROUTE_PERSIST, M, N, K, epi, out_f32))
-    return MK_GEMM_ROUTE_PERSIST;
-  // Short K on 128-multiples that are not 256-multiples: the 128 x 128
-  // kernel with all of K in LDS (two workgroups per CU at K <= 128), faster
-  // there than the generic 128 x 128 kernel (16 x 2048^2 x 128: 59 against
-  // 73 us).  MK_GEMM_SHORTK sets the largest K it takes (0: never, up to
-  // 256; with 256-multiples it is taken only when the persistent kernel
-  // is off).
+  const bool a256 = M % 256 == 0 && N % 256 == 0 && K % 32 == 0;
   const char* sk = getenv("MK_GEMM_SHORTK");
-  const int64_t shortk_max = std::min<int64_t>(sk ? atoll(sk) : 128, 256);
-  if (K <= shortk_max && route_fits(MK_GEMM_ROUTE_SHORT, M, N, K, epi, out_f32)) return MK_GEMM_ROUTE_SHORT;
-  if (tile == 256 && dma && M % 256 == 0 && N % 256 == 0 && K % 32 == 0) {
-    // The pipelined kernel (fragment prefetch + 5-stage ring) for K loops
-    // of 2048 and more, every epilogue included (it has no registers left
-    // to preload an ADD / SWIGLU operand, so it reads it at the store).
-    // Alone it is 3-5 % faster at K = 2048 and 7-9 % from K = 4096.  It runs
-    // at a lower clock (GRBM_GUI_ACTIVE per ns ~2.1 against ~2.35 GHz),
-    // which slows the kernels around it; in the decoder it still gains end
-    // to end: QKV and paired gate/up 2 % (5.00 vs 5.09 ms), then the output
-    // and down projections with their residual-add epilogue another 2.5 %
-    // (4.82 vs 4.95 ms).  MK_GEMM_PIPE_K moves the threshold.
-    const char* pv = getenv("MK_GEMM_PIPE");
-    const char* pk = getenv("MK_GEMM_PIPE_K");
-    const int64_t pipe_k = pk ? atoll(pk) : 2048;
-    const bool pipe = !(pv && atoi(pv) == 0) && K >= pipe_k;
-    return pipe && route_fits(MK_GEMM_ROUTE_PIPE, M, N, K, epi, out_f32) ? MK_GEMM_ROUTE_PIPE : MK_GEMM_ROUTE_RING;
-  }
+  const int64_t shortk_max = std::min<int64_t>(sk ? atoll(sk) : (a256 ? 256 : 128), 256);
+  const char* pe = getenv("MK_GEMM_PERSIST");
+  const bool persist_on = !(pe && pe[0] == '0') && dma;
+  const int cus = device_cus();
+  if (a256 && env_t == 0 && persist_on && big_tiles >= cus && route_fits(MK_GEMM_ROUTE_PERSIST, M, N, K, epi, out_f32))
+    return MK_GEMM_ROUTE_PERSIST;
+  if (K <= shortk_max && (!a256 || big_tiles < cus || !persist_on) && env_t == 0 &&
+      route_fits(MK_GEMM_ROUTE_SHORT, M, N, K, epi, out_f32))
+    return MK_GEMM_ROUTE_SHORT;
+  const char* pv = getenv("MK_GEMM_PIPE");
+  const char* pk = getenv("MK_GEMM_PIPE_K");
+  const int64_t pipe_k = pk ? atoll(pk) : 512;
+  const bool pipe = !(pv && atoi(pv) == 0) && K >= pipe_k && route_fits(MK_GEMM_ROUTE_PIPE, M, N, K, epi, out_f32);
+  if (dma && a256 && (tile == 256 || (pipe && env_t == 0)))
+    return pipe ? MK_GEMM_ROUTE_PIPE : MK_GEMM_ROUTE_RING;
   if (!simple_epi) return MK_GEMM_ROUTE_RING;  // paired SwiGLU: checked aligned by the caller
   if (tile == 256 && route_fits(MK_GEMM_ROUTE_REG256, M, N, K, epi, out_f32)) return MK_GEMM_ROUTE_REG256;
   return tile == 256 ? MK_GEMM_ROUTE_GENERIC256 : MK_GEMM_ROUTE_GENERIC128;

@@ -233,10 +233,10 @@ def test_gemm_bf16_nt_rejects_unaligned_shapes():
                                          (1, 256, 256, 256), (3, 384, 640, 64), (1, 128, 128, 160),
                                          (16, 2048, 2048, 128), (5, 512, 256, 64), (1, 4096, 4096, 128)])
 @pytest.mark.parametrize("epilogue", [None, "add", "swiglu"])
-def test_gemm_bf16_short_k_kernels(batch, M, N, K, epilogue, monkeypatch):
+def test_gemm_bf16_short_k_kernels(batch, M, N, K, epilogue):
     """The two short-K kernels: the 128 x 128 one with all of K in LDS
-    (MK_GEMM_SHORTK=256, K <= 256) and the persistent 256 x 256 one (K <=
-    128, M and N multiples of 256; the default there).  Against float64 on
+    (route "short", K <= 256) and the persistent 256 x 256 one (route
+    "persist", K <= 128, M and N multiples of 256).  Against float64 on
     every element, bit for bit against each other and the 256 x 256 ring
     kernel (each k in the same order in the same MFMA), and with the ADD /
     SWIGLU epilogue bit for bit against the plain product followed by the
@@ -250,15 +250,12 @@ def test_gemm_bf16_short_k_kernels(batch, M, N, K, epilogue, monkeypatch):
     aux = dev_bf16(_case(rng, (batch, M, N), 1.0)) if epilogue else None
     print(f"gemm short-k case b={batch} M={M} N={N} K={K} epilogue={epilogue}", flush=True)
 
-    def run(shortk, persist, tile="0"):
-        monkeypatch.setenv("MK_GEMM_SHORTK", shortk)
-        monkeypatch.setenv("MK_GEMM_PERSIST", persist)
-        monkeypatch.setenv("MK_GEMM_TILE", tile)
-        out = ops.gemm_bf16(a, b, epilogue=epilogue, aux=aux)
+    def run(route):
+        out = ops.gemm_bf16_route(a, b, route, epilogue=epilogue, aux=aux)
         torch.cuda.synchronize()
         return out
 
-    c = run("256", "0")
+    c = run("short")
     if epilogue is None:
         if batch * M * N * K <= 2 ** 30:
             ref, _ = gemm.matmul_bf16(a_h, b_h)
@@ -273,10 +270,10 @@ def test_gemm_bf16_short_k_kernels(batch, M, N, K, epilogue, monkeypatch):
         torch.cuda.synchronize()
         assert torch.equal(c.view(torch.int16), want.view(torch.int16)), f"short-k {epilogue} epilogue"
     if M % 256 == 0 and N % 256 == 0:
-        ring = run("0", "0", "256")
+        ring = run("ring")
         assert torch.equal(c.view(torch.int16), ring.view(torch.int16)), "short-k and ring kernels differ"
         if K <= 128:
-            pers = run("0", "1")
+            pers = run("persist")
             assert torch.equal(pers.view(torch.int16), ring.view(torch.int16)), "persistent and ring kernels differ"
 
 
