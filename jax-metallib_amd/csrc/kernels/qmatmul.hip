@@ -1303,26 +1303,51 @@ __global__ __launch_bounds__(256) void qmm_splitk_reduce_kernel(QArgs a) {
 // workspace), which the bf16 GEMM then multiplies.  int4: (q - z) * s is
 // exact in f32 (at most 12 significant bits) and rounded once to bf16 (RNE);
 // int8: w * s is rounded to f32, then to bf16.  One thread: 8
-// columns of one packed row (int4: k = 2r and 2r + 1) or of one k row (int8);
+// columns of kDeqRows packed rows (int4: k = 2r and 2r + 1) or k rows (int8);
 // every load and store is a whole 8- or 16-byte vector.  wd rows are ldd
 // elements apart; with half = 0 / 1 (gate / up of a paired SwiGLU product)
 // column n goes to 32 (n / 16) + n % 16 + 16 half of a [K, 2N] buffer, the
 // 16-column interleave the MK_EPI_SWIGLU_PAIRS epilogue reads (8-column
 // groups never straddle a 16-column block); half < 0 keeps column n.
+constexpr int kDeqRows = 8;
+
+// Grid of qmm_dequant_kernel: 256 column chunks of 8 by kDeqRows rows.
+inline dim3 dequant_grid(bool int4, int64_t K, int64_t N) {
+  const int64_t rows = int4 ? K / 2 : K;
+  return dim3((unsigned)((N / 8 + 255) / 256), (unsigned)std::min<int64_t>((rows + kDeqRows - 1) / kDeqRows, 65535));
+}
+
 template <bool INT4>
 __global__ __launch_bounds__(256) void qmm_dequant_kernel(QArgs a, uint16_t* wd, int64_t ldd, int half) {
+  // Thread: 8 columns c0..c0+7 (blockIdx.x) of kDeqRows consecutive weight
+  // rows (blockIdx.y), their loads issued together; the scales (and int4
+  // zero points, whose 64-k group the rows share) loaded once.
   const int N8 = a.N / 8;
-  const int64_t rows = INT4 ? a.K / 2 : a.K;
-  const int64_t total = rows * N8;
-  for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += (int64_t)gridDim.x * 256) {
-    const int64_t r = t / N8;
-    const int c0 = (int)(t - r * N8) * 8;
-    const int64_t d0 = half < 0 ? c0 : 32 * (c0 / 16) + c0 % 16 + 16 * half;
-    const u32x2 wb = *reinterpret_cast<const u32x2*>(a.w + r * a.N + c0);
-    if (INT4) {
-      const int64_t g = r / 32;  // 64-k group of rows 2r, 2r + 1
-      const u32x4 sb = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.s) + g * a.N + c0);
-      const u32x2 zb = *reinterpret_cast<const u32x2*>(a.z + g * a.N + c0);
+  const int rows = INT4 ? a.K / 2 : a.K;
+  const int c8 = blockIdx.x * 256 + threadIdx.x;
+  if (c8 >= N8) return;
+  const int c0 = c8 * 8;
+  const int64_t d0 = half < 0 ? c0 : 32 * (c0 / 16) + c0 % 16 + 16 * half;
+  for (int r0 = blockIdx.y * kDeqRows; r0 < rows; r0 += gridDim.y * kDeqRows) {
+  u32x2 wb[kDeqRows];
+#pragma unroll
+  for (int i = 0; i < kDeqRows; ++i)
+    if (r0 + i < rows) wb[i] = *reinterpret_cast<const u32x2*>(a.w + (int64_t)(r0 + i) * a.N + c0);
+  if (INT4) {
+    const int g = r0 / 32;  // 64-k group of rows 2r, 2r + 1 (kDeqRows divides 32)
+    const u32x4 sb = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.s) + (int64_t)g * a.N + c0);
+    const u32x2 zb = *reinterpret_cast<const u32x2*>(a.z + (int64_t)g * a.N + c0);
+    float sv[8];
+    int zv[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const uint32_t sw = (c < 2 ? sb.x : c < 4 ? sb.y : c < 6 ? sb.z : sb.w) >> (16 * (c & 1));
+      sv[c] = bf16_to_f32(sw & 0xffffu);
+      zv[c] = (int)(((c < 4 ? zb.x : zb.y) >> (8 * (c & 3))) & 0xffu);
+    }
+#pragma unroll
+    for (int i = 0; i < kDeqRows; ++i) {
+      if (r0 + i >= rows) break;
       uint32_t lo[4], hi[4];
 #pragma unroll
       for (int j = 0; j < 8; j += 2) {
@@ -1330,31 +1355,34 @@ __global__ __launch_bounds__(256) void qmm_dequant_kernel(QArgs a, uint16_t* wd,
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const int c = j + h;
-          const uint32_t byte = ((c < 4 ? wb.x : wb.y) >> (8 * (c & 3))) & 0xffu;
-          const int zz = (int)(((c < 4 ? zb.x : zb.y) >> (8 * (c & 3))) & 0xffu);
-          const uint32_t sw = (c < 2 ? sb.x : c < 4 ? sb.y : c < 6 ? sb.z : sb.w) >> (16 * (c & 1));
-          const float s = bf16_to_f32(sw & 0xffffu);
-          e[h] = (float)((int)(byte & 15u) - zz) * s;
-          o[h] = (float)((int)(byte >> 4) - zz) * s;
+          const uint32_t byte = ((c < 4 ? wb[i].x : wb[i].y) >> (8 * (c & 3))) & 0xffu;
+          e[h] = (float)((int)(byte & 15u) - zv[c]) * sv[c];
+          o[h] = (float)((int)(byte >> 4) - zv[c]) * sv[c];
         }
         lo[j / 2] = pack_bf16x2(e[0], e[1]);
         hi[j / 2] = pack_bf16x2(o[0], o[1]);
       }
+      const int64_t r = r0 + i;
       *reinterpret_cast<u32x4*>(wd + (2 * r) * ldd + d0) = u32x4{lo[0], lo[1], lo[2], lo[3]};
       *reinterpret_cast<u32x4*>(wd + (2 * r + 1) * ldd + d0) = u32x4{hi[0], hi[1], hi[2], hi[3]};
-    } else {
-      const float* sp = static_cast<const float*>(a.s) + c0;
-      const f32x4 s0 = *reinterpret_cast<const f32x4*>(sp), s1 = *reinterpret_cast<const f32x4*>(sp + 4);
-      const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    }
+  } else {
+    const float* sp = static_cast<const float*>(a.s) + c0;
+    const f32x4 s0 = *reinterpret_cast<const f32x4*>(sp), s1 = *reinterpret_cast<const f32x4*>(sp + 4);
+    const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+    for (int i = 0; i < kDeqRows; ++i) {
+      if (r0 + i >= rows) break;
       uint32_t out[4];
 #pragma unroll
       for (int j = 0; j < 8; j += 2) {
-        const int8_t b0 = (int8_t)(((j < 4 ? wb.x : wb.y) >> (8 * (j & 3))) & 0xffu);
-        const int8_t b1 = (int8_t)(((j < 4 ? wb.x : wb.y) >> (8 * ((j + 1) & 3))) & 0xffu);
+        const int8_t b0 = (int8_t)(((j < 4 ? wb[i].x : wb[i].y) >> (8 * (j & 3))) & 0xffu);
+        const int8_t b1 = (int8_t)(((j < 4 ? wb[i].x : wb[i].y) >> (8 * ((j + 1) & 3))) & 0xffu);
         out[j / 2] = pack_bf16x2((float)b0 * sv[j], (float)b1 * sv[j + 1]);
       }
-      *reinterpret_cast<u32x4*>(wd + r * ldd + d0) = u32x4{out[0], out[1], out[2], out[3]};
+      *reinterpret_cast<u32x4*>(wd + (int64_t)(r0 + i) * ldd + d0) = u32x4{out[0], out[1], out[2], out[3]};
     }
+  }
   }
 }
 
@@ -1808,12 +1836,11 @@ int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, v
   }
   if (p.deq) {
     uint16_t* wd = reinterpret_cast<uint16_t*>(a.part);
-    const int64_t total = (fmt == MK_QFMT_INT4_G64 ? K / 2 : K) * (N / 8);
-    const int blocks = (int)std::min<int64_t>((total + 255) / 256, 16384);
+    const dim3 blocks = mk::dequant_grid(fmt == MK_QFMT_INT4_G64, K, N);
     if (fmt == MK_QFMT_INT4_G64)
-      hipLaunchKernelGGL(mk::qmm_dequant_kernel<true>, dim3(blocks), dim3(256), 0, st, a, wd, (int64_t)N, -1);
+      hipLaunchKernelGGL(mk::qmm_dequant_kernel<true>, blocks, dim3(256), 0, st, a, wd, (int64_t)N, -1);
     else
-      hipLaunchKernelGGL(mk::qmm_dequant_kernel<false>, dim3(blocks), dim3(256), 0, st, a, wd, (int64_t)N, -1);
+      hipLaunchKernelGGL(mk::qmm_dequant_kernel<false>, blocks, dim3(256), 0, st, a, wd, (int64_t)N, -1);
     e = hipGetLastError();
     if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: dequantise launch failed: %s", fn, hipGetErrorString(e));
     const int rc = epi == MK_EPI_NONE ? mk_gemm_bf16(x, wd, y, 1, M, N, K, 0, stream)
@@ -1974,8 +2001,6 @@ int run_pair(int fmt, const void* x, const void* wg, const void* sg, const void*
                      (long long)ws_bytes);
   uint16_t* wd = reinterpret_cast<uint16_t*>(static_cast<unsigned char*>(ws) + mk::kWidePartOffset);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int64_t total = (fmt == MK_QFMT_INT4_G64 ? K / 2 : K) * (N / 8);
-  const int blocks = (int)std::min<int64_t>((total + 255) / 256, 16384);
   for (int half = 0; half < 2; ++half) {
     mk::QArgs a{};
     a.w = static_cast<const uint8_t*>(half ? wu : wg);
@@ -1985,9 +2010,11 @@ int run_pair(int fmt, const void* x, const void* wg, const void* sg, const void*
     a.K = (int)K;
     a.N = (int)N;
     if (fmt == MK_QFMT_INT4_G64)
-      hipLaunchKernelGGL(mk::qmm_dequant_kernel<true>, dim3(blocks), dim3(256), 0, st, a, wd, 2 * N, half);
+      hipLaunchKernelGGL(mk::qmm_dequant_kernel<true>, mk::dequant_grid(true, K, N), dim3(256), 0, st, a, wd,
+                         2 * N, half);
     else
-      hipLaunchKernelGGL(mk::qmm_dequant_kernel<false>, dim3(blocks), dim3(256), 0, st, a, wd, 2 * N, half);
+      hipLaunchKernelGGL(mk::qmm_dequant_kernel<false>, mk::dequant_grid(false, K, N), dim3(256), 0, st, a, wd,
+                         2 * N, half);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: dequantise launch failed: %s", fn, hipGetErrorString(e));
   }
