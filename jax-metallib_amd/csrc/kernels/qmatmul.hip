@@ -1303,86 +1303,139 @@ __global__ __launch_bounds__(256) void qmm_splitk_reduce_kernel(QArgs a) {
 // workspace), which the bf16 GEMM then multiplies.  int4: (q - z) * s is
 // exact in f32 (at most 12 significant bits) and rounded once to bf16 (RNE);
 // int8: w * s is rounded to f32, then to bf16.  One thread: 8
-// columns of kDeqRows packed rows (int4: k = 2r and 2r + 1) or k rows (int8);
+// columns of RPT packed rows (int4: k = 2r and 2r + 1) or k rows (int8);
 // every load and store is a whole 8- or 16-byte vector.  wd rows are ldd
-// elements apart; with half = 0 / 1 (gate / up of a paired SwiGLU product)
-// column n goes to 32 (n / 16) + n % 16 + 16 half of a [K, 2N] buffer, the
-// 16-column interleave the MK_EPI_SWIGLU_PAIRS epilogue reads (8-column
-// groups never straddle a 16-column block); half < 0 keeps column n.
-constexpr int kDeqRows = 8;
-
-// Grid of qmm_dequant_kernel: 256 column chunks of 8 by kDeqRows rows.
-inline dim3 dequant_grid(bool int4, int64_t K, int64_t N) {
-  const int64_t rows = int4 ? K / 2 : K;
-  return dim3((unsigned)((N / 8 + 255) / 256), (unsigned)std::min<int64_t>((rows + kDeqRows - 1) / kDeqRows, 65535));
+// elements apart.  The paired form (below) writes a SwiGLU product's gate
+// and up weights into one [K, 2N] buffer, column n of the gate at
+// 32 (n / 16) + n % 16 and of the up 16 further: the 16-column interleave
+// the MK_EPI_SWIGLU_PAIRS epilogue reads (8-column groups never straddle a
+// 16-column block).
+// Rows per thread of the dequantise kernels (RPT; it divides 32, so a
+// thread's rows share an int4 64-k group).  Medians of one process, us,
+// RPT 1 / 2 / 4 / 8:
+//   int4 4096 x 14336            30.6 / 28.4 / 29.3 / 28.5
+//   int4 2048 x 2048 and 8192 x 2048 (mixed)  10.5 / 10.0 / 9.5 / 9.0
+//   int4 2048 x 6144              8.6 / 8.6 / 8.1 / 8.4
+//   int4 pair 2048 x 2 x 8192    19.4 / 19.5 / 22.8 / 27.2
+//   int8 4096 x 14336            43.0 / 33.5 / 35.0 / 37.9
+// so 8 for an int4 weight, 2 for the pair (two weights per thread) and for
+// int8.  MK_QMM_DEQ_RPT forces one.
+inline int dequant_rpt(bool int4, bool pair) {
+  if (const char* e = getenv("MK_QMM_DEQ_RPT")) {
+    const int r = atoi(e);
+    if (r == 1 || r == 2 || r == 4 || r == 8) return r;
+  }
+  return int4 && !pair ? 8 : 2;
 }
 
-template <bool INT4>
-__global__ __launch_bounds__(256) void qmm_dequant_kernel(QArgs a, uint16_t* wd, int64_t ldd, int half) {
-  // Thread: 8 columns c0..c0+7 (blockIdx.x) of kDeqRows consecutive weight
-  // rows (blockIdx.y), their loads issued together; the scales (and int4
-  // zero points, whose 64-k group the rows share) loaded once.
+// Grid: 256 column chunks of 8 by RPT rows.
+inline dim3 dequant_grid(bool int4, int64_t K, int64_t N, int rpt) {
+  const int64_t rows = int4 ? K / 2 : K;
+  return dim3((unsigned)((N / 8 + 255) / 256), (unsigned)std::min<int64_t>((rows + rpt - 1) / rpt, 65535));
+}
+
+// One thread's share of a weight: 8 columns c0..c0+7 of RPT rows from r0
+// (every row < rows), the scales (and int4 zero points, whose 64-k group
+// the rows share) loaded once.
+template <bool INT4, int RPT>
+struct DeqRows {
+  u32x2 wb[RPT];
+  float sv[8];
+  int zv[8];
+
+  __device__ __forceinline__ void load(const QArgs& a, int r0, int rows, int c0) {
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+      if (r0 + i < rows) wb[i] = *reinterpret_cast<const u32x2*>(a.w + (int64_t)(r0 + i) * a.N + c0);
+    if (INT4) {
+      const int g = r0 / 32;  // 64-k group of rows 2r, 2r + 1 (RPT divides 32)
+      const u32x4 sb = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.s) + (int64_t)g * a.N + c0);
+      const u32x2 zb = *reinterpret_cast<const u32x2*>(a.z + (int64_t)g * a.N + c0);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const uint32_t sw = (c < 2 ? sb.x : c < 4 ? sb.y : c < 6 ? sb.z : sb.w) >> (16 * (c & 1));
+        sv[c] = bf16_to_f32(sw & 0xffffu);
+        zv[c] = (int)(((c < 4 ? zb.x : zb.y) >> (8 * (c & 3))) & 0xffu);
+      }
+    } else {
+      const float* sp = static_cast<const float*>(a.s) + c0;
+      const f32x4 s0 = *reinterpret_cast<const f32x4*>(sp), s1 = *reinterpret_cast<const f32x4*>(sp + 4);
+      sv[0] = s0.x; sv[1] = s0.y; sv[2] = s0.z; sv[3] = s0.w;
+      sv[4] = s1.x; sv[5] = s1.y; sv[6] = s1.z; sv[7] = s1.w;
+    }
+  }
+
+  // Rows of wd are ldd elements apart; this thread's 8 columns start at d0.
+  __device__ __forceinline__ void emit(int r0, int rows, uint16_t* wd, int64_t ldd, int64_t d0) const {
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      if (r0 + i >= rows) break;
+      const int64_t r = r0 + i;
+      if (INT4) {
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+          float e[2], o[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int c = j + h;
+            const uint32_t byte = ((c < 4 ? wb[i].x : wb[i].y) >> (8 * (c & 3))) & 0xffu;
+            e[h] = (float)((int)(byte & 15u) - zv[c]) * sv[c];
+            o[h] = (float)((int)(byte >> 4) - zv[c]) * sv[c];
+          }
+          lo[j / 2] = pack_bf16x2(e[0], e[1]);
+          hi[j / 2] = pack_bf16x2(o[0], o[1]);
+        }
+        *reinterpret_cast<u32x4*>(wd + (2 * r) * ldd + d0) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+        *reinterpret_cast<u32x4*>(wd + (2 * r + 1) * ldd + d0) = u32x4{hi[0], hi[1], hi[2], hi[3]};
+      } else {
+        uint32_t out[4];
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+          const int8_t b0 = (int8_t)(((j < 4 ? wb[i].x : wb[i].y) >> (8 * (j & 3))) & 0xffu);
+          const int8_t b1 = (int8_t)(((j < 4 ? wb[i].x : wb[i].y) >> (8 * ((j + 1) & 3))) & 0xffu);
+          out[j / 2] = pack_bf16x2((float)b0 * sv[j], (float)b1 * sv[j + 1]);
+        }
+        *reinterpret_cast<u32x4*>(wd + r * ldd + d0) = u32x4{out[0], out[1], out[2], out[3]};
+      }
+    }
+  }
+};
+
+template <bool INT4, int RPT>
+__global__ __launch_bounds__(256) void qmm_dequant_kernel(QArgs a, uint16_t* wd, int64_t ldd) {
   const int N8 = a.N / 8;
   const int rows = INT4 ? a.K / 2 : a.K;
   const int c8 = blockIdx.x * 256 + threadIdx.x;
   if (c8 >= N8) return;
   const int c0 = c8 * 8;
-  const int64_t d0 = half < 0 ? c0 : 32 * (c0 / 16) + c0 % 16 + 16 * half;
-  for (int r0 = blockIdx.y * kDeqRows; r0 < rows; r0 += gridDim.y * kDeqRows) {
-  u32x2 wb[kDeqRows];
-#pragma unroll
-  for (int i = 0; i < kDeqRows; ++i)
-    if (r0 + i < rows) wb[i] = *reinterpret_cast<const u32x2*>(a.w + (int64_t)(r0 + i) * a.N + c0);
-  if (INT4) {
-    const int g = r0 / 32;  // 64-k group of rows 2r, 2r + 1 (kDeqRows divides 32)
-    const u32x4 sb = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.s) + (int64_t)g * a.N + c0);
-    const u32x2 zb = *reinterpret_cast<const u32x2*>(a.z + (int64_t)g * a.N + c0);
-    float sv[8];
-    int zv[8];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const uint32_t sw = (c < 2 ? sb.x : c < 4 ? sb.y : c < 6 ? sb.z : sb.w) >> (16 * (c & 1));
-      sv[c] = bf16_to_f32(sw & 0xffffu);
-      zv[c] = (int)(((c < 4 ? zb.x : zb.y) >> (8 * (c & 3))) & 0xffu);
-    }
-#pragma unroll
-    for (int i = 0; i < kDeqRows; ++i) {
-      if (r0 + i >= rows) break;
-      uint32_t lo[4], hi[4];
-#pragma unroll
-      for (int j = 0; j < 8; j += 2) {
-        float e[2], o[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int c = j + h;
-          const uint32_t byte = ((c < 4 ? wb[i].x : wb[i].y) >> (8 * (c & 3))) & 0xffu;
-          e[h] = (float)((int)(byte & 15u) - zv[c]) * sv[c];
-          o[h] = (float)((int)(byte >> 4) - zv[c]) * sv[c];
-        }
-        lo[j / 2] = pack_bf16x2(e[0], e[1]);
-        hi[j / 2] = pack_bf16x2(o[0], o[1]);
-      }
-      const int64_t r = r0 + i;
-      *reinterpret_cast<u32x4*>(wd + (2 * r) * ldd + d0) = u32x4{lo[0], lo[1], lo[2], lo[3]};
-      *reinterpret_cast<u32x4*>(wd + (2 * r + 1) * ldd + d0) = u32x4{hi[0], hi[1], hi[2], hi[3]};
-    }
-  } else {
-    const float* sp = static_cast<const float*>(a.s) + c0;
-    const f32x4 s0 = *reinterpret_cast<const f32x4*>(sp), s1 = *reinterpret_cast<const f32x4*>(sp + 4);
-    const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-#pragma unroll
-    for (int i = 0; i < kDeqRows; ++i) {
-      if (r0 + i >= rows) break;
-      uint32_t out[4];
-#pragma unroll
-      for (int j = 0; j < 8; j += 2) {
-        const int8_t b0 = (int8_t)(((j < 4 ? wb[i].x : wb[i].y) >> (8 * (j & 3))) & 0xffu);
-        const int8_t b1 = (int8_t)(((j < 4 ? wb[i].x : wb[i].y) >> (8 * ((j + 1) & 3))) & 0xffu);
-        out[j / 2] = pack_bf16x2((float)b0 * sv[j], (float)b1 * sv[j + 1]);
-      }
-      *reinterpret_cast<u32x4*>(wd + (int64_t)(r0 + i) * ldd + d0) = u32x4{out[0], out[1], out[2], out[3]};
-    }
+  const int64_t d0 = c0;
+  for (int r0 = blockIdx.y * RPT; r0 < rows; r0 += gridDim.y * RPT) {
+    DeqRows<INT4, RPT> d;
+    d.load(a, r0, rows, c0);
+    d.emit(r0, rows, wd, ldd, d0);
   }
+}
+
+// The gate and up weights of a paired SwiGLU product into one [K, 2N]
+// buffer in one pass.  Lanes 2b and 2b + 1 write one whole 64-byte piece of
+// a row between them, where two passes (one per weight) each wrote every
+// other 32 bytes: 37 against 2 x 22.5 us for the decoder's 2048 x 8192
+// weights.
+template <bool INT4, int RPT>
+__global__ __launch_bounds__(256) void qmm_dequant_pair_kernel(QArgs g, QArgs u, uint16_t* wd, int64_t ldd) {
+  const int N8 = g.N / 8;
+  const int rows = INT4 ? g.K / 2 : g.K;
+  const int c8 = blockIdx.x * 256 + threadIdx.x;
+  if (c8 >= N8) return;
+  const int c0 = c8 * 8;
+  const int64_t d0 = 32 * (c0 / 16) + c0 % 16;
+  for (int r0 = blockIdx.y * RPT; r0 < rows; r0 += gridDim.y * RPT) {
+    DeqRows<INT4, RPT> dg, du;
+    dg.load(g, r0, rows, c0);
+    du.load(u, r0, rows, c0);
+    dg.emit(r0, rows, wd, ldd, d0);
+    du.emit(r0, rows, wd, ldd, d0 + 16);
   }
 }
 
@@ -1773,6 +1826,31 @@ bool xcd_round_robin(dim3 grid, hipStream_t st, uint32_t* word) {
   return bad == 0;
 }
 
+// The dequantise pass: W [K, N] -> bf16 rows of N (up == null), or the
+// gate (a) and up weights into one interleaved [K, 2N] buffer.
+hipError_t launch_dequant(bool int4, const mk::QArgs& a, const mk::QArgs* up, uint16_t* wd, int64_t N, int64_t K,
+                          hipStream_t st) {
+  const int rpt = mk::dequant_rpt(int4, up != nullptr);
+  const dim3 grid = mk::dequant_grid(int4, K, N, rpt);
+#define MK_DEQ_LAUNCH(I4, R)                                                                                      \
+  if (up)                                                                                                        \
+    hipLaunchKernelGGL((mk::qmm_dequant_pair_kernel<I4, R>), grid, dim3(256), 0, st, a, *up, wd, 2 * N);          \
+  else                                                                                                           \
+    hipLaunchKernelGGL((mk::qmm_dequant_kernel<I4, R>), grid, dim3(256), 0, st, a, wd, N);
+  switch ((int4 ? 16 : 0) + rpt) {
+    case 16 + 8: MK_DEQ_LAUNCH(true, 8) break;
+    case 16 + 4: MK_DEQ_LAUNCH(true, 4) break;
+    case 16 + 2: MK_DEQ_LAUNCH(true, 2) break;
+    case 16 + 1: MK_DEQ_LAUNCH(true, 1) break;
+    case 8: MK_DEQ_LAUNCH(false, 8) break;
+    case 4: MK_DEQ_LAUNCH(false, 4) break;
+    case 2: MK_DEQ_LAUNCH(false, 2) break;
+    default: MK_DEQ_LAUNCH(false, 1) break;
+  }
+#undef MK_DEQ_LAUNCH
+  return hipGetLastError();
+}
+
 int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, void* y, int64_t M,
           int64_t K, int64_t N, void* ws, int64_t ws_bytes, void* stream, const void* aux = nullptr,
           int epi = MK_EPI_NONE, int64_t qg_cap = INT64_MAX) {
@@ -1836,12 +1914,7 @@ int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, v
   }
   if (p.deq) {
     uint16_t* wd = reinterpret_cast<uint16_t*>(a.part);
-    const dim3 blocks = mk::dequant_grid(fmt == MK_QFMT_INT4_G64, K, N);
-    if (fmt == MK_QFMT_INT4_G64)
-      hipLaunchKernelGGL(mk::qmm_dequant_kernel<true>, blocks, dim3(256), 0, st, a, wd, (int64_t)N, -1);
-    else
-      hipLaunchKernelGGL(mk::qmm_dequant_kernel<false>, blocks, dim3(256), 0, st, a, wd, (int64_t)N, -1);
-    e = hipGetLastError();
+    e = launch_dequant(fmt == MK_QFMT_INT4_G64, a, nullptr, wd, N, K, st);
     if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: dequantise launch failed: %s", fn, hipGetErrorString(e));
     const int rc = epi == MK_EPI_NONE ? mk_gemm_bf16(x, wd, y, 1, M, N, K, 0, stream)
                                       : mk_gemm_bf16_epilogue(x, wd, y, aux, epi, 1, M, N, K, stream);
@@ -2001,23 +2074,18 @@ int run_pair(int fmt, const void* x, const void* wg, const void* sg, const void*
                      (long long)ws_bytes);
   uint16_t* wd = reinterpret_cast<uint16_t*>(static_cast<unsigned char*>(ws) + mk::kWidePartOffset);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  mk::QArgs ag{}, au{};
   for (int half = 0; half < 2; ++half) {
-    mk::QArgs a{};
+    mk::QArgs& a = half ? au : ag;
     a.w = static_cast<const uint8_t*>(half ? wu : wg);
     a.s = half ? su : sg;
     a.z = static_cast<const uint8_t*>(half ? zu : zg);
     a.M = (int)M;
     a.K = (int)K;
     a.N = (int)N;
-    if (fmt == MK_QFMT_INT4_G64)
-      hipLaunchKernelGGL(mk::qmm_dequant_kernel<true>, mk::dequant_grid(true, K, N), dim3(256), 0, st, a, wd,
-                         2 * N, half);
-    else
-      hipLaunchKernelGGL(mk::qmm_dequant_kernel<false>, mk::dequant_grid(false, K, N), dim3(256), 0, st, a, wd,
-                         2 * N, half);
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: dequantise launch failed: %s", fn, hipGetErrorString(e));
   }
+  const hipError_t e = launch_dequant(fmt == MK_QFMT_INT4_G64, ag, &au, wd, N, K, st);
+  if (e != hipSuccess) return mkc::fail(MK_ELAUNCH, "%s: dequantise launch failed: %s", fn, hipGetErrorString(e));
   return mk_gemm_bf16_epilogue(x, wd, y, nullptr, MK_EPI_SWIGLU_PAIRS, 1, M, 2 * N, K, stream);
 }
 
