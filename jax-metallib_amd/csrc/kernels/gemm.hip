@@ -1208,7 +1208,10 @@ int check_gemm(const char* fn, const void* a, const void* b, void* c, int64_t ba
   if (K % 8 != 0 || N % 8 != 0)
     return mkc::fail(MK_EUNSUPPORTED, "%s: needs K %% 8 == 0 and N %% 8 == 0 (got K=%lld, N=%lld)",
                      fn, (long long)K, (long long)N);
-  if (M > (1 << 24) || N > (1 << 24) || K > (1 << 24) || batch > 65535 || M * K > ((int64_t)1 << 40))
+  // Every kernel's grid (64-row tiles at the smallest, times the batch for
+  // the persistent kernel's tile count) stays below 2^31 workgroups.
+  if (M > (1 << 24) || N > (1 << 24) || K > (1 << 24) || batch > 65535 || M * K > ((int64_t)1 << 40) ||
+      ((M + 63) / 64) * ((N + 63) / 64) * batch > (int64_t)INT32_MAX)
     return mkc::fail(MK_EINVAL, "%s: shape too large", fn);
   return MK_OK;
 }
