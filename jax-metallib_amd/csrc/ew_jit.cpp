@@ -301,12 +301,23 @@ std::string generate(int dtype, const mk_ew_instr* prog, int n_instr, int n_inpu
       decl += (l ? ", " : "      float ") + v + sfx + " = (" + ex + ")";
     }
     s += decl + ";\n";
+    // max, min, neg, abs, floor and ceil of bf16 values are bf16 values:
+    // their rounding would change nothing, so it is not emitted.
+    bool kept_exact = false;
+    {
+      auto ex = [&](int k) { return k >= 0 && k < 16 && exact[k]; };
+      if (rnd && (((opc == MK_EW_MAX || opc == MK_EW_MIN) && ex(in.a) && ex(in.b)) ||
+                  ((opc == MK_EW_NEG || opc == MK_EW_ABS || opc == MK_EW_FLOOR || opc == MK_EW_CEIL) && ex(in.a)))) {
+        rnd = false;
+        kept_exact = true;
+      }
+    }
     if (rnd) s += "      R2(" + v + "_0, " + v + "_1);\n";
     {
       uint32_t ib;
       memcpy(&ib, &in.imm, 4);
       auto ex_of = [&](int k) { return k >= 0 && k < 16 && exact[k]; };
-      bool e = rnd;
+      bool e = rnd || kept_exact;
       if (opc == MK_EW_LOAD) e = bf && half[in.a];
       else if (opc == MK_EW_CONST) e = (ib & 0xFFFFu) == 0u;
       else if (opc >= MK_EW_CMP_EQ && opc <= MK_EW_CMP_GE) e = true;
