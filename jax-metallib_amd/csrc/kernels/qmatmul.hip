@@ -1129,10 +1129,35 @@ __device__ __forceinline__ void lds_tr8x16(uint32_t wb, u32x2 (&o)[16]) {
       : "memory");
 }
 
-template <int S, int R>  // 32-k steps per wave; ring of R steps
+// Eight transposing byte reads (the column-split waves' 128-column slots).
+__device__ __forceinline__ void lds_tr8x8(uint32_t wb, u32x2 (&o)[8]) {
+  asm volatile(
+      "ds_read_b64_tr_b8 %0, %8\n\t"
+      "ds_read_b64_tr_b8 %1, %9\n\t"
+      "ds_read_b64_tr_b8 %2, %10\n\t"
+      "ds_read_b64_tr_b8 %3, %11\n\t"
+      "ds_read_b64_tr_b8 %4, %12\n\t"
+      "ds_read_b64_tr_b8 %5, %13\n\t"
+      "ds_read_b64_tr_b8 %6, %14\n\t"
+      "ds_read_b64_tr_b8 %7, %15\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&v"(o[4]), "=&v"(o[5]), "=&v"(o[6]), "=&v"(o[7])
+      : "v"(wb), "v"(wb ^ 16u), "v"(wb ^ 32u), "v"(wb ^ 48u), "v"(wb ^ 64u), "v"(wb ^ 80u), "v"(wb ^ 96u),
+        "v"(wb ^ 112u)
+      : "memory");
+}
+
+// CS = 2 (column split, as in the wide int4 kernel): wave w covers columns
+// [128 (w % 2), +128) of the tile over twice the k steps; a slot row is then
+// 128 B and chunk c of row r sits at position c ^ ((r / 2) % 8), which keeps
+// one transposing read (8 rows per 16-lane group, 32 rows per wave) on
+// distinct 16-byte bank groups.
+template <int S, int R, int CS = 1>  // 32-k steps per wave; ring of R steps; column split
 __global__ __launch_bounds__(8 * kWave) void int8pc_wide_kernel(QArgs a) {
-  constexpr int TN = kWideTN, NB = TN / 16;
-  constexpr int DPS = kWide8Slot / 1024;  // weight DMAs per step
+  constexpr int TN = kWideTN, TNW = TN / CS, NB = TNW / 16;
+  constexpr int SLOT = 32 * TNW;          // one 32-k step: 32 weight rows x TNW bytes
+  constexpr int DPS = SLOT / 1024;        // weight DMAs per step
+  static_assert(CS == 1 || CS == 2, "256 or 128 columns per wave");
   static_assert(R >= 1 && R <= S, "ring of at most S steps");
   extern __shared__ __align__(16) unsigned char smem[];
   const int lane = threadIdx.x & 63;
@@ -1145,7 +1170,8 @@ __global__ __launch_bounds__(8 * kWave) void int8pc_wide_kernel(QArgs a) {
   const int mrows = min(kQRows, a.M - m0);
   const int n0 = tile * TN;
   const int c = lane & 15, j = lane >> 4;
-  const int kbeg = ksi * (a.K / a.ks) + wv * 32 * S;
+  const int kbeg = ksi * (a.K / a.ks) + (wv / CS) * 32 * S;
+  const int n0w = n0 + TNW * (wv % CS);
   const size_t N = (size_t)a.N;
   unsigned char* wl = smem + wv * a.wave_lds;
 
@@ -1157,8 +1183,8 @@ __global__ __launch_bounds__(8 * kWave) void int8pc_wide_kernel(QArgs a) {
   // [S][16 rows][4 chunks of 16 B], chunk q of row r at position
   // q ^ ((r >> 2) & 3), which makes the 16-byte reads conflict-free.  Longer
   // waves keep it in registers (the LDS would not hold it).
-  constexpr bool XL = S <= 4;
-  unsigned char* xblk = wl + R * kWide8Slot;
+  constexpr bool XL = CS == 1 ? S <= 4 : S <= 8;
+  unsigned char* xblk = wl + R * SLOT;
   u32x4 xr[XL ? 1 : S];
   if constexpr (XL) {
     const int r = lane >> 2, q = (lane & 3) ^ ((lane >> 4) & 3);
@@ -1172,15 +1198,22 @@ __global__ __launch_bounds__(8 * kWave) void int8pc_wide_kernel(QArgs a) {
   }
   const uint32_t xa = lds_addr(xblk) + (uint32_t)(c * 64 + 16 * (j ^ ((c >> 2) & 3)));
   // Step t, DMA q: lane L fills slot row rr = 4 q + L / 16 (W row
-  // kbeg + 32 t + rr), position L % 16, from chunk (L % 16) ^ (rr & 15).
+  // kbeg + 32 t + rr), position L % 16, from chunk (L % 16) ^ (rr & 15);
+  // with 128-byte rows, row 8 q + L / 8, position L % 8, from chunk
+  // (L % 8) ^ ((rr / 2) % 8).
   const uint8_t* wsrc[DPS];
 #pragma unroll
   for (int q = 0; q < DPS; ++q) {
-    const int rr = 4 * q + (lane >> 4);
-    wsrc[q] = a.w + (size_t)(kbeg + rr) * N + n0 + 16 * ((lane & 15) ^ (rr & 15));
+    if constexpr (CS == 1) {
+      const int rr = 4 * q + (lane >> 4);
+      wsrc[q] = a.w + (size_t)(kbeg + rr) * N + n0w + 16 * ((lane & 15) ^ (rr & 15));
+    } else {
+      const int rr = 8 * q + (lane >> 3);
+      wsrc[q] = a.w + (size_t)(kbeg + rr) * N + n0w + 16 * ((lane & 7) ^ ((rr >> 1) & 7));
+    }
   }
   auto issue = [&](int t) {
-    unsigned char* slot = wl + (t % R) * kWide8Slot;
+    unsigned char* slot = wl + (t % R) * SLOT;
 #pragma unroll
     for (int q = 0; q < DPS; ++q) dma16(wsrc[q] + (size_t)(32 * t) * N, slot + q * 1024);
   };
@@ -1191,7 +1224,8 @@ __global__ __launch_bounds__(8 * kWave) void int8pc_wide_kernel(QArgs a) {
   // group names the two 8-byte halves of chunk b in slot row 8 j + r, at
   // position b ^ (row & 15): the address of block b is wb ^ (16 b).
   const int wrow = 8 * j + ((lane & 15) >> 1);
-  const uint32_t woff = (uint32_t)(wrow * TN + 16 * (wrow & 15) + 8 * (lane & 1));
+  const uint32_t woff = CS == 1 ? (uint32_t)(wrow * TNW + 16 * (wrow & 15) + 8 * (lane & 1))
+                                : (uint32_t)(wrow * TNW + 16 * ((wrow >> 1) & 7) + 8 * (lane & 1));
   const uint32_t ring0 = lds_addr(wl);
 
   const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0
@@ -1204,7 +1238,8 @@ __global__ __launch_bounds__(8 * kWave) void int8pc_wide_kernel(QArgs a) {
     const int issued = (R + t < S) ? R + t : S;  // steps issued before this wait
     vm_wait(DPS * (issued - (t + 1)));
     u32x2 w8[NB];
-    lds_tr8x16(ring0 + (uint32_t)((t % R) * kWide8Slot) + woff, w8);
+    if constexpr (CS == 1) lds_tr8x16(ring0 + (uint32_t)((t % R) * SLOT) + woff, w8);
+    else lds_tr8x8(ring0 + (uint32_t)((t % R) * SLOT) + woff, w8);
     // This step's slot is read: refill it.
     if (t + R < S) issue(t + R);
     u32x4 A;
@@ -1218,7 +1253,7 @@ __global__ __launch_bounds__(8 * kWave) void int8pc_wide_kernel(QArgs a) {
   f32x4 y[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) y[b] = acc[b] - 128.f * xs;
-  wide_finish<8, true>(a, smem, wl, y, tile, ksi, rb, m0, mrows, n0, c, j);
+  wide_finish<8, true, CS>(a, smem, wl, y, tile, ksi, rb, m0, mrows, n0, c, j);
 }
 
 template <int S, int R>  // 32-k steps per wave, ring of R steps (3 KB each)
@@ -1459,6 +1494,7 @@ struct QPlan {
   int wide_cs;       // wide int4 kernel: column split (1: waves split K only; 2: also the columns in halves)
   int wide_tn;       // wide int4 kernel: tile columns (256, or 128 for narrow tiles)
   int wide8_steps;   // > 0: wide int8 kernel with this many 32-k steps per wave
+  int wide8_cs;      // its column split (1: every wave over all 256 columns; 2: halves)
   int deq;           // 1: dequantise W to bf16 in the workspace, then the bf16 GEMM
   int qg;            // 1: the many-row kernel of qgemm.hip (K split ks ways)
   size_t lds_bytes;
@@ -1599,6 +1635,10 @@ bool plan_wide(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p) {
 // counter region bounds ks > 1).  A 2-step ring: 16 KB per wave, the size of
 // its y spill.  MK_QMM_WIDE=0 disables it.
 constexpr int kWide8Ring = 2;
+// Waves split over two 128-column halves (twice the k steps each), as in
+// the wide int4 kernel: M = 16 17.33 -> 16.54 us, M = 1 16.8 -> 16.0 us (one
+// box, three interleaved repeats).  MK_QMM_WIDE8_CS overrides.
+constexpr int kWide8ColumnSplit = 2;
 
 bool plan_wide8(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p) {
   const char* env = getenv("MK_QMM_WIDE");
@@ -1606,26 +1646,31 @@ bool plan_wide8(int fmt, int64_t M, int64_t K, int64_t N, QPlan* p) {
   const int ntiles = (int)(N / mk::kWideTN);
   const int rb = (int)((M + mk::kQRows - 1) / mk::kQRows);
   const int ks_env = env_int("MK_QMM_KS", 0);
+  const int cs = env_int("MK_QMM_WIDE8_CS", kWide8ColumnSplit);
+  if (cs != 1 && cs != 2) return false;
   int best = 0;
   for (int ks = 1; ks <= 8; ks *= 2) {
     if (ks_env > 0 && ks != ks_env) continue;
     if (K % ((int64_t)ks * 1024) != 0) break;
-    const int64_t S = K / ((int64_t)ks * 256);
+    const int64_t S = K * cs / ((int64_t)ks * 256);
     if (S != 4 && S != 8 && S != 16) continue;
     if (ks > 1 && (int64_t)rb * ntiles > mk::kWideCounters) break;
     best = ks;
     if ((int64_t)ntiles * rb * ks >= 192) break;
   }
   if (best == 0 || (int64_t)ntiles * rb * best < 128) return false;
-  const int64_t S = K / ((int64_t)best * 256);
-  // ring, the x block when the kernel stages x in LDS (S <= 4), the y spill
-  int wl = std::max(kWide8Ring * mk::kWide8Slot + (S <= 4 ? (int)S * 1024 : 0), mk::kQRows * mk::kWideRedStride * 4);
+  const int64_t S = K * cs / ((int64_t)best * 256);
+  // ring, the x block when the kernel stages x in LDS (S <= 4, or 8 with
+  // the column split), the y spill
+  const bool xl = cs == 1 ? S <= 4 : S <= 8;
+  int wl = std::max(kWide8Ring * mk::kWide8Slot / cs + (xl ? (int)S * 1024 : 0), mk::kQRows * mk::kWideRedStride * 4);
   wl = (wl + 255) & ~255;
   p->ks = best;
   p->nw = 8;
   p->ntiles = ntiles;
   p->rowblocks = rb;
-  p->wide8_steps = (int)(K / ((int64_t)best * 256));
+  p->wide8_steps = (int)S;
+  p->wide8_cs = cs;
   p->kwave = 32 * p->wide8_steps;
   p->wave_lds = wl;
   p->lds_bytes = (size_t)8 * wl;
@@ -1732,12 +1777,12 @@ hipError_t launch_wide(const mk::QArgs& a, const QPlan& p, hipStream_t st) {
   return hipErrorInvalidValue;
 }
 
-template <int S>
+template <int S, int CS>
 hipError_t launch_wide8(const mk::QArgs& a, const QPlan& p, hipStream_t st) {
   dim3 grid(p.ntiles * p.ks, p.rowblocks), block(8 * mk::kWave);
-  hipError_t e = lds_opt_in((const void*)mk::int8pc_wide_kernel<S, kWide8Ring>, p.lds_bytes);
+  hipError_t e = lds_opt_in((const void*)mk::int8pc_wide_kernel<S, kWide8Ring, CS>, p.lds_bytes);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((mk::int8pc_wide_kernel<S, kWide8Ring>), grid, block, p.lds_bytes, st, a);
+  hipLaunchKernelGGL((mk::int8pc_wide_kernel<S, kWide8Ring, CS>), grid, block, p.lds_bytes, st, a);
   return hipGetLastError();
 }
 
@@ -1950,10 +1995,13 @@ int run_q(int fmt, const void* x, const void* w, const void* s, const void* z, v
     }
   } else if (p.wide8_steps > 0) {
     if (p.part_bytes > 0) a.cnt = static_cast<uint32_t*>(ws);
-    switch (p.wide8_steps) {
-      case 4: e = launch_wide8<4>(a, p, st); break;
-      case 8: e = launch_wide8<8>(a, p, st); break;
-      default: e = launch_wide8<16>(a, p, st); break;
+    switch (p.wide8_steps * 4 + p.wide8_cs) {
+      case 4 * 4 + 1: e = launch_wide8<4, 1>(a, p, st); break;
+      case 8 * 4 + 1: e = launch_wide8<8, 1>(a, p, st); break;
+      case 16 * 4 + 1: e = launch_wide8<16, 1>(a, p, st); break;
+      case 4 * 4 + 2: e = launch_wide8<4, 2>(a, p, st); break;
+      case 8 * 4 + 2: e = launch_wide8<8, 2>(a, p, st); break;
+      default: e = launch_wide8<16, 2>(a, p, st); break;
     }
   } else if (p.stream_steps > 0) {
     // Split-K partials combined in the kernel (the counters live in the

@@ -436,16 +436,21 @@ WIDE8_SHAPES = [
 ]
 
 
+@pytest.mark.parametrize("cs", ["1", "2"], ids=["all-columns", "column-split"])
 @pytest.mark.parametrize("M,K,N", WIDE8_SHAPES)
-def test_int8_wide_kernel_matches_oracle(M, K, N):
+def test_int8_wide_kernel_matches_oracle(M, K, N, cs, monkeypatch):
+    """Both wave layouts of the wide int8 kernel (MK_QMM_WIDE8_CS: every
+    wave over all 256 columns, or waves split over two 128-column halves
+    with twice the k steps) against the C oracle."""
     ops = _ops()
+    monkeypatch.setenv("MK_QMM_WIDE8_CS", cs)
     rng = np.random.default_rng(11 * M + K + N)
     x, w, s = quant.make_int8_case(rng, M, K, N)
-    print(f"int8 wide case M={M} K={K} N={N}", flush=True)
+    print(f"int8 wide case M={M} K={K} N={N} cs={cs}", flush=True)
     y = ops.int8_pc_matmul(dev_bf16(x), dev(w), dev(s))
     torch.cuda.synchronize()
     ref = cport.int8_pc_matmul(x, w, s)
-    assert_rel_close(host_bf16(y), ref, BF16_RTOL, f"int8 wide {M}x{K}x{N}")
+    assert_rel_close(host_bf16(y), ref, BF16_RTOL, f"int8 wide {M}x{K}x{N} cs={cs}")
 
 
 def test_int8_wide_kernel_is_planned_and_deterministic(monkeypatch):
