@@ -248,8 +248,10 @@ int mk_gemm_bf16_autotune(const void* a, const void* b, void* c, const void* aux
  * MK_GEMM_ROUTE_DEFAULT when it has none. */
 int mk_gemm_tuned_route(int64_t batch, int64_t M, int64_t N, int64_t K, int epilogue, int out_f32);
 
-/* The route table as a text file: a header line "mk-gemm-autotune 1",
- * then one line per entry, "<arch> <CUs> <batch> <M> <N> <K>
+/* The route table as a text file: the header line that
+ * mk_gemm_autotune_header returns ("mk-gemm-autotune 1 build <stamp>",
+ * the stamp that of this library's build, so a table measured against
+ * other kernels is refused), then one line per entry, "<arch> <CUs> <batch> <M> <N> <K>
  * <epilogue class> <out_f32> <route> <us>".  save writes it atomically
  * (a temporary file renamed) and returns the number of entries; load
  * merges a file's entries into the table and returns their number.  Both
@@ -259,6 +261,7 @@ int mk_gemm_tuned_route(int64_t batch, int64_t M, int64_t N, int64_t K, int epil
 int mk_gemm_autotune_save(const char* path);
 int mk_gemm_autotune_load(const char* path);
 void mk_gemm_autotune_clear(void);
+const char* mk_gemm_autotune_header(void);
 
 /* mk_dot_general: the dot_general cases the tiled GEMMs do not take,
  * with the reference's semantics (HandleDotGeneral,

@@ -1538,7 +1538,19 @@ std::string tune_key(const std::string& tag, int64_t batch, int64_t M, int64_t N
   return buf;
 }
 
-constexpr const char* kTuneHeader = "mk-gemm-autotune 1";
+// The table file's first line: the format version and this library's build
+// stamp.  A table measured against another build of these kernels is refused,
+// so a rebuilt library re-measures instead of following stale choices.
+const std::string& tune_header() {
+  static const std::string h = [] {
+    std::string s = "mk-gemm-autotune 1 build ";
+    for (const char* p = __DATE__ " " __TIME__; *p; ++p)  // "Dec  2 2026 10:11:12" -> "Dec_2_2026_10:11:12"
+      if (*p != ' ') s += *p;
+      else if (s.back() != '_') s += '_';
+    return s;
+  }();
+  return h;
+}
 
 }  // namespace
 
@@ -1619,7 +1631,7 @@ extern "C" int mk_gemm_autotune_save(const char* path) {
   int n = 0;
   {
     std::lock_guard<std::mutex> g(g_tune_mu);
-    fprintf(f, "%s\n", kTuneHeader);
+    fprintf(f, "%s\n", tune_header().c_str());
     for (const auto& [k, v] : g_tune) {
       fprintf(f, "%s %d %.3f\n", k.c_str(), v.route, v.us);
       ++n;
@@ -1642,10 +1654,12 @@ extern "C" int mk_gemm_autotune_load(const char* path) {
   FILE* f = fopen(path, "r");
   if (!f) return -mkc::fail(MK_EINVAL, "mk_gemm_autotune_load: cannot read %s", path);
   char line[256];
-  if (!fgets(line, sizeof line, f) || strncmp(line, kTuneHeader, strlen(kTuneHeader)) != 0 ||
-      (line[strlen(kTuneHeader)] != '\n' && line[strlen(kTuneHeader)] != '\0')) {
+  const std::string& hdr = tune_header();
+  if (!fgets(line, sizeof line, f) || strncmp(line, hdr.c_str(), hdr.size()) != 0 ||
+      (line[hdr.size()] != '\n' && line[hdr.size()] != '\0')) {
     fclose(f);
-    return -mkc::fail(MK_EINVAL, "mk_gemm_autotune_load: %s is not a route table (header \"%s\")", path, kTuneHeader);
+    return -mkc::fail(MK_EINVAL, "mk_gemm_autotune_load: %s is not a route table of this build (header \"%s\")",
+                      path, hdr.c_str());
   }
   std::vector<std::pair<std::string, TuneEntry>> got;
   int lineno = 1;
@@ -1671,6 +1685,8 @@ extern "C" int mk_gemm_autotune_load(const char* path) {
   for (auto& [key, v] : got) g_tune[key] = v;
   return (int)got.size();
 }
+
+extern "C" const char* mk_gemm_autotune_header(void) { return tune_header().c_str(); }
 
 extern "C" void mk_gemm_autotune_clear(void) {
   std::lock_guard<std::mutex> g(g_tune_mu);

@@ -59,6 +59,7 @@ SIGNATURES = {
     "mk_gemm_autotune_save": (_i32, [ctypes.c_char_p]),
     "mk_gemm_autotune_load": (_i32, [ctypes.c_char_p]),
     "mk_gemm_autotune_clear": (None, []),
+    "mk_gemm_autotune_header": (ctypes.c_char_p, []),
     "mk_int4g64_matmul_epilogue_bf16": (_i32, [_p, _p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _p, _i64, _p]),
     "mk_int8pc_matmul_epilogue_bf16": (_i32, [_p, _p, _p, _p, _p, _i32, _i64, _i64, _i64, _p, _i64, _p]),
     "mk_qmatmul_swiglu_pair_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64]),

@@ -126,10 +126,13 @@ def test_gemm_routes_fit_and_reject_on_host():
 def test_gemm_route_table_file_round_trip(tmp_path):
     """The route table's text file: load merges entries (any device's), save
     writes them back byte for byte (sorted by key), and a file with another
-    header or a malformed line is refused with the table unchanged."""
+    header (another format, or a table measured against another build of the
+    library) or a malformed line is refused with the table unchanged."""
     L = _lib.lib()
     L.mk_gemm_autotune_clear()
-    text = ("mk-gemm-autotune 1\n"
+    hdr = L.mk_gemm_autotune_header().decode()
+    assert hdr.startswith("mk-gemm-autotune 1 build ") and " " not in hdr[len("mk-gemm-autotune 1 build "):]
+    text = (hdr + "\n"
             "gfx950 256 1 4096 4096 4096 0 0 2 112.500\n"
             "gfx950 256 16 2048 2048 128 0 0 3 50.125\n"
             "gfx942 304 1 384 640 64 1 0 4 9.000\n")
@@ -139,11 +142,15 @@ def test_gemm_route_table_file_round_trip(tmp_path):
     out = tmp_path / "saved.txt"
     assert L.mk_gemm_autotune_save(str(out).encode()) == 3
     lines = out.read_text().splitlines()
-    assert lines[0] == "mk-gemm-autotune 1" and sorted(lines[1:]) == lines[1:]
+    assert lines[0] == hdr and sorted(lines[1:]) == lines[1:]
     assert set(lines[1:]) == set(text.splitlines()[1:])
-    for bad in ("mk-gemm-autotune 2\n", "mk-gemm-autotune 1\ngfx950 256 1 64 64 64 0 0 9 1.0\n",
-                "mk-gemm-autotune 1\ngfx950 256 1 64 64 0 0 2 1.0\n",
-                "mk-gemm-autotune 1\ngfx950 256 1 64 64 64 0 0 2 1.0 extra\n"):
+    good = "gfx950 256 1 64 64 64 0 0 2 1.0\n"
+    for bad in ("mk-gemm-autotune 1\n" + good,  # no build stamp
+                "mk-gemm-autotune 1 build Jan_1_2000_00:00:00\n" + good,  # another build's table
+                hdr + "X\n" + good, "mk-gemm-autotune 2\n",
+                hdr + "\ngfx950 256 1 64 64 64 0 0 9 1.0\n",
+                hdr + "\ngfx950 256 1 64 64 0 0 2 1.0\n",
+                hdr + "\ngfx950 256 1 64 64 64 0 0 2 1.0 extra\n"):
         f = tmp_path / "bad.txt"
         f.write_text(bad)
         assert L.mk_gemm_autotune_load(str(f).encode()) == -_lib.MK_EINVAL, bad
