@@ -100,9 +100,17 @@ def test_rmsnorm_f32_and_bf16(shape):
     assert_rel_close(yb, ref, BF16_RTOL, f"rmsnorm bf16 {shape}")
 
 
+@pytest.mark.parametrize("wave", ["1", "0"])
 @pytest.mark.parametrize("shape,seed", [((512, 37), 0), ((300, 1), 0), ((8, 2049), 3), ((64, 300), 5),
-                                        ((16, 8192), 6), ((4, 20000), 7)])
-def test_argmax_special_values_bit_exact(shape, seed):
+                                        ((16, 8192), 6), ((4, 20000), 7), ((33, 1576), 8), ((5, 16384), 9),
+                                        ((70, 8), 10)])
+def test_argmax_special_values_bit_exact(shape, seed, wave, monkeypatch):
+    """Both argmax kernels (one wave per row, and MK_ROW_WAVE=0's workgroup
+    per row) against the oracle on rows dense with NaN, +-inf and +-0;
+    aligned shapes of up to 16 vectors per lane (32 for bf16: 16384
+    columns) take the wave kernel, with a partly filled last vector row at
+    1576 columns."""
+    monkeypatch.setenv("MK_ROW_WAVE", wave)
     ops = _ops()
     x = _edge(shape, seed)
     got = ops.argmax(dev(x)).cpu().numpy()
@@ -149,6 +157,26 @@ def test_reduce_sum_max(shape):
     np.testing.assert_array_equal(m, rowops.reduce_max(x).astype(np.float32))
 
 
+@pytest.mark.parametrize("wave", ["1", "0"])
+@pytest.mark.parametrize("shape,seed", [((64, 300), 12), ((33, 1576), 13), ((16, 8192), 14), ((5, 16384), 15)])
+def test_reduce_max_min_special_values(shape, seed, wave, monkeypatch):
+    """Row max and min of both kernels on rows dense with NaN, +-inf and
+    +-0, exactly (max puts +0 above -0, min -0 below +0)."""
+    monkeypatch.setenv("MK_ROW_WAVE", wave)
+    ops = _ops()
+    x = _edge(shape, seed)
+    for xs, host in ((dev(x), x), (dev_bf16(obf.f32_to_bf16_bits(x)), None)):
+        ref_in = x if host is not None else obf.bf16_bits_to_f32(obf.f32_to_bf16_bits(x))
+        for op, ref in (("max", rowops.reduce_max(ref_in)), ("min", -rowops.reduce_max(-ref_in))):
+            got = ops.reduce_lastdim(xs, op)
+            got = got.cpu().numpy() if host is not None else obf.bf16_bits_to_f32(host_bf16_bits(got))
+            ref = ref.astype(np.float32)
+            assert np.array_equal(np.isnan(got), np.isnan(ref)), (op, shape)
+            ok = ~np.isnan(ref)
+            np.testing.assert_array_equal(got[ok], ref[ok], err_msg=f"{op} {shape}")
+            np.testing.assert_array_equal(np.signbit(got[ok]), np.signbit(ref[ok]), err_msg=f"{op} sign {shape}")
+
+
 def test_reduce_max_nan_and_signed_zero():
     ops = _ops()
     x = np.array([[1.0, np.nan, 2.0], [-0.0, 0.0, -1.0], [-0.0, -0.0, -2.0], [1.0, 2.0, 3.0]], np.float32)
@@ -163,8 +191,19 @@ def test_reduce_max_nan_and_signed_zero():
 def test_more_rows_than_one_launch_row_each(op):
     """More rows than the launch gives workgroups (2^20): rows stride over the
     grid, and the last rows are computed like the first."""
+    _more_rows(op, (1 << 20) + 37)
+
+
+def test_argmax_more_rows_than_the_wave_grid():
+    """argmax over more rows than the one-wave-per-row launch covers (4 x
+    2^20 waves): waves stride over rows, and the last rows are computed like
+    the first."""
+    _more_rows("argmax", 4 * (1 << 20) + 37)
+
+
+def _more_rows(op, rows):
     ops = _ops()
-    rows, cols = (1 << 20) + 37, 16
+    cols = 16
     x = _x((rows, cols), 21)
     print(f"rows case {op} {rows}x{cols}", flush=True)
     xd = dev(x)
