@@ -883,6 +883,7 @@ def main():
             r = bench_rowop(torch, ops, kind, dt, max(50, args.steps // 10), 5)
             log(f"[bench] {kind} {dt} 8192x8192: {r['sec_per_call'] * 1e6:.1f} us, {r['gbs']:.0f} GB/s")
             prof = (f"mk_ew_jit_chain6_{dt}_8192x8192" if kind == "chain6"
+                    else f"row_wave_kernel_{kind}_{dt}_8192x8192" if (kind, dt) == ("argmax", "bf16")
                     else f"row_cached_kernel_{kind}_{dt}_8192x8192")
             entry = _hbm_entry(r["gbs"], r["sec_per_call"] * 1e6, profile=prof)
             if not args.no_cpu:
