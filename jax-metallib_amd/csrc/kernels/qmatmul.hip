@@ -944,6 +944,15 @@ __global__ __launch_bounds__(NW * kWave) void int4g64_wide_kernel(QArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
+  // Column split: the second wave of each SIMD (wv >= NW / 2) issues its
+  // first loads at a raised priority (dropped after them).  Without it those
+  // waves start their streams 0.6 us after the first four and end their K
+  // loop 1 us later; the age-ordered issue of the K loop then favours the
+  // first four, which evens them out (headline shape 11.31 -> 11.05 us on
+  // one box, 11.35-11.44 -> 11.16-11.28 on another, same bits; the
+  // 128-column tiles measured 0.8 % slower with it).
+  constexpr bool PR = CS == 2;
+  if (PR && __builtin_amdgcn_readfirstlane(wv) >= NW / 2) __builtin_amdgcn_s_setprio(1);
   const uint32_t L = xcd_logical_id(blockIdx.x, gridDim.x);
   const int tile = (int)(L / (uint32_t)a.ks);
   const int ksi = (int)(L - (uint32_t)tile * a.ks);
@@ -1015,6 +1024,7 @@ __global__ __launch_bounds__(NW * kWave) void int4g64_wide_kernel(QArgs a) {
   };
 #pragma unroll
   for (int t = 0; t < R; ++t) issue(t);
+  if (PR) __builtin_amdgcn_s_setprio(0);
 
   // Per-lane LDS offsets.  Transposing weight read of lane (c, j) for the
   // column-block pair (b, b+1), b even: lane pair (2r, 2r+1) of each 16-lane
@@ -1162,6 +1172,10 @@ __global__ __launch_bounds__(8 * kWave) void int8pc_wide_kernel(QArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
+  // Waves 4-7 issue their first loads at a raised priority, as in the int4
+  // kernel (M = 16, K = 4096: N = 14336 16.68-16.71 -> 16.52-16.68 us, N =
+  // 8192 9.59-9.64 -> 9.53-9.56 us; same bits).
+  if (__builtin_amdgcn_readfirstlane(wv) >= 4) __builtin_amdgcn_s_setprio(1);
   const uint32_t L = xcd_logical_id(blockIdx.x, gridDim.x);
   const int tile = (int)(L / (uint32_t)a.ks);
   const int ksi = (int)(L - (uint32_t)tile * a.ks);
@@ -1219,6 +1233,7 @@ __global__ __launch_bounds__(8 * kWave) void int8pc_wide_kernel(QArgs a) {
   };
 #pragma unroll
   for (int t = 0; t < R; ++t) issue(t);
+  __builtin_amdgcn_s_setprio(0);
 
   // Transposing read of lane (c, j): lane pair (2r, 2r + 1) of the 16-lane
   // group names the two 8-byte halves of chunk b in slot row 8 j + r, at
