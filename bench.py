@@ -482,37 +482,130 @@ def available_cores():
     return cores
 
 
-def cpu_baseline_int4(target_s, M=16, K=4096, N=14336):
-    """Time the oracle's C port (OpenMP, every available core) on a column
-    slice of the headline case, sized to roughly target_s seconds; report
-    GB/s of the same algorithmic bytes per processed column."""
+def cpu_baseline_qmm(fmt, target_s, M=16, K=4096, N=14336, unit="GB/s"):
+    """Time the oracle's C port of the int4 g64 / int8 per-channel matmul
+    (OpenMP, every available core) on a column slice of the [M, K] x [K, N]
+    case, sized to roughly target_s seconds; report the GPU line's unit:
+    GB/s of its algorithmic bytes per processed column, or TFLOP/s."""
     from oracle import cport, quant
 
     cores = available_cores()
     cport.threads(cores)
     rng = np.random.default_rng(0)
-    x, packed, s, z = quant.make_int4_case(rng, M, K, N)
-    ncols = 256
+    if fmt == "int4":
+        args = quant.make_int4_case(rng, M, K, N)
+        call, nbytes = cport.int4_g64_matmul, int4_bytes(M, K, N)
+    else:
+        args = quant.make_int8_case(rng, M, K, N)
+        call, nbytes = cport.int8_pc_matmul, int8_bytes(M, K, N)
+    ncols = 64
     t0 = time.perf_counter()
-    cport.int4_g64_matmul(x, packed, s, z, n_range=(0, ncols))
+    call(*args, n_range=(0, ncols))
     t1 = time.perf_counter() - t0
-    ncols = int(min(N, max(256, ncols * target_s / max(t1, 1e-6))))
+    ncols = int(min(N, max(64, ncols * target_s / max(t1, 1e-6))))
     ncols -= ncols % 64
     ncols = max(ncols, 64)
     reps = 0
     t0 = time.perf_counter()
     while True:
-        cport.int4_g64_matmul(x, packed, s, z, n_range=(0, ncols))
+        call(*args, n_range=(0, ncols))
         reps += 1
         el = time.perf_counter() - t0
         if el >= target_s:
             break
     per_call = el / reps
-    frac = ncols / N
-    gbs = int4_bytes(M, K, N) * frac / per_call / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"oracle/c int4 g64 M={M} K={K}, columns [0,{ncols}) of N={N}, "
+    if unit == "GB/s":
+        value = nbytes * (ncols / N) / per_call / 1e9
+    else:
+        value = 2.0 * M * K * ncols / per_call / 1e12
+    name = "int4 g64" if fmt == "int4" else "int8 per-channel"
+    return {"value": round(value, 4 if unit != "GB/s" else 3), "unit": unit, "cores": cores, "kind": "port",
+            "sample": f"oracle/c {name} M={M} K={K}, columns [0,{ncols}) of N={N}, "
                       f"{reps} run(s), {el:.1f}s, OpenMP threads={cores}"}
+
+
+def cpu_baseline_int4(target_s, M=16, K=4096, N=14336):
+    """The headline's CPU baseline: cpu_baseline_qmm for int4 g64 in GB/s."""
+    return cpu_baseline_qmm("int4", target_s, M, K, N)
+
+
+def cpu_baseline_bmm(target_s, batch=16, M=2048, K=128, N=2048):
+    """The C port's bf16 GEMM on a row slice of one batch of the batched
+    product; GB/s of the GPU line's algorithmic bytes (A + B + C) per
+    processed output row."""
+    from oracle import cport
+    from oracle.bf16 import f32_to_bf16_bits
+
+    cores = available_cores()
+    cport.threads(cores)
+    rng = np.random.default_rng(0)
+    a = f32_to_bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    b = f32_to_bf16_bits(rng.standard_normal((K, N)).astype(np.float32))
+    rows = cores
+    t0 = time.perf_counter()
+    cport.gemm_bf16(a, b, m_range=(0, rows))
+    t1 = time.perf_counter() - t0
+    rows = int(min(M, max(cores, rows * target_s / max(t1, 1e-6))))
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        cport.gemm_bf16(a, b, m_range=(0, rows))
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= target_s:
+            break
+    line_bytes = batch * (M * K + K * N + M * N) * 2
+    gbs = line_bytes * rows / (batch * M) / (el / reps) / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"oracle/c bf16 GEMM [{M},{K}] x [{K},{N}] (one of {batch} batches), rows [0,{rows}), "
+                      f"{reps} run(s), {el:.1f}s, OpenMP threads={cores}"}
+
+
+def cpu_baseline_gemm_f32(target_s, n=2048):
+    """The C port's f32 GEMM on a row slice of the n^3 product; TFLOP/s."""
+    from oracle import cport
+
+    cores = available_cores()
+    cport.threads(cores)
+    rng = np.random.default_rng(0)
+    a = rng.standard_normal((n, n)).astype(np.float32)
+    b = rng.standard_normal((n, n)).astype(np.float32)
+    rows = cores
+    t0 = time.perf_counter()
+    cport.gemm_f32(a, b, m_range=(0, rows))
+    t1 = time.perf_counter() - t0
+    rows = int(min(n, max(cores, rows * target_s / max(t1, 1e-6))))
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        cport.gemm_f32(a, b, m_range=(0, rows))
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= target_s:
+            break
+    tflops = 2.0 * rows * n * n / (el / reps) / 1e12
+    return {"value": round(tflops, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"oracle/c f32 GEMM K={n} N={n}, rows [0,{rows}) of M={n}, {reps} run(s), {el:.1f}s, "
+                      f"OpenMP threads={cores}"}
+
+
+def cpu_baseline_decoder(layers=4, S=2048, hidden=2048, heads=16, head_dim=128, ffn=8192):
+    """The decoder oracle (oracle/decoder.py: float64 numpy, bf16 roundings
+    where the plugin writes bf16) on one layer of one S-token sequence, every
+    position; tokens/s of the `layers`-layer forward (each token passes every
+    layer).  A single timed call: it takes seconds."""
+    from mi355x import synthetic
+    from oracle import decoder as odec
+    from oracle.bf16 import bf16_bits_to_f32
+
+    cores = available_cores()
+    rng = np.random.default_rng(0)
+    x, w, _, _ = synthetic.decoder_layer_case(rng, 1, S, hidden, heads, head_dim, ffn)
+    x0 = bf16_bits_to_f32(x).reshape(S, hidden)
+    t0 = time.perf_counter()
+    odec.layer_rows(x0, np.arange(S), w, heads, head_dim)
+    el = time.perf_counter() - t0
+    return {"value": round(S / (el * layers), 2), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"oracle/decoder.py (float64 numpy, BLAS threads as the host sets them) one layer of one "
+                      f"{S}-token sequence, {el:.1f}s, scaled to {layers} layers"}
 
 
 def cpu_baseline_gemm(target_s, M=4096, K=4096, N=4096):
@@ -781,6 +874,8 @@ def main():
                          "unit": "GB/s", "frac": round(r8["gbs"] / HBM_PEAK_GBS, 4), "traffic": int8_traffic,
                          "traffic_note": int8_note},
         }
+        if not args.no_cpu:
+            secondary["int8_pc_dequant_matmul_M16"]["cpu_baseline"] = cpu_baseline_qmm("int8", args.cpu_row_seconds)
 
     def want(name):
         return not only or name in only
@@ -818,6 +913,9 @@ def main():
                             "kernel": f"qmm_dequant_kernel<{'true' if fmt == 'int4' else 'false'}>",
                             "algorithmic_bytes": 149553152 if fmt == "int4" else 176218112,
                             "traffic": dt, "traffic_note": dn}
+                if not args.no_cpu:
+                    entry["cpu_baseline"] = cpu_baseline_qmm(fmt, args.cpu_row_seconds, M=M,
+                                                             unit="GB/s" if M == 1 else "TFLOP/s")
                 secondary[f"{fmt}_dequant_matmul_M{M}"] = entry
 
     if want("shard"):
@@ -831,6 +929,9 @@ def main():
                 r["gbs"], r["sec_per_call"] * 1e6,
                 {"what": "one of 8 GPUs' share of the headline shape when sharded by N (K=4096, N=1792)"},
                 profile=f"{'int4g64' if fmt == 'int4' else 'int8pc'}_shard_M16_K4096_N1792")
+            if not args.no_cpu:
+                secondary[f"{fmt}_dequant_matmul_M16_shard_N1792"]["cpu_baseline"] = cpu_baseline_qmm(
+                    fmt, args.cpu_row_seconds, M=16, N=1792)
 
     if want("gemm"):
         log("[bench] bf16 GEMM 4096^3 ...")
@@ -860,6 +961,8 @@ def main():
         secondary["bf16_bmm_16x2048x128x2048"] = _hbm_entry(gbs, rb["sec_per_call"] * 1e6,
                                                            {"tflops": round(rb["tflops"], 2)},
                                                            profile="gemm_bf16_batched_16x2048x128x2048")
+        if not args.no_cpu:
+            secondary["bf16_bmm_16x2048x128x2048"]["cpu_baseline"] = cpu_baseline_bmm(args.cpu_row_seconds)
         rf = bench_gemm_f32(torch, ops, max(50, args.steps // 20), 5)
         log(f"[bench] f32 gemm 2048^3: {rf['sec_per_call'] * 1e6:.1f} us, {rf['tflops']:.1f} TFLOP/s")
         ft, fnote = traffic_from_profiles("gemm_f32_kernel_2048")
@@ -868,6 +971,8 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(rf["tflops"], 2), "peak": 157.3,
                          "unit": "TFLOP/s", "frac": round(rf["tflops"] / 157.3, 4), "traffic": ft,
                          "traffic_note": fnote}}
+        if not args.no_cpu:
+            secondary["f32_gemm_2048"]["cpu_baseline"] = cpu_baseline_gemm_f32(args.cpu_row_seconds)
     if want("decoder"):
         rd = bench_decoder(torch)
         log(f"[bench] decoder forward: {rd['ms']:.3f} ms, {rd['tokens_per_s']:.0f} tokens/s, {rd['tflops']:.1f} TFLOP/s")
@@ -876,6 +981,10 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(rd["tflops"], 2), "peak": BF16_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(rd["tflops"] / BF16_PEAK_TFLOPS, 4), "traffic": None},
             "config": rd["config"]}
+        if not args.no_cpu:
+            cpu_dec = cpu_baseline_decoder()
+            log(f"[bench] cpu decoder: {cpu_dec['value']} tokens/s")
+            secondary["llama_decoder_forward_4x2048_b4s2048_int4"]["cpu_baseline"] = cpu_dec
     for kind in ("softmax", "rmsnorm", "argmax", "chain6"):
         if not want(kind):
             continue
@@ -917,6 +1026,11 @@ def main():
                 "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                              "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None},
                 "plan_steps": st["steps"]}
+            if not args.no_cpu:
+                # The same workload as the hand-fused line: its CPU figure.
+                hand = secondary.get("llama_decoder_forward_4x2048_b4s2048_int4", {})
+                secondary["llama_decoder_forward_jit_4x2048_b4s2048_int4"]["cpu_baseline"] = (
+                    hand.get("cpu_baseline") or cpu_baseline_decoder())
 
     cpu = None
     if not args.no_cpu:

@@ -12,6 +12,8 @@
  *   int8 pc:   Y = s[n] * sum_k X[m,k] W[k,n]  (f32 accumulation).
  *   bf16 GEMM: C = A @ B with f32 accumulation (reference
  *              ops/binary_ops.mm:775-782: bf16 x bf16 -> f32 preferred type).
+ *   f32 GEMM:  C = A @ B in f32, k ascending (the reference's f32 dot,
+ *              ops/binary_ops.mm:775-782, at f32 throughout).
  *   argmax:    first NaN, else first maximum, -0 == +0
  *              (reference ops/reduction_ops.mm:1478-1536).
  *   softmax:   exp(x - max) / sum over the last axis; a NaN or infinite row
@@ -137,6 +139,22 @@ void orc_gemm_bf16(const uint16_t* a, const uint16_t* b, int64_t M, int64_t K, i
             float av = bf16_to_f32(a[m * K + k]);
             const uint16_t* br = b + k * N;
             for (int64_t n = 0; n < N; ++n) cr[n] += av * bf16_to_f32(br[n]);
+        }
+    }
+}
+
+/* C[M,N] (f32) = A[M,K] (f32) @ B[K,N] (f32), rows m in [m0, m1). */
+void orc_gemm_f32(const float* a, const float* b, int64_t M, int64_t K, int64_t N,
+                  int64_t m0, int64_t m1, float* c) {
+    (void)M;
+    #pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t m = m0; m < m1; ++m) {
+        float* cr = c + m * N;
+        for (int64_t n = 0; n < N; ++n) cr[n] = 0.f;
+        for (int64_t k = 0; k < K; ++k) {
+            const float av = a[m * K + k];
+            const float* br = b + k * N;
+            for (int64_t n = 0; n < N; ++n) cr[n] += av * br[n];
         }
     }
 }

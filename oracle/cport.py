@@ -23,6 +23,7 @@ def lib():
         L.orc_int4_g64_matmul.argtypes = [p, p, p, p, i64, i64, i64, i64, i64, p]
         L.orc_int8_pc_matmul.argtypes = [p, p, p, i64, i64, i64, i64, i64, p]
         L.orc_gemm_bf16.argtypes = [p, p, i64, i64, i64, i64, i64, p]
+        L.orc_gemm_f32.argtypes = [p, p, i64, i64, i64, i64, i64, p]
         L.orc_argmax_f32.argtypes = [p, i64, i64, p]
         L.orc_argmax_bf16.argtypes = [p, i64, i64, p]
         L.orc_softmax_f32.argtypes = [p, i64, i64, i64, p]
@@ -73,6 +74,17 @@ def gemm_bf16(a_bits, b_bits, m_range=None):
     a = np.ascontiguousarray(a_bits)
     b = np.ascontiguousarray(b_bits)
     lib().orc_gemm_bf16(_ptr(a), _ptr(b), M, K, N, m0, m1, _ptr(c))
+    return c
+
+
+def gemm_f32(a, b, m_range=None):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    M, K = a.shape
+    N = b.shape[1]
+    m0, m1 = m_range or (0, M)
+    c = np.zeros((M, N), dtype=np.float32)
+    lib().orc_gemm_f32(_ptr(a), _ptr(b), M, K, N, m0, m1, _ptr(c))
     return c
 
 

@@ -508,6 +508,27 @@ def test_cport_gemm_bf16_closed_forms():
     np.testing.assert_array_equal(c, K * np.outer(np.arange(5), np.arange(3)))
 
 
+def test_cport_gemm_f32_pins():
+    """The C port's f32 GEMM (the f32 GEMM line's CPU baseline): against
+    float64 within the f32 accumulation bound on a ragged shape, a row slice
+    equal to the full product's rows, A @ I == A exactly, and the
+    row-index x column-index closed form K m n (exact in f32), which a
+    transposed operand or a wrong stride fails."""
+    cport = _cport()
+    rng = np.random.default_rng(35)
+    M, K, N = 37, 130, 45
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    b = rng.standard_normal((K, N)).astype(np.float32)
+    _close_f32_accum(cport.gemm_f32(a, b), a.astype(np.float64) @ b.astype(np.float64), K)
+    part = cport.gemm_f32(a, b, m_range=(2, M - 3))
+    np.testing.assert_array_equal(part[2:M - 3], cport.gemm_f32(a, b)[2:M - 3])
+    np.testing.assert_array_equal(cport.gemm_f32(a, np.eye(K, dtype=np.float32)), a)
+    Kc = 24
+    am = np.repeat(np.arange(6, dtype=np.float32)[:, None], Kc, axis=1)
+    bn = np.repeat(np.arange(5, dtype=np.float32)[None, :], Kc, axis=0)
+    np.testing.assert_array_equal(cport.gemm_f32(am, bn), Kc * np.outer(np.arange(6), np.arange(5)))
+
+
 @pytest.mark.parametrize("shape,seed", [((512, 37), 0), ((300, 1), 0), ((8, 2049), 3), ((64, 300), 5)])
 def test_cport_argmax_matches_brute(shape, seed):
     cport = _cport()
