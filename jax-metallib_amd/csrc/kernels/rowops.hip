@@ -277,7 +277,7 @@ __global__ __launch_bounds__(kRowThreads) void row_wave_kernel(RowArgs a) {
 
 // Register-cached row kernel: the row is covered by 256 threads x VPT vectors
 // (VPT * 256 * Vec::N >= cols, cols % Vec::N == 0, rows 16-byte aligned).
-template <typename T, int OP, int VPT>
+template <typename T, int OP, int VPT, bool GE = sizeof(T) == 4>
 __global__ __launch_bounds__(kRowThreads) void row_cached_kernel(RowArgs a) {
   using V = Vec<T>;
   constexpr int E = V::N;
@@ -296,6 +296,17 @@ __global__ __launch_bounds__(kRowThreads) void row_cached_kernel(RowArgs a) {
     const int64_t c = (int64_t)(q * kRowThreads + tid) * E;
     ok[q] = c < a.cols;
     if (ok[q]) V::load(a.x, base + c, v[q]);
+  }
+  // RMSNorm, GE: the weight g is loaded with the row, so its latency is not
+  // exposed after the reduction.  8192^2 f32: 100.4 -> 91.6 us.  bf16 keeps
+  // the load after the reduction: loaded early it costs VGPRs and waves per
+  // SIMD (47.6 against 49.0 us packed, 52.9 us unpacked).
+  u32x4 graw[OP == ROW_RMSNORM ? VPT : 1];
+  if constexpr (OP == ROW_RMSNORM && GE) {
+#pragma unroll
+    for (int q = 0; q < VPT; ++q)
+      if (ok[q])
+        graw[q] = *reinterpret_cast<const u32x4*>(static_cast<const T*>(a.g) + (int64_t)(q * kRowThreads + tid) * E);
   }
 
   if (OP == ROW_SOFTMAX) {
@@ -354,10 +365,9 @@ __global__ __launch_bounds__(kRowThreads) void row_cached_kernel(RowArgs a) {
     for (int q = 0; q < VPT; ++q)
       if (ok[q]) {
         const int64_t c = (int64_t)(q * kRowThreads + tid) * E;
-        float gv[E];
-        V::load(a.g, c, gv);
+        if constexpr (!GE) graw[q] = *reinterpret_cast<const u32x4*>(static_cast<const T*>(a.g) + c);
 #pragma unroll
-        for (int e = 0; e < E; ++e) v[q][e] = v[q][e] * r * gv[e];
+        for (int e = 0; e < E; ++e) v[q][e] = v[q][e] * r * row_elem<T>(graw[q], e);
         V::store(a.y, base + c, v[q]);
       }
   } else if (OP == ROW_ARGMAX) {
