@@ -820,6 +820,18 @@ __device__ __forceinline__ void wide_finish(const QArgs& a, unsigned char* smem,
   constexpr int IT = 16 * QPR / (NW * kWave);     // output quads per thread
   const size_t N = (size_t)a.N;
   const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+  // FMT8: the per-channel scales of this thread's output quads, loaded now
+  // so that their latency hides under the wave sum and the exchange instead
+  // of following the last arriver's partial loads (int8 headline shape
+  // 16.52-16.72 -> 16.19-16.27 us).
+  f32x4 scl[FMT8 ? IT : 1];
+  if constexpr (FMT8) {
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int q = threadIdx.x + NW * kWave * it;
+      scl[it] = *reinterpret_cast<const f32x4*>(static_cast<const float*>(a.s) + n0 + 4 * (q % QPR));
+    }
+  }
   // Sum the waves: each spills y as [16 m][TN] f32 (padded rows; its own
   // columns only) into its own region; lane (c, j) holds column
   // col0 + 16b + c, rows 4j..4j+3.
@@ -915,7 +927,7 @@ __device__ __forceinline__ void wide_finish(const QArgs& a, unsigned char* smem,
     const int q = threadIdx.x + NW * kWave * it;
     const int m = q / QPR, n = n0 + 4 * (q % QPR);
     if (m >= mrows) continue;
-    if (FMT8) own[it] *= *reinterpret_cast<const f32x4*>(static_cast<const float*>(a.s) + n);
+    if constexpr (FMT8) own[it] *= scl[it];
     epi_store_bf16x4(a.y, a.aux, a.epi, (size_t)(m0 + m) * N + n, own[it]);
   }
 }
