@@ -217,9 +217,25 @@ template <int NW, bool FMT8>
 __device__ __forceinline__ void reduce_and_store(const QArgs& a, unsigned char* smem, int ksi,
                                                  int rb, int m0, int mrows, int n0) {
   constexpr int kItems = kQRows * (kQCols / 4);
+  constexpr int IPT = (kItems + NW * kWave - 1) / (NW * kWave);  // items per thread
+  // FMT8: this thread's per-channel scales, loaded before the sums so their
+  // latency is not added after the last arriver's partial loads.
+  f32x4 scl[FMT8 ? IPT : 1];
+  if constexpr (FMT8) {
+#pragma unroll
+    for (int i = 0; i < IPT; ++i) {
+      const int item = threadIdx.x + i * NW * kWave;
+      const int n = n0 + 4 * (item % (kQCols / 4));
+      scl[i] = f32x4{1.f, 1.f, 1.f, 1.f};
+      if (item < kItems && n < a.N) scl[i] = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(a.s) + n);
+    }
+  }
   __syncthreads();
   const bool exchange = a.ks > 1 && a.cnt != nullptr;
-  for (int item = threadIdx.x; item < kItems; item += NW * kWave) {
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    const int item = threadIdx.x + i * NW * kWave;
+    if (item >= kItems) break;
     const int m = item / (kQCols / 4), ch = item % (kQCols / 4);
     const int n = n0 + 4 * ch;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -233,7 +249,7 @@ __device__ __forceinline__ void reduce_and_store(const QArgs& a, unsigned char* 
     } else if (a.ks > 1) {
       *reinterpret_cast<f32x4*>(dst) = acc;
     } else {
-      if (FMT8) acc *= *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(a.s) + n);
+      if constexpr (FMT8) acc *= scl[i];
       epi_store_bf16x4(a.y, a.aux, a.epi, (size_t)(m0 + m) * a.N + n, acc);
     }
   }
@@ -253,7 +269,10 @@ __device__ __forceinline__ void reduce_and_store(const QArgs& a, unsigned char* 
   }
   __syncthreads();
   if (!*flag) return;
-  for (int item = threadIdx.x; item < kItems; item += NW * kWave) {
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    const int item = threadIdx.x + i * NW * kWave;
+    if (item >= kItems) break;
     const int m = item / (kQCols / 4), ch = item % (kQCols / 4);
     const int n = n0 + 4 * ch;
     if (m >= mrows || n >= a.N) continue;
@@ -271,7 +290,7 @@ __device__ __forceinline__ void reduce_and_store(const QArgs& a, unsigned char* 
       acc += v3;
     }
     for (; k < a.ks; ++k) acc += ld1_sc1(src + k * kstride);
-    if (FMT8) acc *= *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(a.s) + n);
+    if constexpr (FMT8) acc *= scl[i];
     epi_store_bf16x4(a.y, a.aux, a.epi, (size_t)(m0 + m) * a.N + n, acc);
   }
 }
