@@ -405,7 +405,7 @@ __global__ __launch_bounds__(256) void qgemm_kernel(QgArgs a) {
 // ---------------------------------------------------------------------------
 constexpr int kQgXBuf = kQgRows * 64 * 2;  // bf16 x [256 rows][64 k]
 constexpr int kQgWSt = 2048 + 512;         // packed weights (int4 1 KB, int8 2 KB) + scales 256 B + zeros 128 B
-constexpr int kQgWsLds = 2 * kQgBuf + 3 * kQgXBuf + 4 * 2 * kQgWSt + 16;
+constexpr int kQgWsLds = 2 * kQgBuf + 3 * kQgXBuf + 4 * 2 * kQgWSt + 16 + kQgCols * 4;
 
 template <bool INT4>
 __global__ __launch_bounds__(512) void qgemm_ws_kernel(QgArgs a) {
@@ -414,6 +414,7 @@ __global__ __launch_bounds__(512) void qgemm_ws_kernel(QgArgs a) {
   unsigned char* xbuf = smem + 2 * kQgBuf;         // [3][kQgXBuf]
   unsigned char* wst = xbuf + 3 * kQgXBuf;         // [4][2][kQgWSt]
   volatile uint32_t* last_flag = reinterpret_cast<volatile uint32_t*>(wst + 4 * 2 * kQgWSt);
+  float* scl = reinterpret_cast<float*>(wst + 4 * 2 * kQgWSt + 16);  // int8: the tile's per-channel scales
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool producer = wave >= 4;
@@ -496,6 +497,12 @@ __global__ __launch_bounds__(512) void qgemm_ws_kernel(QgArgs a) {
     }
   } else {
     // ---- consumers: fragments from LDS, MFMAs ----
+    // int8: the tile's 128 per-channel scales go to LDS now, so the epilogue
+    // reads them from LDS instead of loading them after the exchange (many
+    // barriers separate this write from those reads).
+    if (!INT4 && wave == 0 && lane < kQgCols / 4)
+      *reinterpret_cast<f32x4*>(scl + 4 * lane) =
+          *reinterpret_cast<const f32x4*>(static_cast<const float*>(a.s) + n0 + 4 * lane);
     // B fragment of column block j: k row 8 g + r (g = lane / 16,
     // r = lane % 16 / 4), columns 16 j + 4 q .. +3 (q = lane % 4); the
     // swizzled address is bbase ^ (32 j) (the bits of 32 j and of the
@@ -588,7 +595,7 @@ __global__ __launch_bounds__(512) void qgemm_ws_kernel(QgArgs a) {
       const int n = n0 + 16 * j + 4 * (lane >> 4);
       f32x4 v = acc[i][j];
       if (!INT4) {
-        const f32x4 sc = *reinterpret_cast<const f32x4*>(static_cast<const float*>(a.s) + n);
+        const f32x4 sc = *reinterpret_cast<const f32x4*>(scl + (n - n0));
         v = f32x4{v.x * sc.x, v.y * sc.y, v.z * sc.z, v.w * sc.w};
       }
       epi_store_bf16x4(a.y, a.aux, a.epi, (size_t)m * N + n, v);
